@@ -1,0 +1,180 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decode path: codec frames/s, batch 1.
+
+Workload (one "step" = one frame): the full 28-layer Talker (hidden 2048,
+16/8 heads, FFN 6144, codec vocab 3072) plus the 5-layer code predictor
+(15 codebooks), random Q4 weights, a synthetic prompt of 64 text ids
+(uniform in [0, 151936)) embedded through the text projection and
+prefilled at positions 0..63, then --steps frames decoded with the KV cache
+growing from 64 (2048 frames: 64 -> 2112), top-k 50, temperature 0.9,
+repetition penalty 1.05, seed 42, EOS disabled (random weights can emit it).
+
+Printed as one JSON line: frames/s over the timed frames (whole job, inputs
+resident in HBM), the roofline of the dominant kernel (HIP events around
+each launch), the Q4 GEMV bandwidth on a rotating pool of 64 weights, and
+the oracle's CPU frame rate on a bounded sample as the CPU baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
+
+HBM_PEAK_GBS = 8000.0
+TTS_PAD = 151671          # generate_new.rs:28
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds):
+    """Oracle (C restatement of the reference's AVX2 CPU path, gemv pool of
+    min(nproc, 16) workers) timed on a bounded sample: frames at KV ~kv_len
+    after a synthetic N(0,1) KV prefill."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import qtts
+    workers = min(os.cpu_count() or 1, 16)
+    oracle.set_workers(workers, workers)
+    om = oracle.Model(talker, pred, kv_cap=kv_len + 64)
+    rng = np.random.Generator(np.random.PCG64(7))
+    L = len(talker.layers)
+    K = rng.standard_normal((L, kv_len, 8, 128), dtype=np.float32)
+    V = rng.standard_normal((L, kv_len, 8, 128), dtype=np.float32)
+    om.kv_load(K, V)
+    del K, V
+    params = qtts.sample_params(eos_enabled=False)
+    om.gen_begin(logits, hidden, kv_len, 42)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        om.frame(params, pad)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 64:
+            break
+    om.close()
+    return {"value": n / el, "unit": "frames/s", "cores": workers, "kind": "port",
+            "sample": f"{n} frames of the 28-layer talker + 5-layer predictor at KV {kv_len}..{kv_len + n} "
+                      f"(synthetic N(0,1) KV prefill), {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048, help="timed frames (KV grows from 64)")
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--gemv-copies", type=int, default=64)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              f"(decode of one utterance is a serial chain; see the sharding notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import qtts
+    from qtts import synth
+
+    t_gen = time.time()
+    talker = synth.make_talker(seed=1, n_layers=args.layers)
+    pred = synth.make_predictor(seed=2)
+    log(f"synthetic model generated in {time.time() - t_gen:.1f}s")
+
+    ctx = qtts.Context(0, kv_capacity=4096)
+    t_up = time.time()
+    ctx.upload_model(talker, pred)
+    log(f"uploaded in {time.time() - t_up:.1f}s")
+
+    rng = np.random.Generator(np.random.PCG64(42))
+    ids = rng.integers(0, 151936, 64)
+    prompt = np.stack([ctx.embed_text_token(int(i)) for i in ids])
+    pad = ctx.embed_text_token(TTS_PAD)
+    ctx.gen_set_text(None, pad)
+    hidden = ctx.prefill_talker_raw_from(prompt, 0)
+    logits = ctx.apply_codec_head(hidden)
+    params = qtts.sample_params(eos_enabled=False)
+    log("prefill done (64 positions)")
+
+    # warm-up frames, then rewind the KV cache to the prompt
+    ctx.gen_begin(logits, hidden, 64, 42, params)
+    ctx.gen_frames(args.warmup)
+    ctx.kv_truncate(64)
+    ctx.gen_begin(logits, hidden, 64, 42, params)
+    ctx.lib.qtts_sync(ctx.h)
+
+    t0 = time.perf_counter()
+    codes, eos = ctx.gen_frames(args.steps)
+    ctx.lib.qtts_sync(ctx.h)
+    dt = time.perf_counter() - t0
+    frames = codes.shape[0]
+    fps = frames / dt
+    log(f"{frames} frames in {dt:.3f}s -> {fps:.1f} frames/s (KV 64 -> {64 + frames})")
+
+    # kernel rooflines at the final KV length (~2112)
+    gu_us, gu_bytes = ctx.time_kernel(0, 4 * args.layers)
+    at_us, at_bytes = ctx.time_kernel(1, 4 * args.layers)
+    kern = {
+        "talker gate|up Q4 GEMV (k_gemv, RMSNorm prologue)": (gu_us, gu_bytes),
+        f"talker decode attention (k_talker_attn, KV {ctx.kv_len()})": (at_us, at_bytes),
+    }
+    name = max(kern, key=lambda k: kern[k][0])
+    us, byts = kern[name]
+    ach = byts / (us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "avg_us": round(us, 2), "bytes_per_launch": int(byts)}
+    log(f"gate|up {gu_us:.2f}us ({gu_bytes / gu_us / 1e3:.0f} GB/s), attention {at_us:.2f}us "
+        f"({at_bytes / at_us / 1e3:.0f} GB/s)")
+
+    # Q4 GEMV (k=2048 -> n=6144) over a pool of distinct weights (> 256 MB last-level cache)
+    grng = np.random.Generator(np.random.PCG64(1))
+    pool = [ctx.upload(synth.q4_random(grng, 2048, 6144)) for _ in range(args.gemv_copies)]
+    g_us, g_bytes = ctx.time_gemv(pool, 4 * args.gemv_copies)
+    for w in pool:
+        w.free()
+    g_gbs = g_bytes / (g_us * 1e-6) / 1e9
+    log(f"Q4 GEMV 2048x6144: {g_us:.2f}us/launch, {g_gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        lg, hd, _, _ = ctx.gen_state()
+        log("timing the CPU baseline (oracle)")
+        cpu = cpu_baseline(talker, pred, lg, hd, pad, 2048, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads")
+
+    out = {
+        "metric": "codec frames/s (talker+predictor, batch 1) @KV 2048; Q4 GEMV HBM GB/s (% peak)",
+        "value": round(fps, 3),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": frames,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / max(frames, 1), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random Q4 weights of the 1.7B shapes; random prompt ids)",
+        "config": {"workload": f"full frame loop: {args.layers}-layer talker + 5-layer predictor, 64-token prompt, "
+                               f"{frames} frames, KV 64->{64 + frames}, top-k 50, T 0.9, seed 42",
+                   "kv_start": 64, "kv_end": 64 + frames, "parallelism": "single GPU"},
+        "roofline": roof,
+        "q4_gemv": {"shape": [2048, 6144], "us_per_launch": round(g_us, 2), "gbs": round(g_gbs, 1),
+                    "frac_peak": round(g_gbs / HBM_PEAK_GBS, 4), "pool_copies": args.gemv_copies,
+                    "bytes_per_launch": int(g_bytes)},
+        "cpu_baseline": cpu,
+    }
+    ctx.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

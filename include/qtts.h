@@ -1,0 +1,284 @@
+/*
+ * qtts.h — C ABI of the MI355X (gfx950) decode path for QORA-TTS 12 Hz 1.7B.
+ *
+ * The path covered is the per-frame autoregressive decode: the 28-layer
+ * Talker step and the 5-layer code predictor's 15-codebook chain, with the
+ * talker sampler between them.  Every entry point below replaces one Rust
+ * function of the reference crate (cited as file:line); a Rust `ffi.rs`
+ * binding this header is given in INTEGRATION.md.
+ *
+ * Conventions (mirroring the reference's borrow/own rules):
+ *  - Every call returns an int status: QTTS_OK (0) or a negative QTTS_ERR_*.
+ *    qtts_last_error(ctx) returns a message for the last failure.
+ *  - Inputs are borrowed; uploads copy (and repack) into device memory owned
+ *    by the context.  Output buffers are caller-owned.
+ *  - Host pointers are the default.  Where a call takes `flags`,
+ *    QTTS_DEVICE_PTRS says the float buffers are device pointers instead.
+ *  - One context per host thread; a context is not re-entrant.
+ *  - Weights are the reference's Q4 layout (gemv.rs:26-31): a linear map
+ *    in -> out is stored input-major as `packed[k=in][n/2]` (two 4-bit codes
+ *    per byte, low nibble = even output column) and `scales[k][n/32]` f16;
+ *    value = (nibble - 8) * scale.
+ */
+#ifndef QTTS_H
+#define QTTS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QTTS_OK             0
+#define QTTS_ERR_INVALID   -1   /* bad argument, shape or handle           */
+#define QTTS_ERR_HIP       -2   /* HIP runtime error                       */
+#define QTTS_ERR_OOM       -3   /* device allocation failed                */
+#define QTTS_ERR_CAPACITY  -4   /* KV cache or workspace capacity exceeded */
+#define QTTS_ERR_STATE     -5   /* call out of order (no model, no begin)  */
+#define QTTS_ERR_IO        -6   /* model file missing, truncated or bad    */
+#define QTTS_ERR_NAN       -7   /* non-finite logits reached a sampler     */
+#define QTTS_ERR_UNSUPPORTED -8 /* format the device path does not run     */
+
+#define QTTS_DEVICE_PTRS   1    /* flags: float buffers are device memory  */
+
+typedef struct qtts_ctx qtts_ctx;
+typedef struct qtts_w   qtts_w;      /* one uploaded Q4 weight             */
+
+/* ---- host-side weight descriptors (plain pointers into caller memory) ---- */
+
+/* One Q4 weight, layout of `Q4Weight` (gemv.rs:26-31). */
+typedef struct qtts_q4_host {
+    const uint8_t  *packed;   /* k * (n/32) * 16 bytes                    */
+    const uint16_t *scales;   /* k * (n/32) f16 bit patterns              */
+    int64_t k;                /* input dim  (rows)                        */
+    int64_t n;                /* output dim (columns)                     */
+} qtts_q4_host;
+
+/* One decoder layer: `TalkerLayerWeights` (talker.rs:19-31) and
+ * `PredictorLayerWeights` (code_predictor.rs:14-26) share this shape. */
+typedef struct qtts_layer_host {
+    qtts_q4_host q_proj, k_proj, v_proj, o_proj;
+    const uint16_t *q_norm, *k_norm;             /* [head_dim] f16         */
+    qtts_q4_host gate_proj, up_proj, down_proj;
+    const uint16_t *input_norm, *post_attn_norm; /* [hidden] f16           */
+} qtts_layer_host;
+
+/* `TalkerWeights` (talker.rs:33-56). */
+typedef struct qtts_talker_host {
+    int32_t n_layers, hidden, text_hidden, n_heads, n_kv_heads, head_dim;
+    int32_t inter, vocab;
+    const qtts_layer_host *layers;               /* [n_layers]             */
+    qtts_q4_host codec_embedding;                /* [vocab x hidden]       */
+    qtts_q4_host text_embedding;                 /* [text_vocab x text_hidden] */
+    qtts_q4_host text_fc1, text_fc2;
+    const float *text_fc1_bias, *text_fc2_bias;
+    qtts_q4_host codec_head;                     /* hidden -> vocab        */
+    const uint16_t *final_norm;                  /* [hidden] f16           */
+    const float *rope_cos, *rope_sin;            /* [rope_max_pos][head_dim/2] */
+    int64_t rope_max_pos;
+} qtts_talker_host;
+
+/* `CodePredictorWeights` (code_predictor.rs:28-46). */
+typedef struct qtts_predictor_host {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, inter;
+    int32_t vocab;                               /* codes per codebook (2048) */
+    int32_t n_groups;                            /* acoustic codebooks (15)   */
+    int32_t has_input_proj;
+    qtts_q4_host input_proj;                     /* talker hidden -> hidden */
+    const float *input_proj_bias;
+    const qtts_q4_host *codec_embeddings;        /* [n_groups]              */
+    const qtts_layer_host *layers;               /* [n_layers]              */
+    const qtts_q4_host *lm_heads;                /* [n_groups]              */
+    const uint16_t *final_norm;
+    const float *rope_cos, *rope_sin;
+    int64_t rope_max_pos;
+} qtts_predictor_host;
+
+/* Sampler parameters: the fields of `TTSParams` (generate_new.rs:38-61)
+ * that `sample_token` and the frame loop read. */
+typedef struct qtts_sample_params {
+    float    temperature;          /* generate_new.rs:82-88 (after onset)    */
+    int32_t  top_k;                /* 0 = off                                */
+    float    top_p;                /* >=1 or <=0 = off                       */
+    float    repetition_penalty;   /* 1.0 = off                              */
+    uint32_t codec_eos_id;         /* 2150; stop when sampled                */
+    int32_t  eos_enabled;          /* 0: never stop (throughput runs)        */
+    int32_t  onset_frames;         /* frames using onset_temperature         */
+    float    onset_temperature;
+} qtts_sample_params;
+
+/* ---- context ---------------------------------------------------------- */
+
+/* Create a context on HIP device `device` with room for `kv_capacity`
+ * talker positions (0 = 4096).  No reference counterpart: the reference
+ * keeps all state in host Vecs. */
+int  qtts_ctx_create(int device, int64_t kv_capacity, qtts_ctx **out);
+void qtts_ctx_destroy(qtts_ctx *ctx);
+const char *qtts_last_error(const qtts_ctx *ctx);
+/* Wait for all work queued on the context's stream. */
+int  qtts_sync(qtts_ctx *ctx);
+/* The HIP stream (hipStream_t) the context launches on. */
+void *qtts_stream(qtts_ctx *ctx);
+
+/* ---- operator level --------------------------------------------------- */
+
+/* Upload one Q4 weight (repacked for the device).  Replaces building a
+ * `Weight::Q4` (gemv.rs:26-36) for the device path. */
+int qtts_q4_upload(qtts_ctx *ctx, const qtts_q4_host *w, qtts_w **out);
+int qtts_q4_free(qtts_ctx *ctx, qtts_w *w);
+
+/* y[n] = x[k] * W.  Replaces `gemv` (gemv.rs:149-154) -> `gemv_q4`
+ * (gemv.rs:290-346).  Output columns past (n/32)*32 are left zero, as in
+ * `gemv_q4_scalar` (gemv.rs:249-287). */
+int qtts_gemv_q4(qtts_ctx *ctx, const qtts_w *w, const float *x, float *y,
+                 int flags);
+
+/* Y[rows][n] = X[rows][k] * W.  Replaces `gemm` (gemv.rs:157-162) ->
+ * `gemm_q4` (gemv.rs:349-412): two rows share each pass over W. */
+int qtts_gemm_q4(qtts_ctx *ctx, const qtts_w *w, const float *X, int64_t rows,
+                 float *Y, int flags);
+
+/* out[n] = dequantised row `row`.  Replaces `embed_lookup_q4`
+ * (gemv.rs:415-437); exact in f32. */
+int qtts_embed_lookup_q4(qtts_ctx *ctx, const qtts_w *w, int64_t row,
+                         float *out, int flags);
+
+/* ---- model level ------------------------------------------------------ */
+
+/* Upload talker + predictor.  Replaces holding `TalkerWeights` /
+ * `CodePredictorWeights` (talker.rs:33-56, code_predictor.rs:28-46). */
+int qtts_model_upload(qtts_ctx *ctx, const qtts_talker_host *talker,
+                      const qtts_predictor_host *predictor);
+
+/* Read the talker and predictor sections of a `.qora-tts` file (QTTS v1,
+ * Q4 format byte) straight into the context.  Replaces `save::load_model`
+ * (save.rs:262-298) -> `load_talker` / `load_predictor` (save.rs:300-409);
+ * the decoder and speaker sections after them are not read. */
+int qtts_model_load_qtts(qtts_ctx *ctx, const char *path);
+
+/* Shapes of the uploaded model (hidden, vocab, ...); 0 on success. */
+int qtts_model_dims(qtts_ctx *ctx, int32_t *talker_hidden,
+                    int32_t *talker_vocab, int32_t *talker_layers,
+                    int32_t *pred_hidden, int32_t *pred_vocab,
+                    int32_t *pred_groups);
+
+/* ---- talker ------------------------------------------------------------ */
+
+/* One decode step: `forward_with_embedding` (talker.rs:263-360).  Appends
+ * one position to the talker KV cache (RoPE at `position`) and writes the
+ * final-normed hidden [hidden] and the codec-head logits [vocab]. */
+int qtts_talker_step(qtts_ctx *ctx, const float *embedding, int64_t position,
+                     float *hidden_out, float *logits_out, int flags);
+
+/* Prefill `seq` rows of pre-built embeddings at positions
+ * start_pos..start_pos+seq-1 on top of the cached prefix:
+ * `prefill_talker_raw_from` (talker.rs:379-482).  Requires
+ * kv_len == start_pos.  Writes the last row's final-normed hidden. */
+int qtts_talker_prefill(qtts_ctx *ctx, const float *X, int64_t seq,
+                        int64_t start_pos, float *hidden_out, int flags);
+
+/* logits = hidden * codec_head: `apply_codec_head` (talker.rs:647-649). */
+int qtts_codec_head(qtts_ctx *ctx, const float *hidden, float *logits,
+                    int flags);
+
+/* `embed_text_token` (talker.rs:105-116): text row + fc1/SiLU/fc2. */
+int qtts_embed_text_token(qtts_ctx *ctx, uint32_t token, float *out,
+                          int flags);
+/* `embed_codec_token` (talker.rs:152-154). */
+int qtts_embed_codec_token(qtts_ctx *ctx, uint32_t token, float *out,
+                           int flags);
+
+/* ---- talker KV cache (paged, device resident) ------------------------- */
+
+/* Drop every cached position (`empty_kv_cache`, gemv.rs:79-86). */
+int qtts_kv_reset(qtts_ctx *ctx);
+int qtts_kv_len(qtts_ctx *ctx, int64_t *len);
+/* Copy layer `layer`'s cache out in the reference layout
+ * `[len][n_kv_heads][head_dim]` f32 (gemv.rs:75-77).  Bit-exact. */
+int qtts_kv_gather(qtts_ctx *ctx, int32_t layer, float *K, float *V);
+/* Overwrite the cache with `len` positions per layer, reference layout,
+ * K and V each [n_layers][len][n_kv_heads][head_dim] (test and bench
+ * set-up).  Bit-exact. */
+int qtts_kv_load(qtts_ctx *ctx, const float *K, const float *V, int64_t len);
+/* Keep the first `len` positions and drop the rest (prefix reuse,
+ * generate_new.rs:537-551: the cached prefix is kept, the suffix redone). */
+int qtts_kv_truncate(qtts_ctx *ctx, int64_t len);
+
+/* ---- code predictor --------------------------------------------------- */
+
+/* `generate_acoustic_codes` (code_predictor.rs:218-273): 2-token prefill,
+ * 14 autoregressive steps, greedy argmax (last index on ties). */
+int qtts_predictor_chain(qtts_ctx *ctx, const float *talker_hidden,
+                         const float *semantic_embed, uint32_t *codes_out,
+                         int flags);
+
+/* `get_acoustic_embeddings_sum` (code_predictor.rs:287-300). */
+int qtts_acoustic_embed_sum(qtts_ctx *ctx, const uint32_t *codes, float *out,
+                            int flags);
+
+/* ---- sampler ---------------------------------------------------------- */
+
+/* `sample_token` (generate_new.rs:771-862) with `simple_rand`
+ * (generate_new.rs:17-22) advancing *rng by one draw.  `prev` holds
+ * `n_prev` previous tokens for the repetition penalty. */
+int qtts_sample_token(qtts_ctx *ctx, const float *logits, int64_t n,
+                      const qtts_sample_params *p, const uint32_t *prev,
+                      int64_t n_prev, uint64_t *rng, float temperature,
+                      uint32_t *out);
+
+/* ---- frame loop (generate_new.rs:606-675) ----------------------------- */
+
+/* Start a generation: the prefill's logits [vocab] and final-normed hidden
+ * [hidden], the next RoPE position, the RNG seed and the sampler settings.
+ * prev_tokens start at zero (generate_new.rs:583). */
+int qtts_gen_begin(qtts_ctx *ctx, const float *logits, const float *hidden,
+                   int64_t position, uint64_t seed,
+                   const qtts_sample_params *p);
+
+/* Trailing text rows added to frames 0..n_text-1, then `pad` for every
+ * later frame (generate_new.rs:645-654).  text may be NULL when n_text=0. */
+int qtts_gen_set_text(qtts_ctx *ctx, const float *text, int64_t n_text,
+                      const float *pad);
+
+/* Run up to `max_frames` frames.  codes_out is [max_frames][16]
+ * (code 0 = talker sample, 1..15 = predictor).  Stops after the frame whose
+ * sampled code 0 is the EOS id (that frame's codes are not emitted, as in
+ * generate_new.rs:611-614).  *frames_done counts emitted frames, *eos is 1
+ * when EOS stopped the run.  One host synchronisation per call batch. */
+int qtts_gen_frames(qtts_ctx *ctx, int64_t max_frames, uint32_t *codes_out,
+                    int64_t *frames_done, int32_t *eos);
+
+/* Teacher-forced frames for parity checks: frame f predicts 16 codes into
+ * pred_out[f] but feeds forced[f] downstream (talker input, predictor chain
+ * steps, repetition history).  No EOS stop. */
+int qtts_gen_frames_forced(qtts_ctx *ctx, int64_t n_frames,
+                           const uint32_t *forced, uint32_t *pred_out);
+
+/* Current generation state: logits [vocab], hidden [hidden], position and
+ * RNG state (host copies). */
+int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
+                   int64_t *position, uint64_t *rng);
+
+/* ---- measurement ------------------------------------------------------ */
+
+/* Average device time (us) of one kernel launch, from HIP events recorded
+ * around each of `iters` launches on the context stream; *bytes gets the
+ * algorithmic bytes one launch moves.  No reference counterpart (the
+ * reference times phases with Instant, generate_new.rs:600-678).
+ *   kind 0: talker gate|up GEMV (RMSNorm prologue), cycling the layers;
+ *   kind 1: talker decode attention over the cached positions, cycling
+ *           the layers. */
+int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
+                     double *avg_us, double *bytes);
+
+/* Same for the standalone Q4 GEMV, cycling through `n_w` uploaded weights
+ * of one shape (a pool larger than the 256 MB last-level cache measures
+ * HBM, not cache). */
+int qtts_time_gemv(qtts_ctx *ctx, const qtts_w *const *ws, int32_t n_w,
+                   int32_t iters, double *avg_us, double *bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QTTS_H */

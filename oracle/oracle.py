@@ -1,0 +1,333 @@
+"""ctypes binding of the CPU oracle (oracle/liboqtts_oracle.so).
+
+TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg use this module.  It restates the reference's CPU decode
+path (see qtts_oracle.c) and is the checker for the HIP path, never part of
+it.
+"""
+import ctypes
+import os
+import subprocess
+import sys
+from ctypes import POINTER, byref, c_double, c_float, c_int, c_int32, c_int64, c_uint16, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
+from qtts import hostdesc  # noqa: E402  (descriptor structs only)
+from qtts.hostdesc import LayerHost, PredictorHost, Q4Host, SampleParams, TalkerHost, ptr  # noqa: E402
+
+LIB = os.path.join(HERE, "liboqtts_oracle.so")
+
+
+class OqKv(ctypes.Structure):
+    _fields_ = [("n_layers", c_int32), ("n_kv", c_int32), ("hd", c_int32), ("cap", c_int64),
+                ("len", POINTER(c_int64)), ("K", POINTER(POINTER(c_float))), ("V", POINTER(POINTER(c_float)))]
+
+
+class OqGen(ctypes.Structure):
+    _fields_ = [("logits", c_void_p), ("hidden", c_void_p), ("prev", c_uint32 * 16), ("rng", c_uint64),
+                ("position", c_int64), ("frame_idx", c_int64)]
+
+
+_SIG = {
+    "oq_f16_to_f32": ([c_uint16], c_float),
+    "oq_f32_to_f16": ([c_float], c_uint16),
+    "oq_xorshift": ([POINTER(c_uint64)], c_uint64),
+    "oq_simple_rand": ([POINTER(c_uint64)], c_float),
+    "oq_gemv_q4_scalar": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], None),
+    "oq_gemv_q4_avx2": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], c_int),
+    "oq_set_workers": ([c_int, c_int], None),
+    "oq_get_workers": ([], c_int),
+    "oq_gemv_q4": ([c_void_p, POINTER(Q4Host), c_void_p], None),
+    "oq_gemm_q4": ([c_void_p, c_int64, POINTER(Q4Host), c_void_p], None),
+    "oq_embed_lookup_q4": ([POINTER(Q4Host), c_int64, c_int64, c_void_p], None),
+    "oq_quantize_q4": ([c_void_p, c_int64, c_int64, c_void_p, c_void_p], None),
+    "oq_rms_norm_f16": ([c_void_p, c_void_p, c_int64, c_void_p], None),
+    "oq_softmax_raw": ([c_void_p, c_int64], None),
+    "oq_silu": ([c_float], c_float),
+    "oq_qk_norm": ([c_void_p, c_int64, c_int64, c_void_p], None),
+    "oq_rope_table": ([c_int64, c_int64, c_double, c_void_p, c_void_p], None),
+    "oq_rope_apply": ([c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64], None),
+    "oq_kv_new": ([c_int32, c_int32, c_int32, c_int64], POINTER(OqKv)),
+    "oq_kv_free": ([POINTER(OqKv)], None),
+    "oq_kv_reset": ([POINTER(OqKv)], None),
+    "oq_kv_k": ([POINTER(OqKv), c_int32], POINTER(c_float)),
+    "oq_kv_v": ([POINTER(OqKv), c_int32], POINTER(c_float)),
+    "oq_kv_len": ([POINTER(OqKv), c_int32], c_int64),
+    "oq_kv_set_len": ([POINTER(OqKv), c_int64], None),
+    "oq_talker_step": ([POINTER(TalkerHost), c_void_p, POINTER(OqKv), c_int64, c_void_p], c_int),
+    "oq_talker_prefill": ([POINTER(TalkerHost), c_void_p, c_int64, POINTER(OqKv), c_int64, c_void_p], c_int),
+    "oq_codec_head": ([POINTER(TalkerHost), c_void_p, c_void_p], None),
+    "oq_embed_text_token": ([POINTER(TalkerHost), c_uint32, c_void_p], None),
+    "oq_embed_codec_token": ([POINTER(TalkerHost), c_uint32, c_void_p], None),
+    "oq_predictor_chain": ([POINTER(PredictorHost), c_void_p, c_void_p, POINTER(OqKv), c_void_p, c_void_p], c_int),
+    "oq_acoustic_embed_sum": ([POINTER(PredictorHost), c_void_p, c_int32, c_void_p], None),
+    "oq_argmax_last": ([c_void_p, c_int64], c_uint32),
+    "oq_sample_token": ([c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64, POINTER(c_uint64), c_float,
+                         POINTER(c_uint32)], c_int),
+    "oq_frame": ([POINTER(TalkerHost), POINTER(PredictorHost), POINTER(OqKv), POINTER(OqKv), POINTER(OqGen),
+                  POINTER(SampleParams), c_void_p, c_void_p, POINTER(c_int32), c_void_p], c_int),
+}
+
+_lib = None
+
+
+def build():
+    """Compile the oracle with its Makefile (gcc, strict IEEE)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        _lib = ctypes.CDLL(LIB)
+        for k, (a, r) in _SIG.items():
+            f = getattr(_lib, k)
+            f.argtypes = a
+            f.restype = r
+    return _lib
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------------------
+# numeric kernels
+# ---------------------------------------------------------------------------
+
+def gemv_scalar(x, w, k0=0, k1=None):
+    """gemv_q4_scalar (gemv.rs:249-287) over rows k0..k1."""
+    x = f32(x)
+    out = np.empty(w.n, np.float32)
+    lib().oq_gemv_q4_scalar(ptr(x), ptr(w.packed), ptr(w.scales), w.n, k0, w.k if k1 is None else k1, ptr(out))
+    return out
+
+
+def gemv_avx2(x, w, k0=0, k1=None):
+    """gemv_q4_avx2 (simd.rs:76-153); None when the host lacks AVX2."""
+    x = f32(x)
+    out = np.empty(w.n, np.float32)
+    ok = lib().oq_gemv_q4_avx2(ptr(x), ptr(w.packed), ptr(w.scales), w.n, k0, w.k if k1 is None else k1, ptr(out))
+    return out if ok else None
+
+
+def set_workers(workers=16, threads=0):
+    lib().oq_set_workers(workers, threads)
+
+
+def gemv(x, w):
+    """gemv_q4 chunk policy (gemv.rs:290-346)."""
+    x = f32(x)
+    out = np.empty(w.n, np.float32)
+    lib().oq_gemv_q4(ptr(x), byref(hostdesc.q4_host(w)), ptr(out))
+    return out
+
+
+def gemm(X, w):
+    X = f32(X).reshape(-1, w.k)
+    Y = np.empty((X.shape[0], w.n), np.float32)
+    lib().oq_gemm_q4(ptr(X), X.shape[0], byref(hostdesc.q4_host(w)), ptr(Y))
+    return Y
+
+
+def embed_lookup(w, row, width=None):
+    width = w.n if width is None else width
+    out = np.empty(width, np.float32)
+    lib().oq_embed_lookup_q4(byref(hostdesc.q4_host(w)), row, width, ptr(out))
+    return out
+
+
+def quantize(data, k, n):
+    d = f32(data)
+    packed = np.empty((k, n // 32 * 16), np.uint8)
+    scales = np.empty((k, n // 32), np.uint16)
+    lib().oq_quantize_q4(ptr(d), k, n, ptr(packed), ptr(scales))
+    return packed, scales
+
+
+def rms_norm(x, gamma):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().oq_rms_norm_f16(ptr(x), ptr(gamma), x.size, ptr(out))
+    return out
+
+
+def softmax_raw(s):
+    s = f32(s).copy()
+    lib().oq_softmax_raw(ptr(s), s.size)
+    return s
+
+
+def silu(x):
+    return lib().oq_silu(x)
+
+
+def qk_norm(d, heads, hd, gamma):
+    d = f32(d).copy()
+    lib().oq_qk_norm(ptr(d), heads, hd, ptr(gamma))
+    return d
+
+
+def rope_table(head_dim, max_pos, theta=1_000_000.0):
+    half = head_dim // 2
+    c = np.empty((max_pos, half), np.float32)
+    s = np.empty((max_pos, half), np.float32)
+    lib().oq_rope_table(head_dim, max_pos, theta, ptr(c), ptr(s))
+    return c, s
+
+
+def rope_apply(d, heads, hd, pos, cos_t, sin_t):
+    d = f32(d).copy()
+    lib().oq_rope_apply(ptr(d), heads, hd, pos, ptr(cos_t), ptr(sin_t), cos_t.shape[0])
+    return d
+
+
+def f16_to_f32(h):
+    return lib().oq_f16_to_f32(h)
+
+
+def f32_to_f16(f):
+    return lib().oq_f32_to_f16(f)
+
+
+def simple_rand(state):
+    s = c_uint64(state)
+    r = lib().oq_simple_rand(byref(s))
+    return r, s.value
+
+
+def argmax_last(v):
+    v = f32(v)
+    return lib().oq_argmax_last(ptr(v), v.size)
+
+
+def sample_token(logits, params, prev, rng, temperature):
+    lg = f32(logits)
+    pv = np.ascontiguousarray(prev, dtype=np.uint32)
+    s = c_uint64(rng)
+    out = c_uint32()
+    rc = lib().oq_sample_token(ptr(lg), lg.size, byref(params), ptr(pv) if pv.size else None, pv.size, byref(s),
+                               temperature, byref(out))
+    if rc != 0:
+        raise RuntimeError(f"oracle sample_token rc={rc}")
+    return out.value, s.value
+
+
+# ---------------------------------------------------------------------------
+# model-level oracle
+# ---------------------------------------------------------------------------
+
+class Model:
+    """Talker + predictor held by the oracle, with its own KV caches."""
+
+    def __init__(self, talker, predictor, kv_cap=4096):
+        self.t, self.p = talker, predictor
+        self.th, self._kt = hostdesc.talker_host(talker)
+        self.ph, self._kp = hostdesc.predictor_host(predictor)
+        self.tkv = lib().oq_kv_new(len(talker.layers), talker.n_kv_heads, talker.head_dim, kv_cap)
+        self.pkv = lib().oq_kv_new(len(predictor.layers), predictor.n_kv_heads, predictor.head_dim, 16)
+
+    def close(self):
+        if self.tkv:
+            lib().oq_kv_free(self.tkv)
+            lib().oq_kv_free(self.pkv)
+            self.tkv = self.pkv = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def kv_len(self):
+        return lib().oq_kv_len(self.tkv, 0)
+
+    def kv_layer(self, layer):
+        n = self.kv_len()
+        cnt = n * self.t.n_kv_heads * self.t.head_dim
+        K = np.ctypeslib.as_array(lib().oq_kv_k(self.tkv, layer), shape=(cnt,)).reshape(n, 8, 128).copy()
+        V = np.ctypeslib.as_array(lib().oq_kv_v(self.tkv, layer), shape=(cnt,)).reshape(n, 8, 128).copy()
+        return K, V
+
+    def kv_load(self, K, V):
+        """K, V: [n_layers][len][8][128]."""
+        n = K.shape[1]
+        for l in range(len(self.t.layers)):
+            cnt = n * 8 * 128
+            ctypes.memmove(lib().oq_kv_k(self.tkv, l), f32(K[l]).ctypes.data, cnt * 4)
+            ctypes.memmove(lib().oq_kv_v(self.tkv, l), f32(V[l]).ctypes.data, cnt * 4)
+        lib().oq_kv_set_len(self.tkv, n)
+
+    def kv_reset(self):
+        lib().oq_kv_reset(self.tkv)
+
+    def forward_with_embedding(self, emb, position):
+        e = f32(emb)
+        out = np.empty(self.t.hidden + self.t.vocab, np.float32)
+        rc = lib().oq_talker_step(byref(self.th), ptr(e), self.tkv, position, ptr(out))
+        if rc:
+            raise RuntimeError(f"oracle talker step rc={rc}")
+        return out
+
+    def prefill(self, X, start_pos):
+        X = f32(X).reshape(-1, self.t.hidden)
+        out = np.empty(self.t.hidden, np.float32)
+        rc = lib().oq_talker_prefill(byref(self.th), ptr(X), X.shape[0], self.tkv, start_pos, ptr(out))
+        if rc:
+            raise RuntimeError(f"oracle prefill rc={rc}")
+        return out
+
+    def codec_head(self, hidden):
+        h = f32(hidden)
+        out = np.empty(self.t.vocab, np.float32)
+        lib().oq_codec_head(byref(self.th), ptr(h), ptr(out))
+        return out
+
+    def embed_text_token(self, tok):
+        out = np.empty(self.t.hidden, np.float32)
+        lib().oq_embed_text_token(byref(self.th), tok, ptr(out))
+        return out
+
+    def embed_codec_token(self, tok):
+        out = np.empty(self.t.hidden, np.float32)
+        lib().oq_embed_codec_token(byref(self.th), tok, ptr(out))
+        return out
+
+    def predictor_chain(self, th, sem, forced=None):
+        a, b = f32(th), f32(sem)
+        codes = np.empty(len(self.p.lm_heads), np.uint32)
+        fc = None if forced is None else np.ascontiguousarray(forced, dtype=np.uint32)
+        rc = lib().oq_predictor_chain(byref(self.ph), ptr(a), ptr(b), self.pkv, ptr(codes), ptr(fc) if fc is not None else None)
+        if rc:
+            raise RuntimeError(f"oracle predictor rc={rc}")
+        return codes
+
+    def acoustic_embed_sum(self, codes):
+        c = np.ascontiguousarray(codes, dtype=np.uint32)
+        out = np.empty(self.t.hidden, np.float32)
+        lib().oq_acoustic_embed_sum(byref(self.ph), ptr(c), c.size, ptr(out))
+        return out
+
+    # frame loop ---------------------------------------------------------------
+    def gen_begin(self, logits, hidden, position, seed):
+        self.g_logits = f32(logits).copy()
+        self.g_hidden = f32(hidden).copy()
+        self.gen = OqGen(self.g_logits.ctypes.data, self.g_hidden.ctypes.data, (c_uint32 * 16)(), seed, position, 0)
+
+    def frame(self, params, text_add, forced=None):
+        """One frame: (codes[16] predicted, eos)."""
+        codes = np.empty(16, np.uint32)
+        eos = c_int32()
+        ta = f32(text_add)
+        fc = None if forced is None else np.ascontiguousarray(forced, dtype=np.uint32)
+        rc = lib().oq_frame(byref(self.th), byref(self.ph), self.tkv, self.pkv, byref(self.gen), byref(params), ptr(ta),
+                            ptr(codes), byref(eos), ptr(fc) if fc is not None else None)
+        if rc:
+            raise RuntimeError(f"oracle frame rc={rc}")
+        return codes, bool(eos.value)

@@ -1,0 +1,104 @@
+// qtts_kernels.h — model/workspace descriptors and the enqueue functions the
+// runtime calls.  Everything here lives in device memory except the
+// descriptor structs themselves (host copies passed by value to kernels).
+#pragma once
+#include "qtts_device.h"
+
+namespace qtts {
+
+constexpr int MAX_CHUNKS = 128;          // KV pages per sequence (8192 positions)
+constexpr int RING_FRAMES = 64;          // frames per host synchronisation, max
+
+struct KvPaged {
+    float *base;           // [layers][n_phys][2 (K,V)][8 heads][64 pos][128]
+    const int32_t *ptab;   // logical page -> physical page
+    int32_t n_phys;
+};
+
+// One decoder layer on the device.  q|k|v and gate|up are fused along the
+// output dimension (columns [q | k | v], [gate | up]).
+struct LayerDev {
+    Q4Tiled qkv, o, gate_up, down;
+    const uint16_t *q_norm, *k_norm, *input_norm, *post_norm;
+};
+
+struct TalkerDev {
+    int n_layers, hidden, text_hidden, n_heads, n_kv_heads, inter, vocab;
+    const LayerDev *layers;              // host array [n_layers]
+    Q4Tiled codec_head, text_fc1, text_fc2;
+    const float *text_fc1_bias, *text_fc2_bias;
+    Q4Rows codec_rows, text_rows;        // embedding tables, reference layout
+    const uint16_t *final_norm;
+    const float *rope_cos, *rope_sin;
+    int64_t rope_rows;
+    KvPaged kv;
+};
+
+struct PredictorDev {
+    int n_layers, hidden, n_heads, n_kv_heads, inter, vocab, n_groups;
+    const LayerDev *layers;              // host array
+    Q4Tiled proj;
+    const float *proj_bias;
+    const Q4Tiled *heads;                // host array [n_groups]
+    Q4Rows emb_rows;                     // [n_groups][rows][...] contiguous
+    const uint16_t *final_norm;
+    const float *rope_cos, *rope_sin;
+    int64_t rope_rows;
+};
+
+struct Workspace {
+    float *x;          // talker residual stream [hidden]
+    float *px;         // predictor residual rows [2][p.hidden]
+    float *pin;        // predictor API input rows [2][t.hidden]
+    float *qbuf;       // q after norm + RoPE [16][128]
+    float *am, *al;    // attention chunk max / sum [MAX_CHUNKS][16]
+    float *aacc;       // attention chunk P.V [MAX_CHUNKS][16][128]
+    float *pattn;      // predictor attention output [2][16*128]
+    float *pk, *pv;    // predictor KV [layers][16][8][128]
+    float *part_a, *part_b, *part_head;   // split-K partial sums
+    float *hid_work;   // final-normed hidden of the running step
+    float *hidden;     // last_hidden kept across frames
+    float *logits;     // logits kept across frames
+    float *text;       // trailing text rows [n][hidden]
+    float *pad;        // tts_pad row [hidden]
+    uint32_t *ring_pred, *ring_used;      // [RING_FRAMES][16]
+    int attn_grid;
+};
+
+struct SampleArgsHost {
+    float temperature, top_p, rep;
+    int top_k;
+    const uint32_t *prev;   // device
+    int n_prev;
+};
+
+hipError_t enqueue_gemv_plain(const Q4Tiled &w, const float *x, int NB, int ld, float *part, hipStream_t st);
+hipError_t enqueue_gemv_store(const Q4Tiled &w, const float *x, float *y, const float *bias, float *part,
+                              hipStream_t st);
+hipError_t enqueue_gemv_rows(const Q4Tiled &w, const float *X, int rows, float *Y, float *part, hipStream_t st);
+hipError_t enqueue_embed_row(const Q4Rows &e, const uint32_t *code_dev, uint32_t code, float *out,
+                             hipStream_t st);
+hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *codes, float *out, hipStream_t st);
+hipError_t enqueue_silu(float *x, int n, hipStream_t st);
+
+hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
+                               hipStream_t s);
+hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,
+                              int slot, hipStream_t s);
+hipError_t enqueue_final_norm(const TalkerDev &m, const Workspace &ws, float *hidden_out, hipStream_t s);
+hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const float *hidden, float *logits,
+                              hipStream_t s);
+hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, const Workspace &ws,
+                                   DevState *st, const float *hidden, const float *sem,
+                                   const uint32_t *forced, uint32_t *codes_api, hipStream_t s);
+hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
+                         const uint32_t *forced, hipStream_t s);
+hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &a, uint64_t *rng_dev,
+                              uint32_t *out_dev, DevState *st, hipStream_t s);
+hipError_t enqueue_kv_gather(const KvPaged &kv, int layer, int len, float *K, float *V, hipStream_t s);
+hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float *K, const float *V,
+                              hipStream_t s);
+hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
+hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int len, hipStream_t s);
+
+}  // namespace qtts

@@ -1,0 +1,1365 @@
+// qtts_kernels.hip — hand-written gfx950 kernels for the QORA-TTS decode
+// path, and the host functions that enqueue one talker step, one predictor
+// chain and one frame on a stream.
+//
+// Reference functions restated (src/ of the reference crate):
+//   Q4 GEMV            gemv.rs:249-346      (k_gemv + k_reduce_parts)
+//   RMSNorm            gemv.rs:445-454      (ProRms prologue)
+//   QK-norm + RoPE     talker.rs:286-297, rope.rs:79-92 (k_talker_qkv_fin)
+//   KV append          talker.rs:299-302    (k_talker_qkv_fin, paged)
+//   decode attention   talker.rs:304-331    (k_talker_attn + ProAttn)
+//   SwiGLU             talker.rs:338-349    (ProSwiglu prologue)
+//   predictor layers   code_predictor.rs:345-513 (k_pred_attn et al.)
+//   argmax             code_predictor.rs:335-341 (k_argmax)
+//   sample_token       generate_new.rs:771-862   (k_sampler)
+//   frame fusion       generate_new.rs:638-654   (k_combine)
+#include "qtts_device.h"
+#include "qtts_kernels.h"
+
+#include <math.h>
+
+namespace qtts {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint32_t h16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// AND kept opaque to the optimiser: with a visible mask the compiler folds
+// `(w & 0x0F0F0F0F) >> 8*b & 0xFF` into one v_bfe_u32 per byte, while an
+// opaque masked word lets each byte feed v_cvt_f32_ubyte{0..3} directly.
+__device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t m)
+{
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(w));
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// block-wide reductions (deterministic tree order)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+// Sum over the whole block; every thread gets the result.  `scratch` holds
+// at least blockDim/64 floats.
+__device__ float block_sum(float v, float *scratch)
+{
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) scratch[wv] = v;
+    __syncthreads();
+    float r = 0.0f;
+    for (int i = 0; i < nw; i++) r += scratch[i];
+    return r;
+}
+
+__device__ float block_max(float v, float *scratch)
+{
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) scratch[wv] = v;
+    __syncthreads();
+    float r = -INFINITY;
+    for (int i = 0; i < nw; i++) r = fmaxf(r, scratch[i]);
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Q4 dequantisation of one reference-layout row slice (exact in f32)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int col)
+{
+    const int g = col >> 5, j = col & 31;
+    const uint8_t b = e.packed[(size_t)row * e.G * 16 + g * 16 + (j >> 1)];
+    const int q = (int)((j & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+    return h2f(e.scales[(size_t)row * e.G + g]) * (float)q;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV prologues: fill xs[b*KC + i] with input row b, rows k0+i.
+// ---------------------------------------------------------------------------
+
+template <int NB>
+struct ProPlain {
+    const float *x;
+    int ld, k;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
+            const int b = i / KC, r = k0 + (i - b * KC);
+            xs[i] = r < k ? x[(size_t)b * ld + r] : 0.0f;
+        }
+    }
+};
+
+// RMSNorm (gemv.rs:445-454) of the whole input row, then the slice.
+// Tiles of column-tile 0 also store the normed slice to `side` (the
+// final-normed hidden the frame loop keeps, talker.rs:352-359).
+template <int NB>
+struct ProRms {
+    const float *x;
+    int ld, k;
+    const uint16_t *gamma;
+    float *side;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        __shared__ float scratch[16];
+        float inv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            float ss = 0.0f;
+            for (int i = threadIdx.x; i < k; i += blockDim.x) {
+                const float v = x[(size_t)b * ld + i];
+                ss += v * v;
+            }
+            ss = block_sum(ss, scratch);
+            inv[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
+        }
+        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
+            const int b = i / KC, r = k0 + (i - b * KC);
+            float v = 0.0f;
+            if (r < k) {
+                v = x[(size_t)b * ld + r] * inv[b] * h2f(gamma[r]);
+                if (side && ctile == 0) side[(size_t)b * ld + r] = v;
+            }
+            xs[i] = v;
+        }
+    }
+};
+
+// silu(gate) * up from the gate|up GEMV partials (talker.rs:343-345).
+template <int NB>
+struct ProSwiglu {
+    const float *part;
+    int S, npad, inter;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
+            const int b = i / KC, r = k0 + (i - b * KC);
+            float v = 0.0f;
+            if (r < inter) {
+                float g = 0.0f, u = 0.0f;
+                for (int s = 0; s < S; s++) {
+                    const float *p = part + ((size_t)s * NB + b) * npad;
+                    g += p[r];
+                    u += p[inter + r];
+                }
+                v = silu_f(g) * u;
+            }
+            xs[i] = v;
+        }
+    }
+};
+
+// Combine the split-K attention chunks of the heads in this k-slice
+// (flash-decoding merge of (max, sum, acc) per chunk).
+struct ProAttn {
+    const float *am, *al, *aacc;   // [chunk][16], [chunk][16], [chunk][16][128]
+    const DevState *st;
+    int len_override;               // >= 0: attended length; else kv_len + 1
+    int n_heads;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        __shared__ float wts[MAX_CHUNKS * 16];
+        __shared__ float hm[16], hl[16];
+        const int L = len_override >= 0 ? len_override : st->kv_len + 1;
+        const int C = (L + KV_PAGE - 1) / KV_PAGE;
+        const int h0 = k0 / HEAD_DIM;
+        const int nh = min(KC / HEAD_DIM, n_heads - h0);
+        // per-head max and normaliser
+        for (int hh = threadIdx.x; hh < nh; hh += blockDim.x) {
+            const int h = h0 + hh;
+            float M = -INFINITY;
+            for (int c = 0; c < C; c++) M = fmaxf(M, am[c * 16 + h]);
+            float Ls = 0.0f;
+            for (int c = 0; c < C; c++) Ls += al[c * 16 + h] * expf(am[c * 16 + h] - M);
+            hm[hh] = M;
+            hl[hh] = Ls;
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < C * nh; i += blockDim.x) {
+            const int c = i / nh, hh = i - c * nh;
+            wts[i] = expf(am[c * 16 + h0 + hh] - hm[hh]) / hl[hh];
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
+            const int hh = i / HEAD_DIM, d = i - hh * HEAD_DIM;
+            float v = 0.0f;
+            if (hh < nh) {
+                const int h = h0 + hh;
+                for (int c = 0; c < C; c++)
+                    v += wts[c * nh + hh] * aacc[((size_t)c * 16 + h) * HEAD_DIM + d];
+            }
+            xs[i] = v;
+        }
+    }
+};
+
+// One dequantised embedding row (embed_lookup_q4, gemv.rs:415-437); the row
+// index is read from device memory.
+struct ProEmbed {
+    Q4Rows emb;
+    const uint32_t *code;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        const uint32_t row = *code;
+        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
+            const int r = k0 + i;
+            xs[i] = r < emb.n ? q4_row_value(emb, row, r) : 0.0f;
+        }
+    }
+};
+
+// Predictor prefill input: row 0 = talker hidden, row 1 = codec embedding
+// of the semantic code (code_predictor.rs:235-241, generate_new.rs:620).
+struct ProHidEmbed {
+    const float *hidden;
+    Q4Rows emb;
+    const uint32_t *code;
+    int k;
+    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    {
+        const uint32_t row = *code;
+        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
+            const int r = k0 + i;
+            xs[i] = r < k ? hidden[r] : 0.0f;
+            xs[KC + i] = r < k ? q4_row_value(emb, row, r) : 0.0f;
+        }
+    }
+};
+
+// ---------------------------------------------------------------------------
+// GEMV epilogues: receive (slice s, row b, column col, value y)
+// ---------------------------------------------------------------------------
+
+template <int NB>
+struct EpiPart {
+    float *part;
+    int npad;
+    __device__ void operator()(int s, int b, int col, float y) const
+    {
+        part[((size_t)s * NB + b) * npad + col] = y;
+    }
+};
+
+// Single-slice weights: add into the residual stream x (talker.rs:334-336,
+// 347-349).
+template <int NB>
+struct EpiResid {
+    float *x;
+    int ld, n;
+    __device__ void operator()(int s, int b, int col, float y) const
+    {
+        if (col < n) x[(size_t)b * ld + col] += y;
+    }
+};
+
+template <int NB>
+struct EpiStore {
+    float *y;
+    int ld, n;
+    const float *bias;
+    __device__ void operator()(int s, int b, int col, float v) const
+    {
+        if (col < n) y[(size_t)b * ld + col] = bias ? v + bias[col] : v;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// The split-K Q4 GEMV.
+//
+// Thread t of a T-thread workgroup owns 32-column group gl = t % GB of the
+// tile and rows r*P + ph (P = T/GB, ph = t/GB, r < R) of its k-slice.  Per
+// row it loads one 16-byte block of 32 nibbles and computes
+//     acc[j] += a * nib_j,   a = f32(scale) * x[row]
+// with nibbles split into two byte lanes (& 0x0F0F0F0F for even columns,
+// & 0xF0F0F0F0 for odd ones, the latter scaled by a/16), so each output
+// costs one byte->float convert and one FMA; the -8 offset is applied once
+// as acc[j] -= 8 * sum(a).  Lanes sharing a group are folded by a
+// butterfly reduce-scatter, waves through LDS, in fixed order.
+// ---------------------------------------------------------------------------
+
+template <int M, int CNT, int NB>
+__device__ __forceinline__ void rs_steps(float (&v)[NB][32], int lane, int &base)
+{
+    if constexpr (M < 64) {
+        if constexpr (CNT > 1) {
+            constexpr int H = CNT / 2;
+            const bool hi = (lane & M) != 0;
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+#pragma unroll
+                for (int i = 0; i < H; i++) {
+                    const float send = hi ? v[b][i] : v[b][i + H];
+                    const float keep = hi ? v[b][i + H] : v[b][i];
+                    v[b][i] = keep + __shfl_xor(send, M);
+                }
+            }
+            if (hi) base += H;
+            rs_steps<M * 2, H, NB>(v, lane, base);
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; b++) v[b][0] += __shfl_xor(v[b][0], M);
+            rs_steps<M * 2, 1, NB>(v, lane, base);
+        }
+    }
+}
+
+template <int T, int GB, int R, int NB, class Pro, class Epi>
+__global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
+{
+    constexpr int P = T / GB;
+    constexpr int KC = R * P;
+    constexpr int NW = T / 64;
+    constexpr int C = GB * 32;
+    constexpr int NL = 64 / GB;
+    constexpr int CNTF = (32 / NL) > 0 ? (32 / NL) : 1;
+    constexpr int DUP = (GB == 1) ? 32 : 0;     // lanes holding duplicates
+    static_assert(R == 8, "scale block is one 16-byte load");
+    __shared__ float xs[NB * KC];
+    __shared__ float red[NW * NB * C];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wv = t >> 6;
+    const int gl = t % GB, ph = t / GB;
+    const int items = w.S * w.CT;
+
+    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+        const int s = item / w.CT, c = item - s * w.CT;
+        const uint8_t *tile = w.data + (size_t)item * w.tile_bytes;
+        // weight stream first: independent of the prologue
+        u32x4 q[R];
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            q[r] = __builtin_nontemporal_load((const u32x4 *)(tile + ((size_t)r * T + t) * 16));
+        const u32x4 sc = __builtin_nontemporal_load((const u32x4 *)(tile + (size_t)R * T * 16 + (size_t)t * 16));
+
+        __syncthreads();               // xs / red of the previous item are free
+        pro(xs, s * KC, KC, c);
+        __syncthreads();
+
+        float acc[NB][32];
+        float asum[NB];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            asum[b] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 32; j++) acc[b][j] = 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t sw = sc[r >> 1];
+            const float scl = h2f((r & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+            float a[NB], a16[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                a[b] = scl * xs[b * KC + r * P + ph];
+                a16[b] = a[b] * 0.0625f;
+                asum[b] += a[b];
+            }
+#pragma unroll
+            for (int wi = 0; wi < 4; wi++) {
+                const uint32_t wd = q[r][wi];
+                const uint32_t lo = and_opaque(wd, 0x0F0F0F0Fu);
+                const uint32_t hi = and_opaque(wd, 0xF0F0F0F0u);
+#pragma unroll
+                for (int bb = 0; bb < 4; bb++) {
+                    const float fl = (float)((lo >> (8 * bb)) & 0xFFu);
+                    const float fh = (float)((hi >> (8 * bb)) & 0xFFu);
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        acc[b][wi * 8 + bb * 2] = fmaf(a[b], fl, acc[b][wi * 8 + bb * 2]);
+                        acc[b][wi * 8 + bb * 2 + 1] = fmaf(a16[b], fh, acc[b][wi * 8 + bb * 2 + 1]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float off = -8.0f * asum[b];
+#pragma unroll
+            for (int j = 0; j < 32; j++) acc[b][j] += off;
+        }
+
+        int base = 0;
+        rs_steps<GB, 32, NB>(acc, lane, base);
+        if ((lane & DUP) == 0) {
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int i = 0; i < CNTF; i++)
+                    red[(wv * NB + b) * C + gl * 32 + base + i] = acc[b][i];
+        }
+        __syncthreads();
+        for (int col = t; col < NB * C; col += T) {
+            const int b = col / C, cc = col - b * C;
+            float y = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; i++) y += red[(i * NB + b) * C + cc];
+            epi(s, b, c * C + cc, y);
+        }
+    }
+}
+
+template <int NB, class Pro, class Epi>
+static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st)
+{
+    const int items = w.S * w.CT;
+    const int grid = items;
+    switch (w.cfg) {
+    case TILE_S256: hipLaunchKernelGGL((k_gemv<256, 8, 8, NB, Pro, Epi>), dim3(grid), dim3(256), 0, st, w, pro, epi); break;
+    case TILE_S128: hipLaunchKernelGGL((k_gemv<128, 8, 8, NB, Pro, Epi>), dim3(grid), dim3(128), 0, st, w, pro, epi); break;
+    case TILE_D256: hipLaunchKernelGGL((k_gemv<256, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(256), 0, st, w, pro, epi); break;
+    case TILE_D384: hipLaunchKernelGGL((k_gemv<384, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(384), 0, st, w, pro, epi); break;
+    case TILE_D768: hipLaunchKernelGGL((k_gemv<768, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(768), 0, st, w, pro, epi); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// y[b][j] = (resid ? y : 0) + sum_s part[s][b][j] (+ bias[j]); summation in
+// slice order, then the residual/bias add, as gemv.rs:340-345 then the
+// caller's `+=` (talker.rs:110, code_predictor.rs:55).
+__global__ void k_reduce_parts(const float *part, int S, int NB, int npad, int n,
+                               float *y, int ld, const float *bias, int resid)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int b = blockIdx.y;
+    if (j >= n) return;
+    float v = 0.0f;
+    for (int s = 0; s < S; s++) v += part[((size_t)s * NB + b) * npad + j];
+    float *o = y + (size_t)b * ld + j;
+    if (resid) v = *o + v;
+    if (bias) v += bias[j];
+    *o = v;
+}
+
+static hipError_t reduce_parts(const float *part, int S, int NB, int npad, int n, float *y,
+                               int ld, const float *bias, int resid, hipStream_t st)
+{
+    hipLaunchKernelGGL(k_reduce_parts, dim3((n + 255) / 256, NB), dim3(256), 0, st, part, S, NB,
+                       npad, n, y, ld, bias, resid);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// talker: QKV partial sums -> QK-norm -> RoPE -> q buffer + paged KV append
+// (talker.rs:281-302).  Grid: one workgroup per KV head, 256 threads:
+// threads 0..127 own dim d of q head 2h and of k; 128..255 of q head 2h+1
+// and of v.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
+{
+    const int pg = kv.ptab[pos / KV_PAGE];
+    const size_t blk = ((size_t)layer * kv.n_phys + pg) * 2 + isv;
+    return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
+}
+
+__device__ __forceinline__ void rope_rotate(float *buf, int d, float v, const float *cs,
+                                            const float *sn, float &out)
+{
+    // buf holds the head's 128 values (post-norm); pair (i, i+64)
+    if (d < 64) out = buf[d] * cs[d] - buf[d + 64] * sn[d];
+    else out = buf[d] * cs[d - 64] + buf[d - 64] * sn[d - 64];
+}
+
+__global__ void __launch_bounds__(256)
+k_talker_qkv_fin(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
+                 const float *rope_cos, const float *rope_sin, const DevState *st,
+                 int64_t pos_override, int slot_override, int layer, KvPaged kv, float *qbuf)
+{
+    __shared__ float scratch[16];
+    __shared__ float vbuf[3][HEAD_DIM];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int d = t & 127, upper = t >> 7;
+    const int64_t pos = pos_override >= 0 ? pos_override : st->position;
+    const int slot = slot_override >= 0 ? slot_override : st->kv_len;
+    const int qcol = (2 * h + upper) * HEAD_DIM + d;
+    const int kvcol = 16 * HEAD_DIM + upper * 8 * HEAD_DIM + h * HEAD_DIM + d;   // k | v
+    float qv = 0.0f, kvv = 0.0f;
+    for (int s = 0; s < S; s++) {
+        const float *p = part + (size_t)s * npad;
+        qv += p[qcol];
+        kvv += p[kvcol];
+    }
+    // sums of squares: waves 0-1 -> q head 2h and k; waves 2-3 -> q head 2h+1
+    const float qsq = wave_sum(qv * qv);
+    const float ksq = wave_sum(kvv * kvv);
+    const int wv = t >> 6, lane = t & 63;
+    if (lane == 0) { scratch[wv] = qsq; scratch[4 + wv] = ksq; }
+    __syncthreads();
+    const float ssq = upper ? scratch[2] + scratch[3] : scratch[0] + scratch[1];
+    const float ssk = scratch[4] + scratch[5];
+    const float invq = 1.0f / sqrtf(ssq / 128.0f + 1e-6f);
+    const float invk = 1.0f / sqrtf(ssk / 128.0f + 1e-6f);
+    const float qn = qv * invq * h2f(qn_g[d]);
+    vbuf[upper][d] = qn;
+    if (!upper) vbuf[2][d] = kvv * invk * h2f(kn_g[d]);
+    __syncthreads();
+    const float *cs = rope_cos + pos * 64, *sn = rope_sin + pos * 64;
+    float qo, ko = 0.0f;
+    rope_rotate(vbuf[upper], d, qn, cs, sn, qo);
+    if (!upper) rope_rotate(vbuf[2], d, 0.0f, cs, sn, ko);
+    qbuf[qcol] = qo;
+    if (!upper) kv_ptr(kv, layer, slot, h, 0)[d] = ko;
+    else kv_ptr(kv, layer, slot, h, 1)[d] = kvv;
+}
+
+// ---------------------------------------------------------------------------
+// talker decode attention, split over 64-position pages (flash-decoding).
+// Work item (chunk c, kv head h): both query heads 2h, 2h+1 share one pass
+// over the page's K and V (GQA, talker.rs:310).  Writes per (chunk, q head)
+// the running max, the exp-sum and the unnormalised P.V.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_talker_attn(const float *qbuf, KvPaged kv, int layer, const DevState *st, int len_override,
+              float *am, float *al, float *aacc)
+{
+    __shared__ float sc[2][KV_PAGE];
+    __shared__ float pv[2][2][HEAD_DIM];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int L = len_override >= 0 ? len_override : st->kv_len + 1;
+    const int C = (L + KV_PAGE - 1) / KV_PAGE;
+    const float scale = 1.0f / sqrtf(128.0f);
+    const int j16 = lane & 15;
+    for (int item = blockIdx.x; item < 8 * C; item += gridDim.x) {
+        const int c = item >> 3, h = item & 7;
+        const int ntok = min(KV_PAGE, L - c * KV_PAGE);
+        const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
+        const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
+        float q0[8], q1[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            q0[i] = qbuf[(2 * h) * HEAD_DIM + j16 * 8 + i];
+            q1[i] = qbuf[(2 * h + 1) * HEAD_DIM + j16 * 8 + i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int tok = wv * 16 + it * 4 + (lane >> 4);
+            float d0 = 0.0f, d1 = 0.0f;
+            if (tok < ntok) {
+                const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
+                const float4 ka = kr[0], kb = kr[1];
+                const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    d0 = fmaf(q0[i], kk[i], d0);
+                    d1 = fmaf(q1[i], kk[i], d1);
+                }
+            }
+#pragma unroll
+            for (int m = 8; m >= 1; m >>= 1) {
+                d0 += __shfl_xor(d0, m);
+                d1 += __shfl_xor(d1, m);
+            }
+            if (j16 == 0) {
+                sc[0][tok] = tok < ntok ? d0 * scale : -INFINITY;
+                sc[1][tok] = tok < ntok ? d1 * scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        if (t < 128) {
+            const int hh = t >> 6, tok = t & 63;
+            const float v = sc[hh][tok];
+            const float m = wave_max(v);
+            const float p = tok < ntok ? expf(v - m) : 0.0f;
+            const float l = wave_sum(p);
+            sc[hh][tok] = p;
+            if (tok == 0) {
+                am[c * 16 + 2 * h + hh] = m;
+                al[c * 16 + 2 * h + hh] = l;
+            }
+        }
+        __syncthreads();
+        {
+            const int d = t & 127, half = t >> 7;
+            float a0 = 0.0f, a1 = 0.0f;
+            const int t0 = half * 32, t1 = min(t0 + 32, ntok);
+            for (int tok = t0; tok < t1; tok++) {
+                const float v = Vp[(size_t)tok * HEAD_DIM + d];
+                a0 = fmaf(sc[0][tok], v, a0);
+                a1 = fmaf(sc[1][tok], v, a1);
+            }
+            pv[half][0][d] = a0;
+            pv[half][1][d] = a1;
+        }
+        __syncthreads();
+        {
+            const int d = t & 127, hh = t >> 7;
+            aacc[((size_t)c * 16 + 2 * h + hh) * HEAD_DIM + d] = pv[0][hh][d] + pv[1][hh][d];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// predictor: QKV sums -> QK-norm -> RoPE -> KV append -> causal attention
+// over <= 16 positions, fused (code_predictor.rs:369-414, 457-498).
+// Grid: one workgroup per KV head; NB tokens at positions pos0..pos0+NB-1.
+// Output: attn[b][16*128] (final, normalised).
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
+            const float *rope_cos, const float *rope_sin, int pos0, float *Kc, float *Vc,
+            float *attn)
+{
+    __shared__ float scratch[16];
+    __shared__ float vbuf[3][HEAD_DIM];
+    __shared__ float qr[2][2][HEAD_DIM];          // [token][head][d]
+    __shared__ float Ks[PRED_KV_CAP][HEAD_DIM], Vs[PRED_KV_CAP][HEAD_DIM];
+    __shared__ float prob[2][2][PRED_KV_CAP];
+    const int h = blockIdx.x, t = threadIdx.x;
+    const int d = t & 127, upper = t >> 7, wv = t >> 6, lane = t & 63;
+    const size_t kvrow = 8 * HEAD_DIM;
+    for (int b = 0; b < NB; b++) {
+        const int pos = pos0 + b;
+        const int qcol = (2 * h + upper) * HEAD_DIM + d;
+        const int kvcol = 16 * HEAD_DIM + upper * 8 * HEAD_DIM + h * HEAD_DIM + d;
+        float qv = 0.0f, kvv = 0.0f;
+        for (int s = 0; s < S; s++) {
+            const float *p = part + ((size_t)s * NB + b) * npad;
+            qv += p[qcol];
+            kvv += p[kvcol];
+        }
+        const float qsq = wave_sum(qv * qv);
+        const float ksq = wave_sum(kvv * kvv);
+        __syncthreads();
+        if (lane == 0) { scratch[wv] = qsq; scratch[4 + wv] = ksq; }
+        __syncthreads();
+        const float ssq = upper ? scratch[2] + scratch[3] : scratch[0] + scratch[1];
+        const float ssk = scratch[4] + scratch[5];
+        const float qn = qv * (1.0f / sqrtf(ssq / 128.0f + 1e-6f)) * h2f(qn_g[d]);
+        vbuf[upper][d] = qn;
+        if (!upper) vbuf[2][d] = kvv * (1.0f / sqrtf(ssk / 128.0f + 1e-6f)) * h2f(kn_g[d]);
+        __syncthreads();
+        const float *cs = rope_cos + (size_t)pos * 64, *sn = rope_sin + (size_t)pos * 64;
+        float qo, ko = 0.0f;
+        rope_rotate(vbuf[upper], d, qn, cs, sn, qo);
+        if (!upper) rope_rotate(vbuf[2], d, 0.0f, cs, sn, ko);
+        qr[b][upper][d] = qo;
+        if (!upper) {
+            Ks[pos][d] = ko;
+            Kc[pos * kvrow + h * HEAD_DIM + d] = ko;
+        } else {
+            Vs[pos][d] = kvv;
+            Vc[pos * kvrow + h * HEAD_DIM + d] = kvv;
+        }
+    }
+    // earlier positions of this head, written by previous launches
+    for (int i = t; i < pos0 * HEAD_DIM; i += blockDim.x) {
+        const int p = i / HEAD_DIM, dd = i - p * HEAD_DIM;
+        Ks[p][dd] = Kc[p * kvrow + h * HEAD_DIM + dd];
+        Vs[p][dd] = Vc[p * kvrow + h * HEAD_DIM + dd];
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf(128.0f);
+    for (int b = 0; b < NB; b++) {
+        const int len = pos0 + b + 1;
+        // scores: thread -> (head hh, position p, 16-dim part j) = 2 x 16 x 8
+        {
+            const int hh = t >> 7, p = (t >> 3) & 15, j = t & 7;
+            float dot = 0.0f;
+            if (p < len) {
+#pragma unroll
+                for (int i = 0; i < 16; i++) dot = fmaf(qr[b][hh][j * 16 + i], Ks[p][j * 16 + i], dot);
+            }
+#pragma unroll
+            for (int m = 4; m >= 1; m >>= 1) dot += __shfl_xor(dot, m);
+            if (j == 0) prob[b][hh][p] = p < len ? dot * scale : -INFINITY;
+        }
+        __syncthreads();
+        // softmax_raw (gemv.rs:471-482), sequential per head
+        if (t < 2) {
+            float *sv = prob[b][t];
+            float m = -INFINITY;
+            for (int p = 0; p < len; p++) m = fmaxf(m, sv[p]);
+            float sum = 0.0f;
+            for (int p = 0; p < len; p++) { sv[p] = expf(sv[p] - m); sum += sv[p]; }
+            const float inv = 1.0f / sum;
+            for (int p = 0; p < len; p++) sv[p] *= inv;
+        }
+        __syncthreads();
+        {
+            const int hh = t >> 7;
+            float o = 0.0f;
+            for (int p = 0; p < len; p++) o += prob[b][hh][p] * Vs[p][d];
+            attn[(size_t)b * 16 * HEAD_DIM + (2 * h + hh) * HEAD_DIM + d] = o;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// argmax over the lm-head logits (sample_argmax, code_predictor.rs:335-341):
+// the LAST index among equal maxima.  Writes pred[slot]/used[slot]/prev.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(1024)
+k_argmax(const float *part, int S, int npad, int n, DevState *st, int slot,
+         const uint32_t *forced, uint32_t *codes_api)
+{
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    __shared__ int nanf;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    if (t == 0) nanf = 0;
+    __syncthreads();
+    float best = -INFINITY;
+    int bidx = -1;
+    for (int j = t; j < n; j += blockDim.x) {
+        float v = 0.0f;
+        for (int s = 0; s < S; s++) v += part[(size_t)s * npad + j];
+        if (isnan(v)) nanf = 1;
+        if (bidx < 0 || v >= best) { best = v; bidx = j; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = __shfl_xor(best, m);
+        const int oi = __shfl_xor(bidx, m);
+        if (oi >= 0 && (bidx < 0 || ov > best || (ov == best && oi > bidx))) { best = ov; bidx = oi; }
+    }
+    if (lane == 0) { bv[wv] = best; bi[wv] = bidx; }
+    __syncthreads();
+    if (t == 0) {
+        float b = bv[0];
+        int i0 = bi[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) {
+            if (bi[w] >= 0 && (i0 < 0 || bv[w] > b || (bv[w] == b && bi[w] > i0))) { b = bv[w]; i0 = bi[w]; }
+        }
+        uint32_t code = i0 < 0 ? 0u : (uint32_t)i0;
+        if (nanf) { st->nan_flag = 1; code = 0; }
+        st->pred[slot] = code;
+        uint32_t used = code;
+        if (st->force && forced) used = forced[(size_t)(st->frame_idx - st->forced_base) * 16 + slot];
+        st->used[slot] = used;
+        st->prev[slot] = used;
+        if (codes_api) codes_api[slot - 1] = code;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// talker input for the next step (generate_new.rs:638-654), bit-exact:
+// sum = 0; sum += e_g (g = 0..14); x = semantic + sum; x += text.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, const DevState *st, const float *text,
+          const float *pad, float *x, int H)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= H) return;
+    const float sem = q4_row_value(tcodec, st->used[0], j);
+    float sum = 0.0f;
+    for (int g = 0; g < n_groups; g++) {
+        Q4Rows e = cpemb;
+        e.packed += (size_t)g * e.rows * e.G * 16;
+        e.scales += (size_t)g * e.rows * e.G;
+        sum += q4_row_value(e, st->used[g + 1], j);
+    }
+    float v = sem + sum;
+    const int f = st->frame_idx;
+    const float *tr = (f < st->n_text) ? text + (size_t)f * H : pad;
+    v += tr[j];
+    x[j] = v;
+}
+
+// code_predictor.rs:287-300 for the operator-level API.
+__global__ void k_embed_sum(Q4Rows cpemb, int n_groups, const uint32_t *codes, float *out, int n)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    float sum = 0.0f;
+    for (int g = 0; g < n_groups; g++) {
+        Q4Rows e = cpemb;
+        e.packed += (size_t)g * e.rows * e.G * 16;
+        e.scales += (size_t)g * e.rows * e.G;
+        sum += q4_row_value(e, codes[g], j);
+    }
+    out[j] = sum;
+}
+
+__global__ void k_embed_row(Q4Rows e, const uint32_t *code, uint32_t code_imm, float *out, int n)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    out[j] = q4_row_value(e, code ? *code : code_imm, j);
+}
+
+// ---------------------------------------------------------------------------
+// sampler (sample_token, generate_new.rs:771-862) in one workgroup.
+// Ranking uses a bitonic sort of (p desc, index asc) == Rust's stable sort.
+// The final cumulative sum runs over nonzero probabilities in index order.
+// ---------------------------------------------------------------------------
+
+constexpr int SAMP_MAX = 4096;
+
+__device__ __forceinline__ bool rank_before(float pa, int ia, float pb, int ib)
+{
+    return pa > pb || (pa == pb && ia < ib);
+}
+
+__device__ void bitonic_sort_desc(float *kp, int *ki, int N)
+{
+    for (int k = 2; k <= N; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < N; i += blockDim.x) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const bool up = (i & k) == 0;   // this block sorted "before-first"
+                    const float pa = kp[i], pb = kp[ixj];
+                    const int ia = ki[i], ib = ki[ixj];
+                    const bool swap = up ? rank_before(pb, ib, pa, ia) : rank_before(pa, ia, pb, ib);
+                    if (swap) { kp[i] = pb; kp[ixj] = pa; ki[i] = ib; ki[ixj] = ia; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ float simple_rand_dev(uint64_t &s)
+{
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    return (float)s / 18446744073709551616.0f;   // (state as f32) / (u64::MAX as f32)
+}
+
+// mode 0: frame (reads state sampler params and temperature schedule, writes
+// code 0, honours stop/force); mode 1: API call with explicit params.
+struct SampleArgs {
+    float temperature, top_p, rep;
+    int top_k;
+    const uint32_t *prev;
+    int n_prev;
+};
+
+__global__ void __launch_bounds__(1024)
+k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, uint64_t *rng_api,
+          uint32_t *out_api, const uint32_t *forced)
+{
+    __shared__ float p[SAMP_MAX];
+    __shared__ float kp[SAMP_MAX];
+    __shared__ int ki[SAMP_MAX];
+    __shared__ float scratch[16];
+    __shared__ int cnt[1024];
+    __shared__ int nanf;
+    const int t = threadIdx.x;
+    if (mode == 0 && st->stop) return;
+    float temp, top_p, rep;
+    int top_k, n_prev;
+    const uint32_t *prev;
+    if (mode == 0) {
+        temp = st->frame_idx < st->onset_frames ? st->onset_temperature : st->temperature;
+        top_p = st->top_p; rep = st->rep_penalty; top_k = st->top_k;
+        prev = st->prev; n_prev = 16;
+    } else {
+        temp = api.temperature; top_p = api.top_p; rep = api.rep; top_k = api.top_k;
+        prev = api.prev; n_prev = api.n_prev;
+    }
+    if (t == 0) nanf = 0;
+    for (int i = t; i < n; i += blockDim.x) p[i] = logits[i];
+    __syncthreads();
+    if (t == 0 && rep != 1.0f) {
+        for (int i = 0; i < n_prev; i++) {
+            const uint32_t tok = prev[i];
+            if ((int)tok < n && tok < (uint32_t)n) {
+                const float v = p[tok];
+                p[tok] = v > 0.0f ? v / rep : v * rep;
+            }
+        }
+    }
+    __syncthreads();
+    const bool use_t = temp != 1.0f && temp > 0.0f;
+    float mx = -INFINITY;
+    for (int i = t; i < n; i += blockDim.x) {
+        float v = p[i];
+        if (use_t) v = v / temp;
+        p[i] = v;
+        mx = fmaxf(mx, v);
+    }
+    mx = block_max(mx, scratch);
+    float sum = 0.0f;
+    for (int i = t; i < n; i += blockDim.x) {
+        const float e = expf(p[i] - mx);
+        p[i] = e;
+        sum += e;
+    }
+    sum = block_sum(sum, scratch);
+    for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / sum;
+    __syncthreads();
+
+    const bool do_k = top_k > 0 && top_k < n;
+    const bool do_p = top_p > 0.0f && top_p < 1.0f;
+    if (do_k || do_p) {
+        int N = 1;
+        while (N < n) N <<= 1;
+        for (int i = t; i < N; i += blockDim.x) {
+            const float v = i < n ? p[i] : -1.0f;
+            if (i < n && isnan(v)) nanf = 1;
+            kp[i] = v;
+            ki[i] = i < n ? i : 0x7fffffff;
+        }
+        __syncthreads();
+        if (nanf) {
+            if (t == 0) {
+                st->nan_flag = 1;
+                if (mode == 0) { st->stop = 1; } else { *out_api = 0; }
+            }
+            return;
+        }
+        bitonic_sort_desc(kp, ki, N);
+        if (do_k) {
+            for (int r = t; r < n; r += blockDim.x)
+                if (r >= top_k) p[ki[r]] = 0.0f;
+            __syncthreads();
+            float s2 = 0.0f;
+            for (int i = t; i < n; i += blockDim.x) s2 += p[i];
+            s2 = block_sum(s2, scratch);
+            if (s2 > 0.0f)
+                for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s2;
+            __syncthreads();
+        }
+        if (do_p) {
+            // ranks are unchanged by the renormalisation; zeroed entries
+            // rank after all nonzero ones.
+            __shared__ int cutoff_s;
+            if (t == 0) {
+                float cum = 0.0f;
+                int cutoff = n;
+                for (int r = 0; r < n; r++) {
+                    const int idx = ki[r];
+                    const float pr = (do_k && r >= top_k) ? 0.0f : p[idx];
+                    cum += pr;
+                    if (cum >= top_p) { cutoff = r + 1; break; }
+                }
+                cutoff_s = cutoff < 1 ? 1 : cutoff;
+            }
+            __syncthreads();
+            for (int r = t; r < n; r += blockDim.x)
+                if (r >= cutoff_s) p[ki[r]] = 0.0f;
+            __syncthreads();
+            float s3 = 0.0f;
+            for (int i = t; i < n; i += blockDim.x) s3 += p[i];
+            s3 = block_sum(s3, scratch);
+            if (s3 > 0.0f)
+                for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s3;
+            __syncthreads();
+        }
+    }
+    // compact nonzero probabilities in index order
+    const int per = (n + blockDim.x - 1) / blockDim.x;
+    const int i0 = t * per, i1 = min(i0 + per, n);
+    int c = 0;
+    for (int i = i0; i < i1; i++) c += p[i] != 0.0f;
+    cnt[t] = c;
+    __syncthreads();
+    if (t == 0) {
+        int acc = 0;
+        for (int i = 0; i < (int)blockDim.x; i++) { const int v = cnt[i]; cnt[i] = acc; acc += v; }
+    }
+    __syncthreads();
+    {
+        int o = cnt[t];
+        for (int i = i0; i < i1; i++)
+            if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
+    }
+    __syncthreads();
+    if (t == 0) {
+        const int nz = cnt[blockDim.x - 1] + 0;   // exclusive prefix of the last thread
+        int total = nz;
+        {
+            const int li0 = (blockDim.x - 1) * per, li1 = min(li0 + per, n);
+            for (int i = li0; i < li1; i++) total += p[i] != 0.0f;
+        }
+        uint64_t rs = mode == 0 ? st->rng : *rng_api;
+        const float r = simple_rand_dev(rs);
+        float cs = 0.0f;
+        uint32_t res = 0;
+        for (int k = 0; k < total; k++) {
+            cs += kp[k];
+            if (r < cs) { res = (uint32_t)ki[k]; break; }
+        }
+        if (mode == 0) {
+            st->rng = rs;
+            st->pred[0] = res;
+            uint32_t used = res;
+            if (st->force && forced) used = forced[(size_t)(st->frame_idx - st->forced_base) * 16];
+            st->used[0] = used;
+            st->prev[0] = used;
+            if (st->eos_enabled && !st->force && res == st->eos_id) { st->stop = 1; st->eos = 1; }
+        } else {
+            *rng_api = rs;
+            *out_api = res;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// end of a talker step: logits from the codec-head partials, the normed
+// hidden kept, position and KV length advanced; in frame mode also the
+// frame's codes recorded.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(1024)
+k_step_end(const float *part, int S, int npad, int V, const float *hid_work, int H, float *logits,
+           float *hidden, DevState *st, int frame_mode, uint32_t *ring_pred, uint32_t *ring_used)
+{
+    const int t = threadIdx.x;
+    if (frame_mode && st->stop) return;
+    for (int j = t; j < V; j += blockDim.x) {
+        float v = 0.0f;
+        for (int s = 0; s < S; s++) v += part[(size_t)s * npad + j];
+        logits[j] = v;
+    }
+    for (int j = t; j < H; j += blockDim.x) hidden[j] = hid_work[j];
+    const int f = st->frame_idx;
+    if (frame_mode && t < 16) {
+        ring_pred[(size_t)(f - st->ring_base) * 16 + t] = st->pred[t];
+        ring_used[(size_t)(f - st->ring_base) * 16 + t] = st->used[t];
+    }
+    __syncthreads();
+    if (t == 0) {
+        st->position += 1;
+        st->kv_len += 1;
+        if (frame_mode) st->frame_idx = f + 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// KV cache copies between the paged layout and the reference layout
+// [len][8][128] (gemv.rs:75-77).  Pure copies: bit-exact.
+// ---------------------------------------------------------------------------
+
+__global__ void k_kv_gather(KvPaged kv, int layer, int len, float *K, float *V)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)len * 8 * HEAD_DIM) return;
+    const int pos = (int)(i / (8 * HEAD_DIM));
+    const int rem = (int)(i - (size_t)pos * 8 * HEAD_DIM);
+    const int h = rem / HEAD_DIM, d = rem % HEAD_DIM;
+    K[i] = kv_ptr(kv, layer, pos, h, 0)[d];
+    V[i] = kv_ptr(kv, layer, pos, h, 1)[d];
+}
+
+__global__ void k_kv_scatter(KvPaged kv, int layer, int len, const float *K, const float *V)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)len * 8 * HEAD_DIM) return;
+    const int pos = (int)(i / (8 * HEAD_DIM));
+    const int rem = (int)(i - (size_t)pos * 8 * HEAD_DIM);
+    const int h = rem / HEAD_DIM, d = rem % HEAD_DIM;
+    kv_ptr(kv, layer, pos, h, 0)[d] = K[i];
+    kv_ptr(kv, layer, pos, h, 1)[d] = V[i];
+}
+
+__global__ void k_fill_u32(uint32_t *p, uint32_t v, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+// ===========================================================================
+// host-side enqueue functions
+// ===========================================================================
+
+#define QCHK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return e_; } while (0)
+
+hipError_t enqueue_gemv_plain(const Q4Tiled &w, const float *x, int NB, int ld, float *part,
+                              hipStream_t st)
+{
+    if (NB == 1) return launch_gemv<1>(w, ProPlain<1>{x, ld, w.k}, EpiPart<1>{part, w.npad}, st);
+    if (NB == 2) return launch_gemv<2>(w, ProPlain<2>{x, ld, w.k}, EpiPart<2>{part, w.npad}, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t enqueue_gemv_store(const Q4Tiled &w, const float *x, float *y, const float *bias,
+                              float *part, hipStream_t st)
+{
+    if (w.S == 1)
+        return launch_gemv<1>(w, ProPlain<1>{x, w.k, w.k}, EpiStore<1>{y, w.n, w.n, bias}, st);
+    QCHK(launch_gemv<1>(w, ProPlain<1>{x, w.k, w.k}, EpiPart<1>{part, w.npad}, st));
+    return reduce_parts(part, w.S, 1, w.npad, w.n, y, w.n, bias, 0, st);
+}
+
+hipError_t enqueue_gemv_rows(const Q4Tiled &w, const float *X, int rows, float *Y, float *part,
+                             hipStream_t st)
+{
+    for (int r = 0; r < rows; r += 2) {
+        const int nb = rows - r >= 2 ? 2 : 1;
+        QCHK(enqueue_gemv_plain(w, X + (size_t)r * w.k, nb, w.k, part, st));
+        QCHK(reduce_parts(part, w.S, nb, w.npad, w.n, Y + (size_t)r * w.n, w.n, nullptr, 0, st));
+    }
+    return hipSuccess;
+}
+
+hipError_t enqueue_embed_row(const Q4Rows &e, const uint32_t *code_dev, uint32_t code, float *out,
+                             hipStream_t st)
+{
+    hipLaunchKernelGGL(k_embed_row, dim3((e.n + 255) / 256), dim3(256), 0, st, e, code_dev, code, out, e.n);
+    return hipGetLastError();
+}
+
+__global__ void k_silu(float *x, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = silu_f(x[i]);
+}
+
+hipError_t enqueue_silu(float *x, int n, hipStream_t st)
+{
+    hipLaunchKernelGGL(k_silu, dim3((n + 255) / 256), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
+
+hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *codes, float *out,
+                             hipStream_t st)
+{
+    hipLaunchKernelGGL(k_embed_sum, dim3((cp.n + 255) / 256), dim3(256), 0, st, cp, n_groups, codes, out, cp.n);
+    return hipGetLastError();
+}
+
+// One talker layer, decode (talker.rs:274-350).  x is updated in place.
+static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, float *x,
+                               const DevState *st, int64_t pos_ovr, int slot_ovr, int len_ovr,
+                               hipStream_t s)
+{
+    const LayerDev &L = m.layers[l];
+    const int H = m.hidden;
+    // 1. RMSNorm + fused q|k|v GEMV -> partials
+    QCHK(launch_gemv<1>(L.qkv, ProRms<1>{x, H, H, L.input_norm, nullptr},
+                        EpiPart<1>{ws.part_a, L.qkv.npad}, s));
+    // 2. sums, QK-norm, RoPE, KV append
+    hipLaunchKernelGGL(k_talker_qkv_fin, dim3(m.n_kv_heads), dim3(256), 0, s, ws.part_a, L.qkv.S,
+                       L.qkv.npad, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr,
+                       l, m.kv, ws.qbuf);
+    QCHK(hipGetLastError());
+    // 3. split-K attention over the pages
+    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.qbuf, m.kv, l, st,
+                       len_ovr, ws.am, ws.al, ws.aacc);
+    QCHK(hipGetLastError());
+    // 4. merge chunks + o_proj + residual
+    if (L.o.S == 1) {
+        QCHK(launch_gemv<1>(L.o, ProAttn{ws.am, ws.al, ws.aacc, st, len_ovr, m.n_heads},
+                            EpiResid<1>{x, H, H}, s));
+    } else {
+        QCHK(launch_gemv<1>(L.o, ProAttn{ws.am, ws.al, ws.aacc, st, len_ovr, m.n_heads},
+                            EpiPart<1>{ws.part_b, L.o.npad}, s));
+        QCHK(reduce_parts(ws.part_b, L.o.S, 1, L.o.npad, H, x, H, nullptr, 1, s));
+    }
+    // 5. RMSNorm + fused gate|up GEMV -> partials
+    QCHK(launch_gemv<1>(L.gate_up, ProRms<1>{x, H, H, L.post_norm, nullptr},
+                        EpiPart<1>{ws.part_a, L.gate_up.npad}, s));
+    // 6. silu(gate)*up + down + residual
+    const ProSwiglu<1> sw{ws.part_a, L.gate_up.S, L.gate_up.npad, m.inter};
+    if (L.down.S == 1) {
+        QCHK(launch_gemv<1>(L.down, sw, EpiResid<1>{x, H, H}, s));
+    } else {
+        QCHK(launch_gemv<1>(L.down, sw, EpiPart<1>{ws.part_b, L.down.npad}, s));
+        QCHK(reduce_parts(ws.part_b, L.down.S, 1, L.down.npad, H, x, H, nullptr, 1, s));
+    }
+    return hipSuccess;
+}
+
+// forward_with_embedding (talker.rs:263-360) on the workspace input ws.x:
+// 28 layers, final norm (hidden -> ws.hid_work), codec head partials
+// (ws.part_head), then k_step_end.
+hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
+                               hipStream_t s)
+{
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, -1, -1, -1, s));
+    QCHK(launch_gemv<1>(m.codec_head, ProRms<1>{ws.x, m.hidden, m.hidden, m.final_norm, ws.hid_work},
+                        EpiPart<1>{ws.part_head, m.codec_head.npad}, s));
+    hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1024), 0, s, ws.part_head, m.codec_head.S,
+                       m.codec_head.npad, m.vocab, ws.hid_work, m.hidden, ws.logits, ws.hidden, st,
+                       frame_mode, ws.ring_pred, ws.ring_used);
+    return hipGetLastError();
+}
+
+// One row of a prefill: same layers, RoPE at pos, KV slot = pos - start +
+// kv_len0 handled by the overrides; no codec head.
+hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st,
+                              int64_t pos, int slot, hipStream_t s)
+{
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, pos, slot, slot + 1, s));
+    return hipSuccess;
+}
+
+hipError_t enqueue_final_norm(const TalkerDev &m, const Workspace &ws, float *hidden_out, hipStream_t s)
+{
+    // normed hidden only (talker.rs:480-481): reuse the codec-head prologue
+    QCHK(launch_gemv<1>(m.codec_head, ProRms<1>{ws.x, m.hidden, m.hidden, m.final_norm, hidden_out},
+                        EpiPart<1>{ws.part_head, m.codec_head.npad}, s));
+    return hipSuccess;
+}
+
+hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const float *hidden, float *logits,
+                              hipStream_t s)
+{
+    QCHK(launch_gemv<1>(m.codec_head, ProPlain<1>{hidden, m.hidden, m.hidden},
+                        EpiPart<1>{ws.part_head, m.codec_head.npad}, s));
+    return reduce_parts(ws.part_head, m.codec_head.S, 1, m.codec_head.npad, m.vocab, logits, m.vocab,
+                        nullptr, 0, s);
+}
+
+// One predictor layer over NB tokens at positions pos0.. (code_predictor.rs:
+// 354-432 for NB=2, 450-510 for NB=1).  x: [NB][h].
+template <int NB>
+static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, float *x, int pos0,
+                             hipStream_t s)
+{
+    const LayerDev &L = p.layers[l];
+    const int h = p.hidden;
+    QCHK(launch_gemv<NB>(L.qkv, ProRms<NB>{x, h, h, L.input_norm, nullptr},
+                         EpiPart<NB>{ws.part_a, L.qkv.npad}, s));
+    hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_a, L.qkv.S, NB,
+                       L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
+                       ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM,
+                       ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM, ws.pattn);
+    QCHK(hipGetLastError());
+    const int qd = p.n_heads * HEAD_DIM;
+    if (L.o.S == 1) {
+        QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiResid<NB>{x, h, h}, s));
+    } else {
+        QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiPart<NB>{ws.part_b, L.o.npad}, s));
+        QCHK(reduce_parts(ws.part_b, L.o.S, NB, L.o.npad, h, x, h, nullptr, 1, s));
+    }
+    QCHK(launch_gemv<NB>(L.gate_up, ProRms<NB>{x, h, h, L.post_norm, nullptr},
+                         EpiPart<NB>{ws.part_a, L.gate_up.npad}, s));
+    const ProSwiglu<NB> sw{ws.part_a, L.gate_up.S, L.gate_up.npad, p.inter};
+    if (L.down.S == 1) {
+        QCHK(launch_gemv<NB>(L.down, sw, EpiResid<NB>{x, h, h}, s));
+    } else {
+        QCHK(launch_gemv<NB>(L.down, sw, EpiPart<NB>{ws.part_b, L.down.npad}, s));
+        QCHK(reduce_parts(ws.part_b, L.down.S, NB, L.down.npad, h, x, h, nullptr, 1, s));
+    }
+    return hipSuccess;
+}
+
+// generate_acoustic_codes (code_predictor.rs:218-273).  Inputs: talker
+// hidden (ws.hidden or `hidden`), semantic code in st->used[0] (frame mode)
+// or the explicit semantic embedding `sem` (API mode).  Codes go to
+// st->pred[1..15] / st->used[1..15] (and codes_api when given).
+hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, const Workspace &ws,
+                                   DevState *st, const float *hidden, const float *sem,
+                                   const uint32_t *forced, uint32_t *codes_api, hipStream_t s)
+{
+    const int h = p.hidden;
+    float *x = ws.px;   // [2][h]
+    // projections of [talker hidden, semantic embedding] (:235-241)
+    if (sem) {
+        // API mode: stage [hidden; sem] into ws.pin (2 rows) then plain GEMV
+        QCHK(hipMemcpyAsync(ws.pin, hidden, sizeof(float) * m.hidden, hipMemcpyDeviceToDevice, s));
+        QCHK(hipMemcpyAsync(ws.pin + m.hidden, sem, sizeof(float) * m.hidden, hipMemcpyDeviceToDevice, s));
+        QCHK(launch_gemv<2>(p.proj, ProPlain<2>{ws.pin, m.hidden, m.hidden},
+                            EpiPart<2>{ws.part_b, p.proj.npad}, s));
+    } else {
+        QCHK(launch_gemv<2>(p.proj, ProHidEmbed{hidden, m.codec_rows, &st->used[0], m.hidden},
+                            EpiPart<2>{ws.part_b, p.proj.npad}, s));
+    }
+    QCHK(reduce_parts(ws.part_b, p.proj.S, 2, p.proj.npad, h, x, h, p.proj_bias, 0, s));
+    for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, x, 0, s));
+    // final norm of the last row + lm_head[0] + argmax (:247-248)
+    QCHK(launch_gemv<1>(p.heads[0], ProRms<1>{x + h, h, h, p.final_norm, nullptr},
+                        EpiPart<1>{ws.part_head, p.heads[0].npad}, s));
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[0].S,
+                       p.heads[0].npad, p.vocab, st, 1, forced, codes_api);
+    QCHK(hipGetLastError());
+    for (int g = 1; g < p.n_groups; g++) {
+        // embed the previous code with codebook g-1, project (:255-260)
+        Q4Rows e = p.emb_rows;
+        e.packed += (size_t)(g - 1) * e.rows * e.G * 16;
+        e.scales += (size_t)(g - 1) * e.rows * e.G;
+        QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_b, p.proj.npad}, s));
+        QCHK(reduce_parts(ws.part_b, p.proj.S, 1, p.proj.npad, h, x, h, p.proj_bias, 0, s));
+        for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, x, 1 + g, s));
+        QCHK(launch_gemv<1>(p.heads[g], ProRms<1>{x, h, h, p.final_norm, nullptr},
+                            EpiPart<1>{ws.part_head, p.heads[g].npad}, s));
+        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[g].S,
+                           p.heads[g].npad, p.vocab, st, g + 1, forced, codes_api);
+        QCHK(hipGetLastError());
+    }
+    return hipSuccess;
+}
+
+// One frame (generate_new.rs:606-675): sample code 0, predictor chain,
+// fuse embeddings + text, talker step, record.
+hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
+                         const uint32_t *forced, hipStream_t s)
+{
+    SampleArgs none{};
+    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(1024), 0, s, ws.logits, m.vocab, st, 0, none,
+                       (uint64_t *)nullptr, (uint32_t *)nullptr, forced);
+    QCHK(hipGetLastError());
+    QCHK(enqueue_predictor_chain(p, m, ws, st, ws.hidden, nullptr, forced, nullptr, s));
+    hipLaunchKernelGGL(k_combine, dim3((m.hidden + 255) / 256), dim3(256), 0, s, m.codec_rows,
+                       p.emb_rows, p.n_groups, st, ws.text, ws.pad, ws.x, m.hidden);
+    QCHK(hipGetLastError());
+    return enqueue_talker_step(m, ws, st, 1, s);
+}
+
+hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &a, uint64_t *rng_dev,
+                              uint32_t *out_dev, DevState *st, hipStream_t s)
+{
+    SampleArgs sa{a.temperature, a.top_p, a.rep, a.top_k, a.prev, a.n_prev};
+    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(1024), 0, s, logits, n, st, 1, sa, rng_dev, out_dev,
+                       (const uint32_t *)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t enqueue_kv_gather(const KvPaged &kv, int layer, int len, float *K, float *V, hipStream_t s)
+{
+    const size_t n = (size_t)len * 8 * HEAD_DIM;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_kv_gather, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kv, layer, len, K, V);
+    return hipGetLastError();
+}
+
+hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float *K, const float *V,
+                              hipStream_t s)
+{
+    const size_t n = (size_t)len * 8 * HEAD_DIM;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_kv_scatter, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, kv, layer, len, K, V);
+    return hipGetLastError();
+}
+
+hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s)
+{
+    const LayerDev &L = m.layers[l];
+    return launch_gemv<1>(L.gate_up, ProRms<1>{ws.x, m.hidden, m.hidden, L.post_norm, nullptr},
+                          EpiPart<1>{ws.part_a, L.gate_up.npad}, s);
+}
+
+hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int len, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.qbuf, m.kv, l,
+                       (const DevState *)nullptr, len, ws.am, ws.al, ws.aacc);
+    return hipGetLastError();
+}
+
+}  // namespace qtts

@@ -1,0 +1,1130 @@
+// qtts_runtime.cpp — context, weight upload (repack into device tiles),
+// KV-cache management, frame graphs and the C ABI declared in
+// include/qtts.h.
+#include "../../include/qtts.h"
+#include "qtts_device.h"
+#include "qtts_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <thread>
+#include <vector>
+
+using namespace qtts;
+
+struct qtts_w {
+    Q4Tiled t;
+    Q4Rows rows;
+    float *x = nullptr, *y = nullptr, *part = nullptr;
+    std::vector<void *> allocs;
+};
+
+struct qtts_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    int64_t kv_cap = 4096;
+
+    bool has_model = false;
+    TalkerDev tm{};
+    PredictorDev pm{};
+    std::vector<LayerDev> tlayers, players;
+    std::vector<Q4Tiled> pheads;
+    std::vector<void *> model_allocs;
+    Workspace ws{};
+    std::vector<void *> ws_allocs;
+    int64_t text_cap = 0;
+
+    DevState *st_gen = nullptr, *st_api = nullptr;   // device
+    DevState *h_st = nullptr;                        // pinned host mirror
+    uint32_t *h_ring = nullptr;                      // pinned [RING_FRAMES][16]
+    uint32_t *d_forced = nullptr;                    // forced codes
+    int64_t forced_cap = 0;
+    uint32_t *d_codes_api = nullptr;                 // [16]
+    uint64_t *d_rng_api = nullptr;
+    uint32_t *d_prev_api = nullptr;                  // [4096]
+    float *d_io = nullptr;                           // API staging, 2 rows of max(hidden,vocab,4096)
+    float *d_io2 = nullptr;
+    int64_t io_floats = 0;
+
+    hipGraphExec_t frame_exec = nullptr;
+    bool gen_started = false;
+};
+
+// ---------------------------------------------------------------------------
+// error helpers
+// ---------------------------------------------------------------------------
+
+static int fail(qtts_ctx *c, int code, const char *fmt, ...)
+{
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+#define HIPCHK(c, x)                                                                       \
+    do {                                                                                   \
+        hipError_t e_ = (x);                                                               \
+        if (e_ != hipSuccess)                                                              \
+            return fail((c), e_ == hipErrorOutOfMemory ? QTTS_ERR_OOM : QTTS_ERR_HIP,      \
+                        "%s: %s (%s:%d)", #x, hipGetErrorString(e_), __FILE__, __LINE__);  \
+    } while (0)
+
+#define RCHK(x)                          \
+    do {                                 \
+        int r_ = (x);                    \
+        if (r_ != QTTS_OK) return r_;    \
+    } while (0)
+
+template <class T>
+static int dev_alloc(qtts_ctx *c, std::vector<void *> &list, T **p, size_t count)
+{
+    void *m = nullptr;
+    HIPCHK(c, hipMalloc(&m, std::max<size_t>(count * sizeof(T), 256)));
+    list.push_back(m);
+    *p = (T *)m;
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// repacking a (column-concatenated) Q4 weight into device tiles
+// ---------------------------------------------------------------------------
+
+struct SrcW {
+    const uint8_t *packed;
+    const uint16_t *scales;
+    int64_t k, n;
+};
+
+static int env_tile(const char *name, int dflt)
+{
+    char key[64];
+    snprintf(key, sizeof key, "QTTS_TILE_%s", name);
+    const char *v = getenv(key);
+    if (!v || !*v) return dflt;
+    const int x = atoi(v);
+    return (x >= 0 && x < TILE_COUNT) ? x : dflt;
+}
+
+// Split-K tiling for weights whose partial sums a consumer reduces;
+// single-slice ("direct") tiling for the residual projections.
+static int choose_cfg(int64_t k, int64_t G, bool direct)
+{
+    if (direct) {
+        if (k <= 2048) return TILE_D256;
+        if (k <= 3072) return TILE_D384;
+        if (k <= 6144) return TILE_D768;
+    }
+    const int64_t items = ((k + 255) / 256) * ((G + 7) / 8);
+    return items >= 128 ? TILE_S256 : TILE_S128;
+}
+
+static void parallel_for(int64_t n, const std::function<void(int64_t, int64_t)> &fn);
+
+static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vector<SrcW> &srcs, int cfg,
+                       Q4Tiled *out, void **mem_out)
+{
+    if (srcs.empty()) return fail(c, QTTS_ERR_INVALID, "empty weight list");
+    const int64_t k = srcs[0].k;
+    std::vector<int64_t> g0;   // first group of each source
+    int64_t Gt = 0;
+    for (const SrcW &s : srcs) {
+        if (s.k != k) return fail(c, QTTS_ERR_INVALID, "fused weights disagree on k");
+        if (!s.packed || !s.scales || s.k <= 0 || s.n <= 0)
+            return fail(c, QTTS_ERR_INVALID, "weight with null data or bad shape (k=%lld n=%lld)",
+                        (long long)s.k, (long long)s.n);
+        if (srcs.size() > 1 && s.n % 32) return fail(c, QTTS_ERR_INVALID, "fused weight n %% 32 != 0");
+        g0.push_back(Gt);
+        Gt += s.n / 32;
+    }
+    if (Gt == 0) return fail(c, QTTS_ERR_INVALID, "weight narrower than one 32-column group");
+    const TileShape ts = tile_shape(cfg);
+    const int P = ts.T / ts.GB, KC = ts.R * P;
+    const int64_t G = (Gt + ts.GB - 1) / ts.GB * ts.GB;
+    const int64_t S = (k + KC - 1) / KC, CT = G / ts.GB;
+    const int64_t tile_bytes = (int64_t)ts.R * ts.T * 16 + (int64_t)ts.T * ts.R * 2;
+    const size_t total = (size_t)(S * CT * tile_bytes);
+    std::vector<uint8_t> host(total);
+    parallel_for(S * CT, [&](int64_t i0, int64_t i1) {
+        for (int64_t item = i0; item < i1; item++) {
+            const int64_t s = item / CT, ct = item % CT;
+            uint8_t *tile = host.data() + item * tile_bytes;
+            uint16_t *scl = (uint16_t *)(tile + (size_t)ts.R * ts.T * 16);
+            for (int t = 0; t < ts.T; t++) {
+                const int64_t g = ct * ts.GB + t % ts.GB;
+                int si = -1;
+                int64_t lg = 0;
+                if (g < Gt) {
+                    si = (int)(std::upper_bound(g0.begin(), g0.end(), g) - g0.begin()) - 1;
+                    lg = g - g0[si];
+                }
+                for (int r = 0; r < ts.R; r++) {
+                    const int64_t row = s * KC + (int64_t)r * P + t / ts.GB;
+                    uint8_t *dst = tile + ((size_t)r * ts.T + t) * 16;
+                    uint16_t sc = 0;
+                    if (si >= 0 && row < k) {
+                        const SrcW &w = srcs[si];
+                        const int64_t Gw = w.n / 32;
+                        memcpy(dst, w.packed + (size_t)row * Gw * 16 + lg * 16, 16);
+                        sc = w.scales[(size_t)row * Gw + lg];
+                    } else {
+                        memset(dst, 0x88, 16);
+                    }
+                    scl[(size_t)t * ts.R + r] = sc;
+                }
+            }
+        }
+    });
+    void *mem = nullptr;
+    HIPCHK(c, hipMalloc(&mem, total));
+    allocs.push_back(mem);
+    HIPCHK(c, hipMemcpy(mem, host.data(), total, hipMemcpyHostToDevice));
+    Q4Tiled d{};
+    d.data = (const uint8_t *)mem;
+    d.k = (int32_t)k;
+    int64_t n_all = 0;
+    for (const SrcW &s : srcs) n_all += s.n;
+    d.n = (int32_t)(srcs.size() > 1 ? Gt * 32 : n_all);
+    d.G = (int32_t)G;
+    d.S = (int32_t)S;
+    d.CT = (int32_t)CT;
+    d.KC = KC;
+    d.cfg = cfg;
+    d.tile_bytes = (int32_t)tile_bytes;
+    d.npad = (int32_t)(G * 32);
+    *out = d;
+    if (mem_out) *mem_out = mem;
+    return QTTS_OK;
+}
+
+static void parallel_for(int64_t n, const std::function<void(int64_t, int64_t)> &fn)
+{
+    int nt = (int)std::min<int64_t>(std::max(1u, std::thread::hardware_concurrency()), 16);
+    if (n < 64 || nt <= 1) { fn(0, n); return; }
+    std::vector<std::thread> th;
+    const int64_t per = (n + nt - 1) / nt;
+    for (int i = 0; i < nt; i++) {
+        const int64_t a = i * per, b = std::min(n, a + per);
+        if (a >= b) break;
+        th.emplace_back([&fn, a, b] { fn(a, b); });
+    }
+    for (auto &t : th) t.join();
+}
+
+// Reference-layout copy of row-indexed tables (embeddings).
+static int upload_rows(qtts_ctx *c, std::vector<void *> &allocs, const std::vector<qtts_q4_host> &ws,
+                       Q4Rows *out)
+{
+    const int64_t rows = ws[0].k, n = ws[0].n, G = n / 32;
+    for (const auto &w : ws)
+        if (w.k != rows || w.n != n || !w.packed || !w.scales)
+            return fail(c, QTTS_ERR_INVALID, "embedding tables disagree in shape");
+    const size_t pb = (size_t)rows * G * 16, sb = (size_t)rows * G * 2;
+    uint8_t *pm = nullptr;
+    uint16_t *sm = nullptr;
+    RCHK(dev_alloc(c, allocs, &pm, pb * ws.size()));
+    RCHK(dev_alloc(c, allocs, &sm, (sb / 2) * ws.size()));
+    for (size_t i = 0; i < ws.size(); i++) {
+        HIPCHK(c, hipMemcpy(pm + i * pb, ws[i].packed, pb, hipMemcpyHostToDevice));
+        HIPCHK(c, hipMemcpy((uint8_t *)sm + i * sb, ws[i].scales, sb, hipMemcpyHostToDevice));
+    }
+    out->packed = pm;
+    out->scales = sm;
+    out->rows = (int32_t)rows;
+    out->n = (int32_t)n;
+    out->G = (int32_t)G;
+    return QTTS_OK;
+}
+
+template <class T>
+static int upload_vec(qtts_ctx *c, std::vector<void *> &allocs, const T *src, size_t count, const T **out)
+{
+    if (!src) return fail(c, QTTS_ERR_INVALID, "null vector in model descriptor");
+    T *d = nullptr;
+    RCHK(dev_alloc(c, allocs, &d, count));
+    HIPCHK(c, hipMemcpy(d, src, count * sizeof(T), hipMemcpyHostToDevice));
+    *out = d;
+    return QTTS_OK;
+}
+
+static SrcW src_of(const qtts_q4_host &w) { return SrcW{w.packed, w.scales, w.k, w.n}; }
+
+static int upload_layer(qtts_ctx *c, const qtts_layer_host &L, int hidden, int head_dim, LayerDev *out,
+                        bool predictor)
+{
+    auto &A = c->model_allocs;
+    const char *pfx = predictor ? "P" : "T";
+    char name[32];
+    const int64_t Gqkv = (L.q_proj.n + L.k_proj.n + L.v_proj.n) / 32;
+    snprintf(name, sizeof name, "%sQKV", pfx);
+    RCHK(build_tiled(c, A, {src_of(L.q_proj), src_of(L.k_proj), src_of(L.v_proj)},
+                     env_tile(name, choose_cfg(L.q_proj.k, Gqkv, false)), &out->qkv, nullptr));
+    snprintf(name, sizeof name, "%sO", pfx);
+    RCHK(build_tiled(c, A, {src_of(L.o_proj)}, env_tile(name, choose_cfg(L.o_proj.k, L.o_proj.n / 32, true)),
+                     &out->o, nullptr));
+    const int64_t Ggu = (L.gate_proj.n + L.up_proj.n) / 32;
+    snprintf(name, sizeof name, "%sGU", pfx);
+    RCHK(build_tiled(c, A, {src_of(L.gate_proj), src_of(L.up_proj)},
+                     env_tile(name, choose_cfg(L.gate_proj.k, Ggu, false)), &out->gate_up, nullptr));
+    snprintf(name, sizeof name, "%sDOWN", pfx);
+    RCHK(build_tiled(c, A, {src_of(L.down_proj)},
+                     env_tile(name, choose_cfg(L.down_proj.k, L.down_proj.n / 32, true)), &out->down, nullptr));
+    RCHK(upload_vec(c, A, L.q_norm, head_dim, &out->q_norm));
+    RCHK(upload_vec(c, A, L.k_norm, head_dim, &out->k_norm));
+    RCHK(upload_vec(c, A, L.input_norm, hidden, &out->input_norm));
+    RCHK(upload_vec(c, A, L.post_attn_norm, hidden, &out->post_norm));
+    if (L.q_proj.n != 16 * HEAD_DIM || L.k_proj.n != 8 * HEAD_DIM || L.v_proj.n != 8 * HEAD_DIM)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "device path expects 16 q heads / 8 kv heads of 128");
+    if (L.o_proj.n != hidden || L.down_proj.n != hidden || L.q_proj.k != hidden)
+        return fail(c, QTTS_ERR_INVALID, "layer shapes disagree with hidden size %d", hidden);
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+
+static void free_list(std::vector<void *> &l)
+{
+    for (void *p : l) hipFree(p);
+    l.clear();
+}
+
+static void drop_graph(qtts_ctx *c)
+{
+    if (c->frame_exec) hipGraphExecDestroy(c->frame_exec);
+    c->frame_exec = nullptr;
+}
+
+extern "C" int qtts_ctx_create(int device, int64_t kv_capacity, qtts_ctx **out)
+{
+    if (!out) return QTTS_ERR_INVALID;
+    *out = nullptr;
+    qtts_ctx *c = new qtts_ctx();
+    c->device = device;
+    c->kv_cap = kv_capacity <= 0 ? 4096 : kv_capacity;
+    if (c->kv_cap > (int64_t)MAX_CHUNKS * KV_PAGE || c->kv_cap % KV_PAGE) {
+        delete c;
+        return QTTS_ERR_CAPACITY;
+    }
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) {
+        delete c;
+        return QTTS_ERR_HIP;
+    }
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return QTTS_ERR_HIP;
+    }
+    bool ok = hipMalloc(&c->st_gen, sizeof(DevState)) == hipSuccess &&
+              hipMalloc(&c->st_api, sizeof(DevState)) == hipSuccess &&
+              hipHostMalloc(&c->h_st, sizeof(DevState), hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc(&c->h_ring, sizeof(uint32_t) * RING_FRAMES * 16 * 2, hipHostMallocDefault) == hipSuccess &&
+              hipMalloc(&c->d_codes_api, sizeof(uint32_t) * 16) == hipSuccess &&
+              hipMalloc(&c->d_rng_api, sizeof(uint64_t)) == hipSuccess &&
+              hipMalloc(&c->d_prev_api, sizeof(uint32_t) * 4096) == hipSuccess;
+    if (!ok) {
+        qtts_ctx_destroy(c);
+        return QTTS_ERR_OOM;
+    }
+    memset(c->h_st, 0, sizeof(DevState));
+    hipMemcpy(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice);
+    hipMemcpy(c->st_api, c->h_st, sizeof(DevState), hipMemcpyHostToDevice);
+    *out = c;
+    return QTTS_OK;
+}
+
+static void free_model(qtts_ctx *c)
+{
+    drop_graph(c);
+    free_list(c->model_allocs);
+    free_list(c->ws_allocs);
+    c->has_model = false;
+    c->gen_started = false;
+    c->text_cap = 0;
+}
+
+extern "C" void qtts_ctx_destroy(qtts_ctx *c)
+{
+    if (!c) return;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    free_model(c);
+    if (c->d_forced) hipFree(c->d_forced);
+    if (c->d_io) hipFree(c->d_io);
+    if (c->d_io2) hipFree(c->d_io2);
+    if (c->st_gen) hipFree(c->st_gen);
+    if (c->st_api) hipFree(c->st_api);
+    if (c->h_st) hipHostFree(c->h_st);
+    if (c->h_ring) hipHostFree(c->h_ring);
+    if (c->d_codes_api) hipFree(c->d_codes_api);
+    if (c->d_rng_api) hipFree(c->d_rng_api);
+    if (c->d_prev_api) hipFree(c->d_prev_api);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+}
+
+extern "C" const char *qtts_last_error(const qtts_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+extern "C" int qtts_sync(qtts_ctx *c)
+{
+    if (!c) return QTTS_ERR_INVALID;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" void *qtts_stream(qtts_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+static int ensure_io(qtts_ctx *c, int64_t floats)
+{
+    if (floats <= c->io_floats) return QTTS_OK;
+    if (c->d_io) hipFree(c->d_io);
+    if (c->d_io2) hipFree(c->d_io2);
+    c->d_io = c->d_io2 = nullptr;
+    HIPCHK(c, hipMalloc(&c->d_io, floats * sizeof(float)));
+    HIPCHK(c, hipMalloc(&c->d_io2, floats * sizeof(float)));
+    c->io_floats = floats;
+    return QTTS_OK;
+}
+
+// Copy n floats in (host or device source) to a device buffer.
+static int stage_in(qtts_ctx *c, const float *src, int64_t n, float *dst, int flags)
+{
+    HIPCHK(c, hipMemcpyAsync(dst, src, n * sizeof(float),
+                             (flags & QTTS_DEVICE_PTRS) ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
+                             c->stream));
+    return QTTS_OK;
+}
+
+static int stage_out(qtts_ctx *c, const float *src, int64_t n, float *dst, int flags)
+{
+    if (!dst) return QTTS_OK;
+    HIPCHK(c, hipMemcpyAsync(dst, src, n * sizeof(float),
+                             (flags & QTTS_DEVICE_PTRS) ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost,
+                             c->stream));
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// operator level
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_q4_upload(qtts_ctx *c, const qtts_q4_host *w, qtts_w **out)
+{
+    if (!c || !w || !out) return QTTS_ERR_INVALID;
+    *out = nullptr;
+    hipSetDevice(c->device);
+    qtts_w *h = new qtts_w();
+    const int64_t G = w->n / 32;
+    int r = build_tiled(c, h->allocs, {src_of(*w)}, env_tile("GEMV", choose_cfg(w->k, G, false)), &h->t, nullptr);
+    if (r == QTTS_OK) r = upload_rows(c, h->allocs, {*w}, &h->rows);
+    if (r == QTTS_OK) r = dev_alloc(c, h->allocs, &h->x, (size_t)w->k * 2);
+    if (r == QTTS_OK) r = dev_alloc(c, h->allocs, &h->y, (size_t)std::max<int64_t>(w->n, h->t.npad) * 2);
+    if (r == QTTS_OK) r = dev_alloc(c, h->allocs, &h->part, (size_t)h->t.S * 2 * h->t.npad);
+    if (r != QTTS_OK) {
+        free_list(h->allocs);
+        delete h;
+        return r;
+    }
+    *out = h;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_q4_free(qtts_ctx *c, qtts_w *w)
+{
+    if (!c || !w) return QTTS_ERR_INVALID;
+    hipStreamSynchronize(c->stream);
+    free_list(w->allocs);
+    delete w;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_gemv_q4(qtts_ctx *c, const qtts_w *w, const float *x, float *y, int flags)
+{
+    if (!c || !w || !x || !y) return QTTS_ERR_INVALID;
+    RCHK(stage_in(c, x, w->t.k, w->x, flags));
+    // columns past the last full group come out zero: their padded groups
+    // carry zero scales (gemv.rs:255 starts from vec![0.0; n])
+    HIPCHK(c, enqueue_gemv_store(w->t, w->x, w->y, nullptr, w->part, c->stream));
+    RCHK(stage_out(c, w->y, w->t.n, y, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_gemm_q4(qtts_ctx *c, const qtts_w *w, const float *X, int64_t rows, float *Y, int flags)
+{
+    if (!c || !w || !X || !Y || rows < 0) return QTTS_ERR_INVALID;
+    if (rows == 0) return QTTS_OK;
+    RCHK(ensure_io(c, std::max<int64_t>(rows * w->t.k, rows * w->t.npad)));
+    RCHK(stage_in(c, X, rows * w->t.k, c->d_io, flags));
+    HIPCHK(c, hipMemsetAsync(c->d_io2, 0, rows * w->t.n * sizeof(float), c->stream));
+    HIPCHK(c, enqueue_gemv_rows(w->t, c->d_io, (int)rows, c->d_io2, w->part, c->stream));
+    RCHK(stage_out(c, c->d_io2, rows * w->t.n, Y, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_embed_lookup_q4(qtts_ctx *c, const qtts_w *w, int64_t row, float *out, int flags)
+{
+    if (!c || !w || !out) return QTTS_ERR_INVALID;
+    if (row < 0 || row >= w->rows.rows) return fail(c, QTTS_ERR_INVALID, "row %lld out of range", (long long)row);
+    HIPCHK(c, hipMemsetAsync(w->y, 0, w->rows.n * sizeof(float), c->stream));
+    Q4Rows e = w->rows;
+    e.n = e.G * 32;
+    HIPCHK(c, enqueue_embed_row(e, nullptr, (uint32_t)row, w->y, c->stream));
+    RCHK(stage_out(c, w->y, w->rows.n, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// model upload
+// ---------------------------------------------------------------------------
+
+static int alloc_workspace(qtts_ctx *c)
+{
+    auto &A = c->ws_allocs;
+    Workspace &w = c->ws;
+    const TalkerDev &m = c->tm;
+    const PredictorDev &p = c->pm;
+    const int H = m.hidden, h = p.hidden;
+    // largest split-K partial buffer: S * NB * npad
+    size_t pa = 0, pb = 0, ph = 0;
+    auto upd = [](size_t &v, const Q4Tiled &t, int nb) { v = std::max(v, (size_t)t.S * nb * t.npad); };
+    for (const LayerDev &L : c->tlayers) { upd(pa, L.qkv, 1); upd(pa, L.gate_up, 1); upd(pb, L.o, 1); upd(pb, L.down, 1); }
+    for (const LayerDev &L : c->players) { upd(pa, L.qkv, 2); upd(pa, L.gate_up, 2); upd(pb, L.o, 2); upd(pb, L.down, 2); }
+    upd(pb, p.proj, 2);
+    upd(ph, m.codec_head, 1);
+    for (const Q4Tiled &t : c->pheads) upd(ph, t, 1);
+    upd(pb, m.text_fc1, 1);
+    upd(pb, m.text_fc2, 1);
+    RCHK(dev_alloc(c, A, &w.x, 2 * (size_t)std::max(H, m.text_hidden)));
+    RCHK(dev_alloc(c, A, &w.px, 2 * (size_t)h));
+    RCHK(dev_alloc(c, A, &w.pin, 2 * (size_t)H));
+    RCHK(dev_alloc(c, A, &w.qbuf, 16 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.am, MAX_CHUNKS * 16));
+    RCHK(dev_alloc(c, A, &w.al, MAX_CHUNKS * 16));
+    RCHK(dev_alloc(c, A, &w.aacc, (size_t)MAX_CHUNKS * 16 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.pattn, 2 * 16 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.pk, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.pv, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.part_a, pa));
+    RCHK(dev_alloc(c, A, &w.part_b, pb));
+    RCHK(dev_alloc(c, A, &w.part_head, ph));
+    RCHK(dev_alloc(c, A, &w.hid_work, H));
+    RCHK(dev_alloc(c, A, &w.hidden, H));
+    RCHK(dev_alloc(c, A, &w.logits, std::max(m.vocab, 4096)));
+    RCHK(dev_alloc(c, A, &w.pad, H));
+    RCHK(dev_alloc(c, A, &w.ring_pred, RING_FRAMES * 16));
+    RCHK(dev_alloc(c, A, &w.ring_used, RING_FRAMES * 16));
+    c->text_cap = 256;
+    RCHK(dev_alloc(c, A, &w.text, (size_t)c->text_cap * H));
+    HIPCHK(c, hipMemset(w.pad, 0, sizeof(float) * H));
+    w.attn_grid = 8 * (int)(c->kv_cap / KV_PAGE);
+    RCHK(ensure_io(c, std::max<int64_t>(8192, 4 * (int64_t)std::max(H, m.vocab))));
+    return QTTS_OK;
+}
+
+static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predictor_host *p)
+{
+    auto &A = c->model_allocs;
+    if (t->n_layers <= 0 || !t->layers || t->head_dim != HEAD_DIM || t->n_heads != 16 || t->n_kv_heads != 8)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "talker shape not supported (heads %d/%d, head_dim %d)",
+                    t->n_heads, t->n_kv_heads, t->head_dim);
+    if (p->n_layers <= 0 || !p->layers || p->head_dim != HEAD_DIM || p->n_heads != 16 || p->n_kv_heads != 8)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "predictor shape not supported");
+    if (!p->has_input_proj)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "predictor without input projection not supported");
+    if (p->n_groups < 1 || p->n_groups > 15 || !p->lm_heads || !p->codec_embeddings)
+        return fail(c, QTTS_ERR_INVALID, "predictor needs 1..15 heads and embeddings");
+    if (t->vocab > 4096 || t->vocab <= 0) return fail(c, QTTS_ERR_UNSUPPORTED, "talker vocab must be <= 4096");
+    if (t->rope_max_pos < 1 || !t->rope_cos || !t->rope_sin || p->rope_max_pos < PRED_KV_CAP)
+        return fail(c, QTTS_ERR_INVALID, "rope tables missing");
+
+    TalkerDev &m = c->tm;
+    m.n_layers = t->n_layers; m.hidden = t->hidden; m.text_hidden = t->text_hidden;
+    m.n_heads = t->n_heads; m.n_kv_heads = t->n_kv_heads; m.inter = t->inter; m.vocab = t->vocab;
+    c->tlayers.assign(t->n_layers, LayerDev{});
+    for (int l = 0; l < t->n_layers; l++) RCHK(upload_layer(c, t->layers[l], t->hidden, t->head_dim, &c->tlayers[l], false));
+    m.layers = c->tlayers.data();
+    RCHK(build_tiled(c, A, {src_of(t->codec_head)}, env_tile("HEAD", choose_cfg(t->hidden, t->codec_head.n / 32, false)),
+                     &m.codec_head, nullptr));
+    RCHK(build_tiled(c, A, {src_of(t->text_fc1)}, choose_cfg(t->text_fc1.k, t->text_fc1.n / 32, false), &m.text_fc1, nullptr));
+    RCHK(build_tiled(c, A, {src_of(t->text_fc2)}, choose_cfg(t->text_fc2.k, t->text_fc2.n / 32, false), &m.text_fc2, nullptr));
+    RCHK(upload_vec(c, A, t->text_fc1_bias, t->text_fc1.n, &m.text_fc1_bias));
+    RCHK(upload_vec(c, A, t->text_fc2_bias, t->text_fc2.n, &m.text_fc2_bias));
+    RCHK(upload_rows(c, A, {t->codec_embedding}, &m.codec_rows));
+    RCHK(upload_rows(c, A, {t->text_embedding}, &m.text_rows));
+    RCHK(upload_vec(c, A, t->final_norm, t->hidden, &m.final_norm));
+    RCHK(upload_vec(c, A, t->rope_cos, (size_t)t->rope_max_pos * 64, &m.rope_cos));
+    RCHK(upload_vec(c, A, t->rope_sin, (size_t)t->rope_max_pos * 64, &m.rope_sin));
+    m.rope_rows = t->rope_max_pos;
+    if (m.codec_rows.n != m.hidden) return fail(c, QTTS_ERR_INVALID, "codec embedding width != hidden");
+
+    // paged KV pool (identity page table)
+    const int n_phys = (int)(c->kv_cap / KV_PAGE);
+    float *kvb = nullptr;
+    RCHK(dev_alloc(c, A, &kvb, (size_t)t->n_layers * n_phys * 2 * 8 * KV_PAGE * HEAD_DIM));
+    std::vector<int32_t> ptab(MAX_CHUNKS);
+    for (int i = 0; i < MAX_CHUNKS; i++) ptab[i] = i < n_phys ? i : 0;
+    const int32_t *dptab = nullptr;
+    RCHK(upload_vec(c, A, ptab.data(), ptab.size(), &dptab));
+    m.kv = KvPaged{kvb, dptab, n_phys};
+
+    PredictorDev &q = c->pm;
+    q.n_layers = p->n_layers; q.hidden = p->hidden; q.n_heads = p->n_heads; q.n_kv_heads = p->n_kv_heads;
+    q.inter = p->inter; q.vocab = p->vocab; q.n_groups = p->n_groups;
+    c->players.assign(p->n_layers, LayerDev{});
+    for (int l = 0; l < p->n_layers; l++) RCHK(upload_layer(c, p->layers[l], p->hidden, p->head_dim, &c->players[l], true));
+    q.layers = c->players.data();
+    RCHK(build_tiled(c, A, {src_of(p->input_proj)}, env_tile("PPROJ", choose_cfg(p->input_proj.k, p->input_proj.n / 32, false)),
+                     &q.proj, nullptr));
+    if (q.proj.n != q.hidden || p->input_proj.k != t->hidden)
+        return fail(c, QTTS_ERR_INVALID, "predictor input projection shape");
+    RCHK(upload_vec(c, A, p->input_proj_bias, p->input_proj.n, &q.proj_bias));
+    c->pheads.assign(p->n_groups, Q4Tiled{});
+    for (int g = 0; g < p->n_groups; g++) {
+        RCHK(build_tiled(c, A, {src_of(p->lm_heads[g])},
+                         env_tile("PHEAD", choose_cfg(p->lm_heads[g].k, p->lm_heads[g].n / 32, false)), &c->pheads[g], nullptr));
+        if (c->pheads[g].n != p->vocab) return fail(c, QTTS_ERR_INVALID, "lm_head %d width != vocab", g);
+    }
+    q.heads = c->pheads.data();
+    std::vector<qtts_q4_host> embs(p->codec_embeddings, p->codec_embeddings + p->n_groups);
+    RCHK(upload_rows(c, A, embs, &q.emb_rows));
+    if (q.emb_rows.n != t->hidden) return fail(c, QTTS_ERR_INVALID, "predictor embedding width != talker hidden");
+    RCHK(upload_vec(c, A, p->final_norm, p->hidden, &q.final_norm));
+    RCHK(upload_vec(c, A, p->rope_cos, (size_t)p->rope_max_pos * 64, &q.rope_cos));
+    RCHK(upload_vec(c, A, p->rope_sin, (size_t)p->rope_max_pos * 64, &q.rope_sin));
+    q.rope_rows = p->rope_max_pos;
+    RCHK(alloc_workspace(c));
+    return QTTS_OK;
+}
+
+static int write_state(qtts_ctx *c)
+{
+    HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+static int read_state(qtts_ctx *c)
+{
+    HIPCHK(c, hipMemcpyAsync(c->h_st, c->st_gen, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_model_upload(qtts_ctx *c, const qtts_talker_host *t, const qtts_predictor_host *p)
+{
+    if (!c || !t || !p) return QTTS_ERR_INVALID;
+    hipSetDevice(c->device);
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    free_model(c);
+    const int r = upload_model(c, t, p);
+    if (r != QTTS_OK) {
+        free_model(c);
+        return r;
+    }
+    memset(c->h_st, 0, sizeof(DevState));
+    RCHK(write_state(c));
+    c->has_model = true;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_model_dims(qtts_ctx *c, int32_t *th, int32_t *tv, int32_t *tl, int32_t *ph, int32_t *pv,
+                               int32_t *pg)
+{
+    if (!c) return QTTS_ERR_INVALID;
+    if (!c->has_model) return fail(c, QTTS_ERR_STATE, "no model uploaded");
+    if (th) *th = c->tm.hidden;
+    if (tv) *tv = c->tm.vocab;
+    if (tl) *tl = c->tm.n_layers;
+    if (ph) *ph = c->pm.hidden;
+    if (pv) *pv = c->pm.vocab;
+    if (pg) *pg = c->pm.n_groups;
+    return QTTS_OK;
+}
+
+#define NEED_MODEL(c)                                                                \
+    do {                                                                             \
+        if (!(c)) return QTTS_ERR_INVALID;                                           \
+        if (!(c)->has_model) return fail((c), QTTS_ERR_STATE, "no model uploaded");  \
+        hipSetDevice((c)->device);                                                   \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// talker
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_talker_step(qtts_ctx *c, const float *emb, int64_t position, float *hidden_out,
+                                float *logits_out, int flags)
+{
+    NEED_MODEL(c);
+    if (!emb || position < 0) return QTTS_ERR_INVALID;
+    if (position >= c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
+    if (c->h_st->kv_len + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full");
+    c->gen_started = false;
+    RCHK(stage_in(c, emb, c->tm.hidden, c->ws.x, flags));
+    c->h_st->position = position;
+    HIPCHK(c, hipMemcpyAsync(&c->st_gen->position, &c->h_st->position, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, c->stream));
+    RCHK(stage_out(c, c->ws.hidden, c->tm.hidden, hidden_out, flags));
+    RCHK(stage_out(c, c->ws.logits, c->tm.vocab, logits_out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->h_st->kv_len += 1;
+    c->h_st->position = position + 1;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int64_t start_pos, float *hidden_out,
+                                   int flags)
+{
+    NEED_MODEL(c);
+    if (!X || seq < 1 || start_pos < 0) return QTTS_ERR_INVALID;
+    if (c->h_st->kv_len != start_pos)
+        return fail(c, QTTS_ERR_STATE, "prefill at %lld but %d positions cached", (long long)start_pos, c->h_st->kv_len);
+    if (start_pos + seq > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full");
+    if (start_pos + seq > c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
+    c->gen_started = false;
+    const int H = c->tm.hidden;
+    for (int64_t t = 0; t < seq; t++) {
+        RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
+        HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t), c->stream));
+    }
+    HIPCHK(c, enqueue_final_norm(c->tm, c->ws, c->ws.hid_work, c->stream));
+    RCHK(stage_out(c, c->ws.hid_work, H, hidden_out, flags));
+    c->h_st->kv_len = (int32_t)(start_pos + seq);
+    c->h_st->position = start_pos + seq;
+    HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_codec_head(qtts_ctx *c, const float *hidden, float *logits, int flags)
+{
+    NEED_MODEL(c);
+    if (!hidden || !logits) return QTTS_ERR_INVALID;
+    RCHK(stage_in(c, hidden, c->tm.hidden, c->d_io, flags));
+    HIPCHK(c, enqueue_codec_head(c->tm, c->ws, c->d_io, c->d_io2, c->stream));
+    RCHK(stage_out(c, c->d_io2, c->tm.vocab, logits, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_embed_text_token(qtts_ctx *c, uint32_t token, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (!out) return QTTS_ERR_INVALID;
+    const TalkerDev &m = c->tm;
+    if ((int64_t)token >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", token);
+    float *raw = c->d_io, *h1 = c->d_io + 2 * std::max(m.text_hidden, m.hidden), *o = c->d_io2;
+    Q4Rows e = m.text_rows;
+    e.n = m.text_hidden;
+    HIPCHK(c, enqueue_embed_row(e, nullptr, token, raw, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc1, raw, h1, m.text_fc1_bias, c->ws.part_b, c->stream));
+    HIPCHK(c, enqueue_silu(h1, m.text_fc1.n, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc2, h1, o, m.text_fc2_bias, c->ws.part_b, c->stream));
+    RCHK(stage_out(c, o, m.text_fc2.n, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_embed_codec_token(qtts_ctx *c, uint32_t token, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (!out) return QTTS_ERR_INVALID;
+    if ((int64_t)token >= c->tm.codec_rows.rows) return fail(c, QTTS_ERR_INVALID, "codec token %u out of range", token);
+    HIPCHK(c, enqueue_embed_row(c->tm.codec_rows, nullptr, token, c->d_io, c->stream));
+    RCHK(stage_out(c, c->d_io, c->tm.hidden, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// KV cache
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_kv_reset(qtts_ctx *c)
+{
+    NEED_MODEL(c);
+    c->gen_started = false;
+    c->h_st->kv_len = 0;
+    c->h_st->position = 0;
+    return write_state(c);
+}
+
+extern "C" int qtts_kv_len(qtts_ctx *c, int64_t *len)
+{
+    NEED_MODEL(c);
+    if (!len) return QTTS_ERR_INVALID;
+    *len = c->h_st->kv_len;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_kv_truncate(qtts_ctx *c, int64_t len)
+{
+    NEED_MODEL(c);
+    if (len < 0 || len > c->h_st->kv_len) return QTTS_ERR_INVALID;
+    c->gen_started = false;
+    c->h_st->kv_len = (int32_t)len;
+    return write_state(c);
+}
+
+extern "C" int qtts_kv_gather(qtts_ctx *c, int32_t layer, float *K, float *V)
+{
+    NEED_MODEL(c);
+    if (layer < 0 || layer >= c->tm.n_layers || !K || !V) return QTTS_ERR_INVALID;
+    const int len = c->h_st->kv_len;
+    const size_t n = (size_t)len * 8 * HEAD_DIM;
+    if (n == 0) return QTTS_OK;
+    float *dk = nullptr, *dv = nullptr;
+    HIPCHK(c, hipMalloc(&dk, n * sizeof(float)));
+    HIPCHK(c, hipMalloc(&dv, n * sizeof(float)));
+    int r = QTTS_OK;
+    if (enqueue_kv_gather(c->tm.kv, layer, len, dk, dv, c->stream) != hipSuccess ||
+        hipMemcpyAsync(K, dk, n * sizeof(float), hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipMemcpyAsync(V, dv, n * sizeof(float), hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
+        hipStreamSynchronize(c->stream) != hipSuccess)
+        r = fail(c, QTTS_ERR_HIP, "kv gather failed");
+    hipFree(dk);
+    hipFree(dv);
+    return r;
+}
+
+extern "C" int qtts_kv_load(qtts_ctx *c, const float *K, const float *V, int64_t len)
+{
+    NEED_MODEL(c);
+    if (!K || !V || len < 0) return QTTS_ERR_INVALID;
+    if (len > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "kv_load of %lld > capacity", (long long)len);
+    c->gen_started = false;
+    const size_t n = (size_t)len * 8 * HEAD_DIM;
+    if (n) {
+        float *dk = nullptr, *dv = nullptr;
+        HIPCHK(c, hipMalloc(&dk, n * sizeof(float)));
+        HIPCHK(c, hipMalloc(&dv, n * sizeof(float)));
+        int r = QTTS_OK;
+        for (int l = 0; l < c->tm.n_layers && r == QTTS_OK; l++) {
+            if (hipMemcpyAsync(dk, K + (size_t)l * n, n * sizeof(float), hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                hipMemcpyAsync(dv, V + (size_t)l * n, n * sizeof(float), hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+                enqueue_kv_scatter(c->tm.kv, l, (int)len, dk, dv, c->stream) != hipSuccess)
+                r = fail(c, QTTS_ERR_HIP, "kv load failed");
+        }
+        hipStreamSynchronize(c->stream);
+        hipFree(dk);
+        hipFree(dv);
+        if (r != QTTS_OK) return r;
+    }
+    c->h_st->kv_len = (int32_t)len;
+    return write_state(c);
+}
+
+// ---------------------------------------------------------------------------
+// predictor and sampler (operator level)
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_predictor_chain(qtts_ctx *c, const float *th, const float *sem, uint32_t *codes_out, int flags)
+{
+    NEED_MODEL(c);
+    if (!th || !sem || !codes_out) return QTTS_ERR_INVALID;
+    const int H = c->tm.hidden;
+    RCHK(stage_in(c, th, H, c->d_io, flags));
+    RCHK(stage_in(c, sem, H, c->d_io2, flags));
+    DevState z{};
+    HIPCHK(c, hipMemcpyAsync(c->st_api, &z, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, enqueue_predictor_chain(c->pm, c->tm, c->ws, c->st_api, c->d_io, c->d_io2, nullptr, c->d_codes_api,
+                                      c->stream));
+    HIPCHK(c, hipMemcpyAsync(codes_out, c->d_codes_api, sizeof(uint32_t) * c->pm.n_groups, hipMemcpyDeviceToHost,
+                             c->stream));
+    DevState back{};
+    HIPCHK(c, hipMemcpyAsync(&back, c->st_api, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (back.nan_flag) return fail(c, QTTS_ERR_NAN, "NaN logits in the predictor");
+    return QTTS_OK;
+}
+
+extern "C" int qtts_acoustic_embed_sum(qtts_ctx *c, const uint32_t *codes, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (!codes || !out) return QTTS_ERR_INVALID;
+    for (int g = 0; g < c->pm.n_groups; g++)
+        if ((int64_t)codes[g] >= c->pm.emb_rows.rows) return fail(c, QTTS_ERR_INVALID, "code %u out of range", codes[g]);
+    HIPCHK(c, hipMemcpyAsync(c->d_codes_api, codes, sizeof(uint32_t) * c->pm.n_groups, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, enqueue_embed_sum(c->pm.emb_rows, c->pm.n_groups, c->d_codes_api, c->d_io, c->stream));
+    RCHK(stage_out(c, c->d_io, c->pm.emb_rows.n, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_sample_token(qtts_ctx *c, const float *logits, int64_t n, const qtts_sample_params *p,
+                                 const uint32_t *prev, int64_t n_prev, uint64_t *rng, float temperature,
+                                 uint32_t *out)
+{
+    if (!c || !logits || !p || !rng || !out || n <= 0 || n_prev < 0 || (n_prev > 0 && !prev)) return QTTS_ERR_INVALID;
+    if (n > 4096 || n_prev > 4096) return fail(c, QTTS_ERR_UNSUPPORTED, "sampler supports n <= 4096");
+    hipSetDevice(c->device);
+    RCHK(ensure_io(c, 8192));
+    HIPCHK(c, hipMemcpyAsync(c->d_io, logits, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    if (n_prev) HIPCHK(c, hipMemcpyAsync(c->d_prev_api, prev, n_prev * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_rng_api, rng, sizeof(uint64_t), hipMemcpyHostToDevice, c->stream));
+    DevState z{};
+    HIPCHK(c, hipMemcpyAsync(c->st_api, &z, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    SampleArgsHost a{temperature, p->top_p, p->repetition_penalty, p->top_k, c->d_prev_api, (int)n_prev};
+    HIPCHK(c, enqueue_sample_api(c->d_io, (int)n, a, c->d_rng_api, c->d_codes_api, c->st_api, c->stream));
+    DevState back{};
+    HIPCHK(c, hipMemcpyAsync(&back, c->st_api, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(rng, c->d_rng_api, sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(out, c->d_codes_api, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (back.nan_flag) return fail(c, QTTS_ERR_NAN, "NaN in sampler input");
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// frame loop
+// ---------------------------------------------------------------------------
+
+static int build_frame_graph(qtts_ctx *c)
+{
+    if (c->frame_exec) return QTTS_OK;
+    hipGraph_t g = nullptr;
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    const hipError_t e = enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, c->stream);
+    const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+    if (e != hipSuccess || e2 != hipSuccess) {
+        if (g) hipGraphDestroy(g);
+        return fail(c, QTTS_ERR_HIP, "frame capture failed: %s / %s", hipGetErrorString(e), hipGetErrorString(e2));
+    }
+    const hipError_t e3 = hipGraphInstantiate(&c->frame_exec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (e3 != hipSuccess) {
+        c->frame_exec = nullptr;
+        return fail(c, QTTS_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e3));
+    }
+    return QTTS_OK;
+}
+
+extern "C" int qtts_gen_begin(qtts_ctx *c, const float *logits, const float *hidden, int64_t position, uint64_t seed,
+                              const qtts_sample_params *p)
+{
+    NEED_MODEL(c);
+    if (!logits || !hidden || !p || position < 0) return QTTS_ERR_INVALID;
+    HIPCHK(c, hipMemcpyAsync(c->ws.logits, logits, sizeof(float) * c->tm.vocab, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->ws.hidden, hidden, sizeof(float) * c->tm.hidden, hipMemcpyHostToDevice, c->stream));
+    DevState &s = *c->h_st;
+    const int32_t kv = s.kv_len;
+    const int32_t n_text = s.n_text;
+    memset(&s, 0, sizeof s);
+    s.kv_len = kv;
+    s.n_text = n_text;
+    s.position = position;
+    s.rng = seed;
+    s.temperature = p->temperature;
+    s.top_k = p->top_k;
+    s.top_p = p->top_p;
+    s.rep_penalty = p->repetition_penalty;
+    s.eos_id = p->codec_eos_id;
+    s.eos_enabled = p->eos_enabled;
+    s.onset_frames = p->onset_frames;
+    s.onset_temperature = p->onset_temperature;
+    RCHK(write_state(c));
+    c->gen_started = true;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_gen_set_text(qtts_ctx *c, const float *text, int64_t n_text, const float *pad)
+{
+    NEED_MODEL(c);
+    if (n_text < 0 || (n_text > 0 && !text) || !pad) return QTTS_ERR_INVALID;
+    const int H = c->tm.hidden;
+    if (n_text > c->text_cap) {
+        drop_graph(c);
+        float *nt = nullptr;
+        HIPCHK(c, hipMalloc(&nt, (size_t)n_text * H * sizeof(float)));
+        for (auto &p : c->ws_allocs)
+            if (p == c->ws.text) { hipFree(p); p = nt; }
+        c->ws.text = nt;
+        c->text_cap = n_text;
+    }
+    if (n_text) HIPCHK(c, hipMemcpyAsync(c->ws.text, text, (size_t)n_text * H * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->ws.pad, pad, (size_t)H * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    c->h_st->n_text = (int32_t)n_text;
+    HIPCHK(c, hipMemcpyAsync(&c->st_gen->n_text, &c->h_st->n_text, sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// Run frames in batches of up to RING_FRAMES graph launches per host sync.
+static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done, int32_t *eos, bool forced)
+{
+    RCHK(build_frame_graph(c));
+    int64_t emitted = 0;
+    *eos = 0;
+    while (emitted < n) {
+        const int64_t batch = std::min<int64_t>(n - emitted, RING_FRAMES);
+        if (c->h_st->kv_len + batch > c->kv_cap)
+            return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full at %d positions", c->h_st->kv_len);
+        if (c->h_st->position + batch > c->tm.rope_rows)
+            return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
+        c->h_st->ring_base = c->h_st->frame_idx;
+        HIPCHK(c, hipMemcpyAsync(&c->st_gen->ring_base, &c->h_st->ring_base, sizeof(int32_t), hipMemcpyHostToDevice,
+                                 c->stream));
+        for (int64_t f = 0; f < batch; f++) HIPCHK(c, hipGraphLaunch(c->frame_exec, c->stream));
+        HIPCHK(c, hipMemcpyAsync(c->h_ring, c->ws.ring_pred, sizeof(uint32_t) * batch * 16, hipMemcpyDeviceToHost,
+                                 c->stream));
+        const int32_t base = c->h_st->ring_base;
+        HIPCHK(c, hipMemcpyAsync(c->h_st, c->st_gen, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        const int64_t got = c->h_st->frame_idx - base;
+        if (got < 0 || got > batch) return fail(c, QTTS_ERR_STATE, "frame counter out of step");
+        if (pred_out) memcpy(pred_out + emitted * 16, c->h_ring, sizeof(uint32_t) * got * 16);
+        emitted += got;
+        if (c->h_st->nan_flag) {
+            *done = emitted;
+            return fail(c, QTTS_ERR_NAN, "NaN logits during generation");
+        }
+        if (!forced && c->h_st->stop) {
+            *eos = c->h_st->eos;
+            break;
+        }
+        if (got < batch) break;
+    }
+    *done = emitted;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_gen_frames(qtts_ctx *c, int64_t max_frames, uint32_t *codes_out, int64_t *frames_done,
+                               int32_t *eos)
+{
+    NEED_MODEL(c);
+    if (max_frames < 0 || !frames_done || !eos) return QTTS_ERR_INVALID;
+    if (!c->gen_started) return fail(c, QTTS_ERR_STATE, "qtts_gen_begin first");
+    *frames_done = 0;
+    *eos = c->h_st->eos;
+    if (c->h_st->stop) return QTTS_OK;
+    return run_frames(c, max_frames, codes_out, frames_done, eos, false);
+}
+
+extern "C" int qtts_gen_frames_forced(qtts_ctx *c, int64_t n_frames, const uint32_t *forced, uint32_t *pred_out)
+{
+    NEED_MODEL(c);
+    if (n_frames < 0 || (n_frames > 0 && !forced)) return QTTS_ERR_INVALID;
+    if (!c->gen_started) return fail(c, QTTS_ERR_STATE, "qtts_gen_begin first");
+    // forced codes index embedding tables on the device: validate them here
+    for (int64_t f = 0; f < n_frames; f++) {
+        if ((int64_t)forced[f * 16] >= c->tm.codec_rows.rows)
+            return fail(c, QTTS_ERR_INVALID, "forced code 0 of frame %lld out of range", (long long)f);
+        for (int g = 1; g <= c->pm.n_groups; g++)
+            if ((int64_t)forced[f * 16 + g] >= c->pm.emb_rows.rows)
+                return fail(c, QTTS_ERR_INVALID, "forced code %d of frame %lld out of range", g, (long long)f);
+    }
+    if (n_frames > c->forced_cap) {
+        drop_graph(c);
+        if (c->d_forced) hipFree(c->d_forced);
+        c->d_forced = nullptr;
+        HIPCHK(c, hipMalloc(&c->d_forced, sizeof(uint32_t) * 16 * n_frames));
+        c->forced_cap = n_frames;
+    }
+    if (!c->d_forced) {
+        HIPCHK(c, hipMalloc(&c->d_forced, sizeof(uint32_t) * 16));
+        c->forced_cap = 1;
+    }
+    if (n_frames) HIPCHK(c, hipMemcpyAsync(c->d_forced, forced, sizeof(uint32_t) * 16 * n_frames, hipMemcpyHostToDevice, c->stream));
+    c->h_st->force = 1;
+    c->h_st->forced_base = c->h_st->frame_idx;
+    HIPCHK(c, hipMemcpyAsync(&c->st_gen->force, &c->h_st->force, sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(&c->st_gen->forced_base, &c->h_st->forced_base, sizeof(int32_t), hipMemcpyHostToDevice,
+                             c->stream));
+    int64_t done = 0;
+    int32_t eos = 0;
+    const int r = run_frames(c, n_frames, pred_out, &done, &eos, true);
+    c->h_st->force = 0;
+    HIPCHK(c, hipMemcpyAsync(&c->st_gen->force, &c->h_st->force, sizeof(int32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (r == QTTS_OK && done != n_frames) return fail(c, QTTS_ERR_STATE, "forced run stopped early");
+    return r;
+}
+
+extern "C" int qtts_gen_state(qtts_ctx *c, float *logits, float *hidden, int64_t *position, uint64_t *rng)
+{
+    NEED_MODEL(c);
+    RCHK(read_state(c));
+    if (logits) HIPCHK(c, hipMemcpy(logits, c->ws.logits, sizeof(float) * c->tm.vocab, hipMemcpyDeviceToHost));
+    if (hidden) HIPCHK(c, hipMemcpy(hidden, c->ws.hidden, sizeof(float) * c->tm.hidden, hipMemcpyDeviceToHost));
+    if (position) *position = c->h_st->position;
+    if (rng) *rng = c->h_st->rng;
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// measurement
+// ---------------------------------------------------------------------------
+
+static int time_launches(qtts_ctx *c, int32_t iters, const std::function<hipError_t(int)> &launch, double *avg_us)
+{
+    std::vector<hipEvent_t> ev(2 * (size_t)iters);
+    for (auto &e : ev) HIPCHK(c, hipEventCreate(&e));
+    for (int i = 0; i < iters; i++) {
+        HIPCHK(c, hipEventRecord(ev[2 * i], c->stream));
+        HIPCHK(c, launch(i));
+        HIPCHK(c, hipEventRecord(ev[2 * i + 1], c->stream));
+    }
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    double tot = 0.0;
+    for (int i = 0; i < iters; i++) {
+        float ms = 0.0f;
+        HIPCHK(c, hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
+        tot += ms;
+    }
+    for (auto &e : ev) hipEventDestroy(e);
+    *avg_us = tot * 1000.0 / iters;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double *avg_us, double *bytes)
+{
+    NEED_MODEL(c);
+    if (iters < 1 || !avg_us || !bytes) return QTTS_ERR_INVALID;
+    const TalkerDev &m = c->tm;
+    if (kind == 0) {
+        const LayerDev &L = m.layers[0];
+        *bytes = (double)L.gate_up.k * (L.gate_up.n) * 0.5625 + 4.0 * L.gate_up.k + 4.0 * L.gate_up.n;
+        return time_launches(c, iters, [&](int i) { return enqueue_gateup_timing(m, c->ws, i % m.n_layers, c->stream); },
+                             avg_us);
+    }
+    if (kind == 1) {
+        const int len = std::max(1, c->h_st->kv_len);
+        *bytes = (double)len * 8 * HEAD_DIM * 4 * 2 + 16.0 * HEAD_DIM * 4 * 2;
+        return time_launches(c, iters, [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, len, c->stream); },
+                             avg_us);
+    }
+    return QTTS_ERR_INVALID;
+}
+
+extern "C" int qtts_time_gemv(qtts_ctx *c, const qtts_w *const *ws, int32_t n_w, int32_t iters, double *avg_us,
+                              double *bytes)
+{
+    if (!c || !ws || n_w < 1 || iters < 1 || !avg_us || !bytes) return QTTS_ERR_INVALID;
+    hipSetDevice(c->device);
+    const Q4Tiled &t0 = ws[0]->t;
+    *bytes = (double)t0.k * (t0.n / 32) * 32 * 0.5625 + 4.0 * t0.k + 4.0 * t0.n;
+    return time_launches(
+        c, iters,
+        [&](int i) {
+            const qtts_w *w = ws[i % n_w];
+            return enqueue_gemv_plain(w->t, w->x, 1, w->t.k, w->part, c->stream);
+        },
+        avg_us);
+}

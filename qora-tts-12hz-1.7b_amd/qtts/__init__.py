@@ -1,0 +1,322 @@
+"""Python binding of libqtts_hip.so (include/qtts.h) for the MI355X decode path.
+
+The functions mirror the reference crate's forward-call surface:
+
+    gemv / gemm / embed_lookup        gemv.rs:149, 157, 165
+    forward_with_embedding            talker.rs:263
+    prefill_talker_raw_from           talker.rs:379
+    apply_codec_head                  talker.rs:647
+    embed_text_token / codec_token    talker.rs:105, 152
+    generate_acoustic_codes           code_predictor.rs:218
+    get_acoustic_embeddings_sum       code_predictor.rs:287
+    sample_token                      generate_new.rs:771
+    frame loop                        generate_new.rs:606-675
+
+Every call goes through the C ABI; there is no CPU fallback.  A missing or
+unloadable library raises QttsError.
+"""
+import ctypes
+import os
+from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_uint32, c_uint64, c_void_p
+
+import numpy as np
+
+from . import hostdesc
+from .hostdesc import PredictorHost, Q4Host, SampleParams, TalkerHost, ptr, sample_params
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libqtts_hip.so")
+
+OK, ERR_INVALID, ERR_HIP, ERR_OOM, ERR_CAPACITY, ERR_STATE, ERR_IO, ERR_NAN, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6, -7, -8
+DEVICE_PTRS = 1
+
+# Exported symbols and their signatures (argtypes, restype), in header order.
+SIGNATURES = {
+    "qtts_ctx_create": ([c_int, c_int64, POINTER(c_void_p)], c_int),
+    "qtts_ctx_destroy": ([c_void_p], None),
+    "qtts_last_error": ([c_void_p], c_char_p),
+    "qtts_sync": ([c_void_p], c_int),
+    "qtts_stream": ([c_void_p], c_void_p),
+    "qtts_q4_upload": ([c_void_p, POINTER(Q4Host), POINTER(c_void_p)], c_int),
+    "qtts_q4_free": ([c_void_p, c_void_p], c_int),
+    "qtts_gemv_q4": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
+    "qtts_gemm_q4": ([c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_embed_lookup_q4": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_model_upload": ([c_void_p, POINTER(TalkerHost), POINTER(PredictorHost)], c_int),
+    "qtts_model_load_qtts": ([c_void_p, c_char_p], c_int),
+    "qtts_model_dims": ([c_void_p] + [POINTER(c_int32)] * 6, c_int),
+    "qtts_talker_step": ([c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int], c_int),
+    "qtts_talker_prefill": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int], c_int),
+    "qtts_codec_head": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
+    "qtts_embed_text_token": ([c_void_p, c_uint32, c_void_p, c_int], c_int),
+    "qtts_embed_codec_token": ([c_void_p, c_uint32, c_void_p, c_int], c_int),
+    "qtts_kv_reset": ([c_void_p], c_int),
+    "qtts_kv_len": ([c_void_p, POINTER(c_int64)], c_int),
+    "qtts_kv_gather": ([c_void_p, c_int32, c_void_p, c_void_p], c_int),
+    "qtts_kv_load": ([c_void_p, c_void_p, c_void_p, c_int64], c_int),
+    "qtts_kv_truncate": ([c_void_p, c_int64], c_int),
+    "qtts_predictor_chain": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
+    "qtts_acoustic_embed_sum": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
+    "qtts_sample_token": ([c_void_p, c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64,
+                           POINTER(c_uint64), c_float, POINTER(c_uint32)], c_int),
+    "qtts_gen_begin": ([c_void_p, c_void_p, c_void_p, c_int64, c_uint64, POINTER(SampleParams)], c_int),
+    "qtts_gen_set_text": ([c_void_p, c_void_p, c_int64, c_void_p], c_int),
+    "qtts_gen_frames": ([c_void_p, c_int64, c_void_p, POINTER(c_int64), POINTER(c_int32)], c_int),
+    "qtts_gen_frames_forced": ([c_void_p, c_int64, c_void_p, c_void_p], c_int),
+    "qtts_gen_state": ([c_void_p, c_void_p, c_void_p, POINTER(c_int64), POINTER(c_uint64)], c_int),
+    "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
+    "qtts_time_gemv": ([c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
+}
+
+
+class QttsError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"qtts error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load_library(path=None):
+    """Load libqtts_hip.so (built by __graft_entry__.build()).  Raises
+    QttsError when it is missing: the device path has no fallback."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or os.environ.get("QTTS_LIB", LIB_PATH)
+    if not os.path.exists(p):
+        raise QttsError(ERR_STATE, f"{p} not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(p)
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _f32(a, n=None):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if n is not None and a.size != n:
+        raise ValueError(f"expected {n} floats, got {a.size}")
+    return a
+
+
+class Weight:
+    """A Q4 weight uploaded for the operator-level calls."""
+
+    def __init__(self, ctx, w):
+        self.ctx, self.k, self.n = ctx, w.k, w.n
+        self._src = w
+        h = c_void_p()
+        ctx._check(ctx.lib.qtts_q4_upload(ctx.h, byref(hostdesc.q4_host(w)), byref(h)))
+        self.h = h
+
+    def free(self):
+        if self.h:
+            self.ctx.lib.qtts_q4_free(self.ctx.h, self.h)
+            self.h = None
+
+
+class Context:
+    """One device context (qtts_ctx): model, paged talker KV cache, stream."""
+
+    def __init__(self, device=0, kv_capacity=0, lib=None):
+        self.lib = lib or load_library()
+        h = c_void_p()
+        rc = self.lib.qtts_ctx_create(device, kv_capacity, byref(h))
+        if rc != OK:
+            raise QttsError(rc, "qtts_ctx_create failed (no HIP device?)")
+        self.h = h
+        self._keep = []
+
+    def close(self):
+        if self.h:
+            self.lib.qtts_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc):
+        if rc != OK:
+            raise QttsError(rc, (self.lib.qtts_last_error(self.h) or b"").decode())
+        return rc
+
+    # ---- operator level -------------------------------------------------
+    def upload(self, w):
+        return Weight(self, w)
+
+    def gemv(self, w, x):
+        """`gemv` (gemv.rs:149) for an uploaded weight."""
+        x = _f32(x, w.k)
+        y = np.empty(w.n, np.float32)
+        self._check(self.lib.qtts_gemv_q4(self.h, w.h, ptr(x), ptr(y), 0))
+        return y
+
+    def gemm(self, w, X):
+        """`gemm` (gemv.rs:157): rows of X times W."""
+        X = _f32(X).reshape(-1, w.k)
+        Y = np.empty((X.shape[0], w.n), np.float32)
+        self._check(self.lib.qtts_gemm_q4(self.h, w.h, ptr(X), X.shape[0], ptr(Y), 0))
+        return Y
+
+    def embed_lookup(self, w, row):
+        """`embed_lookup_q4` (gemv.rs:415)."""
+        out = np.empty(w.n, np.float32)
+        self._check(self.lib.qtts_embed_lookup_q4(self.h, w.h, row, ptr(out), 0))
+        return out
+
+    # ---- model -----------------------------------------------------------
+    def upload_model(self, talker, predictor):
+        th, keep_t = hostdesc.talker_host(talker)
+        ph, keep_p = hostdesc.predictor_host(predictor)
+        self._check(self.lib.qtts_model_upload(self.h, byref(th), byref(ph)))
+        self.dims()
+
+    def load_qtts(self, path):
+        self._check(self.lib.qtts_model_load_qtts(self.h, os.fsencode(path)))
+        self.dims()
+
+    def dims(self):
+        v = [c_int32() for _ in range(6)]
+        self._check(self.lib.qtts_model_dims(self.h, *[byref(x) for x in v]))
+        (self.hidden, self.vocab, self.n_layers, self.p_hidden, self.p_vocab, self.n_groups) = [x.value for x in v]
+        return self.hidden, self.vocab, self.n_layers, self.p_hidden, self.p_vocab, self.n_groups
+
+    def forward_with_embedding(self, embedding, position):
+        """`forward_with_embedding` (talker.rs:263-360): [hidden | logits]."""
+        e = _f32(embedding, self.hidden)
+        hid = np.empty(self.hidden, np.float32)
+        lg = np.empty(self.vocab, np.float32)
+        self._check(self.lib.qtts_talker_step(self.h, ptr(e), position, ptr(hid), ptr(lg), 0))
+        return np.concatenate([hid, lg])
+
+    def prefill_talker_raw_from(self, X, start_pos):
+        """`prefill_talker_raw_from` (talker.rs:379-482): last row's normed hidden."""
+        X = _f32(X).reshape(-1, self.hidden)
+        out = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_talker_prefill(self.h, ptr(X), X.shape[0], start_pos, ptr(out), 0))
+        return out
+
+    def apply_codec_head(self, hidden):
+        h = _f32(hidden, self.hidden)
+        out = np.empty(self.vocab, np.float32)
+        self._check(self.lib.qtts_codec_head(self.h, ptr(h), ptr(out), 0))
+        return out
+
+    def embed_text_token(self, token):
+        out = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_embed_text_token(self.h, token, ptr(out), 0))
+        return out
+
+    def embed_codec_token(self, token):
+        out = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_embed_codec_token(self.h, token, ptr(out), 0))
+        return out
+
+    # ---- KV -----------------------------------------------------------------
+    def kv_reset(self):
+        self._check(self.lib.qtts_kv_reset(self.h))
+
+    def kv_len(self):
+        n = c_int64()
+        self._check(self.lib.qtts_kv_len(self.h, byref(n)))
+        return n.value
+
+    def kv_gather(self, layer):
+        n = self.kv_len()
+        K = np.empty((n, 8, 128), np.float32)
+        V = np.empty((n, 8, 128), np.float32)
+        self._check(self.lib.qtts_kv_gather(self.h, layer, ptr(K), ptr(V)))
+        return K, V
+
+    def kv_load(self, K, V):
+        """K, V: [n_layers][len][8][128] f32."""
+        K = _f32(K)
+        V = _f32(V)
+        self._check(self.lib.qtts_kv_load(self.h, ptr(K), ptr(V), K.shape[1]))
+
+    def kv_truncate(self, n):
+        self._check(self.lib.qtts_kv_truncate(self.h, n))
+
+    # ---- predictor / sampler -----------------------------------------------
+    def generate_acoustic_codes(self, talker_hidden, semantic_embed):
+        th = _f32(talker_hidden, self.hidden)
+        se = _f32(semantic_embed, self.hidden)
+        codes = np.empty(self.n_groups, np.uint32)
+        self._check(self.lib.qtts_predictor_chain(self.h, ptr(th), ptr(se), ptr(codes), 0))
+        return codes
+
+    def get_acoustic_embeddings_sum(self, codes):
+        c = np.ascontiguousarray(codes, dtype=np.uint32)
+        out = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_acoustic_embed_sum(self.h, ptr(c), ptr(out), 0))
+        return out
+
+    def sample_token(self, logits, params, prev_tokens, rng_state, temperature):
+        """`sample_token` (generate_new.rs:771-862): returns (token, rng_state)."""
+        lg = _f32(logits)
+        prev = np.ascontiguousarray(prev_tokens, dtype=np.uint32)
+        rng = c_uint64(rng_state)
+        out = c_uint32()
+        self._check(self.lib.qtts_sample_token(self.h, ptr(lg), lg.size, byref(params), ptr(prev) if prev.size else None,
+                                               prev.size, byref(rng), temperature, byref(out)))
+        return out.value, rng.value
+
+    # ---- frame loop -----------------------------------------------------------
+    def gen_begin(self, logits, hidden, position, seed, params):
+        lg = _f32(logits, self.vocab)
+        hd = _f32(hidden, self.hidden)
+        self._check(self.lib.qtts_gen_begin(self.h, ptr(lg), ptr(hd), position, seed, byref(params)))
+
+    def gen_set_text(self, text_rows, pad):
+        t = None if text_rows is None or len(text_rows) == 0 else _f32(text_rows).reshape(-1, self.hidden)
+        p = _f32(pad, self.hidden)
+        self._check(self.lib.qtts_gen_set_text(self.h, ptr(t) if t is not None else None,
+                                               0 if t is None else t.shape[0], ptr(p)))
+
+    def gen_frames(self, max_frames):
+        """Frames until EOS or max_frames: (codes [frames][16], eos)."""
+        out = np.empty((max(max_frames, 1), 16), np.uint32)
+        done, eos = c_int64(), c_int32()
+        self._check(self.lib.qtts_gen_frames(self.h, max_frames, ptr(out), byref(done), byref(eos)))
+        return out[: done.value].copy(), bool(eos.value)
+
+    def gen_frames_forced(self, forced):
+        f = np.ascontiguousarray(forced, dtype=np.uint32).reshape(-1, 16)
+        pred = np.empty_like(f)
+        self._check(self.lib.qtts_gen_frames_forced(self.h, f.shape[0], ptr(f), ptr(pred)))
+        return pred
+
+    def gen_state(self):
+        lg = np.empty(self.vocab, np.float32)
+        hd = np.empty(self.hidden, np.float32)
+        pos, rng = c_int64(), c_uint64()
+        self._check(self.lib.qtts_gen_state(self.h, ptr(lg), ptr(hd), byref(pos), byref(rng)))
+        return lg, hd, pos.value, rng.value
+
+    # ---- measurement ----------------------------------------------------------
+    def time_kernel(self, kind, iters):
+        us, b = c_double(), c_double()
+        self._check(self.lib.qtts_time_kernel(self.h, kind, iters, byref(us), byref(b)))
+        return us.value, b.value
+
+    def time_gemv(self, weights, iters):
+        arr = (c_void_p * len(weights))(*[w.h for w in weights])
+        us, b = c_double(), c_double()
+        self._check(self.lib.qtts_time_gemv(self.h, arr, len(weights), iters, byref(us), byref(b)))
+        return us.value, b.value
+
+
+def header_symbols(header_path=None):
+    """Function names declared in include/qtts.h."""
+    import re
+    hp = header_path or os.path.join(os.path.dirname(PKG_DIR), "include", "qtts.h")
+    text = open(hp).read()
+    return sorted(set(re.findall(r"\b(qtts_[a-z0-9_]+)\s*\(", text)))

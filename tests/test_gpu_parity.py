@@ -1,0 +1,282 @@
+"""Parity of the HIP path (libqtts_hip.so via the C ABI) with the oracle.
+
+Bars (from the decode path's contract): KV append/gather, embedding rows and
+sums, argmax indices are bit-exact; GEMV, attention and whole-step outputs
+agree within |d| <= 1e-3 * max(max|ref|, rms(ref)) (f32 accumulation in a
+different order); predicted codes agree.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import qtts
+import refgen
+from qtts import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def close(got, ref, rel=TOL):
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), np.sqrt((ref ** 2).mean()), 1e-30)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    return err <= rel * scale, err / scale
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def ctx(ctx_factory):
+    return ctx_factory(4096)
+
+
+@pytest.fixture(scope="module")
+def small_model():
+    t = synth.make_talker(seed=101, n_layers=2, text_vocab=512, rope_max_pos=4096)
+    p = synth.make_predictor(seed=102, n_layers=5)
+    return t, p
+
+
+@pytest.fixture(scope="module")
+def loaded(ctx, small_model):
+    t, p = small_model
+    ctx.upload_model(t, p)
+    O.set_workers(16, 8)
+    om = O.Model(t, p, kv_cap=4096)
+    return ctx, om, t, p
+
+
+# ---- operator level ------------------------------------------------------
+
+def test_gemv_config1(ctx):
+    # one Q4 GEMV, k=2048 -> n=6144, nibbles uniform, scales |N(0,0.02)|, x ~ N(0,1)
+    rng = np.random.Generator(np.random.PCG64(1))
+    w = synth.q4_random(rng, 2048, 6144)
+    x = rng.standard_normal(2048).astype(np.float32)
+    dw = ctx.upload(w)
+    y = ctx.gemv(dw, x)
+    ok, e = close(y, O.gemv_scalar(x, w))
+    dw.free()
+    assert ok, f"rel err {e}"
+
+
+@pytest.mark.parametrize("k,n,seed,iz,sz", [c + (0.0, 0.0) for c in refgen.SHAPE_CASES] + refgen.SPARSE_CASES
+                         + [(16, 100, 31, 0.0, 0.0)])
+def test_gemv_reference_cases(ctx, k, n, seed, iz, sz):
+    x, w = refgen.case(k, n, seed, iz, sz)
+    dw = ctx.upload(w)
+    y = ctx.gemv(dw, x)
+    dw.free()
+    ref = O.gemv_scalar(x, w)
+    ok, e = close(y, ref)
+    assert ok, f"rel err {e}"
+    assert np.all(y[(n // 32) * 32:] == 0.0)
+
+
+@pytest.mark.parametrize("k,n", [(1024, 2048), (2048, 1024), (3072, 1024), (6144, 2048), (2048, 12288)])
+def test_gemv_model_shapes(ctx, k, n):
+    rng = np.random.Generator(np.random.PCG64(k * 7 + n))
+    w = synth.q4_random(rng, k, n)
+    x = (rng.standard_normal(k) * 3).astype(np.float32)
+    dw = ctx.upload(w)
+    y = ctx.gemv(dw, x)
+    dw.free()
+    ok, e = close(y, O.gemv_scalar(x, w))
+    assert ok, f"rel err {e}"
+
+
+def test_gemm_rows(ctx):
+    rng = np.random.Generator(np.random.PCG64(3))
+    w = synth.q4_random(rng, 2048, 3072)
+    X = rng.standard_normal((5, 2048)).astype(np.float32)
+    dw = ctx.upload(w)
+    Y = ctx.gemm(dw, X)
+    dw.free()
+    R = O.gemm(X, w)
+    for r in range(5):
+        ok, e = close(Y[r], R[r])
+        assert ok, f"row {r} rel err {e}"
+
+
+def test_embed_lookup_exact(ctx):
+    rng = np.random.Generator(np.random.PCG64(4))
+    w = synth.q4_random(rng, 3072, 2048)
+    dw = ctx.upload(w)
+    for row in (0, 1, 2150, 3071):
+        assert np.array_equal(bits(ctx.embed_lookup(dw, row)), bits(O.embed_lookup(w, row)))
+    dw.free()
+
+
+# ---- model level ----------------------------------------------------------
+
+def test_kv_load_gather_bit_exact(loaded):
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(5))
+    L = 200
+    K = rng.standard_normal((len(t.layers), L, 8, 128)).astype(np.float32)
+    V = rng.standard_normal((len(t.layers), L, 8, 128)).astype(np.float32)
+    ctx.kv_load(K, V)
+    assert ctx.kv_len() == L
+    for l in range(len(t.layers)):
+        k, v = ctx.kv_gather(l)
+        assert np.array_equal(bits(k), bits(K[l])) and np.array_equal(bits(v), bits(V[l]))
+    ctx.kv_reset()
+    assert ctx.kv_len() == 0
+
+
+def test_talker_step_kv512(loaded):
+    # config-2 shape on a 2-layer talker: KV prefilled N(0,1) to 512, append one, attend 513
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(6))
+    L = 512
+    K = rng.standard_normal((len(t.layers), L, 8, 128)).astype(np.float32)
+    V = rng.standard_normal((len(t.layers), L, 8, 128)).astype(np.float32)
+    ctx.kv_load(K, V)
+    om.kv_load(K, V)
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    out = ctx.forward_with_embedding(emb, L)
+    ref = om.forward_with_embedding(emb, L)
+    ok_h, eh = close(out[: t.hidden], ref[: t.hidden])
+    ok_l, el = close(out[t.hidden:], ref[t.hidden:])
+    assert ok_h and ok_l, f"hidden {eh} logits {el}"
+    assert ctx.kv_len() == L + 1
+    for l in range(len(t.layers)):
+        k, v = ctx.kv_gather(l)
+        ko, vo = om.kv_layer(l)
+        assert np.array_equal(bits(k[:L]), bits(K[l])) and np.array_equal(bits(v[:L]), bits(V[l]))
+        assert close(k[L], ko[L])[0] and close(v[L], vo[L])[0]
+    ctx.kv_reset()
+    om.kv_reset()
+
+
+def test_prefill_then_steps(loaded):
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(7))
+    X = rng.standard_normal((70, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    h = ctx.prefill_talker_raw_from(X, 0)
+    hr = om.prefill(X, 0)
+    ok, e = close(h, hr)
+    assert ok, f"prefill rel err {e}"
+    for step in range(3):
+        emb = rng.standard_normal(t.hidden).astype(np.float32)
+        out = ctx.forward_with_embedding(emb, 70 + step)
+        ref = om.forward_with_embedding(emb, 70 + step)
+        ok, e = close(out, ref)
+        assert ok, f"step {step} rel err {e}"
+    ctx.kv_reset()
+    om.kv_reset()
+
+
+def test_text_and_codec_embeddings(loaded):
+    ctx, om, t, p = loaded
+    for tok in (0, 7, 511):
+        ok, e = close(ctx.embed_text_token(tok), om.embed_text_token(tok))
+        assert ok, f"text token {tok} rel err {e}"
+    for tok in (0, 2150, 3071):
+        assert np.array_equal(bits(ctx.embed_codec_token(tok)), bits(om.embed_codec_token(tok)))
+
+
+def test_codec_head(loaded):
+    ctx, om, t, p = loaded
+    h = np.random.Generator(np.random.PCG64(8)).standard_normal(t.hidden).astype(np.float32)
+    ok, e = close(ctx.apply_codec_head(h), om.codec_head(h))
+    assert ok, f"rel err {e}"
+
+
+def test_predictor_chain_codes(loaded):
+    # config 3: 5 layers, 15 codebooks, KV 2 -> 16, greedy argmax
+    ctx, om, t, p = loaded
+    agree = total = 0
+    for seed in range(4):
+        rng = np.random.Generator(np.random.PCG64(100 + seed))
+        th = rng.standard_normal(t.hidden).astype(np.float32)
+        sem = om.embed_codec_token(int(rng.integers(0, 2048)))
+        got = ctx.generate_acoustic_codes(th, sem)
+        ref = om.predictor_chain(th, sem)
+        if seed == 0:
+            assert np.array_equal(got, ref), f"{got} vs {ref}"
+        agree += int((got == ref).sum())
+        total += ref.size
+    assert agree >= 0.99 * total
+
+
+def test_acoustic_embed_sum_exact(loaded):
+    ctx, om, t, p = loaded
+    codes = np.random.Generator(np.random.PCG64(9)).integers(0, 2048, 15).astype(np.uint32)
+    assert np.array_equal(bits(ctx.get_acoustic_embeddings_sum(codes)), bits(om.acoustic_embed_sum(codes)))
+
+
+@pytest.mark.parametrize("top_k,top_p,temp,rep", [(50, 1.0, 0.9, 1.05), (1, 1.0, 0.9, 1.05), (0, 0.8, 1.0, 1.0),
+                                                  (50, 0.9, 0.7, 1.2)])
+def test_sampler_matches_oracle(ctx, top_k, top_p, temp, rep):
+    rng = np.random.Generator(np.random.PCG64(10))
+    params = qtts.sample_params(temperature=temp, top_k=top_k, top_p=top_p, repetition_penalty=rep)
+    mismatch = 0
+    s_gpu = s_cpu = 42
+    for i in range(60):
+        lg = (rng.standard_normal(3072) * 3).astype(np.float32)
+        prev = rng.integers(0, 3072, 16).astype(np.uint32)
+        prev[:4] = 0
+        a, s_gpu = ctx.sample_token(lg, params, prev, s_gpu, temp)
+        b, s_cpu = O.sample_token(lg, params, prev, s_cpu, temp)
+        assert s_gpu == s_cpu
+        mismatch += a != b
+    assert mismatch <= 1
+
+
+def test_frames_teacher_forced_greedy(loaded):
+    """Greedy frames (top_k 1): each frame fed the oracle's previous codes;
+    >= 99% of the 16 codes per frame agree."""
+    ctx, om, t, p = loaded
+    n_frames = 60
+    params = qtts.sample_params(top_k=1, eos_enabled=False)
+    rng = np.random.Generator(np.random.PCG64(11))
+    X = rng.standard_normal((16, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    hid = om.prefill(X, 0)
+    ctx.prefill_talker_raw_from(X, 0)
+    logits = om.codec_head(hid)
+    pad = om.embed_text_token(3)
+    ctx.gen_set_text(None, pad)
+    om.gen_begin(logits, hid, 16, 42)
+    ctx.gen_begin(logits, hid, 16, 42, params)
+    ref = np.stack([om.frame(params, pad)[0] for _ in range(n_frames)])
+    pred = ctx.gen_frames_forced(ref)
+    agree = (pred == ref).mean()
+    assert agree >= 0.99, f"agreement {agree:.4f}"
+    ctx.kv_reset()
+    om.kv_reset()
+
+
+def test_frames_free_running_sampled(loaded):
+    """Default sampling (top-k 50, T 0.9, penalty 1.05, seed 42): free-running
+    frames track the oracle; report the first divergence."""
+    ctx, om, t, p = loaded
+    params = qtts.sample_params(eos_enabled=False)
+    rng = np.random.Generator(np.random.PCG64(12))
+    X = rng.standard_normal((16, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    hid = om.prefill(X, 0)
+    ctx.prefill_talker_raw_from(X, 0)
+    logits = om.codec_head(hid)
+    pad = om.embed_text_token(3)
+    ctx.gen_set_text(None, pad)
+    om.gen_begin(logits, hid, 16, 42)
+    ctx.gen_begin(logits, hid, 16, 42, params)
+    n = 20
+    ref = np.stack([om.frame(params, pad)[0] for _ in range(n)])
+    got, eos = ctx.gen_frames(n)
+    assert not eos and got.shape == (n, 16)
+    same = np.all(got == ref, axis=1)
+    first_div = int(np.argmin(same)) if not same.all() else n
+    assert first_div >= 5, f"free-running frames diverge at frame {first_div}"
+    ctx.kv_reset()
+    om.kv_reset()
