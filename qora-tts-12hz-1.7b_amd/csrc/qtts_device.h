@@ -10,24 +10,38 @@ namespace qtts {
 // A tile covers GB 32-column groups x KC rows, KC = R * T / GB, and is
 // stored contiguously: nibble block [R][T] x 16 B, then scale block [T] x
 // R f16.  Thread t of a workgroup owns group (t % GB) and rows
-// r * (T/GB) + t / GB, r = 0..R-1, of the tile.
+// r * (T/GB) + t / GB, r = 0..R-1, of the tile.  A weight with
+// S = ceil(k / KC) k-slices writes S partial sums per output; S = 1 is a
+// full-k pass.
 enum TileCfg : int32_t {
-    TILE_S256 = 0,   // T=256, GB=8,  R=8  -> KC = 256   (split-K)
-    TILE_S128 = 1,   // T=128, GB=8,  R=8  -> KC = 128   (split-K)
-    TILE_D256 = 2,   // T=256, GB=1,  R=8  -> KC = 2048  (one slice for k <= 2048)
-    TILE_D384 = 3,   // T=384, GB=1,  R=8  -> KC = 3072
-    TILE_D768 = 4,   // T=768, GB=1,  R=8  -> KC = 6144
+    TILE_G8_T256 = 0,   // KC = 256
+    TILE_G8_T128 = 1,   // KC = 128
+    TILE_G1_T64 = 2,    // KC = 512
+    TILE_G1_T128 = 3,   // KC = 1024
+    TILE_G1_T256 = 4,   // KC = 2048
+    TILE_G1_T384 = 5,   // KC = 3072
+    TILE_G1_T768 = 6,   // KC = 6144
+    TILE_G2_T256 = 7,   // KC = 1024
+    TILE_G2_T512 = 8,   // KC = 2048
+    TILE_G4_T256 = 9,   // KC = 512
+    TILE_G1_T512 = 10,  // KC = 4096
     TILE_COUNT
 };
 
 struct TileShape { int T, GB, R; };
 __host__ __device__ constexpr TileShape tile_shape(int cfg)
 {
-    return cfg == TILE_S256 ? TileShape{256, 8, 8}
-         : cfg == TILE_S128 ? TileShape{128, 8, 8}
-         : cfg == TILE_D256 ? TileShape{256, 1, 8}
-         : cfg == TILE_D384 ? TileShape{384, 1, 8}
-                            : TileShape{768, 1, 8};
+    return cfg == TILE_G8_T256 ? TileShape{256, 8, 8}
+         : cfg == TILE_G8_T128 ? TileShape{128, 8, 8}
+         : cfg == TILE_G1_T64  ? TileShape{64, 1, 8}
+         : cfg == TILE_G1_T128 ? TileShape{128, 1, 8}
+         : cfg == TILE_G1_T256 ? TileShape{256, 1, 8}
+         : cfg == TILE_G1_T384 ? TileShape{384, 1, 8}
+         : cfg == TILE_G1_T768 ? TileShape{768, 1, 8}
+         : cfg == TILE_G2_T256 ? TileShape{256, 2, 8}
+         : cfg == TILE_G2_T512 ? TileShape{512, 2, 8}
+         : cfg == TILE_G4_T256 ? TileShape{256, 4, 8}
+                               : TileShape{512, 1, 8};
 }
 
 struct Q4Tiled {
@@ -39,6 +53,7 @@ struct Q4Tiled {
     int32_t cfg;           // TileCfg
     int32_t tile_bytes;
     int32_t npad;          // G * 32
+    int32_t interleave;    // 1: two fused weights alternate by group (a0 b0 a1 b1 ...)
 };
 
 // Row-major Q4 (the reference layout) kept for embedding lookups.

@@ -47,15 +47,18 @@ struct PredictorDev {
 };
 
 struct Workspace {
-    float *x;          // talker residual stream [hidden]
-    float *px;         // predictor residual rows [2][p.hidden]
+    float *x;          // talker step input [hidden]
+    float *xa, *xb;    // talker residual stream, ping-pong [hidden]
+    float *pxa, *pxb;  // predictor residual rows, ping-pong [2][p.hidden]
     float *pin;        // predictor API input rows [2][t.hidden]
-    float *qbuf;       // q after norm + RoPE [16][128]
     float *am, *al;    // attention chunk max / sum [MAX_CHUNKS][16]
     float *aacc;       // attention chunk P.V [MAX_CHUNKS][16][128]
+    float *attn;       // talker attention output [16*128]
     float *pattn;      // predictor attention output [2][16*128]
     float *pk, *pv;    // predictor KV [layers][16][8][128]
-    float *part_a, *part_b, *part_head;   // split-K partial sums
+    float *h;          // silu(gate)*up [2][max inter]
+    // split-K partial sums, one buffer per producer role
+    float *part_qkv, *part_o, *part_gu, *part_down, *part_head, *part_proj;
     float *hid_work;   // final-normed hidden of the running step
     float *hidden;     // last_hidden kept across frames
     float *logits;     // logits kept across frames
@@ -99,6 +102,7 @@ hipError_t enqueue_kv_gather(const KvPaged &kv, int layer, int len, float *K, fl
 hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float *K, const float *V,
                               hipStream_t s);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
-hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int len, hipStream_t s);
+hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
+                               hipStream_t s);
 
 }  // namespace qtts

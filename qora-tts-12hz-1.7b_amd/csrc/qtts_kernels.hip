@@ -3,16 +3,21 @@
 // chain and one frame on a stream.
 //
 // Reference functions restated (src/ of the reference crate):
-//   Q4 GEMV            gemv.rs:249-346      (k_gemv + k_reduce_parts)
-//   RMSNorm            gemv.rs:445-454      (ProRms prologue)
-//   QK-norm + RoPE     talker.rs:286-297, rope.rs:79-92 (k_talker_qkv_fin)
-//   KV append          talker.rs:299-302    (k_talker_qkv_fin, paged)
-//   decode attention   talker.rs:304-331    (k_talker_attn + ProAttn)
-//   SwiGLU             talker.rs:338-349    (ProSwiglu prologue)
+//   Q4 GEMV            gemv.rs:249-346      (k_gemv; split-K partials)
+//   RMSNorm + residual gemv.rs:445-454, talker.rs:334-349 (ProResidRms)
+//   QK-norm + RoPE     talker.rs:286-297, rope.rs:79-92 (k_talker_attn prologue)
+//   KV append          talker.rs:299-302    (k_talker_attn, paged)
+//   decode attention   talker.rs:304-331    (k_talker_attn + k_attn_combine)
+//   SwiGLU             talker.rs:338-349    (EpiSwiglu / ProSwiglu)
 //   predictor layers   code_predictor.rs:345-513 (k_pred_attn et al.)
 //   argmax             code_predictor.rs:335-341 (k_argmax)
 //   sample_token       generate_new.rs:771-862   (k_sampler)
 //   frame fusion       generate_new.rs:638-654   (k_combine)
+//
+// Every stage is one kernel; a frame is ~500 of them replayed from a HIP
+// graph.  Stages hand partial sums (one row per k-slice) to the next
+// stage, whose prologue reduces them in slice order, so no stage needs an
+// atomic or a device-wide fence.
 #include "qtts_device.h"
 #include "qtts_kernels.h"
 
@@ -57,8 +62,6 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// Sum over the whole block; every thread gets the result.  `scratch` holds
-// at least blockDim/64 floats.
 __device__ float block_sum(float v, float *scratch)
 {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -85,8 +88,31 @@ __device__ float block_max(float v, float *scratch)
     return r;
 }
 
+// Exclusive prefix sum of one int per thread over the block (thread order).
+__device__ int block_excl_scan(int v, int *scratch, int *total)
+{
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) scratch[wv] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int i = 0; i < nw; i++) {
+        if (i < wv) base += scratch[i];
+        tot += scratch[i];
+    }
+    if (total) *total = tot;
+    return base + x - v;
+}
+
 // ---------------------------------------------------------------------------
-// Q4 dequantisation of one reference-layout row slice (exact in f32)
+// Q4 dequantisation of one reference-layout row element (exact in f32)
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int col)
@@ -98,8 +124,11 @@ __device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int
 }
 
 // ---------------------------------------------------------------------------
-// GEMV prologues: fill xs[b*KC + i] with input row b, rows k0+i.
+// GEMV prologues: fill xs[b*KC + i] with input row b, rows k0+i.  Loads are
+// unrolled so each thread's loads are in flight together.
 // ---------------------------------------------------------------------------
+
+constexpr int MAX_RES = 2048;   // widest residual a prologue normalises
 
 template <int NB>
 struct ProPlain {
@@ -107,49 +136,112 @@ struct ProPlain {
     int ld, k;
     __device__ void operator()(float *xs, int k0, int KC, int ctile) const
     {
-        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
-            const int b = i / KC, r = k0 + (i - b * KC);
-            xs[i] = r < k ? x[(size_t)b * ld + r] : 0.0f;
+        constexpr int U = 8;
+        for (int i0 = threadIdx.x; i0 < NB * KC; i0 += U * blockDim.x) {
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * blockDim.x;
+                const int b = i / KC, r = k0 + (i - b * KC);
+                v[u] = (i < NB * KC && r < k) ? x[(size_t)b * ld + r] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = i0 + u * blockDim.x;
+                if (i < NB * KC) xs[i] = v[u];
+            }
         }
     }
 };
 
-// RMSNorm (gemv.rs:445-454) of the whole input row, then the slice.
-// Tiles of column-tile 0 also store the normed slice to `side` (the
-// final-normed hidden the frame loop keeps, talker.rs:352-359).
+// Residual update + RMSNorm (gemv.rs:445-454):
+//   x = base + sum_s parts[s]   (+ bias)        -- the producer's k-slices in order
+//   xs = x * (1/sqrt(mean(x^2) + 1e-6)) * gamma  -- this tile's rows
+// Workgroup 0 stores x (the residual stream) to x_out and the normed vector
+// to side.  Consumer row b reads producer row prow + b of NBP rows.
 template <int NB>
-struct ProRms {
-    const float *x;
-    int ld, k;
+struct ProResidRms {
+    const float *base;
+    int ldb;
+    const float *parts;
+    int S, NBP, prow, npad;
+    const float *bias;
     const uint16_t *gamma;
+    int k;
+    float *x_out;
     float *side;
     __device__ void operator()(float *xs, int k0, int KC, int ctile) const
     {
+        __shared__ float xf[NB][MAX_RES];
         __shared__ float scratch[16];
+        constexpr int U = 8;
+        const int T = blockDim.x;
+        const bool w0 = blockIdx.x == 0;
+        float gv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int r = threadIdx.x + u * T;
+            gv[u] = (r < KC && k0 + r < k) ? h2f(gamma[k0 + r]) : 0.0f;
+        }
         float inv[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             float ss = 0.0f;
-            for (int i = threadIdx.x; i < k; i += blockDim.x) {
-                const float v = x[(size_t)b * ld + i];
-                ss += v * v;
+            for (int j0 = threadIdx.x; j0 < k; j0 += U * T) {
+                float ps[U], v[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int j = j0 + u * T;
+                    ps[u] = 0.0f;
+                    v[u] = (base && j < k) ? base[(size_t)b * ldb + j] : 0.0f;
+                }
+                if (parts) {
+#pragma unroll 4
+                    for (int s = 0; s < S; s++) {
+                        const float *p = parts + ((size_t)s * NBP + prow + b) * npad;
+#pragma unroll
+                        for (int u = 0; u < U; u++) {
+                            const int j = j0 + u * T;
+                            if (j < k) ps[u] += p[j];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int j = j0 + u * T;
+                    if (j < k) {
+                        float x = parts ? v[u] + ps[u] : v[u];
+                        if (bias) x += bias[j];
+                        xf[b][j] = x;
+                        ss += x * x;
+                    }
+                }
             }
             ss = block_sum(ss, scratch);
             inv[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
         }
-        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
-            const int b = i / KC, r = k0 + (i - b * KC);
-            float v = 0.0f;
-            if (r < k) {
-                v = x[(size_t)b * ld + r] * inv[b] * h2f(gamma[r]);
-                if (side && ctile == 0) side[(size_t)b * ld + r] = v;
+        if (w0 && (x_out || side)) {
+            for (int b = 0; b < NB; b++)
+                for (int j = threadIdx.x; j < k; j += T) {
+                    const float x = xf[b][j];
+                    if (x_out) x_out[(size_t)b * k + j] = x;
+                    if (side) side[(size_t)b * k + j] = x * inv[b] * h2f(gamma[j]);
+                }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int r = threadIdx.x + u * T;
+                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b][k0 + r] * inv[b] * gv[u] : 0.0f;
             }
-            xs[i] = v;
         }
     }
 };
 
-// silu(gate) * up from the gate|up GEMV partials (talker.rs:343-345).
+// silu(gate) * up from gate|up partial sums (talker.rs:343-345).  The fused
+// weight interleaves 32-column groups: gate group j at columns 64j..64j+31,
+// up group j at 64j+32..64j+63.
 template <int NB>
 struct ProSwiglu {
     const float *part;
@@ -160,57 +252,15 @@ struct ProSwiglu {
             const int b = i / KC, r = k0 + (i - b * KC);
             float v = 0.0f;
             if (r < inter) {
+                const int gc = (r >> 5) * 64 + (r & 31);
                 float g = 0.0f, u = 0.0f;
+#pragma unroll 4
                 for (int s = 0; s < S; s++) {
                     const float *p = part + ((size_t)s * NB + b) * npad;
-                    g += p[r];
-                    u += p[inter + r];
+                    g += p[gc];
+                    u += p[gc + 32];
                 }
                 v = silu_f(g) * u;
-            }
-            xs[i] = v;
-        }
-    }
-};
-
-// Combine the split-K attention chunks of the heads in this k-slice
-// (flash-decoding merge of (max, sum, acc) per chunk).
-struct ProAttn {
-    const float *am, *al, *aacc;   // [chunk][16], [chunk][16], [chunk][16][128]
-    const DevState *st;
-    int len_override;               // >= 0: attended length; else kv_len + 1
-    int n_heads;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
-    {
-        __shared__ float wts[MAX_CHUNKS * 16];
-        __shared__ float hm[16], hl[16];
-        const int L = len_override >= 0 ? len_override : st->kv_len + 1;
-        const int C = (L + KV_PAGE - 1) / KV_PAGE;
-        const int h0 = k0 / HEAD_DIM;
-        const int nh = min(KC / HEAD_DIM, n_heads - h0);
-        // per-head max and normaliser
-        for (int hh = threadIdx.x; hh < nh; hh += blockDim.x) {
-            const int h = h0 + hh;
-            float M = -INFINITY;
-            for (int c = 0; c < C; c++) M = fmaxf(M, am[c * 16 + h]);
-            float Ls = 0.0f;
-            for (int c = 0; c < C; c++) Ls += al[c * 16 + h] * expf(am[c * 16 + h] - M);
-            hm[hh] = M;
-            hl[hh] = Ls;
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < C * nh; i += blockDim.x) {
-            const int c = i / nh, hh = i - c * nh;
-            wts[i] = expf(am[c * 16 + h0 + hh] - hm[hh]) / hl[hh];
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
-            const int hh = i / HEAD_DIM, d = i - hh * HEAD_DIM;
-            float v = 0.0f;
-            if (hh < nh) {
-                const int h = h0 + hh;
-                for (int c = 0; c < C; c++)
-                    v += wts[c * nh + hh] * aacc[((size_t)c * 16 + h) * HEAD_DIM + d];
             }
             xs[i] = v;
         }
@@ -251,28 +301,17 @@ struct ProHidEmbed {
 };
 
 // ---------------------------------------------------------------------------
-// GEMV epilogues: receive (slice s, row b, column col, value y)
+// GEMV epilogues: (slice s, row b, column tile c, column cc in the tile,
+// tile width C, this row's tile outputs yb[0..C))
 // ---------------------------------------------------------------------------
 
 template <int NB>
 struct EpiPart {
     float *part;
     int npad;
-    __device__ void operator()(int s, int b, int col, float y) const
+    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
     {
-        part[((size_t)s * NB + b) * npad + col] = y;
-    }
-};
-
-// Single-slice weights: add into the residual stream x (talker.rs:334-336,
-// 347-349).
-template <int NB>
-struct EpiResid {
-    float *x;
-    int ld, n;
-    __device__ void operator()(int s, int b, int col, float y) const
-    {
-        if (col < n) x[(size_t)b * ld + col] += y;
+        part[((size_t)s * NB + b) * npad + c * C + cc] = yb[cc];
     }
 };
 
@@ -281,9 +320,25 @@ struct EpiStore {
     float *y;
     int ld, n;
     const float *bias;
-    __device__ void operator()(int s, int b, int col, float v) const
+    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
     {
-        if (col < n) y[(size_t)b * ld + col] = bias ? v + bias[col] : v;
+        const int col = c * C + cc;
+        if (col < n) y[(size_t)b * ld + col] = bias ? yb[cc] + bias[col] : yb[cc];
+    }
+};
+
+// Single-slice interleaved gate|up: h = silu(gate) * up, straight from the
+// tile (the tile holds whole gate/up group pairs).
+template <int NB>
+struct EpiSwiglu {
+    float *h;
+    int ld;
+    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    {
+        if ((cc & 63) < 32) {
+            const int j = (c * C + cc) >> 6;
+            h[(size_t)b * ld + j * 32 + (cc & 31)] = silu_f(yb[cc]) * yb[cc + 32];
+        }
     }
 };
 
@@ -340,6 +395,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     static_assert(R == 8, "scale block is one 16-byte load");
     __shared__ float xs[NB * KC];
     __shared__ float red[NW * NB * C];
+    __shared__ float ybuf[NB * C];
 
     const int t = threadIdx.x;
     const int lane = t & 63, wv = t >> 6;
@@ -356,7 +412,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             q[r] = __builtin_nontemporal_load((const u32x4 *)(tile + ((size_t)r * T + t) * 16));
         const u32x4 sc = __builtin_nontemporal_load((const u32x4 *)(tile + (size_t)R * T * 16 + (size_t)t * 16));
 
-        __syncthreads();               // xs / red of the previous item are free
+        __syncthreads();               // xs / red / ybuf of the previous item are free
         pro(xs, s * KC, KC, c);
         __syncthreads();
 
@@ -418,7 +474,12 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             float y = 0.0f;
 #pragma unroll
             for (int i = 0; i < NW; i++) y += red[(i * NB + b) * C + cc];
-            epi(s, b, c * C + cc, y);
+            ybuf[col] = y;
+        }
+        __syncthreads();
+        for (int col = t; col < NB * C; col += T) {
+            const int b = col / C, cc = col - b * C;
+            epi(s, b, c, cc, C, ybuf + b * C);
         }
     }
 }
@@ -426,16 +487,26 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
 template <int NB, class Pro, class Epi>
 static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st)
 {
-    const int items = w.S * w.CT;
-    const int grid = items;
+    const int grid = w.S * w.CT;
+#define QTTS_GEMV_CASE(CFG, T, GB)                                                              \
+    case CFG:                                                                                   \
+        hipLaunchKernelGGL((k_gemv<T, GB, 8, NB, Pro, Epi>), dim3(grid), dim3(T), 0, st, w, pro, epi); \
+        break;
     switch (w.cfg) {
-    case TILE_S256: hipLaunchKernelGGL((k_gemv<256, 8, 8, NB, Pro, Epi>), dim3(grid), dim3(256), 0, st, w, pro, epi); break;
-    case TILE_S128: hipLaunchKernelGGL((k_gemv<128, 8, 8, NB, Pro, Epi>), dim3(grid), dim3(128), 0, st, w, pro, epi); break;
-    case TILE_D256: hipLaunchKernelGGL((k_gemv<256, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(256), 0, st, w, pro, epi); break;
-    case TILE_D384: hipLaunchKernelGGL((k_gemv<384, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(384), 0, st, w, pro, epi); break;
-    case TILE_D768: hipLaunchKernelGGL((k_gemv<768, 1, 8, NB, Pro, Epi>), dim3(grid), dim3(768), 0, st, w, pro, epi); break;
+        QTTS_GEMV_CASE(TILE_G8_T256, 256, 8)
+        QTTS_GEMV_CASE(TILE_G8_T128, 128, 8)
+        QTTS_GEMV_CASE(TILE_G1_T64, 64, 1)
+        QTTS_GEMV_CASE(TILE_G1_T128, 128, 1)
+        QTTS_GEMV_CASE(TILE_G1_T256, 256, 1)
+        QTTS_GEMV_CASE(TILE_G1_T384, 384, 1)
+        QTTS_GEMV_CASE(TILE_G1_T768, 768, 1)
+        QTTS_GEMV_CASE(TILE_G2_T256, 256, 2)
+        QTTS_GEMV_CASE(TILE_G2_T512, 512, 2)
+        QTTS_GEMV_CASE(TILE_G4_T256, 256, 4)
+        QTTS_GEMV_CASE(TILE_G1_T512, 512, 1)
     default: return hipErrorInvalidValue;
     }
+#undef QTTS_GEMV_CASE
     return hipGetLastError();
 }
 
@@ -449,6 +520,7 @@ __global__ void k_reduce_parts(const float *part, int S, int NB, int npad, int n
     const int b = blockIdx.y;
     if (j >= n) return;
     float v = 0.0f;
+#pragma unroll 8
     for (int s = 0; s < S; s++) v += part[((size_t)s * NB + b) * npad + j];
     float *o = y + (size_t)b * ld + j;
     if (resid) v = *o + v;
@@ -465,10 +537,7 @@ static hipError_t reduce_parts(const float *part, int S, int NB, int npad, int n
 }
 
 // ---------------------------------------------------------------------------
-// talker: QKV partial sums -> QK-norm -> RoPE -> q buffer + paged KV append
-// (talker.rs:281-302).  Grid: one workgroup per KV head, 256 threads:
-// threads 0..127 own dim d of q head 2h and of k; 128..255 of q head 2h+1
-// and of v.
+// paged talker KV cache and RoPE
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
@@ -478,86 +547,92 @@ __device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, 
     return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
 }
 
-__device__ __forceinline__ void rope_rotate(float *buf, int d, float v, const float *cs,
-                                            const float *sn, float &out)
+// rotate-half pair (i, i+64) of one head held in buf (rope.rs:79-92)
+__device__ __forceinline__ float rope_rotate(const float *buf, int d, const float *cs, const float *sn)
 {
-    // buf holds the head's 128 values (post-norm); pair (i, i+64)
-    if (d < 64) out = buf[d] * cs[d] - buf[d + 64] * sn[d];
-    else out = buf[d] * cs[d - 64] + buf[d - 64] * sn[d - 64];
+    if (d < 64) return buf[d] * cs[d] - buf[d + 64] * sn[d];
+    return buf[d] * cs[d - 64] + buf[d - 64] * sn[d - 64];
 }
 
-__global__ void __launch_bounds__(256)
-k_talker_qkv_fin(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
-                 const float *rope_cos, const float *rope_sin, const DevState *st,
-                 int64_t pos_override, int slot_override, int layer, KvPaged kv, float *qbuf)
+// q heads 2h, 2h+1 and k, v of KV head h from the fused q|k|v partials:
+// sums over slices, QK-norm (talker.rs:89-99), RoPE at the table row cs/sn.
+// Thread t: d = t & 127; threads 0..127 own q(2h) and k, 128..255 q(2h+1)
+// and v.  Leaves the roped q in qr[upper][d]; returns k (normed, roped) or
+// v (raw).
+__device__ __forceinline__ float qkv_head_prologue(const float *part, int S, int NBP, int b, int npad,
+                                                   const uint16_t *qn_g, const uint16_t *kn_g,
+                                                   const float *cs, const float *sn, int h,
+                                                   float (*qr)[HEAD_DIM], float (*vb)[HEAD_DIM],
+                                                   float *scratch)
 {
-    __shared__ float scratch[16];
-    __shared__ float vbuf[3][HEAD_DIM];
-    const int h = blockIdx.x, t = threadIdx.x;
-    const int d = t & 127, upper = t >> 7;
-    const int64_t pos = pos_override >= 0 ? pos_override : st->position;
-    const int slot = slot_override >= 0 ? slot_override : st->kv_len;
+    const int t = threadIdx.x, d = t & 127, upper = t >> 7;
+    const int wv = t >> 6, lane = t & 63;
     const int qcol = (2 * h + upper) * HEAD_DIM + d;
     const int kvcol = 16 * HEAD_DIM + upper * 8 * HEAD_DIM + h * HEAD_DIM + d;   // k | v
     float qv = 0.0f, kvv = 0.0f;
+#pragma unroll 4
     for (int s = 0; s < S; s++) {
-        const float *p = part + (size_t)s * npad;
+        const float *p = part + ((size_t)s * NBP + b) * npad;
         qv += p[qcol];
         kvv += p[kvcol];
     }
-    // sums of squares: waves 0-1 -> q head 2h and k; waves 2-3 -> q head 2h+1
     const float qsq = wave_sum(qv * qv);
     const float ksq = wave_sum(kvv * kvv);
-    const int wv = t >> 6, lane = t & 63;
+    __syncthreads();
     if (lane == 0) { scratch[wv] = qsq; scratch[4 + wv] = ksq; }
     __syncthreads();
     const float ssq = upper ? scratch[2] + scratch[3] : scratch[0] + scratch[1];
     const float ssk = scratch[4] + scratch[5];
-    const float invq = 1.0f / sqrtf(ssq / 128.0f + 1e-6f);
-    const float invk = 1.0f / sqrtf(ssk / 128.0f + 1e-6f);
-    const float qn = qv * invq * h2f(qn_g[d]);
-    vbuf[upper][d] = qn;
-    if (!upper) vbuf[2][d] = kvv * invk * h2f(kn_g[d]);
+    const float qn = qv * (1.0f / sqrtf(ssq / 128.0f + 1e-6f)) * h2f(qn_g[d]);
+    vb[upper][d] = qn;
+    if (!upper) vb[2][d] = kvv * (1.0f / sqrtf(ssk / 128.0f + 1e-6f)) * h2f(kn_g[d]);
     __syncthreads();
-    const float *cs = rope_cos + pos * 64, *sn = rope_sin + pos * 64;
-    float qo, ko = 0.0f;
-    rope_rotate(vbuf[upper], d, qn, cs, sn, qo);
-    if (!upper) rope_rotate(vbuf[2], d, 0.0f, cs, sn, ko);
-    qbuf[qcol] = qo;
-    if (!upper) kv_ptr(kv, layer, slot, h, 0)[d] = ko;
-    else kv_ptr(kv, layer, slot, h, 1)[d] = kvv;
+    qr[upper][d] = rope_rotate(vb[upper], d, cs, sn);
+    return upper ? kvv : rope_rotate(vb[2], d, cs, sn);
 }
 
 // ---------------------------------------------------------------------------
 // talker decode attention, split over 64-position pages (flash-decoding).
-// Work item (chunk c, kv head h): both query heads 2h, 2h+1 share one pass
-// over the page's K and V (GQA, talker.rs:310).  Writes per (chunk, q head)
-// the running max, the exp-sum and the unnormalised P.V.
+// Work item (chunk c, kv head h): the q/k/v prologue, then both query heads
+// 2h, 2h+1 share one pass over the page's K and V (GQA, talker.rs:310).
+// The item owning the newest position appends K (normed, roped) and V (raw)
+// first (talker.rs:299-302).  Writes per (chunk, q head) the running max,
+// the exp-sum and the unnormalised P.V.
 // ---------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(256)
-k_talker_attn(const float *qbuf, KvPaged kv, int layer, const DevState *st, int len_override,
-              float *am, float *al, float *aacc)
+k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
+              const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
+              int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
+    __shared__ float scratch[16];
+    __shared__ float vb[3][HEAD_DIM];
+    __shared__ float qr[2][HEAD_DIM];
     __shared__ float sc[2][KV_PAGE];
     __shared__ float pv[2][2][HEAD_DIM];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int L = len_override >= 0 ? len_override : st->kv_len + 1;
+    const int slot = slot_ovr >= 0 ? slot_ovr : st->kv_len;
+    const int64_t pos = pos_ovr >= 0 ? pos_ovr : st->position;
+    const int L = slot + 1;
     const int C = (L + KV_PAGE - 1) / KV_PAGE;
     const float scale = 1.0f / sqrtf(128.0f);
+    const float *cs = rope_cos + pos * 64, *sn = rope_sin + pos * 64;
     const int j16 = lane & 15;
     for (int item = blockIdx.x; item < 8 * C; item += gridDim.x) {
         const int c = item >> 3, h = item & 7;
         const int ntok = min(KV_PAGE, L - c * KV_PAGE);
+        __syncthreads();
+        const float kvnew = qkv_head_prologue(part, S, 1, 0, npad, qn_g, kn_g, cs, sn, h, qr, vb, scratch);
+        if (c == C - 1) kv_ptr(kv, layer, slot, h, t >> 7)[t & 127] = kvnew;
+        __syncthreads();
         const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
         const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
         float q0[8], q1[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            q0[i] = qbuf[(2 * h) * HEAD_DIM + j16 * 8 + i];
-            q1[i] = qbuf[(2 * h + 1) * HEAD_DIM + j16 * 8 + i];
+            q0[i] = qr[0][j16 * 8 + i];
+            q1[i] = qr[1][j16 * 8 + i];
         }
-        __syncthreads();
 #pragma unroll
         for (int it = 0; it < 4; it++) {
             const int tok = wv * 16 + it * 4 + (lane >> 4);
@@ -616,11 +691,34 @@ k_talker_attn(const float *qbuf, KvPaged kv, int layer, const DevState *st, int 
     }
 }
 
+// Merge the chunks of one query head: out = sum_c w_c acc_c / sum_c w_c l_c,
+// w_c = exp(m_c - max m).  Grid: 16 heads x 128 threads.
+__global__ void __launch_bounds__(128)
+k_attn_combine(const float *am, const float *al, const float *aacc, const DevState *st, int slot_ovr,
+               float *out)
+{
+    __shared__ float w[MAX_CHUNKS];
+    __shared__ float scratch[16];
+    const int h = blockIdx.x, d = threadIdx.x;
+    const int L = (slot_ovr >= 0 ? slot_ovr : st->kv_len) + 1;
+    const int C = (L + KV_PAGE - 1) / KV_PAGE;
+    const float m = d < C ? am[d * 16 + h] : -INFINITY;
+    const float l = d < C ? al[d * 16 + h] : 0.0f;
+    const float M = block_max(m, scratch);
+    const float wc = d < C ? expf(m - M) : 0.0f;
+    if (d < C) w[d] = wc;
+    const float Ls = block_sum(l * wc, scratch);
+    float o = 0.0f;
+#pragma unroll 8
+    for (int c = 0; c < C; c++) o += w[c] * aacc[((size_t)c * 16 + h) * HEAD_DIM + d];
+    out[h * HEAD_DIM + d] = o / Ls;
+}
+
 // ---------------------------------------------------------------------------
-// predictor: QKV sums -> QK-norm -> RoPE -> KV append -> causal attention
-// over <= 16 positions, fused (code_predictor.rs:369-414, 457-498).
-// Grid: one workgroup per KV head; NB tokens at positions pos0..pos0+NB-1.
-// Output: attn[b][16*128] (final, normalised).
+// predictor: q|k|v partial sums -> QK-norm -> RoPE -> KV append -> causal
+// attention over <= 16 positions, fused (code_predictor.rs:369-414,
+// 457-498).  Grid: one workgroup per KV head; NB tokens at positions
+// pos0..pos0+NB-1.  Output: attn[b][16*128] (final, normalised).
 // ---------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(256)
@@ -629,52 +727,30 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
             float *attn)
 {
     __shared__ float scratch[16];
-    __shared__ float vbuf[3][HEAD_DIM];
+    __shared__ float vb[3][HEAD_DIM];
     __shared__ float qr[2][2][HEAD_DIM];          // [token][head][d]
     __shared__ float Ks[PRED_KV_CAP][HEAD_DIM], Vs[PRED_KV_CAP][HEAD_DIM];
     __shared__ float prob[2][2][PRED_KV_CAP];
     const int h = blockIdx.x, t = threadIdx.x;
-    const int d = t & 127, upper = t >> 7, wv = t >> 6, lane = t & 63;
+    const int d = t & 127, upper = t >> 7;
     const size_t kvrow = 8 * HEAD_DIM;
-    for (int b = 0; b < NB; b++) {
-        const int pos = pos0 + b;
-        const int qcol = (2 * h + upper) * HEAD_DIM + d;
-        const int kvcol = 16 * HEAD_DIM + upper * 8 * HEAD_DIM + h * HEAD_DIM + d;
-        float qv = 0.0f, kvv = 0.0f;
-        for (int s = 0; s < S; s++) {
-            const float *p = part + ((size_t)s * NB + b) * npad;
-            qv += p[qcol];
-            kvv += p[kvcol];
-        }
-        const float qsq = wave_sum(qv * qv);
-        const float ksq = wave_sum(kvv * kvv);
-        __syncthreads();
-        if (lane == 0) { scratch[wv] = qsq; scratch[4 + wv] = ksq; }
-        __syncthreads();
-        const float ssq = upper ? scratch[2] + scratch[3] : scratch[0] + scratch[1];
-        const float ssk = scratch[4] + scratch[5];
-        const float qn = qv * (1.0f / sqrtf(ssq / 128.0f + 1e-6f)) * h2f(qn_g[d]);
-        vbuf[upper][d] = qn;
-        if (!upper) vbuf[2][d] = kvv * (1.0f / sqrtf(ssk / 128.0f + 1e-6f)) * h2f(kn_g[d]);
-        __syncthreads();
-        const float *cs = rope_cos + (size_t)pos * 64, *sn = rope_sin + (size_t)pos * 64;
-        float qo, ko = 0.0f;
-        rope_rotate(vbuf[upper], d, qn, cs, sn, qo);
-        if (!upper) rope_rotate(vbuf[2], d, 0.0f, cs, sn, ko);
-        qr[b][upper][d] = qo;
-        if (!upper) {
-            Ks[pos][d] = ko;
-            Kc[pos * kvrow + h * HEAD_DIM + d] = ko;
-        } else {
-            Vs[pos][d] = kvv;
-            Vc[pos * kvrow + h * HEAD_DIM + d] = kvv;
-        }
-    }
     // earlier positions of this head, written by previous launches
     for (int i = t; i < pos0 * HEAD_DIM; i += blockDim.x) {
         const int p = i / HEAD_DIM, dd = i - p * HEAD_DIM;
         Ks[p][dd] = Kc[p * kvrow + h * HEAD_DIM + dd];
         Vs[p][dd] = Vc[p * kvrow + h * HEAD_DIM + dd];
+    }
+    for (int b = 0; b < NB; b++) {
+        const int pos = pos0 + b;
+        const float *cs = rope_cos + (size_t)pos * 64, *sn = rope_sin + (size_t)pos * 64;
+        const float kvnew = qkv_head_prologue(part, S, NB, b, npad, qn_g, kn_g, cs, sn, h, qr[b], vb, scratch);
+        if (!upper) {
+            Ks[pos][d] = kvnew;
+            Kc[pos * kvrow + h * HEAD_DIM + d] = kvnew;
+        } else {
+            Vs[pos][d] = kvnew;
+            Vc[pos * kvrow + h * HEAD_DIM + d] = kvnew;
+        }
     }
     __syncthreads();
     const float scale = 1.0f / sqrtf(128.0f);
@@ -732,6 +808,7 @@ k_argmax(const float *part, int S, int npad, int n, DevState *st, int slot,
     int bidx = -1;
     for (int j = t; j < n; j += blockDim.x) {
         float v = 0.0f;
+#pragma unroll 4
         for (int s = 0; s < S; s++) v += part[(size_t)s * npad + j];
         if (isnan(v)) nanf = 1;
         if (bidx < 0 || v >= best) { best = v; bidx = j; }
@@ -809,13 +886,23 @@ __global__ void k_embed_row(Q4Rows e, const uint32_t *code, uint32_t code_imm, f
     out[j] = q4_row_value(e, code ? *code : code_imm, j);
 }
 
+__global__ void k_silu(float *x, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = silu_f(x[i]);
+}
+
 // ---------------------------------------------------------------------------
 // sampler (sample_token, generate_new.rs:771-862) in one workgroup.
-// Ranking uses a bitonic sort of (p desc, index asc) == Rust's stable sort.
-// The final cumulative sum runs over nonzero probabilities in index order.
+// Top-k keeps the k largest probabilities with ties broken by lower index
+// (Rust's stable sort): a 4-pass radix select finds the k-th largest value,
+// then equal values are admitted in index order.  Top-p sorts the kept
+// entries (bitonic, rank = (p desc, index asc)).  The draw walks nonzero
+// probabilities in index order.
 // ---------------------------------------------------------------------------
 
 constexpr int SAMP_MAX = 4096;
+constexpr int SAMP_T = 1024;
 
 __device__ __forceinline__ bool rank_before(float pa, int ia, float pb, int ib)
 {
@@ -829,7 +916,7 @@ __device__ void bitonic_sort_desc(float *kp, int *ki, int N)
             for (int i = threadIdx.x; i < N; i += blockDim.x) {
                 const int ixj = i ^ j;
                 if (ixj > i) {
-                    const bool up = (i & k) == 0;   // this block sorted "before-first"
+                    const bool up = (i & k) == 0;
                     const float pa = kp[i], pb = kp[ixj];
                     const int ia = ki[i], ib = ki[ixj];
                     const bool swap = up ? rank_before(pb, ib, pa, ia) : rank_before(pa, ia, pb, ib);
@@ -849,8 +936,6 @@ __device__ __forceinline__ float simple_rand_dev(uint64_t &s)
     return (float)s / 18446744073709551616.0f;   // (state as f32) / (u64::MAX as f32)
 }
 
-// mode 0: frame (reads state sampler params and temperature schedule, writes
-// code 0, honours stop/force); mode 1: API call with explicit params.
 struct SampleArgs {
     float temperature, top_p, rep;
     int top_k;
@@ -858,7 +943,56 @@ struct SampleArgs {
     int n_prev;
 };
 
-__global__ void __launch_bounds__(1024)
+// Keeps the top_k largest entries of p[0..n) (p >= 0, no NaN), zeroing the
+// rest; among equal values the lower indices are kept.
+__device__ void topk_select(float *p, int n, int top_k, int *hist, int *iscratch)
+{
+    __shared__ uint32_t prefix_s, mask_s;
+    __shared__ int need_s;
+    const int t = threadIdx.x;
+    if (t == 0) { prefix_s = 0; mask_s = 0; need_s = top_k; }
+    __syncthreads();
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        for (int i = t; i < 256; i += blockDim.x) hist[i] = 0;
+        __syncthreads();
+        const uint32_t prefix = prefix_s, mask = mask_s;
+        for (int i = t; i < n; i += blockDim.x) {
+            const uint32_t b = __float_as_uint(p[i]);
+            if ((b & mask) == prefix) atomicAdd(&hist[(b >> shift) & 0xFF], 1);
+        }
+        __syncthreads();
+        if (t == 0) {
+            int need = need_s, bin = 255;
+            for (; bin > 0; bin--) {
+                if (hist[bin] >= need) break;
+                need -= hist[bin];
+            }
+            prefix_s = prefix | ((uint32_t)bin << shift);
+            mask_s = mask | (0xFFu << shift);
+            need_s = need;
+        }
+        __syncthreads();
+    }
+    // thr: bits of the k-th largest value; need_eq: how many entries equal
+    // to it stay (the lowest indices)
+    const uint32_t thr = prefix_s;
+    const int need_eq = need_s;
+    const int per = (n + blockDim.x - 1) / blockDim.x;
+    const int i0 = t * per, i1 = min(i0 + per, n);
+    int eq = 0;
+    for (int i = i0; i < i1; i++) eq += __float_as_uint(p[i]) == thr;
+    int before = block_excl_scan(eq, iscratch, nullptr);
+    for (int i = i0; i < i1; i++) {
+        const uint32_t b = __float_as_uint(p[i]);
+        bool keep = b > thr;
+        if (b == thr) keep = before++ < need_eq;
+        if (!keep) p[i] = 0.0f;
+    }
+    __syncthreads();
+}
+
+__global__ void __launch_bounds__(SAMP_T)
 k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, uint64_t *rng_api,
           uint32_t *out_api, const uint32_t *forced)
 {
@@ -866,8 +1000,10 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
     __shared__ float kp[SAMP_MAX];
     __shared__ int ki[SAMP_MAX];
     __shared__ float scratch[16];
-    __shared__ int cnt[1024];
+    __shared__ int iscratch[16];
+    __shared__ int hist[256];
     __shared__ int nanf;
+    __shared__ int cutoff_s;
     const int t = threadIdx.x;
     if (mode == 0 && st->stop) return;
     float temp, top_p, rep;
@@ -887,7 +1023,7 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
     if (t == 0 && rep != 1.0f) {
         for (int i = 0; i < n_prev; i++) {
             const uint32_t tok = prev[i];
-            if ((int)tok < n && tok < (uint32_t)n) {
+            if (tok < (uint32_t)n) {
                 const float v = p[tok];
                 p[tok] = v > 0.0f ? v / rep : v * rep;
             }
@@ -910,92 +1046,76 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
         sum += e;
     }
     sum = block_sum(sum, scratch);
-    for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / sum;
+    for (int i = t; i < n; i += blockDim.x) {
+        const float v = p[i] / sum;
+        if (isnan(v)) nanf = 1;
+        p[i] = v;
+    }
     __syncthreads();
 
     const bool do_k = top_k > 0 && top_k < n;
     const bool do_p = top_p > 0.0f && top_p < 1.0f;
-    if (do_k || do_p) {
+    if ((do_k || do_p) && nanf) {        // Rust panics in partial_cmp().unwrap()
+        if (t == 0) {
+            st->nan_flag = 1;
+            if (mode == 0) st->stop = 1; else *out_api = 0;
+        }
+        return;
+    }
+    if (do_k) {
+        topk_select(p, n, top_k, hist, iscratch);
+        float s2 = 0.0f;
+        for (int i = t; i < n; i += blockDim.x) s2 += p[i];
+        s2 = block_sum(s2, scratch);
+        if (s2 > 0.0f)
+            for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s2;
+        __syncthreads();
+    }
+    if (do_p) {
+        // rank the nonzero entries (after top-k at most top_k of them)
+        const int per = (n + blockDim.x - 1) / blockDim.x;
+        const int i0 = t * per, i1 = min(i0 + per, n);
+        int c = 0;
+        for (int i = i0; i < i1; i++) c += p[i] != 0.0f;
+        int tot = 0;
+        int o = block_excl_scan(c, iscratch, &tot);
+        for (int i = i0; i < i1; i++)
+            if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
         int N = 1;
-        while (N < n) N <<= 1;
-        for (int i = t; i < N; i += blockDim.x) {
-            const float v = i < n ? p[i] : -1.0f;
-            if (i < n && isnan(v)) nanf = 1;
-            kp[i] = v;
-            ki[i] = i < n ? i : 0x7fffffff;
+        while (N < tot) N <<= 1;
+        for (int i = tot + t; i < N; i += blockDim.x) { kp[i] = -1.0f; ki[i] = 0x7fffffff; }
+        __syncthreads();
+        bitonic_sort_desc(kp, ki, N);
+        if (t == 0) {
+            float cum = 0.0f;
+            int cutoff = n;
+            for (int r = 0; r < tot; r++) {
+                cum += kp[r];
+                if (cum >= top_p) { cutoff = r + 1; break; }
+            }
+            cutoff_s = cutoff < 1 ? 1 : cutoff;
         }
         __syncthreads();
-        if (nanf) {
-            if (t == 0) {
-                st->nan_flag = 1;
-                if (mode == 0) { st->stop = 1; } else { *out_api = 0; }
-            }
-            return;
-        }
-        bitonic_sort_desc(kp, ki, N);
-        if (do_k) {
-            for (int r = t; r < n; r += blockDim.x)
-                if (r >= top_k) p[ki[r]] = 0.0f;
-            __syncthreads();
-            float s2 = 0.0f;
-            for (int i = t; i < n; i += blockDim.x) s2 += p[i];
-            s2 = block_sum(s2, scratch);
-            if (s2 > 0.0f)
-                for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s2;
-            __syncthreads();
-        }
-        if (do_p) {
-            // ranks are unchanged by the renormalisation; zeroed entries
-            // rank after all nonzero ones.
-            __shared__ int cutoff_s;
-            if (t == 0) {
-                float cum = 0.0f;
-                int cutoff = n;
-                for (int r = 0; r < n; r++) {
-                    const int idx = ki[r];
-                    const float pr = (do_k && r >= top_k) ? 0.0f : p[idx];
-                    cum += pr;
-                    if (cum >= top_p) { cutoff = r + 1; break; }
-                }
-                cutoff_s = cutoff < 1 ? 1 : cutoff;
-            }
-            __syncthreads();
-            for (int r = t; r < n; r += blockDim.x)
-                if (r >= cutoff_s) p[ki[r]] = 0.0f;
-            __syncthreads();
-            float s3 = 0.0f;
-            for (int i = t; i < n; i += blockDim.x) s3 += p[i];
-            s3 = block_sum(s3, scratch);
-            if (s3 > 0.0f)
-                for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s3;
-            __syncthreads();
-        }
+        for (int r = cutoff_s + t; r < tot; r += blockDim.x) p[ki[r]] = 0.0f;
+        __syncthreads();
+        float s3 = 0.0f;
+        for (int i = t; i < n; i += blockDim.x) s3 += p[i];
+        s3 = block_sum(s3, scratch);
+        if (s3 > 0.0f)
+            for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s3;
+        __syncthreads();
     }
-    // compact nonzero probabilities in index order
+    // compact nonzero probabilities in index order, then the cumulative draw
     const int per = (n + blockDim.x - 1) / blockDim.x;
     const int i0 = t * per, i1 = min(i0 + per, n);
     int c = 0;
     for (int i = i0; i < i1; i++) c += p[i] != 0.0f;
-    cnt[t] = c;
+    int total = 0;
+    int o = block_excl_scan(c, iscratch, &total);
+    for (int i = i0; i < i1; i++)
+        if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
     __syncthreads();
     if (t == 0) {
-        int acc = 0;
-        for (int i = 0; i < (int)blockDim.x; i++) { const int v = cnt[i]; cnt[i] = acc; acc += v; }
-    }
-    __syncthreads();
-    {
-        int o = cnt[t];
-        for (int i = i0; i < i1; i++)
-            if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
-    }
-    __syncthreads();
-    if (t == 0) {
-        const int nz = cnt[blockDim.x - 1] + 0;   // exclusive prefix of the last thread
-        int total = nz;
-        {
-            const int li0 = (blockDim.x - 1) * per, li1 = min(li0 + per, n);
-            for (int i = li0; i < li1; i++) total += p[i] != 0.0f;
-        }
         uint64_t rs = mode == 0 ? st->rng : *rng_api;
         const float r = simple_rand_dev(rs);
         float cs = 0.0f;
@@ -1033,6 +1153,7 @@ k_step_end(const float *part, int S, int npad, int V, const float *hid_work, int
     if (frame_mode && st->stop) return;
     for (int j = t; j < V; j += blockDim.x) {
         float v = 0.0f;
+#pragma unroll 4
         for (int s = 0; s < S; s++) v += part[(size_t)s * npad + j];
         logits[j] = v;
     }
@@ -1077,12 +1198,6 @@ __global__ void k_kv_scatter(KvPaged kv, int layer, int len, const float *K, con
     kv_ptr(kv, layer, pos, h, 1)[d] = V[i];
 }
 
-__global__ void k_fill_u32(uint32_t *p, uint32_t v, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = v;
-}
-
 // ===========================================================================
 // host-side enqueue functions
 // ===========================================================================
@@ -1124,12 +1239,6 @@ hipError_t enqueue_embed_row(const Q4Rows &e, const uint32_t *code_dev, uint32_t
     return hipGetLastError();
 }
 
-__global__ void k_silu(float *x, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) x[i] = silu_f(x[i]);
-}
-
 hipError_t enqueue_silu(float *x, int n, hipStream_t st)
 {
     hipLaunchKernelGGL(k_silu, dim3((n + 255) / 256), dim3(256), 0, st, x, n);
@@ -1143,78 +1252,84 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
     return hipGetLastError();
 }
 
-// One talker layer, decode (talker.rs:274-350).  x is updated in place.
-static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, float *x,
-                               const DevState *st, int64_t pos_ovr, int slot_ovr, int len_ovr,
-                               hipStream_t s)
+// gate|up then down: h = silu(gate) * up written by the gate|up epilogue when
+// the gate|up weight is one slice, else formed in the down prologue.
+template <int NB, class ProGU>
+static hipError_t swiglu_down(const LayerDev &L, const Workspace &ws, const ProGU &pro_gu, int inter,
+                              hipStream_t s)
 {
-    const LayerDev &L = m.layers[l];
-    const int H = m.hidden;
-    // 1. RMSNorm + fused q|k|v GEMV -> partials
-    QCHK(launch_gemv<1>(L.qkv, ProRms<1>{x, H, H, L.input_norm, nullptr},
-                        EpiPart<1>{ws.part_a, L.qkv.npad}, s));
-    // 2. sums, QK-norm, RoPE, KV append
-    hipLaunchKernelGGL(k_talker_qkv_fin, dim3(m.n_kv_heads), dim3(256), 0, s, ws.part_a, L.qkv.S,
-                       L.qkv.npad, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr,
-                       l, m.kv, ws.qbuf);
-    QCHK(hipGetLastError());
-    // 3. split-K attention over the pages
-    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.qbuf, m.kv, l, st,
-                       len_ovr, ws.am, ws.al, ws.aacc);
-    QCHK(hipGetLastError());
-    // 4. merge chunks + o_proj + residual
-    if (L.o.S == 1) {
-        QCHK(launch_gemv<1>(L.o, ProAttn{ws.am, ws.al, ws.aacc, st, len_ovr, m.n_heads},
-                            EpiResid<1>{x, H, H}, s));
-    } else {
-        QCHK(launch_gemv<1>(L.o, ProAttn{ws.am, ws.al, ws.aacc, st, len_ovr, m.n_heads},
-                            EpiPart<1>{ws.part_b, L.o.npad}, s));
-        QCHK(reduce_parts(ws.part_b, L.o.S, 1, L.o.npad, H, x, H, nullptr, 1, s));
+    if (L.gate_up.S == 1 && tile_shape(L.gate_up.cfg).GB % 2 == 0) {
+        QCHK(launch_gemv<NB>(L.gate_up, pro_gu, EpiSwiglu<NB>{ws.h, inter}, s));
+        return launch_gemv<NB>(L.down, ProPlain<NB>{ws.h, inter, inter}, EpiPart<NB>{ws.part_down, L.down.npad}, s);
     }
-    // 5. RMSNorm + fused gate|up GEMV -> partials
-    QCHK(launch_gemv<1>(L.gate_up, ProRms<1>{x, H, H, L.post_norm, nullptr},
-                        EpiPart<1>{ws.part_a, L.gate_up.npad}, s));
-    // 6. silu(gate)*up + down + residual
-    const ProSwiglu<1> sw{ws.part_a, L.gate_up.S, L.gate_up.npad, m.inter};
-    if (L.down.S == 1) {
-        QCHK(launch_gemv<1>(L.down, sw, EpiResid<1>{x, H, H}, s));
-    } else {
-        QCHK(launch_gemv<1>(L.down, sw, EpiPart<1>{ws.part_b, L.down.npad}, s));
-        QCHK(reduce_parts(ws.part_b, L.down.S, 1, L.down.npad, H, x, H, nullptr, 1, s));
-    }
-    return hipSuccess;
+    QCHK(launch_gemv<NB>(L.gate_up, pro_gu, EpiPart<NB>{ws.part_gu, L.gate_up.npad}, s));
+    return launch_gemv<NB>(L.down, ProSwiglu<NB>{ws.part_gu, L.gate_up.S, L.gate_up.npad, inter},
+                           EpiPart<NB>{ws.part_down, L.down.npad}, s);
 }
 
-// forward_with_embedding (talker.rs:263-360) on the workspace input ws.x:
-// 28 layers, final norm (hidden -> ws.hid_work), codec head partials
-// (ws.part_head), then k_step_end.
+// One talker layer, decode (talker.rs:274-350).  The residual stream enters
+// as base (+ the previous layer's down partials) and leaves as ws.xa plus
+// this layer's down partials.
+static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, const float *x_in,
+                               const DevState *st, int64_t pos_ovr, int slot_ovr, hipStream_t s)
+{
+    const LayerDev &L = m.layers[l];
+    const LayerDev *P = l > 0 ? &m.layers[l - 1] : nullptr;
+    const int H = m.hidden;
+    // 1. residual + RMSNorm + fused q|k|v GEMV -> partials
+    const ProResidRms<1> pre_attn{l == 0 ? x_in : ws.xa, H, P ? ws.part_down : nullptr, P ? P->down.S : 0, 1, 0,
+                                  P ? P->down.npad : 0, nullptr, L.input_norm, H, ws.xb, nullptr};
+    QCHK(launch_gemv<1>(L.qkv, pre_attn, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
+    // 2. QK-norm, RoPE, KV append, split-K attention over the pages
+    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
+                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
+                       ws.al, ws.aacc);
+    QCHK(hipGetLastError());
+    // 3. merge the chunks
+    hipLaunchKernelGGL(k_attn_combine, dim3(m.n_heads), dim3(HEAD_DIM), 0, s, ws.am, ws.al, ws.aacc, st,
+                       slot_ovr, ws.attn);
+    QCHK(hipGetLastError());
+    // 4. o_proj -> partials
+    QCHK(launch_gemv<1>(L.o, ProPlain<1>{ws.attn, 16 * HEAD_DIM, 16 * HEAD_DIM}, EpiPart<1>{ws.part_o, L.o.npad}, s));
+    // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
+    const ProResidRms<1> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
+    return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);
+}
+
+// Final norm of the residual (talker.rs:352-353) into `side` + codec-head
+// partials.
+static hipError_t talker_head(const TalkerDev &m, const Workspace &ws, float *side, hipStream_t s)
+{
+    const LayerDev &P = m.layers[m.n_layers - 1];
+    const ProResidRms<1> pre{ws.xa, m.hidden, ws.part_down, P.down.S, 1, 0, P.down.npad, nullptr, m.final_norm,
+                             m.hidden, nullptr, side};
+    return launch_gemv<1>(m.codec_head, pre, EpiPart<1>{ws.part_head, m.codec_head.npad}, s);
+}
+
+// forward_with_embedding (talker.rs:263-360) on the input ws.x: 28 layers,
+// final norm (hidden -> ws.hid_work), codec head, then k_step_end.
 hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
                                hipStream_t s)
 {
-    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, -1, -1, -1, s));
-    QCHK(launch_gemv<1>(m.codec_head, ProRms<1>{ws.x, m.hidden, m.hidden, m.final_norm, ws.hid_work},
-                        EpiPart<1>{ws.part_head, m.codec_head.npad}, s));
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, -1, -1, s));
+    QCHK(talker_head(m, ws, ws.hid_work, s));
     hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1024), 0, s, ws.part_head, m.codec_head.S,
                        m.codec_head.npad, m.vocab, ws.hid_work, m.hidden, ws.logits, ws.hidden, st,
                        frame_mode, ws.ring_pred, ws.ring_used);
     return hipGetLastError();
 }
 
-// One row of a prefill: same layers, RoPE at pos, KV slot = pos - start +
-// kv_len0 handled by the overrides; no codec head.
-hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st,
-                              int64_t pos, int slot, hipStream_t s)
+// One prefill row: RoPE at pos, KV slot `slot`, no codec head.
+hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,
+                              int slot, hipStream_t s)
 {
-    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, pos, slot, slot + 1, s));
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, pos, slot, s));
     return hipSuccess;
 }
 
 hipError_t enqueue_final_norm(const TalkerDev &m, const Workspace &ws, float *hidden_out, hipStream_t s)
 {
-    // normed hidden only (talker.rs:480-481): reuse the codec-head prologue
-    QCHK(launch_gemv<1>(m.codec_head, ProRms<1>{ws.x, m.hidden, m.hidden, m.final_norm, hidden_out},
-                        EpiPart<1>{ws.part_head, m.codec_head.npad}, s));
-    return hipSuccess;
+    return talker_head(m, ws, hidden_out, s);
 }
 
 hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const float *hidden, float *logits,
@@ -1227,81 +1342,70 @@ hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const flo
 }
 
 // One predictor layer over NB tokens at positions pos0.. (code_predictor.rs:
-// 354-432 for NB=2, 450-510 for NB=1).  x: [NB][h].
+// 354-432 for NB=2, 450-510 for NB=1).  Layer 0 starts from the input
+// projection partials + bias.
 template <int NB>
-static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, float *x, int pos0,
-                             hipStream_t s)
+static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
 {
     const LayerDev &L = p.layers[l];
     const int h = p.hidden;
-    QCHK(launch_gemv<NB>(L.qkv, ProRms<NB>{x, h, h, L.input_norm, nullptr},
-                         EpiPart<NB>{ws.part_a, L.qkv.npad}, s));
-    hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_a, L.qkv.S, NB,
-                       L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
+    const ProResidRms<NB> pre_attn =
+        l == 0 ? ProResidRms<NB>{nullptr, h, ws.part_proj, p.proj.S, NB, 0, p.proj.npad, p.proj_bias, L.input_norm,
+                                 h, ws.pxb, nullptr}
+               : ProResidRms<NB>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
+                                 p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
+    QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
+    hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, NB, L.qkv.npad,
+                       L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
                        ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM,
                        ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM, ws.pattn);
     QCHK(hipGetLastError());
     const int qd = p.n_heads * HEAD_DIM;
-    if (L.o.S == 1) {
-        QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiResid<NB>{x, h, h}, s));
-    } else {
-        QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiPart<NB>{ws.part_b, L.o.npad}, s));
-        QCHK(reduce_parts(ws.part_b, L.o.S, NB, L.o.npad, h, x, h, nullptr, 1, s));
-    }
-    QCHK(launch_gemv<NB>(L.gate_up, ProRms<NB>{x, h, h, L.post_norm, nullptr},
-                         EpiPart<NB>{ws.part_a, L.gate_up.npad}, s));
-    const ProSwiglu<NB> sw{ws.part_a, L.gate_up.S, L.gate_up.npad, p.inter};
-    if (L.down.S == 1) {
-        QCHK(launch_gemv<NB>(L.down, sw, EpiResid<NB>{x, h, h}, s));
-    } else {
-        QCHK(launch_gemv<NB>(L.down, sw, EpiPart<NB>{ws.part_b, L.down.npad}, s));
-        QCHK(reduce_parts(ws.part_b, L.down.S, NB, L.down.npad, h, x, h, nullptr, 1, s));
-    }
-    return hipSuccess;
+    QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiPart<NB>{ws.part_o, L.o.npad}, s));
+    const ProResidRms<NB> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
+    return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s);
+}
+
+// final norm of row `row` of the last layer's output + lm_head[g] + argmax
+static hipError_t pred_head(const PredictorDev &p, const Workspace &ws, DevState *st, int g, int NBP, int row,
+                            const uint32_t *forced, uint32_t *codes_api, hipStream_t s)
+{
+    const LayerDev &P = p.layers[p.n_layers - 1];
+    const ProResidRms<1> pre{ws.pxa + (size_t)row * p.hidden, p.hidden, ws.part_down, P.down.S, NBP, row,
+                             P.down.npad, nullptr, p.final_norm, p.hidden, nullptr, nullptr};
+    QCHK(launch_gemv<1>(p.heads[g], pre, EpiPart<1>{ws.part_head, p.heads[g].npad}, s));
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[g].S, p.heads[g].npad, p.vocab,
+                       st, g + 1, forced, codes_api);
+    return hipGetLastError();
 }
 
 // generate_acoustic_codes (code_predictor.rs:218-273).  Inputs: talker
-// hidden (ws.hidden or `hidden`), semantic code in st->used[0] (frame mode)
-// or the explicit semantic embedding `sem` (API mode).  Codes go to
+// hidden and either the semantic code in st->used[0] (frame mode, sem ==
+// nullptr) or an explicit semantic embedding `sem` (API mode).  Codes go to
 // st->pred[1..15] / st->used[1..15] (and codes_api when given).
 hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, const Workspace &ws,
                                    DevState *st, const float *hidden, const float *sem,
                                    const uint32_t *forced, uint32_t *codes_api, hipStream_t s)
 {
-    const int h = p.hidden;
-    float *x = ws.px;   // [2][h]
     // projections of [talker hidden, semantic embedding] (:235-241)
     if (sem) {
-        // API mode: stage [hidden; sem] into ws.pin (2 rows) then plain GEMV
         QCHK(hipMemcpyAsync(ws.pin, hidden, sizeof(float) * m.hidden, hipMemcpyDeviceToDevice, s));
         QCHK(hipMemcpyAsync(ws.pin + m.hidden, sem, sizeof(float) * m.hidden, hipMemcpyDeviceToDevice, s));
-        QCHK(launch_gemv<2>(p.proj, ProPlain<2>{ws.pin, m.hidden, m.hidden},
-                            EpiPart<2>{ws.part_b, p.proj.npad}, s));
+        QCHK(launch_gemv<2>(p.proj, ProPlain<2>{ws.pin, m.hidden, m.hidden}, EpiPart<2>{ws.part_proj, p.proj.npad}, s));
     } else {
         QCHK(launch_gemv<2>(p.proj, ProHidEmbed{hidden, m.codec_rows, &st->used[0], m.hidden},
-                            EpiPart<2>{ws.part_b, p.proj.npad}, s));
+                            EpiPart<2>{ws.part_proj, p.proj.npad}, s));
     }
-    QCHK(reduce_parts(ws.part_b, p.proj.S, 2, p.proj.npad, h, x, h, p.proj_bias, 0, s));
-    for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, x, 0, s));
-    // final norm of the last row + lm_head[0] + argmax (:247-248)
-    QCHK(launch_gemv<1>(p.heads[0], ProRms<1>{x + h, h, h, p.final_norm, nullptr},
-                        EpiPart<1>{ws.part_head, p.heads[0].npad}, s));
-    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[0].S,
-                       p.heads[0].npad, p.vocab, st, 1, forced, codes_api);
-    QCHK(hipGetLastError());
+    for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, 0, s));
+    QCHK(pred_head(p, ws, st, 0, 2, 1, forced, codes_api, s));           // :247-248
     for (int g = 1; g < p.n_groups; g++) {
         // embed the previous code with codebook g-1, project (:255-260)
         Q4Rows e = p.emb_rows;
         e.packed += (size_t)(g - 1) * e.rows * e.G * 16;
         e.scales += (size_t)(g - 1) * e.rows * e.G;
-        QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_b, p.proj.npad}, s));
-        QCHK(reduce_parts(ws.part_b, p.proj.S, 1, p.proj.npad, h, x, h, p.proj_bias, 0, s));
-        for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, x, 1 + g, s));
-        QCHK(launch_gemv<1>(p.heads[g], ProRms<1>{x, h, h, p.final_norm, nullptr},
-                            EpiPart<1>{ws.part_head, p.heads[g].npad}, s));
-        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[g].S,
-                           p.heads[g].npad, p.vocab, st, g + 1, forced, codes_api);
-        QCHK(hipGetLastError());
+        QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_proj, p.proj.npad}, s));
+        for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
+        QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
     }
     return hipSuccess;
 }
@@ -1312,7 +1416,7 @@ hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Worksp
                          const uint32_t *forced, hipStream_t s)
 {
     SampleArgs none{};
-    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(1024), 0, s, ws.logits, m.vocab, st, 0, none,
+    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(SAMP_T), 0, s, ws.logits, m.vocab, st, 0, none,
                        (uint64_t *)nullptr, (uint32_t *)nullptr, forced);
     QCHK(hipGetLastError());
     QCHK(enqueue_predictor_chain(p, m, ws, st, ws.hidden, nullptr, forced, nullptr, s));
@@ -1326,7 +1430,7 @@ hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &
                               uint32_t *out_dev, DevState *st, hipStream_t s)
 {
     SampleArgs sa{a.temperature, a.top_p, a.rep, a.top_k, a.prev, a.n_prev};
-    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(1024), 0, s, logits, n, st, 1, sa, rng_dev, out_dev,
+    hipLaunchKernelGGL(k_sampler, dim3(1), dim3(SAMP_T), 0, s, logits, n, st, 1, sa, rng_dev, out_dev,
                        (const uint32_t *)nullptr);
     return hipGetLastError();
 }
@@ -1348,17 +1452,27 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
     return hipGetLastError();
 }
 
+// Timing helpers: the gate|up GEMV of layer l with its real prologue, and the
+// decode attention of layer l over `len` positions.
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
-    return launch_gemv<1>(L.gate_up, ProRms<1>{ws.x, m.hidden, m.hidden, L.post_norm, nullptr},
-                          EpiPart<1>{ws.part_a, L.gate_up.npad}, s);
+    const ProResidRms<1> pre{ws.xb, m.hidden, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, m.hidden,
+                             nullptr, nullptr};
+    if (L.gate_up.S == 1 && tile_shape(L.gate_up.cfg).GB % 2 == 0)
+        return launch_gemv<1>(L.gate_up, pre, EpiSwiglu<1>{ws.h, m.inter}, s);
+    return launch_gemv<1>(L.gate_up, pre, EpiPart<1>{ws.part_gu, L.gate_up.npad}, s);
 }
 
-hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int len, hipStream_t s)
+hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
+                               hipStream_t s)
 {
-    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.qbuf, m.kv, l,
-                       (const DevState *)nullptr, len, ws.am, ws.al, ws.aacc);
+    const LayerDev &L = m.layers[l];
+    // a decode step's attention: appends at the free slot `slot` (beyond the
+    // cached length, so cached positions are untouched) and attends slot+1
+    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
+                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, (const DevState *)nullptr, pos, slot, l, m.kv,
+                       ws.am, ws.al, ws.aacc);
     return hipGetLastError();
 }
 

@@ -119,24 +119,32 @@ static int env_tile(const char *name, int dflt)
     return (x >= 0 && x < TILE_COUNT) ? x : dflt;
 }
 
-// Split-K tiling for weights whose partial sums a consumer reduces;
-// single-slice ("direct") tiling for the residual projections.
-static int choose_cfg(int64_t k, int64_t G, bool direct)
+// Default tile of each weight role (QTTS_TILE_<ROLE> overrides it).  Each
+// choice gives roughly 100-250 workgroups at the 1.7B shapes while keeping
+// the number of k-slices (partial sums the next stage reduces) at 1-4.
+static int default_cfg(const char *role, int64_t k)
 {
-    if (direct) {
-        if (k <= 2048) return TILE_D256;
-        if (k <= 3072) return TILE_D384;
-        if (k <= 6144) return TILE_D768;
-    }
-    const int64_t items = ((k + 255) / 256) * ((G + 7) / 8);
-    return items >= 128 ? TILE_S256 : TILE_S128;
+    const std::string r(role);
+    if (r == "TQKV" || r == "TO" || r == "HEAD" || r == "PDOWN") return TILE_G1_T128;   // KC 1024
+    if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;                    // one slice, SiLU epilogue
+    if (r == "PGU") return k <= 1024 ? TILE_G2_T256 : TILE_G2_T512;
+    if (r == "TDOWN") return TILE_G1_T256;                                              // KC 2048
+    if (r == "PQKV") return TILE_G1_T128;
+    if (r == "PO" || r == "PHEAD" || r == "PPROJ") return TILE_G1_T64;                 // KC 512
+    return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                                     // text fc, GEMV
 }
+
+static int role_cfg(const char *role, int64_t k) { return env_tile(role, default_cfg(role, k)); }
 
 static void parallel_for(int64_t n, const std::function<void(int64_t, int64_t)> &fn);
 
+// interleave = true (two sources of equal width): groups alternate a0 b0 a1
+// b1 ..., so a tile of an even number of groups holds matching pairs.
 static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vector<SrcW> &srcs, int cfg,
-                       Q4Tiled *out, void **mem_out)
+                       Q4Tiled *out, void **mem_out, bool interleave = false)
 {
+    if (interleave && (srcs.size() != 2 || srcs[0].n != srcs[1].n))
+        return fail(c, QTTS_ERR_INVALID, "interleaved weights must be two of equal width");
     if (srcs.empty()) return fail(c, QTTS_ERR_INVALID, "empty weight list");
     const int64_t k = srcs[0].k;
     std::vector<int64_t> g0;   // first group of each source
@@ -168,8 +176,13 @@ static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vect
                 int si = -1;
                 int64_t lg = 0;
                 if (g < Gt) {
-                    si = (int)(std::upper_bound(g0.begin(), g0.end(), g) - g0.begin()) - 1;
-                    lg = g - g0[si];
+                    if (interleave) {
+                        si = (int)(g & 1);
+                        lg = g >> 1;
+                    } else {
+                        si = (int)(std::upper_bound(g0.begin(), g0.end(), g) - g0.begin()) - 1;
+                        lg = g - g0[si];
+                    }
                 }
                 for (int r = 0; r < ts.R; r++) {
                     const int64_t row = s * KC + (int64_t)r * P + t / ts.GB;
@@ -205,6 +218,7 @@ static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vect
     d.cfg = cfg;
     d.tile_bytes = (int32_t)tile_bytes;
     d.npad = (int32_t)(G * 32);
+    d.interleave = interleave ? 1 : 0;
     *out = d;
     if (mem_out) *mem_out = mem;
     return QTTS_OK;
@@ -268,20 +282,16 @@ static int upload_layer(qtts_ctx *c, const qtts_layer_host &L, int hidden, int h
     auto &A = c->model_allocs;
     const char *pfx = predictor ? "P" : "T";
     char name[32];
-    const int64_t Gqkv = (L.q_proj.n + L.k_proj.n + L.v_proj.n) / 32;
     snprintf(name, sizeof name, "%sQKV", pfx);
-    RCHK(build_tiled(c, A, {src_of(L.q_proj), src_of(L.k_proj), src_of(L.v_proj)},
-                     env_tile(name, choose_cfg(L.q_proj.k, Gqkv, false)), &out->qkv, nullptr));
+    RCHK(build_tiled(c, A, {src_of(L.q_proj), src_of(L.k_proj), src_of(L.v_proj)}, role_cfg(name, L.q_proj.k),
+                     &out->qkv, nullptr));
     snprintf(name, sizeof name, "%sO", pfx);
-    RCHK(build_tiled(c, A, {src_of(L.o_proj)}, env_tile(name, choose_cfg(L.o_proj.k, L.o_proj.n / 32, true)),
-                     &out->o, nullptr));
-    const int64_t Ggu = (L.gate_proj.n + L.up_proj.n) / 32;
+    RCHK(build_tiled(c, A, {src_of(L.o_proj)}, role_cfg(name, L.o_proj.k), &out->o, nullptr));
     snprintf(name, sizeof name, "%sGU", pfx);
-    RCHK(build_tiled(c, A, {src_of(L.gate_proj), src_of(L.up_proj)},
-                     env_tile(name, choose_cfg(L.gate_proj.k, Ggu, false)), &out->gate_up, nullptr));
+    RCHK(build_tiled(c, A, {src_of(L.gate_proj), src_of(L.up_proj)}, role_cfg(name, L.gate_proj.k),
+                     &out->gate_up, nullptr, true));
     snprintf(name, sizeof name, "%sDOWN", pfx);
-    RCHK(build_tiled(c, A, {src_of(L.down_proj)},
-                     env_tile(name, choose_cfg(L.down_proj.k, L.down_proj.n / 32, true)), &out->down, nullptr));
+    RCHK(build_tiled(c, A, {src_of(L.down_proj)}, role_cfg(name, L.down_proj.k), &out->down, nullptr));
     RCHK(upload_vec(c, A, L.q_norm, head_dim, &out->q_norm));
     RCHK(upload_vec(c, A, L.k_norm, head_dim, &out->k_norm));
     RCHK(upload_vec(c, A, L.input_norm, hidden, &out->input_norm));
@@ -429,7 +439,8 @@ extern "C" int qtts_q4_upload(qtts_ctx *c, const qtts_q4_host *w, qtts_w **out)
     hipSetDevice(c->device);
     qtts_w *h = new qtts_w();
     const int64_t G = w->n / 32;
-    int r = build_tiled(c, h->allocs, {src_of(*w)}, env_tile("GEMV", choose_cfg(w->k, G, false)), &h->t, nullptr);
+    (void)G;
+    int r = build_tiled(c, h->allocs, {src_of(*w)}, role_cfg("GEMV", w->k), &h->t, nullptr);
     if (r == QTTS_OK) r = upload_rows(c, h->allocs, {*w}, &h->rows);
     if (r == QTTS_OK) r = dev_alloc(c, h->allocs, &h->x, (size_t)w->k * 2);
     if (r == QTTS_OK) r = dev_alloc(c, h->allocs, &h->y, (size_t)std::max<int64_t>(w->n, h->t.npad) * 2);
@@ -456,9 +467,11 @@ extern "C" int qtts_gemv_q4(qtts_ctx *c, const qtts_w *w, const float *x, float 
 {
     if (!c || !w || !x || !y) return QTTS_ERR_INVALID;
     RCHK(stage_in(c, x, w->t.k, w->x, flags));
-    // columns past the last full group come out zero: their padded groups
-    // carry zero scales (gemv.rs:255 starts from vec![0.0; n])
     HIPCHK(c, enqueue_gemv_store(w->t, w->x, w->y, nullptr, w->part, c->stream));
+    // columns past the last full group stay zero (gemv.rs:255 starts from
+    // vec![0.0; n] and only full groups are accumulated)
+    const int64_t full = (int64_t)(w->t.n / 32) * 32;
+    if (full < w->t.n) HIPCHK(c, hipMemsetAsync(w->y + full, 0, (w->t.n - full) * sizeof(float), c->stream));
     RCHK(stage_out(c, w->y, w->t.n, y, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
@@ -501,29 +514,36 @@ static int alloc_workspace(qtts_ctx *c)
     const TalkerDev &m = c->tm;
     const PredictorDev &p = c->pm;
     const int H = m.hidden, h = p.hidden;
-    // largest split-K partial buffer: S * NB * npad
-    size_t pa = 0, pb = 0, ph = 0;
+    // split-K partial buffers: S * NB * npad per producer role
+    size_t pq = 0, po = 0, pg = 0, pd = 0, ph = 0, pp = 0;
     auto upd = [](size_t &v, const Q4Tiled &t, int nb) { v = std::max(v, (size_t)t.S * nb * t.npad); };
-    for (const LayerDev &L : c->tlayers) { upd(pa, L.qkv, 1); upd(pa, L.gate_up, 1); upd(pb, L.o, 1); upd(pb, L.down, 1); }
-    for (const LayerDev &L : c->players) { upd(pa, L.qkv, 2); upd(pa, L.gate_up, 2); upd(pb, L.o, 2); upd(pb, L.down, 2); }
-    upd(pb, p.proj, 2);
+    for (const LayerDev &L : c->tlayers) { upd(pq, L.qkv, 1); upd(po, L.o, 1); upd(pg, L.gate_up, 1); upd(pd, L.down, 1); }
+    for (const LayerDev &L : c->players) { upd(pq, L.qkv, 2); upd(po, L.o, 2); upd(pg, L.gate_up, 2); upd(pd, L.down, 2); }
     upd(ph, m.codec_head, 1);
     for (const Q4Tiled &t : c->pheads) upd(ph, t, 1);
-    upd(pb, m.text_fc1, 1);
-    upd(pb, m.text_fc2, 1);
+    upd(pp, p.proj, 2);
+    upd(pp, m.text_fc1, 1);
+    upd(pp, m.text_fc2, 1);
     RCHK(dev_alloc(c, A, &w.x, 2 * (size_t)std::max(H, m.text_hidden)));
-    RCHK(dev_alloc(c, A, &w.px, 2 * (size_t)h));
+    RCHK(dev_alloc(c, A, &w.xa, H));
+    RCHK(dev_alloc(c, A, &w.xb, H));
+    RCHK(dev_alloc(c, A, &w.pxa, 2 * (size_t)h));
+    RCHK(dev_alloc(c, A, &w.pxb, 2 * (size_t)h));
     RCHK(dev_alloc(c, A, &w.pin, 2 * (size_t)H));
-    RCHK(dev_alloc(c, A, &w.qbuf, 16 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.am, MAX_CHUNKS * 16));
     RCHK(dev_alloc(c, A, &w.al, MAX_CHUNKS * 16));
     RCHK(dev_alloc(c, A, &w.aacc, (size_t)MAX_CHUNKS * 16 * HEAD_DIM));
+    RCHK(dev_alloc(c, A, &w.attn, 16 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.pattn, 2 * 16 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.pk, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.pv, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
-    RCHK(dev_alloc(c, A, &w.part_a, pa));
-    RCHK(dev_alloc(c, A, &w.part_b, pb));
+    RCHK(dev_alloc(c, A, &w.h, 2 * (size_t)std::max(m.inter, p.inter)));
+    RCHK(dev_alloc(c, A, &w.part_qkv, pq));
+    RCHK(dev_alloc(c, A, &w.part_o, po));
+    RCHK(dev_alloc(c, A, &w.part_gu, pg));
+    RCHK(dev_alloc(c, A, &w.part_down, pd));
     RCHK(dev_alloc(c, A, &w.part_head, ph));
+    RCHK(dev_alloc(c, A, &w.part_proj, pp));
     RCHK(dev_alloc(c, A, &w.hid_work, H));
     RCHK(dev_alloc(c, A, &w.hidden, H));
     RCHK(dev_alloc(c, A, &w.logits, std::max(m.vocab, 4096)));
@@ -551,6 +571,8 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     if (p->n_groups < 1 || p->n_groups > 15 || !p->lm_heads || !p->codec_embeddings)
         return fail(c, QTTS_ERR_INVALID, "predictor needs 1..15 heads and embeddings");
     if (t->vocab > 4096 || t->vocab <= 0) return fail(c, QTTS_ERR_UNSUPPORTED, "talker vocab must be <= 4096");
+    if (t->hidden > 2048 || p->hidden > 2048 || t->hidden % 32 || p->hidden % 32)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "hidden sizes must be multiples of 32 and <= 2048");
     if (t->rope_max_pos < 1 || !t->rope_cos || !t->rope_sin || p->rope_max_pos < PRED_KV_CAP)
         return fail(c, QTTS_ERR_INVALID, "rope tables missing");
 
@@ -560,10 +582,9 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     c->tlayers.assign(t->n_layers, LayerDev{});
     for (int l = 0; l < t->n_layers; l++) RCHK(upload_layer(c, t->layers[l], t->hidden, t->head_dim, &c->tlayers[l], false));
     m.layers = c->tlayers.data();
-    RCHK(build_tiled(c, A, {src_of(t->codec_head)}, env_tile("HEAD", choose_cfg(t->hidden, t->codec_head.n / 32, false)),
-                     &m.codec_head, nullptr));
-    RCHK(build_tiled(c, A, {src_of(t->text_fc1)}, choose_cfg(t->text_fc1.k, t->text_fc1.n / 32, false), &m.text_fc1, nullptr));
-    RCHK(build_tiled(c, A, {src_of(t->text_fc2)}, choose_cfg(t->text_fc2.k, t->text_fc2.n / 32, false), &m.text_fc2, nullptr));
+    RCHK(build_tiled(c, A, {src_of(t->codec_head)}, role_cfg("HEAD", t->hidden), &m.codec_head, nullptr));
+    RCHK(build_tiled(c, A, {src_of(t->text_fc1)}, role_cfg("TEXT", t->text_fc1.k), &m.text_fc1, nullptr));
+    RCHK(build_tiled(c, A, {src_of(t->text_fc2)}, role_cfg("TEXT", t->text_fc2.k), &m.text_fc2, nullptr));
     RCHK(upload_vec(c, A, t->text_fc1_bias, t->text_fc1.n, &m.text_fc1_bias));
     RCHK(upload_vec(c, A, t->text_fc2_bias, t->text_fc2.n, &m.text_fc2_bias));
     RCHK(upload_rows(c, A, {t->codec_embedding}, &m.codec_rows));
@@ -590,15 +611,13 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     c->players.assign(p->n_layers, LayerDev{});
     for (int l = 0; l < p->n_layers; l++) RCHK(upload_layer(c, p->layers[l], p->hidden, p->head_dim, &c->players[l], true));
     q.layers = c->players.data();
-    RCHK(build_tiled(c, A, {src_of(p->input_proj)}, env_tile("PPROJ", choose_cfg(p->input_proj.k, p->input_proj.n / 32, false)),
-                     &q.proj, nullptr));
+    RCHK(build_tiled(c, A, {src_of(p->input_proj)}, role_cfg("PPROJ", p->input_proj.k), &q.proj, nullptr));
     if (q.proj.n != q.hidden || p->input_proj.k != t->hidden)
         return fail(c, QTTS_ERR_INVALID, "predictor input projection shape");
     RCHK(upload_vec(c, A, p->input_proj_bias, p->input_proj.n, &q.proj_bias));
     c->pheads.assign(p->n_groups, Q4Tiled{});
     for (int g = 0; g < p->n_groups; g++) {
-        RCHK(build_tiled(c, A, {src_of(p->lm_heads[g])},
-                         env_tile("PHEAD", choose_cfg(p->lm_heads[g].k, p->lm_heads[g].n / 32, false)), &c->pheads[g], nullptr));
+        RCHK(build_tiled(c, A, {src_of(p->lm_heads[g])}, role_cfg("PHEAD", p->lm_heads[g].k), &c->pheads[g], nullptr));
         if (c->pheads[g].n != p->vocab) return fail(c, QTTS_ERR_INVALID, "lm_head %d width != vocab", g);
     }
     q.heads = c->pheads.data();
@@ -734,9 +753,9 @@ extern "C" int qtts_embed_text_token(qtts_ctx *c, uint32_t token, float *out, in
     Q4Rows e = m.text_rows;
     e.n = m.text_hidden;
     HIPCHK(c, enqueue_embed_row(e, nullptr, token, raw, c->stream));
-    HIPCHK(c, enqueue_gemv_store(m.text_fc1, raw, h1, m.text_fc1_bias, c->ws.part_b, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc1, raw, h1, m.text_fc1_bias, c->ws.part_proj, c->stream));
     HIPCHK(c, enqueue_silu(h1, m.text_fc1.n, c->stream));
-    HIPCHK(c, enqueue_gemv_store(m.text_fc2, h1, o, m.text_fc2_bias, c->ws.part_b, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc2, h1, o, m.text_fc2_bias, c->ws.part_proj, c->stream));
     RCHK(stage_out(c, o, m.text_fc2.n, out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
@@ -967,9 +986,18 @@ extern "C" int qtts_gen_set_text(qtts_ctx *c, const float *text, int64_t n_text,
 }
 
 // Run frames in batches of up to RING_FRAMES graph launches per host sync.
+// QTTS_NO_GRAPH=1 enqueues each frame's kernels directly instead of
+// replaying the captured graph (same kernels; used under profilers).
+static bool use_graph()
+{
+    const char *v = getenv("QTTS_NO_GRAPH");
+    return !(v && *v && *v != '0');
+}
+
 static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done, int32_t *eos, bool forced)
 {
-    RCHK(build_frame_graph(c));
+    const bool graph = use_graph();
+    if (graph) RCHK(build_frame_graph(c));
     int64_t emitted = 0;
     *eos = 0;
     while (emitted < n) {
@@ -981,7 +1009,10 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
         c->h_st->ring_base = c->h_st->frame_idx;
         HIPCHK(c, hipMemcpyAsync(&c->st_gen->ring_base, &c->h_st->ring_base, sizeof(int32_t), hipMemcpyHostToDevice,
                                  c->stream));
-        for (int64_t f = 0; f < batch; f++) HIPCHK(c, hipGraphLaunch(c->frame_exec, c->stream));
+        for (int64_t f = 0; f < batch; f++) {
+            if (graph) HIPCHK(c, hipGraphLaunch(c->frame_exec, c->stream));
+            else HIPCHK(c, enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, c->stream));
+        }
         HIPCHK(c, hipMemcpyAsync(c->h_ring, c->ws.ring_pred, sizeof(uint32_t) * batch * 16, hipMemcpyDeviceToHost,
                                  c->stream));
         const int32_t base = c->h_st->ring_base;
@@ -1105,9 +1136,14 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
                              avg_us);
     }
     if (kind == 1) {
-        const int len = std::max(1, c->h_st->kv_len);
-        *bytes = (double)len * 8 * HEAD_DIM * 4 * 2 + 16.0 * HEAD_DIM * 4 * 2;
-        return time_launches(c, iters, [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, len, c->stream); },
+        // one decode step's attention at the current length: appends at the
+        // free slot kv_len (cached positions untouched), attends kv_len + 1
+        const int slot = c->h_st->kv_len;
+        if (slot + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "no free KV slot to time attention");
+        const int64_t pos = std::min<int64_t>(c->h_st->position, m.rope_rows - 1);
+        *bytes = (double)(slot + 1) * 8 * HEAD_DIM * 4 * 2 + 16.0 * HEAD_DIM * 4 * 3;
+        return time_launches(c, iters,
+                             [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->stream); },
                              avg_us);
     }
     return QTTS_ERR_INVALID;
