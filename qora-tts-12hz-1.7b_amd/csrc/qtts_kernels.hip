@@ -128,38 +128,45 @@ __device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int
 // unrolled so each thread's loads are in flight together.
 // ---------------------------------------------------------------------------
 
-constexpr int MAX_RES = 2048;   // widest residual a prologue normalises
-
 template <int NB>
 struct ProPlain {
     const float *x;
     int ld, k;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    template <int T>
+    __device__ void load(float *xs, int k0, int KC, int ctile) const
     {
+        // KC, k0, ld and k are multiples of 4: float4 loads, all in flight
         constexpr int U = 8;
-        for (int i0 = threadIdx.x; i0 < NB * KC; i0 += U * blockDim.x) {
-            float v[U];
+        const int n4 = NB * KC / 4;
+        const int kc4 = KC / 4;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += U * blockDim.x) {
+            float4 v[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = i0 + u * blockDim.x;
-                const int b = i / KC, r = k0 + (i - b * KC);
-                v[u] = (i < NB * KC && r < k) ? x[(size_t)b * ld + r] : 0.0f;
+                const int b = i / kc4, r = k0 + 4 * (i - b * kc4);
+                v[u] = (i < n4 && r < k) ? *(const float4 *)(x + (size_t)b * ld + r) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int i = i0 + u * blockDim.x;
-                if (i < NB * KC) xs[i] = v[u];
+                if (i < n4) *(float4 *)(xs + 4 * i) = v[u];
             }
         }
     }
+    __device__ void finish(int s, int c, int nct) const {}
 };
 
 // Residual update + RMSNorm (gemv.rs:445-454):
 //   x = base + sum_s parts[s]   (+ bias)        -- the producer's k-slices in order
 //   xs = x * (1/sqrt(mean(x^2) + 1e-6)) * gamma  -- this tile's rows
-// Workgroup 0 stores x (the residual stream) to x_out and the normed vector
-// to side.  Consumer row b reads producer row prow + b of NBP rows.
-template <int NB>
+// Every workgroup rebuilds x in LDS (float4 loads, all in flight); after the
+// tile's GEMV, the slice-0 workgroups store x (the residual stream) to x_out
+// and the normed vector to side, each a share of the columns.  Consumer row b
+// reads producer row prow + b of NBP rows.  Needs k % 4 == 0 and k <= KMAX.
+constexpr int RES_MAX_S = 4;   // slices summed per batch of loads
+
+template <int NB, int KMAX>
 struct ProResidRms {
     const float *base;
     int ldb;
@@ -170,70 +177,108 @@ struct ProResidRms {
     int k;
     float *x_out;
     float *side;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    __device__ static float *xf_lds()
     {
-        __shared__ float xf[NB][MAX_RES];
+        __shared__ float xf[NB * KMAX];
+        return xf;
+    }
+    __device__ static float *inv_lds()
+    {
+        __shared__ float inv[NB];
+        return inv;
+    }
+    template <int T>
+    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    {
         __shared__ float scratch[16];
-        constexpr int U = 8;
-        const int T = blockDim.x;
-        const bool w0 = blockIdx.x == 0;
-        float gv[8];
+        constexpr int U = (KMAX / 4 + T - 1) / T;   // float4 per thread
+        constexpr int KCT = 8 * T;                   // KC <= 8T for every tile shape
+        float *xf = xf_lds();
+        const int k4 = k >> 2;
+        float gv[(KCT + T - 1) / T];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < KCT / T; u++) {
             const int r = threadIdx.x + u * T;
             gv[u] = (r < KC && k0 + r < k) ? h2f(gamma[k0 + r]) : 0.0f;
         }
-        float inv[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            float ss = 0.0f;
-            for (int j0 = threadIdx.x; j0 < k; j0 += U * T) {
-                float ps[U], v[U];
+            float4 ps[U];
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int j = j0 + u * T;
-                    ps[u] = 0.0f;
-                    v[u] = (base && j < k) ? base[(size_t)b * ldb + j] : 0.0f;
-                }
-                if (parts) {
-#pragma unroll 4
-                    for (int s = 0; s < S; s++) {
-                        const float *p = parts + ((size_t)s * NBP + prow + b) * npad;
+            for (int u = 0; u < U; u++) {
+                const int i = threadIdx.x + u * T;
+                ps[u] = (base && i < k4) ? *(const float4 *)(base + (size_t)b * ldb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if (parts) {
+                float4 acc[U];
+                for (int s0 = 0; s0 < S; s0 += RES_MAX_S) {
+                    float4 pv[RES_MAX_S][U];
+#pragma unroll
+                    for (int s = 0; s < RES_MAX_S; s++)
 #pragma unroll
                         for (int u = 0; u < U; u++) {
-                            const int j = j0 + u * T;
-                            if (j < k) ps[u] += p[j];
+                            const int i = threadIdx.x + u * T;
+                            pv[s][u] = (s0 + s < S && i < k4)
+                                           ? *(const float4 *)(parts + ((size_t)(s0 + s) * NBP + prow + b) * npad + 4 * i)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
                         }
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+                        float4 a = s0 == 0 ? pv[0][u] : acc[u];
+                        if (s0 != 0) { a.x += pv[0][u].x; a.y += pv[0][u].y; a.z += pv[0][u].z; a.w += pv[0][u].w; }
+#pragma unroll
+                        for (int s = 1; s < RES_MAX_S; s++)
+                            if (s0 + s < S) { a.x += pv[s][u].x; a.y += pv[s][u].y; a.z += pv[s][u].z; a.w += pv[s][u].w; }
+                        acc[u] = a;
                     }
                 }
 #pragma unroll
                 for (int u = 0; u < U; u++) {
-                    const int j = j0 + u * T;
-                    if (j < k) {
-                        float x = parts ? v[u] + ps[u] : v[u];
-                        if (bias) x += bias[j];
-                        xf[b][j] = x;
-                        ss += x * x;
+                    if (base) { ps[u].x += acc[u].x; ps[u].y += acc[u].y; ps[u].z += acc[u].z; ps[u].w += acc[u].w; }
+                    else ps[u] = acc[u];
+                }
+            }
+            float ss = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int i = threadIdx.x + u * T;
+                if (i < k4) {
+                    float4 x = ps[u];
+                    if (bias) {
+                        const float4 bb = *(const float4 *)(bias + 4 * i);
+                        x.x += bb.x; x.y += bb.y; x.z += bb.z; x.w += bb.w;
                     }
+                    *(float4 *)(xf + b * KMAX + 4 * i) = x;
+                    ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
                 }
             }
             ss = block_sum(ss, scratch);
-            inv[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
+            if (threadIdx.x == 0) inv_lds()[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
         }
-        if (w0 && (x_out || side)) {
-            for (int b = 0; b < NB; b++)
-                for (int j = threadIdx.x; j < k; j += T) {
-                    const float x = xf[b][j];
-                    if (x_out) x_out[(size_t)b * k + j] = x;
-                    if (side) side[(size_t)b * k + j] = x * inv[b] * h2f(gamma[j]);
-                }
-        }
+        __syncthreads();
 #pragma unroll
         for (int b = 0; b < NB; b++) {
+            const float iv = inv_lds()[b];
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < KCT / T; u++) {
                 const int r = threadIdx.x + u * T;
-                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b][k0 + r] * inv[b] * gv[u] : 0.0f;
+                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * gv[u] : 0.0f;
+            }
+        }
+    }
+    // after the tile: slice-0 workgroups store their share of x / normed x
+    __device__ void finish(int s, int c, int nct) const
+    {
+        if (s != 0 || (!x_out && !side)) return;
+        const float *xf = xf_lds();
+        const int per = (k + nct - 1) / nct;
+        const int j0 = c * per, j1 = min(j0 + per, k);
+        for (int b = 0; b < NB; b++) {
+            const float iv = inv_lds()[b];
+            for (int j = j0 + threadIdx.x; j < j1; j += blockDim.x) {
+                const float x = xf[b * KMAX + j];
+                if (x_out) x_out[(size_t)b * k + j] = x;
+                if (side) side[(size_t)b * k + j] = x * iv * h2f(gamma[j]);
             }
         }
     }
@@ -246,7 +291,8 @@ template <int NB>
 struct ProSwiglu {
     const float *part;
     int S, npad, inter;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    template <int T>
+    __device__ void load(float *xs, int k0, int KC, int ctile) const
     {
         for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
             const int b = i / KC, r = k0 + (i - b * KC);
@@ -265,6 +311,7 @@ struct ProSwiglu {
             xs[i] = v;
         }
     }
+    __device__ void finish(int s, int c, int nct) const {}
 };
 
 // One dequantised embedding row (embed_lookup_q4, gemv.rs:415-437); the row
@@ -272,7 +319,8 @@ struct ProSwiglu {
 struct ProEmbed {
     Q4Rows emb;
     const uint32_t *code;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    template <int T>
+    __device__ void load(float *xs, int k0, int KC, int ctile) const
     {
         const uint32_t row = *code;
         for (int i = threadIdx.x; i < KC; i += blockDim.x) {
@@ -280,6 +328,7 @@ struct ProEmbed {
             xs[i] = r < emb.n ? q4_row_value(emb, row, r) : 0.0f;
         }
     }
+    __device__ void finish(int s, int c, int nct) const {}
 };
 
 // Predictor prefill input: row 0 = talker hidden, row 1 = codec embedding
@@ -289,7 +338,8 @@ struct ProHidEmbed {
     Q4Rows emb;
     const uint32_t *code;
     int k;
-    __device__ void operator()(float *xs, int k0, int KC, int ctile) const
+    template <int T>
+    __device__ void load(float *xs, int k0, int KC, int ctile) const
     {
         const uint32_t row = *code;
         for (int i = threadIdx.x; i < KC; i += blockDim.x) {
@@ -298,6 +348,7 @@ struct ProHidEmbed {
             xs[KC + i] = r < k ? q4_row_value(emb, row, r) : 0.0f;
         }
     }
+    __device__ void finish(int s, int c, int nct) const {}
 };
 
 // ---------------------------------------------------------------------------
@@ -413,7 +464,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
         const u32x4 sc = __builtin_nontemporal_load((const u32x4 *)(tile + (size_t)R * T * 16 + (size_t)t * 16));
 
         __syncthreads();               // xs / red / ybuf of the previous item are free
-        pro(xs, s * KC, KC, c);
+        pro.template load<T>(xs, s * KC, KC, c);
         __syncthreads();
 
         float acc[NB][32];
@@ -481,6 +532,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             const int b = col / C, cc = col - b * C;
             epi(s, b, c, cc, C, ybuf + b * C);
         }
+        pro.finish(s, c, w.CT);
     }
 }
 
@@ -627,6 +679,28 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         __syncthreads();
         const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
         const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
+        // all K and V loads of this thread in flight together
+        float kk[4][8];
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int tok = wv * 16 + it * 4 + (lane >> 4);
+            if (tok < ntok) {
+                const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
+                const float4 ka = kr[0], kb = kr[1];
+                kk[it][0] = ka.x; kk[it][1] = ka.y; kk[it][2] = ka.z; kk[it][3] = ka.w;
+                kk[it][4] = kb.x; kk[it][5] = kb.y; kk[it][6] = kb.z; kk[it][7] = kb.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) kk[it][i] = 0.0f;
+            }
+        }
+        const int dv = t & 127, half = t >> 7;
+        float vv[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const int tok = half * 32 + i;
+            vv[i] = tok < ntok ? Vp[(size_t)tok * HEAD_DIM + dv] : 0.0f;
+        }
         float q0[8], q1[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -637,15 +711,10 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         for (int it = 0; it < 4; it++) {
             const int tok = wv * 16 + it * 4 + (lane >> 4);
             float d0 = 0.0f, d1 = 0.0f;
-            if (tok < ntok) {
-                const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
-                const float4 ka = kr[0], kb = kr[1];
-                const float kk[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    d0 = fmaf(q0[i], kk[i], d0);
-                    d1 = fmaf(q1[i], kk[i], d1);
-                }
+            for (int i = 0; i < 8; i++) {
+                d0 = fmaf(q0[i], kk[it][i], d0);
+                d1 = fmaf(q1[i], kk[it][i], d1);
             }
 #pragma unroll
             for (int m = 8; m >= 1; m >>= 1) {
@@ -672,16 +741,15 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         }
         __syncthreads();
         {
-            const int d = t & 127, half = t >> 7;
             float a0 = 0.0f, a1 = 0.0f;
-            const int t0 = half * 32, t1 = min(t0 + 32, ntok);
-            for (int tok = t0; tok < t1; tok++) {
-                const float v = Vp[(size_t)tok * HEAD_DIM + d];
-                a0 = fmaf(sc[0][tok], v, a0);
-                a1 = fmaf(sc[1][tok], v, a1);
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+                const int tok = half * 32 + i;       // p = 0 past ntok
+                a0 = fmaf(sc[0][tok], vv[i], a0);
+                a1 = fmaf(sc[1][tok], vv[i], a1);
             }
-            pv[half][0][d] = a0;
-            pv[half][1][d] = a1;
+            pv[half][0][dv] = a0;
+            pv[half][1][dv] = a1;
         }
         __syncthreads();
         {
@@ -962,15 +1030,15 @@ __device__ void topk_select(float *p, int n, int top_k, int *hist, int *iscratch
             if ((b & mask) == prefix) atomicAdd(&hist[(b >> shift) & 0xFF], 1);
         }
         __syncthreads();
-        if (t == 0) {
-            int need = need_s, bin = 255;
-            for (; bin > 0; bin--) {
-                if (hist[bin] >= need) break;
-                need -= hist[bin];
-            }
-            prefix_s = prefix | ((uint32_t)bin << shift);
+        // bins in descending order: thread t < 256 owns bin 255 - t; the bin
+        // holding the need-th largest is where the running count crosses need
+        const int need = need_s;
+        const int hv = t < 256 ? hist[255 - t] : 0;
+        const int above = block_excl_scan(hv, iscratch, nullptr);
+        if (t < 256 && above < need && above + hv >= need) {
+            prefix_s = prefix | ((uint32_t)(255 - t) << shift);
             mask_s = mask | (0xFFu << shift);
-            need_s = need;
+            need_s = need - above;
         }
         __syncthreads();
     }
@@ -1277,7 +1345,7 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
     const LayerDev *P = l > 0 ? &m.layers[l - 1] : nullptr;
     const int H = m.hidden;
     // 1. residual + RMSNorm + fused q|k|v GEMV -> partials
-    const ProResidRms<1> pre_attn{l == 0 ? x_in : ws.xa, H, P ? ws.part_down : nullptr, P ? P->down.S : 0, 1, 0,
+    const ProResidRms<1, 2048> pre_attn{l == 0 ? x_in : ws.xa, H, P ? ws.part_down : nullptr, P ? P->down.S : 0, 1, 0,
                                   P ? P->down.npad : 0, nullptr, L.input_norm, H, ws.xb, nullptr};
     QCHK(launch_gemv<1>(L.qkv, pre_attn, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
     // 2. QK-norm, RoPE, KV append, split-K attention over the pages
@@ -1292,7 +1360,7 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
     // 4. o_proj -> partials
     QCHK(launch_gemv<1>(L.o, ProPlain<1>{ws.attn, 16 * HEAD_DIM, 16 * HEAD_DIM}, EpiPart<1>{ws.part_o, L.o.npad}, s));
     // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
-    const ProResidRms<1> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
+    const ProResidRms<1, 2048> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
     return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);
 }
 
@@ -1301,7 +1369,7 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
 static hipError_t talker_head(const TalkerDev &m, const Workspace &ws, float *side, hipStream_t s)
 {
     const LayerDev &P = m.layers[m.n_layers - 1];
-    const ProResidRms<1> pre{ws.xa, m.hidden, ws.part_down, P.down.S, 1, 0, P.down.npad, nullptr, m.final_norm,
+    const ProResidRms<1, 2048> pre{ws.xa, m.hidden, ws.part_down, P.down.S, 1, 0, P.down.npad, nullptr, m.final_norm,
                              m.hidden, nullptr, side};
     return launch_gemv<1>(m.codec_head, pre, EpiPart<1>{ws.part_head, m.codec_head.npad}, s);
 }
@@ -1349,10 +1417,10 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
 {
     const LayerDev &L = p.layers[l];
     const int h = p.hidden;
-    const ProResidRms<NB> pre_attn =
-        l == 0 ? ProResidRms<NB>{nullptr, h, ws.part_proj, p.proj.S, NB, 0, p.proj.npad, p.proj_bias, L.input_norm,
+    const ProResidRms<NB, 1024> pre_attn =
+        l == 0 ? ProResidRms<NB, 1024>{nullptr, h, ws.part_proj, p.proj.S, NB, 0, p.proj.npad, p.proj_bias, L.input_norm,
                                  h, ws.pxb, nullptr}
-               : ProResidRms<NB>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
+               : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
                                  p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
     QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
     hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, NB, L.qkv.npad,
@@ -1362,7 +1430,7 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
     QCHK(hipGetLastError());
     const int qd = p.n_heads * HEAD_DIM;
     QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiPart<NB>{ws.part_o, L.o.npad}, s));
-    const ProResidRms<NB> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
+    const ProResidRms<NB, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
     return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s);
 }
 
@@ -1371,7 +1439,7 @@ static hipError_t pred_head(const PredictorDev &p, const Workspace &ws, DevState
                             const uint32_t *forced, uint32_t *codes_api, hipStream_t s)
 {
     const LayerDev &P = p.layers[p.n_layers - 1];
-    const ProResidRms<1> pre{ws.pxa + (size_t)row * p.hidden, p.hidden, ws.part_down, P.down.S, NBP, row,
+    const ProResidRms<1, 1024> pre{ws.pxa + (size_t)row * p.hidden, p.hidden, ws.part_down, P.down.S, NBP, row,
                              P.down.npad, nullptr, p.final_norm, p.hidden, nullptr, nullptr};
     QCHK(launch_gemv<1>(p.heads[g], pre, EpiPart<1>{ws.part_head, p.heads[g].npad}, s));
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[g].S, p.heads[g].npad, p.vocab,
@@ -1457,7 +1525,7 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
-    const ProResidRms<1> pre{ws.xb, m.hidden, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, m.hidden,
+    const ProResidRms<1, 2048> pre{ws.xb, m.hidden, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, m.hidden,
                              nullptr, nullptr};
     if (L.gate_up.S == 1 && tile_shape(L.gate_up.cfg).GB % 2 == 0)
         return launch_gemv<1>(L.gate_up, pre, EpiSwiglu<1>{ws.h, m.inter}, s);
