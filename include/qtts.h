@@ -262,8 +262,9 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
 
 /* ---- measurement ------------------------------------------------------ */
 
-/* Average device time (us) of one kernel launch, from HIP events recorded
- * around each of `iters` launches on the context stream; *bytes gets the
+/* Average device time (us) of one kernel launch: one HIP event pair around
+ * `iters` back-to-back launches on the context stream (after one warm-up
+ * launch), divided by `iters`; *bytes gets the
  * algorithmic bytes one launch moves.  No reference counterpart (the
  * reference times phases with Instant, generate_new.rs:600-678).
  *   kind 0: talker gate|up GEMV (RMSNorm prologue), cycling the layers;

@@ -9,39 +9,41 @@ namespace qtts {
 // Tiling of one Q4 weight for the split-K GEMV (see qtts_kernels.hip).
 // A tile covers GB 32-column groups x KC rows, KC = R * T / GB, and is
 // stored contiguously: nibble block [R][T] x 16 B, then scale block [T] x
-// R f16.  Thread t of a workgroup owns group (t % GB) and rows
+// R f16 (R = 2, 4 or 8 rows per thread).  Thread t of a workgroup owns group (t % GB) and rows
 // r * (T/GB) + t / GB, r = 0..R-1, of the tile.  A weight with
 // S = ceil(k / KC) k-slices writes S partial sums per output; S = 1 is a
 // full-k pass.
 enum TileCfg : int32_t {
-    TILE_G8_T256 = 0,   // KC = 256
-    TILE_G8_T128 = 1,   // KC = 128
-    TILE_G1_T64 = 2,    // KC = 512
-    TILE_G1_T128 = 3,   // KC = 1024
-    TILE_G1_T256 = 4,   // KC = 2048
-    TILE_G1_T384 = 5,   // KC = 3072
-    TILE_G1_T768 = 6,   // KC = 6144
-    TILE_G2_T256 = 7,   // KC = 1024
-    TILE_G2_T512 = 8,   // KC = 2048
-    TILE_G4_T256 = 9,   // KC = 512
-    TILE_G1_T512 = 10,  // KC = 4096
+    TILE_G8_T256 = 0,       // KC = 256
+    TILE_G8_T128 = 1,       // KC = 128
+    TILE_G1_T64 = 2,        // KC = 512
+    TILE_G1_T128 = 3,       // KC = 1024
+    TILE_G1_T256 = 4,       // KC = 2048
+    TILE_G1_T384 = 5,       // KC = 3072
+    TILE_G1_T768 = 6,       // KC = 6144
+    TILE_G2_T256 = 7,       // KC = 1024
+    TILE_G2_T512 = 8,       // KC = 2048
+    TILE_G4_T256 = 9,       // KC = 512
+    TILE_G1_T512 = 10,      // KC = 4096
+    TILE_G1_T256_R4 = 11,   // KC = 1024
+    TILE_G1_T256_R2 = 12,   // KC = 512
+    TILE_G1_T512_R4 = 13,   // KC = 2048
+    TILE_G2_T512_R4 = 14,   // KC = 1024
+    TILE_G1_T512_R2 = 15,   // KC = 1024
+    TILE_G2_T256_R4 = 16,   // KC = 512
+    TILE_G1_T1024_R2 = 17,  // KC = 2048
+    TILE_G2_T1024_R4 = 18,  // KC = 2048
     TILE_COUNT
 };
 
 struct TileShape { int T, GB, R; };
 __host__ __device__ constexpr TileShape tile_shape(int cfg)
 {
-    return cfg == TILE_G8_T256 ? TileShape{256, 8, 8}
-         : cfg == TILE_G8_T128 ? TileShape{128, 8, 8}
-         : cfg == TILE_G1_T64  ? TileShape{64, 1, 8}
-         : cfg == TILE_G1_T128 ? TileShape{128, 1, 8}
-         : cfg == TILE_G1_T256 ? TileShape{256, 1, 8}
-         : cfg == TILE_G1_T384 ? TileShape{384, 1, 8}
-         : cfg == TILE_G1_T768 ? TileShape{768, 1, 8}
-         : cfg == TILE_G2_T256 ? TileShape{256, 2, 8}
-         : cfg == TILE_G2_T512 ? TileShape{512, 2, 8}
-         : cfg == TILE_G4_T256 ? TileShape{256, 4, 8}
-                               : TileShape{512, 1, 8};
+    constexpr TileShape tab[TILE_COUNT] = {
+        {256, 8, 8}, {128, 8, 8}, {64, 1, 8}, {128, 1, 8}, {256, 1, 8}, {384, 1, 8}, {768, 1, 8},
+        {256, 2, 8}, {512, 2, 8}, {256, 4, 8}, {512, 1, 8}, {256, 1, 4}, {256, 1, 2}, {512, 1, 4},
+        {512, 2, 4}, {512, 1, 2}, {256, 2, 4}, {1024, 1, 2}, {1024, 2, 4}};
+    return tab[cfg];
 }
 
 struct Q4Tiled {

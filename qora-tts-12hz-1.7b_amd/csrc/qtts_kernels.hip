@@ -135,22 +135,43 @@ struct ProPlain {
     template <int T>
     __device__ void load(float *xs, int k0, int KC, int ctile) const
     {
-        // KC, k0, ld and k are multiples of 4: float4 loads, all in flight
+        // KC, k0, ld and k are multiples of 4: float4 loads, all in flight.
+        // Loads use clamped (always valid) addresses and are masked after, so
+        // no load sits behind a branch (a guarded load compiles to branch +
+        // wait, serialising the round trips).
         constexpr int U = 8;
+        if ((k & 3) || (ld & 3)) {          // general shapes: scalar, clamped
+            for (int i0 = threadIdx.x; i0 < NB * KC; i0 += U * T) {
+                float v[U];
+#pragma unroll
+                for (int u = 0; u < U; u++) {
+                    const int i = min(i0 + u * T, NB * KC - 1);
+                    const int b = i / KC, r = k0 + (i - b * KC);
+                    const float xv = x[(size_t)b * ld + min(r, k - 1)];
+                    v[u] = r < k ? xv : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < U; u++)
+                    if (i0 + u * T < NB * KC) xs[i0 + u * T] = v[u];
+            }
+            return;
+        }
         const int n4 = NB * KC / 4;
         const int kc4 = KC / 4;
-        for (int i0 = threadIdx.x; i0 < n4; i0 += U * blockDim.x) {
+        for (int i0 = threadIdx.x; i0 < n4; i0 += U * T) {
             float4 v[U];
+            bool ok[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int i = i0 + u * blockDim.x;
+                const int i = min(i0 + u * T, n4 - 1);
                 const int b = i / kc4, r = k0 + 4 * (i - b * kc4);
-                v[u] = (i < n4 && r < k) ? *(const float4 *)(x + (size_t)b * ld + r) : make_float4(0.f, 0.f, 0.f, 0.f);
+                ok[u] = i0 + u * T < n4 && r < k;
+                v[u] = *(const float4 *)(x + (size_t)b * ld + min(r, k - 4));
             }
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int i = i0 + u * blockDim.x;
-                if (i < n4) *(float4 *)(xs + 4 * i) = v[u];
+                const int i = i0 + u * T;
+                if (i < n4) *(float4 *)(xs + 4 * i) = ok[u] ? v[u] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
     }
@@ -199,29 +220,28 @@ struct ProResidRms {
 #pragma unroll
         for (int u = 0; u < KCT / T; u++) {
             const int r = threadIdx.x + u * T;
-            gv[u] = (r < KC && k0 + r < k) ? h2f(gamma[k0 + r]) : 0.0f;
+            const float g = h2f(gamma[min(k0 + r, k - 1)]);     // clamped, unconditional
+            gv[u] = (r < KC && k0 + r < k) ? g : 0.0f;
         }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             float4 ps[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int i = threadIdx.x + u * T;
-                ps[u] = (base && i < k4) ? *(const float4 *)(base + (size_t)b * ldb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const int i = min((int)threadIdx.x + u * T, k4 - 1);
+                ps[u] = base ? *(const float4 *)(base + (size_t)b * ldb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
             if (parts) {
                 float4 acc[U];
                 for (int s0 = 0; s0 < S; s0 += RES_MAX_S) {
                     float4 pv[RES_MAX_S][U];
 #pragma unroll
-                    for (int s = 0; s < RES_MAX_S; s++)
+                    for (int s = 0; s < RES_MAX_S; s++) {
+                        const float *src = parts + ((size_t)min(s0 + s, S - 1) * NBP + prow + b) * npad;
 #pragma unroll
-                        for (int u = 0; u < U; u++) {
-                            const int i = threadIdx.x + u * T;
-                            pv[s][u] = (s0 + s < S && i < k4)
-                                           ? *(const float4 *)(parts + ((size_t)(s0 + s) * NBP + prow + b) * npad + 4 * i)
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
-                        }
+                        for (int u = 0; u < U; u++)
+                            pv[s][u] = *(const float4 *)(src + 4 * min((int)threadIdx.x + u * T, k4 - 1));
+                    }
 #pragma unroll
                     for (int u = 0; u < U; u++) {
                         float4 a = s0 == 0 ? pv[0][u] : acc[u];
@@ -245,7 +265,7 @@ struct ProResidRms {
                 if (i < k4) {
                     float4 x = ps[u];
                     if (bias) {
-                        const float4 bb = *(const float4 *)(bias + 4 * i);
+                        const float4 bb = *(const float4 *)(bias + 4 * min(i, k4 - 1));
                         x.x += bb.x; x.y += bb.y; x.z += bb.z; x.w += bb.w;
                     }
                     *(float4 *)(xf + b * KMAX + 4 * i) = x;
@@ -325,7 +345,8 @@ struct ProEmbed {
         const uint32_t row = *code;
         for (int i = threadIdx.x; i < KC; i += blockDim.x) {
             const int r = k0 + i;
-            xs[i] = r < emb.n ? q4_row_value(emb, row, r) : 0.0f;
+            const float v = q4_row_value(emb, row, min(r, emb.n - 1));
+            xs[i] = r < emb.n ? v : 0.0f;
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -343,9 +364,10 @@ struct ProHidEmbed {
     {
         const uint32_t row = *code;
         for (int i = threadIdx.x; i < KC; i += blockDim.x) {
-            const int r = k0 + i;
-            xs[i] = r < k ? hidden[r] : 0.0f;
-            xs[KC + i] = r < k ? q4_row_value(emb, row, r) : 0.0f;
+            const int r = k0 + i, rc = min(r, k - 1);
+            const float hv = hidden[rc], ev = q4_row_value(emb, row, rc);
+            xs[i] = r < k ? hv : 0.0f;
+            xs[KC + i] = r < k ? ev : 0.0f;
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -443,7 +465,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     constexpr int NL = 64 / GB;
     constexpr int CNTF = (32 / NL) > 0 ? (32 / NL) : 1;
     constexpr int DUP = (GB == 1) ? 32 : 0;     // lanes holding duplicates
-    static_assert(R == 8, "scale block is one 16-byte load");
+    static_assert(R == 2 || R == 4 || R == 8, "scale block is one 4/8/16-byte load");
     __shared__ float xs[NB * KC];
     __shared__ float red[NW * NB * C];
     __shared__ float ybuf[NB * C];
@@ -461,7 +483,20 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
 #pragma unroll
         for (int r = 0; r < R; r++)
             q[r] = __builtin_nontemporal_load((const u32x4 *)(tile + ((size_t)r * T + t) * 16));
-        const u32x4 sc = __builtin_nontemporal_load((const u32x4 *)(tile + (size_t)R * T * 16 + (size_t)t * 16));
+        uint32_t sc[R / 2];
+        {
+            const uint8_t *sp = tile + (size_t)R * T * 16 + (size_t)t * (2 * R);
+            if constexpr (R == 8) {
+                const u32x4 v = __builtin_nontemporal_load((const u32x4 *)sp);
+                sc[0] = v[0]; sc[1] = v[1]; sc[2] = v[2]; sc[3] = v[3];
+            } else if constexpr (R == 4) {
+                typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 v = __builtin_nontemporal_load((const u32x2 *)sp);
+                sc[0] = v[0]; sc[1] = v[1];
+            } else {
+                sc[0] = __builtin_nontemporal_load((const uint32_t *)sp);
+            }
+        }
 
         __syncthreads();               // xs / red / ybuf of the previous item are free
         pro.template load<T>(xs, s * KC, KC, c);
@@ -540,22 +575,32 @@ template <int NB, class Pro, class Epi>
 static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st)
 {
     const int grid = w.S * w.CT;
-#define QTTS_GEMV_CASE(CFG, T, GB)                                                              \
-    case CFG:                                                                                   \
-        hipLaunchKernelGGL((k_gemv<T, GB, 8, NB, Pro, Epi>), dim3(grid), dim3(T), 0, st, w, pro, epi); \
-        break;
+#define QTTS_GEMV_CASE(CFG)                                                                     \
+    case CFG: {                                                                                 \
+        constexpr TileShape ts = tile_shape(CFG);                                               \
+        hipLaunchKernelGGL((k_gemv<ts.T, ts.GB, ts.R, NB, Pro, Epi>), dim3(grid), dim3(ts.T), 0, st, w, pro, epi); \
+        break;                                                                                  \
+    }
     switch (w.cfg) {
-        QTTS_GEMV_CASE(TILE_G8_T256, 256, 8)
-        QTTS_GEMV_CASE(TILE_G8_T128, 128, 8)
-        QTTS_GEMV_CASE(TILE_G1_T64, 64, 1)
-        QTTS_GEMV_CASE(TILE_G1_T128, 128, 1)
-        QTTS_GEMV_CASE(TILE_G1_T256, 256, 1)
-        QTTS_GEMV_CASE(TILE_G1_T384, 384, 1)
-        QTTS_GEMV_CASE(TILE_G1_T768, 768, 1)
-        QTTS_GEMV_CASE(TILE_G2_T256, 256, 2)
-        QTTS_GEMV_CASE(TILE_G2_T512, 512, 2)
-        QTTS_GEMV_CASE(TILE_G4_T256, 256, 4)
-        QTTS_GEMV_CASE(TILE_G1_T512, 512, 1)
+        QTTS_GEMV_CASE(TILE_G8_T256)
+        QTTS_GEMV_CASE(TILE_G8_T128)
+        QTTS_GEMV_CASE(TILE_G1_T64)
+        QTTS_GEMV_CASE(TILE_G1_T128)
+        QTTS_GEMV_CASE(TILE_G1_T256)
+        QTTS_GEMV_CASE(TILE_G1_T384)
+        QTTS_GEMV_CASE(TILE_G1_T768)
+        QTTS_GEMV_CASE(TILE_G2_T256)
+        QTTS_GEMV_CASE(TILE_G2_T512)
+        QTTS_GEMV_CASE(TILE_G4_T256)
+        QTTS_GEMV_CASE(TILE_G1_T512)
+        QTTS_GEMV_CASE(TILE_G1_T256_R4)
+        QTTS_GEMV_CASE(TILE_G1_T256_R2)
+        QTTS_GEMV_CASE(TILE_G1_T512_R4)
+        QTTS_GEMV_CASE(TILE_G2_T512_R4)
+        QTTS_GEMV_CASE(TILE_G1_T512_R2)
+        QTTS_GEMV_CASE(TILE_G2_T256_R4)
+        QTTS_GEMV_CASE(TILE_G1_T1024_R2)
+        QTTS_GEMV_CASE(TILE_G2_T1024_R4)
     default: return hipErrorInvalidValue;
     }
 #undef QTTS_GEMV_CASE
@@ -571,9 +616,13 @@ __global__ void k_reduce_parts(const float *part, int S, int NB, int npad, int n
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     const int b = blockIdx.y;
     if (j >= n) return;
+    // columns past the last whole 32-column group (j >= npad) have no
+    // partials and stay zero, as gemv.rs:255 leaves them
     float v = 0.0f;
+    if (j < npad) {
 #pragma unroll 8
-    for (int s = 0; s < S; s++) v += part[((size_t)s * NB + b) * npad + j];
+        for (int s = 0; s < S; s++) v += part[((size_t)s * NB + b) * npad + j];
+    }
     float *o = y + (size_t)b * ld + j;
     if (resid) v = *o + v;
     if (bias) v += bias[j];
@@ -684,22 +733,20 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
 #pragma unroll
         for (int it = 0; it < 4; it++) {
             const int tok = wv * 16 + it * 4 + (lane >> 4);
-            if (tok < ntok) {
-                const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
-                const float4 ka = kr[0], kb = kr[1];
-                kk[it][0] = ka.x; kk[it][1] = ka.y; kk[it][2] = ka.z; kk[it][3] = ka.w;
-                kk[it][4] = kb.x; kk[it][5] = kb.y; kk[it][6] = kb.z; kk[it][7] = kb.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) kk[it][i] = 0.0f;
-            }
+            // pages are allocated whole: rows past ntok are read and masked
+            const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
+            const float4 ka = kr[0], kb = kr[1];
+            const bool ok = tok < ntok;
+            kk[it][0] = ok ? ka.x : 0.f; kk[it][1] = ok ? ka.y : 0.f; kk[it][2] = ok ? ka.z : 0.f; kk[it][3] = ok ? ka.w : 0.f;
+            kk[it][4] = ok ? kb.x : 0.f; kk[it][5] = ok ? kb.y : 0.f; kk[it][6] = ok ? kb.z : 0.f; kk[it][7] = ok ? kb.w : 0.f;
         }
         const int dv = t & 127, half = t >> 7;
         float vv[32];
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             const int tok = half * 32 + i;
-            vv[i] = tok < ntok ? Vp[(size_t)tok * HEAD_DIM + dv] : 0.0f;
+            const float v = Vp[(size_t)tok * HEAD_DIM + dv];
+            vv[i] = tok < ntok ? v : 0.0f;
         }
         float q0[8], q1[8];
 #pragma unroll

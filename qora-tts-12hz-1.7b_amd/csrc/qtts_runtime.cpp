@@ -119,19 +119,22 @@ static int env_tile(const char *name, int dflt)
     return (x >= 0 && x < TILE_COUNT) ? x : dflt;
 }
 
-// Default tile of each weight role (QTTS_TILE_<ROLE> overrides it).  Each
-// choice gives roughly 100-250 workgroups at the 1.7B shapes while keeping
-// the number of k-slices (partial sums the next stage reduces) at 1-4.
+// Default tile of each weight role (QTTS_TILE_<ROLE> overrides it), chosen by
+// a per-role sweep of frames/s on MI355X at the 1.7B shapes.  Wide
+// workgroups with few rows per thread (R 2-4) win on the small predictor
+// and attention-side weights: more waves share each tile, so the per-lane
+// dequant chain and the cross-wave reduction are shorter.
 static int default_cfg(const char *role, int64_t k)
 {
     const std::string r(role);
-    if (r == "TQKV" || r == "TO" || r == "HEAD" || r == "PDOWN") return TILE_G1_T128;   // KC 1024
-    if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;                    // one slice, SiLU epilogue
-    if (r == "PGU") return k <= 1024 ? TILE_G2_T256 : TILE_G2_T512;
-    if (r == "TDOWN") return TILE_G1_T256;                                              // KC 2048
-    if (r == "PQKV") return TILE_G1_T128;
-    if (r == "PO" || r == "PHEAD" || r == "PPROJ") return TILE_G1_T64;                 // KC 512
-    return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                                     // text fc, GEMV
+    if (r == "TQKV") return TILE_G1_T512_R2;                                    // KC 1024
+    if (r == "TO" || r == "PQKV" || r == "PO" || r == "PPROJ") return TILE_G1_T256_R2;   // KC 512
+    if (r == "HEAD" || r == "PHEAD") return TILE_G1_T256_R4;                    // KC 1024
+    if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;            // one slice, SiLU epilogue
+    if (r == "PGU") return k <= 1024 ? TILE_G2_T512_R4 : TILE_G2_T512;          // one slice, SiLU epilogue
+    if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
+    if (r == "PDOWN") return TILE_G1_T512_R2;                                   // KC 1024
+    return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                             // text fc, GEMV
 }
 
 static int role_cfg(const char *role, int64_t k) { return env_tile(role, default_cfg(role, k)); }
@@ -1103,25 +1106,27 @@ extern "C" int qtts_gen_state(qtts_ctx *c, float *logits, float *hidden, int64_t
 // measurement
 // ---------------------------------------------------------------------------
 
+// Average launch duration: one event pair around `iters` back-to-back
+// launches on the context stream (a warm-up launch first), so the figure is
+// the kernel plus the dispatch gap, without per-event overhead.
 static int time_launches(qtts_ctx *c, int32_t iters, const std::function<hipError_t(int)> &launch, double *avg_us)
 {
-    std::vector<hipEvent_t> ev(2 * (size_t)iters);
-    for (auto &e : ev) HIPCHK(c, hipEventCreate(&e));
-    for (int i = 0; i < iters; i++) {
-        HIPCHK(c, hipEventRecord(ev[2 * i], c->stream));
-        HIPCHK(c, launch(i));
-        HIPCHK(c, hipEventRecord(ev[2 * i + 1], c->stream));
-    }
-    HIPCHK(c, hipStreamSynchronize(c->stream));
-    double tot = 0.0;
-    for (int i = 0; i < iters; i++) {
-        float ms = 0.0f;
-        HIPCHK(c, hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]));
-        tot += ms;
-    }
-    for (auto &e : ev) hipEventDestroy(e);
-    *avg_us = tot * 1000.0 / iters;
-    return QTTS_OK;
+    hipEvent_t e0, e1;
+    HIPCHK(c, hipEventCreate(&e0));
+    HIPCHK(c, hipEventCreate(&e1));
+    int rc = QTTS_OK;
+    hipError_t err = launch(0);
+    if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters && err == hipSuccess; i++) err = launch(i);
+    if (err == hipSuccess) err = hipEventRecord(e1, c->stream);
+    if (err == hipSuccess) err = hipEventSynchronize(e1);
+    float ms = 0.0f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+    if (err != hipSuccess) rc = fail(c, QTTS_ERR_HIP, "kernel timing: %s", hipGetErrorString(err));
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    *avg_us = ms * 1000.0 / iters;
+    return rc;
 }
 
 extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double *avg_us, double *bytes)

@@ -27,6 +27,13 @@ from .hostdesc import PredictorHost, Q4Host, SampleParams, TalkerHost, ptr, samp
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libqtts_hip.so")
 
+# GEMV tile shapes (T threads, GB 32-column groups, R rows per thread), indexed
+# by the TileCfg value that QTTS_TILE_<ROLE> environment overrides take
+# (csrc/qtts_device.h, tile_shape()).
+TILE_SHAPES = [(256, 8, 8), (128, 8, 8), (64, 1, 8), (128, 1, 8), (256, 1, 8), (384, 1, 8), (768, 1, 8),
+               (256, 2, 8), (512, 2, 8), (256, 4, 8), (512, 1, 8), (256, 1, 4), (256, 1, 2), (512, 1, 4),
+               (512, 2, 4), (512, 1, 2), (256, 2, 4), (1024, 1, 2), (1024, 2, 4)]
+
 OK, ERR_INVALID, ERR_HIP, ERR_OOM, ERR_CAPACITY, ERR_STATE, ERR_IO, ERR_NAN, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6, -7, -8
 DEVICE_PTRS = 1
 

@@ -89,6 +89,28 @@ def test_gemv_model_shapes(ctx, k, n):
     assert ok, f"rel err {e}"
 
 
+@pytest.mark.parametrize("cfg", range(len(qtts.TILE_SHAPES)))
+def test_gemv_every_tile_config(ctx, cfg, monkeypatch):
+    """Each tile shape (QTTS_TILE_GEMV override) on ragged shapes: k not a
+    multiple of the slice height, n not a multiple of 32, k % 4 != 0; one
+    row (NB 1) and three rows (NB 2 + NB 1)."""
+    monkeypatch.setenv("QTTS_TILE_GEMV", str(cfg))
+    rng = np.random.Generator(np.random.PCG64(1000 + cfg))
+    for k, n in ((3072, 1000), (2048, 4096), (100, 96)):
+        w = synth.q4_random(rng, k, n)
+        X = rng.standard_normal((3, k)).astype(np.float32)
+        dw = ctx.upload(w)
+        y = ctx.gemv(dw, X[0])
+        Y = ctx.gemm(dw, X)
+        dw.free()
+        R = O.gemm(X, w)
+        ok, e = close(y, R[0])
+        assert ok, f"cfg {cfg} {qtts.TILE_SHAPES[cfg]} k={k} n={n} gemv rel err {e}"
+        for r in range(3):
+            ok, e = close(Y[r], R[r])
+            assert ok, f"cfg {cfg} k={k} n={n} gemm row {r} rel err {e}"
+
+
 def test_gemm_rows(ctx):
     rng = np.random.Generator(np.random.PCG64(3))
     w = synth.q4_random(rng, 2048, 3072)

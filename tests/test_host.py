@@ -8,6 +8,8 @@ import pytest
 import qtts
 from qtts import hostdesc, synth
 
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
 
 def test_library_exports_every_header_symbol():
     lib = ctypes.CDLL(qtts.LIB_PATH)
@@ -47,3 +49,15 @@ def test_synth_shapes_and_determinism():
 def test_missing_library_raises(tmp_path):
     with pytest.raises(qtts.QttsError):
         qtts.load_library(str(tmp_path / "nope.so"))
+
+
+def test_tile_shapes_match_device_table():
+    """qtts.TILE_SHAPES mirrors tile_shape() in csrc/qtts_device.h."""
+    import re
+    src = open(os.path.join(ROOT, "qora-tts-12hz-1.7b_amd", "csrc", "qtts_device.h")).read()
+    body = src[src.index("constexpr TileShape tab[TILE_COUNT]"):]
+    body = body[body.index("{") + 1: body.index("};")]
+    tab = [tuple(int(v) for v in m) for m in re.findall(r"\{(\d+),\s*(\d+),\s*(\d+)\}", body)]
+    assert tab == qtts.TILE_SHAPES
+    n_enum = len(re.findall(r"^\s*TILE_G\d+_T\d+(?:_R\d)?\s*=\s*\d+", src, re.M))
+    assert n_enum == len(tab)
