@@ -10,9 +10,11 @@ growing from 64 (2048 frames: 64 -> 2112), top-k 50, temperature 0.9,
 repetition penalty 1.05, seed 42, EOS disabled (random weights can emit it).
 
 Printed as one JSON line: frames/s over the timed frames (whole job, inputs
-resident in HBM), the roofline of the dominant kernel (HIP events around
-each launch), the Q4 GEMV bandwidth on a rotating pool of 64 weights, and
-the oracle's CPU frame rate on a bounded sample as the CPU baseline.
+resident in HBM); the roofline of the Q4 GEMV k=2048 -> n=6144 on a rotating
+pool of 64 weights (HIP events around back-to-back launches); the talker
+gate|up and attention kernels and a float4 copy (with --stream, the same
+GEMV kernel streaming a 113 MB weight); and the oracle's CPU frame rate on a
+bounded sample as the CPU baseline.
 """
 import argparse
 import json
@@ -27,6 +29,27 @@ sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
 
 HBM_PEAK_GBS = 8000.0
 TTS_PAD = 151671          # generate_new.rs:28
+
+
+# The standalone GEMV's kernel instance (tile G8_T256, plain prologue, partial
+# epilogue); no frame stage uses this instance, so rocprof's line for it
+# covers exactly the GEMV timing launches.
+GEMV_KERNEL = "k_gemv<256, 8, 8, 1, ProPlain<1>, EpiPart<1>>"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_2048x6144_hbm_traffic.txt")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel factor), or
+    None when that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1])), os.path.relpath(TRAFFIC_FILE, ROOT)
+    except OSError:
+        pass
+    return None, None
 
 
 def log(msg):
@@ -74,6 +97,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-copies", type=int, default=64)
+    ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -118,23 +142,16 @@ def main():
     fps = frames / dt
     log(f"{frames} frames in {dt:.3f}s -> {fps:.1f} frames/s (KV 64 -> {64 + frames})")
 
-    # kernel rooflines at the final KV length (~2112)
+    # kernels at the final KV length (~2112): HIP events around back-to-back launches
     gu_us, gu_bytes = ctx.time_kernel(0, 4 * args.layers)
     at_us, at_bytes = ctx.time_kernel(1, 4 * args.layers)
-    kern = {
-        "talker gate|up Q4 GEMV (k_gemv, RMSNorm prologue)": (gu_us, gu_bytes),
-        f"talker decode attention (k_talker_attn, KV {ctx.kv_len()})": (at_us, at_bytes),
-    }
-    name = max(kern, key=lambda k: kern[k][0])
-    us, byts = kern[name]
-    ach = byts / (us * 1e-6) / 1e9
-    roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
-            "avg_us": round(us, 2), "bytes_per_launch": int(byts)}
+    cp_us, cp_bytes = ctx.time_kernel(2, 20)
     log(f"gate|up {gu_us:.2f}us ({gu_bytes / gu_us / 1e3:.0f} GB/s), attention {at_us:.2f}us "
-        f"({at_bytes / at_us / 1e3:.0f} GB/s)")
+        f"({at_bytes / at_us / 1e3:.0f} GB/s), float4 copy 256 MiB {cp_bytes / cp_us / 1e3:.0f} GB/s")
 
-    # Q4 GEMV (k=2048 -> n=6144) over a pool of distinct weights (> 256 MB last-level cache)
+    # Q4 GEMV k=2048 -> n=6144 (the dominant kernel family: k_gemv is ~3/4 of
+    # the frame's GPU time) over a pool of distinct weights (> 256 MB
+    # last-level cache), then the same kernel streaming a 113 MB weight
     grng = np.random.Generator(np.random.PCG64(1))
     pool = [ctx.upload(synth.q4_random(grng, 2048, 6144)) for _ in range(args.gemv_copies)]
     g_us, g_bytes = ctx.time_gemv(pool, 4 * args.gemv_copies)
@@ -142,6 +159,33 @@ def main():
         w.free()
     g_gbs = g_bytes / (g_us * 1e-6) / 1e9
     log(f"Q4 GEMV 2048x6144: {g_us:.2f}us/launch, {g_gbs:.0f} GB/s")
+    traffic, traffic_src = measured_traffic(GEMV_KERNEL)
+    roof = {"bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(g_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": f"{GEMV_KERNEL} (Q4 GEMV k=2048 -> n=6144, tile 8 groups x 256 rows)",
+            "avg_us": round(g_us, 3), "bytes_per_launch": int(g_bytes), "traffic_source": traffic_src}
+    kernels = {
+        "talker_gate_up_rmsnorm": {"us": round(gu_us, 2), "gbs": round(gu_bytes / gu_us / 1e3, 1),
+                                   "bytes": int(gu_bytes)},
+        f"talker_attention_kv{ctx.kv_len()}": {"us": round(at_us, 2), "gbs": round(at_bytes / at_us / 1e3, 1),
+                                               "bytes": int(at_bytes)},
+        "float4_copy_256MiB": {"us": round(cp_us, 2), "gbs": round(cp_bytes / cp_us / 1e3, 1),
+                               "bytes": int(cp_bytes)},
+    }
+    if args.stream:
+        # the same kernel streaming one 113 MB weight per launch (4 copies);
+        # opt-in, so the default run's profile line for the kernel covers the
+        # 2048 x 6144 launches alone
+        big = synth.q4_random(grng, 2048, 98304)
+        pool = [ctx.upload(big) for _ in range(4)]
+        s_us, s_bytes = ctx.time_gemv(pool, 32)
+        for w in pool:
+            w.free()
+        del big
+        s_gbs = s_bytes / (s_us * 1e-6) / 1e9
+        log(f"Q4 GEMV 2048x98304: {s_us:.2f}us/launch, {s_gbs:.0f} GB/s")
+        kernels["q4_gemv_stream_2048x98304"] = {"us": round(s_us, 2), "gbs": round(s_gbs, 1),
+                                                "frac": round(s_gbs / HBM_PEAK_GBS, 4), "bytes": int(s_bytes)}
 
     cpu = None
     if not args.no_cpu:
@@ -167,9 +211,7 @@ def main():
                                f"{frames} frames, KV 64->{64 + frames}, top-k 50, T 0.9, seed 42",
                    "kv_start": 64, "kv_end": 64 + frames, "parallelism": "single GPU"},
         "roofline": roof,
-        "q4_gemv": {"shape": [2048, 6144], "us_per_launch": round(g_us, 2), "gbs": round(g_gbs, 1),
-                    "frac_peak": round(g_gbs / HBM_PEAK_GBS, 4), "pool_copies": args.gemv_copies,
-                    "bytes_per_launch": int(g_bytes)},
+        "kernels": kernels,
         "cpu_baseline": cpu,
     }
     ctx.close()

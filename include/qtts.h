@@ -269,7 +269,9 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
  * reference times phases with Instant, generate_new.rs:600-678).
  *   kind 0: talker gate|up GEMV (RMSNorm prologue), cycling the layers;
  *   kind 1: talker decode attention over the cached positions, cycling
- *           the layers. */
+ *           the layers;
+ *   kind 2: plain float4 copy of 256 MiB (no model needed), the HBM
+ *           calibration point for byte counters. */
 int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
                      double *avg_us, double *bytes);
 

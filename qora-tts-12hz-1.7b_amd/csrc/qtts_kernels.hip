@@ -1569,6 +1569,33 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
 
 // Timing helpers: the gate|up GEMV of layer l with its real prologue, and the
 // decode attention of layer l over `len` positions.
+// Plain 16-byte-per-lane copy, 8 loads per thread in flight; n % 4 == 0.
+__global__ void __launch_bounds__(256) k_copy_f4(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, int64_t n4)
+{
+    constexpr int U = 8;
+    const int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int64_t i = base + (int64_t)u * 256;
+        v[u] = __builtin_nontemporal_load(src + (i < n4 ? i : n4 - 1));
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int64_t i = base + (int64_t)u * 256;
+        if (i < n4) __builtin_nontemporal_store(v[u], dst + i);
+    }
+}
+
+hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s)
+{
+    if (n <= 0 || n % 4) return hipErrorInvalidValue;
+    const int64_t n4 = n / 4;
+    const int64_t grid = (n4 + 256 * 8 - 1) / (256 * 8);
+    hipLaunchKernelGGL(k_copy_f4, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4 *)src, (u32x4 *)dst, n4);
+    return hipGetLastError();
+}
+
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];

@@ -56,6 +56,9 @@ struct qtts_ctx {
 
     hipGraphExec_t frame_exec = nullptr;
     bool gen_started = false;
+
+    float *d_copy = nullptr;                         // copy-calibration buffers, 2 x copy_floats
+    int64_t copy_floats = 0;
 };
 
 // ---------------------------------------------------------------------------
@@ -134,7 +137,8 @@ static int default_cfg(const char *role, int64_t k)
     if (r == "PGU") return k <= 1024 ? TILE_G2_T512_R4 : TILE_G2_T512;          // one slice, SiLU epilogue
     if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
     if (r == "PDOWN") return TILE_G1_T512_R2;                                   // KC 1024
-    return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                             // text fc, GEMV
+    if (r == "GEMV") return TILE_G8_T256;                                       // standalone Q4 GEMV
+    return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                             // text fc
 }
 
 static int role_cfg(const char *role, int64_t k) { return env_tile(role, default_cfg(role, k)); }
@@ -379,6 +383,7 @@ extern "C" void qtts_ctx_destroy(qtts_ctx *c)
     if (c->d_forced) hipFree(c->d_forced);
     if (c->d_io) hipFree(c->d_io);
     if (c->d_io2) hipFree(c->d_io2);
+    if (c->d_copy) hipFree(c->d_copy);
     if (c->st_gen) hipFree(c->st_gen);
     if (c->st_api) hipFree(c->st_api);
     if (c->h_st) hipHostFree(c->h_st);
@@ -1131,8 +1136,22 @@ static int time_launches(qtts_ctx *c, int32_t iters, const std::function<hipErro
 
 extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double *avg_us, double *bytes)
 {
+    if (!c || iters < 1 || !avg_us || !bytes) return QTTS_ERR_INVALID;
+    if (kind == 2) {
+        // plain float4 copy of 256 MiB (read + write), the HBM calibration
+        // point for byte counters and for achievable bandwidth
+        hipSetDevice(c->device);
+        const int64_t n = 64ll << 20;
+        if (!c->d_copy) {
+            HIPCHK(c, hipMalloc(&c->d_copy, 2 * n * sizeof(float)));
+            HIPCHK(c, hipMemsetAsync(c->d_copy, 0, 2 * n * sizeof(float), c->stream));
+            c->copy_floats = n;
+        }
+        *bytes = 2.0 * n * sizeof(float);
+        return time_launches(c, iters, [&](int) { return enqueue_copy(c->d_copy, c->d_copy + n, n, c->stream); },
+                             avg_us);
+    }
     NEED_MODEL(c);
-    if (iters < 1 || !avg_us || !bytes) return QTTS_ERR_INVALID;
     const TalkerDev &m = c->tm;
     if (kind == 0) {
         const LayerDev &L = m.layers[0];
