@@ -194,6 +194,17 @@ def test_rms_norm_against_float64():
     assert np.abs(O.rms_norm(x, g) - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
+def test_rms_norm_eps_is_1e_6():
+    # rows with mean(x^2) = 1e-6: the eps doubles the variance term, so the
+    # output is x / sqrt(2e-6) * gamma; eps 1e-5 would give x / sqrt(1.1e-5)
+    x = np.full(1024, 1e-3, np.float32)
+    x[1::2] = -1e-3
+    g = np.full(1024, np.float16(1.0)).view(np.uint16)
+    out = O.rms_norm(x, g).astype(np.float64)
+    ref = x.astype(np.float64) / np.sqrt(2e-6)
+    assert np.abs(out - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
 def test_rms_norm_constant_vector():
     # closed form: rms of c*ones is |c|, so out = sign(c) * gamma (eps aside)
     g = np.full(1024, np.float16(1.0)).view(np.uint16)
