@@ -100,8 +100,8 @@ def main():
     ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              f"(decode of one utterance is a serial chain; see the sharding notes)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              f"(one utterance's decode is a serial chain; independent text chunks would each take one GPU)", file=sys.stderr)
         sys.exit(2)
 
     import qtts

@@ -4,8 +4,7 @@
  * The path covered is the per-frame autoregressive decode: the 28-layer
  * Talker step and the 5-layer code predictor's 15-codebook chain, with the
  * talker sampler between them.  Every entry point below replaces one Rust
- * function of the reference crate (cited as file:line); a Rust `ffi.rs`
- * binding this header is given in INTEGRATION.md.
+ * function of the reference crate (cited as file:line).
  *
  * Conventions (mirroring the reference's borrow/own rules):
  *  - Every call returns an int status: QTTS_OK (0) or a negative QTTS_ERR_*.

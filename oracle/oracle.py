@@ -2,8 +2,8 @@
 
 TEST INFRASTRUCTURE: only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg use this module.  It restates the reference's CPU decode
-path (see qtts_oracle.c) and is the checker for the HIP path, never part of
-it.
+path (see qtts_oracle.c) and is the oracle the HIP path is tested
+against, never part of it.
 """
 import ctypes
 import os

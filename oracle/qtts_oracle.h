@@ -2,7 +2,8 @@
  * qtts_oracle.h — CPU restatement of the QORA-TTS decode path (test
  * infrastructure only).
  *
- * This library is the checker for the HIP path and the timed CPU baseline.
+ * This library is the oracle the HIP path is tested against, and the timed
+ * CPU baseline.
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
  * load it; the product library never links or calls it.
  *
@@ -13,7 +14,7 @@
  *
  * Parity pinning (what checks each function beyond the restatement itself)
  * is listed per function in tests/test_oracle.py; functions with no such
- * check are marked "parity unpinned" there and in DESIGN.md.
+ * check are marked "parity unpinned" there.
  */
 #ifndef QTTS_ORACLE_H
 #define QTTS_ORACLE_H

@@ -52,7 +52,7 @@ def loaded(ctx, small_model):
 
 # ---- operator level ------------------------------------------------------
 
-def test_gemv_config1(ctx):
+def test_gemv_2048x6144(ctx):
     # one Q4 GEMV, k=2048 -> n=6144, nibbles uniform, scales |N(0,0.02)|, x ~ N(0,1)
     rng = np.random.Generator(np.random.PCG64(1))
     w = synth.q4_random(rng, 2048, 6144)
@@ -151,7 +151,7 @@ def test_kv_load_gather_bit_exact(loaded):
 
 
 def test_talker_step_kv512(loaded):
-    # config-2 shape on a 2-layer talker: KV prefilled N(0,1) to 512, append one, attend 513
+    # 1.7B layer shapes on a 2-layer talker: KV prefilled N(0,1) to 512, append one, attend 513
     ctx, om, t, p = loaded
     rng = np.random.Generator(np.random.PCG64(6))
     L = 512
@@ -212,7 +212,7 @@ def test_codec_head(loaded):
 
 
 def test_predictor_chain_codes(loaded):
-    # config 3: 5 layers, 15 codebooks, KV 2 -> 16, greedy argmax
+    # predictor chain: 5 layers, 15 codebooks, KV 2 -> 16, greedy argmax
     ctx, om, t, p = loaded
     agree = total = 0
     for seed in range(4):
