@@ -270,7 +270,9 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
  *   kind 1: talker decode attention over the cached positions, cycling
  *           the layers;
  *   kind 2: plain float4 copy of 256 MiB (no model needed), the HBM
- *           calibration point for byte counters. */
+ *           calibration point for byte counters;
+ *   kind 3: predictor attention + o-proj, one row at position 8;
+ *   kind 4: one whole predictor layer step, one row at position 8. */
 int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
                      double *avg_us, double *bytes);
 

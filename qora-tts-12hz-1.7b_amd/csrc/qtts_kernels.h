@@ -101,6 +101,8 @@ hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &
 hipError_t enqueue_kv_gather(const KvPaged &kv, int layer, int len, float *K, float *V, hipStream_t s);
 hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float *K, const float *V,
                               hipStream_t s);
+hipError_t enqueue_pred_attn_o_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
+hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
 hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,

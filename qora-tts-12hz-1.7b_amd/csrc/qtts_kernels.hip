@@ -23,6 +23,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace qtts {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -124,54 +126,103 @@ __device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int
 }
 
 // ---------------------------------------------------------------------------
-// GEMV prologues: fill xs[b*KC + i] with input row b, rows k0+i.  Loads are
-// unrolled so each thread's loads are in flight together.
+// DPP wave reductions: lane exchanges on the VALU (quad permutes, half-row
+// and row mirrors), then the four row totals read as uniform values.  Every
+// lane gets the same result.
 // ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_mov<0x141>(v);   // row_half_mirror: the other quad of the half row
+    v += dpp_mov<0x140>(v);   // row_mirror: the other half of the row
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v = row_sum16(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// ---------------------------------------------------------------------------
+// GEMV prologues.  A prologue fills xs[b*KC + i] with input row b, rows
+// k0 + i, in two stages:
+//   fetch<T, KC>(f, k0, ctile): every global load the prologue needs, into
+//     the registers of f, issued before the tile's weight loads and without
+//     a barrier.  Vector loads retire in issue order, so a load issued after
+//     the weights could only be waited on by also waiting for the weights.
+//   load<T, KC>(f, xs, k0, ctile): the arithmetic, LDS writes and barriers;
+//     its waits cover the prologue's loads while the weights stay in flight.
+// Loads use clamped (always valid) addresses and are masked afterwards, so no
+// load sits behind a branch.
+// ---------------------------------------------------------------------------
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p; }
 
 template <int NB>
 struct ProPlain {
     const float *x;
     int ld, k;
-    template <int T>
-    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    template <int T, int KC>
+    struct Fetch {
+        f32x4 v[(NB * KC / 4 + T - 1) / T];
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
-        // KC, k0, ld and k are multiples of 4: float4 loads, all in flight.
-        // Loads use clamped (always valid) addresses and are masked after, so
-        // no load sits behind a branch (a guarded load compiles to branch +
-        // wait, serialising the round trips).
-        constexpr int U = 8;
-        if ((k & 3) || (ld & 3)) {          // general shapes: scalar, clamped
-            for (int i0 = threadIdx.x; i0 < NB * KC; i0 += U * T) {
-                float v[U];
+        constexpr int N4 = NB * KC / 4, U = (N4 + T - 1) / T;
+        const bool vec = !((k & 3) | (ld & 3));
 #pragma unroll
-                for (int u = 0; u < U; u++) {
-                    const int i = min(i0 + u * T, NB * KC - 1);
-                    const int b = i / KC, r = k0 + (i - b * KC);
-                    const float xv = x[(size_t)b * ld + min(r, k - 1)];
-                    v[u] = r < k ? xv : 0.0f;
-                }
-#pragma unroll
-                for (int u = 0; u < U; u++)
-                    if (i0 + u * T < NB * KC) xs[i0 + u * T] = v[u];
-            }
-            return;
+        for (int u = 0; u < U; u++) {
+            const int i = min((int)threadIdx.x + u * T, N4 - 1);
+            const int b = i / (KC / 4), r = k0 + 4 * (i - b * (KC / 4));
+            const float *row = x + (size_t)b * ld;
+            if (vec)
+                f.v[u] = ld4(row + min(r, k - 4));
+            else
+                f.v[u] = f32x4{row[min(r, k - 1)], row[min(r + 1, k - 1)], row[min(r + 2, k - 1)],
+                               row[min(r + 3, k - 1)]};
         }
-        const int n4 = NB * KC / 4;
-        const int kc4 = KC / 4;
-        for (int i0 = threadIdx.x; i0 < n4; i0 += U * T) {
-            float4 v[U];
-            bool ok[U];
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        constexpr int N4 = NB * KC / 4, U = (N4 + T - 1) / T;
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int i = min(i0 + u * T, n4 - 1);
-                const int b = i / kc4, r = k0 + 4 * (i - b * kc4);
-                ok[u] = i0 + u * T < n4 && r < k;
-                v[u] = *(const float4 *)(x + (size_t)b * ld + min(r, k - 4));
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int i = i0 + u * T;
-                if (i < n4) *(float4 *)(xs + 4 * i) = ok[u] ? v[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < U; u++) {
+            const int i = threadIdx.x + u * T;
+            if (i < N4) {
+                const int b = i / (KC / 4), r = k0 + 4 * (i - b * (KC / 4));
+                f32x4 v = f.v[u];
+                v.x = r < k ? v.x : 0.0f;
+                v.y = r + 1 < k ? v.y : 0.0f;
+                v.z = r + 2 < k ? v.z : 0.0f;
+                v.w = r + 3 < k ? v.w : 0.0f;
+                *(f32x4 *)(xs + 4 * i) = v;
             }
         }
     }
@@ -181,11 +232,12 @@ struct ProPlain {
 // Residual update + RMSNorm (gemv.rs:445-454):
 //   x = base + sum_s parts[s]   (+ bias)        -- the producer's k-slices in order
 //   xs = x * (1/sqrt(mean(x^2) + 1e-6)) * gamma  -- this tile's rows
-// Every workgroup rebuilds x in LDS (float4 loads, all in flight); after the
-// tile's GEMV, the slice-0 workgroups store x (the residual stream) to x_out
-// and the normed vector to side, each a share of the columns.  Consumer row b
-// reads producer row prow + b of NBP rows.  Needs k % 4 == 0 and k <= KMAX.
-constexpr int RES_MAX_S = 4;   // slices summed per batch of loads
+// Every workgroup rebuilds x in LDS; after the tile's GEMV, the slice-0
+// workgroups store x (the residual stream) to x_out and the normed vector to
+// side, each a share of the columns.  Consumer row b reads producer row
+// prow + b of NBP rows.  Needs k % 4 == 0 and k <= KMAX.  Up to RES_MAX_S
+// producer slices are fetched ahead; more are read in the load stage.
+constexpr int RES_MAX_S = 4;
 
 template <int NB, int KMAX>
 struct ProResidRms {
@@ -208,81 +260,82 @@ struct ProResidRms {
         __shared__ float inv[NB];
         return inv;
     }
-    template <int T>
-    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    template <int T, int KC>
+    struct Fetch {
+        static constexpr int U = (KMAX / 4 + T - 1) / T;   // float4 of a row per thread
+        static constexpr int UG = (KC + T - 1) / T;         // gamma values per thread
+        f32x4 base[NB][U];
+        f32x4 part[NB][RES_MAX_S][U];
+        f32x4 bias[U];
+        uint32_t g[UG];
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
-        __shared__ float scratch[16];
-        constexpr int U = (KMAX / 4 + T - 1) / T;   // float4 per thread
-        constexpr int KCT = 8 * T;                   // KC <= 8T for every tile shape
-        float *xf = xf_lds();
-        const int k4 = k >> 2;
-        float gv[(KCT + T - 1) / T];
+        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
+        const int k4 = k >> 2, t = threadIdx.x;
 #pragma unroll
-        for (int u = 0; u < KCT / T; u++) {
-            const int r = threadIdx.x + u * T;
-            const float g = h2f(gamma[min(k0 + r, k - 1)]);     // clamped, unconditional
-            gv[u] = (r < KC && k0 + r < k) ? g : 0.0f;
-        }
+        for (int u = 0; u < UG; u++) f.g[u] = gamma[min(k0 + t + u * T, k - 1)];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            float4 ps[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int i = min((int)threadIdx.x + u * T, k4 - 1);
-                ps[u] = base ? *(const float4 *)(base + (size_t)b * ldb + 4 * i) : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            if (parts) {
-                float4 acc[U];
-                for (int s0 = 0; s0 < S; s0 += RES_MAX_S) {
-                    float4 pv[RES_MAX_S][U];
+                const int i = min(t + u * T, k4 - 1);
+                if (base) f.base[b][u] = ld4(base + (size_t)b * ldb + 4 * i);
+                if (parts) {
 #pragma unroll
-                    for (int s = 0; s < RES_MAX_S; s++) {
-                        const float *src = parts + ((size_t)min(s0 + s, S - 1) * NBP + prow + b) * npad;
-#pragma unroll
-                        for (int u = 0; u < U; u++)
-                            pv[s][u] = *(const float4 *)(src + 4 * min((int)threadIdx.x + u * T, k4 - 1));
-                    }
-#pragma unroll
-                    for (int u = 0; u < U; u++) {
-                        float4 a = s0 == 0 ? pv[0][u] : acc[u];
-                        if (s0 != 0) { a.x += pv[0][u].x; a.y += pv[0][u].y; a.z += pv[0][u].z; a.w += pv[0][u].w; }
-#pragma unroll
-                        for (int s = 1; s < RES_MAX_S; s++)
-                            if (s0 + s < S) { a.x += pv[s][u].x; a.y += pv[s][u].y; a.z += pv[s][u].z; a.w += pv[s][u].w; }
-                        acc[u] = a;
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < U; u++) {
-                    if (base) { ps[u].x += acc[u].x; ps[u].y += acc[u].y; ps[u].z += acc[u].z; ps[u].w += acc[u].w; }
-                    else ps[u] = acc[u];
+                    for (int s = 0; s < RES_MAX_S; s++)
+                        f.part[b][s][u] = ld4(parts + ((size_t)min(s, S - 1) * NBP + prow + b) * npad + 4 * i);
                 }
             }
+        }
+        if (bias) {
+#pragma unroll
+            for (int u = 0; u < U; u++) f.bias[u] = ld4(bias + 4 * min(t + u * T, k4 - 1));
+        }
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        __shared__ float scratch[16];
+        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
+        float *xf = xf_lds();
+        const int k4 = k >> 2, t = threadIdx.x;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
             float ss = 0.0f;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int i = threadIdx.x + u * T;
+                const int i = t + u * T;
+                f32x4 x = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if (parts) {
+                    f32x4 a = f.part[b][0][u];
+#pragma unroll
+                    for (int s = 1; s < RES_MAX_S; s++)
+                        if (s < S) a += f.part[b][s][u];
+                    for (int s = RES_MAX_S; s < S; s++)
+                        a += ld4(parts + ((size_t)s * NBP + prow + b) * npad + 4 * min(i, k4 - 1));
+                    x = base ? f.base[b][u] + a : a;
+                } else if (base) {
+                    x = f.base[b][u];
+                }
+                if (bias) x += f.bias[u];
                 if (i < k4) {
-                    float4 x = ps[u];
-                    if (bias) {
-                        const float4 bb = *(const float4 *)(bias + 4 * min(i, k4 - 1));
-                        x.x += bb.x; x.y += bb.y; x.z += bb.z; x.w += bb.w;
-                    }
-                    *(float4 *)(xf + b * KMAX + 4 * i) = x;
+                    *(f32x4 *)(xf + b * KMAX + 4 * i) = x;
                     ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
                 }
             }
             ss = block_sum(ss, scratch);
-            if (threadIdx.x == 0) inv_lds()[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
+            if (t == 0) inv_lds()[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
         }
         __syncthreads();
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const float iv = inv_lds()[b];
 #pragma unroll
-            for (int u = 0; u < KCT / T; u++) {
-                const int r = threadIdx.x + u * T;
-                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * gv[u] : 0.0f;
+            for (int u = 0; u < UG; u++) {
+                const int r = t + u * T;
+                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * h2f(f.g[u]) : 0.0f;
             }
         }
     }
@@ -306,13 +359,18 @@ struct ProResidRms {
 
 // silu(gate) * up from gate|up partial sums (talker.rs:343-345).  The fused
 // weight interleaves 32-column groups: gate group j at columns 64j..64j+31,
-// up group j at 64j+32..64j+63.
+// up group j at 64j+32..64j+63.  Used only when gate|up runs in more than one
+// k-slice (the SiLU epilogue covers the single-slice case).
 template <int NB>
 struct ProSwiglu {
     const float *part;
     int S, npad, inter;
-    template <int T>
-    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    template <int T, int KC>
+    struct Fetch {};
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &, int, int) const {}
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &, float *xs, int k0, int ctile) const
     {
         for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
             const int b = i / KC, r = k0 + (i - b * KC);
@@ -334,19 +392,47 @@ struct ProSwiglu {
     __device__ void finish(int s, int c, int nct) const {}
 };
 
+// Raw Q4 element of a reference-layout row: the packed byte and the scale.
+struct Q4Elem {
+    uint32_t byte, scale;
+};
+
+__device__ __forceinline__ Q4Elem q4_row_fetch(const Q4Rows &e, uint32_t row, int col)
+{
+    const int g = col >> 5, j = col & 31;
+    return Q4Elem{e.packed[(size_t)row * e.G * 16 + g * 16 + (j >> 1)], e.scales[(size_t)row * e.G + g]};
+}
+
+__device__ __forceinline__ float q4_elem_value(Q4Elem v, int col)
+{
+    const int q = (int)((col & 1) ? (v.byte >> 4) : (v.byte & 0x0F)) - 8;
+    return h2f(v.scale) * (float)q;
+}
+
 // One dequantised embedding row (embed_lookup_q4, gemv.rs:415-437); the row
 // index is read from device memory.
 struct ProEmbed {
     Q4Rows emb;
     const uint32_t *code;
-    template <int T>
-    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    template <int T, int KC>
+    struct Fetch {
+        Q4Elem e[(KC + T - 1) / T];
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
         const uint32_t row = *code;
-        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
-            const int r = k0 + i;
-            const float v = q4_row_value(emb, row, min(r, emb.n - 1));
-            xs[i] = r < emb.n ? v : 0.0f;
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++)
+            f.e[u] = q4_row_fetch(emb, row, min(k0 + (int)threadIdx.x + u * T, emb.n - 1));
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++) {
+            const int i = threadIdx.x + u * T, r = k0 + i;
+            if (i < KC) xs[i] = r < emb.n ? q4_elem_value(f.e[u], r) : 0.0f;
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -359,15 +445,32 @@ struct ProHidEmbed {
     Q4Rows emb;
     const uint32_t *code;
     int k;
-    template <int T>
-    __device__ void load(float *xs, int k0, int KC, int ctile) const
+    template <int T, int KC>
+    struct Fetch {
+        float h[(KC + T - 1) / T];
+        Q4Elem e[(KC + T - 1) / T];
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
         const uint32_t row = *code;
-        for (int i = threadIdx.x; i < KC; i += blockDim.x) {
-            const int r = k0 + i, rc = min(r, k - 1);
-            const float hv = hidden[rc], ev = q4_row_value(emb, row, rc);
-            xs[i] = r < k ? hv : 0.0f;
-            xs[KC + i] = r < k ? ev : 0.0f;
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++) {
+            const int rc = min(k0 + (int)threadIdx.x + u * T, k - 1);
+            f.h[u] = hidden[rc];
+            f.e[u] = q4_row_fetch(emb, row, rc);
+        }
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++) {
+            const int i = threadIdx.x + u * T, r = k0 + i;
+            if (i < KC) {
+                xs[i] = r < k ? f.h[u] : 0.0f;
+                xs[KC + i] = r < k ? q4_elem_value(f.e[u], r) : 0.0f;
+            }
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -478,7 +581,11 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
         const int s = item / w.CT, c = item - s * w.CT;
         const uint8_t *tile = w.data + (size_t)item * w.tile_bytes;
-        // weight stream first: independent of the prologue
+        // the prologue's loads first, then the weight stream: the prologue's
+        // waits then leave the weights in flight
+        typename Pro::template Fetch<T, KC> pf;
+        pro.template fetch<T, KC>(pf, s * KC, c);
+        asm volatile("" ::: "memory");
         u32x4 q[R];
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -499,7 +606,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
         }
 
         __syncthreads();               // xs / red / ybuf of the previous item are free
-        pro.template load<T>(xs, s * KC, KC, c);
+        pro.template load<T, KC>(pf, xs, s * KC, c);
         __syncthreads();
 
         float acc[NB][32];
@@ -571,6 +678,13 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     }
 }
 
+// A prologue that only supports one workgroup size declares it as
+// `static constexpr int kOnlyT`; other tile shapes are then rejected.
+template <class P, class = void>
+struct OnlyT { static constexpr int v = 0; };
+template <class P>
+struct OnlyT<P, std::void_t<decltype(P::kOnlyT)>> { static constexpr int v = P::kOnlyT; };
+
 template <int NB, class Pro, class Epi>
 static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st)
 {
@@ -578,7 +692,11 @@ static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, 
 #define QTTS_GEMV_CASE(CFG)                                                                     \
     case CFG: {                                                                                 \
         constexpr TileShape ts = tile_shape(CFG);                                               \
-        hipLaunchKernelGGL((k_gemv<ts.T, ts.GB, ts.R, NB, Pro, Epi>), dim3(grid), dim3(ts.T), 0, st, w, pro, epi); \
+        if constexpr (OnlyT<Pro>::v == 0 || OnlyT<Pro>::v == ts.T) {                            \
+            hipLaunchKernelGGL((k_gemv<ts.T, ts.GB, ts.R, NB, Pro, Epi>), dim3(grid), dim3(ts.T), 0, st, w, pro, epi); \
+        } else {                                                                                \
+            return hipErrorInvalidValue;                                                        \
+        }                                                                                       \
         break;                                                                                  \
     }
     switch (w.cfg) {
@@ -903,6 +1021,195 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
         }
     }
 }
+
+// Predictor o-proj prologue with the attention fused in (code_predictor.rs:
+// 369-414, 457-498).  The workgroup owning o-proj input rows k0..k0+511
+// (query heads 4s..4s+3, kv heads 2s, 2s+1) rebuilds those heads' q, k, v
+// from the qkv partial sums (QK-norm, RoPE at pos0 + b), attends over the
+// cached positions plus the new ones (causal among the NB new rows) and
+// leaves the normalised attention output in xs.  Column tile 0 appends the
+// new K (normed, roped) and V (raw) to the cache; no workgroup of the same
+// launch reads those entries back from memory, so there is no race.
+// Needs T == 256 (one wave per query head of the slice), KC == 512 and at
+// most RES_MAX_S qkv k-slices.
+template <int NB>
+struct ProPredAttn {
+    static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
+    static constexpr int HPW = 2;        // kv heads per workgroup
+    static constexpr int NC4 = HPW * PRED_KV_CAP * (HEAD_DIM / 4) / 256;   // cached float4 per thread
+    const float *part;       // qkv partial sums [S][NB][npad]
+    int S, npad;
+    const uint16_t *qn_g, *kn_g;
+    const float *rope_cos, *rope_sin;
+    int pos0;                // position of row 0
+    float *Kc, *Vc;          // this layer's cache [PRED_KV_CAP][8][HEAD_DIM]
+
+    template <int T, int KC>
+    struct Fetch {
+        float q[NB][HPW][RES_MAX_S], kv[NB][HPW][RES_MAX_S];
+        uint32_t gq, gk;
+        float cs[NB], sn[NB];
+        f32x4 kc[NC4], vc[NC4];
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        const int t = threadIdx.x, d = t & 127, sel = t >> 7;
+        const int h0 = k0 / (2 * HEAD_DIM);
+        const size_t kvrow = 8 * HEAD_DIM;
+        const int plast = pos0 > 0 ? pos0 - 1 : 0;
+        // cached positions 0..pos0-1 of both kv heads: float4 i -> (head j, position p, dims 4*d4..)
+#pragma unroll
+        for (int u = 0; u < NC4; u++) {
+            const int i = t + u * 256, j = i >> 9, p = (i >> 5) & 15, d4 = i & 31;
+            const size_t off = (size_t)min(p, plast) * kvrow + (size_t)(h0 + j) * HEAD_DIM + d4 * 4;
+            f.kc[u] = ld4(Kc + off);
+            f.vc[u] = ld4(Vc + off);
+        }
+        // this thread's q (head 2(h0+j)+sel) and k (sel 0) / v (sel 1) slices
+#pragma unroll
+        for (int s = 0; s < RES_MAX_S; s++) {
+            const int sc = min(s, S - 1);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                const float *pp = part + ((size_t)sc * NB + b) * npad;
+#pragma unroll
+                for (int j = 0; j < HPW; j++) {
+                    f.q[b][j][s] = pp[(2 * (h0 + j) + sel) * HEAD_DIM + d];
+                    f.kv[b][j][s] = pp[16 * HEAD_DIM + sel * 8 * HEAD_DIM + (h0 + j) * HEAD_DIM + d];
+                }
+            }
+        }
+        f.gq = qn_g[d];
+        f.gk = kn_g[d];
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            f.cs[b] = rope_cos[(size_t)(pos0 + b) * 64 + (d & 63)];
+            f.sn[b] = rope_sin[(size_t)(pos0 + b) * 64 + (d & 63)];
+        }
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        __shared__ float Ks[HPW * PRED_KV_CAP * HEAD_DIM], Vs[HPW * PRED_KV_CAP * HEAD_DIM];
+        __shared__ float qn[NB * HPW * 2 * HEAD_DIM], qr[NB * HPW * 2 * HEAD_DIM], kn[NB * HPW * HEAD_DIM];
+        __shared__ float ssq[NB * HPW * 4 * 2];
+        const int t = threadIdx.x, d = t & 127, sel = t >> 7, lane = t & 63, wv = t >> 6;
+        const int h0 = k0 / (2 * HEAD_DIM);
+        const size_t kvrow = 8 * HEAD_DIM;
+        // k-slice sums in slice order; cached K/V into LDS; sums of squares
+        float qv[NB][HPW], kv[NB][HPW];
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < HPW; j++) {
+                float a = f.q[b][j][0], c = f.kv[b][j][0];
+#pragma unroll
+                for (int s = 1; s < RES_MAX_S; s++) {
+                    a = s < S ? a + f.q[b][j][s] : a;
+                    c = s < S ? c + f.kv[b][j][s] : c;
+                }
+                qv[b][j] = a;
+                kv[b][j] = c;
+            }
+#pragma unroll
+        for (int u = 0; u < NC4; u++) {
+            const int i = t + u * 256, j = i >> 9, p = (i >> 5) & 15, d4 = i & 31;
+            if (p < pos0) {
+                *(f32x4 *)(Ks + (j * PRED_KV_CAP + p) * HEAD_DIM + d4 * 4) = f.kc[u];
+                *(f32x4 *)(Vs + (j * PRED_KV_CAP + p) * HEAD_DIM + d4 * 4) = f.vc[u];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < HPW; j++) {
+                const float q2 = wave_sum_dpp(qv[b][j] * qv[b][j]);
+                const float k2 = wave_sum_dpp(kv[b][j] * kv[b][j]);
+                if (lane == 0) {
+                    ssq[((b * HPW + j) * 4 + wv) * 2] = q2;
+                    ssq[((b * HPW + j) * 4 + wv) * 2 + 1] = k2;
+                }
+            }
+        __syncthreads();
+        // QK-norm (talker.rs:89-99; code_predictor.rs:84-93); V raw into LDS
+        const float gq = h2f(f.gq), gk = h2f(f.gk);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int j = 0; j < HPW; j++) {
+                const float *sp = ssq + (b * HPW + j) * 8;
+                const float sq = sp[(2 * sel) * 2] + sp[(2 * sel + 1) * 2];
+                const float sk = sp[1] + sp[3];
+                qn[((b * HPW + j) * 2 + sel) * HEAD_DIM + d] = qv[b][j] * (1.0f / sqrtf(sq / 128.0f + 1e-6f)) * gq;
+                if (!sel)
+                    kn[(b * HPW + j) * HEAD_DIM + d] = kv[b][j] * (1.0f / sqrtf(sk / 128.0f + 1e-6f)) * gk;
+                else
+                    Vs[(j * PRED_KV_CAP + pos0 + b) * HEAD_DIM + d] = kv[b][j];
+            }
+        __syncthreads();
+        // rotate-half RoPE (rope.rs:79-92) into separate buffers; the new K / V
+        // of column tile 0 also go to the cache
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float cs = f.cs[b], sn = f.sn[b];
+#pragma unroll
+            for (int j = 0; j < HPW; j++) {
+                const float *qb = qn + ((b * HPW + j) * 2 + sel) * HEAD_DIM;
+                qr[((b * HPW + j) * 2 + sel) * HEAD_DIM + d] =
+                    d < 64 ? qb[d] * cs - qb[d + 64] * sn : qb[d] * cs + qb[d - 64] * sn;
+                const size_t cache = (size_t)(pos0 + b) * kvrow + (size_t)(h0 + j) * HEAD_DIM + d;
+                if (!sel) {
+                    const float *kb = kn + (b * HPW + j) * HEAD_DIM;
+                    const float kr = d < 64 ? kb[d] * cs - kb[d + 64] * sn : kb[d] * cs + kb[d - 64] * sn;
+                    Ks[(j * PRED_KV_CAP + pos0 + b) * HEAD_DIM + d] = kr;
+                    if (ctile == 0) Kc[cache] = kr;
+                } else if (ctile == 0) {
+                    Vc[cache] = kv[b][j];
+                }
+            }
+        }
+        __syncthreads();
+        // wave w = query head 4s + w (kv head h0 + w/2): lane -> position
+        // p = lane/4 and a quarter of the head dims; softmax_raw
+        // (gemv.rs:471-482) over the positions 0..len-1
+        const int jw = wv >> 1, sw = wv & 1, p = lane >> 2, q4i = lane & 3;
+        const float scale = 1.0f / sqrtf(128.0f);
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int len = pos0 + b + 1;
+            const float *qrow = qr + ((b * HPW + jw) * 2 + sw) * HEAD_DIM + q4i * 32;
+            const float *krow = Ks + (jw * PRED_KV_CAP + p) * HEAD_DIM + q4i * 32;
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                const f32x4 a = *(const f32x4 *)(qrow + i), c = *(const f32x4 *)(krow + i);
+                dot = fmaf(a.x, c.x, dot);
+                dot = fmaf(a.y, c.y, dot);
+                dot = fmaf(a.z, c.z, dot);
+                dot = fmaf(a.w, c.w, dot);
+            }
+            dot += dpp_mov<0xB1>(dot);
+            dot += dpp_mov<0x4E>(dot);
+            const float sc = p < len ? dot * scale : -INFINITY;
+            const float m = wave_max_dpp(sc);
+            const float e = p < len ? expf(sc - m) : 0.0f;
+            const float prob = e * (1.0f / wave_sum_dpp(q4i == 0 ? e : 0.0f));
+            float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+            for (int pp = 0; pp < PRED_KV_CAP; pp++) {
+                const float w = lane_value(prob, 4 * pp);
+                const float *vrow = Vs + (jw * PRED_KV_CAP + pp) * HEAD_DIM;
+                const float v0 = vrow[lane], v1 = vrow[lane + 64];
+                o0 = pp < len ? fmaf(w, v0, o0) : o0;
+                o1 = pp < len ? fmaf(w, v1, o1) : o1;
+            }
+            xs[b * KC + wv * HEAD_DIM + lane] = o0;
+            xs[b * KC + wv * HEAD_DIM + lane + 64] = o1;
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const {}
+};
 
 // ---------------------------------------------------------------------------
 // argmax over the lm-head logits (sample_argmax, code_predictor.rs:335-341):
@@ -1459,6 +1766,18 @@ hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const flo
 // One predictor layer over NB tokens at positions pos0.. (code_predictor.rs:
 // 354-432 for NB=2, 450-510 for NB=1).  Layer 0 starts from the input
 // projection partials + bias.
+template <int NB, class Pro>
+static hipError_t launch_gemv_then_mlp(const PredictorDev &p, const LayerDev &L, const Workspace &ws,
+                                       const Pro &pro, hipStream_t s);
+
+// The fused attention prologue covers 2 kv heads per workgroup of 256
+// threads: o-proj tiles of 256 threads and 512 rows, 16 / 8 heads of 128.
+static bool pred_attn_fusable(const PredictorDev &p, const LayerDev &L)
+{
+    return tile_shape(L.o.cfg).T == 256 && L.o.KC == 512 && p.n_heads == 16 && p.n_kv_heads == 8 &&
+           L.qkv.npad >= 32 * HEAD_DIM && L.qkv.S <= RES_MAX_S;
+}
+
 template <int NB>
 static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
 {
@@ -1470,13 +1789,27 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
                : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
                                  p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
     QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
+    float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+    float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+    if (pred_attn_fusable(p, L)) {
+        // attention inside the o-proj prologue
+        const ProPredAttn<NB> pro{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
+                                  pos0, Kc, Vc};
+        return launch_gemv_then_mlp<NB>(p, L, ws, pro, s);
+    }
     hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, NB, L.qkv.npad,
-                       L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
-                       ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM,
-                       ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM, ws.pattn);
+                       L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0, Kc, Vc, ws.pattn);
     QCHK(hipGetLastError());
     const int qd = p.n_heads * HEAD_DIM;
-    QCHK(launch_gemv<NB>(L.o, ProPlain<NB>{ws.pattn, qd, qd}, EpiPart<NB>{ws.part_o, L.o.npad}, s));
+    return launch_gemv_then_mlp<NB>(p, L, ws, ProPlain<NB>{ws.pattn, qd, qd}, s);
+}
+
+template <int NB, class Pro>
+static hipError_t launch_gemv_then_mlp(const PredictorDev &p, const LayerDev &L, const Workspace &ws,
+                                       const Pro &pro, hipStream_t s)
+{
+    const int h = p.hidden;
+    QCHK(launch_gemv<NB>(L.o, pro, EpiPart<NB>{ws.part_o, L.o.npad}, s));
     const ProResidRms<NB, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
     return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s);
 }
@@ -1569,6 +1902,30 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
 
 // Timing helpers: the gate|up GEMV of layer l with its real prologue, and the
 // decode attention of layer l over `len` positions.
+// Predictor timing: attention + o-proj of layer l for one row at position
+// pos0 (the path pred_layer takes), or the whole layer step.
+hipError_t enqueue_pred_attn_o_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
+{
+    const LayerDev &L = p.layers[l];
+    float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+    float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+    if (pred_attn_fusable(p, L)) {
+        const ProPredAttn<1> pro{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
+                                 pos0, Kc, Vc};
+        return launch_gemv<1>(L.o, pro, EpiPart<1>{ws.part_o, L.o.npad}, s);
+    }
+    hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, 1, L.qkv.npad,
+                       L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0, Kc, Vc, ws.pattn);
+    QCHK(hipGetLastError());
+    const int qd = p.n_heads * HEAD_DIM;
+    return launch_gemv<1>(L.o, ProPlain<1>{ws.pattn, qd, qd}, EpiPart<1>{ws.part_o, L.o.npad}, s);
+}
+
+hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
+{
+    return pred_layer<1>(p, ws, l, pos0, s);
+}
+
 // Plain 16-byte-per-lane copy, 8 loads per thread in flight; n % 4 == 0.
 __global__ void __launch_bounds__(256) k_copy_f4(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, int64_t n4)
 {

@@ -1170,6 +1170,20 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
                              [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->stream); },
                              avg_us);
     }
+    if (kind == 3 || kind == 4) {
+        // predictor, one row at position 8 (a mid-chain step), cycling the layers
+        const PredictorDev &p = c->pm;
+        const LayerDev &L = p.layers[0];
+        const double w = kind == 3 ? (double)L.o.k * L.o.n * 0.5625
+                                   : (double)(L.qkv.k * L.qkv.n + L.o.k * L.o.n + L.gate_up.k * L.gate_up.n +
+                                              L.down.k * L.down.n) * 0.5625;
+        *bytes = w + 9.0 * 8 * HEAD_DIM * 4 * 2;
+        if (kind == 3)
+            return time_launches(c, iters, [&](int i) { return enqueue_pred_attn_o_timing(p, c->ws, i % p.n_layers, 8, c->stream); },
+                                 avg_us);
+        return time_launches(c, iters, [&](int i) { return enqueue_pred_layer_timing(p, c->ws, i % p.n_layers, 8, c->stream); },
+                             avg_us);
+    }
     return QTTS_ERR_INVALID;
 }
 
