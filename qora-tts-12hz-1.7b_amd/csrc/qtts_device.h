@@ -9,8 +9,10 @@ namespace qtts {
 // Tiling of one Q4 weight for the split-K GEMV (see qtts_kernels.hip).
 // A tile covers GB 32-column groups x KC rows, KC = R * T / GB, and is
 // stored contiguously: nibble block [R][T] x 16 B, then scale block [T] x
-// R f16 (R = 2, 4 or 8 rows per thread).  Thread t of a workgroup owns group (t % GB) and rows
-// r * (T/GB) + t / GB, r = 0..R-1, of the tile.  A weight with
+// R f16 (R = 2, 4 or 8 rows per thread).  Thread t of a workgroup owns one
+// group gl and rows r * (T/GB) + ph, r = 0..R-1, of the tile: with NW = T/64
+// waves, gl = (t/64) % GB and ph = (t/64)/GB * 64 + t % 64 when NW % GB == 0
+// (one group per wave), else gl = t % GB and ph = t / GB.  A weight with
 // S = ceil(k / KC) k-slices writes S partial sums per output; S = 1 is a
 // full-k pass.
 enum TileCfg : int32_t {

@@ -521,16 +521,62 @@ struct EpiSwiglu {
 // ---------------------------------------------------------------------------
 // The split-K Q4 GEMV.
 //
-// Thread t of a T-thread workgroup owns 32-column group gl = t % GB of the
-// tile and rows r*P + ph (P = T/GB, ph = t/GB, r < R) of its k-slice.  Per
-// row it loads one 16-byte block of 32 nibbles and computes
+// Thread t of a T-thread workgroup owns one 32-column group gl of the tile
+// and rows r*P + ph (P = T/GB, r < R) of its k-slice.  When the number of
+// waves NW is a multiple of GB, whole waves share a group: wave w holds group
+// w % GB and ph = (w / GB) * 64 + lane; otherwise gl = t % GB, ph = t / GB.
+// Per row a thread loads one 16-byte block of 32 nibbles and computes
 //     acc[j] += a * nib_j,   a = f32(scale) * x[row]
 // with nibbles split into two byte lanes (& 0x0F0F0F0F for even columns,
 // & 0xF0F0F0F0 for odd ones, the latter scaled by a/16), so each output
 // costs one byte->float convert and one FMA; the -8 offset is applied once
-// as acc[j] -= 8 * sum(a).  Lanes sharing a group are folded by a
-// butterfly reduce-scatter, waves through LDS, in fixed order.
+// as acc[j] -= 8 * sum(a).  The lanes of a group are folded by a
+// reduce-scatter (DPP lane exchanges in the one-group-per-wave layout),
+// the waves through LDS, in fixed order.
 // ---------------------------------------------------------------------------
+
+// One halving step of the in-wave reduce-scatter: the lane keeps half H of
+// its values (the upper half when `sel`) and adds the partner lane's copy
+// of that half; CTRL is the DPP lane exchange with the partner.
+template <int H, int CTRL, int NB>
+__device__ __forceinline__ void rs_dpp_step(float (&v)[NB][32], bool sel)
+{
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int j = 0; j < H; j++) {
+            const float send = sel ? v[b][j] : v[b][j + H];
+            const float keep = sel ? v[b][j + H] : v[b][j];
+            v[b][j] = keep + dpp_mov<CTRL>(send);
+        }
+}
+
+// Reduce-scatter of 32 column sums held by all 64 lanes of a wave.  Partner
+// masks in order: lane^15 (row_mirror), ^7 (row_half_mirror), ^3 and ^1
+// (quad permutes), ^16 (swizzle), then ^32 adds the last value; each mask
+// leaves the bits chosen by earlier steps unchanged, so partners always hold
+// the same columns.  Lanes l and l^32 end with column wave_rs_col(l).
+template <int NB>
+__device__ __forceinline__ void wave_rs32(float (&v)[NB][32], int lane)
+{
+    rs_dpp_step<16, 0x140, NB>(v, lane & 8);
+    rs_dpp_step<8, 0x141, NB>(v, lane & 4);
+    rs_dpp_step<4, 0x1B, NB>(v, lane & 2);
+    rs_dpp_step<2, 0xB1, NB>(v, lane & 1);
+    const bool s16 = lane & 16;
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const float send = s16 ? v[b][0] : v[b][1];
+        const float keep = s16 ? v[b][1] : v[b][0];
+        v[b][0] = keep + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
+        v[b][0] += __shfl_xor(v[b][0], 32);
+    }
+}
+
+__device__ __forceinline__ int wave_rs_col(int lane)
+{
+    return ((lane >> 3) & 1) * 16 + ((lane >> 2) & 1) * 8 + ((lane >> 1) & 1) * 4 + (lane & 1) * 2 + ((lane >> 4) & 1);
+}
 
 template <int M, int CNT, int NB>
 __device__ __forceinline__ void rs_steps(float (&v)[NB][32], int lane, int &base)
@@ -573,9 +619,11 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     __shared__ float red[NW * NB * C];
     __shared__ float ybuf[NB * C];
 
+    constexpr bool WAVE_GROUPS = NW % GB == 0;   // one group per wave
     const int t = threadIdx.x;
     const int lane = t & 63, wv = t >> 6;
-    const int gl = t % GB, ph = t / GB;
+    const int gl = WAVE_GROUPS ? wv % GB : t % GB;
+    const int ph = WAVE_GROUPS ? (wv / GB) * 64 + lane : t / GB;
     const int items = w.S * w.CT;
 
     for (int item = blockIdx.x; item < items; item += gridDim.x) {
@@ -652,22 +700,39 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             for (int j = 0; j < 32; j++) acc[b][j] += off;
         }
 
-        int base = 0;
-        rs_steps<GB, 32, NB>(acc, lane, base);
-        if ((lane & DUP) == 0) {
+        if constexpr (WAVE_GROUPS) {
+            wave_rs32<NB>(acc, lane);
+            if (lane < 32) {
+                const int col = wave_rs_col(lane);
 #pragma unroll
-            for (int b = 0; b < NB; b++)
+                for (int b = 0; b < NB; b++) red[(wv * NB + b) * 32 + col] = acc[b][0];
+            }
+            __syncthreads();
+            for (int col = t; col < NB * C; col += T) {
+                const int b = col / C, cc = col - b * C, g = cc >> 5;
+                float y = 0.0f;
 #pragma unroll
-                for (int i = 0; i < CNTF; i++)
-                    red[(wv * NB + b) * C + gl * 32 + base + i] = acc[b][i];
-        }
-        __syncthreads();
-        for (int col = t; col < NB * C; col += T) {
-            const int b = col / C, cc = col - b * C;
-            float y = 0.0f;
+                for (int i = 0; i < NW / GB; i++) y += red[((i * GB + g) * NB + b) * 32 + (cc & 31)];
+                ybuf[col] = y;
+            }
+        } else {
+            int base = 0;
+            rs_steps<GB, 32, NB>(acc, lane, base);
+            if ((lane & DUP) == 0) {
 #pragma unroll
-            for (int i = 0; i < NW; i++) y += red[(i * NB + b) * C + cc];
-            ybuf[col] = y;
+                for (int b = 0; b < NB; b++)
+#pragma unroll
+                    for (int i = 0; i < CNTF; i++)
+                        red[(wv * NB + b) * C + gl * 32 + base + i] = acc[b][i];
+            }
+            __syncthreads();
+            for (int col = t; col < NB * C; col += T) {
+                const int b = col / C, cc = col - b * C;
+                float y = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NW; i++) y += red[(i * NB + b) * C + cc];
+                ybuf[col] = y;
+            }
         }
         __syncthreads();
         for (int col = t; col < NB * C; col += T) {

@@ -178,8 +178,13 @@ static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vect
             const int64_t s = item / CT, ct = item % CT;
             uint8_t *tile = host.data() + item * tile_bytes;
             uint16_t *scl = (uint16_t *)(tile + (size_t)ts.R * ts.T * 16);
+            // thread t -> (group, row offset): one group per wave when the
+            // wave count is a multiple of GB, else interleaved by thread
+            const bool wave_groups = (ts.T / 64) % ts.GB == 0;
             for (int t = 0; t < ts.T; t++) {
-                const int64_t g = ct * ts.GB + t % ts.GB;
+                const int gt = wave_groups ? (t / 64) % ts.GB : t % ts.GB;
+                const int pt = wave_groups ? (t / 64) / ts.GB * 64 + t % 64 : t / ts.GB;
+                const int64_t g = ct * ts.GB + gt;
                 int si = -1;
                 int64_t lg = 0;
                 if (g < Gt) {
@@ -192,7 +197,7 @@ static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vect
                     }
                 }
                 for (int r = 0; r < ts.R; r++) {
-                    const int64_t row = s * KC + (int64_t)r * P + t / ts.GB;
+                    const int64_t row = s * KC + (int64_t)r * P + pt;
                     uint8_t *dst = tile + ((size_t)r * ts.T + t) * 16;
                     uint16_t sc = 0;
                     if (si >= 0 && row < k) {
