@@ -77,6 +77,7 @@ struct DevState {
     uint32_t prev[16];       // repetition-penalty history
     uint32_t used[16];       // codes fed downstream this frame
     uint32_t pred[16];       // codes predicted this frame
+    uint32_t fcode[16];      // teacher-forced codes of this frame (force on)
     int32_t stop;            // 1 after EOS: frame kernels become no-ops
     int32_t eos;             // sticky EOS flag
     int32_t nan_flag;        // a sampler met a NaN

@@ -8,6 +8,7 @@ namespace qtts {
 
 constexpr int MAX_CHUNKS = 128;          // KV pages per sequence (8192 positions)
 constexpr int RING_FRAMES = 64;          // frames per host synchronisation, max
+constexpr int MAX_CAND = 64;             // lm-head column tiles reduced by one wave
 
 struct KvPaged {
     float *base;           // [layers][n_phys][2 (K,V)][8 heads][64 pos][128]
@@ -65,6 +66,7 @@ struct Workspace {
     float *text;       // trailing text rows [n][hidden]
     float *pad;        // tts_pad row [hidden]
     uint32_t *ring_pred, *ring_used;      // [RING_FRAMES][16]
+    float2 *cand;      // lm-head argmax candidates [16 heads][MAX_CAND] (value, index bits)
     int attn_grid;
 };
 

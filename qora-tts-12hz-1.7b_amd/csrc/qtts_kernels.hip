@@ -166,6 +166,55 @@ __device__ __forceinline__ float wave_max_dpp(float v)
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+
+// (v, i) pairs: the larger value wins, equal values go to the larger index
+// (the last maximum, as Iterator::max_by in code_predictor.rs:335-341).
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float ov, int oi)
+{
+    if (ov > v || (ov == v && oi > i)) { v = ov; i = oi; }
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp_step(float &v, int &i)
+{
+    const float ov = dpp_mov<CTRL>(v);
+    const int oi = dpp_mov_i<CTRL>(i);
+    argmax_merge(v, i, ov, oi);
+}
+
+// Wave-wide argmax of one (value, index) per lane; uniform result.
+__device__ __forceinline__ void wave_argmax_last(float &v, int &i)
+{
+    argmax_dpp_step<0xB1>(v, i);
+    argmax_dpp_step<0x4E>(v, i);
+    argmax_dpp_step<0x141>(v, i);
+    argmax_dpp_step<0x140>(v, i);
+    float bv = lane_value(v, 0);
+    int bi = __builtin_amdgcn_readlane(i, 0);
+#pragma unroll
+    for (int r = 16; r < 64; r += 16) argmax_merge(bv, bi, lane_value(v, r), __builtin_amdgcn_readlane(i, r));
+    v = bv;
+    i = bi;
+}
+
+// Code chosen from the per-tile argmax candidates of one lm head (one per
+// lane, ncand <= 64): the last maximum; any NaN tile -> code 0 and nan.
+__device__ __forceinline__ uint32_t cand_argmax(const float2 *cand, int ncand, bool &nan)
+{
+    const int lane = threadIdx.x & 63;
+    const float2 cv = cand[min(lane, ncand - 1)];
+    float v = lane < ncand ? cv.x : -INFINITY;
+    int i = lane < ncand ? __builtin_bit_cast(int, cv.y) : -2;
+    nan = __ballot(i == -1) != 0;
+    wave_argmax_last(v, i);
+    return (nan || i < 0) ? 0u : (uint32_t)i;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV prologues.  A prologue fills xs[b*KC + i] with input row b, rows
 // k0 + i, in two stages:
@@ -438,6 +487,53 @@ struct ProEmbed {
     __device__ void finish(int s, int c, int nct) const {}
 };
 
+// Predictor step input: the previous head's code chosen from its argmax
+// candidates (code_predictor.rs:253-260; the teacher-forced code when forcing),
+// then that code's embedding row.  The wave argmax runs in every wave, so
+// the row loads need no barrier; workgroup (0, 0) records the code.
+struct ProArgmaxEmbed {
+    Q4Rows emb;
+    const float2 *cand;
+    int ncand;
+    DevState *st;
+    int slot;
+    uint32_t *codes_api;
+    template <int T, int KC>
+    struct Fetch {
+        Q4Elem e[(KC + T - 1) / T];
+        uint32_t pred, used;
+        bool nan;
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        const int force = st->force;
+        const uint32_t fc = st->fcode[slot];
+        f.pred = cand_argmax(cand, ncand, f.nan);
+        f.used = force ? fc : f.pred;
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++)
+            f.e[u] = q4_row_fetch(emb, f.used, min(k0 + (int)threadIdx.x + u * T, emb.n - 1));
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+#pragma unroll
+        for (int u = 0; u < (KC + T - 1) / T; u++) {
+            const int i = threadIdx.x + u * T, r = k0 + i;
+            if (i < KC) xs[i] = r < emb.n ? q4_elem_value(f.e[u], r) : 0.0f;
+        }
+        if (k0 == 0 && ctile == 0 && threadIdx.x == 0) {
+            st->pred[slot] = f.pred;
+            st->used[slot] = f.used;
+            st->prev[slot] = f.used;
+            if (f.nan) st->nan_flag = 1;
+            if (codes_api) codes_api[slot - 1] = f.pred;
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const {}
+};
+
 // Predictor prefill input: row 0 = talker hidden, row 1 = codec embedding
 // of the semantic code (code_predictor.rs:235-241, generate_new.rs:620).
 struct ProHidEmbed {
@@ -515,6 +611,26 @@ struct EpiSwiglu {
             const int j = (c * C + cc) >> 6;
             h[(size_t)b * ld + j * 32 + (cc & 31)] = silu_f(yb[cc]) * yb[cc + 32];
         }
+    }
+};
+
+// Single-slice lm head: the tile's argmax candidate (value, index) with the
+// last maximum among its columns below n; index -1 marks a NaN in the tile.
+struct EpiArgmax {
+    float2 *cand;
+    int n;
+    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    {
+        if (cc != 0) return;
+        float best = -INFINITY;
+        int bi = -1;
+        bool nan = false;
+        for (int j = 0; j < C && c * C + j < n; j++) {
+            const float v = yb[j];
+            nan |= isnan(v);
+            if (bi < 0 || v >= best) { best = v; bi = c * C + j; }
+        }
+        cand[c] = make_float2(best, __builtin_bit_cast(float, nan ? -1 : bi));
     }
 };
 
@@ -1331,10 +1447,24 @@ k_argmax(const float *part, int S, int npad, int n, DevState *st, int slot,
 // ---------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(256)
-k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, const DevState *st, const float *text,
-          const float *pad, float *x, int H)
+k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, DevState *st, const float *text,
+          const float *pad, float *x, int H, const float2 *cand_last, int ncand)
 {
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    // the last code straight from the last head's argmax candidates (every
+    // wave chooses it; workgroup 0 records it)
+    uint32_t last = 0;
+    if (cand_last) {
+        bool nan;
+        const uint32_t pred = cand_argmax(cand_last, ncand, nan);
+        last = st->force ? st->fcode[n_groups] : pred;
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            st->pred[n_groups] = pred;
+            st->used[n_groups] = last;
+            st->prev[n_groups] = last;
+            if (nan) st->nan_flag = 1;
+        }
+    }
     if (j >= H) return;
     const float sem = q4_row_value(tcodec, st->used[0], j);
     float sum = 0.0f;
@@ -1342,13 +1472,31 @@ k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, const DevState *st, const f
         Q4Rows e = cpemb;
         e.packed += (size_t)g * e.rows * e.G * 16;
         e.scales += (size_t)g * e.rows * e.G;
-        sum += q4_row_value(e, st->used[g + 1], j);
+        const uint32_t code = (cand_last && g == n_groups - 1) ? last : st->used[g + 1];
+        sum += q4_row_value(e, code, j);
     }
     float v = sem + sum;
     const int f = st->frame_idx;
     const float *tr = (f < st->n_text) ? text + (size_t)f * H : pad;
     v += tr[j];
     x[j] = v;
+}
+
+// The code of `slot` from an lm head's argmax candidates (API calls, where
+// no frame combine follows the chain).
+__global__ void __launch_bounds__(64)
+k_cand_final(const float2 *cand, int ncand, DevState *st, int slot, uint32_t *codes_api)
+{
+    bool nan;
+    const uint32_t pred = cand_argmax(cand, ncand, nan);
+    if (threadIdx.x == 0) {
+        const uint32_t used = st->force ? st->fcode[slot] : pred;
+        st->pred[slot] = pred;
+        st->used[slot] = used;
+        st->prev[slot] = used;
+        if (nan) st->nan_flag = 1;
+        if (codes_api) codes_api[slot - 1] = pred;
+    }
 }
 
 // code_predictor.rs:287-300 for the operator-level API.
@@ -1615,7 +1763,12 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
             st->rng = rs;
             st->pred[0] = res;
             uint32_t used = res;
-            if (st->force && forced) used = forced[(size_t)(st->frame_idx - st->forced_base) * 16];
+            if (st->force && forced) {
+                // this frame's forced codes, staged for the predictor chain
+                const uint32_t *fr = forced + (size_t)(st->frame_idx - st->forced_base) * 16;
+                for (int i = 0; i < 16; i++) st->fcode[i] = fr[i];
+                used = fr[0];
+            }
             st->used[0] = used;
             st->prev[0] = used;
             if (st->eos_enabled && !st->force && res == st->eos_id) { st->stop = 1; st->eos = 1; }
@@ -1879,6 +2032,10 @@ static hipError_t launch_gemv_then_mlp(const PredictorDev &p, const LayerDev &L,
     return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s);
 }
 
+// A single-slice lm head whose column tiles fit one wave writes per-tile
+// argmax candidates; the consumer of the code chooses among them.
+static bool head_cand(const PredictorDev &p, int g) { return p.heads[g].S == 1 && p.heads[g].CT <= MAX_CAND; }
+
 // final norm of row `row` of the last layer's output + lm_head[g] + argmax
 static hipError_t pred_head(const PredictorDev &p, const Workspace &ws, DevState *st, int g, int NBP, int row,
                             const uint32_t *forced, uint32_t *codes_api, hipStream_t s)
@@ -1886,6 +2043,7 @@ static hipError_t pred_head(const PredictorDev &p, const Workspace &ws, DevState
     const LayerDev &P = p.layers[p.n_layers - 1];
     const ProResidRms<1, 1024> pre{ws.pxa + (size_t)row * p.hidden, p.hidden, ws.part_down, P.down.S, NBP, row,
                              P.down.npad, nullptr, p.final_norm, p.hidden, nullptr, nullptr};
+    if (head_cand(p, g)) return launch_gemv<1>(p.heads[g], pre, EpiArgmax{ws.cand + g * MAX_CAND, p.vocab}, s);
     QCHK(launch_gemv<1>(p.heads[g], pre, EpiPart<1>{ws.part_head, p.heads[g].npad}, s));
     hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, ws.part_head, p.heads[g].S, p.heads[g].npad, p.vocab,
                        st, g + 1, forced, codes_api);
@@ -1916,9 +2074,20 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
         Q4Rows e = p.emb_rows;
         e.packed += (size_t)(g - 1) * e.rows * e.G * 16;
         e.scales += (size_t)(g - 1) * e.rows * e.G;
-        QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_proj, p.proj.npad}, s));
+        if (head_cand(p, g - 1))
+            QCHK(launch_gemv<1>(p.proj, ProArgmaxEmbed{e, ws.cand + (g - 1) * MAX_CAND, p.heads[g - 1].CT, st, g, codes_api},
+                                EpiPart<1>{ws.part_proj, p.proj.npad}, s));
+        else
+            QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_proj, p.proj.npad}, s));
         for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
         QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
+    }
+    // API calls resolve the last code here; a frame's combine does it itself
+    const int gl = p.n_groups - 1;
+    if (sem && head_cand(p, gl)) {
+        hipLaunchKernelGGL(k_cand_final, dim3(1), dim3(64), 0, s, ws.cand + gl * MAX_CAND, p.heads[gl].CT, st,
+                           p.n_groups, codes_api);
+        QCHK(hipGetLastError());
     }
     return hipSuccess;
 }
@@ -1933,8 +2102,11 @@ hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Worksp
                        (uint64_t *)nullptr, (uint32_t *)nullptr, forced);
     QCHK(hipGetLastError());
     QCHK(enqueue_predictor_chain(p, m, ws, st, ws.hidden, nullptr, forced, nullptr, s));
+    const int gl = p.n_groups - 1;
     hipLaunchKernelGGL(k_combine, dim3((m.hidden + 255) / 256), dim3(256), 0, s, m.codec_rows,
-                       p.emb_rows, p.n_groups, st, ws.text, ws.pad, ws.x, m.hidden);
+                       p.emb_rows, p.n_groups, st, ws.text, ws.pad, ws.x, m.hidden,
+                       head_cand(p, gl) ? (const float2 *)(ws.cand + gl * MAX_CAND) : (const float2 *)nullptr,
+                       p.heads[gl].CT);
     QCHK(hipGetLastError());
     return enqueue_talker_step(m, ws, st, 1, s);
 }

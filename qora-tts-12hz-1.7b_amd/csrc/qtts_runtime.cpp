@@ -563,6 +563,7 @@ static int alloc_workspace(qtts_ctx *c)
     RCHK(dev_alloc(c, A, &w.pad, H));
     RCHK(dev_alloc(c, A, &w.ring_pred, RING_FRAMES * 16));
     RCHK(dev_alloc(c, A, &w.ring_used, RING_FRAMES * 16));
+    RCHK(dev_alloc(c, A, &w.cand, 16 * MAX_CAND));
     c->text_cap = 256;
     RCHK(dev_alloc(c, A, &w.text, (size_t)c->text_cap * H));
     HIPCHK(c, hipMemset(w.pad, 0, sizeof(float) * H));
