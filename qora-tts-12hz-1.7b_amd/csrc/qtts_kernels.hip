@@ -993,114 +993,151 @@ __device__ __forceinline__ float qkv_head_prologue(const float *part, int S, int
 
 // ---------------------------------------------------------------------------
 // talker decode attention, split over 64-position pages (flash-decoding).
-// Work item (chunk c, kv head h): the q/k/v prologue, then both query heads
-// 2h, 2h+1 share one pass over the page's K and V (GQA, talker.rs:310).
-// The item owning the newest position appends K (normed, roped) and V (raw)
-// first (talker.rs:299-302).  Writes per (chunk, q head) the running max,
-// the exp-sum and the unnormalised P.V.
+// Work item (page c, kv head h): both query heads 2h, 2h+1 share one pass
+// over the page's K and V (GQA, talker.rs:310).  All global loads are issued
+// first (q/k/v partial sums, then the page's K and V as 16-byte loads), so
+// the q/k/v prologue (QK-norm, RoPE) runs while the page streams in.  The
+// item owning the newest position appends K (normed, roped) and V (raw)
+// (talker.rs:299-302) and patches that row in its registers (the page was
+// read before the append).  Writes per (page, query head) the max score, the
+// exp-sum and the unnormalised P.V.
+// Thread t: K rows t/4 (dims 32*(t%4)..+32); V dims 4*(t%32)..+4 of rows
+// 8*(t/32)..+8.
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
               const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
               int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
-    __shared__ float scratch[16];
-    __shared__ float vb[3][HEAD_DIM];
-    __shared__ float qr[2][HEAD_DIM];
-    __shared__ float sc[2][KV_PAGE];
-    __shared__ float pv[2][2][HEAD_DIM];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    __shared__ float ssq[4][2];
+    __shared__ float qn[2][HEAD_DIM], kvn[2][HEAD_DIM];
+    __shared__ float qr[2][HEAD_DIM], knew[HEAD_DIM];
+    __shared__ float pr[2][KV_PAGE];
+    __shared__ float wred[4][2][2];
+    __shared__ float ored[4][2][HEAD_DIM];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127, sel = t >> 7;
     const int slot = slot_ovr >= 0 ? slot_ovr : st->kv_len;
     const int64_t pos = pos_ovr >= 0 ? pos_ovr : st->position;
     const int L = slot + 1;
     const int C = (L + KV_PAGE - 1) / KV_PAGE;
     const float scale = 1.0f / sqrtf(128.0f);
-    const float *cs = rope_cos + pos * 64, *sn = rope_sin + pos * 64;
-    const int j16 = lane & 15;
+    const int tk = t >> 2, kq = t & 3;             // K: row, quarter of the dims
+    const int vd = (t & 31) * 4, vt0 = (t >> 5) * 8; // V: 4 dims, 8 rows
     for (int item = blockIdx.x; item < 8 * C; item += gridDim.x) {
         const int c = item >> 3, h = item & 7;
         const int ntok = min(KV_PAGE, L - c * KV_PAGE);
-        __syncthreads();
-        const float kvnew = qkv_head_prologue(part, S, 1, 0, npad, qn_g, kn_g, cs, sn, h, qr, vb, scratch);
-        if (c == C - 1) kv_ptr(kv, layer, slot, h, t >> 7)[t & 127] = kvnew;
-        __syncthreads();
+        __syncthreads();                           // LDS of the previous item is free
+        // ---- loads: q / k-or-v partials, gammas, rope, then the page
+        float qp[RES_MAX_S], kp[RES_MAX_S];
+#pragma unroll
+        for (int s = 0; s < RES_MAX_S; s++) {
+            const float *p = part + (size_t)min(s, S - 1) * npad;
+            qp[s] = p[(2 * h + sel) * HEAD_DIM + d];
+            kp[s] = p[16 * HEAD_DIM + sel * 8 * HEAD_DIM + h * HEAD_DIM + d];
+        }
+        const uint32_t gq = qn_g[d], gk = kn_g[d];
+        const float cs = rope_cos[pos * 64 + (d & 63)], sn = rope_sin[pos * 64 + (d & 63)];
         const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
         const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
-        // all K and V loads of this thread in flight together
-        float kk[4][8];
+        f32x4 kk[8], vv[8];
 #pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int tok = wv * 16 + it * 4 + (lane >> 4);
-            // pages are allocated whole: rows past ntok are read and masked
-            const float4 *kr = (const float4 *)(Kp + (size_t)tok * HEAD_DIM + j16 * 8);
-            const float4 ka = kr[0], kb = kr[1];
-            const bool ok = tok < ntok;
-            kk[it][0] = ok ? ka.x : 0.f; kk[it][1] = ok ? ka.y : 0.f; kk[it][2] = ok ? ka.z : 0.f; kk[it][3] = ok ? ka.w : 0.f;
-            kk[it][4] = ok ? kb.x : 0.f; kk[it][5] = ok ? kb.y : 0.f; kk[it][6] = ok ? kb.z : 0.f; kk[it][7] = ok ? kb.w : 0.f;
-        }
-        const int dv = t & 127, half = t >> 7;
-        float vv[32];
+        for (int i = 0; i < 8; i++) kk[i] = ld4(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const int tok = half * 32 + i;
-            const float v = Vp[(size_t)tok * HEAD_DIM + dv];
-            vv[i] = tok < ntok ? v : 0.0f;
+        for (int i = 0; i < 8; i++) vv[i] = ld4(Vp + (vt0 + i) * HEAD_DIM + vd);
+        // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92)
+        float qv = qp[0], kvv = kp[0];
+#pragma unroll
+        for (int s = 1; s < RES_MAX_S; s++) {
+            qv = s < S ? qv + qp[s] : qv;
+            kvv = s < S ? kvv + kp[s] : kvv;
         }
-        float q0[8], q1[8];
+        for (int s = RES_MAX_S; s < S; s++) {
+            const float *p = part + (size_t)s * npad;
+            qv += p[(2 * h + sel) * HEAD_DIM + d];
+            kvv += p[16 * HEAD_DIM + sel * 8 * HEAD_DIM + h * HEAD_DIM + d];
+        }
+        const float q2 = wave_sum_dpp(qv * qv), k2 = wave_sum_dpp(kvv * kvv);
+        if (lane == 0) { ssq[wv][0] = q2; ssq[wv][1] = k2; }
+        __syncthreads();
+        const float sq = ssq[2 * sel][0] + ssq[2 * sel + 1][0];
+        const float sk = ssq[0][1] + ssq[1][1];
+        qn[sel][d] = qv * (1.0f / sqrtf(sq / 128.0f + 1e-6f)) * h2f(gq);
+        kvn[sel][d] = sel ? kvv : kvv * (1.0f / sqrtf(sk / 128.0f + 1e-6f)) * h2f(gk);
+        __syncthreads();
+        qr[sel][d] = d < 64 ? qn[sel][d] * cs - qn[sel][d + 64] * sn : qn[sel][d] * cs + qn[sel][d - 64] * sn;
+        if (!sel) knew[d] = d < 64 ? kvn[0][d] * cs - kvn[0][d + 64] * sn : kvn[0][d] * cs + kvn[0][d - 64] * sn;
+        __syncthreads();
+        if (c == C - 1) {
+            // append (talker.rs:299-302), then patch the stale row in registers
+            kv_ptr(kv, layer, slot, h, sel)[d] = sel ? kvn[1][d] : knew[d];
+            const int ts = slot - c * KV_PAGE;
+            if (tk == ts) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) kk[i] = *(const f32x4 *)&knew[kq * 32 + 4 * i];
+            }
+            const f32x4 vn = *(const f32x4 *)&kvn[1][vd];
+#pragma unroll
+            for (int i = 0; i < 8; i++) vv[i] = vt0 + i == ts ? vn : vv[i];
+        }
+        // ---- scores of row tk for both query heads
+        float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            q0[i] = qr[0][j16 * 8 + i];
-            q1[i] = qr[1][j16 * 8 + i];
+            const f32x4 a = *(const f32x4 *)&qr[0][kq * 32 + 4 * i];
+            const f32x4 b = *(const f32x4 *)&qr[1][kq * 32 + 4 * i];
+            const f32x4 k = kk[i];
+            d0 = fmaf(a.x, k.x, fmaf(a.y, k.y, fmaf(a.z, k.z, fmaf(a.w, k.w, d0))));
+            d1 = fmaf(b.x, k.x, fmaf(b.y, k.y, fmaf(b.z, k.z, fmaf(b.w, k.w, d1))));
         }
-#pragma unroll
-        for (int it = 0; it < 4; it++) {
-            const int tok = wv * 16 + it * 4 + (lane >> 4);
-            float d0 = 0.0f, d1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                d0 = fmaf(q0[i], kk[it][i], d0);
-                d1 = fmaf(q1[i], kk[it][i], d1);
-            }
-#pragma unroll
-            for (int m = 8; m >= 1; m >>= 1) {
-                d0 += __shfl_xor(d0, m);
-                d1 += __shfl_xor(d1, m);
-            }
-            if (j16 == 0) {
-                sc[0][tok] = tok < ntok ? d0 * scale : -INFINITY;
-                sc[1][tok] = tok < ntok ? d1 * scale : -INFINITY;
-            }
-        }
+        d0 += dpp_mov<0xB1>(d0);
+        d0 += dpp_mov<0x4E>(d0);
+        d1 += dpp_mov<0xB1>(d1);
+        d1 += dpp_mov<0x4E>(d1);
+        const bool valid = tk < ntok;
+        const float s0 = valid ? d0 * scale : -INFINITY, s1 = valid ? d1 * scale : -INFINITY;
+        // ---- softmax_raw pieces over the page (gemv.rs:471-482)
+        const float mw0 = wave_max_dpp(s0), mw1 = wave_max_dpp(s1);
+        if (lane == 0) { wred[wv][0][0] = mw0; wred[wv][1][0] = mw1; }
         __syncthreads();
-        if (t < 128) {
-            const int hh = t >> 6, tok = t & 63;
-            const float v = sc[hh][tok];
-            const float m = wave_max(v);
-            const float p = tok < ntok ? expf(v - m) : 0.0f;
-            const float l = wave_sum(p);
-            sc[hh][tok] = p;
-            if (tok == 0) {
-                am[c * 16 + 2 * h + hh] = m;
-                al[c * 16 + 2 * h + hh] = l;
-            }
-        }
+        const float m0 = fmaxf(fmaxf(wred[0][0][0], wred[1][0][0]), fmaxf(wred[2][0][0], wred[3][0][0]));
+        const float m1 = fmaxf(fmaxf(wred[0][1][0], wred[1][1][0]), fmaxf(wred[2][1][0], wred[3][1][0]));
+        const float e0 = valid ? expf(s0 - m0) : 0.0f, e1 = valid ? expf(s1 - m1) : 0.0f;
+        const float lw0 = wave_sum_dpp(kq == 0 ? e0 : 0.0f), lw1 = wave_sum_dpp(kq == 0 ? e1 : 0.0f);
+        if (lane == 0) { wred[wv][0][1] = lw0; wred[wv][1][1] = lw1; }
+        if (kq == 0) { pr[0][tk] = e0; pr[1][tk] = e1; }
         __syncthreads();
-        {
-            float a0 = 0.0f, a1 = 0.0f;
+        // ---- P.V over this thread's 8 rows and 4 dims, both heads
+        f32x4 a0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
 #pragma unroll
-            for (int i = 0; i < 32; i++) {
-                const int tok = half * 32 + i;       // p = 0 past ntok
-                a0 = fmaf(sc[0][tok], vv[i], a0);
-                a1 = fmaf(sc[1][tok], vv[i], a1);
-            }
-            pv[half][0][dv] = a0;
-            pv[half][1][dv] = a1;
+        for (int i = 0; i < 8; i++) {
+            const bool ok = vt0 + i < ntok;              // rows past the page's end may hold anything
+            const float p0 = pr[0][vt0 + i], p1 = pr[1][vt0 + i];
+            const f32x4 v = vv[i];
+            a0.x = ok ? fmaf(p0, v.x, a0.x) : a0.x; a0.y = ok ? fmaf(p0, v.y, a0.y) : a0.y;
+            a0.z = ok ? fmaf(p0, v.z, a0.z) : a0.z; a0.w = ok ? fmaf(p0, v.w, a0.w) : a0.w;
+            a1.x = ok ? fmaf(p1, v.x, a1.x) : a1.x; a1.y = ok ? fmaf(p1, v.y, a1.y) : a1.y;
+            a1.z = ok ? fmaf(p1, v.z, a1.z) : a1.z; a1.w = ok ? fmaf(p1, v.w, a1.w) : a1.w;
+        }
+        // rows 8*(t/32): lanes l and l^32 of a wave hold the same dims
+        a0.x += __shfl_xor(a0.x, 32); a0.y += __shfl_xor(a0.y, 32);
+        a0.z += __shfl_xor(a0.z, 32); a0.w += __shfl_xor(a0.w, 32);
+        a1.x += __shfl_xor(a1.x, 32); a1.y += __shfl_xor(a1.y, 32);
+        a1.z += __shfl_xor(a1.z, 32); a1.w += __shfl_xor(a1.w, 32);
+        if (lane < 32) {
+            *(f32x4 *)&ored[wv][0][vd] = a0;
+            *(f32x4 *)&ored[wv][1][vd] = a1;
         }
         __syncthreads();
         {
-            const int d = t & 127, hh = t >> 7;
-            aacc[((size_t)c * 16 + 2 * h + hh) * HEAD_DIM + d] = pv[0][hh][d] + pv[1][hh][d];
+            const int hh = t >> 7;
+            const float o = (ored[0][hh][d] + ored[1][hh][d]) + (ored[2][hh][d] + ored[3][hh][d]);
+            aacc[((size_t)c * 16 + 2 * h + hh) * HEAD_DIM + d] = o;
+            if (d == 0) {
+                am[c * 16 + 2 * h + hh] = hh ? m1 : m0;
+                al[c * 16 + 2 * h + hh] = hh ? (wred[0][1][1] + wred[1][1][1]) + (wred[2][1][1] + wred[3][1][1])
+                                             : (wred[0][0][1] + wred[1][0][1]) + (wred[2][0][1] + wred[3][0][1]);
+            }
         }
     }
 }
