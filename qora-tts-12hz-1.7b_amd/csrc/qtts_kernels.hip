@@ -346,10 +346,12 @@ struct ProResidRms {
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
-        __shared__ float scratch[16];
+        constexpr int NW = T / 64;
+        __shared__ float wss[NB][NW];
         constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
         float *xf = xf_lds();
         const int k4 = k >> 2, t = threadIdx.x;
+        float ssb[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             float ss = 0.0f;
@@ -374,13 +376,21 @@ struct ProResidRms {
                     ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
                 }
             }
-            ss = block_sum(ss, scratch);
-            if (t == 0) inv_lds()[b] = 1.0f / sqrtf(ss / (float)k + 1e-6f);
+            ssb[b] = ss;
+        }
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const float w = wave_sum_dpp(ssb[b]);
+            if ((t & 63) == 0) wss[b][t >> 6] = w;
         }
         __syncthreads();
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float iv = inv_lds()[b];
+            float tot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; i++) tot += wss[b][i];
+            const float iv = 1.0f / sqrtf(tot / (float)k + 1e-6f);
+            if (t == 0) inv_lds()[b] = iv;
 #pragma unroll
             for (int u = 0; u < UG; u++) {
                 const int r = t + u * T;
@@ -616,23 +626,34 @@ struct EpiSwiglu {
 
 // Single-slice lm head: the tile's argmax candidate (value, index) with the
 // last maximum among its columns below n; index -1 marks a NaN in the tile.
+// Runs on wave 0 (lane l takes columns l, l + 64, ...) instead of per column.
 struct EpiArgmax {
+    static constexpr bool kWave = true;
     float2 *cand;
     int n;
-    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    __device__ void wave(int s, int c, int C, const float *yb, int lane) const
     {
-        if (cc != 0) return;
-        float best = -INFINITY;
-        int bi = -1;
-        bool nan = false;
-        for (int j = 0; j < C && c * C + j < n; j++) {
-            const float v = yb[j];
-            nan |= isnan(v);
-            if (bi < 0 || v >= best) { best = v; bi = c * C + j; }
+        float v = -INFINITY;
+        int i = -2;
+        bool nanl = false;
+        for (int j0 = 0; j0 < C; j0 += 64) {
+            const int col = j0 + lane;
+            const bool ok = col < C && c * C + col < n;
+            const float y = ok ? yb[min(col, C - 1)] : -INFINITY;
+            nanl |= ok && isnan(y);
+            argmax_merge(v, i, y, ok ? c * C + col : -2);
         }
-        cand[c] = make_float2(best, __builtin_bit_cast(float, nan ? -1 : bi));
+        const bool nan = __ballot(nanl) != 0;
+        wave_argmax_last(v, i);
+        if (lane == 0) cand[c] = make_float2(v, __builtin_bit_cast(float, nan ? -1 : i));
     }
+    __device__ void operator()(int, int, int, int, int, const float *) const {}
 };
+
+template <class E, class = void>
+struct WaveEpi { static constexpr bool v = false; };
+template <class E>
+struct WaveEpi<E, std::void_t<decltype(E::kWave)>> { static constexpr bool v = E::kWave; };
 
 // ---------------------------------------------------------------------------
 // The split-K Q4 GEMV.
@@ -851,9 +872,14 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             }
         }
         __syncthreads();
-        for (int col = t; col < NB * C; col += T) {
-            const int b = col / C, cc = col - b * C;
-            epi(s, b, c, cc, C, ybuf + b * C);
+        if constexpr (WaveEpi<Epi>::v) {
+            static_assert(NB == 1, "wave epilogue: one row");
+            if (wv == 0) epi.wave(s, c, C, ybuf, lane);
+        } else {
+            for (int col = t; col < NB * C; col += T) {
+                const int b = col / C, cc = col - b * C;
+                epi(s, b, c, cc, C, ybuf + b * C);
+            }
         }
         pro.finish(s, c, w.CT);
     }
@@ -1248,9 +1274,9 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
 // leaves the normalised attention output in xs.  Column tile 0 appends the
 // new K (normed, roped) and V (raw) to the cache; no workgroup of the same
 // launch reads those entries back from memory, so there is no race.
-// Needs T == 256 (one wave per query head of the slice), KC == 512 and at
-// most RES_MAX_S qkv k-slices.
-template <int NB>
+// Needs T == 256 (one wave per query head of the slice), KC == 512 and
+// exactly MS qkv k-slices.
+template <int NB, int MS>
 struct ProPredAttn {
     static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
     static constexpr int HPW = 2;        // kv heads per workgroup
@@ -1264,7 +1290,7 @@ struct ProPredAttn {
 
     template <int T, int KC>
     struct Fetch {
-        float q[NB][HPW][RES_MAX_S], kv[NB][HPW][RES_MAX_S];
+        float q[NB][HPW][MS], kv[NB][HPW][MS];
         uint32_t gq, gk;
         float cs[NB], sn[NB];
         f32x4 kc[NC4], vc[NC4];
@@ -1286,7 +1312,7 @@ struct ProPredAttn {
         }
         // this thread's q (head 2(h0+j)+sel) and k (sel 0) / v (sel 1) slices
 #pragma unroll
-        for (int s = 0; s < RES_MAX_S; s++) {
+        for (int s = 0; s < MS; s++) {
             const int sc = min(s, S - 1);
 #pragma unroll
             for (int b = 0; b < NB; b++) {
@@ -1323,7 +1349,7 @@ struct ProPredAttn {
             for (int j = 0; j < HPW; j++) {
                 float a = f.q[b][j][0], c = f.kv[b][j][0];
 #pragma unroll
-                for (int s = 1; s < RES_MAX_S; s++) {
+                for (int s = 1; s < MS; s++) {
                     a = s < S ? a + f.q[b][j][s] : a;
                     c = s < S ? c + f.kv[b][j][s] : c;
                 }
@@ -2033,6 +2059,14 @@ static bool pred_attn_fusable(const PredictorDev &p, const LayerDev &L)
            L.qkv.npad >= 32 * HEAD_DIM && L.qkv.S <= RES_MAX_S;
 }
 
+template <int NB, int MS>
+static ProPredAttn<NB, MS> pred_attn_pro(const PredictorDev &p, const LayerDev &L, const Workspace &ws, int pos0,
+                                         float *Kc, float *Vc)
+{
+    return ProPredAttn<NB, MS>{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
+                               pos0, Kc, Vc};
+}
+
 template <int NB>
 static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
 {
@@ -2048,9 +2082,12 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
     float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     if (pred_attn_fusable(p, L)) {
         // attention inside the o-proj prologue
-        const ProPredAttn<NB> pro{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
-                                  pos0, Kc, Vc};
-        return launch_gemv_then_mlp<NB>(p, L, ws, pro, s);
+        switch (L.qkv.S) {
+        case 1: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 1>(p, L, ws, pos0, Kc, Vc), s);
+        case 2: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 2>(p, L, ws, pos0, Kc, Vc), s);
+        case 3: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 3>(p, L, ws, pos0, Kc, Vc), s);
+        default: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 4>(p, L, ws, pos0, Kc, Vc), s);
+        }
     }
     hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, NB, L.qkv.npad,
                        L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0, Kc, Vc, ws.pattn);
@@ -2184,9 +2221,13 @@ hipError_t enqueue_pred_attn_o_timing(const PredictorDev &p, const Workspace &ws
     float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     if (pred_attn_fusable(p, L)) {
-        const ProPredAttn<1> pro{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
-                                 pos0, Kc, Vc};
-        return launch_gemv<1>(L.o, pro, EpiPart<1>{ws.part_o, L.o.npad}, s);
+        const EpiPart<1> epi{ws.part_o, L.o.npad};
+        switch (L.qkv.S) {
+        case 1: return launch_gemv<1>(L.o, pred_attn_pro<1, 1>(p, L, ws, pos0, Kc, Vc), epi, s);
+        case 2: return launch_gemv<1>(L.o, pred_attn_pro<1, 2>(p, L, ws, pos0, Kc, Vc), epi, s);
+        case 3: return launch_gemv<1>(L.o, pred_attn_pro<1, 3>(p, L, ws, pos0, Kc, Vc), epi, s);
+        default: return launch_gemv<1>(L.o, pred_attn_pro<1, 4>(p, L, ws, pos0, Kc, Vc), epi, s);
+        }
     }
     hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, 1, L.qkv.npad,
                        L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0, Kc, Vc, ws.pattn);
