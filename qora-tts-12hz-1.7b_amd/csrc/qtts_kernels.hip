@@ -425,27 +425,50 @@ struct ProSwiglu {
     const float *part;
     int S, npad, inter;
     template <int T, int KC>
-    struct Fetch {};
+    struct Fetch {
+        static constexpr int U = (NB * KC + T - 1) / T;
+        float g[U][RES_MAX_S], u[U][RES_MAX_S];
+    };
     template <int T, int KC>
-    __device__ void fetch(Fetch<T, KC> &, int, int) const {}
-    template <int T, int KC>
-    __device__ void load(const Fetch<T, KC> &, float *xs, int k0, int ctile) const
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
-        for (int i = threadIdx.x; i < NB * KC; i += blockDim.x) {
-            const int b = i / KC, r = k0 + (i - b * KC);
-            float v = 0.0f;
-            if (r < inter) {
-                const int gc = (r >> 5) * 64 + (r & 31);
-                float g = 0.0f, u = 0.0f;
-#pragma unroll 4
-                for (int s = 0; s < S; s++) {
+        constexpr int U = Fetch<T, KC>::U;
+#pragma unroll
+        for (int q = 0; q < U; q++) {
+            const int i = min((int)threadIdx.x + q * T, NB * KC - 1);
+            const int b = i / KC, r = min(k0 + (i - b * KC), inter - 1);
+            const int gc = (r >> 5) * 64 + (r & 31);
+#pragma unroll
+            for (int s = 0; s < RES_MAX_S; s++) {
+                const float *p = part + ((size_t)min(s, S - 1) * NB + b) * npad;
+                f.g[q][s] = p[gc];
+                f.u[q][s] = p[gc + 32];
+            }
+        }
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        constexpr int U = Fetch<T, KC>::U;
+#pragma unroll
+        for (int q = 0; q < U; q++) {
+            const int i = threadIdx.x + q * T;
+            if (i < NB * KC) {
+                const int b = i / KC, r = k0 + (i - b * KC);
+                float g = f.g[q][0], u = f.u[q][0];
+#pragma unroll
+                for (int s = 1; s < RES_MAX_S; s++) {
+                    g = s < S ? g + f.g[q][s] : g;
+                    u = s < S ? u + f.u[q][s] : u;
+                }
+                const int gc = (min(r, inter - 1) >> 5) * 64 + (min(r, inter - 1) & 31);
+                for (int s = RES_MAX_S; s < S; s++) {
                     const float *p = part + ((size_t)s * NB + b) * npad;
                     g += p[gc];
                     u += p[gc + 32];
                 }
-                v = silu_f(g) * u;
+                xs[i] = r < inter ? silu_f(g) * u : 0.0f;
             }
-            xs[i] = v;
         }
     }
     __device__ void finish(int s, int c, int nct) const {}

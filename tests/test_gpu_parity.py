@@ -302,3 +302,32 @@ def test_frames_free_running_sampled(loaded):
     assert first_div >= 5, f"free-running frames diverge at frame {first_div}"
     ctx.kv_reset()
     om.kv_reset()
+
+
+@pytest.mark.parametrize("tiles", [{"TGU": "14", "PGU": "16"}, {"TGU": "11", "PGU": "12", "PO": "11"},
+                                   {"TQKV": "3", "TDOWN": "12", "PQKV": "2", "PDOWN": "3"}])
+def test_alternative_tiles_step_and_chain(ctx_factory, small_model, tiles, monkeypatch):
+    """Other tile shapes per role (QTTS_TILE_<ROLE>): split-K gate|up with the
+    SwiGLU prologue in the down projection, the unfused predictor attention,
+    multi-slice q|k|v; a talker step at KV 100 and the predictor codes match
+    the oracle."""
+    for role, cfg in tiles.items():
+        monkeypatch.setenv(f"QTTS_TILE_{role}", cfg)
+    t, p = small_model
+    c = ctx_factory(1024)
+    c.upload_model(t, p)
+    om = O.Model(t, p, kv_cap=1024)
+    rng = np.random.Generator(np.random.PCG64(21))
+    K = rng.standard_normal((len(t.layers), 100, 8, 128)).astype(np.float32)
+    V = rng.standard_normal((len(t.layers), 100, 8, 128)).astype(np.float32)
+    c.kv_load(K, V)
+    om.kv_load(K, V)
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    ok, e = close(c.forward_with_embedding(emb, 100), om.forward_with_embedding(emb, 100))
+    assert ok, f"{tiles}: talker step rel err {e}"
+    th = rng.standard_normal(t.hidden).astype(np.float32)
+    sem = om.embed_codec_token(77)
+    got, ref = c.generate_acoustic_codes(th, sem), om.predictor_chain(th, sem)
+    assert (got == ref).mean() >= 14 / 15, f"{tiles}: codes {got} vs {ref}"
+    om.close()
+    c.close()
