@@ -786,7 +786,10 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     const int ph = WAVE_GROUPS ? (wv / GB) * 64 + lane : t / GB;
     const int items = w.S * w.CT;
 
-    for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    {
+        // launch_gemv starts exactly one workgroup per tile
+        const int item = blockIdx.x;
+        if (item >= items) return;
         const int s = item / w.CT, c = item - s * w.CT;
         const uint8_t *tile = w.data + (size_t)item * w.tile_bytes;
         // the prologue's loads first, then the weight stream: the prologue's
@@ -1291,14 +1294,16 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
 
 // Predictor o-proj prologue with the attention fused in (code_predictor.rs:
 // 369-414, 457-498).  The workgroup owning o-proj input rows k0..k0+511
-// (query heads 4s..4s+3, kv heads 2s, 2s+1) rebuilds those heads' q, k, v
-// from the qkv partial sums (QK-norm, RoPE at pos0 + b), attends over the
-// cached positions plus the new ones (causal among the NB new rows) and
-// leaves the normalised attention output in xs.  Column tile 0 appends the
-// new K (normed, roped) and V (raw) to the cache; no workgroup of the same
-// launch reads those entries back from memory, so there is no race.
-// Needs T == 256 (one wave per query head of the slice), KC == 512 and
-// exactly MS qkv k-slices.
+// (query heads 4s..4s+3, kv heads h0 = 2s, h0 + 1) rebuilds those heads'
+// q, k, v from the qkv partial sums, attends over the cached positions plus
+// the new ones (causal among the NB new rows) and leaves the normalised
+// attention output in xs.  Wave w owns query head 4s + w and one more head
+// vector (w = 0, 1: k of kv head h0 + w; w = 2, 3: v of kv head h0 + w - 2);
+// lane l holds dims l and l + 64, the two halves of a rotate-half RoPE pair,
+// so QK-norm is a wave sum and RoPE stays in registers.  Column tile 0
+// appends the new K (normed, roped) and V (raw) to the cache; no workgroup
+// of the same launch reads those entries back from memory.
+// Needs T == 256, KC == 512 and exactly MS qkv k-slices.
 template <int NB, int MS>
 struct ProPredAttn {
     static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
@@ -1313,72 +1318,57 @@ struct ProPredAttn {
 
     template <int T, int KC>
     struct Fetch {
-        float q[NB][HPW][MS], kv[NB][HPW][MS];
-        uint32_t gq, gk;
+        float q[NB][MS][2], kv[NB][MS][2];
+        uint32_t gq[2], gk[2];
         float cs[NB], sn[NB];
         f32x4 kc[NC4], vc[NC4];
     };
     template <int T, int KC>
     __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
-        const int t = threadIdx.x, d = t & 127, sel = t >> 7;
+        const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
         const int h0 = k0 / (2 * HEAD_DIM);
-        const size_t kvrow = 8 * HEAD_DIM;
         const int plast = pos0 > 0 ? pos0 - 1 : 0;
         // cached positions 0..pos0-1 of both kv heads: float4 i -> (head j, position p, dims 4*d4..)
 #pragma unroll
         for (int u = 0; u < NC4; u++) {
             const int i = t + u * 256, j = i >> 9, p = (i >> 5) & 15, d4 = i & 31;
-            const size_t off = (size_t)min(p, plast) * kvrow + (size_t)(h0 + j) * HEAD_DIM + d4 * 4;
+            const int off = min(p, plast) * (8 * HEAD_DIM) + (h0 + j) * HEAD_DIM + d4 * 4;
             f.kc[u] = ld4(Kc + off);
             f.vc[u] = ld4(Vc + off);
         }
-        // this thread's q (head 2(h0+j)+sel) and k (sel 0) / v (sel 1) slices
+        const int qcol = (2 * h0 + wv) * HEAD_DIM + lane;
+        const int kvcol = 16 * HEAD_DIM + (wv >> 1) * 8 * HEAD_DIM + (h0 + (wv & 1)) * HEAD_DIM + lane;
 #pragma unroll
-        for (int s = 0; s < MS; s++) {
-            const int sc = min(s, S - 1);
+        for (int s = 0; s < MS; s++)
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                const float *pp = part + ((size_t)sc * NB + b) * npad;
-#pragma unroll
-                for (int j = 0; j < HPW; j++) {
-                    f.q[b][j][s] = pp[(2 * (h0 + j) + sel) * HEAD_DIM + d];
-                    f.kv[b][j][s] = pp[16 * HEAD_DIM + sel * 8 * HEAD_DIM + (h0 + j) * HEAD_DIM + d];
-                }
+                const float *pp = part + (s * NB + b) * npad;
+                f.q[b][s][0] = pp[qcol];
+                f.q[b][s][1] = pp[qcol + 64];
+                f.kv[b][s][0] = pp[kvcol];
+                f.kv[b][s][1] = pp[kvcol + 64];
             }
-        }
-        f.gq = qn_g[d];
-        f.gk = kn_g[d];
+        f.gq[0] = qn_g[lane];
+        f.gq[1] = qn_g[lane + 64];
+        f.gk[0] = kn_g[lane];
+        f.gk[1] = kn_g[lane + 64];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            f.cs[b] = rope_cos[(size_t)(pos0 + b) * 64 + (d & 63)];
-            f.sn[b] = rope_sin[(size_t)(pos0 + b) * 64 + (d & 63)];
+            f.cs[b] = rope_cos[(pos0 + b) * 64 + lane];
+            f.sn[b] = rope_sin[(pos0 + b) * 64 + lane];
         }
     }
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
         __shared__ float Ks[HPW * PRED_KV_CAP * HEAD_DIM], Vs[HPW * PRED_KV_CAP * HEAD_DIM];
-        __shared__ float qn[NB * HPW * 2 * HEAD_DIM], qr[NB * HPW * 2 * HEAD_DIM], kn[NB * HPW * HEAD_DIM];
-        __shared__ float ssq[NB * HPW * 4 * 2];
-        const int t = threadIdx.x, d = t & 127, sel = t >> 7, lane = t & 63, wv = t >> 6;
+        __shared__ float qr[NB * 4 * HEAD_DIM];
+        const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
         const int h0 = k0 / (2 * HEAD_DIM);
-        const size_t kvrow = 8 * HEAD_DIM;
-        // k-slice sums in slice order; cached K/V into LDS; sums of squares
-        float qv[NB][HPW], kv[NB][HPW];
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int j = 0; j < HPW; j++) {
-                float a = f.q[b][j][0], c = f.kv[b][j][0];
-#pragma unroll
-                for (int s = 1; s < MS; s++) {
-                    a = s < S ? a + f.q[b][j][s] : a;
-                    c = s < S ? c + f.kv[b][j][s] : c;
-                }
-                qv[b][j] = a;
-                kv[b][j] = c;
-            }
+        const bool isk = wv < 2;
+        const int jn = wv & 1;                       // kv head offset of this wave's k / v vector
+        // cached K / V rows into LDS
 #pragma unroll
         for (int u = 0; u < NC4; u++) {
             const int i = t + u * 256, j = i >> 9, p = (i >> 5) & 15, d4 = i & 31;
@@ -1387,65 +1377,49 @@ struct ProPredAttn {
                 *(f32x4 *)(Vs + (j * PRED_KV_CAP + p) * HEAD_DIM + d4 * 4) = f.vc[u];
             }
         }
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int j = 0; j < HPW; j++) {
-                const float q2 = wave_sum_dpp(qv[b][j] * qv[b][j]);
-                const float k2 = wave_sum_dpp(kv[b][j] * kv[b][j]);
-                if (lane == 0) {
-                    ssq[((b * HPW + j) * 4 + wv) * 2] = q2;
-                    ssq[((b * HPW + j) * 4 + wv) * 2 + 1] = k2;
-                }
-            }
-        __syncthreads();
-        // QK-norm (talker.rs:89-99; code_predictor.rs:84-93); V raw into LDS
-        const float gq = h2f(f.gq), gk = h2f(f.gk);
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int j = 0; j < HPW; j++) {
-                const float *sp = ssq + (b * HPW + j) * 8;
-                const float sq = sp[(2 * sel) * 2] + sp[(2 * sel + 1) * 2];
-                const float sk = sp[1] + sp[3];
-                qn[((b * HPW + j) * 2 + sel) * HEAD_DIM + d] = qv[b][j] * (1.0f / sqrtf(sq / 128.0f + 1e-6f)) * gq;
-                if (!sel)
-                    kn[(b * HPW + j) * HEAD_DIM + d] = kv[b][j] * (1.0f / sqrtf(sk / 128.0f + 1e-6f)) * gk;
-                else
-                    Vs[(j * PRED_KV_CAP + pos0 + b) * HEAD_DIM + d] = kv[b][j];
-            }
-        __syncthreads();
-        // rotate-half RoPE (rope.rs:79-92) into separate buffers; the new K / V
-        // of column tile 0 also go to the cache
+        const float gq0 = h2f(f.gq[0]), gq1 = h2f(f.gq[1]), gk0 = h2f(f.gk[0]), gk1 = h2f(f.gk[1]);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
-            const float cs = f.cs[b], sn = f.sn[b];
+            // k-slice sums in slice order
+            float q0 = f.q[b][0][0], q1 = f.q[b][0][1], v0 = f.kv[b][0][0], v1 = f.kv[b][0][1];
 #pragma unroll
-            for (int j = 0; j < HPW; j++) {
-                const float *qb = qn + ((b * HPW + j) * 2 + sel) * HEAD_DIM;
-                qr[((b * HPW + j) * 2 + sel) * HEAD_DIM + d] =
-                    d < 64 ? qb[d] * cs - qb[d + 64] * sn : qb[d] * cs + qb[d - 64] * sn;
-                const size_t cache = (size_t)(pos0 + b) * kvrow + (size_t)(h0 + j) * HEAD_DIM + d;
-                if (!sel) {
-                    const float *kb = kn + (b * HPW + j) * HEAD_DIM;
-                    const float kr = d < 64 ? kb[d] * cs - kb[d + 64] * sn : kb[d] * cs + kb[d - 64] * sn;
-                    Ks[(j * PRED_KV_CAP + pos0 + b) * HEAD_DIM + d] = kr;
-                    if (ctile == 0) Kc[cache] = kr;
-                } else if (ctile == 0) {
-                    Vc[cache] = kv[b][j];
-                }
+            for (int s = 1; s < MS; s++) {
+                q0 += f.q[b][s][0]; q1 += f.q[b][s][1];
+                v0 += f.kv[b][s][0]; v1 += f.kv[b][s][1];
+            }
+            // QK-norm over the head's 128 dims (talker.rs:89-99; code_predictor.rs:84-93)
+            const float iq = 1.0f / sqrtf(wave_sum_dpp(q0 * q0 + q1 * q1) / 128.0f + 1e-6f);
+            const float ik = 1.0f / sqrtf(wave_sum_dpp(v0 * v0 + v1 * v1) / 128.0f + 1e-6f);
+            const float a0 = q0 * iq * gq0, a1 = q1 * iq * gq1;
+            // rotate-half RoPE (rope.rs:79-92): pair (l, l + 64)
+            const float cs = f.cs[b], sn = f.sn[b];
+            qr[(b * 4 + wv) * HEAD_DIM + lane] = a0 * cs - a1 * sn;
+            qr[(b * 4 + wv) * HEAD_DIM + lane + 64] = a1 * cs + a0 * sn;
+            float n0 = v0, n1 = v1;                  // V stays raw
+            if (isk) {
+                const float c0 = v0 * ik * gk0, c1 = v1 * ik * gk1;
+                n0 = c0 * cs - c1 * sn;
+                n1 = c1 * cs + c0 * sn;
+            }
+            float *row = (isk ? Ks : Vs) + (jn * PRED_KV_CAP + pos0 + b) * HEAD_DIM;
+            row[lane] = n0;
+            row[lane + 64] = n1;
+            if (ctile == 0) {
+                float *cache = (isk ? Kc : Vc) + (pos0 + b) * (8 * HEAD_DIM) + (h0 + jn) * HEAD_DIM;
+                cache[lane] = n0;
+                cache[lane + 64] = n1;
             }
         }
         __syncthreads();
         // wave w = query head 4s + w (kv head h0 + w/2): lane -> position
         // p = lane/4 and a quarter of the head dims; softmax_raw
         // (gemv.rs:471-482) over the positions 0..len-1
-        const int jw = wv >> 1, sw = wv & 1, p = lane >> 2, q4i = lane & 3;
+        const int jw = wv >> 1, p = lane >> 2, q4i = lane & 3;
         const float scale = 1.0f / sqrtf(128.0f);
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             const int len = pos0 + b + 1;
-            const float *qrow = qr + ((b * HPW + jw) * 2 + sw) * HEAD_DIM + q4i * 32;
+            const float *qrow = qr + (b * 4 + wv) * HEAD_DIM + q4i * 32;
             const float *krow = Ks + (jw * PRED_KV_CAP + p) * HEAD_DIM + q4i * 32;
             float dot = 0.0f;
 #pragma unroll
@@ -1467,9 +1441,9 @@ struct ProPredAttn {
             for (int pp = 0; pp < PRED_KV_CAP; pp++) {
                 const float w = lane_value(prob, 4 * pp);
                 const float *vrow = Vs + (jw * PRED_KV_CAP + pp) * HEAD_DIM;
-                const float v0 = vrow[lane], v1 = vrow[lane + 64];
-                o0 = pp < len ? fmaf(w, v0, o0) : o0;
-                o1 = pp < len ? fmaf(w, v1, o1) : o1;
+                const float x0 = vrow[lane], x1 = vrow[lane + 64];
+                o0 = pp < len ? fmaf(w, x0, o0) : o0;
+                o1 = pp < len ? fmaf(w, x1, o1) : o1;
             }
             xs[b * KC + wv * HEAD_DIM + lane] = o0;
             xs[b * KC + wv * HEAD_DIM + lane + 64] = o1;
