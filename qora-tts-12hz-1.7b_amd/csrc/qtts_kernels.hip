@@ -614,9 +614,10 @@ template <int NB>
 struct EpiPart {
     float *part;
     int npad;
-    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
     {
-        part[((size_t)s * NB + b) * npad + c * C + cc] = yb[cc];
+        part[((size_t)s * NB + b) * npad + c * C + cc] = y(cc);
     }
 };
 
@@ -625,10 +626,11 @@ struct EpiStore {
     float *y;
     int ld, n;
     const float *bias;
-    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &yv) const
     {
         const int col = c * C + cc;
-        if (col < n) y[(size_t)b * ld + col] = bias ? yb[cc] + bias[col] : yb[cc];
+        if (col < n) y[(size_t)b * ld + col] = bias ? yv(cc) + bias[col] : yv(cc);
     }
 };
 
@@ -638,11 +640,12 @@ template <int NB>
 struct EpiSwiglu {
     float *h;
     int ld;
-    __device__ void operator()(int s, int b, int c, int cc, int C, const float *yb) const
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
     {
         if ((cc & 63) < 32) {
             const int j = (c * C + cc) >> 6;
-            h[(size_t)b * ld + j * 32 + (cc & 31)] = silu_f(yb[cc]) * yb[cc + 32];
+            h[(size_t)b * ld + j * 32 + (cc & 31)] = silu_f(y(cc)) * y(cc + 32);
         }
     }
 };
@@ -654,7 +657,8 @@ struct EpiArgmax {
     static constexpr bool kWave = true;
     float2 *cand;
     int n;
-    __device__ void wave(int s, int c, int C, const float *yb, int lane) const
+    template <class Y>
+    __device__ void wave(int s, int c, int C, const Y &y, int lane) const
     {
         float v = -INFINITY;
         int i = -2;
@@ -662,15 +666,16 @@ struct EpiArgmax {
         for (int j0 = 0; j0 < C; j0 += 64) {
             const int col = j0 + lane;
             const bool ok = col < C && c * C + col < n;
-            const float y = ok ? yb[min(col, C - 1)] : -INFINITY;
-            nanl |= ok && isnan(y);
-            argmax_merge(v, i, y, ok ? c * C + col : -2);
+            const float yv = y(min(col, C - 1));
+            nanl |= ok && isnan(yv);
+            argmax_merge(v, i, ok ? yv : -INFINITY, ok ? c * C + col : -2);
         }
         const bool nan = __ballot(nanl) != 0;
         wave_argmax_last(v, i);
         if (lane == 0) cand[c] = make_float2(v, __builtin_bit_cast(float, nan ? -1 : i));
     }
-    __device__ void operator()(int, int, int, int, int, const float *) const {}
+    template <class Y>
+    __device__ void operator()(int, int, int, int, int, const Y &) const {}
 };
 
 template <class E, class = void>
@@ -701,13 +706,15 @@ struct WaveEpi<E, std::void_t<decltype(E::kWave)>> { static constexpr bool v = E
 template <int H, int CTRL, int NB>
 __device__ __forceinline__ void rs_dpp_step(float (&v)[NB][32], bool sel)
 {
+    // both halves summed with the partner (DPP operands are values from the
+    // previous step, so no VALU -> DPP hazard waits), then the lane's half
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int j = 0; j < H; j++) {
-            const float send = sel ? v[b][j] : v[b][j + H];
-            const float keep = sel ? v[b][j + H] : v[b][j];
-            v[b][j] = keep + dpp_mov<CTRL>(send);
+            const float lo = v[b][j] + dpp_mov<CTRL>(v[b][j]);
+            const float hi = v[b][j + H] + dpp_mov<CTRL>(v[b][j + H]);
+            v[b][j] = sel ? hi : lo;
         }
 }
 
@@ -871,12 +878,29 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
                 for (int b = 0; b < NB; b++) red[(wv * NB + b) * 32 + col] = acc[b][0];
             }
             __syncthreads();
-            for (int col = t; col < NB * C; col += T) {
-                const int b = col / C, cc = col - b * C, g = cc >> 5;
-                float y = 0.0f;
+            // column sums straight from the per-wave partials, waves in fixed order
+            if constexpr (WaveEpi<Epi>::v) {
+                static_assert(NB == 1, "wave epilogue: one row");
+                if (wv == 0) {
+                    const auto y = [&](int cc) {
+                        float v = 0.0f;
 #pragma unroll
-                for (int i = 0; i < NW / GB; i++) y += red[((i * GB + g) * NB + b) * 32 + (cc & 31)];
-                ybuf[col] = y;
+                        for (int i = 0; i < NW / GB; i++) v += red[(i * GB + (cc >> 5)) * 32 + (cc & 31)];
+                        return v;
+                    };
+                    epi.wave(s, c, C, y, lane);
+                }
+            } else {
+                for (int col = t; col < NB * C; col += T) {
+                    const int b = col / C, cc = col - b * C;
+                    const auto y = [&](int j) {
+                        float v = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < NW / GB; i++) v += red[((i * GB + (j >> 5)) * NB + b) * 32 + (j & 31)];
+                        return v;
+                    };
+                    epi(s, b, c, cc, C, y);
+                }
             }
         } else {
             int base = 0;
@@ -896,15 +920,15 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
                 for (int i = 0; i < NW; i++) y += red[(i * NB + b) * C + cc];
                 ybuf[col] = y;
             }
-        }
-        __syncthreads();
-        if constexpr (WaveEpi<Epi>::v) {
-            static_assert(NB == 1, "wave epilogue: one row");
-            if (wv == 0) epi.wave(s, c, C, ybuf, lane);
-        } else {
-            for (int col = t; col < NB * C; col += T) {
-                const int b = col / C, cc = col - b * C;
-                epi(s, b, c, cc, C, ybuf + b * C);
+            __syncthreads();
+            if constexpr (WaveEpi<Epi>::v) {
+                static_assert(NB == 1, "wave epilogue: one row");
+                if (wv == 0) epi.wave(s, c, C, [&](int j) { return ybuf[j]; }, lane);
+            } else {
+                for (int col = t; col < NB * C; col += T) {
+                    const int b = col / C, cc = col - b * C;
+                    epi(s, b, c, cc, C, [&](int j) { return ybuf[b * C + j]; });
+                }
             }
         }
         pro.finish(s, c, w.CT);
