@@ -784,7 +784,7 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
     static_assert(R == 2 || R == 4 || R == 8, "scale block is one 4/8/16-byte load");
     __shared__ float xs[NB * KC];
     __shared__ float red[NW * NB * C];
-    __shared__ float ybuf[NB * C];
+    __shared__ float ybuf[(NW % GB == 0) ? 1 : NB * C];
 
     constexpr bool WAVE_GROUPS = NW % GB == 0;   // one group per wave
     const int t = threadIdx.x;
@@ -823,7 +823,6 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
             }
         }
 
-        __syncthreads();               // xs / red / ybuf of the previous item are free
         pro.template load<T, KC>(pf, xs, s * KC, c);
         __syncthreads();
 
