@@ -31,10 +31,11 @@ HBM_PEAK_GBS = 8000.0
 TTS_PAD = 151671          # generate_new.rs:28
 
 
-# The standalone GEMV's kernel instance (tile G8_T256, plain prologue, partial
-# epilogue); no frame stage uses this instance, so rocprof's line for it
-# covers exactly the GEMV timing launches.
-GEMV_KERNEL = "k_gemv<256, 8, 8, 1, ProPlain<1>, EpiPart<1>>"
+# The standalone GEMV's kernel instance (tile G1_T256: one 32-column group x
+# 2048 rows per workgroup, plain prologue, partial epilogue); no frame stage
+# uses this instance, so rocprof's line for it covers exactly the GEMV
+# timing launches.
+GEMV_KERNEL = "k_gemv<256, 1, 8, 1, ProPlain<1>, EpiPart<1>>"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4_gemv_2048x6144_hbm_traffic.txt")
 
 
@@ -162,7 +163,7 @@ def main():
     traffic, traffic_src = measured_traffic(GEMV_KERNEL)
     roof = {"bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(g_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": f"{GEMV_KERNEL} (Q4 GEMV k=2048 -> n=6144, tile 8 groups x 256 rows)",
+            "kernel": f"{GEMV_KERNEL} (Q4 GEMV k=2048 -> n=6144, tile 1 group x 2048 rows)",
             "avg_us": round(g_us, 3), "bytes_per_launch": int(g_bytes), "traffic_source": traffic_src}
     kernels = {
         "talker_gate_up_rmsnorm": {"us": round(gu_us, 2), "gbs": round(gu_bytes / gu_us / 1e3, 1),

@@ -137,7 +137,7 @@ static int default_cfg(const char *role, int64_t k)
     if (r == "PGU") return k <= 1024 ? TILE_G2_T256_R4 : TILE_G2_T512;          // 2 slices, SwiGLU in the down prologue
     if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
     if (r == "PDOWN") return TILE_G1_T512_R2;                                   // KC 1024
-    if (r == "GEMV") return TILE_G8_T256;                                       // standalone Q4 GEMV
+    if (r == "GEMV") return TILE_G1_T256;                                       // standalone Q4 GEMV
     return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                             // text fc
 }
 
