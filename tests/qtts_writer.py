@@ -1,0 +1,110 @@
+"""Writer of the `.qora-tts` stream's header, talker and predictor sections
+(save.rs:23-137, field order of save_model / save_talker / save_predictor;
+weight and vector encodings of gemv.rs:645-687), for round-trip tests of
+qtts_model_load_qtts.  Little-endian throughout:
+
+    "QTTS", u32 version = 1, u8 format (1 = Q4, 0 = F16)
+    talker:    u32 n_layers, hidden, text_hidden, n_heads, n_kv_heads, head_dim,
+               n_kv_groups, u32 n_sections, u32 sections[n]
+               per layer: W q k v o, f16v q_norm k_norm, W gate up down,
+                          f16v input_norm post_norm
+               W codec_emb, W text_emb, W fc1, f32v fc1_bias, W fc2, f32v fc2_bias,
+               W codec_head, f16v final_norm, f32v rope_cos, f32v rope_sin
+    predictor: u32 n_layers, hidden, n_heads, n_kv_heads, head_dim, n_kv_groups,
+               u8 has_proj [W proj, f32v bias], u32 n_emb, W emb[n],
+               layers as above, u32 n_heads_lm, W heads[n], f16v final_norm,
+               f32v rope_cos, f32v rope_sin
+    W    = u64 k, u64 n, u64 len + packed bytes, u64 len + len f16 scales
+    f16v = u64 len + len * 2 bytes;  f32v = u64 len + len * 4 bytes
+
+The speech-decoder and speaker-encoder sections that follow in a real file
+are not written: the device loader stops after the predictor.
+"""
+import struct
+
+import numpy as np
+
+
+def _u32(f, v):
+    f.write(struct.pack("<I", v))
+
+
+def _u64(f, v):
+    f.write(struct.pack("<Q", v))
+
+
+def _bytes(f, b):
+    b = np.ascontiguousarray(b, np.uint8)
+    _u64(f, b.size)
+    f.write(b.tobytes())
+
+
+def _f16v(f, bits):
+    bits = np.ascontiguousarray(bits, np.uint16)
+    _u64(f, bits.size)
+    f.write(bits.tobytes())
+
+
+def _f32v(f, v):
+    v = np.ascontiguousarray(v, np.float32)
+    _u64(f, v.size)
+    f.write(v.tobytes())
+
+
+def _weight(f, w):
+    _u64(f, w.k)
+    _u64(f, w.n)
+    _bytes(f, w.packed.reshape(-1))
+    _f16v(f, w.scales.reshape(-1))
+
+
+def _layer(f, L):
+    for w in (L.q_proj, L.k_proj, L.v_proj, L.o_proj):
+        _weight(f, w)
+    _f16v(f, L.q_norm)
+    _f16v(f, L.k_norm)
+    for w in (L.gate_proj, L.up_proj, L.down_proj):
+        _weight(f, w)
+    _f16v(f, L.input_norm)
+    _f16v(f, L.post_attn_norm)
+
+
+def write_qtts(path, talker, predictor, format_id=1, mrope_section=(24, 20, 20)):
+    t, p = talker, predictor
+    with open(path, "wb") as f:
+        f.write(b"QTTS")
+        _u32(f, 1)
+        f.write(bytes([format_id]))
+        for v in (len(t.layers), t.hidden, t.text_hidden, t.n_heads, t.n_kv_heads, t.head_dim,
+                  t.n_heads // t.n_kv_heads, len(mrope_section)):
+            _u32(f, v)
+        for v in mrope_section:
+            _u32(f, v)
+        for L in t.layers:
+            _layer(f, L)
+        _weight(f, t.codec_embedding)
+        _weight(f, t.text_embedding)
+        _weight(f, t.text_fc1)
+        _f32v(f, t.text_fc1_bias)
+        _weight(f, t.text_fc2)
+        _f32v(f, t.text_fc2_bias)
+        _weight(f, t.codec_head)
+        _f16v(f, t.final_norm)
+        _f32v(f, t.rope_cos.reshape(-1))
+        _f32v(f, t.rope_sin.reshape(-1))
+        for v in (len(p.layers), p.hidden, p.n_heads, p.n_kv_heads, p.head_dim, p.n_heads // p.n_kv_heads):
+            _u32(f, v)
+        f.write(bytes([1]))
+        _weight(f, p.input_proj)
+        _f32v(f, p.input_proj_bias)
+        _u32(f, len(p.codec_embeddings))
+        for w in p.codec_embeddings:
+            _weight(f, w)
+        for L in p.layers:
+            _layer(f, L)
+        _u32(f, len(p.lm_heads))
+        for w in p.lm_heads:
+            _weight(f, w)
+        _f16v(f, p.final_norm)
+        _f32v(f, p.rope_cos.reshape(-1))
+        _f32v(f, p.rope_sin.reshape(-1))

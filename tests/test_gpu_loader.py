@@ -1,0 +1,75 @@
+"""`.qora-tts` loading (save.rs:262-409 -> qtts_model_load_qtts): a model
+written in the reference's stream layout by tests/qtts_writer.py and loaded
+from the file behaves bit-for-bit like the same weights uploaded from
+memory, and malformed files fail with the documented status."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import qtts
+from qtts import synth
+from qtts_writer import write_qtts
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def model_file(tmp_path_factory):
+    t = synth.make_talker(seed=301, n_layers=2, text_vocab=256, rope_max_pos=2048)
+    p = synth.make_predictor(seed=302, n_layers=5, rope_max_pos=64)
+    path = str(tmp_path_factory.mktemp("qtts") / "model.qora-tts")
+    write_qtts(path, t, p)
+    return path, t, p
+
+
+def test_loaded_model_matches_upload(ctx_factory, model_file):
+    path, t, p = model_file
+    a, b = ctx_factory(1024), ctx_factory(1024)
+    a.upload_model(t, p)
+    b.load_qtts(path)
+    assert b.dims() == a.dims() == (t.hidden, t.vocab, len(t.layers), p.hidden, p.vocab, len(p.lm_heads))
+    rng = np.random.Generator(np.random.PCG64(31))
+    X = rng.standard_normal((12, t.hidden)).astype(np.float32)
+    ha = a.prefill_talker_raw_from(X, 0)
+    hb = b.prefill_talker_raw_from(X, 0)
+    assert np.array_equal(bits(ha), bits(hb))
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    assert np.array_equal(bits(a.forward_with_embedding(emb, 12)), bits(b.forward_with_embedding(emb, 12)))
+    for tok in (0, 100, 255):
+        assert np.array_equal(bits(a.embed_text_token(tok)), bits(b.embed_text_token(tok)))
+    sem = a.embed_codec_token(2000)
+    assert np.array_equal(a.generate_acoustic_codes(ha, sem), b.generate_acoustic_codes(hb, sem))
+    # and the loaded model against the oracle
+    om = O.Model(t, p, kv_cap=64)
+    ref = om.prefill(X, 0)
+    scale = max(np.abs(ref).max(), np.sqrt((ref ** 2).mean()))
+    assert np.abs(hb - ref).max() <= 1e-3 * scale
+    om.close()
+
+
+def test_malformed_files(ctx_factory, model_file, tmp_path):
+    path, t, p = model_file
+    c = ctx_factory(256)
+    data = open(path, "rb").read()
+    cases = {
+        "bad_magic": (b"QTTX" + data[4:], qtts.ERR_IO),
+        "bad_version": (data[:4] + (2).to_bytes(4, "little") + data[8:], qtts.ERR_IO),
+        "truncated": (data[: len(data) // 2], qtts.ERR_IO),
+        "f16_format": (data[:8] + bytes([0]) + data[9:], qtts.ERR_UNSUPPORTED),
+        "empty": (b"", qtts.ERR_IO),
+    }
+    for name, (blob, code) in cases.items():
+        f = tmp_path / f"{name}.qora-tts"
+        f.write_bytes(blob)
+        with pytest.raises(qtts.QttsError) as e:
+            c.load_qtts(str(f))
+        assert e.value.code == code, f"{name}: status {e.value.code}"
+    with pytest.raises(qtts.QttsError) as e:
+        c.load_qtts(str(tmp_path / "missing.qora-tts"))
+    assert e.value.code == qtts.ERR_IO
