@@ -40,6 +40,10 @@ extern "C" {
 #define QTTS_ERR_UNSUPPORTED -8 /* format the device path does not run     */
 
 #define QTTS_DEVICE_PTRS   1    /* flags: float buffers are device memory  */
+/* Path choice for qtts_gemm_q4 and qtts_talker_prefill (default: by row
+ * count, the matrix cores from 16 rows up). */
+#define QTTS_PATH_ROWWISE  2    /* flags: one GEMV pass per row            */
+#define QTTS_PATH_MFMA     4    /* flags: matrix-core GEMM at any row count */
 
 typedef struct qtts_ctx qtts_ctx;
 typedef struct qtts_w   qtts_w;      /* one uploaded Q4 weight             */

@@ -1,0 +1,71 @@
+// qtts_devutil.h — device helpers shared by the decode kernels
+// (qtts_kernels.hip) and the prefill kernels (qtts_prefill.hip).
+#pragma once
+#include "qtts_kernels.h"
+
+#include <math.h>
+
+namespace qtts {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint32_t h16)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// DPP wave reductions: lane exchanges on the VALU (quad permutes, half-row
+// and row mirrors), then the four row totals read as uniform values.  Every
+// lane gets the same result.
+// ---------------------------------------------------------------------------
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+__device__ __forceinline__ float row_sum16(float v)
+{
+    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
+    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
+    v += dpp_mov<0x141>(v);   // row_half_mirror: the other quad of the half row
+    v += dpp_mov<0x140>(v);   // row_mirror: the other half of the row
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v = row_sum16(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p; }
+
+__device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
+{
+    const int pg = kv.ptab[pos / KV_PAGE];
+    const size_t blk = ((size_t)layer * kv.n_phys + pg) * 2 + isv;
+    return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
+}
+
+}  // namespace qtts

@@ -70,6 +70,16 @@ struct Workspace {
     int attn_grid;
 };
 
+// Buffers of the batched prefill, rows of one prompt chunk.
+struct PrefillWs {
+    float *x;          // residual rows [cap_rows][hidden]
+    float *qkv;        // q|k|v rows [cap_rows][32*128]; q rewritten normed + roped
+    float *attn;       // attention rows [cap_rows][16*128]
+    float *h;          // silu(gate)*up rows [cap_rows][inter]
+    float *inv;        // per-row 1/rms [cap_rows]
+    int cap_rows;
+};
+
 struct SampleArgsHost {
     float temperature, top_p, rep;
     int top_k;
@@ -106,6 +116,11 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
 hipError_t enqueue_pred_attn_o_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
 hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
 hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s);
+bool gemm_supported(const Q4Tiled &w);
+hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s);
+bool prefill_supported(const TalkerDev &m);
+hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M, int64_t start,
+                                  float *hidden_out, hipStream_t s);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
                                hipStream_t s);

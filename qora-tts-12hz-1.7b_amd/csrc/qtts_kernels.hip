@@ -20,6 +20,7 @@
 // atomic or a device-wide fence.
 #include "qtts_device.h"
 #include "qtts_kernels.h"
+#include "qtts_devutil.h"
 
 #include <math.h>
 
@@ -27,14 +28,8 @@
 
 namespace qtts {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float h2f(uint32_t h16)
-{
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)h16);
-}
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 // AND kept opaque to the optimiser: with a visible mask the compiler folds
 // `(w & 0x0F0F0F0F) >> 8*b & 0xFF` into one v_bfe_u32 per byte, while an
@@ -125,47 +120,6 @@ __device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int
     return h2f(e.scales[(size_t)row * e.G + g]) * (float)q;
 }
 
-// ---------------------------------------------------------------------------
-// DPP wave reductions: lane exchanges on the VALU (quad permutes, half-row
-// and row mirrors), then the four row totals read as uniform values.  Every
-// lane gets the same result.
-// ---------------------------------------------------------------------------
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
-}
-
-__device__ __forceinline__ float lane_value(float v, int lane)
-{
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
-}
-
-__device__ __forceinline__ float row_sum16(float v)
-{
-    v += dpp_mov<0xB1>(v);    // quad_perm [1,0,3,2]: lane ^ 1
-    v += dpp_mov<0x4E>(v);    // quad_perm [2,3,0,1]: lane ^ 2
-    v += dpp_mov<0x141>(v);   // row_half_mirror: the other quad of the half row
-    v += dpp_mov<0x140>(v);   // row_mirror: the other half of the row
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum_dpp(float v)
-{
-    v = row_sum16(v);
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
-}
-
-__device__ __forceinline__ float wave_max_dpp(float v)
-{
-    v = fmaxf(v, dpp_mov<0xB1>(v));
-    v = fmaxf(v, dpp_mov<0x4E>(v));
-    v = fmaxf(v, dpp_mov<0x141>(v));
-    v = fmaxf(v, dpp_mov<0x140>(v));
-    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
-}
-
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov_i(int v)
 {
@@ -228,9 +182,7 @@ __device__ __forceinline__ uint32_t cand_argmax(const float2 *cand, int ncand, b
 // load sits behind a branch.
 // ---------------------------------------------------------------------------
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p; }
 
 template <int NB>
 struct ProPlain {
@@ -1015,12 +967,6 @@ static hipError_t reduce_parts(const float *part, int S, int NB, int npad, int n
 // paged talker KV cache and RoPE
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
-{
-    const int pg = kv.ptab[pos / KV_PAGE];
-    const size_t blk = ((size_t)layer * kv.n_phys + pg) * 2 + isv;
-    return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
-}
 
 // rotate-half pair (i, i+64) of one head held in buf (rope.rs:79-92)
 __device__ __forceinline__ float rope_rotate(const float *buf, int d, const float *cs, const float *sn)

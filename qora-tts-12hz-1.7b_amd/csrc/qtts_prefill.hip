@@ -1,0 +1,457 @@
+// qtts_prefill.hip — batched talker prefill for long prompts on the matrix
+// cores (prefill_talker_raw_from, talker.rs:379-482).
+//
+// A prompt of M rows runs layer by layer: per layer
+//   k_row_inv            1/rms of every residual row         gemv.rs:445-454
+//   k_gemm_q4 (store)    [M x 2048] x [2048 x 4096] q|k|v    talker.rs:392-400
+//   k_prefill_qkv_post   QK-norm, RoPE, K/V append           talker.rs:402-425
+//   k_prefill_attn       causal attention over the cache     talker.rs:427-458
+//   k_gemm_q4 (add)      x += attn x o_proj                  talker.rs:460-461
+//   k_row_inv            post-attention norm
+//   k_gemm_q4 (swiglu)   silu(gate) * up, gate|up fused      talker.rs:464-472
+//   k_gemm_q4 (add)      x += h x down_proj                  talker.rs:473-474
+// then k_final_rms on the last row (talker.rs:477-481).
+//
+// k_gemm_q4 contracts on v_mfma_f32_16x16x4_f32: f32 operands and f32
+// accumulation, the arithmetic the reference's gemm_q4 (gemv.rs:349-412)
+// does on the CPU, so results agree to f32 rounding.  The weight is read
+// from the same tiled Q4 layout the decode GEMV streams (no second copy in
+// HBM) and dequantised into LDS once per 64-row block of the prompt.
+
+#include "qtts_device.h"
+#include "qtts_kernels.h"
+#include "qtts_devutil.h"
+
+#include <algorithm>
+
+namespace qtts {
+
+// ---------------------------------------------------------------------------
+// per-row 1/rms (rms_norm_f16, gemv.rs:445-454): inv = 1 / sqrt(sum x^2 / K
+// + 1e-6).  One wave per row.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_row_inv(const float *X, int ld, int M, int K, float *inv)
+{
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const float *x = X + (size_t)m * ld;
+    float s = 0.0f;
+    for (int k = lane * 4; k < K; k += 256) {
+        const f32x4 v = ld4(x + k);
+        s = fmaf(v.x, v.x, s);
+        s = fmaf(v.y, v.y, s);
+        s = fmaf(v.z, v.z, s);
+        s = fmaf(v.w, v.w, s);
+    }
+    s = wave_sum_dpp(s);
+    if (lane == 0) inv[m] = 1.0f / sqrtf(s / (float)K + 1e-6f);
+}
+
+// ---------------------------------------------------------------------------
+// Q4 GEMM on the matrix cores: Y[M][n] (op)= A'[M][K] x W[K][n], with
+// A' = A * inv[row] * gamma[k] when a norm is fused (the reference's
+// x * inv_rms * gamma order) and W dequantised as (nibble - 8) * scale,
+// exact in f32.
+//
+// Workgroup tile 64 rows x 64 columns (two 32-column groups), K in chunks
+// of 32, double-buffered LDS.  Wave w owns rows 32*(w&1)..+32 and the
+// 16-column blocks (w>>1) and (w>>1)+2, so for the gate|up weight (groups
+// interleaved gate, up, gate, up, ...) a lane holds gate and up of the same
+// output column and the SwiGLU epilogue stays in registers.
+//
+// v_mfma_f32_16x16x4_f32 lane layout: A operand lane l = A[l%16][l/16],
+// B operand B[l/16][l%16], result element i = D[4*(l/16)+i][l%16].  The
+// contraction index of lane group q = l/16 at sub-step e is k = 4q + e of a
+// 16-wide slice, so each lane reads its A row and B column as one 16-byte
+// LDS load (As is [row][k], Bs is [column][k]).
+// ---------------------------------------------------------------------------
+
+constexpr int GM = 64, GN = 64, GK = 32, GLD = GK + 4;
+
+enum GemmEpi : int { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2 };
+
+struct GemmA {
+    const float *A;
+    int lda;
+    const float *inv;        // per-row 1/rms, or null
+    const uint16_t *gamma;   // [K] f16, or null
+    int M;
+};
+
+// Address of the 16-byte word and the scale of (row k, group g) in the
+// tiled layout built by the runtime (qtts_device.h).
+__device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k, int g, const uint8_t *&word,
+                                           const uint16_t *&scale)
+{
+    const int P = ts.T / ts.GB;
+    const int s = k / w.KC, rr = k - s * w.KC, r = rr / P, pt = rr - r * P;
+    const int ct = g / ts.GB, gt = g - ct * ts.GB;
+    const bool wave_groups = (ts.T / 64) % ts.GB == 0;
+    const int t = wave_groups ? ((pt >> 6) * ts.GB + gt) * 64 + (pt & 63) : pt * ts.GB + gt;
+    const uint8_t *tile = w.data + (size_t)(s * w.CT + ct) * w.tile_bytes;
+    word = tile + ((size_t)r * ts.T + t) * 16;
+    scale = (const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + t * ts.R + r;
+}
+
+template <int EPI>
+__global__ void __launch_bounds__(256, 2)
+k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm)
+{
+    __shared__ __attribute__((aligned(16))) float As[2][GM * GLD];
+    __shared__ __attribute__((aligned(16))) float Bs[2][GN * GLD];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    // Workgroups are dealt round-robin to the 8 XCDs: give each XCD a
+    // contiguous run of tiles (row blocks fastest) so the row blocks that
+    // share a weight tile share that XCD's L2.
+    const int nwg = gridDim.x, id = blockIdx.x;
+    const int xcd = id & 7, qq = nwg >> 3, rem = nwg & 7;
+    const int logical = xcd * qq + min(xcd, rem) + (id >> 3);
+    const int mt = logical % tm, nt = logical / tm;
+    const int m0 = mt * GM;
+    const TileShape ts = tile_shape(w.cfg);
+
+    // staging roles: A rows t/4, 4 floats at k = 4*(t&3) and +16;
+    // B row kr = t&31 of group 2*nt + (t>>7), bytes 4*((t>>5)&3)..+4
+    const int ar = t >> 2, ak = (t & 3) * 4;
+    const int am = m0 + ar;
+    const bool arow = am < a.M;
+    const float *Arow = a.A + (size_t)(arow ? am : 0) * a.lda;
+    const float ainv = (a.inv && arow) ? a.inv[am] : 1.0f;
+    const int kr = t & 31, qw = (t >> 5) & 3, gi = t >> 7;
+    const int g = 2 * nt + gi;
+    const bool bvalid = g < w.G;
+
+    f32x4 ra0, ra1;
+    uint32_t rb = 0x88888888u, rs = 0;
+    auto fetch = [&](int k0) {
+        if (arow) {
+            ra0 = ld4(Arow + k0 + ak);
+            ra1 = ld4(Arow + k0 + 16 + ak);
+        } else {
+            ra0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            ra1 = ra0;
+        }
+        if (bvalid) {
+            const uint8_t *wp;
+            const uint16_t *sp;
+            tiled_word(w, ts, k0 + kr, g, wp, sp);
+            rb = *(const uint32_t *)(wp + 4 * qw);
+            rs = *sp;
+        }
+    };
+    auto stage = [&](int buf, int k0) {
+        f32x4 x0 = ra0, x1 = ra1;
+        if (a.inv) {
+            x0 *= ainv;
+            x1 *= ainv;
+        }
+        if (a.gamma) {
+            const int ka = k0 + ak;
+            x0.x *= h2f(a.gamma[ka]); x0.y *= h2f(a.gamma[ka + 1]);
+            x0.z *= h2f(a.gamma[ka + 2]); x0.w *= h2f(a.gamma[ka + 3]);
+            x1.x *= h2f(a.gamma[ka + 16]); x1.y *= h2f(a.gamma[ka + 17]);
+            x1.z *= h2f(a.gamma[ka + 18]); x1.w *= h2f(a.gamma[ka + 19]);
+        }
+        *(f32x4 *)&As[buf][ar * GLD + ak] = x0;
+        *(f32x4 *)&As[buf][ar * GLD + 16 + ak] = x1;
+        // 8 columns 32*gi + 8*qw + c, c = 0..7: byte c/2, low nibble even c
+        const float sc = h2f(rs);
+        float *bp = &Bs[buf][(32 * gi + 8 * qw) * GLD + kr];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int nib = (int)((rb >> (4 * c)) & 15u) - 8;
+            bp[c * GLD] = (float)nib * sc;
+        }
+    };
+
+    // compute roles
+    const int wm = wv & 1, wn = wv >> 1, r16 = lane & 15, q = lane >> 4;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nch = K / GK;
+    fetch(0);
+    stage(0, 0);
+    __syncthreads();
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        if (c + 1 < nch) fetch((c + 1) * GK);
+#pragma unroll
+        for (int kk = 0; kk < GK / 16; kk++) {
+            f32x4 av[2], bv[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++) av[i] = *(const f32x4 *)&As[buf][(32 * wm + 16 * i + r16) * GLD + 16 * kk + 4 * q];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (wn + 2 * j) + r16) * GLD + 16 * kk + 4 * q];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
+        }
+        if (c + 1 < nch) stage(buf ^ 1, (c + 1) * GK);
+        __syncthreads();
+    }
+
+    // epilogue: element e of acc[i][j] is row 32wm + 16i + 4q + e, column
+    // 64nt + 16(wn + 2j) + r16
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + 32 * wm + 16 * i + 4 * q + e;
+            if (m >= a.M) continue;
+            float *yr = Y + (size_t)m * ldy;
+            if (EPI == GEMM_SWIGLU) {
+                const int col = 32 * nt + 16 * wn + r16;
+                if (col < ncols) yr[col] = silu_f(acc[i][0][e]) * acc[i][1][e];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int col = 64 * nt + 16 * (wn + 2 * j) + r16;
+                    if (col >= ncols) continue;
+                    if (EPI == GEMM_ADD) yr[col] += acc[i][j][e];
+                    else yr[col] = acc[i][j][e];
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// q|k|v rows -> QK-norm (talker.rs:89-99), RoPE at start + row (rope.rs:
+// 79-92), K (normed, roped) and V (raw) appended to the paged cache at the
+// same position (talker.rs:419-425).  q is rewritten in place.  One wave per
+// (row, head): heads 0..15 q, 16..23 k, 24..31 v; lane holds dims (l, l+64).
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_prefill_qkv_post(float *qkv, int ldq, int M, int64_t start, const uint16_t *qn_g, const uint16_t *kn_g,
+                   const float *rope_cos, const float *rope_sin, KvPaged kv, int layer)
+{
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x, hh = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (m >= M) return;
+    const int64_t pos = start + m;
+    float *row = qkv + (size_t)m * ldq + hh * HEAD_DIM;
+    const float x0 = row[lane], x1 = row[lane + 64];
+    if (hh >= 24) {
+        float *vp = kv_ptr(kv, layer, (int)pos, hh - 24, 1);
+        vp[lane] = x0;
+        vp[lane + 64] = x1;
+        return;
+    }
+    const uint16_t *gam = hh < 16 ? qn_g : kn_g;
+    const float ss = wave_sum_dpp(x0 * x0 + x1 * x1);
+    const float inv = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+    const float n0 = x0 * inv * h2f(gam[lane]), n1 = x1 * inv * h2f(gam[lane + 64]);
+    const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
+    const float r0 = n0 * cs - n1 * sn, r1 = n1 * cs + n0 * sn;
+    if (hh < 16) {
+        row[lane] = r0;
+        row[lane + 64] = r1;
+    } else {
+        float *kp = kv_ptr(kv, layer, (int)pos, hh - 16, 0);
+        kp[lane] = r0;
+        kp[lane + 64] = r1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Causal prefill attention (talker.rs:427-458): query row m (position
+// start + m) attends to cached positions 0..start+m.  Workgroup (row, kv
+// head h) serves q heads 2h and 2h+1 with one pass over the K/V pages and
+// an online softmax across pages (the reference's softmax_raw over the
+// whole row, regrouped).  Thread t: K row t/4 of the page (dims 32*(t%4)
+// ..+32); V dims 4*(t%32)..+4 of page rows 8*(t/32)..+8.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_prefill_attn(const float *q, int ldq, int M, int64_t start, KvPaged kv, int layer, float *out, int ldo)
+{
+    __shared__ __attribute__((aligned(16))) float qs[2][HEAD_DIM];
+    __shared__ float pr[2][KV_PAGE];
+    __shared__ float wred[4][2];
+    __shared__ __attribute__((aligned(16))) float ored[4][2][HEAD_DIM];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127, sel = t >> 7;
+    const int m = blockIdx.x, h = blockIdx.y;
+    const int L = (int)(start + m) + 1;
+    const int C = (L + KV_PAGE - 1) / KV_PAGE;
+    const float scale = 1.0f / sqrtf(128.0f);
+    const int tk = t >> 2, kq = t & 3;
+    const int vd = (t & 31) * 4, vt0 = (t >> 5) * 8;
+    qs[sel][d] = q[(size_t)m * ldq + (2 * h + sel) * HEAD_DIM + d];
+    float mrun0 = -INFINITY, mrun1 = -INFINITY, lrun0 = 0.0f, lrun1 = 0.0f;
+    f32x4 a0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+    __syncthreads();
+    for (int c = 0; c < C; c++) {
+        const int ntok = min(KV_PAGE, L - c * KV_PAGE);
+        const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
+        const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
+        f32x4 kk[8], vv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) kk[i] = ld4(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
+#pragma unroll
+        for (int i = 0; i < 8; i++) vv[i] = ld4(Vp + (vt0 + i) * HEAD_DIM + vd);
+        float d0 = 0.0f, d1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f32x4 qa = *(const f32x4 *)&qs[0][kq * 32 + 4 * i];
+            const f32x4 qb = *(const f32x4 *)&qs[1][kq * 32 + 4 * i];
+            const f32x4 k = kk[i];
+            d0 = fmaf(qa.x, k.x, fmaf(qa.y, k.y, fmaf(qa.z, k.z, fmaf(qa.w, k.w, d0))));
+            d1 = fmaf(qb.x, k.x, fmaf(qb.y, k.y, fmaf(qb.z, k.z, fmaf(qb.w, k.w, d1))));
+        }
+        d0 += dpp_mov<0xB1>(d0);
+        d0 += dpp_mov<0x4E>(d0);
+        d1 += dpp_mov<0xB1>(d1);
+        d1 += dpp_mov<0x4E>(d1);
+        const bool valid = tk < ntok;
+        const float s0 = valid ? d0 * scale : -INFINITY, s1 = valid ? d1 * scale : -INFINITY;
+        const float mw0 = wave_max_dpp(s0), mw1 = wave_max_dpp(s1);
+        if (lane == 0) { wred[wv][0] = mw0; wred[wv][1] = mw1; }
+        __syncthreads();
+        const float pm0 = fmaxf(fmaxf(wred[0][0], wred[1][0]), fmaxf(wred[2][0], wred[3][0]));
+        const float pm1 = fmaxf(fmaxf(wred[0][1], wred[1][1]), fmaxf(wred[2][1], wred[3][1]));
+        const float mn0 = fmaxf(mrun0, pm0), mn1 = fmaxf(mrun1, pm1);
+        const float f0 = expf(mrun0 - mn0), f1 = expf(mrun1 - mn1);   // 0 on the first page
+        const float e0 = valid ? expf(s0 - mn0) : 0.0f, e1 = valid ? expf(s1 - mn1) : 0.0f;
+        if (kq == 0) { pr[0][tk] = e0; pr[1][tk] = e1; }
+        const float lw0 = wave_sum_dpp(kq == 0 ? e0 : 0.0f), lw1 = wave_sum_dpp(kq == 0 ? e1 : 0.0f);
+        __syncthreads();
+        if (lane == 0) { wred[wv][0] = lw0; wred[wv][1] = lw1; }
+        a0 *= f0;
+        a1 *= f1;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const bool ok = vt0 + i < ntok;          // rows past the sequence may hold anything
+            const float p0 = pr[0][vt0 + i], p1 = pr[1][vt0 + i];
+            const f32x4 v = vv[i];
+            a0.x = ok ? fmaf(p0, v.x, a0.x) : a0.x; a0.y = ok ? fmaf(p0, v.y, a0.y) : a0.y;
+            a0.z = ok ? fmaf(p0, v.z, a0.z) : a0.z; a0.w = ok ? fmaf(p0, v.w, a0.w) : a0.w;
+            a1.x = ok ? fmaf(p1, v.x, a1.x) : a1.x; a1.y = ok ? fmaf(p1, v.y, a1.y) : a1.y;
+            a1.z = ok ? fmaf(p1, v.z, a1.z) : a1.z; a1.w = ok ? fmaf(p1, v.w, a1.w) : a1.w;
+        }
+        __syncthreads();
+        lrun0 = lrun0 * f0 + ((wred[0][0] + wred[1][0]) + (wred[2][0] + wred[3][0]));
+        lrun1 = lrun1 * f1 + ((wred[0][1] + wred[1][1]) + (wred[2][1] + wred[3][1]));
+        mrun0 = mn0;
+        mrun1 = mn1;
+        __syncthreads();                             // wred and pr are reused by the next page
+    }
+    // rows 8*(t/32): lanes l and l^32 of a wave hold the same dims
+    a0.x += __shfl_xor(a0.x, 32); a0.y += __shfl_xor(a0.y, 32);
+    a0.z += __shfl_xor(a0.z, 32); a0.w += __shfl_xor(a0.w, 32);
+    a1.x += __shfl_xor(a1.x, 32); a1.y += __shfl_xor(a1.y, 32);
+    a1.z += __shfl_xor(a1.z, 32); a1.w += __shfl_xor(a1.w, 32);
+    if (lane < 32) {
+        *(f32x4 *)&ored[wv][0][vd] = a0;
+        *(f32x4 *)&ored[wv][1][vd] = a1;
+    }
+    __syncthreads();
+    const float o = (ored[0][sel][d] + ored[1][sel][d]) + (ored[2][sel][d] + ored[3][sel][d]);
+    out[(size_t)m * ldo + (2 * h + sel) * HEAD_DIM + d] = o / (sel ? lrun1 : lrun0);
+}
+
+// final-normed hidden of one row (talker.rs:477-481)
+__global__ void __launch_bounds__(256)
+k_final_rms(const float *x, const uint16_t *gamma, int H, float *out)
+{
+    __shared__ float red[4];
+    const int t = threadIdx.x, lane = t & 63;
+    float s = 0.0f;
+    for (int k = t; k < H; k += 256) s = fmaf(x[k], x[k], s);
+    s = wave_sum_dpp(s);
+    if (lane == 0) red[t >> 6] = s;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + 1e-6f);
+    for (int k = t; k < H; k += 256) out[k] = x[k] * inv * h2f(gamma[k]);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+#define PCHK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return e_; } while (0)
+
+static bool gemm_shape_ok(const Q4Tiled &w, int K)
+{
+    return K == w.k && K % GK == 0 && K >= GK;
+}
+
+template <int EPI>
+static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, float *Y, int ldy, int ncols, hipStream_t s)
+{
+    if (!gemm_shape_ok(w, w.k) || a.M < 1 || a.lda % 4) return hipErrorInvalidValue;
+    if (EPI == GEMM_SWIGLU && !w.interleave) return hipErrorInvalidValue;
+    const int tm = (a.M + GM - 1) / GM, tn = (w.G * 32 + GN - 1) / GN;
+    hipLaunchKernelGGL(k_gemm_q4<EPI>, dim3(tm * tn), dim3(256), 0, s, a, w, w.k, Y, ldy, ncols, tm);
+    return hipGetLastError();
+}
+
+bool gemm_supported(const Q4Tiled &w)
+{
+    return gemm_shape_ok(w, w.k);
+}
+
+hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s)
+{
+    const GemmA a{X, w.k, nullptr, nullptr, rows};
+    return launch_gemm<GEMM_STORE>(a, w, Y, ldy, std::min(ldy, w.G * 32), s);
+}
+
+bool prefill_supported(const TalkerDev &m)
+{
+    if (m.n_heads != 16 || m.n_kv_heads != 8 || m.hidden % GK) return false;
+    for (int l = 0; l < m.n_layers; l++) {
+        const LayerDev &L = m.layers[l];
+        if (!gemm_shape_ok(L.qkv, m.hidden) || !gemm_shape_ok(L.o, 16 * HEAD_DIM) ||
+            !gemm_shape_ok(L.gate_up, m.hidden) || !gemm_shape_ok(L.down, m.inter) || !L.gate_up.interleave ||
+            L.qkv.G * 32 < 32 * HEAD_DIM || L.gate_up.G * 16 < m.inter)
+            return false;
+    }
+    return true;
+}
+
+// Rows pw.x[0..M) at positions start..start+M-1 through every layer; the
+// last row's final-normed hidden goes to hidden_out.  Positions
+// start..start+M-1 must be backed by the page table.
+hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M, int64_t start, float *hidden_out,
+                                  hipStream_t s)
+{
+    if (M < 1 || M > pw.cap_rows) return hipErrorInvalidValue;
+    const int H = m.hidden, QKV = 32 * HEAD_DIM;
+    const dim3 rows4((M + 3) / 4);
+    for (int l = 0; l < m.n_layers; l++) {
+        const LayerDev &L = m.layers[l];
+        hipLaunchKernelGGL(k_row_inv, rows4, dim3(256), 0, s, pw.x, H, M, H, pw.inv);
+        PCHK(hipGetLastError());
+        PCHK(launch_gemm<GEMM_STORE>(GemmA{pw.x, H, pw.inv, L.input_norm, M}, L.qkv, pw.qkv, QKV, QKV, s));
+        hipLaunchKernelGGL(k_prefill_qkv_post, dim3(M, 8), dim3(256), 0, s, pw.qkv, QKV, M, start, L.q_norm,
+                           L.k_norm, m.rope_cos, m.rope_sin, m.kv, l);
+        PCHK(hipGetLastError());
+        hipLaunchKernelGGL(k_prefill_attn, dim3(M, 8), dim3(256), 0, s, pw.qkv, QKV, M, start, m.kv, l, pw.attn,
+                           16 * HEAD_DIM);
+        PCHK(hipGetLastError());
+        PCHK(launch_gemm<GEMM_ADD>(GemmA{pw.attn, 16 * HEAD_DIM, nullptr, nullptr, M}, L.o, pw.x, H, H, s));
+        hipLaunchKernelGGL(k_row_inv, rows4, dim3(256), 0, s, pw.x, H, M, H, pw.inv);
+        PCHK(hipGetLastError());
+        PCHK(launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, H, pw.inv, L.post_norm, M}, L.gate_up, pw.h, m.inter, m.inter,
+                                      s));
+        PCHK(launch_gemm<GEMM_ADD>(GemmA{pw.h, m.inter, nullptr, nullptr, M}, L.down, pw.x, H, H, s));
+    }
+    hipLaunchKernelGGL(k_final_rms, dim3(1), dim3(256), 0, s, pw.x + (size_t)(M - 1) * H, m.final_norm, H,
+                       hidden_out);
+    return hipGetLastError();
+}
+
+}  // namespace qtts

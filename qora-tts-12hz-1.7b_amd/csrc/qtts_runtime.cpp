@@ -59,7 +59,15 @@ struct qtts_ctx {
 
     float *d_copy = nullptr;                         // copy-calibration buffers, 2 x copy_floats
     int64_t copy_floats = 0;
+
+    PrefillWs pf{};                                  // batched-prefill rows (allocated on first use)
+    void *pf_mem = nullptr;
 };
+
+// Prompts at least this long take the matrix-core prefill; shorter ones run
+// row by row through the decode kernels.  Same for qtts_gemm_q4 rows.
+constexpr int64_t MFMA_MIN_ROWS = 16;
+constexpr int PREFILL_MAX_ROWS = 1024;   // rows per prefill chunk
 
 // ---------------------------------------------------------------------------
 // error helpers
@@ -374,6 +382,9 @@ static void free_model(qtts_ctx *c)
     drop_graph(c);
     free_list(c->model_allocs);
     free_list(c->ws_allocs);
+    if (c->pf_mem) hipFree(c->pf_mem);   // sized for the model's hidden / inter
+    c->pf_mem = nullptr;
+    c->pf = PrefillWs{};
     c->has_model = false;
     c->gen_started = false;
     c->text_cap = 0;
@@ -421,6 +432,33 @@ static int ensure_io(qtts_ctx *c, int64_t floats)
     HIPCHK(c, hipMalloc(&c->d_io2, floats * sizeof(float)));
     c->io_floats = floats;
     return QTTS_OK;
+}
+
+// Row buffers of the batched prefill for `rows` rows (grown on demand).
+static int ensure_prefill(qtts_ctx *c, int rows)
+{
+    if (rows <= c->pf.cap_rows) return QTTS_OK;
+    if (c->pf_mem) hipFree(c->pf_mem);
+    c->pf_mem = nullptr;
+    c->pf = PrefillWs{};
+    const int64_t H = c->tm.hidden, QKV = 32 * HEAD_DIM, A = 16 * HEAD_DIM, I = c->tm.inter;
+    const int64_t per_row = H + QKV + A + I + 1;
+    float *base = nullptr;
+    HIPCHK(c, hipMalloc(&base, (size_t)rows * per_row * sizeof(float)));
+    c->pf_mem = base;
+    c->pf.x = base;
+    c->pf.qkv = c->pf.x + rows * H;
+    c->pf.attn = c->pf.qkv + rows * QKV;
+    c->pf.h = c->pf.attn + rows * A;
+    c->pf.inv = c->pf.h + rows * I;
+    c->pf.cap_rows = rows;
+    return QTTS_OK;
+}
+
+static bool use_mfma(int flags, int64_t rows)
+{
+    if (flags & QTTS_PATH_ROWWISE) return false;
+    return (flags & QTTS_PATH_MFMA) || rows >= MFMA_MIN_ROWS;
 }
 
 // Copy n floats in (host or device source) to a device buffer.
@@ -497,7 +535,10 @@ extern "C" int qtts_gemm_q4(qtts_ctx *c, const qtts_w *w, const float *X, int64_
     RCHK(ensure_io(c, std::max<int64_t>(rows * w->t.k, rows * w->t.npad)));
     RCHK(stage_in(c, X, rows * w->t.k, c->d_io, flags));
     HIPCHK(c, hipMemsetAsync(c->d_io2, 0, rows * w->t.n * sizeof(float), c->stream));
-    HIPCHK(c, enqueue_gemv_rows(w->t, c->d_io, (int)rows, c->d_io2, w->part, c->stream));
+    if (use_mfma(flags, rows) && gemm_supported(w->t))
+        HIPCHK(c, enqueue_gemm_rows(w->t, c->d_io, (int)rows, c->d_io2, w->t.n, c->stream));
+    else
+        HIPCHK(c, enqueue_gemv_rows(w->t, c->d_io, (int)rows, c->d_io2, w->part, c->stream));
     RCHK(stage_out(c, c->d_io2, rows * w->t.n, Y, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
@@ -733,11 +774,20 @@ extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int
     if (start_pos + seq > c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
     c->gen_started = false;
     const int H = c->tm.hidden;
-    for (int64_t t = 0; t < seq; t++) {
-        RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
-        HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t), c->stream));
+    if (use_mfma(flags, seq) && prefill_supported(c->tm)) {
+        RCHK(ensure_prefill(c, (int)std::min<int64_t>(seq, PREFILL_MAX_ROWS)));
+        for (int64_t r0 = 0; r0 < seq; r0 += c->pf.cap_rows) {
+            const int rows = (int)std::min<int64_t>(c->pf.cap_rows, seq - r0);
+            RCHK(stage_in(c, X + r0 * H, (int64_t)rows * H, c->pf.x, flags));
+            HIPCHK(c, enqueue_talker_prefill(c->tm, c->pf, rows, start_pos + r0, c->ws.hid_work, c->stream));
+        }
+    } else {
+        for (int64_t t = 0; t < seq; t++) {
+            RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
+            HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t), c->stream));
+        }
+        HIPCHK(c, enqueue_final_norm(c->tm, c->ws, c->ws.hid_work, c->stream));
     }
-    HIPCHK(c, enqueue_final_norm(c->tm, c->ws, c->ws.hid_work, c->stream));
     RCHK(stage_out(c, c->ws.hid_work, H, hidden_out, flags));
     c->h_st->kv_len = (int32_t)(start_pos + seq);
     c->h_st->position = start_pos + seq;

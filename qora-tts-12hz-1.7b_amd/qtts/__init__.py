@@ -36,6 +36,8 @@ TILE_SHAPES = [(256, 8, 8), (128, 8, 8), (64, 1, 8), (128, 1, 8), (256, 1, 8), (
 
 OK, ERR_INVALID, ERR_HIP, ERR_OOM, ERR_CAPACITY, ERR_STATE, ERR_IO, ERR_NAN, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6, -7, -8
 DEVICE_PTRS = 1
+PATH_ROWWISE, PATH_MFMA = 2, 4
+_PATH_FLAGS = {None: 0, "rowwise": PATH_ROWWISE, "mfma": PATH_MFMA}
 
 # Exported symbols and their signatures (argtypes, restype), in header order.
 SIGNATURES = {
@@ -166,11 +168,12 @@ class Context:
         self._check(self.lib.qtts_gemv_q4(self.h, w.h, ptr(x), ptr(y), 0))
         return y
 
-    def gemm(self, w, X):
-        """`gemm` (gemv.rs:157): rows of X times W."""
+    def gemm(self, w, X, path=None):
+        """`gemm` (gemv.rs:157): rows of X times W.  path: None (by row
+        count), "rowwise" (GEMV per row) or "mfma" (matrix cores)."""
         X = _f32(X).reshape(-1, w.k)
         Y = np.empty((X.shape[0], w.n), np.float32)
-        self._check(self.lib.qtts_gemm_q4(self.h, w.h, ptr(X), X.shape[0], ptr(Y), 0))
+        self._check(self.lib.qtts_gemm_q4(self.h, w.h, ptr(X), X.shape[0], ptr(Y), _PATH_FLAGS[path]))
         return Y
 
     def embed_lookup(self, w, row):
@@ -204,11 +207,13 @@ class Context:
         self._check(self.lib.qtts_talker_step(self.h, ptr(e), position, ptr(hid), ptr(lg), 0))
         return np.concatenate([hid, lg])
 
-    def prefill_talker_raw_from(self, X, start_pos):
-        """`prefill_talker_raw_from` (talker.rs:379-482): last row's normed hidden."""
+    def prefill_talker_raw_from(self, X, start_pos, path=None):
+        """`prefill_talker_raw_from` (talker.rs:379-482): last row's normed
+        hidden.  path as for gemm()."""
         X = _f32(X).reshape(-1, self.hidden)
         out = np.empty(self.hidden, np.float32)
-        self._check(self.lib.qtts_talker_prefill(self.h, ptr(X), X.shape[0], start_pos, ptr(out), 0))
+        self._check(self.lib.qtts_talker_prefill(self.h, ptr(X), X.shape[0], start_pos, ptr(out),
+                                                 _PATH_FLAGS[path]))
         return out
 
     def apply_codec_head(self, hidden):
