@@ -28,6 +28,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
 
 HBM_PEAK_GBS = 8000.0
+F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix peak
+ICL_ROWS = 400                 # ICL prompt positions (text + reference codes)
 TTS_PAD = 151671          # generate_new.rs:28
 
 
@@ -89,6 +91,23 @@ def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds):
                       f"(synthetic N(0,1) KV prefill), {el:.1f} s"}
 
 
+def time_prefill(ctx, layers):
+    """The ICL-prompt prefill on the matrix cores: the gate|up GEMM alone
+    (cycling the layers) and the whole 400-position prefill, as achieved
+    TFLOP/s against the f32 MFMA peak."""
+    g_us, g_fl = ctx.time_prefill(ICL_ROWS, 0, 4 * layers)
+    p_us, p_fl = ctx.time_prefill(ICL_ROWS, 1, 3)
+    g_tf, p_tf = g_fl / g_us / 1e6, p_fl / p_us / 1e6
+    log(f"prefill {ICL_ROWS} rows: {p_us / 1e3:.2f} ms ({p_tf:.1f} TFLOP/s); gate|up GEMM {g_us:.1f} us "
+        f"({g_tf:.1f} TFLOP/s, {g_tf / F32_MFMA_PEAK_TFLOPS:.1%} of f32 MFMA peak)")
+    return {"rows": ICL_ROWS, "ms": round(p_us / 1e3, 3), "tflops": round(p_tf, 2),
+            "frac_f32_mfma": round(p_tf / F32_MFMA_PEAK_TFLOPS, 4), "flops": p_fl,
+            "gate_up_gemm": {"shape": f"[{ICL_ROWS} x 2048] x [2048 x 12288], SwiGLU epilogue", "us": round(g_us, 2),
+                             "tflops": round(g_tf, 2), "frac_f32_mfma": round(g_tf / F32_MFMA_PEAK_TFLOPS, 4),
+                             "flops": g_fl},
+            "peak_tflops": F32_MFMA_PEAK_TFLOPS, "dtype": "f32 (v_mfma_f32_16x16x4_f32)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -99,6 +118,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-copies", type=int, default=64)
     ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
+    ap.add_argument("--prefill-only", action="store_true", help="time only the matrix-core prefill")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -117,6 +137,11 @@ def main():
     t_up = time.time()
     ctx.upload_model(talker, pred)
     log(f"uploaded in {time.time() - t_up:.1f}s")
+    if args.prefill_only:
+        pf = time_prefill(ctx, args.layers)
+        ctx.close()
+        print(json.dumps({"prefill": pf}), flush=True)
+        return
 
     rng = np.random.Generator(np.random.PCG64(42))
     ids = rng.integers(0, 151936, 64)
@@ -188,9 +213,11 @@ def main():
         kernels["q4_gemv_stream_2048x98304"] = {"us": round(s_us, 2), "gbs": round(s_gbs, 1),
                                                 "frac": round(s_gbs / HBM_PEAK_GBS, 4), "bytes": int(s_bytes)}
 
+    lg, hd, _, _ = ctx.gen_state()
+    kernels["icl_prefill"] = time_prefill(ctx, args.layers)   # rewrites the KV cache
+
     cpu = None
     if not args.no_cpu:
-        lg, hd, _, _ = ctx.gen_state()
         log("timing the CPU baseline (oracle)")
         cpu = cpu_baseline(talker, pred, lg, hd, pad, 2048, args.cpu_seconds)
         log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads")

@@ -47,6 +47,7 @@ extern "C" {
 
 typedef struct qtts_ctx qtts_ctx;
 typedef struct qtts_w   qtts_w;      /* one uploaded Q4 weight             */
+typedef struct qtts_prefix qtts_prefix; /* a kept talker KV prefix          */
 
 /* ---- host-side weight descriptors (plain pointers into caller memory) ---- */
 
@@ -208,6 +209,54 @@ int qtts_kv_load(qtts_ctx *ctx, const float *K, const float *V, int64_t len);
  * generate_new.rs:537-551: the cached prefix is kept, the suffix redone). */
 int qtts_kv_truncate(qtts_ctx *ctx, int64_t len);
 
+/* ---- talker prefix cache (page-table fork) ---------------------------- */
+
+/* Keep cached positions 0..kv_len-1 as a reusable prefix: the
+ * `TalkerPrefixCache` built once per run (generate_new.rs:317-355).  The
+ * full 64-position pages are shared with the running sequence, not copied
+ * (copy-on-write if the sequence rewrites them); the last partial page is
+ * copied.  The context's page pool holds 2 * kv_capacity / 64 pages. */
+int qtts_prefix_capture(qtts_ctx *ctx, qtts_prefix **out);
+/* Start the cache from a kept prefix: `pfx.kv.clone()` then a suffix
+ * prefill at start_pos = prefix length (generate_new.rs:537-551).  The full
+ * pages are mapped into the page table; the partial page is copied.  Sets
+ * kv_len and position to the prefix length. */
+int qtts_prefix_attach(qtts_ctx *ctx, const qtts_prefix *prefix);
+int qtts_prefix_len(const qtts_prefix *prefix, int64_t *len);
+/* Release a prefix (its pages return to the pool once no sequence holds
+ * them).  Prefixes die with their model: after a new upload this only
+ * frees the handle. */
+int qtts_prefix_free(qtts_ctx *ctx, qtts_prefix *prefix);
+/* `prefix_suffix_split` (generate_new.rs:307-316): 1 and *suffix_len =
+ * block_len - n_ref when a prefix of 9 + n_ref positions covers the
+ * chunk-independent part of an ICL block, else 0 (full prefill needed).
+ * Host only; needs no device. */
+int qtts_prefix_suffix_split(int64_t block_len, int64_t n_ref, int64_t prefix_len,
+                             int64_t *suffix_len);
+
+/* ---- prompt construction on the device -------------------------------- */
+
+/* `icl_block_layout` (generate_new.rs:120-128): rows of the ICL block
+ * (n_frames + 1) and of the trailing-text remainder.  Host only. */
+int qtts_icl_layout(int64_t n_ref, int64_t n_text, int64_t n_frames,
+                    int64_t *icl_len, int64_t *remainder_len);
+/* `embed_text_token` (talker.rs:105-116) over `n` ids in one batch (ids in
+ * host memory): the table rows, then fc1 + bias, SiLU, fc2 + bias on the
+ * matrix cores.  out [n][hidden]. */
+int qtts_embed_text_tokens(qtts_ctx *ctx, const uint32_t *ids, int64_t n,
+                           float *out, int flags);
+/* `build_icl_block` (generate_new.rs:140-195) on the device.  ref_codes is
+ * [16][n_frames] (codebook-major, values < 2048), ids and codes in host
+ * memory.  icl_out gets [n_frames + 1][hidden]: text side (ref_tokens ++
+ * text_tokens, then tts_eos; tts_pad past its end) + codec side (codec_bos,
+ * then per frame the talker codec row of code 0 plus the predictor rows of
+ * codes 1..15, added in that order).  remainder_out gets the text rows past
+ * the block, [remainder_len][hidden] (may be null when that is 0). */
+int qtts_build_icl_block(qtts_ctx *ctx, const uint32_t *ref_tokens, int64_t n_ref,
+                         const uint32_t *text_tokens, int64_t n_text,
+                         const uint32_t *ref_codes, int64_t n_frames,
+                         float *icl_out, float *remainder_out, int flags);
+
 /* ---- code predictor --------------------------------------------------- */
 
 /* `generate_acoustic_codes` (code_predictor.rs:218-273): 2-token prefill,
@@ -285,6 +334,18 @@ int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
  * HBM, not cache). */
 int qtts_time_gemv(qtts_ctx *ctx, const qtts_w *const *ws, int32_t n_w,
                    int32_t iters, double *avg_us, double *bytes);
+
+/* Average device time (us) of the matrix-core prefill over `rows`
+ * synthetic rows (same event scheme); *flops gets the algorithmic
+ * floating-point operations of one launch.  No reference counterpart.
+ *   what 0: the talker gate|up GEMM with its SwiGLU epilogue
+ *           ([rows x hidden] x [hidden x 2 inter]), cycling the layers;
+ *   what 1: the whole prefill_talker_raw_from over positions 0..rows-1
+ *           (every layer, attention included, input rows restaged per
+ *           launch).  Overwrites cached positions 0..rows-1 and leaves
+ *           the cache length at 0. */
+int qtts_time_prefill(qtts_ctx *ctx, int64_t rows, int32_t what, int32_t iters,
+                      double *avg_us, double *flops);
 
 #ifdef __cplusplus
 }

@@ -68,4 +68,16 @@ __device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, 
     return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
 }
 
+// ---------------------------------------------------------------------------
+// Q4 dequantisation of one reference-layout row element (exact in f32)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int col)
+{
+    const int g = col >> 5, j = col & 31;
+    const uint8_t b = e.packed[(size_t)row * e.G * 16 + g * 16 + (j >> 1)];
+    const int q = (int)((j & 1) ? (b >> 4) : (b & 0x0F)) - 8;
+    return h2f(e.scales[(size_t)row * e.G + g]) * (float)q;
+}
+
 }  // namespace qtts

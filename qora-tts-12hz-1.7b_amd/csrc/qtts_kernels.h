@@ -118,7 +118,17 @@ hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws,
 hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s);
 bool gemm_supported(const Q4Tiled &w);
 hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s);
+hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,
+                             int ldy, hipStream_t s);
 bool prefill_supported(const TalkerDev &m);
+hipError_t enqueue_gather_rows(const Q4Rows &e, const uint32_t *ids, int n, float *out, int ld, hipStream_t s);
+hipError_t enqueue_codec_frame_rows(const Q4Rows &tcodec, const Q4Rows &pemb, int n_groups, const uint32_t *codes,
+                                    int n_frames, float *out, int ld, hipStream_t s);
+hipError_t enqueue_add_rows(const float *a, int lda, const float *b, int ldb, float *out, int ldo, int rows, int n,
+                            hipStream_t s);
+hipError_t enqueue_fill_rows(float *x, int64_t n, uint32_t seed, hipStream_t s);
+hipError_t enqueue_row_inv(const float *X, int ld, int M, int K, float *inv, hipStream_t s);
+hipError_t enqueue_gemm_gateup(const TalkerDev &m, const PrefillWs &pw, int l, int M, hipStream_t s);
 hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M, int64_t start,
                                   float *hidden_out, hipStream_t s);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);

@@ -108,18 +108,6 @@ __device__ int block_excl_scan(int v, int *scratch, int *total)
     return base + x - v;
 }
 
-// ---------------------------------------------------------------------------
-// Q4 dequantisation of one reference-layout row element (exact in f32)
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float q4_row_value(const Q4Rows &e, uint32_t row, int col)
-{
-    const int g = col >> 5, j = col & 31;
-    const uint8_t b = e.packed[(size_t)row * e.G * 16 + g * 16 + (j >> 1)];
-    const int q = (int)((j & 1) ? (b >> 4) : (b & 0x0F)) - 8;
-    return h2f(e.scales[(size_t)row * e.G + g]) * (float)q;
-}
-
 template <int CTRL>
 __device__ __forceinline__ int dpp_mov_i(int v)
 {

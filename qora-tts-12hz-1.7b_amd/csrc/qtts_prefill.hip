@@ -71,7 +71,7 @@ k_row_inv(const float *X, int ld, int M, int K, float *inv)
 
 constexpr int GM = 64, GN = 64, GK = 32, GLD = GK + 4;
 
-enum GemmEpi : int { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2 };
+enum GemmEpi : int { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2, GEMM_BIAS = 3, GEMM_BIAS_SILU = 4 };
 
 struct GemmA {
     const float *A;
@@ -98,7 +98,7 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
 
 template <int EPI>
 __global__ void __launch_bounds__(256, 2)
-k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm)
+k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm, const float *bias)
 {
     __shared__ __attribute__((aligned(16))) float As[2][GM * GLD];
     __shared__ __attribute__((aligned(16))) float Bs[2][GN * GLD];
@@ -220,6 +220,8 @@ k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm)
                     const int col = 64 * nt + 16 * (wn + 2 * j) + r16;
                     if (col >= ncols) continue;
                     if (EPI == GEMM_ADD) yr[col] += acc[i][j][e];
+                    else if (EPI == GEMM_BIAS) yr[col] = acc[i][j][e] + bias[col];
+                    else if (EPI == GEMM_BIAS_SILU) yr[col] = silu_f(acc[i][j][e] + bias[col]);
                     else yr[col] = acc[i][j][e];
                 }
             }
@@ -377,6 +379,18 @@ k_final_rms(const float *x, const uint16_t *gamma, int H, float *out)
     for (int k = t; k < H; k += 256) out[k] = x[k] * inv * h2f(gamma[k]);
 }
 
+// Synthetic rows for timing: x[i] uniform in [-1, 1) from a hash of (seed, i).
+__global__ void k_fill_rows(float *x, int64_t n, uint32_t seed)
+{
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        uint32_t h = (uint32_t)i * 0x9E3779B1u ^ seed * 0x85EBCA77u;
+        h ^= h >> 15;
+        h *= 0x2C1B3C6Du;
+        h ^= h >> 12;
+        x[i] = (float)(h >> 8) * (1.0f / 8388608.0f) - 1.0f;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -389,12 +403,14 @@ static bool gemm_shape_ok(const Q4Tiled &w, int K)
 }
 
 template <int EPI>
-static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, float *Y, int ldy, int ncols, hipStream_t s)
+static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, float *Y, int ldy, int ncols, hipStream_t s,
+                              const float *bias = nullptr)
 {
     if (!gemm_shape_ok(w, w.k) || a.M < 1 || a.lda % 4) return hipErrorInvalidValue;
     if (EPI == GEMM_SWIGLU && !w.interleave) return hipErrorInvalidValue;
+    if ((EPI == GEMM_BIAS || EPI == GEMM_BIAS_SILU) && !bias) return hipErrorInvalidValue;
     const int tm = (a.M + GM - 1) / GM, tn = (w.G * 32 + GN - 1) / GN;
-    hipLaunchKernelGGL(k_gemm_q4<EPI>, dim3(tm * tn), dim3(256), 0, s, a, w, w.k, Y, ldy, ncols, tm);
+    hipLaunchKernelGGL(k_gemm_q4<EPI>, dim3(tm * tn), dim3(256), 0, s, a, w, w.k, Y, ldy, ncols, tm, bias);
     return hipGetLastError();
 }
 
@@ -409,6 +425,17 @@ hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *
     return launch_gemm<GEMM_STORE>(a, w, Y, ldy, std::min(ldy, w.G * 32), s);
 }
 
+// Y = X W + bias, optionally through SiLU (the text projection's fc1 / fc2,
+// talker.rs:105-116, over a batch of rows).
+hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,
+                             int ldy, hipStream_t s)
+{
+    const GemmA a{X, w.k, nullptr, nullptr, rows};
+    const int ncols = std::min(ldy, w.n);
+    return silu ? launch_gemm<GEMM_BIAS_SILU>(a, w, Y, ldy, ncols, s, bias)
+                : launch_gemm<GEMM_BIAS>(a, w, Y, ldy, ncols, s, bias);
+}
+
 bool prefill_supported(const TalkerDev &m)
 {
     if (m.n_heads != 16 || m.n_kv_heads != 8 || m.hidden % GK) return false;
@@ -420,6 +447,27 @@ bool prefill_supported(const TalkerDev &m)
             return false;
     }
     return true;
+}
+
+hipError_t enqueue_fill_rows(float *x, int64_t n, uint32_t seed, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_fill_rows, dim3(1024), dim3(256), 0, s, x, n, seed);
+    return hipGetLastError();
+}
+
+hipError_t enqueue_row_inv(const float *X, int ld, int M, int K, float *inv, hipStream_t s)
+{
+    if (K % 4 || ld % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_row_inv, dim3((M + 3) / 4), dim3(256), 0, s, X, ld, M, K, inv);
+    return hipGetLastError();
+}
+
+// The prefill's gate|up GEMM of layer l alone (pw.x rows and pw.inv set).
+hipError_t enqueue_gemm_gateup(const TalkerDev &m, const PrefillWs &pw, int l, int M, hipStream_t s)
+{
+    const LayerDev &L = m.layers[l];
+    return launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, m.hidden, pw.inv, L.post_norm, M}, L.gate_up, pw.h, m.inter,
+                                    m.inter, s);
 }
 
 // Rows pw.x[0..M) at positions start..start+M-1 through every layer; the

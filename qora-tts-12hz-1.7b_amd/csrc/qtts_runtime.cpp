@@ -62,12 +62,35 @@ struct qtts_ctx {
 
     PrefillWs pf{};                                  // batched-prefill rows (allocated on first use)
     void *pf_mem = nullptr;
+
+    // Talker KV page pool: 2 * kv_cap/64 physical pages shared by the running
+    // sequence and captured prefixes.  seq_ptab is the host copy of the
+    // sequence's page table (d_ptab on the device), page_ref counts the
+    // holders of each physical page (the sequence, prefixes).
+    std::vector<int32_t> seq_ptab, page_ref, free_pages;
+    int32_t *d_ptab = nullptr;
+    uint64_t model_gen = 0;                          // bumped by every model upload
+};
+
+// A kept talker prefix (TalkerPrefixCache, generate_new.rs:317-325; built by
+// build_talker_prefix, generate_new.rs:330-355): the
+// physical pages holding positions 0..len-1 of every layer.  Full pages are
+// shared with the sequences that attach it; the last partial page is its
+// own copy.
+struct qtts_prefix {
+    const qtts_ctx *owner = nullptr;
+    uint64_t model_gen = 0;
+    int64_t len = 0;
+    std::vector<int32_t> pages;
 };
 
 // Prompts at least this long take the matrix-core prefill; shorter ones run
 // row by row through the decode kernels.  Same for qtts_gemm_q4 rows.
 constexpr int64_t MFMA_MIN_ROWS = 16;
 constexpr int PREFILL_MAX_ROWS = 1024;   // rows per prefill chunk
+
+// special ids of the prompt layout (generate_new.rs:25-36)
+constexpr uint32_t TTS_PAD_ID = 151671, TTS_EOS_ID = 151673, CODEC_BOS_ID = 2149;
 
 // ---------------------------------------------------------------------------
 // error helpers
@@ -650,15 +673,24 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     m.rope_rows = t->rope_max_pos;
     if (m.codec_rows.n != m.hidden) return fail(c, QTTS_ERR_INVALID, "codec embedding width != hidden");
 
-    // paged KV pool (identity page table)
-    const int n_phys = (int)(c->kv_cap / KV_PAGE);
+    // paged KV pool: the sequence starts on pages 0..kv_cap/64-1, the other
+    // half of the pool is free for prefixes and copy-on-write
+    const int n_seq = (int)(c->kv_cap / KV_PAGE), n_pool = 2 * n_seq;
     float *kvb = nullptr;
-    RCHK(dev_alloc(c, A, &kvb, (size_t)t->n_layers * n_phys * 2 * 8 * KV_PAGE * HEAD_DIM));
-    std::vector<int32_t> ptab(MAX_CHUNKS);
-    for (int i = 0; i < MAX_CHUNKS; i++) ptab[i] = i < n_phys ? i : 0;
+    RCHK(dev_alloc(c, A, &kvb, (size_t)t->n_layers * n_pool * 2 * 8 * KV_PAGE * HEAD_DIM));
+    c->seq_ptab.assign(MAX_CHUNKS, 0);
+    c->page_ref.assign(n_pool, 0);
+    c->free_pages.clear();
+    for (int i = 0; i < n_seq; i++) {
+        c->seq_ptab[i] = i;
+        c->page_ref[i] = 1;
+    }
+    for (int i = n_pool - 1; i >= n_seq; i--) c->free_pages.push_back(i);
     const int32_t *dptab = nullptr;
-    RCHK(upload_vec(c, A, ptab.data(), ptab.size(), &dptab));
-    m.kv = KvPaged{kvb, dptab, n_phys};
+    RCHK(upload_vec(c, A, c->seq_ptab.data(), c->seq_ptab.size(), &dptab));
+    c->d_ptab = const_cast<int32_t *>(dptab);
+    m.kv = KvPaged{kvb, dptab, n_pool};
+    c->model_gen++;
 
     PredictorDev &q = c->pm;
     q.n_layers = p->n_layers; q.hidden = p->hidden; q.n_heads = p->n_heads; q.n_kv_heads = p->n_kv_heads;
@@ -692,6 +724,71 @@ static int write_state(qtts_ctx *c)
     HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// KV page pool
+// ---------------------------------------------------------------------------
+
+static int push_ptab(qtts_ctx *c)
+{
+    HIPCHK(c, hipMemcpyAsync(c->d_ptab, c->seq_ptab.data(), c->seq_ptab.size() * sizeof(int32_t),
+                             hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+static int page_take(qtts_ctx *c, int32_t *page)
+{
+    if (c->free_pages.empty())
+        return fail(c, QTTS_ERR_CAPACITY, "KV page pool exhausted (free unused prefixes)");
+    *page = c->free_pages.back();
+    c->free_pages.pop_back();
+    c->page_ref[*page] = 1;
+    return QTTS_OK;
+}
+
+static void page_drop(qtts_ctx *c, int32_t page)
+{
+    if (--c->page_ref[page] == 0) c->free_pages.push_back(page);
+}
+
+// Copy one physical page (all layers, K and V) to another.
+static int page_copy(qtts_ctx *c, int32_t src, int32_t dst)
+{
+    const size_t blk = (size_t)2 * 8 * KV_PAGE * HEAD_DIM;
+    for (int l = 0; l < c->tm.n_layers; l++) {
+        float *b = c->tm.kv.base + (size_t)l * c->tm.kv.n_phys * blk;
+        HIPCHK(c, hipMemcpyAsync(b + (size_t)dst * blk, b + (size_t)src * blk, blk * sizeof(float),
+                                 hipMemcpyDeviceToDevice, c->stream));
+    }
+    return QTTS_OK;
+}
+
+// Before the sequence writes positions from `pos` on: every logical page from
+// the one holding `pos` that is shared with a prefix gets a private page
+// (copy-on-write, keeping the positions below `pos`).
+static int seq_unshare_from(qtts_ctx *c, int64_t pos)
+{
+    const int n_seq = (int)(c->kv_cap / KV_PAGE);
+    bool changed = false;
+    for (int i = (int)(pos / KV_PAGE); i < n_seq; i++) {
+        const int32_t old = c->seq_ptab[i];
+        if (c->page_ref[old] <= 1) continue;
+        int32_t p;
+        RCHK(page_take(c, &p));
+        if ((int64_t)i * KV_PAGE < pos) {
+            const int r = page_copy(c, old, p);
+            if (r != QTTS_OK) {
+                page_drop(c, p);
+                return r;
+            }
+        }
+        page_drop(c, old);
+        c->seq_ptab[i] = p;
+        changed = true;
+    }
+    return changed ? push_ptab(c) : QTTS_OK;
 }
 
 static int read_state(qtts_ctx *c)
@@ -772,6 +869,7 @@ extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int
         return fail(c, QTTS_ERR_STATE, "prefill at %lld but %d positions cached", (long long)start_pos, c->h_st->kv_len);
     if (start_pos + seq > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full");
     if (start_pos + seq > c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
+    RCHK(seq_unshare_from(c, start_pos));
     c->gen_started = false;
     const int H = c->tm.hidden;
     if (use_mfma(flags, seq) && prefill_supported(c->tm)) {
@@ -843,6 +941,7 @@ extern "C" int qtts_embed_codec_token(qtts_ctx *c, uint32_t token, float *out, i
 extern "C" int qtts_kv_reset(qtts_ctx *c)
 {
     NEED_MODEL(c);
+    RCHK(seq_unshare_from(c, 0));
     c->gen_started = false;
     c->h_st->kv_len = 0;
     c->h_st->position = 0;
@@ -861,6 +960,7 @@ extern "C" int qtts_kv_truncate(qtts_ctx *c, int64_t len)
 {
     NEED_MODEL(c);
     if (len < 0 || len > c->h_st->kv_len) return QTTS_ERR_INVALID;
+    RCHK(seq_unshare_from(c, len));
     c->gen_started = false;
     c->h_st->kv_len = (int32_t)len;
     return write_state(c);
@@ -892,6 +992,7 @@ extern "C" int qtts_kv_load(qtts_ctx *c, const float *K, const float *V, int64_t
     NEED_MODEL(c);
     if (!K || !V || len < 0) return QTTS_ERR_INVALID;
     if (len > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "kv_load of %lld > capacity", (long long)len);
+    RCHK(seq_unshare_from(c, 0));
     c->gen_started = false;
     const size_t n = (size_t)len * 8 * HEAD_DIM;
     if (n) {
@@ -912,6 +1013,213 @@ extern "C" int qtts_kv_load(qtts_ctx *c, const float *K, const float *V, int64_t
     }
     c->h_st->kv_len = (int32_t)len;
     return write_state(c);
+}
+
+// ---------------------------------------------------------------------------
+// talker prefix cache on the page pool
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_prefix_capture(qtts_ctx *c, qtts_prefix **out)
+{
+    NEED_MODEL(c);
+    if (!out) return QTTS_ERR_INVALID;
+    *out = nullptr;
+    const int64_t len = c->h_st->kv_len;
+    if (len < 1) return fail(c, QTTS_ERR_STATE, "no cached positions to keep as a prefix");
+    const int full = (int)(len / KV_PAGE);
+    int32_t tail = -1;
+    if (len % KV_PAGE) {
+        RCHK(page_take(c, &tail));
+        const int r = page_copy(c, c->seq_ptab[full], tail);
+        if (r == QTTS_OK) HIPCHK(c, hipStreamSynchronize(c->stream));
+        if (r != QTTS_OK) {
+            page_drop(c, tail);
+            return r;
+        }
+    }
+    qtts_prefix *p = new qtts_prefix();
+    p->owner = c;
+    p->model_gen = c->model_gen;
+    p->len = len;
+    for (int i = 0; i < full; i++) {
+        p->pages.push_back(c->seq_ptab[i]);
+        c->page_ref[c->seq_ptab[i]]++;
+    }
+    if (tail >= 0) p->pages.push_back(tail);
+    *out = p;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_prefix_attach(qtts_ctx *c, const qtts_prefix *p)
+{
+    NEED_MODEL(c);
+    if (!p) return QTTS_ERR_INVALID;
+    if (p->owner != c || p->model_gen != c->model_gen)
+        return fail(c, QTTS_ERR_STATE, "prefix kept by another context or for another model");
+    const int full = (int)(p->len / KV_PAGE);
+    if (p->len % KV_PAGE) {
+        // the partial page is copied: the sequence appends into it
+        int32_t cur = c->seq_ptab[full];
+        if (c->page_ref[cur] > 1) {
+            int32_t q;
+            RCHK(page_take(c, &q));
+            page_drop(c, cur);
+            c->seq_ptab[full] = q;
+            cur = q;
+        }
+        RCHK(page_copy(c, p->pages[full], cur));
+    }
+    for (int i = 0; i < full; i++) {
+        const int32_t pg = p->pages[i];
+        if (c->seq_ptab[i] == pg) continue;
+        c->page_ref[pg]++;
+        page_drop(c, c->seq_ptab[i]);
+        c->seq_ptab[i] = pg;
+    }
+    RCHK(push_ptab(c));
+    c->gen_started = false;
+    c->h_st->kv_len = (int32_t)p->len;
+    c->h_st->position = p->len;
+    return write_state(c);
+}
+
+extern "C" int qtts_prefix_len(const qtts_prefix *p, int64_t *len)
+{
+    if (!p || !len) return QTTS_ERR_INVALID;
+    *len = p->len;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_prefix_free(qtts_ctx *c, qtts_prefix *p)
+{
+    if (!c || !p || p->owner != c) return QTTS_ERR_INVALID;
+    if (c->has_model && p->model_gen == c->model_gen)
+        for (int32_t pg : p->pages) page_drop(c, pg);
+    delete p;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_prefix_suffix_split(int64_t block_len, int64_t n_ref, int64_t prefix_len, int64_t *suffix_len)
+{
+    if (!suffix_len || block_len < 0 || n_ref < 0 || prefix_len < 0) return QTTS_ERR_INVALID;
+    *suffix_len = 0;
+    if (prefix_len != 9 + n_ref || n_ref >= block_len) return 0;
+    *suffix_len = block_len - n_ref;
+    return 1;
+}
+
+// ---------------------------------------------------------------------------
+// prompt construction
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_icl_layout(int64_t n_ref, int64_t n_text, int64_t n_frames, int64_t *icl_len,
+                               int64_t *remainder_len)
+{
+    if (!icl_len || !remainder_len || n_ref < 0 || n_text < 0 || n_frames < 1) return QTTS_ERR_INVALID;
+    const int64_t text_len = n_ref + n_text + 1, codec_len = n_frames + 1;
+    *icl_len = codec_len;
+    *remainder_len = text_len > codec_len ? text_len - codec_len : 0;
+    return QTTS_OK;
+}
+
+// Text projection of n ids into device rows out[n][hidden]: table rows, then
+// fc1 + bias and SiLU, fc2 + bias on the matrix cores.  `scratch` holds
+// n * (text_hidden + hidden) floats.
+static int text_rows(qtts_ctx *c, const uint32_t *d_ids, int n, float *out, float *scratch)
+{
+    const TalkerDev &m = c->tm;
+    if (!gemm_supported(m.text_fc1) || !gemm_supported(m.text_fc2))
+        return fail(c, QTTS_ERR_UNSUPPORTED, "text projection widths outside the matrix-core GEMM");
+    Q4Rows e = m.text_rows;
+    e.n = m.text_hidden;
+    float *raw = scratch, *h1 = scratch + (size_t)n * m.text_hidden;
+    HIPCHK(c, enqueue_gather_rows(e, d_ids, n, raw, m.text_hidden, c->stream));
+    HIPCHK(c, enqueue_gemm_bias(m.text_fc1, raw, n, m.text_fc1_bias, true, h1, m.text_fc1.n, c->stream));
+    HIPCHK(c, enqueue_gemm_bias(m.text_fc2, h1, n, m.text_fc2_bias, false, out, m.hidden, c->stream));
+    return QTTS_OK;
+}
+
+// Device scratch for one prompt call, freed on every exit.
+struct DevScratch {
+    void *p = nullptr;
+    ~DevScratch() { if (p) hipFree(p); }
+};
+
+extern "C" int qtts_embed_text_tokens(qtts_ctx *c, const uint32_t *ids, int64_t n, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (!ids || !out || n < 0) return QTTS_ERR_INVALID;
+    if (n == 0) return QTTS_OK;
+    const TalkerDev &m = c->tm;
+    for (int64_t i = 0; i < n; i++)
+        if ((int64_t)ids[i] >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", ids[i]);
+    const size_t n_out = (size_t)n * m.hidden;
+    DevScratch buf;
+    HIPCHK(c, hipMalloc(&buf.p, n * sizeof(uint32_t) + ((size_t)n * (m.text_hidden + m.text_fc1.n) + n_out) * sizeof(float)));
+    float *rows = (float *)buf.p, *scratch = rows + n_out;
+    uint32_t *d_ids = (uint32_t *)(scratch + (size_t)n * (m.text_hidden + m.text_fc1.n));
+    HIPCHK(c, hipMemcpyAsync(d_ids, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    RCHK(text_rows(c, d_ids, (int)n, rows, scratch));
+    RCHK(stage_out(c, rows, (int64_t)n_out, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_build_icl_block(qtts_ctx *c, const uint32_t *ref_tokens, int64_t n_ref,
+                                    const uint32_t *text_tokens, int64_t n_text, const uint32_t *ref_codes,
+                                    int64_t n_frames, float *icl_out, float *remainder_out, int flags)
+{
+    NEED_MODEL(c);
+    int64_t icl_len, rem_len;
+    if ((n_ref && !ref_tokens) || (n_text && !text_tokens) || !ref_codes || !icl_out ||
+        qtts_icl_layout(n_ref, n_text, n_frames, &icl_len, &rem_len) != QTTS_OK)
+        return QTTS_ERR_INVALID;
+    if (rem_len && !remainder_out) return QTTS_ERR_INVALID;
+    const TalkerDev &m = c->tm;
+    const PredictorDev &p = c->pm;
+    if (p.n_groups != 15 || p.emb_rows.n != m.hidden)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "ICL block needs 15 predictor tables of the talker width");
+    const int64_t text_len = n_ref + n_text + 1;
+    // ids: ref ++ text ++ [TTS_EOS, TTS_PAD]; codes [16][n_frames]
+    std::vector<uint32_t> ids;
+    ids.insert(ids.end(), ref_tokens, ref_tokens + n_ref);
+    ids.insert(ids.end(), text_tokens, text_tokens + n_text);
+    ids.push_back(TTS_EOS_ID);
+    ids.push_back(TTS_PAD_ID);
+    for (uint32_t t : ids)
+        if ((int64_t)t >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", t);
+    for (int64_t i = 0; i < 16 * n_frames; i++)
+        if (ref_codes[i] >= (uint32_t)p.emb_rows.rows || (i < n_frames && ref_codes[i] >= (uint32_t)m.codec_rows.rows))
+            return fail(c, QTTS_ERR_INVALID, "reference code %u out of range", ref_codes[i]);
+    const int nt = (int)ids.size();
+    const size_t H = m.hidden;
+    DevScratch buf;
+    const size_t f_text = (size_t)nt * H, f_codec = (size_t)(n_frames + 1) * H, f_icl = (size_t)icl_len * H;
+    const size_t f_scr = (size_t)nt * (m.text_hidden + m.text_fc1.n);
+    HIPCHK(c, hipMalloc(&buf.p, (f_text + f_codec + f_icl + f_scr) * sizeof(float) +
+                                    (nt + 16 * n_frames + 1) * sizeof(uint32_t)));
+    float *text = (float *)buf.p, *codec = text + f_text, *icl = codec + f_codec, *scr = icl + f_icl;
+    uint32_t *d_ids = (uint32_t *)(scr + f_scr), *d_codes = d_ids + nt;
+    const uint32_t bos = CODEC_BOS_ID;
+    HIPCHK(c, hipMemcpyAsync(d_ids, ids.data(), nt * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_codes, ref_codes, 16 * n_frames * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_codes + 16 * n_frames, &bos, sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    // text side: rows 0..text_len-1 (tts_eos last), row text_len = tts_pad
+    RCHK(text_rows(c, d_ids, nt, text, scr));
+    // codec side: codec_bos, then the per-frame sums (generate_new.rs:161-172)
+    HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_codes + 16 * n_frames, 1, codec, (int)H, c->stream));
+    HIPCHK(c, enqueue_codec_frame_rows(m.codec_rows, p.emb_rows, 15, d_codes, (int)n_frames, codec + H, (int)H,
+                                       c->stream));
+    // pairs (generate_new.rs:174-189): text row (tts_pad past the text) + codec row
+    const int64_t paired = std::min(text_len, icl_len);
+    HIPCHK(c, enqueue_add_rows(text, (int)H, codec, (int)H, icl, (int)H, (int)paired, (int)H, c->stream));
+    if (icl_len > paired)
+        HIPCHK(c, enqueue_add_rows(text + (size_t)text_len * H, 0, codec + paired * H, (int)H, icl + paired * H, (int)H,
+                                   (int)(icl_len - paired), (int)H, c->stream));
+    RCHK(stage_out(c, icl, (int64_t)f_icl, icl_out, flags));
+    if (rem_len) RCHK(stage_out(c, text + (size_t)icl_len * H, rem_len * (int64_t)H, remainder_out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -1241,6 +1549,51 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
                              avg_us);
     }
     return QTTS_ERR_INVALID;
+}
+
+extern "C" int qtts_time_prefill(qtts_ctx *c, int64_t rows, int32_t what, int32_t iters, double *avg_us,
+                                 double *flops)
+{
+    if (!c || iters < 1 || !avg_us || !flops || rows < 1 || (what != 0 && what != 1)) return QTTS_ERR_INVALID;
+    NEED_MODEL(c);
+    const TalkerDev &m = c->tm;
+    if (!prefill_supported(m)) return fail(c, QTTS_ERR_UNSUPPORTED, "model shapes outside the matrix-core prefill");
+    if (rows > PREFILL_MAX_ROWS) return fail(c, QTTS_ERR_CAPACITY, "at most %d rows per prefill chunk", PREFILL_MAX_ROWS);
+    if (rows > c->kv_cap || rows > m.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "rows beyond the KV cache");
+    hipSetDevice(c->device);
+    RCHK(ensure_prefill(c, (int)rows));
+    RCHK(seq_unshare_from(c, 0));
+    c->gen_started = false;
+    const int M = (int)rows, H = m.hidden;
+    if (what == 0) {
+        HIPCHK(c, enqueue_fill_rows(c->pf.x, (int64_t)M * H, 7u, c->stream));
+        HIPCHK(c, enqueue_row_inv(c->pf.x, H, M, H, c->pf.inv, c->stream));
+        *flops = 2.0 * M * H * 2.0 * m.inter;
+        return time_launches(c, iters, [&](int i) { return enqueue_gemm_gateup(m, c->pf, i % m.n_layers, M, c->stream); },
+                             avg_us);
+    }
+    double f = 0.0;
+    for (int l = 0; l < m.n_layers; l++) {
+        const LayerDev &L = m.layers[l];
+        f += 2.0 * M * ((double)L.qkv.k * 32 * HEAD_DIM + (double)L.o.k * H + (double)H * 2 * m.inter +
+                        (double)m.inter * H);
+        f += 4.0 * 16 * HEAD_DIM * ((double)M * (M + 1) / 2);   // QK and PV of the causal attention
+    }
+    *flops = f;
+    // synthetic input rows, restaged into pf.x before each launch
+    RCHK(ensure_io(c, (int64_t)M * H));
+    float *src = c->d_io;
+    HIPCHK(c, enqueue_fill_rows(src, (int64_t)M * H, 11u, c->stream));
+    const int rc = time_launches(c, iters, [&](int) {
+        hipError_t e = hipMemcpyAsync(c->pf.x, src, (size_t)M * H * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
+        if (e != hipSuccess) return e;
+        return enqueue_talker_prefill(m, c->pf, M, 0, c->ws.hid_work, c->stream);
+    }, avg_us);
+    c->h_st->kv_len = 0;
+    c->h_st->position = 0;
+    HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return rc;
 }
 
 extern "C" int qtts_time_gemv(qtts_ctx *c, const qtts_w *const *ws, int32_t n_w, int32_t iters, double *avg_us,

@@ -64,6 +64,15 @@ SIGNATURES = {
     "qtts_kv_gather": ([c_void_p, c_int32, c_void_p, c_void_p], c_int),
     "qtts_kv_load": ([c_void_p, c_void_p, c_void_p, c_int64], c_int),
     "qtts_kv_truncate": ([c_void_p, c_int64], c_int),
+    "qtts_prefix_capture": ([c_void_p, POINTER(c_void_p)], c_int),
+    "qtts_prefix_attach": ([c_void_p, c_void_p], c_int),
+    "qtts_prefix_len": ([c_void_p, POINTER(c_int64)], c_int),
+    "qtts_prefix_free": ([c_void_p, c_void_p], c_int),
+    "qtts_prefix_suffix_split": ([c_int64, c_int64, c_int64, POINTER(c_int64)], c_int),
+    "qtts_icl_layout": ([c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64)], c_int),
+    "qtts_embed_text_tokens": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_build_icl_block": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
+                              c_void_p, c_int], c_int),
     "qtts_predictor_chain": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_acoustic_embed_sum": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_sample_token": ([c_void_p, c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64,
@@ -75,6 +84,7 @@ SIGNATURES = {
     "qtts_gen_state": ([c_void_p, c_void_p, c_void_p, POINTER(c_int64), POINTER(c_uint64)], c_int),
     "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_gemv": ([c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
+    "qtts_time_prefill": ([c_void_p, c_int64, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
 }
 
 
@@ -258,6 +268,40 @@ class Context:
         self._check(self.lib.qtts_kv_truncate(self.h, n))
 
     # ---- predictor / sampler -----------------------------------------------
+    # ---- prefix cache --------------------------------------------------------
+    def prefix_capture(self):
+        """Keep the cached positions as a prefix (TalkerPrefixCache,
+        generate_new.rs:317-355)."""
+        h = c_void_p()
+        self._check(self.lib.qtts_prefix_capture(self.h, byref(h)))
+        return Prefix(self, h)
+
+    def prefix_attach(self, prefix):
+        """Start the cache from a kept prefix (pfx.kv.clone(), generate_new.rs:541)."""
+        self._check(self.lib.qtts_prefix_attach(self.h, prefix.h))
+
+    # ---- prompt construction ------------------------------------------------
+    def embed_text_tokens(self, ids):
+        """embed_text_token (talker.rs:105-116) over a batch of ids."""
+        ids = np.ascontiguousarray(ids, np.uint32).reshape(-1)
+        out = np.empty((ids.size, self.hidden), np.float32)
+        self._check(self.lib.qtts_embed_text_tokens(self.h, ptr(ids), ids.size, ptr(out), 0))
+        return out
+
+    def build_icl_block(self, ref_tokens, text_tokens, ref_codes):
+        """build_icl_block (generate_new.rs:140-195): (icl rows, remainder rows).
+        ref_codes is [16][n_frames]."""
+        r = np.ascontiguousarray(ref_tokens, np.uint32).reshape(-1)
+        t = np.ascontiguousarray(text_tokens, np.uint32).reshape(-1)
+        codes = np.ascontiguousarray(ref_codes, np.uint32).reshape(16, -1)
+        icl_len, rem_len = icl_layout(r.size, t.size, codes.shape[1], self.lib)
+        icl = np.empty((icl_len, self.hidden), np.float32)
+        rem = np.empty((rem_len, self.hidden), np.float32)
+        self._check(self.lib.qtts_build_icl_block(self.h, ptr(r) if r.size else None, r.size,
+                                                  ptr(t) if t.size else None, t.size, ptr(codes), codes.shape[1],
+                                                  ptr(icl), ptr(rem) if rem_len else None, 0))
+        return icl, rem
+
     def generate_acoustic_codes(self, talker_hidden, semantic_embed):
         th = _f32(talker_hidden, self.hidden)
         se = _f32(semantic_embed, self.hidden)
@@ -324,6 +368,48 @@ class Context:
         us, b = c_double(), c_double()
         self._check(self.lib.qtts_time_gemv(self.h, arr, len(weights), iters, byref(us), byref(b)))
         return us.value, b.value
+
+    def time_prefill(self, rows, what, iters):
+        """(avg us, flops) of the matrix-core prefill over `rows` synthetic
+        rows: what 0 the gate|up GEMM, 1 the whole prefill."""
+        us, fl = c_double(), c_double()
+        self._check(self.lib.qtts_time_prefill(self.h, rows, what, iters, byref(us), byref(fl)))
+        return us.value, fl.value
+
+
+class Prefix:
+    """A kept talker KV prefix (qtts_prefix); free() returns its pages."""
+
+    def __init__(self, ctx, h):
+        self.ctx, self.h = ctx, h
+        n = c_int64()
+        ctx._check(ctx.lib.qtts_prefix_len(h, byref(n)))
+        self.len = n.value
+
+    def free(self):
+        if self.h:
+            self.ctx._check(self.ctx.lib.qtts_prefix_free(self.ctx.h, self.h))
+            self.h = None
+
+
+def icl_layout(n_ref, n_text, n_frames, lib=None):
+    """icl_block_layout (generate_new.rs:120-128): (icl_len, remainder_len)."""
+    lib = lib or load_library()
+    a, b = c_int64(), c_int64()
+    rc = lib.qtts_icl_layout(n_ref, n_text, n_frames, byref(a), byref(b))
+    if rc != OK:
+        raise QttsError(rc, "invalid ICL layout arguments")
+    return a.value, b.value
+
+
+def prefix_suffix_split(block_len, n_ref, prefix_len, lib=None):
+    """prefix_suffix_split (generate_new.rs:307-316): suffix length or None."""
+    lib = lib or load_library()
+    n = c_int64()
+    rc = lib.qtts_prefix_suffix_split(block_len, n_ref, prefix_len, byref(n))
+    if rc < 0:
+        raise QttsError(rc, "invalid prefix split arguments")
+    return n.value if rc == 1 else None
 
 
 def header_symbols(header_path=None):

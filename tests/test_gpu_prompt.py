@@ -1,0 +1,194 @@
+"""Prompt construction on the device and the talker prefix cache.
+
+- embed_text_token over a batch (talker.rs:105-116): within the GEMV bar of
+  the oracle, and bit-identical for an id wherever it sits in a batch (the
+  prefix cache depends on it);
+- build_icl_block (generate_new.rs:140-195): codec side bit-exact (rows are
+  exact Q4 values summed in the reference's order), text side as above, on
+  the three layouts of the reference's own tests;
+- prefix capture / attach (TalkerPrefixCache, generate_new.rs:317-355,
+  537-551): prefix + suffix prefill is bit-identical to one full prefill,
+  hidden and every layer's cache, and the prefix survives the sequence
+  rewriting its cache (copy-on-write).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import qtts
+from qtts import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TTS_PAD, TTS_EOS, CODEC_BOS = 151671, 151673, 2149
+
+
+def close(got, ref, rel=TOL):
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), np.sqrt((ref ** 2).mean()), 1e-30)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    return err <= rel * scale, err / scale
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def model():
+    t = synth.make_talker(seed=501, n_layers=2, rope_max_pos=2048)
+    p = synth.make_predictor(seed=502, n_layers=5)
+    return t, p
+
+
+@pytest.fixture(scope="module")
+def ctx(ctx_factory, model):
+    c = ctx_factory(1024)
+    c.upload_model(*model)
+    return c
+
+
+@pytest.fixture(scope="module")
+def om(model):
+    O.set_workers(16, 8)
+    m = O.Model(*model, kv_cap=64)
+    yield m
+    m.close()
+
+
+def test_embed_text_tokens_batch(ctx, om):
+    rng = np.random.Generator(np.random.PCG64(3001))
+    ids = rng.integers(0, 151936, 37)
+    rows = ctx.embed_text_tokens(ids)
+    for i, tok in enumerate(ids[:12]):
+        ok, e = close(rows[i], om.embed_text_token(int(tok)))
+        assert ok, f"id {tok}: rel err {e}"
+    # the same id gives the same bits alone, first or last in a batch
+    one = ctx.embed_text_tokens(ids[5:6])
+    assert np.array_equal(bits(one[0]), bits(rows[5]))
+    tail = ctx.embed_text_tokens(np.concatenate([ids[:3], ids[5:6]]))
+    assert np.array_equal(bits(tail[3]), bits(rows[5]))
+
+
+def codec_side(t, p, codes):
+    """Codec side of the ICL block in f32, the reference's order
+    (generate_new.rs:161-172)."""
+    rows = [O.embed_lookup(t.codec_embedding, CODEC_BOS)]
+    for f in range(codes.shape[1]):
+        s = O.embed_lookup(t.codec_embedding, int(codes[0, f])).astype(np.float32)
+        for g in range(1, 16):
+            s = s + O.embed_lookup(p.codec_embeddings[g - 1], int(codes[g, f])).astype(np.float32)
+        rows.append(s)
+    return np.stack(rows).astype(np.float32)
+
+
+@pytest.mark.parametrize("n_ref,n_text,n_frames", [(8, 8, 23), (30, 30, 23), (11, 11, 22), (1, 1, 23)])
+def test_icl_block(ctx, model, om, n_ref, n_text, n_frames):
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3100 + n_ref))
+    ref = rng.integers(0, 151936, n_ref)
+    text = rng.integers(0, 151936, n_text)
+    codes = rng.integers(0, 2048, (16, n_frames))
+    icl, rem = ctx.build_icl_block(ref, text, codes)
+    icl_len, rem_len = qtts.icl_layout(n_ref, n_text, n_frames)
+    assert icl.shape == (icl_len, t.hidden) and rem.shape == (rem_len, t.hidden)
+    # text side through the same batched projection
+    text_full = ctx.embed_text_tokens(np.concatenate([ref, text, [TTS_EOS]]))
+    pad = ctx.embed_text_tokens([TTS_PAD])[0]
+    side = np.stack([text_full[i] if i < len(text_full) else pad for i in range(icl_len)])
+    expect = (side + codec_side(t, p, codes)).astype(np.float32)
+    assert np.array_equal(bits(icl), bits(expect))
+    assert np.array_equal(bits(rem), bits(text_full[icl_len:]))
+    # text side against the oracle's per-token projection
+    ok, e = close(text_full[-1], om.embed_text_token(TTS_EOS))
+    assert ok, f"tts_eos rel err {e}"
+
+
+def test_prefix_attach_bit_identical(ctx, model):
+    """A 109-position prefix (9 head rows + 100 reference rows) kept once;
+    two chunks attach it and prefill their suffixes; each equals a full
+    prefill of the same rows bit for bit, and the prefix outlives a reset
+    and a rewrite of the sequence's cache."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3200))
+    P = 109
+    head = rng.standard_normal((P, t.hidden)).astype(np.float32)
+    suf_a = rng.standard_normal((291, t.hidden)).astype(np.float32)
+    suf_b = rng.standard_normal((150, t.hidden)).astype(np.float32)
+
+    def full(X):
+        ctx.kv_reset()
+        h = ctx.prefill_talker_raw_from(X, 0, path="mfma")
+        return h, [ctx.kv_gather(l) for l in range(len(t.layers))]
+
+    ha, kva = full(np.concatenate([head, suf_a]))
+    hb, kvb = full(np.concatenate([head, suf_b]))
+
+    ctx.kv_reset()
+    ctx.prefill_talker_raw_from(head, 0, path="mfma")
+    pfx = ctx.prefix_capture()
+    assert pfx.len == P
+    for suffix, h_ref, kv_ref in ((suf_a, ha, kva), (suf_b, hb, kvb), (suf_a, ha, kva)):
+        ctx.prefix_attach(pfx)
+        assert ctx.kv_len() == P
+        h = ctx.prefill_talker_raw_from(suffix, P, path="mfma")
+        assert np.array_equal(bits(h), bits(h_ref))
+        for l in range(len(t.layers)):
+            k, v = ctx.kv_gather(l)
+            assert np.array_equal(bits(k), bits(kv_ref[l][0])) and np.array_equal(bits(v), bits(kv_ref[l][1]))
+        # the sequence rewrites positions inside the shared pages
+        ctx.kv_reset()
+        ctx.prefill_talker_raw_from(suf_b[:100], 0, path="mfma")
+    pfx.free()
+    ctx.kv_reset()
+
+
+def test_prefix_then_frames(ctx, model):
+    """Greedy frames after attach + suffix equal the frames after a full
+    prefill (same cache bits, same kernels)."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3300))
+    X = rng.standard_normal((140, t.hidden)).astype(np.float32)
+    params = qtts.sample_params(top_k=1, eos_enabled=False)
+    pad = ctx.embed_text_tokens([TTS_PAD])[0]
+    ctx.gen_set_text(None, pad)
+
+    def frames(h):
+        ctx.gen_begin(ctx.apply_codec_head(h), h, 140, 42, params)
+        return ctx.gen_frames(12)[0]
+
+    ctx.kv_reset()
+    ref = frames(ctx.prefill_talker_raw_from(X, 0, path="mfma"))
+    ctx.kv_reset()
+    ctx.prefill_talker_raw_from(X[:70], 0, path="mfma")
+    pfx = ctx.prefix_capture()
+    ctx.prefix_attach(pfx)
+    got = frames(ctx.prefill_talker_raw_from(X[70:], 70, path="mfma"))
+    assert np.array_equal(got, ref)
+    pfx.free()
+    ctx.kv_reset()
+
+
+def test_prefix_pool_capacity(ctx_factory, model):
+    """kv_capacity 256: 4 sequence pages + 4 spare.  A kept prefix pins its
+    pages; once the sequence has unshared them the pool is exhausted and a
+    second capture fails cleanly until the first prefix is freed."""
+    c = ctx_factory(256)
+    c.upload_model(*model)
+    rng = np.random.Generator(np.random.PCG64(3400))
+    X = rng.standard_normal((200, model[0].hidden)).astype(np.float32)
+    c.prefill_talker_raw_from(X, 0, path="mfma")
+    a = c.prefix_capture()                         # 3 shared pages + 1 copied
+    c.kv_reset()                                   # unshares 3 pages: pool empty
+    c.prefill_talker_raw_from(X[:100], 0, path="mfma")
+    with pytest.raises(qtts.QttsError) as e:
+        c.prefix_capture()
+    assert e.value.code == qtts.ERR_CAPACITY
+    a.free()
+    b = c.prefix_capture()
+    assert b.len == 100
+    c.prefix_attach(b)
+    assert c.kv_len() == 100
+    b.free()
+    c.close()

@@ -61,3 +61,23 @@ def test_tile_shapes_match_device_table():
     assert tab == qtts.TILE_SHAPES
     n_enum = len(re.findall(r"^\s*TILE_G\d+_T\d+(?:_R\d)?\s*=\s*\d+", src, re.M))
     assert n_enum == len(tab)
+
+
+def test_icl_layout_known_answers():
+    """icl_block_layout's own tests (generate_new.rs:869-900) through the
+    host-only export."""
+    assert qtts.icl_layout(8, 8, 23) == (24, 0)      # text shorter: pad branch
+    assert qtts.icl_layout(30, 30, 23) == (24, 37)   # text longer: remainder
+    assert qtts.icl_layout(11, 11, 22) == (23, 0)    # equal lengths
+    assert qtts.icl_layout(1, 1, 23) == (24, 0)      # short reference
+    with pytest.raises(qtts.QttsError):
+        qtts.icl_layout(1, 1, 0)
+
+
+def test_prefix_suffix_split_known_answers():
+    """prefix_suffix_split's own tests (generate_new.rs:986-1001)."""
+    assert qtts.prefix_suffix_split(162, 35, 44) == 127
+    assert qtts.prefix_suffix_split(162, 35, 43) is None   # prefix length mismatch
+    assert qtts.prefix_suffix_split(35, 35, 44) is None    # empty suffix
+    assert qtts.prefix_suffix_split(30, 35, 44) is None    # block shorter than the reference
+    assert qtts.prefix_suffix_split(162, 0, 9) == 162
