@@ -73,9 +73,10 @@ struct Workspace {
 // Buffers of the batched prefill, rows of one prompt chunk.
 struct PrefillWs {
     float *x;          // residual rows [cap_rows][hidden]
-    float *qkv;        // q|k|v rows [cap_rows][32*128]; q rewritten normed + roped
+    float *q;          // normed + roped q rows [cap_rows][16*128]
     float *attn;       // attention rows [cap_rows][16*128]
     float *h;          // silu(gate)*up rows [cap_rows][inter]
+    float *part;       // k-slice partial sums of a projection [cap_rows * prefill_part_floats]
     float *inv;        // per-row 1/rms [cap_rows]
     int cap_rows;
 };
@@ -121,6 +122,7 @@ hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *
 hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,
                              int ldy, hipStream_t s);
 bool prefill_supported(const TalkerDev &m);
+int64_t prefill_part_floats(const TalkerDev &m);
 hipError_t enqueue_gather_rows(const Q4Rows &e, const uint32_t *ids, int n, float *out, int ld, hipStream_t s);
 hipError_t enqueue_codec_frame_rows(const Q4Rows &tcodec, const Q4Rows &pemb, int n_groups, const uint32_t *codes,
                                     int n_frames, float *out, int ld, hipStream_t s);

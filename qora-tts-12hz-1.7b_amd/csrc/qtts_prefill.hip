@@ -56,11 +56,14 @@ k_row_inv(const float *X, int ld, int M, int K, float *inv)
 // x * inv_rms * gamma order) and W dequantised as (nibble - 8) * scale,
 // exact in f32.
 //
-// Workgroup tile 64 rows x 64 columns (two 32-column groups), K in chunks
-// of 32, double-buffered LDS.  Wave w owns rows 32*(w&1)..+32 and the
-// 16-column blocks (w>>1) and (w>>1)+2, so for the gate|up weight (groups
-// interleaved gate, up, gate, up, ...) a lane holds gate and up of the same
-// output column and the SwiGLU epilogue stays in registers.
+// Workgroup tile: 16*MB rows x 128 columns (four 32-column groups), K in
+// chunks of 32 through double-buffered LDS; a weight with S k-slices runs S
+// workgroups per tile, each writing its partial sums (GEMM_PART) for the
+// consumer kernel to add in slice order.  All four waves cover every row
+// of the tile; wave w owns the 16-column blocks c = (w&1) + 4*(w>>1) and
+// c + 2, so for the gate|up weight (groups interleaved gate, up, gate, up)
+// a lane holds gate and up of the same output column and the SwiGLU
+// epilogue stays in registers.
 //
 // v_mfma_f32_16x16x4_f32 lane layout: A operand lane l = A[l%16][l/16],
 // B operand B[l/16][l%16], result element i = D[4*(l/16)+i][l%16].  The
@@ -69,9 +72,9 @@ k_row_inv(const float *X, int ld, int M, int K, float *inv)
 // LDS load (As is [row][k], Bs is [column][k]).
 // ---------------------------------------------------------------------------
 
-constexpr int GM = 64, GN = 64, GK = 32, GLD = GK + 4;
+constexpr int GN = 128, GK = 32, GLD = GK + 4;
 
-enum GemmEpi : int { GEMM_STORE = 0, GEMM_ADD = 1, GEMM_SWIGLU = 2, GEMM_BIAS = 3, GEMM_BIAS_SILU = 4 };
+enum GemmEpi : int { GEMM_STORE = 0, GEMM_PART = 1, GEMM_SWIGLU = 2, GEMM_BIAS = 3, GEMM_BIAS_SILU = 4 };
 
 struct GemmA {
     const float *A;
@@ -79,6 +82,13 @@ struct GemmA {
     const float *inv;        // per-row 1/rms, or null
     const uint16_t *gamma;   // [K] f16, or null
     int M;
+};
+
+struct GemmOut {
+    float *Y;
+    int ldy, ncols;
+    const float *bias;       // GEMM_BIAS*: [ncols]
+    size_t slice_stride;     // GEMM_PART: floats between the slices' blocks
 };
 
 // Address of the 16-byte word and the scale of (row k, group g) in the
@@ -96,11 +106,13 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
     scale = (const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + t * ts.R + r;
 }
 
-template <int EPI>
+template <int MB, int EPI, bool NORM>
 __global__ void __launch_bounds__(256, 2)
-k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm, const float *bias)
+k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 {
-    __shared__ __attribute__((aligned(16))) float As[2][GM * GLD];
+    constexpr int BM = 16 * MB;
+    constexpr int NA = (BM * GK / 4 + 255) / 256;   // 16-byte A slots per thread
+    __shared__ __attribute__((aligned(16))) float As[2][BM * GLD];
     __shared__ __attribute__((aligned(16))) float Bs[2][GN * GLD];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     // Workgroups are dealt round-robin to the 8 XCDs: give each XCD a
@@ -109,120 +121,184 @@ k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm, const
     const int nwg = gridDim.x, id = blockIdx.x;
     const int xcd = id & 7, qq = nwg >> 3, rem = nwg & 7;
     const int logical = xcd * qq + min(xcd, rem) + (id >> 3);
-    const int mt = logical % tm, nt = logical / tm;
-    const int m0 = mt * GM;
+    const int mt = logical % tm, rest = logical / tm;
+    const int sl = rest % S, nt = rest / S;
+    const int m0 = mt * BM;
+    const int nch = w.k / GK, c0 = sl * nch / S, c1 = (sl + 1) * nch / S;
     const TileShape ts = tile_shape(w.cfg);
+    const int P = ts.T / ts.GB;
+    const bool wave_groups = (ts.T / 64) % ts.GB == 0;
 
-    // staging roles: A rows t/4, 4 floats at k = 4*(t&3) and +16;
-    // B row kr = t&31 of group 2*nt + (t>>7), bytes 4*((t>>5)&3)..+4
-    const int ar = t >> 2, ak = (t & 3) * 4;
-    const int am = m0 + ar;
-    const bool arow = am < a.M;
-    const float *Arow = a.A + (size_t)(arow ? am : 0) * a.lda;
-    const float ainv = (a.inv && arow) ? a.inv[am] : 1.0f;
+    // A staging: slot i = t + 256 j (clamped: spare threads repeat the last
+    // slot) covers row i / 8, floats 4 (i % 8)..+4 of the chunk.  Rows past
+    // M load row M-1 and stage zeros.
+    const float *arow[NA];
+    int aoff[NA], akk[NA];
+    float amul[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+        const int slot = min(t + 256 * j, BM * GK / 4 - 1);
+        const int r = slot >> 3, m = m0 + r;
+        arow[j] = a.A + (size_t)min(m, a.M - 1) * a.lda + 4 * (slot & 7);
+        aoff[j] = r * GLD + 4 * (slot & 7);
+        akk[j] = 4 * (slot & 7);
+        amul[j] = m < a.M ? (NORM ? a.inv[min(m, a.M - 1)] : 1.0f) : 0.0f;
+    }
+    // B staging: bytes 4*qw..+4 of row kr, groups 4*nt + gi and + 2 (groups
+    // past G stage zeros)
     const int kr = t & 31, qw = (t >> 5) & 3, gi = t >> 7;
-    const int g = 2 * nt + gi;
-    const bool bvalid = g < w.G;
+    int gt[2], gct[2];
+    bool gok[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int g = 4 * nt + gi + 2 * h;
+        gok[h] = g < w.G;
+        const int gc = min(g, w.G - 1);
+        gct[h] = gc / ts.GB;
+        gt[h] = gc - gct[h] * ts.GB;
+    }
 
-    f32x4 ra0, ra1;
-    uint32_t rb = 0x88888888u, rs = 0;
-    auto fetch = [&](int k0) {
-        if (arow) {
-            ra0 = ld4(Arow + k0 + ak);
-            ra1 = ld4(Arow + k0 + 16 + ak);
-        } else {
-            ra0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            ra1 = ra0;
+    // tile position of (pt, group): one group per wave when wave_groups,
+    // else groups interleaved by thread -- one formula for both
+    const int tA = wave_groups ? 1 : ts.GB, tB = wave_groups ? 64 : 1;
+    struct Fetch {
+        f32x4 ra[NA];
+        uint32_t rg[NA][2];
+        uint32_t rb[2], rs[2];
+    };
+    auto fetch = [&](Fetch &f, int k0) {
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            f.ra[j] = ld4(arow[j] + k0);
+            if (NORM) {
+                const uint2 gv = *(const uint2 *)(a.gamma + k0 + akk[j]);
+                f.rg[j][0] = gv.x;
+                f.rg[j][1] = gv.y;
+            }
         }
-        if (bvalid) {
-            const uint8_t *wp;
-            const uint16_t *sp;
-            tiled_word(w, ts, k0 + kr, g, wp, sp);
-            rb = *(const uint32_t *)(wp + 4 * qw);
-            rs = *sp;
+        // k = k0 + kr: slice s, row r, position pt of the tiled layout;
+        // k0 is a multiple of 32, so only P = 16 splits a chunk over rows
+        const int s = k0 / w.KC, rr0 = k0 - s * w.KC, r0 = rr0 / P, pt0 = rr0 - r0 * P;
+        const int ptk = pt0 + kr;
+        const int r = P < 32 ? r0 + (ptk >> 4) : r0, pt = P < 32 ? (ptk & 15) : ptk;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int tt = (pt >> 6) * 64 * ts.GB + (pt & 63) * tA + gt[h] * tB;
+            const uint8_t *tile = w.data + (size_t)(s * w.CT + gct[h]) * w.tile_bytes;
+            const uint32_t word = *(const uint32_t *)(tile + ((size_t)r * ts.T + tt) * 16 + 4 * qw);
+            const uint16_t sc = *((const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + tt * ts.R + r);
+            f.rb[h] = gok[h] ? word : 0x88888888u;
+            f.rs[h] = gok[h] ? (uint32_t)sc : 0u;
         }
     };
-    auto stage = [&](int buf, int k0) {
-        f32x4 x0 = ra0, x1 = ra1;
-        if (a.inv) {
-            x0 *= ainv;
-            x1 *= ainv;
+    auto stage = [&](const Fetch &f, int buf) {
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            f32x4 x = f.ra[j] * amul[j];
+            if (NORM) {
+                x.x *= h2f(f.rg[j][0] & 0xFFFFu);
+                x.y *= h2f(f.rg[j][0] >> 16);
+                x.z *= h2f(f.rg[j][1] & 0xFFFFu);
+                x.w *= h2f(f.rg[j][1] >> 16);
+            }
+            *(f32x4 *)&As[buf][aoff[j]] = x;
         }
-        if (a.gamma) {
-            const int ka = k0 + ak;
-            x0.x *= h2f(a.gamma[ka]); x0.y *= h2f(a.gamma[ka + 1]);
-            x0.z *= h2f(a.gamma[ka + 2]); x0.w *= h2f(a.gamma[ka + 3]);
-            x1.x *= h2f(a.gamma[ka + 16]); x1.y *= h2f(a.gamma[ka + 17]);
-            x1.z *= h2f(a.gamma[ka + 18]); x1.w *= h2f(a.gamma[ka + 19]);
-        }
-        *(f32x4 *)&As[buf][ar * GLD + ak] = x0;
-        *(f32x4 *)&As[buf][ar * GLD + 16 + ak] = x1;
-        // 8 columns 32*gi + 8*qw + c, c = 0..7: byte c/2, low nibble even c
-        const float sc = h2f(rs);
+        // 8 columns 32*g + 8*qw + c, c = 0..7: byte c/2, low nibble even c
         float *bp = &Bs[buf][(32 * gi + 8 * qw) * GLD + kr];
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int nib = (int)((rb >> (4 * c)) & 15u) - 8;
-            bp[c * GLD] = (float)nib * sc;
+        for (int h = 0; h < 2; h++) {
+            const float sc = h2f(f.rs[h]);
+#pragma unroll
+            for (int c = 0; c < 8; c++) bp[(64 * h + c) * GLD] = (float)((int)((f.rb[h] >> (4 * c)) & 15u) - 8) * sc;
         }
     };
 
     // compute roles
-    const int wm = wv & 1, wn = wv >> 1, r16 = lane & 15, q = lane >> 4;
-    f32x4 acc[2][2];
+    const int r16 = lane & 15, q = lane >> 4;
+    const int cb0 = (wv & 1) + 4 * (wv >> 1);
+    f32x4 acc[MB][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int nch = K / GK;
-    fetch(0);
-    stage(0, 0);
-    __syncthreads();
-    for (int c = 0; c < nch; c++) {
-        const int buf = c & 1;
-        if (c + 1 < nch) fetch((c + 1) * GK);
+    auto mfma = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < GK / 16; kk++) {
-            f32x4 av[2], bv[2];
+            f32x4 av[MB], bv[2];
 #pragma unroll
-            for (int i = 0; i < 2; i++) av[i] = *(const f32x4 *)&As[buf][(32 * wm + 16 * i + r16) * GLD + 16 * kk + 4 * q];
+            for (int i = 0; i < MB; i++) av[i] = *(const f32x4 *)&As[buf][(16 * i + r16) * GLD + 16 * kk + 4 * q];
 #pragma unroll
             for (int j = 0; j < 2; j++)
-                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (wn + 2 * j) + r16) * GLD + 16 * kk + 4 * q];
+                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (cb0 + 2 * j) + r16) * GLD + 16 * kk + 4 * q];
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
-                for (int i = 0; i < 2; i++)
+                for (int i = 0; i < MB; i++)
 #pragma unroll
                     for (int j = 0; j < 2; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
         }
-        if (c + 1 < nch) stage(buf ^ 1, (c + 1) * GK);
+    };
+
+    // Two register sets of fetched chunks: chunk c's loads are issued two
+    // chunks ahead of its MFMAs, one chunk ahead of its dequantisation into
+    // LDS, so no wait on memory sits between MFMAs.  Chunks c0.. alternate
+    // LDS buffers 0/1 and register sets fa/fb (c1 - c0 >= 2).
+    Fetch fa, fb;
+    fetch(fa, c0 * GK);
+    fetch(fb, (c0 + 1) * GK);
+    stage(fa, 0);
+    __syncthreads();
+    int c = c0;
+    for (; c + 3 < c1; c += 2) {
+        fetch(fa, (c + 2) * GK);
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        fetch(fb, (c + 3) * GK);
+        mfma(1);
+        stage(fa, 0);
         __syncthreads();
     }
+    if (c + 2 < c1) {
+        fetch(fa, (c + 2) * GK);
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        mfma(1);
+        stage(fa, 0);
+        __syncthreads();
+        mfma(0);
+    } else {
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        mfma(1);
+    }
 
-    // epilogue: element e of acc[i][j] is row 32wm + 16i + 4q + e, column
-    // 64nt + 16(wn + 2j) + r16
+    // epilogue: element e of acc[i][j] is row 16i + 4q + e of the tile,
+    // column 128nt + 16(cb0 + 2j) + r16
+    float *Y = o.Y + (EPI == GEMM_PART ? (size_t)sl * o.slice_stride : 0);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < MB; i++) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const int m = m0 + 32 * wm + 16 * i + 4 * q + e;
+            const int m = m0 + 16 * i + 4 * q + e;
             if (m >= a.M) continue;
-            float *yr = Y + (size_t)m * ldy;
+            float *yr = Y + (size_t)m * o.ldy;
             if (EPI == GEMM_SWIGLU) {
-                const int col = 32 * nt + 16 * wn + r16;
-                if (col < ncols) yr[col] = silu_f(acc[i][0][e]) * acc[i][1][e];
+                // groups (4nt, 4nt+1) and (4nt+2, 4nt+3) are (gate, up) pairs
+                const int col = 32 * (2 * nt + (wv >> 1)) + 16 * (wv & 1) + r16;
+                if (col < o.ncols) yr[col] = silu_f(acc[i][0][e]) * acc[i][1][e];
             } else {
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    const int col = 64 * nt + 16 * (wn + 2 * j) + r16;
-                    if (col >= ncols) continue;
-                    if (EPI == GEMM_ADD) yr[col] += acc[i][j][e];
-                    else if (EPI == GEMM_BIAS) yr[col] = acc[i][j][e] + bias[col];
-                    else if (EPI == GEMM_BIAS_SILU) yr[col] = silu_f(acc[i][j][e] + bias[col]);
-                    else yr[col] = acc[i][j][e];
+                    const int col = GN * nt + 16 * (cb0 + 2 * j) + r16;
+                    if (col >= o.ncols) continue;
+                    const float v = acc[i][j][e];
+                    if (EPI == GEMM_BIAS) yr[col] = v + o.bias[col];
+                    else if (EPI == GEMM_BIAS_SILU) yr[col] = silu_f(v + o.bias[col]);
+                    else yr[col] = v;
                 }
             }
         }
@@ -230,22 +306,28 @@ k_gemm_q4(GemmA a, Q4Tiled w, int K, float *Y, int ldy, int ncols, int tm, const
 }
 
 // ---------------------------------------------------------------------------
-// q|k|v rows -> QK-norm (talker.rs:89-99), RoPE at start + row (rope.rs:
-// 79-92), K (normed, roped) and V (raw) appended to the paged cache at the
-// same position (talker.rs:419-425).  q is rewritten in place.  One wave per
-// (row, head): heads 0..15 q, 16..23 k, 24..31 v; lane holds dims (l, l+64).
+// q|k|v partial rows (S k-slices, added in slice order) -> QK-norm
+// (talker.rs:89-99), RoPE at start + row (rope.rs:79-92), q rows out, K
+// (normed, roped) and V (raw) appended to the paged cache at the same
+// position (talker.rs:419-425).  One wave per (row, head): heads 0..15 q,
+// 16..23 k, 24..31 v; lane holds dims (l, l+64).
 // ---------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(256)
-k_prefill_qkv_post(float *qkv, int ldq, int M, int64_t start, const uint16_t *qn_g, const uint16_t *kn_g,
-                   const float *rope_cos, const float *rope_sin, KvPaged kv, int layer)
+k_prefill_qkv_post(const float *part, int S, size_t slice_stride, int ldp, int M, int64_t start,
+                   const uint16_t *qn_g, const uint16_t *kn_g, const float *rope_cos, const float *rope_sin,
+                   KvPaged kv, int layer, float *q, int ldq)
 {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x, hh = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (m >= M) return;
     const int64_t pos = start + m;
-    float *row = qkv + (size_t)m * ldq + hh * HEAD_DIM;
-    const float x0 = row[lane], x1 = row[lane + 64];
+    const float *row = part + (size_t)m * ldp + hh * HEAD_DIM;
+    float x0 = row[lane], x1 = row[lane + 64];
+    for (int s = 1; s < S; s++) {
+        x0 += row[s * slice_stride + lane];
+        x1 += row[s * slice_stride + lane + 64];
+    }
     if (hh >= 24) {
         float *vp = kv_ptr(kv, layer, (int)pos, hh - 24, 1);
         vp[lane] = x0;
@@ -258,14 +340,39 @@ k_prefill_qkv_post(float *qkv, int ldq, int M, int64_t start, const uint16_t *qn
     const float n0 = x0 * inv * h2f(gam[lane]), n1 = x1 * inv * h2f(gam[lane + 64]);
     const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
     const float r0 = n0 * cs - n1 * sn, r1 = n1 * cs + n0 * sn;
-    if (hh < 16) {
-        row[lane] = r0;
-        row[lane + 64] = r1;
-    } else {
-        float *kp = kv_ptr(kv, layer, (int)pos, hh - 16, 0);
-        kp[lane] = r0;
-        kp[lane + 64] = r1;
+    float *out = hh < 16 ? q + (size_t)m * ldq + hh * HEAD_DIM : kv_ptr(kv, layer, (int)pos, hh - 16, 0);
+    out[lane] = r0;
+    out[lane + 64] = r1;
+}
+
+// ---------------------------------------------------------------------------
+// Residual add of a projection's k-slice partials (x += sum over slices, in
+// slice order: talker.rs:461, 474) fused with the next RMSNorm's 1/rms of
+// the updated row (gemv.rs:445-454).  One workgroup per row.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_resid_add_inv(float *x, int ldx, const float *part, int S, size_t slice_stride, int ldp, int H, float *inv)
+{
+    __shared__ float red[4];
+    const int t = threadIdx.x, m = blockIdx.x;
+    float *xr = x + (size_t)m * ldx;
+    const float *pr = part + (size_t)m * ldp;
+    float ss = 0.0f;
+    for (int j = 4 * t; j < H; j += 1024) {
+        f32x4 p = ld4(pr + j);
+        for (int s = 1; s < S; s++) p += ld4(pr + s * slice_stride + j);
+        const f32x4 v = ld4(xr + j) + p;
+        *(f32x4 *)(xr + j) = v;
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
     }
+    ss = wave_sum_dpp(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    if (t == 0) inv[m] = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)H + 1e-6f);
 }
 
 // ---------------------------------------------------------------------------
@@ -399,19 +506,65 @@ __global__ void k_fill_rows(float *x, int64_t n, uint32_t seed)
 
 static bool gemm_shape_ok(const Q4Tiled &w, int K)
 {
-    return K == w.k && K % GK == 0 && K >= GK;
+    return K == w.k && K % GK == 0 && K >= 2 * GK;   // two chunks at least per k-slice
+}
+
+// Rows per tile, 16 * MB: one tile when M <= 80; else MB in 3..5 with the
+// least padding (larger MB on ties: each weight tile is dequantised once per
+// row tile).
+static int pick_mb(int M)
+{
+    if (M <= 80) return (M + 15) / 16;
+    int best = 5, pad = 1 << 30;
+    for (int mb = 5; mb >= 3; mb--) {
+        const int p = (M + 16 * mb - 1) / (16 * mb) * 16 * mb;
+        if (p < pad) {
+            pad = p;
+            best = mb;
+        }
+    }
+    return best;
+}
+
+// k-slices of a weight for the prefill projections whose consumer adds
+// partials (q|k|v, o, down): about 96 workgroups per row tile.  A function
+// of the weight alone, so a row's sums do not depend on the prompt length
+// (prefix + suffix prefill stays bit-identical to one full prefill).
+static int part_slices(const Q4Tiled &w)
+{
+    const int tn = (w.G * 32 + GN - 1) / GN, nch = w.k / GK;
+    int S = std::max(1, (96 + tn / 2) / tn);
+    S = std::min(S, 8);
+    while (S > 1 && nch / S < 8) S--;
+    return S;
+}
+
+template <int MB, int EPI>
+static hipError_t launch_gemm_mb(const GemmA &a, const Q4Tiled &w, const GemmOut &o, int S, hipStream_t s)
+{
+    const int tm = (a.M + 16 * MB - 1) / (16 * MB), tn = (w.G * 32 + GN - 1) / GN;
+    if (a.inv)
+        hipLaunchKernelGGL((k_gemm_q4<MB, EPI, true>), dim3(tm * tn * S), dim3(256), 0, s, a, w, o, tm, S);
+    else
+        hipLaunchKernelGGL((k_gemm_q4<MB, EPI, false>), dim3(tm * tn * S), dim3(256), 0, s, a, w, o, tm, S);
+    return hipGetLastError();
 }
 
 template <int EPI>
-static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, float *Y, int ldy, int ncols, hipStream_t s,
-                              const float *bias = nullptr)
+static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, const GemmOut &o, int S, hipStream_t s)
 {
-    if (!gemm_shape_ok(w, w.k) || a.M < 1 || a.lda % 4) return hipErrorInvalidValue;
-    if (EPI == GEMM_SWIGLU && !w.interleave) return hipErrorInvalidValue;
-    if ((EPI == GEMM_BIAS || EPI == GEMM_BIAS_SILU) && !bias) return hipErrorInvalidValue;
-    const int tm = (a.M + GM - 1) / GM, tn = (w.G * 32 + GN - 1) / GN;
-    hipLaunchKernelGGL(k_gemm_q4<EPI>, dim3(tm * tn), dim3(256), 0, s, a, w, w.k, Y, ldy, ncols, tm, bias);
-    return hipGetLastError();
+    if (!gemm_shape_ok(w, w.k) || a.M < 1 || a.lda % 4 || S < 1 || S > w.k / (2 * GK)) return hipErrorInvalidValue;
+    if (EPI == GEMM_SWIGLU && (!w.interleave || w.G % 4)) return hipErrorInvalidValue;
+    if ((EPI == GEMM_BIAS || EPI == GEMM_BIAS_SILU) && !o.bias) return hipErrorInvalidValue;
+    if (EPI != GEMM_PART && S != 1) return hipErrorInvalidValue;
+    if (!a.inv != !a.gamma) return hipErrorInvalidValue;   // a fused norm has both
+    switch (pick_mb(a.M)) {
+    case 1: return launch_gemm_mb<1, EPI>(a, w, o, S, s);
+    case 2: return launch_gemm_mb<2, EPI>(a, w, o, S, s);
+    case 3: return launch_gemm_mb<3, EPI>(a, w, o, S, s);
+    case 4: return launch_gemm_mb<4, EPI>(a, w, o, S, s);
+    default: return launch_gemm_mb<5, EPI>(a, w, o, S, s);
+    }
 }
 
 bool gemm_supported(const Q4Tiled &w)
@@ -422,7 +575,7 @@ bool gemm_supported(const Q4Tiled &w)
 hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s)
 {
     const GemmA a{X, w.k, nullptr, nullptr, rows};
-    return launch_gemm<GEMM_STORE>(a, w, Y, ldy, std::min(ldy, w.G * 32), s);
+    return launch_gemm<GEMM_STORE>(a, w, GemmOut{Y, ldy, std::min(ldy, w.G * 32), nullptr, 0}, 1, s);
 }
 
 // Y = X W + bias, optionally through SiLU (the text projection's fc1 / fc2,
@@ -431,9 +584,8 @@ hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const f
                              int ldy, hipStream_t s)
 {
     const GemmA a{X, w.k, nullptr, nullptr, rows};
-    const int ncols = std::min(ldy, w.n);
-    return silu ? launch_gemm<GEMM_BIAS_SILU>(a, w, Y, ldy, ncols, s, bias)
-                : launch_gemm<GEMM_BIAS>(a, w, Y, ldy, ncols, s, bias);
+    const GemmOut o{Y, ldy, std::min(ldy, w.n), bias, 0};
+    return silu ? launch_gemm<GEMM_BIAS_SILU>(a, w, o, 1, s) : launch_gemm<GEMM_BIAS>(a, w, o, 1, s);
 }
 
 bool prefill_supported(const TalkerDev &m)
@@ -443,10 +595,24 @@ bool prefill_supported(const TalkerDev &m)
         const LayerDev &L = m.layers[l];
         if (!gemm_shape_ok(L.qkv, m.hidden) || !gemm_shape_ok(L.o, 16 * HEAD_DIM) ||
             !gemm_shape_ok(L.gate_up, m.hidden) || !gemm_shape_ok(L.down, m.inter) || !L.gate_up.interleave ||
-            L.qkv.G * 32 < 32 * HEAD_DIM || L.gate_up.G * 16 < m.inter)
+            L.gate_up.G % 4 || L.qkv.G * 32 < 32 * HEAD_DIM || L.gate_up.G * 16 < m.inter ||
+            L.o.G * 32 < m.hidden || L.down.G * 32 < m.hidden)
             return false;
     }
     return true;
+}
+
+// Floats per prompt row of the k-slice partials buffer.
+int64_t prefill_part_floats(const TalkerDev &m)
+{
+    int64_t f = 0;
+    for (int l = 0; l < m.n_layers; l++) {
+        const LayerDev &L = m.layers[l];
+        f = std::max<int64_t>(f, (int64_t)part_slices(L.qkv) * L.qkv.G * 32);
+        f = std::max<int64_t>(f, (int64_t)part_slices(L.o) * L.o.G * 32);
+        f = std::max<int64_t>(f, (int64_t)part_slices(L.down) * L.down.G * 32);
+    }
+    return f;
 }
 
 hipError_t enqueue_fill_rows(float *x, int64_t n, uint32_t seed, hipStream_t s)
@@ -466,8 +632,17 @@ hipError_t enqueue_row_inv(const float *X, int ld, int M, int K, float *inv, hip
 hipError_t enqueue_gemm_gateup(const TalkerDev &m, const PrefillWs &pw, int l, int M, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
-    return launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, m.hidden, pw.inv, L.post_norm, M}, L.gate_up, pw.h, m.inter,
-                                    m.inter, s);
+    return launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, m.hidden, pw.inv, L.post_norm, M}, L.gate_up,
+                                    GemmOut{pw.h, m.inter, m.inter, nullptr, 0}, 1, s);
+}
+
+// A projection into k-slice partials: slice s of row m at part[s * M * ld +
+// m * ld], ld = the weight's padded width.
+static hipError_t gemm_parts(const GemmA &a, const Q4Tiled &w, const PrefillWs &pw, int *S, int *ld, hipStream_t s)
+{
+    *S = part_slices(w);
+    *ld = w.G * 32;
+    return launch_gemm<GEMM_PART>(a, w, GemmOut{pw.part, *ld, *ld, nullptr, (size_t)a.M * *ld}, *S, s);
 }
 
 // Rows pw.x[0..M) at positions start..start+M-1 through every layer; the
@@ -477,25 +652,30 @@ hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M
                                   hipStream_t s)
 {
     if (M < 1 || M > pw.cap_rows) return hipErrorInvalidValue;
-    const int H = m.hidden, QKV = 32 * HEAD_DIM;
-    const dim3 rows4((M + 3) / 4);
+    const int H = m.hidden, A = 16 * HEAD_DIM;
+    int S, ld;
+    PCHK(enqueue_row_inv(pw.x, H, M, H, pw.inv, s));
     for (int l = 0; l < m.n_layers; l++) {
         const LayerDev &L = m.layers[l];
-        hipLaunchKernelGGL(k_row_inv, rows4, dim3(256), 0, s, pw.x, H, M, H, pw.inv);
+        // q|k|v (input norm fused), QK-norm + RoPE + KV append, attention
+        PCHK(gemm_parts(GemmA{pw.x, H, pw.inv, L.input_norm, M}, L.qkv, pw, &S, &ld, s));
+        hipLaunchKernelGGL(k_prefill_qkv_post, dim3(M, 8), dim3(256), 0, s, pw.part, S, (size_t)M * ld, ld, M, start,
+                           L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, m.kv, l, pw.q, A);
         PCHK(hipGetLastError());
-        PCHK(launch_gemm<GEMM_STORE>(GemmA{pw.x, H, pw.inv, L.input_norm, M}, L.qkv, pw.qkv, QKV, QKV, s));
-        hipLaunchKernelGGL(k_prefill_qkv_post, dim3(M, 8), dim3(256), 0, s, pw.qkv, QKV, M, start, L.q_norm,
-                           L.k_norm, m.rope_cos, m.rope_sin, m.kv, l);
+        hipLaunchKernelGGL(k_prefill_attn, dim3(M, 8), dim3(256), 0, s, pw.q, A, M, start, m.kv, l, pw.attn, A);
         PCHK(hipGetLastError());
-        hipLaunchKernelGGL(k_prefill_attn, dim3(M, 8), dim3(256), 0, s, pw.qkv, QKV, M, start, m.kv, l, pw.attn,
-                           16 * HEAD_DIM);
+        // o-proj, residual, post-attention norm
+        PCHK(gemm_parts(GemmA{pw.attn, A, nullptr, nullptr, M}, L.o, pw, &S, &ld, s));
+        hipLaunchKernelGGL(k_resid_add_inv, dim3(M), dim3(256), 0, s, pw.x, H, pw.part, S, (size_t)M * ld, ld, H,
+                           pw.inv);
         PCHK(hipGetLastError());
-        PCHK(launch_gemm<GEMM_ADD>(GemmA{pw.attn, 16 * HEAD_DIM, nullptr, nullptr, M}, L.o, pw.x, H, H, s));
-        hipLaunchKernelGGL(k_row_inv, rows4, dim3(256), 0, s, pw.x, H, M, H, pw.inv);
+        // gate|up with SwiGLU, down, residual, next layer's input norm
+        PCHK(launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, H, pw.inv, L.post_norm, M}, L.gate_up,
+                                      GemmOut{pw.h, m.inter, m.inter, nullptr, 0}, 1, s));
+        PCHK(gemm_parts(GemmA{pw.h, m.inter, nullptr, nullptr, M}, L.down, pw, &S, &ld, s));
+        hipLaunchKernelGGL(k_resid_add_inv, dim3(M), dim3(256), 0, s, pw.x, H, pw.part, S, (size_t)M * ld, ld, H,
+                           pw.inv);
         PCHK(hipGetLastError());
-        PCHK(launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, H, pw.inv, L.post_norm, M}, L.gate_up, pw.h, m.inter, m.inter,
-                                      s));
-        PCHK(launch_gemm<GEMM_ADD>(GemmA{pw.h, m.inter, nullptr, nullptr, M}, L.down, pw.x, H, H, s));
     }
     hipLaunchKernelGGL(k_final_rms, dim3(1), dim3(256), 0, s, pw.x + (size_t)(M - 1) * H, m.final_norm, H,
                        hidden_out);

@@ -464,16 +464,17 @@ static int ensure_prefill(qtts_ctx *c, int rows)
     if (c->pf_mem) hipFree(c->pf_mem);
     c->pf_mem = nullptr;
     c->pf = PrefillWs{};
-    const int64_t H = c->tm.hidden, QKV = 32 * HEAD_DIM, A = 16 * HEAD_DIM, I = c->tm.inter;
-    const int64_t per_row = H + QKV + A + I + 1;
+    const int64_t H = c->tm.hidden, A = 16 * HEAD_DIM, I = c->tm.inter, P = prefill_part_floats(c->tm);
+    const int64_t per_row = H + A + A + I + P + 1;
     float *base = nullptr;
     HIPCHK(c, hipMalloc(&base, (size_t)rows * per_row * sizeof(float)));
     c->pf_mem = base;
     c->pf.x = base;
-    c->pf.qkv = c->pf.x + rows * H;
-    c->pf.attn = c->pf.qkv + rows * QKV;
+    c->pf.q = c->pf.x + rows * H;
+    c->pf.attn = c->pf.q + rows * A;
     c->pf.h = c->pf.attn + rows * A;
-    c->pf.inv = c->pf.h + rows * I;
+    c->pf.part = c->pf.h + rows * I;
+    c->pf.inv = c->pf.part + rows * P;
     c->pf.cap_rows = rows;
     return QTTS_OK;
 }
