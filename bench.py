@@ -59,6 +59,68 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+# Decode GEMV shapes (k -> n, fused as the frame runs them) for the per-shape
+# sweep of the standalone Q4 GEMV.
+SWEEP_SHAPES = [("talker q|k|v", 2048, 4096), ("talker o", 2048, 2048), ("talker gate|up", 2048, 12288),
+                ("talker down", 6144, 2048), ("codec head", 2048, 3072), ("predictor q|k|v", 1024, 4096),
+                ("predictor gate|up", 1024, 6144), ("predictor down", 3072, 1024), ("predictor head", 1024, 2048)]
+
+
+def gemv_sweep(ctx, synth, pool_bytes=320 << 20):
+    """Standalone Q4 GEMV GB/s on each decode shape, cycling a pool of device
+    copies larger than the 256 MB last-level cache."""
+    rng = np.random.Generator(np.random.PCG64(5))
+    out = {}
+    for name, k, n in SWEEP_SHAPES:
+        w = synth.q4_random(rng, k, n)
+        copies = max(8, -(-pool_bytes // int(k * n * 0.5625)))
+        pool = [ctx.upload(w) for _ in range(copies)]
+        us, b = ctx.time_gemv(pool, 4 * copies)
+        for d in pool:
+            d.free()
+        out[f"{name} {k}x{n}"] = {"us": round(us, 2), "gbs": round(b / us / 1e3, 1),
+                                   "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def host_info():
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    isa = "avx512f" if "avx512f" in flags else ("avx2" if "avx2" in flags else "other")
+    return {"cpu": model, "nproc": os.cpu_count(), "isa": isa}
+
+
+def cpu_gemv(seconds=3.0):
+    """The oracle's restatement of gemv_q4 (AVX2 kernel + chunk/pool policy)
+    on the 2048 x 6144 GEMV: min(nproc, 16) workers and one thread."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    from qtts import synth
+    rng = np.random.Generator(np.random.PCG64(1))
+    w = synth.q4_random(rng, 2048, 6144)
+    x = rng.standard_normal(2048).astype(np.float32)
+    nbytes = 2048 * 6144 * 0.5625 + 4 * 2048 + 4 * 6144
+    res = {}
+    for label, workers in (("pool", min(os.cpu_count() or 1, 16)), ("one_thread", 1)):
+        oracle.set_workers(workers, workers)
+        oracle.gemv(x, w)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 2:
+            oracle.gemv(x, w)
+            n += 1
+        us = (time.perf_counter() - t0) / n * 1e6
+        res[label] = {"threads": workers, "us": round(us, 1), "gbs": round(nbytes / us / 1e3, 2)}
+    return res
+
+
 def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds):
     """Oracle (C restatement of the reference's AVX2 CPU path, gemv pool of
     min(nproc, 16) workers) timed on a bounded sample: frames at KV ~kv_len
@@ -119,6 +181,7 @@ def main():
     ap.add_argument("--gemv-copies", type=int, default=64)
     ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
     ap.add_argument("--prefill-only", action="store_true", help="time only the matrix-core prefill")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape GEMV sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -215,12 +278,17 @@ def main():
 
     lg, hd, _, _ = ctx.gen_state()
     kernels["icl_prefill"] = time_prefill(ctx, args.layers)   # rewrites the KV cache
+    if not args.no_sweep:
+        kernels["q4_gemv_shapes"] = gemv_sweep(ctx, synth)
+        log("GEMV sweep: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in kernels["q4_gemv_shapes"].items()))
 
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline (oracle)")
         cpu = cpu_baseline(talker, pred, lg, hd, pad, 2048, args.cpu_seconds)
-        log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads")
+        cpu["gemv_2048x6144"] = cpu_gemv()
+        cpu["host"] = host_info()
+        log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads; GEMV {cpu['gemv_2048x6144']}")
 
     out = {
         "metric": "codec frames/s (talker+predictor, batch 1) @KV 2048; Q4 GEMV HBM GB/s (% peak)",

@@ -175,6 +175,13 @@ int qtts_model_dims(qtts_ctx *ctx, int32_t *talker_hidden,
 int qtts_talker_step(qtts_ctx *ctx, const float *embedding, int64_t position,
                      float *hidden_out, float *logits_out, int flags);
 
+/* Legacy `forward_talker_decode` (talker.rs:161-258, the loop of
+ * generate.rs:185-235): embeds `token` itself (text projection when
+ * is_text, else the codec table), runs one step at `position` and writes
+ * the final-normed hidden (no codec head). */
+int qtts_talker_decode_token(qtts_ctx *ctx, uint32_t token, int is_text,
+                             int64_t position, float *hidden_out, int flags);
+
 /* Prefill `seq` rows of pre-built embeddings at positions
  * start_pos..start_pos+seq-1 on top of the cached prefix:
  * `prefill_talker_raw_from` (talker.rs:379-482).  Requires

@@ -841,15 +841,9 @@ extern "C" int qtts_model_dims(qtts_ctx *c, int32_t *th, int32_t *tv, int32_t *t
 // talker
 // ---------------------------------------------------------------------------
 
-extern "C" int qtts_talker_step(qtts_ctx *c, const float *emb, int64_t position, float *hidden_out,
-                                float *logits_out, int flags)
+// One talker step on the input already in ws.x.
+static int talker_step_staged(qtts_ctx *c, int64_t position, float *hidden_out, float *logits_out, int flags)
 {
-    NEED_MODEL(c);
-    if (!emb || position < 0) return QTTS_ERR_INVALID;
-    if (position >= c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
-    if (c->h_st->kv_len + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full");
-    c->gen_started = false;
-    RCHK(stage_in(c, emb, c->tm.hidden, c->ws.x, flags));
     c->h_st->position = position;
     HIPCHK(c, hipMemcpyAsync(&c->st_gen->position, &c->h_st->position, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
     HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, c->stream));
@@ -859,6 +853,55 @@ extern "C" int qtts_talker_step(qtts_ctx *c, const float *emb, int64_t position,
     c->h_st->kv_len += 1;
     c->h_st->position = position + 1;
     return QTTS_OK;
+}
+
+static int step_checks(qtts_ctx *c, int64_t position)
+{
+    if (position < 0) return QTTS_ERR_INVALID;
+    if (position >= c->tm.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the RoPE table");
+    if (c->h_st->kv_len + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full");
+    c->gen_started = false;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_talker_step(qtts_ctx *c, const float *emb, int64_t position, float *hidden_out,
+                                float *logits_out, int flags)
+{
+    NEED_MODEL(c);
+    if (!emb) return QTTS_ERR_INVALID;
+    RCHK(step_checks(c, position));
+    RCHK(stage_in(c, emb, c->tm.hidden, c->ws.x, flags));
+    return talker_step_staged(c, position, hidden_out, logits_out, flags);
+}
+
+// embed_text_token (talker.rs:105-116) of one id into a device row, one
+// GEMV pass per projection.
+static int text_token_row(qtts_ctx *c, uint32_t token, float *out_dev)
+{
+    const TalkerDev &m = c->tm;
+    if ((int64_t)token >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", token);
+    float *raw = c->d_io, *h1 = c->d_io + 2 * std::max(m.text_hidden, m.hidden);
+    Q4Rows e = m.text_rows;
+    e.n = m.text_hidden;
+    HIPCHK(c, enqueue_embed_row(e, nullptr, token, raw, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc1, raw, h1, m.text_fc1_bias, c->ws.part_proj, c->stream));
+    HIPCHK(c, enqueue_silu(h1, m.text_fc1.n, c->stream));
+    HIPCHK(c, enqueue_gemv_store(m.text_fc2, h1, out_dev, m.text_fc2_bias, c->ws.part_proj, c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_talker_decode_token(qtts_ctx *c, uint32_t token, int is_text, int64_t position,
+                                        float *hidden_out, int flags)
+{
+    NEED_MODEL(c);
+    RCHK(step_checks(c, position));
+    if (is_text) {
+        RCHK(text_token_row(c, token, c->ws.x));
+    } else {
+        if ((int64_t)token >= c->tm.codec_rows.rows) return fail(c, QTTS_ERR_INVALID, "codec token %u out of range", token);
+        HIPCHK(c, enqueue_embed_row(c->tm.codec_rows, nullptr, token, c->ws.x, c->stream));
+    }
+    return talker_step_staged(c, position, hidden_out, nullptr, flags);
 }
 
 extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int64_t start_pos, float *hidden_out,
@@ -910,16 +953,8 @@ extern "C" int qtts_embed_text_token(qtts_ctx *c, uint32_t token, float *out, in
 {
     NEED_MODEL(c);
     if (!out) return QTTS_ERR_INVALID;
-    const TalkerDev &m = c->tm;
-    if ((int64_t)token >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", token);
-    float *raw = c->d_io, *h1 = c->d_io + 2 * std::max(m.text_hidden, m.hidden), *o = c->d_io2;
-    Q4Rows e = m.text_rows;
-    e.n = m.text_hidden;
-    HIPCHK(c, enqueue_embed_row(e, nullptr, token, raw, c->stream));
-    HIPCHK(c, enqueue_gemv_store(m.text_fc1, raw, h1, m.text_fc1_bias, c->ws.part_proj, c->stream));
-    HIPCHK(c, enqueue_silu(h1, m.text_fc1.n, c->stream));
-    HIPCHK(c, enqueue_gemv_store(m.text_fc2, h1, o, m.text_fc2_bias, c->ws.part_proj, c->stream));
-    RCHK(stage_out(c, o, m.text_fc2.n, out, flags));
+    RCHK(text_token_row(c, token, c->d_io2));
+    RCHK(stage_out(c, c->d_io2, c->tm.text_fc2.n, out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
 }

@@ -55,6 +55,7 @@ SIGNATURES = {
     "qtts_model_load_qtts": ([c_void_p, c_char_p], c_int),
     "qtts_model_dims": ([c_void_p] + [POINTER(c_int32)] * 6, c_int),
     "qtts_talker_step": ([c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int], c_int),
+    "qtts_talker_decode_token": ([c_void_p, c_uint32, c_int, c_int64, c_void_p, c_int], c_int),
     "qtts_talker_prefill": ([c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int], c_int),
     "qtts_codec_head": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_embed_text_token": ([c_void_p, c_uint32, c_void_p, c_int], c_int),
@@ -216,6 +217,12 @@ class Context:
         lg = np.empty(self.vocab, np.float32)
         self._check(self.lib.qtts_talker_step(self.h, ptr(e), position, ptr(hid), ptr(lg), 0))
         return np.concatenate([hid, lg])
+
+    def forward_talker_decode(self, token, is_text, position):
+        """Legacy `forward_talker_decode` (talker.rs:161-258): final-normed hidden."""
+        hid = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_talker_decode_token(self.h, token, 1 if is_text else 0, position, ptr(hid), 0))
+        return hid
 
     def prefill_talker_raw_from(self, X, start_pos, path=None):
         """`prefill_talker_raw_from` (talker.rs:379-482): last row's normed

@@ -195,6 +195,30 @@ def test_prefill_then_steps(loaded):
     om.kv_reset()
 
 
+def test_forward_talker_decode_legacy(loaded):
+    """Legacy forward_talker_decode (talker.rs:161-258): token embedded on the
+    device, then one step; bit-identical to a step on the embedding API's
+    row, within the bar of the oracle."""
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(71))
+    X = rng.standard_normal((20, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    ctx.prefill_talker_raw_from(X, 0)
+    om.prefill(X, 0)
+    for pos, (tok, is_text) in enumerate(((2149, False), (300, True), (17, False)), start=20):
+        h = ctx.forward_talker_decode(tok, is_text, pos)
+        emb = om.embed_text_token(tok) if is_text else om.embed_codec_token(tok)
+        ok, e = close(h, om.forward_with_embedding(emb, pos)[: t.hidden])
+        assert ok, f"token {tok}: rel err {e}"
+        ctx.kv_truncate(pos)
+        dev_emb = ctx.embed_text_token(tok) if is_text else ctx.embed_codec_token(tok)
+        h2 = ctx.forward_with_embedding(dev_emb, pos)[: t.hidden]
+        assert np.array_equal(bits(h), bits(h2))
+    ctx.kv_reset()
+    om.kv_reset()
+
+
 def test_text_and_codec_embeddings(loaded):
     ctx, om, t, p = loaded
     for tok in (0, 7, 511):
