@@ -139,7 +139,9 @@ int qtts_gemv_q4(qtts_ctx *ctx, const qtts_w *w, const float *x, float *y,
                  int flags);
 
 /* Y[rows][n] = X[rows][k] * W.  Replaces `gemm` (gemv.rs:157-162) ->
- * `gemm_q4` (gemv.rs:349-412): two rows share each pass over W. */
+ * `gemm_q4` (gemv.rs:349-412).  From 16 rows (k a multiple of 32, at least
+ * 64) an f32 matrix-core GEMM; fewer rows run the GEMV, two rows per pass
+ * over W.  flags may force either path (QTTS_PATH_*). */
 int qtts_gemm_q4(qtts_ctx *ctx, const qtts_w *w, const float *X, int64_t rows,
                  float *Y, int flags);
 
@@ -185,7 +187,10 @@ int qtts_talker_decode_token(qtts_ctx *ctx, uint32_t token, int is_text,
 /* Prefill `seq` rows of pre-built embeddings at positions
  * start_pos..start_pos+seq-1 on top of the cached prefix:
  * `prefill_talker_raw_from` (talker.rs:379-482).  Requires
- * kv_len == start_pos.  Writes the last row's final-normed hidden. */
+ * kv_len == start_pos.  Writes the last row's final-normed hidden.  From
+ * 16 rows the layers run as batched matrix-core GEMMs (chunks of up to
+ * 1024 rows); fewer rows go one by one through the decode kernels.  flags
+ * may force either path (QTTS_PATH_*). */
 int qtts_talker_prefill(qtts_ctx *ctx, const float *X, int64_t seq,
                         int64_t start_pos, float *hidden_out, int flags);
 
