@@ -7,7 +7,7 @@
 //   RMSNorm + residual gemv.rs:445-454, talker.rs:334-349 (ProResidRms)
 //   QK-norm + RoPE     talker.rs:286-297, rope.rs:79-92 (k_talker_attn prologue)
 //   KV append          talker.rs:299-302    (k_talker_attn, paged)
-//   decode attention   talker.rs:304-331    (k_talker_attn + k_attn_combine)
+//   decode attention   talker.rs:304-331    (k_talker_attn + the o-proj's ProAttnCombine)
 //   SwiGLU             talker.rs:338-349    (EpiSwiglu / ProSwiglu)
 //   predictor layers   code_predictor.rs:345-513 (k_pred_attn et al.)
 //   argmax             code_predictor.rs:335-341 (k_argmax)
@@ -213,6 +213,84 @@ struct ProPlain {
                 v.w = r + 3 < k ? v.w : 0.0f;
                 *(f32x4 *)(xs + 4 * i) = v;
             }
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const {}
+};
+
+// The talker o-proj's input rows from the per-page attention partials of
+// k_talker_attn (flash-decoding): row h*128 + d of the attention output is
+//   sum_c w_c acc[c][h][d] / sum_c w_c l[c][h],  w_c = exp(m[c][h] - max m),
+// the reference's softmax over the whole row (talker.rs:304-331, softmax_raw
+// gemv.rs:471-482) regrouped by page.  Thread t owns rows t + e*T of the
+// tile's k-slice; the rows of a wave share one head, so the page maxima and
+// sums are wave-uniform loads.  The cache length is read in the fetch stage
+// (a scalar load) and the pages after the weights are in flight.
+struct ProAttnCombine {
+    static constexpr int PF = 8;   // pages of P.V fetched ahead of the weights
+    const float *am, *al;    // [16 heads][MAX_CHUNKS] page max / exp-sum
+    const float *aacc;       // [MAX_CHUNKS][16][128] page P.V
+    const DevState *st;
+    int slot_ovr;            // >= 0: the row's KV slot (prefill rows), else st->kv_len
+    template <int T, int KC>
+    struct Fetch {
+        int L;
+        float m[KC / T][2], l[KC / T][2], a[KC / T][PF];
+    };
+    // every load here is in bounds whatever the cache length (pages past it
+    // are masked in load), so all are issued before the weights
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        static_assert(KC % T == 0 && KC % HEAD_DIM == 0 && MAX_CHUNKS == 128, "rows per thread, pages per lane");
+        const int lane = threadIdx.x & 63;
+        f.L = (slot_ovr >= 0 ? slot_ovr : st->kv_len) + 1;
+#pragma unroll
+        for (int e = 0; e < KC / T; e++) {
+            const int row = k0 + threadIdx.x + e * T;   // rows past the 16 heads (a slice's tail) read head 15
+            const int h = __builtin_amdgcn_readfirstlane(min(row / HEAD_DIM, 15)), d = row & (HEAD_DIM - 1);
+            f.m[e][0] = am[h * MAX_CHUNKS + lane];
+            f.m[e][1] = am[h * MAX_CHUNKS + 64 + lane];
+            f.l[e][0] = al[h * MAX_CHUNKS + lane];
+            f.l[e][1] = al[h * MAX_CHUNKS + 64 + lane];
+#pragma unroll
+            for (int j = 0; j < PF; j++) f.a[e][j] = aacc[((size_t)j * 16 + h) * HEAD_DIM + d];
+        }
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        const int lane = threadIdx.x & 63;
+        const int C = (f.L + KV_PAGE - 1) / KV_PAGE;
+        const bool v0 = lane < C, v1 = lane + 64 < C;
+#pragma unroll
+        for (int e = 0; e < KC / T; e++) {
+            const int i = threadIdx.x + e * T, row = k0 + i;
+            const int h = __builtin_amdgcn_readfirstlane(min(row / HEAD_DIM, 15)), d = row & (HEAD_DIM - 1);
+            // lane j holds pages j and j + 64
+            const float m0 = v0 ? f.m[e][0] : -INFINITY, m1 = v1 ? f.m[e][1] : -INFINITY;
+            const float M = wave_max_dpp(fmaxf(m0, m1));
+            const float w0 = v0 ? expf(m0 - M) : 0.0f, w1 = v1 ? expf(m1 - M) : 0.0f;
+            const float Ls = wave_sum_dpp(w0 * (v0 ? f.l[e][0] : 0.0f) + w1 * (v1 ? f.l[e][1] : 0.0f));
+            float o = 0.0f;
+#pragma unroll
+            for (int j = 0; j < PF; j++) {
+                const float wc = lane_value(w0, j);
+                o = j < C ? fmaf(wc, f.a[e][j], o) : o;
+            }
+            const float *ah = aacc + (size_t)h * HEAD_DIM + d;
+            for (int c0 = PF; c0 < C; c0 += 8) {
+                float av[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) av[j] = ah[(size_t)min(c0 + j, C - 1) * 16 * HEAD_DIM];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const int c = c0 + j;
+                    const float wc = c < 64 ? lane_value(w0, c & 63) : lane_value(w1, c & 63);
+                    o = c < C ? fmaf(wc, av[j], o) : o;
+                }
+            }
+            xs[i] = row < 16 * HEAD_DIM ? o / Ls : 0.0f;
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -1143,35 +1221,12 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             const float o = (ored[0][hh][d] + ored[1][hh][d]) + (ored[2][hh][d] + ored[3][hh][d]);
             aacc[((size_t)c * 16 + 2 * h + hh) * HEAD_DIM + d] = o;
             if (d == 0) {
-                am[c * 16 + 2 * h + hh] = hh ? m1 : m0;
-                al[c * 16 + 2 * h + hh] = hh ? (wred[0][1][1] + wred[1][1][1]) + (wred[2][1][1] + wred[3][1][1])
+                am[(2 * h + hh) * MAX_CHUNKS + c] = hh ? m1 : m0;
+                al[(2 * h + hh) * MAX_CHUNKS + c] = hh ? (wred[0][1][1] + wred[1][1][1]) + (wred[2][1][1] + wred[3][1][1])
                                              : (wred[0][0][1] + wred[1][0][1]) + (wred[2][0][1] + wred[3][0][1]);
             }
         }
     }
-}
-
-// Merge the chunks of one query head: out = sum_c w_c acc_c / sum_c w_c l_c,
-// w_c = exp(m_c - max m).  Grid: 16 heads x 128 threads.
-__global__ void __launch_bounds__(128)
-k_attn_combine(const float *am, const float *al, const float *aacc, const DevState *st, int slot_ovr,
-               float *out)
-{
-    __shared__ float w[MAX_CHUNKS];
-    __shared__ float scratch[16];
-    const int h = blockIdx.x, d = threadIdx.x;
-    const int L = (slot_ovr >= 0 ? slot_ovr : st->kv_len) + 1;
-    const int C = (L + KV_PAGE - 1) / KV_PAGE;
-    const float m = d < C ? am[d * 16 + h] : -INFINITY;
-    const float l = d < C ? al[d * 16 + h] : 0.0f;
-    const float M = block_max(m, scratch);
-    const float wc = d < C ? expf(m - M) : 0.0f;
-    if (d < C) w[d] = wc;
-    const float Ls = block_sum(l * wc, scratch);
-    float o = 0.0f;
-#pragma unroll 8
-    for (int c = 0; c < C; c++) o += w[c] * aacc[((size_t)c * 16 + h) * HEAD_DIM + d];
-    out[h * HEAD_DIM + d] = o / Ls;
 }
 
 // ---------------------------------------------------------------------------
@@ -1942,12 +1997,8 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
                        L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
                        ws.al, ws.aacc);
     QCHK(hipGetLastError());
-    // 3. merge the chunks
-    hipLaunchKernelGGL(k_attn_combine, dim3(m.n_heads), dim3(HEAD_DIM), 0, s, ws.am, ws.al, ws.aacc, st,
-                       slot_ovr, ws.attn);
-    QCHK(hipGetLastError());
-    // 4. o_proj -> partials
-    QCHK(launch_gemv<1>(L.o, ProPlain<1>{ws.attn, 16 * HEAD_DIM, 16 * HEAD_DIM}, EpiPart<1>{ws.part_o, L.o.npad}, s));
+    // 3. o_proj -> partials, the pages merged in its prologue
+    QCHK(launch_gemv<1>(L.o, ProAttnCombine{ws.am, ws.al, ws.aacc, st, slot_ovr}, EpiPart<1>{ws.part_o, L.o.npad}, s));
     // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
     const ProResidRms<1, 2048> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
     return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);
