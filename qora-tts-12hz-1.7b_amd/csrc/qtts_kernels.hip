@@ -542,6 +542,128 @@ struct ProEmbed {
 // candidates (code_predictor.rs:253-260; the teacher-forced code when forcing),
 // then that code's embedding row.  The wave argmax runs in every wave, so
 // the row loads need no barrier; workgroup (0, 0) records the code.
+// Layer 0's input at predictor steps 1..14: the projected embedding row of
+// the step's code (project_input(get_acoustic_embedding(g-1, code)) + bias,
+// code_predictor.rs:51-61, 255-260), read from a table built at upload with
+// the same GEMV, then RMSNorm as in ProResidRms.  The code is the argmax of
+// the previous head's candidates, or the teacher-forced code, or (no
+// candidates) the code already recorded in DevState; with candidates
+// workgroup (0, 0) records it.  Slice-0 workgroups store the row (the
+// layer's residual input) to x_out.
+template <int KMAX>
+struct ProCodeRowRms {
+    const float *table;      // [rows][k]
+    int rows;
+    const float2 *cand;      // null: the code is st->used[slot]
+    int ncand;
+    DevState *st;
+    int slot;
+    uint32_t *codes_api;
+    const uint16_t *gamma;
+    int k;
+    float *x_out;
+    __device__ static float *xf_lds()
+    {
+        __shared__ float xf[KMAX];
+        return xf;
+    }
+    template <int T, int KC>
+    struct Fetch {
+        static constexpr int U = (KMAX / 4 + T - 1) / T;
+        static constexpr int UG = (KC + T - 1) / T;
+        f32x4 x[U];
+        uint32_t g[UG];
+        uint32_t pred, used;
+        bool nan;
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
+        const int k4 = k >> 2, t = threadIdx.x;
+#pragma unroll
+        for (int u = 0; u < UG; u++) f.g[u] = gamma[min(k0 + t + u * T, k - 1)];
+        f.nan = false;
+        if (cand) {
+            const int force = st->force;
+            const uint32_t fc = st->fcode[slot];
+            f.pred = cand_argmax(cand, ncand, f.nan);
+            f.used = force ? fc : f.pred;
+        } else {
+            f.pred = f.used = st->used[slot];
+        }
+        const float *row = table + (size_t)min(f.used, (uint32_t)(rows - 1)) * k;
+#pragma unroll
+        for (int u = 0; u < U; u++) f.x[u] = ld4(row + 4 * min(t + u * T, k4 - 1));
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        constexpr int NW = T / 64;
+        __shared__ float wss[NW];
+        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
+        float *xf = xf_lds();
+        const int k4 = k >> 2, t = threadIdx.x;
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = t + u * T;
+            const f32x4 x = f.x[u];
+            if (i < k4) {
+                *(f32x4 *)(xf + 4 * i) = x;
+                ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+            }
+        }
+        const float w = wave_sum_dpp(ss);
+        if ((t & 63) == 0) wss[t >> 6] = w;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) tot += wss[i];
+        const float iv = 1.0f / sqrtf(tot / (float)k + 1e-6f);
+#pragma unroll
+        for (int u = 0; u < UG; u++) {
+            const int r = t + u * T;
+            if (r < KC) xs[r] = (k0 + r < k) ? xf[k0 + r] * iv * h2f(f.g[u]) : 0.0f;
+        }
+        if (cand && k0 == 0 && ctile == 0 && t == 0) {
+            st->pred[slot] = f.pred;
+            st->used[slot] = f.used;
+            st->prev[slot] = f.used;
+            if (f.nan) st->nan_flag = 1;
+            if (codes_api) codes_api[slot - 1] = f.pred;
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const
+    {
+        if (s != 0 || !x_out) return;
+        const float *xf = xf_lds();
+        const int per = (k + nct - 1) / nct;
+        const int j0 = c * per, j1 = min(j0 + per, k);
+        for (int j = j0 + threadIdx.x; j < j1; j += blockDim.x) x_out[j] = xf[j];
+    }
+};
+
+// Every row of a Q4 table dequantised: out[r][j], grid (column blocks, rows).
+__global__ void k_dequant_rows(Q4Rows e, float *out)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (j < e.n) out[(size_t)r * e.n + j] = q4_row_value(e, r, j);
+}
+
+// x[r][j] = (sum over slices s of part[r][s][j], in slice order) + bias[j]:
+// the order of ProResidRms's residual-free sum, so a table row feeds the
+// same bits into layer 0 as the projection partials would.
+__global__ void k_rows_from_parts(const float *part, int S, int npad, const float *bias, int n, float *out)
+{
+    const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (j >= n) return;
+    const float *pr = part + (size_t)r * S * npad + j;
+    float a = pr[0];
+    for (int s2 = 1; s2 < S; s2++) a += pr[(size_t)s2 * npad];
+    out[(size_t)r * n + j] = bias ? a + bias[j] : a;
+}
+
 struct ProArgmaxEmbed {
     Q4Rows emb;
     const float2 *cand;
@@ -636,6 +758,36 @@ struct EpiPart {
     __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
     {
         part[((size_t)s * NB + b) * npad + c * C + cc] = y(cc);
+    }
+};
+
+// Row blockIdx.y of a batch of single rows: the per-row arithmetic of NB = 1
+// (used to build the predictor's projected-row tables at upload).
+struct ProPlainY {
+    const float *x;
+    int ld, k;
+    template <int T, int KC>
+    using Fetch = typename ProPlain<1>::template Fetch<T, KC>;
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        ProPlain<1>{x + (size_t)blockIdx.y * ld, ld, k}.template fetch<T, KC>(f, k0, ctile);
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        ProPlain<1>{x + (size_t)blockIdx.y * ld, ld, k}.template load<T, KC>(f, xs, k0, ctile);
+    }
+    __device__ void finish(int s, int c, int nct) const {}
+};
+
+struct EpiPartY {
+    float *part;             // [rows][S][npad]
+    int npad, S;
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
+    {
+        part[((size_t)blockIdx.y * S + s) * npad + c * C + cc] = y(cc);
     }
 };
 
@@ -960,14 +1112,14 @@ template <class P>
 struct OnlyT<P, std::void_t<decltype(P::kOnlyT)>> { static constexpr int v = P::kOnlyT; };
 
 template <int NB, class Pro, class Epi>
-static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st)
+static hipError_t launch_gemv(const Q4Tiled &w, const Pro &pro, const Epi &epi, hipStream_t st, int rows = 1)
 {
-    const int grid = w.S * w.CT;
+    const dim3 grid(w.S * w.CT, rows);
 #define QTTS_GEMV_CASE(CFG)                                                                     \
     case CFG: {                                                                                 \
         constexpr TileShape ts = tile_shape(CFG);                                               \
         if constexpr (OnlyT<Pro>::v == 0 || OnlyT<Pro>::v == ts.T) {                            \
-            hipLaunchKernelGGL((k_gemv<ts.T, ts.GB, ts.R, NB, Pro, Epi>), dim3(grid), dim3(ts.T), 0, st, w, pro, epi); \
+            hipLaunchKernelGGL((k_gemv<ts.T, ts.GB, ts.R, NB, Pro, Epi>), grid, dim3(ts.T), 0, st, w, pro, epi); \
         } else {                                                                                \
             return hipErrorInvalidValue;                                                        \
         }                                                                                       \
@@ -2073,16 +2225,21 @@ static ProPredAttn<NB, MS> pred_attn_pro(const PredictorDev &p, const LayerDev &
 }
 
 template <int NB>
-static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s)
+static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s,
+                             const ProCodeRowRms<1024> *row_in = nullptr)
 {
     const LayerDev &L = p.layers[l];
     const int h = p.hidden;
-    const ProResidRms<NB, 1024> pre_attn =
-        l == 0 ? ProResidRms<NB, 1024>{nullptr, h, ws.part_proj, p.proj.S, NB, 0, p.proj.npad, p.proj_bias, L.input_norm,
-                                 h, ws.pxb, nullptr}
-               : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
-                                 p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
-    QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
+    if (NB == 1 && row_in) {
+        QCHK(launch_gemv<1>(L.qkv, *row_in, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
+    } else {
+        const ProResidRms<NB, 1024> pre_attn =
+            l == 0 ? ProResidRms<NB, 1024>{nullptr, h, ws.part_proj, p.proj.S, NB, 0, p.proj.npad, p.proj_bias,
+                                           L.input_norm, h, ws.pxb, nullptr}
+                   : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
+                                           p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
+        QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
+    }
     float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     if (pred_attn_fusable(p, L)) {
@@ -2149,6 +2306,17 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
     for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, 0, s));
     QCHK(pred_head(p, ws, st, 0, 2, 1, forced, codes_api, s));           // :247-248
     for (int g = 1; g < p.n_groups; g++) {
+        if (p.proj_rows) {
+            // the projected embedding row of the previous code, looked up (:255-260)
+            const float2 *cand = head_cand(p, g - 1) ? ws.cand + (g - 1) * MAX_CAND : nullptr;
+            const ProCodeRowRms<1024> row_in{p.proj_rows + (size_t)(g - 1) * p.emb_rows.rows * p.hidden,
+                                             p.emb_rows.rows, cand, p.heads[g - 1].CT, st, g, codes_api,
+                                             p.layers[0].input_norm, p.hidden, ws.pxb};
+            QCHK(pred_layer<1>(p, ws, 0, 1 + g, s, &row_in));
+            for (int l = 1; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
+            QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
+            continue;
+        }
         // embed the previous code with codebook g-1, project (:255-260)
         Q4Rows e = p.emb_rows;
         e.packed += (size_t)(g - 1) * e.rows * e.G * 16;
@@ -2166,6 +2334,29 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
     if (sem && head_cand(p, gl)) {
         hipLaunchKernelGGL(k_cand_final, dim3(1), dim3(64), 0, s, ws.cand + gl * MAX_CAND, p.heads[gl].CT, st,
                            p.n_groups, codes_api);
+        QCHK(hipGetLastError());
+    }
+    return hipSuccess;
+}
+
+// The predictor's projected rows proj(E_g[c]) + bias for every code c of
+// codebooks g = 0..n_tables-1 (the layer-0 inputs of steps 1..n_tables),
+// with the step's own GEMV instance so the rows carry the same bits.
+// Scratch: X [rows][proj.k], part [rows][proj.S][proj.npad].
+hipError_t enqueue_pred_row_tables(const PredictorDev &p, int n_tables, float *X, float *part, float *out,
+                                   hipStream_t s)
+{
+    const int rows = p.emb_rows.rows, kin = p.proj.k;
+    if (p.emb_rows.n != kin) return hipErrorInvalidValue;
+    for (int g = 0; g < n_tables; g++) {
+        Q4Rows e = p.emb_rows;
+        e.packed += (size_t)g * e.rows * e.G * 16;
+        e.scales += (size_t)g * e.rows * e.G;
+        hipLaunchKernelGGL(k_dequant_rows, dim3((kin + 255) / 256, rows), dim3(256), 0, s, e, X);
+        QCHK(hipGetLastError());
+        QCHK(launch_gemv<1>(p.proj, ProPlainY{X, kin, kin}, EpiPartY{part, p.proj.npad, p.proj.S}, s, rows));
+        hipLaunchKernelGGL(k_rows_from_parts, dim3((p.hidden + 255) / 256, rows), dim3(256), 0, s, part, p.proj.S,
+                           p.proj.npad, p.proj_bias, p.hidden, out + (size_t)g * rows * p.hidden);
         QCHK(hipGetLastError());
     }
     return hipSuccess;

@@ -637,6 +637,8 @@ static int alloc_workspace(qtts_ctx *c)
     return QTTS_OK;
 }
 
+static int build_pred_rows(qtts_ctx *c);
+
 static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predictor_host *p)
 {
     auto &A = c->model_allocs;
@@ -717,6 +719,35 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     RCHK(upload_vec(c, A, p->rope_sin, (size_t)p->rope_max_pos * 64, &q.rope_sin));
     q.rope_rows = p->rope_max_pos;
     RCHK(alloc_workspace(c));
+    RCHK(build_pred_rows(c));
+    return QTTS_OK;
+}
+
+// Projected embedding rows of the predictor's steps 1..n_groups-1 (layer 0's
+// input is a function of the step's code alone): 2048 x 1024 floats per
+// codebook, 117 MB for the 1.7B predictor.  QTTS_PRED_ROWS=0 keeps the
+// per-step projection GEMV instead.
+static int build_pred_rows(qtts_ctx *c)
+{
+    PredictorDev &q = c->pm;
+    q.proj_rows = nullptr;
+    const char *env = getenv("QTTS_PRED_ROWS");
+    if (q.n_groups < 2 || q.hidden > 1024 || q.emb_rows.n != q.proj.k || (env && env[0] == '0')) return QTTS_OK;
+    const int ntab = q.n_groups - 1, rows = q.emb_rows.rows;
+    float *tab = nullptr;
+    RCHK(dev_alloc(c, c->model_allocs, &tab, (size_t)ntab * rows * q.hidden));
+    float *X = nullptr, *part = nullptr;
+    HIPCHK(c, hipMalloc(&X, (size_t)rows * q.proj.k * sizeof(float)));
+    if (hipMalloc(&part, (size_t)rows * q.proj.S * q.proj.npad * sizeof(float)) != hipSuccess) {
+        hipFree(X);
+        return fail(c, QTTS_ERR_OOM, "predictor row tables: scratch allocation failed");
+    }
+    hipError_t e = enqueue_pred_row_tables(q, ntab, X, part, tab, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    hipFree(X);
+    hipFree(part);
+    if (e != hipSuccess) return fail(c, QTTS_ERR_HIP, "predictor row tables: %s", hipGetErrorString(e));
+    q.proj_rows = tab;
     return QTTS_OK;
 }
 

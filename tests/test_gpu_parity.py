@@ -328,6 +328,39 @@ def test_frames_free_running_sampled(loaded):
     om.kv_reset()
 
 
+def test_predictor_row_tables_bit_identical(ctx_factory, small_model, monkeypatch):
+    """Layer 0's input of predictor steps 1..14 read from the projected-row
+    tables (built at upload) carries the same bits as the per-step
+    projection GEMV (QTTS_PRED_ROWS=0): chain codes, sampled frames and the
+    final logits/hidden are identical."""
+    t, p = small_model
+    a = ctx_factory(256)
+    a.upload_model(t, p)
+    monkeypatch.setenv("QTTS_PRED_ROWS", "0")
+    b = ctx_factory(256)
+    b.upload_model(t, p)
+    rng = np.random.Generator(np.random.PCG64(81))
+    for _ in range(3):
+        th = rng.standard_normal(t.hidden).astype(np.float32)
+        sem = a.embed_codec_token(int(rng.integers(0, 3072)))
+        assert np.array_equal(a.generate_acoustic_codes(th, sem), b.generate_acoustic_codes(th, sem))
+    X = rng.standard_normal((16, t.hidden)).astype(np.float32)
+    params = qtts.sample_params(eos_enabled=False)
+    outs = []
+    for c in (a, b):
+        h = c.prefill_talker_raw_from(X, 0)
+        c.gen_set_text(None, c.embed_text_token(3))
+        c.gen_begin(c.apply_codec_head(h), h, 16, 42, params)
+        codes, _ = c.gen_frames(24)
+        lg, hd, pos, rng_state = c.gen_state()
+        outs.append((codes, lg, hd, pos, rng_state))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(bits(outs[0][1]), bits(outs[1][1])) and np.array_equal(bits(outs[0][2]), bits(outs[1][2]))
+    assert outs[0][3:] == outs[1][3:]
+    a.close()
+    b.close()
+
+
 @pytest.mark.parametrize("tiles", [{"TGU": "14", "PGU": "16"}, {"TGU": "11", "PGU": "12", "PO": "11"},
                                    {"TQKV": "3", "TDOWN": "12", "PQKV": "2", "PDOWN": "3"}])
 def test_alternative_tiles_step_and_chain(ctx_factory, small_model, tiles, monkeypatch):
