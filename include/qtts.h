@@ -99,6 +99,91 @@ typedef struct qtts_predictor_host {
     int64_t rope_max_pos;
 } qtts_predictor_host;
 
+/* ---- speech decoder (codes -> 24 kHz audio) ---------------------------- */
+
+/* `Conv1dWeight` (conv.rs:29-38): weight [out][in][kernel] f32. */
+typedef struct qtts_conv1d_host {
+    const float *weight, *bias;
+    int32_t in_channels, out_channels, kernel_size, stride;
+    int32_t padding, dilation;
+} qtts_conv1d_host;
+
+/* `ConvTranspose1dWeight` (conv.rs:235-243): weight [in][out][kernel]. */
+typedef struct qtts_convt1d_host {
+    const float *weight, *bias;
+    int32_t in_channels, out_channels, kernel_size, stride;
+    int32_t padding, reserved;
+} qtts_convt1d_host;
+
+/* `DepthwiseConv1dWeight` (conv.rs:351-357): weight [channels][kernel]. */
+typedef struct qtts_dwconv_host {
+    const float *weight, *bias;
+    int32_t channels, kernel_size, padding, reserved;
+} qtts_dwconv_host;
+
+/* `DecoderTfLayer` (decoder.rs:68-80): matrices input-major [k][n]. */
+typedef struct qtts_dec_layer_host {
+    const float *q_proj, *k_proj, *v_proj;     /* [hidden][heads*head_dim] */
+    const float *o_proj;                       /* [heads*head_dim][hidden] */
+    const float *gate_proj, *up_proj;          /* [hidden][inter]          */
+    const float *down_proj;                    /* [inter][hidden]          */
+    const float *input_norm, *post_attn_norm;  /* [hidden]                 */
+    const float *attn_scale, *mlp_scale;       /* [hidden] layer scales    */
+} qtts_dec_layer_host;
+
+/* `UpsampleStage` (decoder.rs:82-93): ConvTranspose1d + ConvNeXt. */
+typedef struct qtts_upsample_host {
+    qtts_convt1d_host conv_t;
+    qtts_dwconv_host dw_conv;
+    const float *norm_w, *norm_b;              /* [channels]               */
+    const float *pw1_w, *pw1_b;                /* [channels][inner], [inner] */
+    const float *pw2_w, *pw2_b;                /* [inner][channels], [channels] */
+    const float *gamma;                        /* [channels]               */
+    int32_t channels, inner;
+} qtts_upsample_host;
+
+/* `VocosResidual` (decoder.rs:102-109). */
+typedef struct qtts_vocos_res_host {
+    const float *act1_alpha, *act1_beta;
+    qtts_conv1d_host conv1;                    /* k 7, dilation 1 / 3 / 9  */
+    const float *act2_alpha, *act2_beta;
+    qtts_conv1d_host conv2;                    /* k 1                      */
+} qtts_vocos_res_host;
+
+/* `VocosBlock` (decoder.rs:95-100). */
+typedef struct qtts_vocos_block_host {
+    const float *pre_snake_alpha, *pre_snake_beta;
+    qtts_convt1d_host upsample;
+    const qtts_vocos_res_host *residuals;
+    int32_t n_residuals, reserved;
+} qtts_vocos_block_host;
+
+/* `SpeechDecoderWeights` (decoder.rs:22-66). */
+typedef struct qtts_decoder_host {
+    int32_t hidden, n_heads, head_dim, inter;  /* transformer: 512, 16, 64, 1024 */
+    int32_t sliding_window, codebook_dim;      /* 72, 256                  */
+    int32_t codebook_size, vq_dim;             /* 2048 entries, 512        */
+    const float *first_codebook;               /* [codebook_size][codebook_dim] */
+    const float *first_output_proj;            /* [codebook_dim][vq_dim]   */
+    const float *const *rest_codebooks;        /* n_rest x [codebook_size][codebook_dim] */
+    const float *rest_output_proj;             /* [codebook_dim][vq_dim]   */
+    int32_t n_rest, latent;                    /* 15, 1024                 */
+    qtts_conv1d_host pre_conv;                 /* vq_dim -> latent, k 3    */
+    const float *tf_input_w, *tf_input_b;      /* [latent][hidden], [hidden] */
+    const qtts_dec_layer_host *tf_layers;
+    const float *tf_norm;                      /* [hidden]                 */
+    const float *tf_output_w, *tf_output_b;    /* [hidden][latent], [latent] */
+    int32_t n_tf_layers, n_upsample;
+    const qtts_upsample_host *upsample;
+    qtts_conv1d_host vocos_init;
+    const qtts_vocos_block_host *vocos_blocks;
+    int32_t n_vocos_blocks, reserved;
+    const float *final_snake_alpha, *final_snake_beta;
+    qtts_conv1d_host output_conv;              /* -> 1 channel, k 7        */
+    const float *rope_cos, *rope_sin;          /* [rope_max_pos][head_dim/2] */
+    int64_t rope_max_pos;
+} qtts_decoder_host;
+
 /* Sampler parameters: the fields of `TTSParams` (generate_new.rs:38-61)
  * that `sample_token` and the frame loop read. */
 typedef struct qtts_sample_params {

@@ -17,7 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
 from qtts import hostdesc  # noqa: E402  (descriptor structs only)
-from qtts.hostdesc import LayerHost, PredictorHost, Q4Host, SampleParams, TalkerHost, ptr  # noqa: E402
+from qtts.hostdesc import (Conv1dHost, ConvT1dHost, DecoderHost, DwConvHost, LayerHost,  # noqa: E402
+                           PredictorHost, Q4Host, SampleParams, TalkerHost, ptr)
 
 LIB = os.path.join(HERE, "liboqtts_oracle.so")
 
@@ -70,6 +71,17 @@ _SIG = {
                          POINTER(c_uint32)], c_int),
     "oq_frame": ([POINTER(TalkerHost), POINTER(PredictorHost), POINTER(OqKv), POINTER(OqKv), POINTER(OqGen),
                   POINTER(SampleParams), c_void_p, c_void_p, POINTER(c_int32), c_void_p], c_int),
+    "od_set_threads": ([c_int], None),
+    "od_causal_conv1d": ([c_void_p, c_int64, POINTER(Conv1dHost), c_void_p], None),
+    "od_conv_transpose1d": ([c_void_p, c_int64, POINTER(ConvT1dHost), c_void_p], c_int64),
+    "od_depthwise_conv1d": ([c_void_p, c_int64, POINTER(DwConvHost), c_void_p], None),
+    "od_gemm_bias": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], None),
+    "od_snake_beta": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p], None),
+    "od_gelu": ([c_float], c_float),
+    "od_layer_norm_cf": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float, c_void_p], None),
+    "od_warmup_trim_len": ([c_int64, c_int64, c_int64], c_int64),
+    "od_decode_to_audio": ([POINTER(DecoderHost), c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+                            POINTER(c_int64)], c_int),
 }
 
 _lib = None
@@ -331,3 +343,79 @@ class Model:
         if rc:
             raise RuntimeError(f"oracle frame rc={rc}")
         return codes, bool(eos.value)
+
+
+# ---------------------------------------------------------------------------
+# speech decoder (qtts_decoder.c)
+# ---------------------------------------------------------------------------
+
+def causal_conv1d(x, c):
+    """causal_conv1d (conv.rs:114-228): x [in][len] -> [out][len]."""
+    x = f32(x)
+    out = np.empty((c.out_channels, x.shape[1]), np.float32)
+    lib().od_causal_conv1d(ptr(x), x.shape[1], byref(hostdesc.conv1d_host(c)), ptr(out))
+    return out
+
+
+def conv_transpose1d(x, c):
+    """conv_transpose1d (conv.rs:247-349), uncropped."""
+    x = f32(x)
+    n = (x.shape[1] - 1) * c.stride - 2 * c.padding + c.kernel_size
+    out = np.empty((c.out_channels, n), np.float32)
+    lib().od_conv_transpose1d(ptr(x), x.shape[1], byref(hostdesc.convt1d_host(c)), ptr(out))
+    return out
+
+
+def depthwise_conv1d(x, c):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().od_depthwise_conv1d(ptr(x), x.shape[1], byref(DwConvHost(ptr(c.weight), ptr(c.bias), c.channels,
+                                                                      c.kernel_size, c.padding, 0)), ptr(out))
+    return out
+
+
+def gemm_bias(a, b, bias):
+    a, b, bias = f32(a), f32(b), f32(bias)
+    out = np.empty((a.shape[0], b.shape[1]), np.float32)
+    lib().od_gemm_bias(ptr(a), ptr(b), ptr(bias), a.shape[0], b.shape[1], a.shape[1], ptr(out))
+    return out
+
+
+def snake_beta(x, alpha, beta):
+    x, alpha, beta = f32(x), f32(alpha), f32(beta)
+    out = np.empty_like(x)
+    lib().od_snake_beta(ptr(x), ptr(alpha), ptr(beta), x.shape[0], x.shape[1], ptr(out))
+    return out
+
+
+def gelu(x):
+    return lib().od_gelu(x)
+
+
+def layer_norm_cf(x, gamma, beta, eps=1e-5):
+    x = f32(x)
+    out = np.empty_like(x)
+    lib().od_layer_norm_cf(ptr(x), ptr(f32(gamma)), ptr(f32(beta)), x.shape[0], x.shape[1], eps, ptr(out))
+    return out
+
+
+def warmup_trim_len(tv, total, n):
+    return lib().od_warmup_trim_len(tv, total, n)
+
+
+def decode_to_audio(d, codes, warmup=None, threads=8):
+    """decode_to_audio (decoder.rs:395-584): codes [16][T] -> samples."""
+    codes = np.ascontiguousarray(codes, np.uint32)
+    T = codes.shape[1]
+    Tv = 0 if warmup is None else warmup.shape[1]
+    if warmup is not None:
+        warmup = np.ascontiguousarray(warmup, np.uint32)
+    cap = (T + Tv) * d.upsample_factor
+    out = np.empty(cap, np.float32)
+    n = c_int64()
+    h, keep = hostdesc.decoder_host(d)
+    lib().od_set_threads(threads)
+    rc = lib().od_decode_to_audio(byref(h), ptr(codes), T, ptr(warmup) if warmup is not None else None, Tv,
+                                  ptr(out), cap, byref(n))
+    assert rc == 0, "oracle decode failed"
+    return out[: n.value].copy()

@@ -143,6 +143,28 @@ int oq_frame(const qtts_talker_host *t, const qtts_predictor_host *p,
              const float *text_add, uint32_t *codes_out, int32_t *eos,
              const uint32_t *forced);
 
+/* -- speech decoder (qtts_decoder.c; decoder.rs, conv.rs) -------------------- */
+void    od_set_threads(int n);
+void    od_causal_conv1d(const float *in, int64_t in_len, const qtts_conv1d_host *w,
+                         float *out);                                  /* conv.rs:114-228 */
+int64_t od_conv_transpose1d(const float *in, int64_t in_len, const qtts_convt1d_host *w,
+                            float *out);                               /* conv.rs:247-349 */
+void    od_depthwise_conv1d(const float *in, int64_t len, const qtts_dwconv_host *w,
+                            float *out);                               /* conv.rs:361-432 */
+void    od_gemm_bias(const float *a, const float *b, const float *bias, int64_t m,
+                     int64_t n, int64_t k, float *c);                  /* conv.rs:434-526 */
+void    od_snake_beta(const float *in, const float *alpha, const float *beta,
+                      int64_t channels, int64_t len, float *out);      /* conv.rs:545-640 */
+float   od_gelu(float x);                                              /* conv.rs:692-694 */
+void    od_layer_norm_cf(const float *in, const float *gamma, const float *beta,
+                         int64_t channels, int64_t len, float eps, float *out); /* decoder.rs:668-690 */
+int64_t od_warmup_trim_len(int64_t tv, int64_t total, int64_t out_len);  /* decoder.rs:661-666 */
+/* decode_to_audio (decoder.rs:395-584): codes [n_rest+1][T] (+ warmup
+ * [n_rest+1][Tv] or NULL) -> clamped samples, warmup portion trimmed. */
+int     od_decode_to_audio(const qtts_decoder_host *w, const uint32_t *codes, int64_t T,
+                           const uint32_t *warmup, int64_t Tv, float *out, int64_t cap,
+                           int64_t *n_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,72 @@ class PredictorHost(ctypes.Structure):
     ]
 
 
+class Conv1dHost(ctypes.Structure):
+    """`Conv1dWeight` (conv.rs:29-38)."""
+    _fields_ = [("weight", c_void_p), ("bias", c_void_p), ("in_channels", c_int32), ("out_channels", c_int32),
+                ("kernel_size", c_int32), ("stride", c_int32), ("padding", c_int32), ("dilation", c_int32)]
+
+
+class ConvT1dHost(ctypes.Structure):
+    """`ConvTranspose1dWeight` (conv.rs:235-243)."""
+    _fields_ = [("weight", c_void_p), ("bias", c_void_p), ("in_channels", c_int32), ("out_channels", c_int32),
+                ("kernel_size", c_int32), ("stride", c_int32), ("padding", c_int32), ("reserved", c_int32)]
+
+
+class DwConvHost(ctypes.Structure):
+    """`DepthwiseConv1dWeight` (conv.rs:351-357)."""
+    _fields_ = [("weight", c_void_p), ("bias", c_void_p), ("channels", c_int32), ("kernel_size", c_int32),
+                ("padding", c_int32), ("reserved", c_int32)]
+
+
+class DecLayerHost(ctypes.Structure):
+    """`DecoderTfLayer` (decoder.rs:68-80)."""
+    _fields_ = [(n, c_void_p) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                        "down_proj", "input_norm", "post_attn_norm", "attn_scale", "mlp_scale")]
+
+
+class UpsampleHost(ctypes.Structure):
+    """`UpsampleStage` (decoder.rs:82-93)."""
+    _fields_ = [("conv_t", ConvT1dHost), ("dw_conv", DwConvHost)] + \
+        [(n, c_void_p) for n in ("norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w", "pw2_b", "gamma")] + \
+        [("channels", c_int32), ("inner", c_int32)]
+
+
+class VocosResHost(ctypes.Structure):
+    """`VocosResidual` (decoder.rs:102-109)."""
+    _fields_ = [("act1_alpha", c_void_p), ("act1_beta", c_void_p), ("conv1", Conv1dHost),
+                ("act2_alpha", c_void_p), ("act2_beta", c_void_p), ("conv2", Conv1dHost)]
+
+
+class VocosBlockHost(ctypes.Structure):
+    """`VocosBlock` (decoder.rs:95-100)."""
+    _fields_ = [("pre_snake_alpha", c_void_p), ("pre_snake_beta", c_void_p), ("upsample", ConvT1dHost),
+                ("residuals", ctypes.POINTER(VocosResHost)), ("n_residuals", c_int32), ("reserved", c_int32)]
+
+
+class DecoderHost(ctypes.Structure):
+    """`SpeechDecoderWeights` (decoder.rs:22-66)."""
+    _fields_ = [
+        ("hidden", c_int32), ("n_heads", c_int32), ("head_dim", c_int32), ("inter", c_int32),
+        ("sliding_window", c_int32), ("codebook_dim", c_int32), ("codebook_size", c_int32), ("vq_dim", c_int32),
+        ("first_codebook", c_void_p), ("first_output_proj", c_void_p),
+        ("rest_codebooks", ctypes.POINTER(c_void_p)), ("rest_output_proj", c_void_p),
+        ("n_rest", c_int32), ("latent", c_int32),
+        ("pre_conv", Conv1dHost),
+        ("tf_input_w", c_void_p), ("tf_input_b", c_void_p),
+        ("tf_layers", ctypes.POINTER(DecLayerHost)),
+        ("tf_norm", c_void_p), ("tf_output_w", c_void_p), ("tf_output_b", c_void_p),
+        ("n_tf_layers", c_int32), ("n_upsample", c_int32),
+        ("upsample", ctypes.POINTER(UpsampleHost)),
+        ("vocos_init", Conv1dHost),
+        ("vocos_blocks", ctypes.POINTER(VocosBlockHost)),
+        ("n_vocos_blocks", c_int32), ("reserved", c_int32),
+        ("final_snake_alpha", c_void_p), ("final_snake_beta", c_void_p),
+        ("output_conv", Conv1dHost),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("rope_max_pos", c_int64),
+    ]
+
+
 class SampleParams(ctypes.Structure):
     """`TTSParams` fields read by `sample_token` (generate_new.rs:38-79)."""
     _fields_ = [
@@ -117,3 +183,45 @@ def predictor_host(p):
         embs, layers, heads, ptr(p.final_norm),
         ptr(p.rope_cos), ptr(p.rope_sin), p.rope_cos.shape[0])
     return h, (layers, embs, heads)
+
+
+def conv1d_host(c):
+    return Conv1dHost(ptr(c.weight), ptr(c.bias), c.in_channels, c.out_channels, c.kernel_size, c.stride,
+                      c.padding, c.dilation)
+
+
+def convt1d_host(c):
+    return ConvT1dHost(ptr(c.weight), ptr(c.bias), c.in_channels, c.out_channels, c.kernel_size, c.stride,
+                       c.padding, 0)
+
+
+def decoder_host(d):
+    """Build a DecoderHost; the returned tuple keeps the nested arrays alive."""
+    rest = (c_void_p * len(d.rest_codebooks))(*[ptr(c) for c in d.rest_codebooks])
+    layers = (DecLayerHost * len(d.tf_layers))(*[
+        DecLayerHost(*[ptr(getattr(L, n)) for n, _ in DecLayerHost._fields_]) for L in d.tf_layers])
+    ups = (UpsampleHost * max(1, len(d.upsample)))(*[
+        UpsampleHost(convt1d_host(u.conv_t),
+                     DwConvHost(ptr(u.dw_conv.weight), ptr(u.dw_conv.bias), u.dw_conv.channels,
+                                u.dw_conv.kernel_size, u.dw_conv.padding, 0),
+                     ptr(u.norm_w), ptr(u.norm_b), ptr(u.pw1_w), ptr(u.pw1_b), ptr(u.pw2_w), ptr(u.pw2_b),
+                     ptr(u.gamma), u.channels, u.inner) for u in d.upsample])
+    res_arrays = []
+    blocks = []
+    for b in d.vocos_blocks:
+        ra = (VocosResHost * len(b.residuals))(*[
+            VocosResHost(ptr(r.act1_alpha), ptr(r.act1_beta), conv1d_host(r.conv1), ptr(r.act2_alpha),
+                         ptr(r.act2_beta), conv1d_host(r.conv2)) for r in b.residuals])
+        res_arrays.append(ra)
+        blocks.append(VocosBlockHost(ptr(b.pre_snake_alpha), ptr(b.pre_snake_beta), convt1d_host(b.upsample),
+                                     ra, len(b.residuals), 0))
+    vb = (VocosBlockHost * max(1, len(blocks)))(*blocks)
+    h = DecoderHost(
+        d.hidden, d.n_heads, d.head_dim, d.inter, d.sliding_window, d.codebook_dim, d.codebook_size, d.vq_dim,
+        ptr(d.first_codebook), ptr(d.first_output_proj), rest, ptr(d.rest_output_proj),
+        len(d.rest_codebooks), d.latent, conv1d_host(d.pre_conv),
+        ptr(d.tf_input_w), ptr(d.tf_input_b), layers, ptr(d.tf_norm), ptr(d.tf_output_w), ptr(d.tf_output_b),
+        len(d.tf_layers), len(d.upsample), ups, conv1d_host(d.vocos_init), vb, len(d.vocos_blocks), 0,
+        ptr(d.final_snake_alpha), ptr(d.final_snake_beta), conv1d_host(d.output_conv),
+        ptr(d.rope_cos), ptr(d.rope_sin), d.rope_cos.shape[0])
+    return h, (rest, layers, ups, res_arrays, vb)

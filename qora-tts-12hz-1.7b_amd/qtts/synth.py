@@ -172,3 +172,203 @@ def make_predictor(seed=2, n_layers=5, hidden=1024, inter=3072, vocab=2048, n_gr
         lm_heads=[q4_random(rng, hidden, vocab) for _ in range(n_groups)],
         final_norm=gamma(rng, hidden), rope_cos=cos, rope_sin=sin,
         hidden=hidden, inter=inter, vocab=vocab)
+
+
+# ---------------------------------------------------------------------------
+# speech decoder (SpeechDecoderWeights, decoder.rs:22-66): f32 weights
+# ---------------------------------------------------------------------------
+
+@dataclass
+class Conv1d:
+    """`Conv1dWeight` (conv.rs:29-38): weight [out][in][k]."""
+    weight: np.ndarray
+    bias: np.ndarray
+    in_channels: int
+    out_channels: int
+    kernel_size: int
+    stride: int = 1
+    padding: int = 0
+    dilation: int = 1
+
+
+@dataclass
+class ConvT1d:
+    """`ConvTranspose1dWeight` (conv.rs:235-243): weight [in][out][k]."""
+    weight: np.ndarray
+    bias: np.ndarray
+    in_channels: int
+    out_channels: int
+    kernel_size: int
+    stride: int
+    padding: int = 0
+
+
+@dataclass
+class DwConv:
+    """`DepthwiseConv1dWeight` (conv.rs:351-357): weight [c][k]."""
+    weight: np.ndarray
+    bias: np.ndarray
+    channels: int
+    kernel_size: int
+    padding: int
+
+
+@dataclass
+class DecLayer:
+    q_proj: np.ndarray
+    k_proj: np.ndarray
+    v_proj: np.ndarray
+    o_proj: np.ndarray
+    gate_proj: np.ndarray
+    up_proj: np.ndarray
+    down_proj: np.ndarray
+    input_norm: np.ndarray
+    post_attn_norm: np.ndarray
+    attn_scale: np.ndarray
+    mlp_scale: np.ndarray
+
+
+@dataclass
+class Upsample:
+    conv_t: ConvT1d
+    dw_conv: DwConv
+    norm_w: np.ndarray
+    norm_b: np.ndarray
+    pw1_w: np.ndarray      # [channels][inner]
+    pw1_b: np.ndarray
+    pw2_w: np.ndarray      # [inner][channels]
+    pw2_b: np.ndarray
+    gamma: np.ndarray
+    channels: int
+    inner: int
+
+
+@dataclass
+class VocosRes:
+    act1_alpha: np.ndarray
+    act1_beta: np.ndarray
+    conv1: Conv1d
+    act2_alpha: np.ndarray
+    act2_beta: np.ndarray
+    conv2: Conv1d
+
+
+@dataclass
+class VocosBlock:
+    pre_snake_alpha: np.ndarray
+    pre_snake_beta: np.ndarray
+    upsample: ConvT1d
+    residuals: List[VocosRes]
+
+
+@dataclass
+class Decoder:
+    first_codebook: np.ndarray       # [codebook_size][codebook_dim]
+    first_output_proj: np.ndarray    # [codebook_dim][vq_dim]
+    rest_codebooks: List[np.ndarray]
+    rest_output_proj: np.ndarray
+    pre_conv: Conv1d
+    tf_input_w: np.ndarray           # [latent][hidden]
+    tf_input_b: np.ndarray
+    tf_layers: List[DecLayer]
+    tf_norm: np.ndarray
+    tf_output_w: np.ndarray          # [hidden][latent]
+    tf_output_b: np.ndarray
+    upsample: List[Upsample]
+    vocos_init: Conv1d
+    vocos_blocks: List[VocosBlock]
+    final_snake_alpha: np.ndarray
+    final_snake_beta: np.ndarray
+    output_conv: Conv1d
+    rope_cos: np.ndarray             # [max_pos][head_dim/2]
+    rope_sin: np.ndarray
+    hidden: int = 512
+    n_heads: int = 16
+    head_dim: int = 64
+    inter: int = 1024
+    sliding_window: int = 72
+    codebook_dim: int = 256
+    codebook_size: int = 2048
+    vq_dim: int = 512
+    latent: int = 1024
+
+    @property
+    def upsample_factor(self) -> int:
+        f = 1
+        for u in self.upsample:
+            f *= u.conv_t.stride
+        for b in self.vocos_blocks:
+            f *= b.upsample.stride
+        return f
+
+
+def _mat(rng, k, n, gain=1.0):
+    return (rng.standard_normal((k, n), dtype=np.float32) * np.float32(gain / np.sqrt(k))).astype(np.float32)
+
+
+def _vec(rng, n, mean=0.0, sigma=0.02):
+    return (mean + sigma * rng.standard_normal(n)).astype(np.float32)
+
+
+def _conv(rng, ic, oc, k, dilation=1, gain=1.0):
+    w = (rng.standard_normal((oc, ic, k), dtype=np.float32) * np.float32(gain / np.sqrt(ic * k))).astype(np.float32)
+    return Conv1d(w, _vec(rng, oc), ic, oc, k, 1, 0, dilation)
+
+
+def _convt(rng, ic, oc, k, s, gain=1.0):
+    w = (rng.standard_normal((ic, oc, k), dtype=np.float32) * np.float32(gain / np.sqrt(ic * k / s))).astype(np.float32)
+    return ConvT1d(w, _vec(rng, oc), ic, oc, k, s, 0)
+
+
+def make_decoder(seed=7, latent=1024, hidden=512, n_heads=16, head_dim=64, inter=1024, n_tf_layers=8,
+                 sliding_window=72, codebook_size=2048, codebook_dim=256, vq_dim=512, n_rest=15, n_upsample=2,
+                 vocos=(1536, 768, 384, 192, 96), rates=(8, 5, 4, 3), dilations=(1, 3, 9), rope_max_pos=8000):
+    """Random decoder of the 12 Hz speech tokenizer's shapes (loader.rs:540-720):
+    16 VQ codebooks -> 512, pre-conv to 1024, an 8-layer transformer (512
+    hidden, 16 x 64 heads, sliding window 72), two 2x ConvTranspose +
+    ConvNeXt upsamplers, Vocos (1536 -> 96 channels, rates 8, 5, 4, 3),
+    1920 samples per frame.  Scales keep every stage's activations O(1)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    A = n_heads * head_dim
+    layers = []
+    for _ in range(n_tf_layers):
+        layers.append(DecLayer(
+            _mat(rng, hidden, A), _mat(rng, hidden, A), _mat(rng, hidden, A), _mat(rng, A, hidden),
+            _mat(rng, hidden, inter), _mat(rng, hidden, inter), _mat(rng, inter, hidden),
+            _vec(rng, hidden, 1.0, 0.05), _vec(rng, hidden, 1.0, 0.05),
+            _vec(rng, hidden, 0.1, 0.02), _vec(rng, hidden, 0.1, 0.02)))
+    ups = []
+    for _ in range(n_upsample):
+        inner = 4 * latent
+        ups.append(Upsample(
+            _convt(rng, latent, latent, 2, 2),
+            DwConv((rng.standard_normal((latent, 7), dtype=np.float32) / np.float32(np.sqrt(7))).astype(np.float32),
+                   _vec(rng, latent), latent, 7, 3),
+            _vec(rng, latent, 1.0, 0.05), _vec(rng, latent), _mat(rng, latent, inner), _vec(rng, inner),
+            _mat(rng, inner, latent), _vec(rng, latent), _vec(rng, latent, 0.1, 0.02), latent, inner))
+    blocks = []
+    for b, r in enumerate(rates[:len(vocos) - 1]):
+        ic, oc = vocos[b], vocos[b + 1]
+        res = [VocosRes(_vec(rng, oc, 0.0, 0.1), _vec(rng, oc, 0.0, 0.1), _conv(rng, oc, oc, 7, d, 0.5),
+                        _vec(rng, oc, 0.0, 0.1), _vec(rng, oc, 0.0, 0.1), _conv(rng, oc, oc, 1, 1, 0.5))
+               for d in dilations]
+        blocks.append(VocosBlock(_vec(rng, ic, 0.0, 0.1), _vec(rng, ic, 0.0, 0.1), _convt(rng, ic, oc, 2 * r, r), res))
+    last = vocos[len(blocks)]
+    cos, sin = rope_table(head_dim, rope_max_pos, theta=10000.0)
+    return Decoder(
+        first_codebook=(0.5 * rng.standard_normal((codebook_size, codebook_dim))).astype(np.float32),
+        first_output_proj=_mat(rng, codebook_dim, vq_dim),
+        rest_codebooks=[(0.15 * rng.standard_normal((codebook_size, codebook_dim))).astype(np.float32)
+                        for _ in range(n_rest)],
+        rest_output_proj=_mat(rng, codebook_dim, vq_dim),
+        pre_conv=_conv(rng, vq_dim, latent, 3),
+        tf_input_w=_mat(rng, latent, hidden), tf_input_b=_vec(rng, hidden),
+        tf_layers=layers, tf_norm=_vec(rng, hidden, 1.0, 0.05),
+        tf_output_w=_mat(rng, hidden, latent), tf_output_b=_vec(rng, latent),
+        upsample=ups, vocos_init=_conv(rng, latent, vocos[0], 7),
+        vocos_blocks=blocks,
+        final_snake_alpha=_vec(rng, last, 0.0, 0.1), final_snake_beta=_vec(rng, last, 0.0, 0.1),
+        output_conv=_conv(rng, last, 1, 7, 1, 0.15),
+        rope_cos=cos, rope_sin=sin,
+        hidden=hidden, n_heads=n_heads, head_dim=head_dim, inter=inter, sliding_window=sliding_window,
+        codebook_dim=codebook_dim, codebook_size=codebook_size, vq_dim=vq_dim, latent=latent)
