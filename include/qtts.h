@@ -354,6 +354,28 @@ int qtts_build_icl_block(qtts_ctx *ctx, const uint32_t *ref_tokens, int64_t n_re
                          const uint32_t *ref_codes, int64_t n_frames,
                          float *icl_out, float *remainder_out, int flags);
 
+/* ---- speech decoder --------------------------------------------------- */
+
+/* Upload the speech decoder (codes -> 24 kHz waveform).  Replaces holding
+ * `SpeechDecoderWeights` (decoder.rs:22-66).  Matrices are repacked for
+ * the matrix-core convolutions; transposed convolutions must have
+ * kernel = stride or 2 * stride and padding 0 (the model's 2x / 8,5,4,3x
+ * stages), head_dim 64 or 16.  Replaces a previously uploaded decoder. */
+int qtts_decoder_upload(qtts_ctx *ctx, const qtts_decoder_host *decoder);
+
+/* `decode_to_audio` (decoder.rs:395-574): codes [n_codebooks][n_frames]
+ * (codebook-major, n_codebooks = n_rest + 1), optional warmup codes
+ * [n_codebooks][n_warmup] prepended and trimmed off the output
+ * (`warmup_trim_len`, decoder.rs:651-656).  audio gets *n_samples
+ * samples in [-1, 1]; with too small a capacity it fails with
+ * QTTS_ERR_CAPACITY and *n_samples holds the size needed.  n_frames 0
+ * gives no samples.  Codes and audio in host memory, or device memory
+ * with QTTS_DEVICE_PTRS for audio. */
+int qtts_decode_to_audio(qtts_ctx *ctx, const uint32_t *codes, int64_t n_frames,
+                         const uint32_t *warmup, int64_t n_warmup,
+                         float *audio, int64_t capacity, int64_t *n_samples,
+                         int flags);
+
 /* ---- code predictor --------------------------------------------------- */
 
 /* `generate_acoustic_codes` (code_predictor.rs:218-273): 2-token prefill,

@@ -1,0 +1,571 @@
+// qtts_decoder.hip — the speech decoder (decode_to_audio, decoder.rs:395-584)
+// on the device: 16 codebook indices per frame -> 24 kHz samples.
+//
+// Activations stay channel-first [channels][positions] as in the reference.
+// Every convolution, projection and pointwise layer is one implicit GEMM on
+// the f32 matrix cores (k_conv_gemm): rows = output channels, columns =
+// positions, contraction = input channels x taps, with the im2col gather
+// done while staging the activation tile:
+//   causal_conv1d        conv.rs:114-228   taps at t + j*dil - (K-1)*dil
+//   conv_transpose1d     conv.rs:247-349   stride phases, 1 or 2 taps each
+//   ConvNeXt pw1 / pw2   decoder.rs:346-388, GELU / gamma-residual epilogues
+//   transformer          decoder.rs:198-340, q|k|v, o (+ layer scale),
+//                        gate|up rows interleaved (SwiGLU epilogue), down
+// Epilogues fuse the bias, SnakeBeta (conv.rs:620-640) of the next stage,
+// the residual adds and the layer scales.  Small kernels do the VQ gather,
+// the column RMSNorm, RoPE, sliding-window attention, depthwise conv +
+// LayerNorm and the one-channel output conv with its clamp.
+
+#include "qtts_device.h"
+#include "qtts_kernels.h"
+#include "qtts_devutil.h"
+
+#include <algorithm>
+
+namespace qtts {
+
+// ---------------------------------------------------------------------------
+// implicit-GEMM convolution
+// ---------------------------------------------------------------------------
+
+constexpr int CGN = 128, CGK = 32, CLD = CGK + 4;
+
+enum ConvEpi : int {
+    CE_STORE = 0,        // y = acc + bias
+    CE_SNAKE = 1,        // y = snake(acc + bias)
+    CE_STORE_SNAKE = 2,  // x = acc + bias (+ res); y = snake(x)
+    CE_GELU = 3,         // y = gelu(acc + bias)
+    CE_SCALE_RES = 4,    // y += scale * (acc + bias)
+    CE_SWIGLU = 5,       // rows (2j, 2j+1) = (gate, up): y[j] = silu(gate) * up
+};
+
+struct ConvIn {
+    const float *x;      // [IC][L_in] (row stride ldx)
+    int ldx, L_in;
+    int IC, K, dil, pad; // tap j of channel ic reads x[ic][t + j*dil - pad]
+};
+
+struct ConvOut {
+    float *y;            // y[oc * ldy + t * os + oo]
+    int ldy, os, oo;
+    const float *bias;   // [M] or null
+    const float *res;    // CE_STORE_SNAKE: residual added to x (same indexing), or null
+    float *x;            // CE_STORE_SNAKE: pre-activation output
+    const float *alpha, *beta;   // snake parameters [M]
+    const float *scale;  // CE_SCALE_RES: [M]
+};
+
+template <int MB, int EPI>
+__global__ void __launch_bounds__(256, 2)
+k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, int tm)
+{
+    constexpr int BM = 16 * MB;
+    constexpr int NA = (BM * CGK / 4 + 255) / 256;
+    __shared__ __attribute__((aligned(16))) float As[2][BM * CLD];
+    __shared__ __attribute__((aligned(16))) float Bs[2][CGN * CLD];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int mt = blockIdx.x % tm, nt = blockIdx.x / tm;
+    const int m0 = mt * BM, n0 = nt * CGN;
+
+    // A slots: row slot/8, k 4*(slot%8)
+    const float *arow[NA];
+    int aoff[NA], akk[NA];
+    bool aok[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) {
+        const int slot = min(t + 256 * j, BM * CGK / 4 - 1);
+        const int r = slot >> 3, m = m0 + r;
+        aok[j] = m < M;
+        arow[j] = A + (size_t)min(m, M - 1) * Kd;
+        aoff[j] = r * CLD + 4 * (slot & 7);
+        akk[j] = 4 * (slot & 7);
+    }
+    // B: column n0 + (t & 127); k quads kq, kq + 2, kq + 4, kq + 6 of the chunk
+    const int bcol = t & 127, bq = t >> 7;
+    const int pos0 = n0 + bcol;
+    const bool bcok = pos0 < N;
+    const float *xb = in.x;
+
+    struct Fetch {
+        f32x4 a[NA];
+        f32x4 b[4];
+    };
+    auto fetch = [&](Fetch &f, int k0) {
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            const int kk = k0 + akk[j];
+            if ((Kd & 3) == 0 && kk + 3 < Kd) {   // rows 16-byte aligned
+                f.a[j] = ld4(arow[j] + kk);
+            } else {
+                f32x4 v;
+                v.x = arow[j][min(kk, Kd - 1)];
+                v.y = arow[j][min(kk + 1, Kd - 1)];
+                v.z = arow[j][min(kk + 2, Kd - 1)];
+                v.w = arow[j][min(kk + 3, Kd - 1)];
+                v.x = kk < Kd ? v.x : 0.0f;
+                v.y = kk + 1 < Kd ? v.y : 0.0f;
+                v.z = kk + 2 < Kd ? v.z : 0.0f;
+                v.w = kk + 3 < Kd ? v.w : 0.0f;
+                f.a[j] = v;
+            }
+            f.a[j] = aok[j] ? f.a[j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int kq = bq + 2 * i;
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int kk = k0 + 4 * kq + e;
+                const int ic = kk / in.K, tap = kk - ic * in.K;
+                const int p = pos0 + tap * in.dil - in.pad;
+                const bool ok = bcok && kk < Kd && p >= 0 && p < in.L_in;
+                const float xv = xb[(size_t)min(ic, in.IC - 1) * in.ldx + min(max(p, 0), in.L_in - 1)];
+                v[e] = ok ? xv : 0.0f;
+            }
+            f.b[i] = f32x4{v[0], v[1], v[2], v[3]};
+        }
+    };
+    auto stage = [&](const Fetch &f, int buf) {
+#pragma unroll
+        for (int j = 0; j < NA; j++) *(f32x4 *)&As[buf][aoff[j]] = f.a[j];
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(f32x4 *)&Bs[buf][bcol * CLD + 4 * (bq + 2 * i)] = f.b[i];
+    };
+
+    const int r16 = lane & 15, q = lane >> 4;
+    f32x4 acc[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mfma = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < CGK / 16; kk++) {
+            f32x4 av[MB], bv[2];
+#pragma unroll
+            for (int i = 0; i < MB; i++) av[i] = *(const f32x4 *)&As[buf][(16 * i + r16) * CLD + 16 * kk + 4 * q];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (2 * wv + j) + r16) * CLD + 16 * kk + 4 * q];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int i = 0; i < MB; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int nch = (Kd + CGK - 1) / CGK;
+    Fetch fa, fb;
+    fetch(fa, 0);
+    if (nch > 1) fetch(fb, CGK);
+    stage(fa, 0);
+    __syncthreads();
+    int c = 0;
+    for (; c + 3 < nch; c += 2) {
+        fetch(fa, (c + 2) * CGK);
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        fetch(fb, (c + 3) * CGK);
+        mfma(1);
+        stage(fa, 0);
+        __syncthreads();
+    }
+    if (c + 2 < nch) {
+        fetch(fa, (c + 2) * CGK);
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        mfma(1);
+        stage(fa, 0);
+        __syncthreads();
+        mfma(0);
+    } else if (c + 1 < nch) {
+        mfma(0);
+        stage(fb, 1);
+        __syncthreads();
+        mfma(1);
+    } else {
+        mfma(0);
+    }
+
+    // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + 16 * (2 * wv + j) + r16;
+            if (n >= N) continue;
+            const int col = n * o.os + o.oo;
+            if (EPI == CE_SWIGLU) {
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const int m = m0 + 16 * i + 4 * q + e;   // even: gate row, m + 1: up row
+                    if (m + 1 >= M) continue;
+                    const float g = acc[i][j][e] + (o.bias ? o.bias[m] : 0.0f);
+                    const float u = acc[i][j][e + 1] + (o.bias ? o.bias[m + 1] : 0.0f);
+                    o.y[(size_t)(m >> 1) * o.ldy + col] = silu_f(g) * u;
+                }
+                continue;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + 16 * i + 4 * q + e;
+                if (m >= M) continue;
+                const size_t idx = (size_t)m * o.ldy + col;
+                const float v = acc[i][j][e] + (o.bias ? o.bias[m] : 0.0f);
+                if (EPI == CE_STORE) {
+                    o.y[idx] = v;
+                } else if (EPI == CE_GELU) {
+                    o.y[idx] = v * 0.5f * (1.0f + tanhf(v * 0.7071067811865476f));
+                } else if (EPI == CE_SCALE_RES) {
+                    o.y[idx] = o.y[idx] + o.scale[m] * v;
+                } else {
+                    const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + o.res[idx] : v;
+                    const float a = expf(o.alpha[m]), ib = expf(-o.beta[m]);
+                    const float s = sinf(a * xv);
+                    if (EPI == CE_STORE_SNAKE) o.x[idx] = xv;
+                    o.y[idx] = xv + ib * s * s;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// small kernels
+// ---------------------------------------------------------------------------
+
+// VQ inputs (codebook_lookup, decoder.rs:147-191) as one contraction of
+// 2*D rows: rows 0..D-1 = first codebook row of code 0, rows D..2D-1 = the
+// sum of the other codebooks' rows (added in codebook order).  codes
+// [n_cb][T]; out [2D][T].
+__global__ void k_vq_gather(const float *first, const float *const *rest, int n_rest, int D, const uint32_t *codes,
+                            int T, int rows_cb, float *out)
+{
+    const int d = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const uint32_t c0 = min(codes[t], (uint32_t)(rows_cb - 1));
+    out[(size_t)d * T + t] = first[(size_t)c0 * D + d];
+    float s = 0.0f;
+    for (int g = 0; g < n_rest; g++) {
+        const uint32_t c = min(codes[(size_t)(g + 1) * T + t], (uint32_t)(rows_cb - 1));
+        s += rest[g][(size_t)c * D + d];
+    }
+    out[(size_t)(D + d) * T + t] = s;
+}
+
+// Column RMSNorm (rms_norm_f32, decoder.rs:589-598) of x [H][T]: one thread
+// per position, the channel sum in channel order.
+__global__ void k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *out)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    float ss = 0.0f;
+    for (int h = 0; h < H; h++) {
+        const float v = x[(size_t)h * T + t];
+        ss += v * v;
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+    for (int h = 0; h < H; h++) out[(size_t)h * T + t] = x[(size_t)h * T + t] * inv * gamma[h];
+}
+
+// Rotate-half RoPE (apply_rope_split_half, decoder.rs:631-655) of the q and
+// k rows of qkv [3A][T] in place; positions past the table stay unrotated.
+__global__ void k_rope_cf(float *qkv, int heads, int hd, int T, const float *cs, const float *sn, int64_t rope_rows)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x, hi = blockIdx.y;   // hi: q heads then k heads
+    const int half = hd / 2;
+    if (t >= T || t >= rope_rows) return;
+    float *b = qkv + (size_t)hi * hd * T;
+    for (int i = 0; i < half; i++) {
+        const float x0 = b[(size_t)i * T + t], x1 = b[(size_t)(half + i) * T + t];
+        const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+        b[(size_t)i * T + t] = x0 * c - x1 * s;
+        b[(size_t)(half + i) * T + t] = x1 * c + x0 * s;
+    }
+}
+
+// Causal sliding-window attention (decoder.rs:264-291): thread per (head,
+// query position); keys t-W+1..t; online softmax; out [A][T].
+template <int HD>
+__global__ void __launch_bounds__(64)
+k_dec_attn(const float *qkv, int heads, int T, int W, float *out)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x, h = blockIdx.y;
+    if (t >= T) return;
+    const size_t A = (size_t)heads * HD;
+    const float *q = qkv + (size_t)h * HD * T, *k = qkv + (A + (size_t)h * HD) * T, *v = qkv + (2 * A + (size_t)h * HD) * T;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float qr[HD], acc[HD];
+#pragma unroll
+    for (int d = 0; d < HD; d++) {
+        qr[d] = q[(size_t)d * T + t];
+        acc[d] = 0.0f;
+    }
+    const int start = t + 1 > W ? t + 1 - W : 0;
+    float m = -INFINITY, l = 0.0f;
+    for (int s = start; s <= t; s++) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int d = 0; d < HD; d++) dot = fmaf(qr[d], k[(size_t)d * T + s], dot);
+        const float sc = dot * scale;
+        const float mn = fmaxf(m, sc);
+        const float f = expf(m - mn), p = expf(sc - mn);
+        l = l * f + p;
+#pragma unroll
+        for (int d = 0; d < HD; d++) acc[d] = fmaf(p, v[(size_t)d * T + s], acc[d] * f);
+        m = mn;
+    }
+    const float il = 1.0f / l;
+#pragma unroll
+    for (int d = 0; d < HD; d++) out[((size_t)h * HD + d) * T + t] = acc[d] * il;
+}
+
+// ConvNeXt front (decoder.rs:346-352): causal depthwise conv then LayerNorm
+// over channels per position (layer_norm_channel_first, decoder.rs:668-690).
+// One workgroup per 64 positions: thread (c-lane, t): dw values go to the
+// output buffer, then the column statistics.
+__global__ void __launch_bounds__(256)
+k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int K, const float *g, const float *b,
+        float eps, float *out)
+{
+    __shared__ float red[4][64][2];
+    const int tl = threadIdx.x & 63, cg = threadIdx.x >> 6;
+    const int t = blockIdx.x * 64 + tl;
+    const bool ok = t < L;
+    float s1 = 0.0f;
+    for (int c = cg; c < C; c += 4) {
+        float v = dw_b[c];
+        for (int k = 0; k < K; k++) {
+            const int p = t + k - (K - 1);
+            v += (ok && p >= 0) ? x[(size_t)c * L + p] * dw_w[c * K + k] : 0.0f;
+        }
+        if (ok) out[(size_t)c * L + t] = v;
+        s1 += v;
+    }
+    red[cg][tl][0] = s1;
+    __syncthreads();
+    const float mean = ((red[0][tl][0] + red[1][tl][0]) + (red[2][tl][0] + red[3][tl][0])) / (float)C;
+    float s2 = 0.0f;
+    for (int c = cg; c < C; c += 4) {
+        const float d = ok ? out[(size_t)c * L + t] - mean : 0.0f;
+        s2 += d * d;
+    }
+    red[cg][tl][1] = s2;
+    __syncthreads();
+    const float var = ((red[0][tl][1] + red[1][tl][1]) + (red[2][tl][1] + red[3][tl][1])) / (float)C;
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (!ok) return;
+    for (int c = cg; c < C; c += 4) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
+}
+
+// Output conv (one channel, causal, conv.rs:191-228) on the snake input,
+// clamp to [-1, 1] (decoder.rs:567-570), written from sample `cut` on.
+__global__ void k_out_conv(const float *x, int C, int L, const float *w, float bias, int K, int dil, int64_t cut,
+                           float *out)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= L || t < cut) return;
+    const int pad = (K - 1) * dil;
+    float s = bias;
+    for (int c = 0; c < C; c++)
+        for (int k = 0; k < K; k++) {
+            const int p = t + k * dil - pad;
+            if (p >= 0) s += x[(size_t)c * L + p] * w[c * K + k];
+        }
+    out[t - cut] = s < -1.0f ? -1.0f : (s > 1.0f ? 1.0f : s);
+}
+
+// SnakeBeta over [C][L] (snake_beta, conv.rs:545-640), out-of-place.
+__global__ void k_snake(const float *x, int C, int L, const float *alpha, const float *beta, float *out)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x, c = blockIdx.y;
+    if (t >= L) return;
+    const float a = expf(alpha[c]), ib = expf(-beta[c]);
+    const float v = x[(size_t)c * L + t];
+    const float s = sinf(a * v);
+    out[(size_t)c * L + t] = v + ib * s * s;
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+
+#define DCHK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return e_; } while (0)
+
+static int conv_mb(int M)
+{
+    return M >= 64 ? 4 : (M >= 32 ? 2 : 1);
+}
+
+template <int EPI>
+static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvOut &o, int N, hipStream_t s)
+{
+    const int Kd = in.IC * in.K;
+    if (M < 1 || N < 1 || Kd < 1) return hipErrorInvalidValue;
+    const int mb = conv_mb(M), tm = (M + 16 * mb - 1) / (16 * mb), tn = (N + CGN - 1) / CGN;
+    const dim3 grid(tm * tn);
+    switch (mb) {
+    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
+    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
+    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
+    }
+    return hipGetLastError();
+}
+
+static ConvIn causal_in(const float *x, int IC, int L, int K, int dil)
+{
+    return ConvIn{x, L, L, IC, K, dil, (K - 1) * dil};
+}
+
+static ConvOut plain_out(float *y, int ld, const float *bias)
+{
+    ConvOut o{};
+    o.y = y;
+    o.ldy = ld;
+    o.os = 1;
+    o.bias = bias;
+    return o;
+}
+
+// Transposed conv with kernel 2*stride or stride (padding 0), cropped to
+// L_in * stride positions (decoder.rs:472-486, 512-525), as `stride` phase
+// GEMMs.  Phase r's weights (repacked at upload) are [OC][IC*taps]: taps =
+// 2 reads x[i-1] (kernel tap r + stride) then x[i] (tap r); taps = 1 reads
+// x[i] (tap r).
+template <int EPI>
+static hipError_t conv_t_phases(const DecConvT &w, const float *x, int L_in, ConvOut o, hipStream_t s)
+{
+    const int taps = w.taps;
+    for (int r = 0; r < w.stride; r++) {
+        ConvIn in{x, L_in, L_in, w.ic, taps, 1, taps - 1};
+        ConvOut op = o;
+        op.os = w.stride;
+        op.oo = r;
+        DCHK(conv_gemm<EPI>(w.phases + (size_t)r * w.oc * w.ic * taps, w.oc, in, op, L_in, s));
+    }
+    return hipSuccess;
+}
+
+hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
+                          float *audio, hipStream_t s)
+{
+    if (T < 1 || T > ws.cap_frames) return hipErrorInvalidValue;
+    const int D = d.codebook_dim, V = d.vq_dim, H = d.hidden, A = d.n_heads * d.head_dim, I = d.inter;
+    const int LAT = d.latent;
+    // 1. VQ -> [V][T]
+    hipLaunchKernelGGL(k_vq_gather, dim3((T + 63) / 64, D), dim3(64), 0, s, d.first_codebook, d.rest_codebooks,
+                       d.n_rest, D, codes, T, d.codebook_size, ws.a);
+    DCHK(hipGetLastError());
+    DCHK(conv_gemm<CE_STORE>(d.vq_proj, V, causal_in(ws.a, 2 * D, T, 1, 1), plain_out(ws.b, T, nullptr), T, s));
+    // 2. pre-conv -> [LAT][T]
+    DCHK(conv_gemm<CE_STORE>(d.pre_conv.w, d.pre_conv.oc, causal_in(ws.b, V, T, d.pre_conv.k, d.pre_conv.dil),
+                             plain_out(ws.a, T, d.pre_conv.b), T, s));
+    // 3. transformer on [H][T]: x in ws.b, normed in ws.c, q|k|v in ws.d, attention in ws.e
+    DCHK(conv_gemm<CE_STORE>(d.tf_in_w, H, causal_in(ws.a, LAT, T, 1, 1), plain_out(ws.b, T, d.tf_in_b), T, s));
+    const dim3 cols((T + 255) / 256);
+    for (int l = 0; l < d.n_tf; l++) {
+        const DecLayer &L = d.tf[l];
+        hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
+        DCHK(hipGetLastError());
+        DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, s));
+        hipLaunchKernelGGL(k_rope_cf, dim3((T + 63) / 64, 2 * d.n_heads), dim3(64), 0, s, ws.d, d.n_heads,
+                           d.head_dim, T, d.rope_cos, d.rope_sin, d.rope_rows);
+        DCHK(hipGetLastError());
+        if (d.head_dim == 64)
+            hipLaunchKernelGGL(k_dec_attn<64>, dim3((T + 63) / 64, d.n_heads), dim3(64), 0, s, ws.d, d.n_heads, T,
+                               d.window, ws.e);
+        else
+            hipLaunchKernelGGL(k_dec_attn<16>, dim3((T + 63) / 64, d.n_heads), dim3(64), 0, s, ws.d, d.n_heads, T,
+                               d.window, ws.e);
+        DCHK(hipGetLastError());
+        ConvOut ro = plain_out(ws.b, T, nullptr);
+        ro.scale = L.attn_scale;
+        DCHK(conv_gemm<CE_SCALE_RES>(L.o, H, causal_in(ws.e, A, T, 1, 1), ro, T, s));
+        hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.post_norm, H, T, 1e-5f, ws.c);
+        DCHK(hipGetLastError());
+        DCHK(conv_gemm<CE_SWIGLU>(L.gate_up, 2 * I, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, s));
+        ConvOut mo = plain_out(ws.b, T, nullptr);
+        mo.scale = L.mlp_scale;
+        DCHK(conv_gemm<CE_SCALE_RES>(L.down, H, causal_in(ws.d, I, T, 1, 1), mo, T, s));
+    }
+    hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, d.tf_norm, H, T, 1e-5f, ws.c);
+    DCHK(hipGetLastError());
+    DCHK(conv_gemm<CE_STORE>(d.tf_out_w, LAT, causal_in(ws.c, H, T, 1, 1), plain_out(ws.a, T, d.tf_out_b), T, s));
+    // 4. upsample stages: ConvT (phases) then ConvNeXt; the signal moves
+    // between ws.a and ws.b
+    int L = T;
+    float *sig = ws.a, *other = ws.b;
+    for (int u = 0; u < d.n_up; u++) {
+        const DecUpsample &U = d.up[u];
+        const int Lo = L * U.conv_t.stride;
+        DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), s));
+        L = Lo;
+        hipLaunchKernelGGL(k_dw_ln, dim3((L + 63) / 64), dim3(256), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
+                           U.norm_w, U.norm_b, 1e-5f, ws.c);
+        DCHK(hipGetLastError());
+        DCHK(conv_gemm<CE_GELU>(U.pw1, U.inner, causal_in(ws.c, U.ch, L, 1, 1), plain_out(ws.d, L, U.pw1_b), L, s));
+        ConvOut po = plain_out(other, L, U.pw2_b);
+        po.scale = U.gamma;
+        DCHK(conv_gemm<CE_SCALE_RES>(U.pw2, U.ch, causal_in(ws.d, U.inner, L, 1, 1), po, L, s));
+        std::swap(sig, other);
+    }
+    // 5. Vocos: init conv with the first block's pre-snake (or the final
+    // snake) fused
+    const float *na = d.n_voc ? d.voc[0].pre_alpha : d.final_alpha;
+    const float *nb = d.n_voc ? d.voc[0].pre_beta : d.final_beta;
+    {
+        ConvOut so = plain_out(ws.c, L, d.voc_init.b);
+        so.alpha = na;
+        so.beta = nb;
+        DCHK(conv_gemm<CE_SNAKE>(d.voc_init.w, d.voc_init.oc,
+                                 causal_in(sig, d.voc_init.ic, L, d.voc_init.k, d.voc_init.dil), so, L, s));
+    }
+    int ch = d.voc_init.oc;
+    float *sn = ws.c, *x = sig, *t1 = other;   // snake(x) / x / scratch
+    for (int b = 0; b < d.n_voc; b++) {
+        const DecVocos &B = d.voc[b];
+        const int Lo = L * B.up.stride;
+        ch = B.up.oc;
+        // ConvT phases: x = convT(snake); sn = snake of the first residual's act1
+        const bool has_res = B.n_res > 0;
+        ConvOut xo = plain_out(x, Lo, B.up.b);
+        xo.x = x;
+        xo.y = t1;
+        xo.alpha = has_res ? B.res[0].a1_alpha : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
+        xo.beta = has_res ? B.res[0].a1_beta : (b + 1 < d.n_voc ? d.voc[b + 1].pre_beta : d.final_beta);
+        DCHK(conv_t_phases<CE_STORE_SNAKE>(B.up, sn, L, xo, s));
+        L = Lo;
+        std::swap(sn, t1);   // sn = snake(x)
+        for (int r = 0; r < B.n_res; r++) {
+            const DecVocosRes &R = B.res[r];
+            // conv1 (k 7, dilation) with act2 fused: t1 = snake2(conv1(sn))
+            ConvOut c1 = plain_out(t1, L, R.c1.b);
+            c1.alpha = R.a2_alpha;
+            c1.beta = R.a2_beta;
+            DCHK(conv_gemm<CE_SNAKE>(R.c1.w, ch, causal_in(sn, ch, L, R.c1.k, R.c1.dil), c1, L, s));
+            // conv2 (k 1) + residual: x += conv2(t1); sn = next snake(x)
+            const float *nal = r + 1 < B.n_res ? B.res[r + 1].a1_alpha
+                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
+            const float *nbe = r + 1 < B.n_res ? B.res[r + 1].a1_beta
+                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_beta : d.final_beta);
+            ConvOut c2 = plain_out(sn, L, R.c2.b);
+            c2.x = x;
+            c2.res = x;
+            c2.alpha = nal;
+            c2.beta = nbe;
+            DCHK(conv_gemm<CE_STORE_SNAKE>(R.c2.w, ch, causal_in(t1, ch, L, R.c2.k, R.c2.dil), c2, L, s));
+        }
+    }
+    // 6. output conv on snake(x) + clamp, first `cut` samples dropped
+    hipLaunchKernelGGL(k_out_conv, dim3((L + 255) / 256), dim3(256), 0, s, sn, ch, L, d.out_w, d.out_b, d.out_k,
+                       d.out_dil, cut, audio);
+    return hipGetLastError();
+}
+
+}  // namespace qtts

@@ -82,6 +82,71 @@ struct PrefillWs {
     int cap_rows;
 };
 
+// Speech decoder on the device (qtts_decoder.hip).  Matrices are stored as
+// the GEMM's A operand, [output channels][input channels x taps].
+struct DecConv {
+    const float *w, *b;      // w [oc][ic*k]
+    int ic, oc, k, dil;
+};
+struct DecConvT {            // kernel == stride (1 tap) or 2*stride (2 taps), padding 0
+    const float *phases, *b; // [stride][oc][ic*taps]; 2 taps: x[i-1] (kernel tap r+stride), x[i] (tap r)
+    int ic, oc, stride, taps;
+};
+struct DecLayer {
+    const float *qkv;        // [3A][hidden] rows q, k, v
+    const float *o;          // [hidden][A]
+    const float *gate_up;    // [2 inter][hidden] rows gate_j, up_j interleaved
+    const float *down;       // [hidden][inter]
+    const float *in_norm, *post_norm, *attn_scale, *mlp_scale;
+};
+struct DecUpsample {
+    DecConvT conv_t;
+    const float *dw_w, *dw_b;
+    int dw_k;
+    const float *norm_w, *norm_b;
+    const float *pw1, *pw1_b;   // [inner][ch]
+    const float *pw2, *pw2_b;   // [ch][inner]
+    const float *gamma;
+    int ch, inner;
+};
+struct DecVocosRes {
+    const float *a1_alpha, *a1_beta, *a2_alpha, *a2_beta;
+    DecConv c1, c2;
+};
+struct DecVocos {
+    const float *pre_alpha, *pre_beta;
+    DecConvT up;
+    const DecVocosRes *res;  // host array
+    int n_res;
+};
+struct DecoderDev {
+    int hidden, n_heads, head_dim, inter, window, codebook_dim, codebook_size, vq_dim, latent, n_rest;
+    const float *first_codebook;
+    const float *const *rest_codebooks;   // device array of n_rest device pointers
+    const float *vq_proj;                 // [vq_dim][2 codebook_dim]: first | rest output projections
+    DecConv pre_conv;
+    const float *tf_in_w, *tf_in_b;       // [hidden][latent]
+    const DecLayer *tf;                   // host array
+    int n_tf;
+    const float *tf_norm, *tf_out_w, *tf_out_b;   // tf_out_w [latent][hidden]
+    const DecUpsample *up;                // host array
+    int n_up;
+    DecConv voc_init;
+    const DecVocos *voc;                  // host array
+    int n_voc;
+    const float *final_alpha, *final_beta;
+    const float *out_w;                   // [ch][k], one output channel
+    float out_b;
+    int out_k, out_dil;
+    const float *rope_cos, *rope_sin;
+    int64_t rope_rows;
+};
+struct DecoderWs {
+    float *a, *b, *c, *d, *e;             // each floats_per_frame * cap_frames
+    uint32_t *codes;                      // [n_rest + 1][cap_frames]
+    int cap_frames;
+};
+
 struct SampleArgsHost {
     float temperature, top_p, rep;
     int top_k;
@@ -136,6 +201,8 @@ hipError_t enqueue_row_inv(const float *X, int ld, int M, int K, float *inv, hip
 hipError_t enqueue_gemm_gateup(const TalkerDev &m, const PrefillWs &pw, int l, int M, hipStream_t s);
 hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M, int64_t start,
                                   float *hidden_out, hipStream_t s);
+hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
+                          float *audio, hipStream_t s);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
                                hipStream_t s);

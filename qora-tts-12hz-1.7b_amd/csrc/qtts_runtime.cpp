@@ -63,6 +63,18 @@ struct qtts_ctx {
     PrefillWs pf{};                                  // batched-prefill rows (allocated on first use)
     void *pf_mem = nullptr;
 
+    // speech decoder (independent of the talker / predictor model)
+    bool has_decoder = false;
+    DecoderDev dec{};
+    std::vector<DecLayer> dec_layers;
+    std::vector<DecUpsample> dec_up;
+    std::vector<DecVocos> dec_voc;
+    std::vector<std::vector<DecVocosRes>> dec_res;
+    std::vector<void *> dec_allocs;
+    int64_t dec_floats_per_frame = 0;                // largest stage, [channels][positions] per frame
+    DecoderWs dws{};
+    void *dws_mem = nullptr;
+
     // Talker KV page pool: 2 * kv_cap/64 physical pages shared by the running
     // sequence and captured prefixes.  seq_ptab is the host copy of the
     // sequence's page table (d_ptab on the device), page_ref counts the
@@ -423,6 +435,8 @@ extern "C" void qtts_ctx_destroy(qtts_ctx *c)
     if (c->d_io) hipFree(c->d_io);
     if (c->d_io2) hipFree(c->d_io2);
     if (c->d_copy) hipFree(c->d_copy);
+    free_list(c->dec_allocs);
+    if (c->dws_mem) hipFree(c->dws_mem);
     if (c->st_gen) hipFree(c->st_gen);
     if (c->st_api) hipFree(c->st_api);
     if (c->h_st) hipHostFree(c->h_st);
@@ -1286,6 +1300,307 @@ extern "C" int qtts_build_icl_block(qtts_ctx *c, const uint32_t *ref_tokens, int
     RCHK(stage_out(c, icl, (int64_t)f_icl, icl_out, flags));
     if (rem_len) RCHK(stage_out(c, text + (size_t)icl_len * H, rem_len * (int64_t)H, remainder_out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// speech decoder
+// ---------------------------------------------------------------------------
+
+// Host matrix [k][n] (input-major) -> device [n][k] (the GEMM's A operand).
+static int upload_t(qtts_ctx *c, const float *src, int k, int n, const float **out)
+{
+    if (!src) return fail(c, QTTS_ERR_INVALID, "null matrix in decoder descriptor");
+    std::vector<float> t((size_t)k * n);
+    for (int i = 0; i < k; i++)
+        for (int j = 0; j < n; j++) t[(size_t)j * k + i] = src[(size_t)i * n + j];
+    return upload_vec(c, c->dec_allocs, t.data(), t.size(), out);
+}
+
+static int upload_conv(qtts_ctx *c, const qtts_conv1d_host &h, DecConv *d)
+{
+    if (!h.weight || !h.bias || h.in_channels < 1 || h.out_channels < 1 || h.kernel_size < 1 || h.dilation < 1)
+        return fail(c, QTTS_ERR_INVALID, "bad conv1d descriptor");
+    if (h.stride != 1) return fail(c, QTTS_ERR_UNSUPPORTED, "strided conv1d not used by the decoder");
+    d->ic = h.in_channels;
+    d->oc = h.out_channels;
+    d->k = h.kernel_size;
+    d->dil = h.dilation;
+    // [out][in][k] is already [oc][ic*k]
+    RCHK(upload_vec(c, c->dec_allocs, h.weight, (size_t)h.out_channels * h.in_channels * h.kernel_size, &d->w));
+    return upload_vec(c, c->dec_allocs, h.bias, (size_t)h.out_channels, &d->b);
+}
+
+// Transposed conv [in][out][k] -> per stride phase r: [oc][ic*taps] with
+// taps (k = 2*stride) x[i-1] <- tap r + stride, x[i] <- tap r.
+static int upload_convt(qtts_ctx *c, const qtts_convt1d_host &h, DecConvT *d)
+{
+    if (!h.weight || !h.bias || h.in_channels < 1 || h.out_channels < 1 || h.stride < 1)
+        return fail(c, QTTS_ERR_INVALID, "bad conv_transpose1d descriptor");
+    if (h.padding != 0 || (h.kernel_size != h.stride && h.kernel_size != 2 * h.stride))
+        return fail(c, QTTS_ERR_UNSUPPORTED, "conv_transpose1d needs kernel = stride or 2*stride, padding 0");
+    const int IC = h.in_channels, OC = h.out_channels, K = h.kernel_size, S = h.stride;
+    const int taps = K / S;
+    std::vector<float> p((size_t)S * OC * IC * taps);
+    for (int r = 0; r < S; r++)
+        for (int oc = 0; oc < OC; oc++)
+            for (int ic = 0; ic < IC; ic++) {
+                float *dst = &p[(((size_t)r * OC + oc) * IC + ic) * taps];
+                const float *w = h.weight + ((size_t)ic * OC + oc) * K;
+                if (taps == 2) {
+                    dst[0] = w[r + S];
+                    dst[1] = w[r];
+                } else {
+                    dst[0] = w[r];
+                }
+            }
+    d->ic = IC;
+    d->oc = OC;
+    d->stride = S;
+    d->taps = taps;
+    RCHK(upload_vec(c, c->dec_allocs, p.data(), p.size(), &d->phases));
+    return upload_vec(c, c->dec_allocs, h.bias, (size_t)OC, &d->b);
+}
+
+static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
+{
+    DecoderDev &d = c->dec;
+    auto &A = c->dec_allocs;
+    const int H = h->hidden, NH = h->n_heads, HD = h->head_dim, I = h->inter, D = h->codebook_dim, V = h->vq_dim;
+    const int LAT = h->latent, AD = NH * HD;
+    if (H < 1 || NH < 1 || (HD != 64 && HD != 16) || I < 1 || D < 1 || V < 1 || LAT < 1 || h->sliding_window < 1)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "decoder shape not supported (head_dim %d)", HD);
+    if (h->n_rest < 0 || h->n_rest > 15 || h->codebook_size < 1 || !h->first_codebook || !h->first_output_proj ||
+        (h->n_rest && (!h->rest_codebooks || !h->rest_output_proj)))
+        return fail(c, QTTS_ERR_INVALID, "decoder codebooks");
+    if (h->output_conv.out_channels != 1 || h->pre_conv.in_channels != V || h->pre_conv.out_channels != LAT)
+        return fail(c, QTTS_ERR_INVALID, "decoder conv shapes");
+    d.hidden = H; d.n_heads = NH; d.head_dim = HD; d.inter = I; d.window = h->sliding_window;
+    d.codebook_dim = D; d.codebook_size = h->codebook_size; d.vq_dim = V; d.latent = LAT; d.n_rest = h->n_rest;
+    const size_t cb = (size_t)h->codebook_size * D;
+    RCHK(upload_vec(c, A, h->first_codebook, cb, &d.first_codebook));
+    std::vector<const float *> rest(std::max(1, h->n_rest));
+    for (int g = 0; g < h->n_rest; g++) RCHK(upload_vec(c, A, h->rest_codebooks[g], cb, &rest[g]));
+    if (!h->n_rest) rest[0] = d.first_codebook;
+    const float *const *drest = nullptr;
+    RCHK(upload_vec(c, A, rest.data(), rest.size(), (const float *const **)&drest));
+    d.rest_codebooks = drest;
+    {   // [V][2D]: first | rest output projections, transposed
+        std::vector<float> vp((size_t)V * 2 * D, 0.0f);
+        for (int k = 0; k < D; k++)
+            for (int v = 0; v < V; v++) {
+                vp[(size_t)v * 2 * D + k] = h->first_output_proj[(size_t)k * V + v];
+                if (h->n_rest) vp[(size_t)v * 2 * D + D + k] = h->rest_output_proj[(size_t)k * V + v];
+            }
+        RCHK(upload_vec(c, A, vp.data(), vp.size(), &d.vq_proj));
+    }
+    RCHK(upload_conv(c, h->pre_conv, &d.pre_conv));
+    RCHK(upload_t(c, h->tf_input_w, LAT, H, &d.tf_in_w));
+    RCHK(upload_vec(c, A, h->tf_input_b, (size_t)H, &d.tf_in_b));
+    c->dec_layers.assign(h->n_tf_layers, DecLayer{});
+    for (int l = 0; l < h->n_tf_layers; l++) {
+        const qtts_dec_layer_host &L = h->tf_layers[l];
+        DecLayer &o = c->dec_layers[l];
+        if (!L.q_proj || !L.k_proj || !L.v_proj || !L.gate_proj || !L.up_proj)
+            return fail(c, QTTS_ERR_INVALID, "decoder layer %d: null matrix", l);
+        std::vector<float> qkv((size_t)3 * AD * H), gu((size_t)2 * I * H);
+        for (int k = 0; k < H; k++) {
+            for (int j = 0; j < AD; j++) {
+                qkv[(size_t)j * H + k] = L.q_proj[(size_t)k * AD + j];
+                qkv[(size_t)(AD + j) * H + k] = L.k_proj[(size_t)k * AD + j];
+                qkv[(size_t)(2 * AD + j) * H + k] = L.v_proj[(size_t)k * AD + j];
+            }
+            for (int j = 0; j < I; j++) {
+                gu[(size_t)(2 * j) * H + k] = L.gate_proj[(size_t)k * I + j];
+                gu[(size_t)(2 * j + 1) * H + k] = L.up_proj[(size_t)k * I + j];
+            }
+        }
+        RCHK(upload_vec(c, A, qkv.data(), qkv.size(), &o.qkv));
+        RCHK(upload_vec(c, A, gu.data(), gu.size(), &o.gate_up));
+        RCHK(upload_t(c, L.o_proj, AD, H, &o.o));
+        RCHK(upload_t(c, L.down_proj, I, H, &o.down));
+        RCHK(upload_vec(c, A, L.input_norm, (size_t)H, &o.in_norm));
+        RCHK(upload_vec(c, A, L.post_attn_norm, (size_t)H, &o.post_norm));
+        RCHK(upload_vec(c, A, L.attn_scale, (size_t)H, &o.attn_scale));
+        RCHK(upload_vec(c, A, L.mlp_scale, (size_t)H, &o.mlp_scale));
+    }
+    d.tf = c->dec_layers.data();
+    d.n_tf = h->n_tf_layers;
+    RCHK(upload_vec(c, A, h->tf_norm, (size_t)H, &d.tf_norm));
+    RCHK(upload_t(c, h->tf_output_w, H, LAT, &d.tf_out_w));
+    RCHK(upload_vec(c, A, h->tf_output_b, (size_t)LAT, &d.tf_out_b));
+    // per-frame sizes of every stage, for the workspace
+    int64_t fpf = std::max<int64_t>({(int64_t)2 * D, V, LAT, H, 3 * AD, I, AD});
+    int64_t factor = 1;
+    c->dec_up.assign(h->n_upsample, DecUpsample{});
+    int ch = LAT;
+    for (int u = 0; u < h->n_upsample; u++) {
+        const qtts_upsample_host &U = h->upsample[u];
+        DecUpsample &o = c->dec_up[u];
+        if (U.channels != ch || U.conv_t.in_channels != ch || U.conv_t.out_channels != ch ||
+            U.dw_conv.channels != ch || U.inner < 1)
+            return fail(c, QTTS_ERR_INVALID, "upsample stage %d shapes", u);
+        RCHK(upload_convt(c, U.conv_t, &o.conv_t));
+        RCHK(upload_vec(c, A, U.dw_conv.weight, (size_t)ch * U.dw_conv.kernel_size, &o.dw_w));
+        RCHK(upload_vec(c, A, U.dw_conv.bias, (size_t)ch, &o.dw_b));
+        o.dw_k = U.dw_conv.kernel_size;
+        RCHK(upload_vec(c, A, U.norm_w, (size_t)ch, &o.norm_w));
+        RCHK(upload_vec(c, A, U.norm_b, (size_t)ch, &o.norm_b));
+        RCHK(upload_t(c, U.pw1_w, ch, U.inner, &o.pw1));
+        RCHK(upload_vec(c, A, U.pw1_b, (size_t)U.inner, &o.pw1_b));
+        RCHK(upload_t(c, U.pw2_w, U.inner, ch, &o.pw2));
+        RCHK(upload_vec(c, A, U.pw2_b, (size_t)ch, &o.pw2_b));
+        RCHK(upload_vec(c, A, U.gamma, (size_t)ch, &o.gamma));
+        o.ch = ch;
+        o.inner = U.inner;
+        factor *= U.conv_t.stride;
+        fpf = std::max<int64_t>(fpf, (int64_t)std::max(U.inner, ch) * factor);
+    }
+    d.up = c->dec_up.data();
+    d.n_up = h->n_upsample;
+    if (h->vocos_init.in_channels != ch) return fail(c, QTTS_ERR_INVALID, "vocos init input channels");
+    RCHK(upload_conv(c, h->vocos_init, &d.voc_init));
+    ch = h->vocos_init.out_channels;
+    fpf = std::max<int64_t>(fpf, (int64_t)ch * factor);
+    c->dec_voc.assign(h->n_vocos_blocks, DecVocos{});
+    c->dec_res.assign(h->n_vocos_blocks, {});
+    for (int b = 0; b < h->n_vocos_blocks; b++) {
+        const qtts_vocos_block_host &B = h->vocos_blocks[b];
+        DecVocos &o = c->dec_voc[b];
+        if (B.upsample.in_channels != ch) return fail(c, QTTS_ERR_INVALID, "vocos block %d input channels", b);
+        RCHK(upload_vec(c, A, B.pre_snake_alpha, (size_t)ch, &o.pre_alpha));
+        RCHK(upload_vec(c, A, B.pre_snake_beta, (size_t)ch, &o.pre_beta));
+        RCHK(upload_convt(c, B.upsample, &o.up));
+        ch = B.upsample.out_channels;
+        factor *= B.upsample.stride;
+        fpf = std::max<int64_t>(fpf, (int64_t)ch * factor);
+        c->dec_res[b].assign(B.n_residuals, DecVocosRes{});
+        for (int r = 0; r < B.n_residuals; r++) {
+            const qtts_vocos_res_host &R = B.residuals[r];
+            DecVocosRes &q = c->dec_res[b][r];
+            if (R.conv1.in_channels != ch || R.conv1.out_channels != ch || R.conv2.in_channels != ch ||
+                R.conv2.out_channels != ch)
+                return fail(c, QTTS_ERR_INVALID, "vocos residual %d.%d shapes", b, r);
+            RCHK(upload_vec(c, A, R.act1_alpha, (size_t)ch, &q.a1_alpha));
+            RCHK(upload_vec(c, A, R.act1_beta, (size_t)ch, &q.a1_beta));
+            RCHK(upload_vec(c, A, R.act2_alpha, (size_t)ch, &q.a2_alpha));
+            RCHK(upload_vec(c, A, R.act2_beta, (size_t)ch, &q.a2_beta));
+            RCHK(upload_conv(c, R.conv1, &q.c1));
+            RCHK(upload_conv(c, R.conv2, &q.c2));
+        }
+        o.res = c->dec_res[b].data();
+        o.n_res = B.n_residuals;
+    }
+    d.voc = c->dec_voc.data();
+    d.n_voc = h->n_vocos_blocks;
+    if (h->output_conv.in_channels != ch) return fail(c, QTTS_ERR_INVALID, "output conv input channels");
+    RCHK(upload_vec(c, A, h->final_snake_alpha, (size_t)ch, &d.final_alpha));
+    RCHK(upload_vec(c, A, h->final_snake_beta, (size_t)ch, &d.final_beta));
+    RCHK(upload_vec(c, A, h->output_conv.weight, (size_t)ch * h->output_conv.kernel_size, &d.out_w));
+    d.out_b = h->output_conv.bias[0];
+    d.out_k = h->output_conv.kernel_size;
+    d.out_dil = h->output_conv.dilation;
+    if (!h->rope_cos || !h->rope_sin || h->rope_max_pos < 1) return fail(c, QTTS_ERR_INVALID, "decoder rope tables");
+    RCHK(upload_vec(c, A, h->rope_cos, (size_t)h->rope_max_pos * (HD / 2), &d.rope_cos));
+    RCHK(upload_vec(c, A, h->rope_sin, (size_t)h->rope_max_pos * (HD / 2), &d.rope_sin));
+    d.rope_rows = h->rope_max_pos;
+    c->dec_floats_per_frame = fpf;
+    return QTTS_OK;
+}
+
+static void free_decoder(qtts_ctx *c)
+{
+    free_list(c->dec_allocs);
+    if (c->dws_mem) hipFree(c->dws_mem);
+    c->dws_mem = nullptr;
+    c->dws = DecoderWs{};
+    c->has_decoder = false;
+}
+
+extern "C" int qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_host *d)
+{
+    if (!c || !d) return QTTS_ERR_INVALID;
+    hipSetDevice(c->device);
+    free_decoder(c);
+    const int r = upload_decoder(c, d);
+    if (r != QTTS_OK) {
+        free_decoder(c);
+        return r;
+    }
+    c->has_decoder = true;
+    return QTTS_OK;
+}
+
+static int ensure_dec_ws(qtts_ctx *c, int frames)
+{
+    if (frames <= c->dws.cap_frames) return QTTS_OK;
+    if (c->dws_mem) hipFree(c->dws_mem);
+    c->dws_mem = nullptr;
+    c->dws = DecoderWs{};
+    const size_t per = (size_t)c->dec_floats_per_frame * frames;
+    void *m = nullptr;
+    HIPCHK(c, hipMalloc(&m, 5 * per * sizeof(float) + (size_t)16 * frames * sizeof(uint32_t)));
+    c->dws_mem = m;
+    float *f = (float *)m;
+    c->dws.a = f;
+    c->dws.b = f + per;
+    c->dws.c = f + 2 * per;
+    c->dws.d = f + 3 * per;
+    c->dws.e = f + 4 * per;
+    c->dws.codes = (uint32_t *)(f + 5 * per);
+    c->dws.cap_frames = frames;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_decode_to_audio(qtts_ctx *c, const uint32_t *codes, int64_t n_frames, const uint32_t *warmup,
+                                    int64_t n_warmup, float *audio, int64_t capacity, int64_t *n_samples, int flags)
+{
+    if (!c || !n_samples) return QTTS_ERR_INVALID;
+    *n_samples = 0;
+    if (!c->has_decoder) return fail(c, QTTS_ERR_STATE, "no speech decoder uploaded");
+    if (n_frames < 0 || n_warmup < 0 || (n_frames && !codes) || (n_warmup && !warmup)) return QTTS_ERR_INVALID;
+    if (n_frames == 0) return QTTS_OK;   // decode_to_audio returns no samples for no codes
+    const DecoderDev &d = c->dec;
+    const int ncb = d.n_rest + 1;
+    const int64_t T = n_frames + n_warmup;
+    if (T > (1 << 20)) return fail(c, QTTS_ERR_CAPACITY, "too many frames");
+    for (int64_t i = 0; i < (int64_t)ncb * n_frames; i++)
+        if (codes[i] >= (uint32_t)d.codebook_size) return fail(c, QTTS_ERR_INVALID, "code %u out of range", codes[i]);
+    for (int64_t i = 0; i < (int64_t)ncb * n_warmup; i++)
+        if (warmup[i] >= (uint32_t)d.codebook_size) return fail(c, QTTS_ERR_INVALID, "warmup code out of range");
+    int64_t factor = 1;
+    for (int u = 0; u < d.n_up; u++) factor *= d.up[u].conv_t.stride;
+    for (int b = 0; b < d.n_voc; b++) factor *= d.voc[b].up.stride;
+    const int64_t len = T * factor;
+    // warmup_trim_len (decoder.rs:661-666)
+    const int64_t cut = n_warmup ? std::min<int64_t>(n_warmup * len / T, len) : 0;
+    const int64_t n = len - cut;
+    if (!audio || capacity < n) {
+        *n_samples = n;
+        return fail(c, QTTS_ERR_CAPACITY, "audio buffer holds %lld samples, %lld needed", (long long)capacity,
+                    (long long)n);
+    }
+    hipSetDevice(c->device);
+    RCHK(ensure_dec_ws(c, (int)T));
+    // codes of warmup ++ frames, codebook-major [ncb][T]
+    std::vector<uint32_t> all((size_t)ncb * T);
+    for (int g = 0; g < ncb; g++) {
+        if (n_warmup) memcpy(&all[(size_t)g * T], warmup + (size_t)g * n_warmup, n_warmup * sizeof(uint32_t));
+        memcpy(&all[(size_t)g * T + n_warmup], codes + (size_t)g * n_frames, n_frames * sizeof(uint32_t));
+    }
+    HIPCHK(c, hipMemcpyAsync(c->dws.codes, all.data(), all.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                             c->stream));
+    float *out = audio;
+    DevScratch tmp;
+    if (!(flags & QTTS_DEVICE_PTRS)) {
+        HIPCHK(c, hipMalloc(&tmp.p, (size_t)n * sizeof(float)));
+        out = (float *)tmp.p;
+    }
+    HIPCHK(c, enqueue_decode(d, c->dws, c->dws.codes, (int)T, cut, out, c->stream));
+    if (!(flags & QTTS_DEVICE_PTRS))
+        HIPCHK(c, hipMemcpyAsync(audio, out, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *n_samples = n;
     return QTTS_OK;
 }
 

@@ -22,7 +22,7 @@ from ctypes import POINTER, byref, c_char_p, c_double, c_float, c_int, c_int32, 
 import numpy as np
 
 from . import hostdesc
-from .hostdesc import PredictorHost, Q4Host, SampleParams, TalkerHost, ptr, sample_params
+from .hostdesc import DecoderHost, PredictorHost, Q4Host, SampleParams, TalkerHost, decoder_host, ptr, sample_params
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libqtts_hip.so")
@@ -74,6 +74,9 @@ SIGNATURES = {
     "qtts_embed_text_tokens": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
     "qtts_build_icl_block": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                               c_void_p, c_int], c_int),
+    "qtts_decoder_upload": ([c_void_p, POINTER(DecoderHost)], c_int),
+    "qtts_decode_to_audio": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int64),
+                              c_int], c_int),
     "qtts_predictor_chain": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_acoustic_embed_sum": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_sample_token": ([c_void_p, c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64,
@@ -151,6 +154,7 @@ class Context:
             raise QttsError(rc, "qtts_ctx_create failed (no HIP device?)")
         self.h = h
         self._keep = []
+        self.dec_codebooks = 16
 
     def close(self):
         if self.h:
@@ -308,6 +312,31 @@ class Context:
                                                   ptr(t) if t.size else None, t.size, ptr(codes), codes.shape[1],
                                                   ptr(icl), ptr(rem) if rem_len else None, 0))
         return icl, rem
+
+    # ---- speech decoder -----------------------------------------------------
+    def upload_decoder(self, decoder):
+        """Upload a SpeechDecoderWeights-shaped decoder (synth.Decoder)."""
+        h, keep = decoder_host(decoder)
+        self._check(self.lib.qtts_decoder_upload(self.h, ctypes.byref(h)))
+        self.dec_codebooks = len(decoder.rest_codebooks) + 1
+
+    def decode_to_audio(self, codes, warmup=None):
+        """decode_to_audio (decoder.rs:395-574): codes [n_codebooks][T],
+        optional warmup codes [n_codebooks][Tv] prepended and trimmed."""
+        c = np.ascontiguousarray(codes, np.uint32).reshape(self.dec_codebooks, -1)
+        w = None if warmup is None else np.ascontiguousarray(warmup, np.uint32).reshape(self.dec_codebooks, -1)
+        nw = 0 if w is None else w.shape[1]
+        n = c_int64(0)
+        rc = self.lib.qtts_decode_to_audio(self.h, ptr(c), c.shape[1], ptr(w) if nw else None, nw, None, 0,
+                                           ctypes.byref(n), 0)
+        if rc == OK:
+            return np.empty(0, np.float32)
+        if rc != ERR_CAPACITY:
+            self._check(rc)
+        out = np.empty(n.value, np.float32)
+        self._check(self.lib.qtts_decode_to_audio(self.h, ptr(c), c.shape[1], ptr(w) if nw else None, nw, ptr(out),
+                                                  out.size, ctypes.byref(n), 0))
+        return out[:n.value]
 
     def generate_acoustic_codes(self, talker_hidden, semantic_embed):
         th = _f32(talker_hidden, self.hidden)

@@ -1,0 +1,128 @@
+"""The speech decoder on the device (decode_to_audio, decoder.rs:395-584)
+against the oracle's C restatement (oracle/qtts_decoder.c, itself pinned
+against a float64 model and the reference's warmup-trim answers).
+
+Bar: the waveform within 1e-3 of the oracle's peak amplitude (f32
+matrix-core sums in another order than the reference's loops; the clamp to
+[-1, 1] is the same).  Size-independent checks: warmup trimming equals
+decoding the concatenation and dropping `warmup_trim_len` samples (bit for
+bit, same kernels and sizes), and a decoder is causal, so a prefix of the
+frames decodes to a prefix of the samples.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import qtts
+from qtts import synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def close(got, ref, rel=TOL):
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), 1e-30)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    return err <= rel * scale, err / scale
+
+
+def small_decoder(seed=11):
+    return synth.make_decoder(seed=seed, latent=64, hidden=64, n_heads=4, head_dim=16, inter=128, n_tf_layers=2,
+                              codebook_size=64, codebook_dim=32, vq_dim=32, vocos=(48, 32, 24, 16, 8),
+                              rope_max_pos=512)
+
+
+def codes_for(d, T, seed):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.integers(0, d.codebook_size, (len(d.rest_codebooks) + 1, T)).astype(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def small():
+    return small_decoder()
+
+
+@pytest.fixture(scope="module")
+def ctx(ctx_factory, small):
+    c = ctx_factory(64)
+    c.upload_decoder(small)
+    return c
+
+
+@pytest.mark.parametrize("T", [1, 5, 80])
+def test_decode_small_vs_oracle(ctx, small, T):
+    codes = codes_for(small, T, 4000 + T)
+    ref = O.decode_to_audio(small, codes, threads=16)
+    got = ctx.decode_to_audio(codes)
+    assert got.shape == ref.shape == (T * small.upsample_factor,)
+    ok, e = close(got, ref)
+    assert ok, f"T={T}: rel err {e}"
+
+
+def test_decode_small_warmup_vs_oracle(ctx, small):
+    codes, warm = codes_for(small, 30, 4100), codes_for(small, 12, 4101)
+    ref = O.decode_to_audio(small, codes, warmup=warm, threads=16)
+    got = ctx.decode_to_audio(codes, warmup=warm)
+    total = 42 * small.upsample_factor
+    assert got.size == ref.size == total - O.warmup_trim_len(12, 42, total)
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+
+
+def test_warmup_is_trimmed_concatenation(ctx, small):
+    codes, warm = codes_for(small, 17, 4200), codes_for(small, 9, 4201)
+    full = ctx.decode_to_audio(np.concatenate([warm, codes], axis=1))
+    got = ctx.decode_to_audio(codes, warmup=warm)
+    cut = O.warmup_trim_len(9, 26, full.size)
+    assert np.array_equal(got.view(np.uint32), full[cut:].view(np.uint32))
+
+
+def test_decode_is_causal(ctx, small):
+    """Every stage is causal (causal convs, left-looking attention window,
+    right-cropped transposed convs), so frames past t leave samples up to t
+    unchanged -- bit for bit, since no kernel's per-sample arithmetic
+    depends on the number of frames."""
+    codes = codes_for(small, 64, 4300)
+    full = ctx.decode_to_audio(codes)
+    head = ctx.decode_to_audio(codes[:, :40])
+    assert np.array_equal(head.view(np.uint32), full[:head.size].view(np.uint32))
+
+
+def test_decode_edges(ctx, small):
+    ncb = len(small.rest_codebooks) + 1
+    assert ctx.decode_to_audio(np.zeros((ncb, 0), np.uint32)).size == 0
+    bad = codes_for(small, 4, 4400)
+    bad[3, 2] = small.codebook_size
+    with pytest.raises(qtts.QttsError) as e:
+        ctx.decode_to_audio(bad)
+    assert e.value.code == qtts.ERR_INVALID
+    # sizes past the first workspace reuse / regrow it
+    for T in (3, 120, 7):
+        codes = codes_for(small, T, 4500 + T)
+        ok, e = close(ctx.decode_to_audio(codes), O.decode_to_audio(small, codes, threads=16))
+        assert ok, f"T={T}: rel err {e}"
+
+
+def test_decode_without_decoder(ctx_factory):
+    c = ctx_factory(64)
+    with pytest.raises(qtts.QttsError) as e:
+        c.decode_to_audio(np.zeros((16, 2), np.uint32))
+    assert e.value.code == qtts.ERR_STATE
+
+
+def test_decode_full_dims_vs_oracle(ctx_factory):
+    """The 12 Hz tokenizer's decoder shapes (16 codebooks of 2048 x 256, an
+    8-layer 512-wide transformer, 1024-channel upsamplers, Vocos 1536 -> 96,
+    1920 samples per frame) on 6 frames after 3 warmup frames."""
+    d = synth.make_decoder(seed=7)
+    c = ctx_factory(64)
+    c.upload_decoder(d)
+    codes, warm = codes_for(d, 6, 4600), codes_for(d, 3, 4601)
+    ref = O.decode_to_audio(d, codes, warmup=warm, threads=16)
+    got = c.decode_to_audio(codes, warmup=warm)
+    assert got.size == ref.size == 6 * 1920
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+    assert np.abs(ref).max() > 0.05            # a live signal, not a clamp or zeros
