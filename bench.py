@@ -170,6 +170,43 @@ def time_prefill(ctx, layers):
             "peak_tflops": F32_MFMA_PEAK_TFLOPS, "dtype": "f32 (v_mfma_f32_16x16x4_f32)"}
 
 
+DEC_FRAMES = 160               # speech-decoder workload: 160 codec frames = 12.8 s of 24 kHz audio
+DEC_RATE = 24000
+
+
+def time_decoder(synth, qtts, cpu_frames=0):
+    """decode_to_audio on the device (the 12 Hz tokenizer's decoder shapes,
+    random f32 weights) over DEC_FRAMES synthetic frames: audio seconds per
+    second and achieved TFLOP/s against the f32 MFMA peak; with cpu_frames,
+    the oracle's C decoder on that many frames (all host threads) beside it."""
+    d = synth.make_decoder(seed=7)
+    ctx = qtts.Context(0, kv_capacity=64)
+    ctx.upload_decoder(d)
+    us, fl = ctx.time_decode(DEC_FRAMES, 5)
+    ctx.close()
+    audio_s = DEC_FRAMES * d.upsample_factor / DEC_RATE
+    tf = fl / us / 1e6
+    log(f"speech decoder {DEC_FRAMES} frames: {us / 1e3:.2f} ms, {audio_s / (us * 1e-6):.0f} audio s/s, "
+        f"{tf:.1f} TFLOP/s ({tf / F32_MFMA_PEAK_TFLOPS:.1%} of f32 MFMA peak)")
+    out = {"frames": DEC_FRAMES, "samples": DEC_FRAMES * d.upsample_factor, "ms": round(us / 1e3, 3),
+           "audio_seconds_per_second": round(audio_s / (us * 1e-6), 1), "frames_per_second": round(DEC_FRAMES / (us * 1e-6), 1),
+           "tflops": round(tf, 2), "frac_f32_mfma": round(tf / F32_MFMA_PEAK_TFLOPS, 4), "flops": fl,
+           "peak_tflops": F32_MFMA_PEAK_TFLOPS, "dtype": "f32 (v_mfma_f32_16x16x4_f32)"}
+    if cpu_frames:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        threads = min(os.cpu_count() or 1, 16)
+        codes = np.random.Generator(np.random.PCG64(5)).integers(0, 2048, (16, cpu_frames)).astype(np.uint32)
+        t0 = time.perf_counter()
+        O.decode_to_audio(d, codes, threads=threads)
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(cpu_frames * d.upsample_factor / DEC_RATE / el, 3),
+                               "unit": "audio s/s", "cores": threads, "kind": "port",
+                               "sample": f"oracle decode of {cpu_frames} frames, {el:.1f} s"}
+        log(f"cpu speech decoder: {out['cpu_baseline']['value']} audio s/s on {threads} threads")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +219,8 @@ def main():
     ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
     ap.add_argument("--prefill-only", action="store_true", help="time only the matrix-core prefill")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape GEMV sweep")
+    ap.add_argument("--decoder-only", action="store_true", help="time only the speech decoder")
+    ap.add_argument("--no-decoder", action="store_true", help="skip the speech decoder")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -190,6 +229,10 @@ def main():
 
     import qtts
     from qtts import synth
+
+    if args.decoder_only:
+        print(json.dumps({"speech_decoder": time_decoder(synth, qtts)}), flush=True)
+        return
 
     t_gen = time.time()
     talker = synth.make_talker(seed=1, n_layers=args.layers)
@@ -281,6 +324,9 @@ def main():
     if not args.no_sweep:
         kernels["q4_gemv_shapes"] = gemv_sweep(ctx, synth)
         log("GEMV sweep: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in kernels["q4_gemv_shapes"].items()))
+
+    if not args.no_decoder:
+        kernels["speech_decoder"] = time_decoder(synth, qtts, 0 if args.no_cpu else 8)
 
     cpu = None
     if not args.no_cpu:

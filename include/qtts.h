@@ -466,6 +466,16 @@ int qtts_time_gemv(qtts_ctx *ctx, const qtts_w *const *ws, int32_t n_w,
 int qtts_time_prefill(qtts_ctx *ctx, int64_t rows, int32_t what, int32_t iters,
                       double *avg_us, double *flops);
 
+/* Average device time (us) of one whole decode_to_audio on the device over
+ * `n_frames` synthetic frames (codes from a fixed generator, already
+ * resident; no warmup trim), same event scheme; *flops gets the
+ * algorithmic floating-point operations of one decode (every projection
+ * and convolution at its true kernel size, attention q.k and p.v).  No
+ * reference counterpart (the reference prints phase times,
+ * decoder.rs:572-574). */
+int qtts_time_decode(qtts_ctx *ctx, int64_t n_frames, int32_t iters,
+                     double *avg_us, double *flops);
+
 #ifdef __cplusplus
 }
 #endif

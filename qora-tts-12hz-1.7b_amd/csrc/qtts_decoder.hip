@@ -30,6 +30,11 @@ namespace qtts {
 
 constexpr int CGN = 128, CGK = 32, CLD = CGK + 4;
 
+// Read (never written) in place of out-of-range taps; a plain global
+// (not const) so that selecting between it and an activation pointer
+// stays in the global address space.
+__device__ float k_zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+
 enum ConvEpi : int {
     CE_STORE = 0,        // y = acc + bias
     CE_SNAKE = 1,        // y = snake(acc + bias)
@@ -55,17 +60,83 @@ struct ConvOut {
     const float *scale;  // CE_SCALE_RES: [M]
 };
 
-template <int MB, int EPI>
+// Per-row constants of an epilogue and the element operation, shared by the
+// GEMM's own epilogue and the split-K reduction.
+struct RowPar {
+    float bias, a, ib, scale;
+};
+
+template <int EPI>
+__device__ __forceinline__ RowPar row_par(const ConvOut &o, int m)
+{
+    RowPar r;
+    r.bias = o.bias ? o.bias[m] : 0.0f;
+    r.a = (EPI == CE_SNAKE || EPI == CE_STORE_SNAKE) ? expf(o.alpha[m]) : 0.0f;
+    r.ib = (EPI == CE_SNAKE || EPI == CE_STORE_SNAKE) ? expf(-o.beta[m]) : 0.0f;
+    r.scale = EPI == CE_SCALE_RES ? o.scale[m] : 0.0f;
+    return r;
+}
+
+template <int EPI>
+__device__ __forceinline__ void epi_store(const ConvOut &o, const RowPar &r, size_t idx, float acc)
+{
+    const float v = acc + r.bias;
+    if (EPI == CE_STORE) {
+        o.y[idx] = v;
+    } else if (EPI == CE_GELU) {
+        o.y[idx] = v * 0.5f * (1.0f + tanhf(v * 0.7071067811865476f));
+    } else if (EPI == CE_SCALE_RES) {
+        o.y[idx] = o.y[idx] + r.scale * v;
+    } else {
+        const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + o.res[idx] : v;
+        const float s = sinf(r.a * xv);
+        if (EPI == CE_STORE_SNAKE) o.x[idx] = xv;
+        o.y[idx] = xv + r.ib * s * s;
+    }
+}
+
+// SwiGLU rows (2j, 2j + 1) = (gate, up) -> y[j]
+__device__ __forceinline__ void epi_swiglu(const ConvOut &o, int m, size_t col, float g, float u)
+{
+    g += o.bias ? o.bias[m] : 0.0f;
+    u += o.bias ? o.bias[m + 1] : 0.0f;
+    o.y[(size_t)(m >> 1) * o.ldy + col] = silu_f(g) * u;
+}
+
+// Contraction order: general, k = ic * K + tap (the [out][in][kernel]
+// weight rows as they are); tap-major (TM), k = tap * IC + ic, for K = 1
+// or IC a multiple of the 32-wide chunk, so that a chunk has one tap and
+// the im2col gather needs no division per element (weights repacked to
+// [out][kernel][in] at upload, conv_tap_major()).
+//
+// Launch geometry (GemmGeo): tm x tn output tiles, times nph stride phases
+// of a transposed conv (phase ph uses A + ph * M * Kd and writes columns
+// n * os + ph), times ks contraction slices.  With ks > 1 each slice writes
+// its raw sums to part[slice][ph][M][N] and k_conv_reduce adds the slices
+// in order and applies the epilogue.
+struct GemmGeo {
+    int tm, tn, nph, ks, cps;   // cps: 32-wide chunks per slice
+    float *part;
+};
+
+template <int MB, int EPI, bool TM>
 __global__ void __launch_bounds__(256, 2)
-k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, int tm)
+k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo g)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * CGK / 4 + 255) / 256;
     __shared__ __attribute__((aligned(16))) float As[2][BM * CLD];
     __shared__ __attribute__((aligned(16))) float Bs[2][CGN * CLD];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int mt = blockIdx.x % tm, nt = blockIdx.x / tm;
+    const int tiles = g.tm * g.tn, tile = blockIdx.x % tiles, rest = blockIdx.x / tiles;
+    const int ph = rest % g.nph, slice = rest / g.nph;
+    const int mt = tile % g.tm, nt = tile / g.tm;
     const int m0 = mt * BM, n0 = nt * CGN;
+    A += (size_t)ph * M * Kd;
+    if (g.nph > 1) o.oo = ph;
+    const int c0 = slice * g.cps;
+    const int nch = min(g.cps, (Kd + CGK - 1) / CGK - c0);
+    const int kb = c0 * CGK;
 
     // A slots: row slot/8, k 4*(slot%8)
     const float *arow[NA];
@@ -110,20 +181,42 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, int tm)
             }
             f.a[j] = aok[j] ? f.a[j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        // Out-of-range taps read k_zero: selecting the address rather than
+        // the value keeps every load unconditional (a select on the value
+        // lets the compiler sink each load into a branch of its own and
+        // wait on it there).
+        if (TM) {
+            const int tap = k0 / in.IC, icb = k0 - tap * in.IC;
+            const int p = pos0 + tap * in.dil - in.pad;
+            const bool pok = bcok && p >= 0 && p < in.L_in;
+            const float *xp = xb + min(max(p, 0), in.L_in - 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int kq = bq + 2 * i;
-            float v[4];
+            for (int i = 0; i < 4; i++) {
+                const int ic = icb + 4 * (bq + 2 * i);
+                const float *row = xp + (size_t)ic * in.ldx;
+                float v[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int kk = k0 + 4 * kq + e;
-                const int ic = kk / in.K, tap = kk - ic * in.K;
-                const int p = pos0 + tap * in.dil - in.pad;
-                const bool ok = bcok && kk < Kd && p >= 0 && p < in.L_in;
-                const float xv = xb[(size_t)min(ic, in.IC - 1) * in.ldx + min(max(p, 0), in.L_in - 1)];
-                v[e] = ok ? xv : 0.0f;
+                for (int e = 0; e < 4; e++) {
+                    const float *src = (pok && ic + e < in.IC) ? row + (size_t)e * in.ldx : k_zero;
+                    v[e] = *src;
+                }
+                f.b[i] = f32x4{v[0], v[1], v[2], v[3]};
             }
-            f.b[i] = f32x4{v[0], v[1], v[2], v[3]};
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int kq = bq + 2 * i;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int kk = k0 + 4 * kq + e;
+                    const int ic = kk / in.K, tap = kk - ic * in.K;
+                    const int p = pos0 + tap * in.dil - in.pad;
+                    const bool ok = bcok && kk < Kd && p >= 0 && p < in.L_in;
+                    v[e] = *(ok ? xb + (size_t)ic * in.ldx + p : k_zero);
+                }
+                f.b[i] = f32x4{v[0], v[1], v[2], v[3]};
+            }
         }
     };
     auto stage = [&](const Fetch &f, int buf) {
@@ -158,25 +251,24 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, int tm)
         }
     };
 
-    const int nch = (Kd + CGK - 1) / CGK;
     Fetch fa, fb;
-    fetch(fa, 0);
-    if (nch > 1) fetch(fb, CGK);
+    fetch(fa, kb);
+    if (nch > 1) fetch(fb, kb + CGK);
     stage(fa, 0);
     __syncthreads();
     int c = 0;
     for (; c + 3 < nch; c += 2) {
-        fetch(fa, (c + 2) * CGK);
+        fetch(fa, kb + (c + 2) * CGK);
         mfma(0);
         stage(fb, 1);
         __syncthreads();
-        fetch(fb, (c + 3) * CGK);
+        fetch(fb, kb + (c + 3) * CGK);
         mfma(1);
         stage(fa, 0);
         __syncthreads();
     }
     if (c + 2 < nch) {
-        fetch(fa, (c + 2) * CGK);
+        fetch(fa, kb + (c + 2) * CGK);
         mfma(0);
         stage(fb, 1);
         __syncthreads();
@@ -194,46 +286,79 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, int tm)
     }
 
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
+    if (g.ks > 1) {
+        float *pp = g.part + ((size_t)slice * g.nph + ph) * M * N;
 #pragma unroll
-    for (int i = 0; i < MB; i++) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + 16 * (2 * wv + j) + r16;
-            if (n >= N) continue;
-            const int col = n * o.os + o.oo;
-            if (EPI == CE_SWIGLU) {
-#pragma unroll
-                for (int e = 0; e < 4; e += 2) {
-                    const int m = m0 + 16 * i + 4 * q + e;   // even: gate row, m + 1: up row
-                    if (m + 1 >= M) continue;
-                    const float g = acc[i][j][e] + (o.bias ? o.bias[m] : 0.0f);
-                    const float u = acc[i][j][e + 1] + (o.bias ? o.bias[m + 1] : 0.0f);
-                    o.y[(size_t)(m >> 1) * o.ldy + col] = silu_f(g) * u;
-                }
-                continue;
-            }
+        for (int i = 0; i < MB; i++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = m0 + 16 * i + 4 * q + e;
                 if (m >= M) continue;
-                const size_t idx = (size_t)m * o.ldy + col;
-                const float v = acc[i][j][e] + (o.bias ? o.bias[m] : 0.0f);
-                if (EPI == CE_STORE) {
-                    o.y[idx] = v;
-                } else if (EPI == CE_GELU) {
-                    o.y[idx] = v * 0.5f * (1.0f + tanhf(v * 0.7071067811865476f));
-                } else if (EPI == CE_SCALE_RES) {
-                    o.y[idx] = o.y[idx] + o.scale[m] * v;
-                } else {
-                    const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + o.res[idx] : v;
-                    const float a = expf(o.alpha[m]), ib = expf(-o.beta[m]);
-                    const float s = sinf(a * xv);
-                    if (EPI == CE_STORE_SNAKE) o.x[idx] = xv;
-                    o.y[idx] = xv + ib * s * s;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = n0 + 16 * (2 * wv + j) + r16;
+                    if (n < N) pp[(size_t)m * N + n] = acc[i][j][e];
                 }
+            }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        if (EPI == CE_SWIGLU) {
+#pragma unroll
+            for (int e = 0; e < 4; e += 2) {
+                const int m = m0 + 16 * i + 4 * q + e;   // even: gate row, m + 1: up row
+                if (m + 1 >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = n0 + 16 * (2 * wv + j) + r16;
+                    if (n < N) epi_swiglu(o, m, (size_t)n * o.os + o.oo, acc[i][j][e], acc[i][j][e + 1]);
+                }
+            }
+            continue;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + 16 * i + 4 * q + e;
+            if (m >= M) continue;
+            const RowPar r = row_par<EPI>(o, m);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int n = n0 + 16 * (2 * wv + j) + r16;
+                if (n < N) epi_store<EPI>(o, r, (size_t)m * o.ldy + (size_t)n * o.os + o.oo, acc[i][j][e]);
             }
         }
     }
+}
+
+// Split-K reduction: thread per (phase, row, column) (row pairs for
+// SwiGLU); slices added in slice order, then the epilogue.
+template <int EPI>
+__global__ void __launch_bounds__(256)
+k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
+{
+    const int rows = EPI == CE_SWIGLU ? M / 2 : M;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (int64_t)nph * rows * N) return;
+    const int n = (int)(id % N);
+    const int64_t r2 = id / N;
+    const int mr = (int)(r2 % rows), ph = (int)(r2 / rows);
+    const size_t plane = (size_t)M * N;
+    const size_t col = (size_t)n * o.os + (nph > 1 ? ph : o.oo);
+    if (EPI == CE_SWIGLU) {
+        const int m = 2 * mr;
+        float gs = 0.0f, us = 0.0f;
+        for (int sl = 0; sl < ks; sl++) {
+            const float *pp = part + ((size_t)sl * nph + ph) * plane;
+            gs += pp[(size_t)m * N + n];
+            us += pp[(size_t)(m + 1) * N + n];
+        }
+        epi_swiglu(o, m, col, gs, us);
+        return;
+    }
+    float sum = 0.0f;
+    for (int sl = 0; sl < ks; sl++) sum += part[((size_t)sl * nph + ph) * plane + (size_t)mr * N + n];
+    epi_store<EPI>(o, row_par<EPI>(o, mr), (size_t)mr * o.ldy + col, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -259,19 +384,30 @@ __global__ void k_vq_gather(const float *first, const float *const *rest, int n_
     out[(size_t)(D + d) * T + t] = s;
 }
 
-// Column RMSNorm (rms_norm_f32, decoder.rs:589-598) of x [H][T]: one thread
-// per position, the channel sum in channel order.
-__global__ void k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *out)
+// Column RMSNorm (rms_norm_f32, decoder.rs:589-598) of x [H][T]:
+// workgroup of 16 positions x 16 channel groups; the sum of squares is
+// the 16 group partials added in group order.
+__global__ void __launch_bounds__(256)
+k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *out)
 {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
+    __shared__ float red[16][17];
+    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
+    const int t = blockIdx.x * 16 + tl;
+    const bool ok = t < T;
+    const float *xc = x + min(t, T - 1);
     float ss = 0.0f;
-    for (int h = 0; h < H; h++) {
-        const float v = x[(size_t)h * T + t];
-        ss += v * v;
+    for (int h = cg; h < H; h += 16) {
+        const float v = xc[(size_t)h * T];
+        ss = fmaf(v, v, ss);
     }
-    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-    for (int h = 0; h < H; h++) out[(size_t)h * T + t] = x[(size_t)h * T + t] * inv * gamma[h];
+    red[cg][tl] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 16; g++) tot += red[g][tl];
+    const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+    if (!ok) return;
+    for (int h = cg; h < H; h += 16) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
 }
 
 // Rotate-half RoPE (apply_rope_split_half, decoder.rs:631-655) of the q and
@@ -326,42 +462,137 @@ k_dec_attn(const float *qkv, int heads, int T, int W, float *out)
     for (int d = 0; d < HD; d++) out[((size_t)h * HD + d) * T + t] = acc[d] * il;
 }
 
+// Sliding-window attention, workgroup per (head, 16 queries): the key and
+// value columns those queries see (positions t0-W+1 .. t0+15, zero before
+// position 0) and the 16 query columns staged in LDS.  Scores: lane (query
+// qi, key slot kl) holds keys kl + 16i; softmax max and sum over the 16
+// lanes of the query's row (DPP); then lane (qi, dim group dg) sums
+// p.v over the query's W keys in position order (keys before position 0
+// have p = 0 and v = 0).  Needs W + 15 <= 16 * ATT_SLOTS.
+constexpr int ATT_QB = 16, ATT_SLOTS = 7;
+
+static inline size_t attn_tile_lds(int hd, int W)
+{
+    const int nkp = ATT_QB + W;   // NK + 1
+    return (size_t)(2 * hd * nkp + hd * ATT_QB + ATT_QB * nkp) * sizeof(float);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(256)
+k_dec_attn_tile(const float *qkv, int heads, int T, int W, float *out)
+{
+    extern __shared__ float sm[];
+    const int NK = ATT_QB + W - 1, NKP = NK + 1;
+    const int h = blockIdx.y, t0 = blockIdx.x * ATT_QB, kb = t0 - (W - 1);
+    const int tid = threadIdx.x;
+    const size_t A = (size_t)heads * HD;
+    const float *q = qkv + (size_t)h * HD * T, *k = qkv + (A + (size_t)h * HD) * T,
+                *v = qkv + (2 * A + (size_t)h * HD) * T;
+    float *Ks = sm, *Vs = Ks + HD * NKP, *Qs = Vs + HD * NKP, *Ps = Qs + HD * ATT_QB;
+    for (int i = tid; i < HD * NK; i += 256) {
+        const int d = i / NK, j = i - d * NK, p = kb + j;
+        const bool ok = p >= 0 && p < T;
+        const size_t src = (size_t)d * T + min(max(p, 0), T - 1);
+        Ks[d * NKP + j] = ok ? k[src] : 0.0f;
+        Vs[d * NKP + j] = ok ? v[src] : 0.0f;
+    }
+    for (int i = tid; i < HD * ATT_QB; i += 256) {
+        const int d = i / ATT_QB, j = i - d * ATT_QB, p = t0 + j;
+        Qs[i] = p < T ? q[(size_t)d * T + p] : 0.0f;
+    }
+    __syncthreads();
+    const int qi = tid >> 4, kl = tid & 15;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float sc[ATT_SLOTS];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < ATT_SLOTS; i++) {
+        const int j = kl + 16 * i;
+        const bool ok = j < NK && j >= qi && j <= qi + W - 1 && kb + j >= 0;
+        float dot = 0.0f;
+        if (ok) {
+#pragma unroll 16
+            for (int d = 0; d < HD; d++) dot = fmaf(Qs[d * ATT_QB + qi], Ks[d * NKP + j], dot);
+        }
+        sc[i] = ok ? dot * scale : -INFINITY;
+        m = fmaxf(m, sc[i]);
+    }
+    m = row_max16(m);
+    float l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ATT_SLOTS; i++) {
+        sc[i] = expf(sc[i] - m);
+        l += sc[i];
+    }
+    l = row_sum16(l);
+    const float il = 1.0f / l;
+#pragma unroll
+    for (int i = 0; i < ATT_SLOTS; i++) {
+        const int j = kl + 16 * i;
+        if (j < NK) Ps[qi * NKP + j] = sc[i] * il;
+    }
+    __syncthreads();
+    constexpr int DE = HD / 16;
+    float o[DE];
+#pragma unroll
+    for (int e = 0; e < DE; e++) o[e] = 0.0f;
+    const float *pr = Ps + qi * NKP + qi;
+    for (int r = 0; r < W; r++) {
+        const float pv = pr[r];
+#pragma unroll
+        for (int e = 0; e < DE; e++) o[e] = fmaf(pv, Vs[(kl + 16 * e) * NKP + qi + r], o[e]);
+    }
+    const int t = t0 + qi;
+    if (t >= T) return;
+#pragma unroll
+    for (int e = 0; e < DE; e++) out[((size_t)h * HD + kl + 16 * e) * T + t] = o[e];
+}
+
 // ConvNeXt front (decoder.rs:346-352): causal depthwise conv then LayerNorm
 // over channels per position (layer_norm_channel_first, decoder.rs:668-690).
-// One workgroup per 64 positions: thread (c-lane, t): dw values go to the
-// output buffer, then the column statistics.
+// Workgroup of 16 positions x 16 channel groups: the conv values go to the
+// output buffer, then the column statistics (group partials in group order).
 __global__ void __launch_bounds__(256)
 k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int K, const float *g, const float *b,
         float eps, float *out)
 {
-    __shared__ float red[4][64][2];
-    const int tl = threadIdx.x & 63, cg = threadIdx.x >> 6;
-    const int t = blockIdx.x * 64 + tl;
+    __shared__ float red[2][16][17];
+    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
+    const int t = blockIdx.x * 16 + tl;
     const bool ok = t < L;
+    const int tc = min(t, L - 1);
     float s1 = 0.0f;
-    for (int c = cg; c < C; c += 4) {
+    for (int c = cg; c < C; c += 16) {
+        const float *xr = x + (size_t)c * L;
+        const float *wr = dw_w + (size_t)c * K;
         float v = dw_b[c];
         for (int k = 0; k < K; k++) {
-            const int p = t + k - (K - 1);
-            v += (ok && p >= 0) ? x[(size_t)c * L + p] * dw_w[c * K + k] : 0.0f;
+            const int p = tc + k - (K - 1);
+            v += p >= 0 ? xr[max(p, 0)] * wr[k] : 0.0f;
         }
         if (ok) out[(size_t)c * L + t] = v;
         s1 += v;
     }
-    red[cg][tl][0] = s1;
+    red[0][cg][tl] = s1;
     __syncthreads();
-    const float mean = ((red[0][tl][0] + red[1][tl][0]) + (red[2][tl][0] + red[3][tl][0])) / (float)C;
+    float mean = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) mean += red[0][q][tl];
+    mean /= (float)C;
     float s2 = 0.0f;
-    for (int c = cg; c < C; c += 4) {
+    for (int c = cg; c < C; c += 16) {
         const float d = ok ? out[(size_t)c * L + t] - mean : 0.0f;
         s2 += d * d;
     }
-    red[cg][tl][1] = s2;
+    red[1][cg][tl] = s2;
     __syncthreads();
-    const float var = ((red[0][tl][1] + red[1][tl][1]) + (red[2][tl][1] + red[3][tl][1])) / (float)C;
+    float var = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) var += red[1][q][tl];
+    var /= (float)C;
     const float inv = 1.0f / sqrtf(var + eps);
     if (!ok) return;
-    for (int c = cg; c < C; c += 4) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
+    for (int c = cg; c < C; c += 16) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
 }
 
 // Output conv (one channel, causal, conv.rs:191-228) on the snake input,
@@ -403,19 +634,59 @@ static int conv_mb(int M)
     return M >= 64 ? 4 : (M >= 32 ? 2 : 1);
 }
 
+template <int EPI, bool TM>
+static void conv_launch(int mb, dim3 grid, const float *A, int M, int Kd, const ConvIn &in, const ConvOut &o, int N,
+                        const GemmGeo &g, hipStream_t s)
+{
+    switch (mb) {
+    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    }
+}
+
+// Contraction slices: split K while the launch has fewer than 2 workgroups
+// per CU and each slice keeps at least 4 chunks, within the partial buffer.
+static int pick_ks(int blocks, int nch, size_t plane_floats, const DecoderWs &ws)
+{
+    int ks = 1;
+    while (blocks * ks < 512 && nch / (2 * ks) >= 4 && (size_t)(2 * ks) * plane_floats <= ws.part_cap) ks *= 2;
+    return ks;
+}
+
+// One implicit-GEMM convolution (nph > 1: the stride phases of a
+// transposed conv, A holding nph consecutive [M][Kd] matrices).  A's rows
+// are tap-major exactly when conv_tap_major(IC, K) (upload repacks by the
+// same predicate).
 template <int EPI>
-static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvOut &o, int N, hipStream_t s)
+static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvOut &o, int N, const DecoderWs &ws,
+                            hipStream_t s, int nph = 1)
 {
     const int Kd = in.IC * in.K;
-    if (M < 1 || N < 1 || Kd < 1) return hipErrorInvalidValue;
-    const int mb = conv_mb(M), tm = (M + 16 * mb - 1) / (16 * mb), tn = (N + CGN - 1) / CGN;
-    const dim3 grid(tm * tn);
-    switch (mb) {
-    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
-    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
-    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, tm); break;
+    if (M < 1 || N < 1 || Kd < 1 || nph < 1 || (EPI == CE_SWIGLU && (M & 1))) return hipErrorInvalidValue;
+    const int mb = conv_mb(M);
+    GemmGeo g{};
+    g.tm = (M + 16 * mb - 1) / (16 * mb);
+    g.tn = (N + CGN - 1) / CGN;
+    g.nph = nph;
+    const int nch = (Kd + CGK - 1) / CGK;
+    g.ks = pick_ks(g.tm * g.tn * nph, nch, (size_t)nph * M * N, ws);
+    g.cps = (nch + g.ks - 1) / g.ks;
+    g.ks = (nch + g.cps - 1) / g.cps;   // no empty slice
+    g.part = ws.part;
+    const dim3 grid(g.tm * g.tn * nph * g.ks);
+    if (conv_tap_major(in.IC, in.K))
+        conv_launch<EPI, true>(mb, grid, A, M, Kd, in, o, N, g, s);
+    else
+        conv_launch<EPI, false>(mb, grid, A, M, Kd, in, o, N, g, s);
+    DCHK(hipGetLastError());
+    if (g.ks > 1) {
+        const int64_t n = (int64_t)nph * (EPI == CE_SWIGLU ? M / 2 : M) * N;
+        hipLaunchKernelGGL(k_conv_reduce<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws.part, g.ks, nph,
+                           M, N, o);
+        DCHK(hipGetLastError());
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 static ConvIn causal_in(const float *x, int IC, int L, int K, int dil)
@@ -439,17 +710,14 @@ static ConvOut plain_out(float *y, int ld, const float *bias)
 // 2 reads x[i-1] (kernel tap r + stride) then x[i] (tap r); taps = 1 reads
 // x[i] (tap r).
 template <int EPI>
-static hipError_t conv_t_phases(const DecConvT &w, const float *x, int L_in, ConvOut o, hipStream_t s)
+static hipError_t conv_t_phases(const DecConvT &w, const float *x, int L_in, ConvOut o, const DecoderWs &ws,
+                                hipStream_t s)
 {
     const int taps = w.taps;
-    for (int r = 0; r < w.stride; r++) {
-        ConvIn in{x, L_in, L_in, w.ic, taps, 1, taps - 1};
-        ConvOut op = o;
-        op.os = w.stride;
-        op.oo = r;
-        DCHK(conv_gemm<EPI>(w.phases + (size_t)r * w.oc * w.ic * taps, w.oc, in, op, L_in, s));
-    }
-    return hipSuccess;
+    ConvIn in{x, L_in, L_in, w.ic, taps, 1, taps - 1};
+    o.os = w.stride;
+    o.oo = 0;
+    return conv_gemm<EPI>(w.phases, w.oc, in, o, L_in, ws, s, w.stride);
 }
 
 hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
@@ -462,22 +730,29 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
     hipLaunchKernelGGL(k_vq_gather, dim3((T + 63) / 64, D), dim3(64), 0, s, d.first_codebook, d.rest_codebooks,
                        d.n_rest, D, codes, T, d.codebook_size, ws.a);
     DCHK(hipGetLastError());
-    DCHK(conv_gemm<CE_STORE>(d.vq_proj, V, causal_in(ws.a, 2 * D, T, 1, 1), plain_out(ws.b, T, nullptr), T, s));
+    DCHK(conv_gemm<CE_STORE>(d.vq_proj, V, causal_in(ws.a, 2 * D, T, 1, 1), plain_out(ws.b, T, nullptr), T, ws, s));
     // 2. pre-conv -> [LAT][T]
     DCHK(conv_gemm<CE_STORE>(d.pre_conv.w, d.pre_conv.oc, causal_in(ws.b, V, T, d.pre_conv.k, d.pre_conv.dil),
-                             plain_out(ws.a, T, d.pre_conv.b), T, s));
+                             plain_out(ws.a, T, d.pre_conv.b), T, ws, s));
     // 3. transformer on [H][T]: x in ws.b, normed in ws.c, q|k|v in ws.d, attention in ws.e
-    DCHK(conv_gemm<CE_STORE>(d.tf_in_w, H, causal_in(ws.a, LAT, T, 1, 1), plain_out(ws.b, T, d.tf_in_b), T, s));
-    const dim3 cols((T + 255) / 256);
+    DCHK(conv_gemm<CE_STORE>(d.tf_in_w, H, causal_in(ws.a, LAT, T, 1, 1), plain_out(ws.b, T, d.tf_in_b), T, ws, s));
+    const dim3 cols((T + 15) / 16);
+    const size_t att_lds = attn_tile_lds(d.head_dim, d.window);
+    const bool att_tile = d.window + ATT_QB - 1 <= 16 * ATT_SLOTS && att_lds <= 65536;
     for (int l = 0; l < d.n_tf; l++) {
         const DecLayer &L = d.tf[l];
         hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
         DCHK(hipGetLastError());
-        DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, s));
+        DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         hipLaunchKernelGGL(k_rope_cf, dim3((T + 63) / 64, 2 * d.n_heads), dim3(64), 0, s, ws.d, d.n_heads,
                            d.head_dim, T, d.rope_cos, d.rope_sin, d.rope_rows);
         DCHK(hipGetLastError());
-        if (d.head_dim == 64)
+        const dim3 ag((T + ATT_QB - 1) / ATT_QB, d.n_heads);
+        if (att_tile && d.head_dim == 64)
+            hipLaunchKernelGGL(k_dec_attn_tile<64>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window, ws.e);
+        else if (att_tile)
+            hipLaunchKernelGGL(k_dec_attn_tile<16>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window, ws.e);
+        else if (d.head_dim == 64)
             hipLaunchKernelGGL(k_dec_attn<64>, dim3((T + 63) / 64, d.n_heads), dim3(64), 0, s, ws.d, d.n_heads, T,
                                d.window, ws.e);
         else
@@ -486,17 +761,17 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         DCHK(hipGetLastError());
         ConvOut ro = plain_out(ws.b, T, nullptr);
         ro.scale = L.attn_scale;
-        DCHK(conv_gemm<CE_SCALE_RES>(L.o, H, causal_in(ws.e, A, T, 1, 1), ro, T, s));
+        DCHK(conv_gemm<CE_SCALE_RES>(L.o, H, causal_in(ws.e, A, T, 1, 1), ro, T, ws, s));
         hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.post_norm, H, T, 1e-5f, ws.c);
         DCHK(hipGetLastError());
-        DCHK(conv_gemm<CE_SWIGLU>(L.gate_up, 2 * I, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, s));
+        DCHK(conv_gemm<CE_SWIGLU>(L.gate_up, 2 * I, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         ConvOut mo = plain_out(ws.b, T, nullptr);
         mo.scale = L.mlp_scale;
-        DCHK(conv_gemm<CE_SCALE_RES>(L.down, H, causal_in(ws.d, I, T, 1, 1), mo, T, s));
+        DCHK(conv_gemm<CE_SCALE_RES>(L.down, H, causal_in(ws.d, I, T, 1, 1), mo, T, ws, s));
     }
     hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, d.tf_norm, H, T, 1e-5f, ws.c);
     DCHK(hipGetLastError());
-    DCHK(conv_gemm<CE_STORE>(d.tf_out_w, LAT, causal_in(ws.c, H, T, 1, 1), plain_out(ws.a, T, d.tf_out_b), T, s));
+    DCHK(conv_gemm<CE_STORE>(d.tf_out_w, LAT, causal_in(ws.c, H, T, 1, 1), plain_out(ws.a, T, d.tf_out_b), T, ws, s));
     // 4. upsample stages: ConvT (phases) then ConvNeXt; the signal moves
     // between ws.a and ws.b
     int L = T;
@@ -504,15 +779,15 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
     for (int u = 0; u < d.n_up; u++) {
         const DecUpsample &U = d.up[u];
         const int Lo = L * U.conv_t.stride;
-        DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), s));
+        DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), ws, s));
         L = Lo;
-        hipLaunchKernelGGL(k_dw_ln, dim3((L + 63) / 64), dim3(256), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
+        hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(256), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
                            U.norm_w, U.norm_b, 1e-5f, ws.c);
         DCHK(hipGetLastError());
-        DCHK(conv_gemm<CE_GELU>(U.pw1, U.inner, causal_in(ws.c, U.ch, L, 1, 1), plain_out(ws.d, L, U.pw1_b), L, s));
+        DCHK(conv_gemm<CE_GELU>(U.pw1, U.inner, causal_in(ws.c, U.ch, L, 1, 1), plain_out(ws.d, L, U.pw1_b), L, ws, s));
         ConvOut po = plain_out(other, L, U.pw2_b);
         po.scale = U.gamma;
-        DCHK(conv_gemm<CE_SCALE_RES>(U.pw2, U.ch, causal_in(ws.d, U.inner, L, 1, 1), po, L, s));
+        DCHK(conv_gemm<CE_SCALE_RES>(U.pw2, U.ch, causal_in(ws.d, U.inner, L, 1, 1), po, L, ws, s));
         std::swap(sig, other);
     }
     // 5. Vocos: init conv with the first block's pre-snake (or the final
@@ -524,7 +799,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         so.alpha = na;
         so.beta = nb;
         DCHK(conv_gemm<CE_SNAKE>(d.voc_init.w, d.voc_init.oc,
-                                 causal_in(sig, d.voc_init.ic, L, d.voc_init.k, d.voc_init.dil), so, L, s));
+                                 causal_in(sig, d.voc_init.ic, L, d.voc_init.k, d.voc_init.dil), so, L, ws, s));
     }
     int ch = d.voc_init.oc;
     float *sn = ws.c, *x = sig, *t1 = other;   // snake(x) / x / scratch
@@ -539,7 +814,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         xo.y = t1;
         xo.alpha = has_res ? B.res[0].a1_alpha : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
         xo.beta = has_res ? B.res[0].a1_beta : (b + 1 < d.n_voc ? d.voc[b + 1].pre_beta : d.final_beta);
-        DCHK(conv_t_phases<CE_STORE_SNAKE>(B.up, sn, L, xo, s));
+        DCHK(conv_t_phases<CE_STORE_SNAKE>(B.up, sn, L, xo, ws, s));
         L = Lo;
         std::swap(sn, t1);   // sn = snake(x)
         for (int r = 0; r < B.n_res; r++) {
@@ -548,7 +823,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
             ConvOut c1 = plain_out(t1, L, R.c1.b);
             c1.alpha = R.a2_alpha;
             c1.beta = R.a2_beta;
-            DCHK(conv_gemm<CE_SNAKE>(R.c1.w, ch, causal_in(sn, ch, L, R.c1.k, R.c1.dil), c1, L, s));
+            DCHK(conv_gemm<CE_SNAKE>(R.c1.w, ch, causal_in(sn, ch, L, R.c1.k, R.c1.dil), c1, L, ws, s));
             // conv2 (k 1) + residual: x += conv2(t1); sn = next snake(x)
             const float *nal = r + 1 < B.n_res ? B.res[r + 1].a1_alpha
                                                : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
@@ -559,13 +834,47 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
             c2.res = x;
             c2.alpha = nal;
             c2.beta = nbe;
-            DCHK(conv_gemm<CE_STORE_SNAKE>(R.c2.w, ch, causal_in(t1, ch, L, R.c2.k, R.c2.dil), c2, L, s));
+            DCHK(conv_gemm<CE_STORE_SNAKE>(R.c2.w, ch, causal_in(t1, ch, L, R.c2.k, R.c2.dil), c2, L, ws, s));
         }
     }
     // 6. output conv on snake(x) + clamp, first `cut` samples dropped
     hipLaunchKernelGGL(k_out_conv, dim3((L + 255) / 256), dim3(256), 0, s, sn, ch, L, d.out_w, d.out_b, d.out_k,
                        d.out_dil, cut, audio);
     return hipGetLastError();
+}
+
+// Algorithmic floating-point operations of enqueue_decode over T frames:
+// 2 per multiply-add of every projection and convolution at its true
+// kernel size (transposed convs: 2 * ic * oc * kernel per input position),
+// plus q.k and p.v of the windowed attention.
+double decode_flops(const DecoderDev &d, int T)
+{
+    const double t = T;
+    const double D = d.codebook_dim, V = d.vq_dim, H = d.hidden, A = (double)d.n_heads * d.head_dim, I = d.inter;
+    const double LAT = d.latent;
+    double f = 2.0 * V * 2 * D * t + 2.0 * LAT * V * d.pre_conv.k * t + 2.0 * H * LAT * t + 2.0 * LAT * H * t;
+    double keys = 0.0;
+    for (int i = 0; i < T; i++) keys += std::min(i + 1, d.window);
+    f += d.n_tf * (2.0 * t * (3 * A * H + H * A + 2 * I * H + H * I) + 4.0 * A * keys);
+    double L = t;
+    for (int u = 0; u < d.n_up; u++) {
+        const DecUpsample &U = d.up[u];
+        f += 2.0 * U.ch * U.ch * U.conv_t.taps * U.conv_t.stride * L;
+        L *= U.conv_t.stride;
+        f += 2.0 * L * (2.0 * U.inner * U.ch + U.dw_k * U.ch);
+    }
+    f += 2.0 * d.voc_init.oc * d.voc_init.ic * d.voc_init.k * L;
+    for (int b = 0; b < d.n_voc; b++) {
+        const DecVocos &B = d.voc[b];
+        f += 2.0 * B.up.oc * B.up.ic * B.up.taps * B.up.stride * L;
+        L *= B.up.stride;
+        for (int r = 0; r < B.n_res; r++)
+            f += 2.0 * L * ((double)B.res[r].c1.oc * B.res[r].c1.ic * B.res[r].c1.k +
+                            (double)B.res[r].c2.oc * B.res[r].c2.ic * B.res[r].c2.k);
+    }
+    const int ch = d.n_voc ? d.voc[d.n_voc - 1].up.oc : d.voc_init.oc;
+    f += 2.0 * ch * d.out_k * L;
+    return f;
 }
 
 }  // namespace qtts

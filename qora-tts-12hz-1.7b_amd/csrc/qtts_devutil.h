@@ -42,6 +42,15 @@ __device__ __forceinline__ float row_sum16(float v)
     return v;
 }
 
+__device__ __forceinline__ float row_max16(float v)
+{
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v)
 {
     v = row_sum16(v);

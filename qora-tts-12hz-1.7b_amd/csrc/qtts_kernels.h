@@ -84,12 +84,17 @@ struct PrefillWs {
 
 // Speech decoder on the device (qtts_decoder.hip).  Matrices are stored as
 // the GEMM's A operand, [output channels][input channels x taps].
+// Decoder convolution weights are stored tap-major ([out][kernel][in])
+// when this holds (K = 1, or the input channels a multiple of the GEMM's
+// 32-wide contraction chunk), else as [out][in][kernel].
+inline bool conv_tap_major(int ic, int k) { return k == 1 || ic % 32 == 0; }
+
 struct DecConv {
-    const float *w, *b;      // w [oc][ic*k]
+    const float *w, *b;      // w [oc][k][ic] when conv_tap_major(ic, k), else [oc][ic][k]
     int ic, oc, k, dil;
 };
 struct DecConvT {            // kernel == stride (1 tap) or 2*stride (2 taps), padding 0
-    const float *phases, *b; // [stride][oc][ic*taps]; 2 taps: x[i-1] (kernel tap r+stride), x[i] (tap r)
+    const float *phases, *b; // [stride][oc] rows of ic x taps (tap-major as DecConv); 2 taps: x[i-1] (kernel tap r+stride), x[i] (tap r)
     int ic, oc, stride, taps;
 };
 struct DecLayer {
@@ -143,6 +148,8 @@ struct DecoderDev {
 };
 struct DecoderWs {
     float *a, *b, *c, *d, *e;             // each floats_per_frame * cap_frames
+    float *part;                          // split-K partial sums
+    size_t part_cap;                      // floats in part
     uint32_t *codes;                      // [n_rest + 1][cap_frames]
     int cap_frames;
 };
@@ -203,6 +210,7 @@ hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M
                                   float *hidden_out, hipStream_t s);
 hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
                           float *audio, hipStream_t s);
+double decode_flops(const DecoderDev &d, int T);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
                                hipStream_t s);

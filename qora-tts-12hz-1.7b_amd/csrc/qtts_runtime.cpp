@@ -1322,13 +1322,21 @@ static int upload_conv(qtts_ctx *c, const qtts_conv1d_host &h, DecConv *d)
     if (!h.weight || !h.bias || h.in_channels < 1 || h.out_channels < 1 || h.kernel_size < 1 || h.dilation < 1)
         return fail(c, QTTS_ERR_INVALID, "bad conv1d descriptor");
     if (h.stride != 1) return fail(c, QTTS_ERR_UNSUPPORTED, "strided conv1d not used by the decoder");
-    d->ic = h.in_channels;
-    d->oc = h.out_channels;
-    d->k = h.kernel_size;
+    const int IC = h.in_channels, OC = h.out_channels, K = h.kernel_size;
+    d->ic = IC;
+    d->oc = OC;
+    d->k = K;
     d->dil = h.dilation;
-    // [out][in][k] is already [oc][ic*k]
-    RCHK(upload_vec(c, c->dec_allocs, h.weight, (size_t)h.out_channels * h.in_channels * h.kernel_size, &d->w));
-    return upload_vec(c, c->dec_allocs, h.bias, (size_t)h.out_channels, &d->b);
+    if (K > 1 && conv_tap_major(IC, K)) {   // [out][in][k] -> [out][k][in]
+        std::vector<float> w((size_t)OC * IC * K);
+        for (int o = 0; o < OC; o++)
+            for (int i = 0; i < IC; i++)
+                for (int k = 0; k < K; k++) w[((size_t)o * K + k) * IC + i] = h.weight[((size_t)o * IC + i) * K + k];
+        RCHK(upload_vec(c, c->dec_allocs, w.data(), w.size(), &d->w));
+    } else {
+        RCHK(upload_vec(c, c->dec_allocs, h.weight, (size_t)OC * IC * K, &d->w));
+    }
+    return upload_vec(c, c->dec_allocs, h.bias, (size_t)OC, &d->b);
 }
 
 // Transposed conv [in][out][k] -> per stride phase r: [oc][ic*taps] with
@@ -1341,17 +1349,16 @@ static int upload_convt(qtts_ctx *c, const qtts_convt1d_host &h, DecConvT *d)
         return fail(c, QTTS_ERR_UNSUPPORTED, "conv_transpose1d needs kernel = stride or 2*stride, padding 0");
     const int IC = h.in_channels, OC = h.out_channels, K = h.kernel_size, S = h.stride;
     const int taps = K / S;
+    const bool tm = conv_tap_major(IC, taps);
     std::vector<float> p((size_t)S * OC * IC * taps);
     for (int r = 0; r < S; r++)
         for (int oc = 0; oc < OC; oc++)
             for (int ic = 0; ic < IC; ic++) {
-                float *dst = &p[(((size_t)r * OC + oc) * IC + ic) * taps];
                 const float *w = h.weight + ((size_t)ic * OC + oc) * K;
-                if (taps == 2) {
-                    dst[0] = w[r + S];
-                    dst[1] = w[r];
-                } else {
-                    dst[0] = w[r];
+                const size_t row = ((size_t)r * OC + oc) * IC * taps;
+                for (int j = 0; j < taps; j++) {
+                    const float v = (taps == 2 && j == 0) ? w[r + S] : w[r];
+                    p[row + (tm ? (size_t)j * IC + ic : (size_t)ic * taps + j)] = v;
                 }
             }
     d->ic = IC;
@@ -1531,6 +1538,11 @@ extern "C" int qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_host *d)
     return QTTS_OK;
 }
 
+// Split-K partial sums of the decoder's convolutions (64 MiB): enough to
+// split every stage of short utterances, where the launches are too small
+// to fill the GPU; long ones have columns enough and do not split.
+static constexpr size_t DEC_PART_FLOATS = (size_t)16 << 20;
+
 static int ensure_dec_ws(qtts_ctx *c, int frames)
 {
     if (frames <= c->dws.cap_frames) return QTTS_OK;
@@ -1538,8 +1550,9 @@ static int ensure_dec_ws(qtts_ctx *c, int frames)
     c->dws_mem = nullptr;
     c->dws = DecoderWs{};
     const size_t per = (size_t)c->dec_floats_per_frame * frames;
+    const size_t part = DEC_PART_FLOATS;
     void *m = nullptr;
-    HIPCHK(c, hipMalloc(&m, 5 * per * sizeof(float) + (size_t)16 * frames * sizeof(uint32_t)));
+    HIPCHK(c, hipMalloc(&m, (5 * per + part) * sizeof(float) + (size_t)16 * frames * sizeof(uint32_t)));
     c->dws_mem = m;
     float *f = (float *)m;
     c->dws.a = f;
@@ -1547,7 +1560,9 @@ static int ensure_dec_ws(qtts_ctx *c, int frames)
     c->dws.c = f + 2 * per;
     c->dws.d = f + 3 * per;
     c->dws.e = f + 4 * per;
-    c->dws.codes = (uint32_t *)(f + 5 * per);
+    c->dws.part = f + 5 * per;
+    c->dws.part_cap = part;
+    c->dws.codes = (uint32_t *)(f + 5 * per + part);
     c->dws.cap_frames = frames;
     return QTTS_OK;
 }
@@ -1976,6 +1991,33 @@ extern "C" int qtts_time_prefill(qtts_ctx *c, int64_t rows, int32_t what, int32_
     HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return rc;
+}
+
+extern "C" int qtts_time_decode(qtts_ctx *c, int64_t n_frames, int32_t iters, double *avg_us, double *flops)
+{
+    if (!c || iters < 1 || !avg_us || !flops || n_frames < 1) return QTTS_ERR_INVALID;
+    if (!c->has_decoder) return fail(c, QTTS_ERR_STATE, "no speech decoder uploaded");
+    if (n_frames > (1 << 16)) return fail(c, QTTS_ERR_CAPACITY, "too many frames");
+    hipSetDevice(c->device);
+    const DecoderDev &d = c->dec;
+    const int T = (int)n_frames, ncb = d.n_rest + 1;
+    RCHK(ensure_dec_ws(c, T));
+    // synthetic codes from a fixed LCG, uniform over the codebook
+    std::vector<uint32_t> codes((size_t)ncb * T);
+    uint64_t x = 0x9E3779B97F4A7C15ull;
+    for (auto &v : codes) {
+        x = x * 6364136223846793005ull + 1442695040888963407ull;
+        v = (uint32_t)((x >> 33) % (uint64_t)d.codebook_size);
+    }
+    HIPCHK(c, hipMemcpyAsync(c->dws.codes, codes.data(), codes.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                             c->stream));
+    int64_t factor = 1;
+    for (int u = 0; u < d.n_up; u++) factor *= d.up[u].conv_t.stride;
+    for (int b = 0; b < d.n_voc; b++) factor *= d.voc[b].up.stride;
+    RCHK(ensure_io(c, (int64_t)T * factor));
+    *flops = decode_flops(d, T);
+    return time_launches(c, iters, [&](int) { return enqueue_decode(d, c->dws, c->dws.codes, T, 0, c->d_io, c->stream); },
+                         avg_us);
 }
 
 extern "C" int qtts_time_gemv(qtts_ctx *c, const qtts_w *const *ws, int32_t n_w, int32_t iters, double *avg_us,

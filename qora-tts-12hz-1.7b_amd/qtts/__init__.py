@@ -89,6 +89,7 @@ SIGNATURES = {
     "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_gemv": ([c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_prefill": ([c_void_p, c_int64, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
+    "qtts_time_decode": ([c_void_p, c_int64, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
 }
 
 
@@ -410,6 +411,13 @@ class Context:
         rows: what 0 the gate|up GEMM, 1 the whole prefill."""
         us, fl = c_double(), c_double()
         self._check(self.lib.qtts_time_prefill(self.h, rows, what, iters, byref(us), byref(fl)))
+        return us.value, fl.value
+
+    def time_decode(self, n_frames, iters):
+        """(avg us, flops) of one device decode_to_audio over `n_frames`
+        synthetic frames."""
+        us, fl = c_double(), c_double()
+        self._check(self.lib.qtts_time_decode(self.h, n_frames, iters, byref(us), byref(fl)))
         return us.value, fl.value
 
 
