@@ -396,6 +396,7 @@ k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *ou
     const bool ok = t < T;
     const float *xc = x + min(t, T - 1);
     float ss = 0.0f;
+#pragma unroll 8
     for (int h = cg; h < H; h += 16) {
         const float v = xc[(size_t)h * T];
         ss = fmaf(v, v, ss);
@@ -407,6 +408,7 @@ k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *ou
     for (int g = 0; g < 16; g++) tot += red[g][tl];
     const float inv = 1.0f / sqrtf(tot / (float)H + eps);
     if (!ok) return;
+#pragma unroll 8
     for (int h = cg; h < H; h += 16) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
 }
 
@@ -464,7 +466,8 @@ k_dec_attn(const float *qkv, int heads, int T, int W, float *out)
 
 // Sliding-window attention, workgroup per (head, 16 queries): the key and
 // value columns those queries see (positions t0-W+1 .. t0+15, zero before
-// position 0) and the 16 query columns staged in LDS.  Scores: lane (query
+// position 0) and the 16 query columns staged in LDS, q and k rotated
+// (RoPE) as they are staged.  Scores: lane (query
 // qi, key slot kl) holds keys kl + 16i; softmax max and sum over the 16
 // lanes of the query's row (DPP); then lane (qi, dim group dg) sums
 // p.v over the query's W keys in position order (keys before position 0
@@ -478,8 +481,24 @@ static inline size_t attn_tile_lds(int hd, int W)
 }
 
 template <int HD>
+__device__ __forceinline__ float rope_at(const float *row0, int d, int T, int p, const float *cs, const float *sn,
+                                         int64_t rope_rows)
+{
+    // row0: dimension 0 of this head's q or k rows ([HD][T]); rotate-half
+    // RoPE of element (d, p) as k_rope_cf computes it
+    const float x = row0[(size_t)d * T + p];
+    if (p >= rope_rows) return x;
+    constexpr int half = HD / 2;
+    const int i = d < half ? d : d - half;
+    const float xp = row0[(size_t)(d < half ? d + half : d - half) * T + p];
+    const float c = cs[(size_t)p * half + i], s = sn[(size_t)p * half + i];
+    return d < half ? x * c - xp * s : x * c + xp * s;
+}
+
+template <int HD>
 __global__ void __launch_bounds__(256)
-k_dec_attn_tile(const float *qkv, int heads, int T, int W, float *out)
+k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, const float *sn, int64_t rope_rows,
+                float *out)
 {
     extern __shared__ float sm[];
     const int NK = ATT_QB + W - 1, NKP = NK + 1;
@@ -489,16 +508,19 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, float *out)
     const float *q = qkv + (size_t)h * HD * T, *k = qkv + (A + (size_t)h * HD) * T,
                 *v = qkv + (2 * A + (size_t)h * HD) * T;
     float *Ks = sm, *Vs = Ks + HD * NKP, *Qs = Vs + HD * NKP, *Ps = Qs + HD * ATT_QB;
+#pragma unroll 4
     for (int i = tid; i < HD * NK; i += 256) {
         const int d = i / NK, j = i - d * NK, p = kb + j;
         const bool ok = p >= 0 && p < T;
-        const size_t src = (size_t)d * T + min(max(p, 0), T - 1);
-        Ks[d * NKP + j] = ok ? k[src] : 0.0f;
-        Vs[d * NKP + j] = ok ? v[src] : 0.0f;
+        const int pc = min(max(p, 0), T - 1);
+        const float kr = rope_at<HD>(k, d, T, pc, cs, sn, rope_rows);
+        Ks[d * NKP + j] = ok ? kr : 0.0f;
+        Vs[d * NKP + j] = *(ok ? v + (size_t)d * T + pc : k_zero);
     }
     for (int i = tid; i < HD * ATT_QB; i += 256) {
         const int d = i / ATT_QB, j = i - d * ATT_QB, p = t0 + j;
-        Qs[i] = p < T ? q[(size_t)d * T + p] : 0.0f;
+        const float qr = rope_at<HD>(q, d, T, min(p, T - 1), cs, sn, rope_rows);
+        Qs[i] = p < T ? qr : 0.0f;
     }
     __syncthreads();
     const int qi = tid >> 4, kl = tid & 15;
@@ -562,10 +584,12 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     const bool ok = t < L;
     const int tc = min(t, L - 1);
     float s1 = 0.0f;
+#pragma unroll 4
     for (int c = cg; c < C; c += 16) {
         const float *xr = x + (size_t)c * L;
         const float *wr = dw_w + (size_t)c * K;
         float v = dw_b[c];
+#pragma unroll 7
         for (int k = 0; k < K; k++) {
             const int p = tc + k - (K - 1);
             v += p >= 0 ? xr[max(p, 0)] * wr[k] : 0.0f;
@@ -580,6 +604,7 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     for (int q = 0; q < 16; q++) mean += red[0][q][tl];
     mean /= (float)C;
     float s2 = 0.0f;
+#pragma unroll 8
     for (int c = cg; c < C; c += 16) {
         const float d = ok ? out[(size_t)c * L + t] - mean : 0.0f;
         s2 += d * d;
@@ -592,23 +617,41 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     var /= (float)C;
     const float inv = 1.0f / sqrtf(var + eps);
     if (!ok) return;
+#pragma unroll 8
     for (int c = cg; c < C; c += 16) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
 }
 
 // Output conv (one channel, causal, conv.rs:191-228) on the snake input,
 // clamp to [-1, 1] (decoder.rs:567-570), written from sample `cut` on.
-__global__ void k_out_conv(const float *x, int C, int L, const float *w, float bias, int K, int dil, int64_t cut,
-                           float *out)
+// Workgroup per 256 samples; 16-channel slabs of the input with the
+// (K-1)*dil left halo (at most OUT_HALO, zero before position 0) staged in
+// LDS; each thread sums channel by channel, taps in order.
+constexpr int OUT_HALO = 64;
+
+__global__ void __launch_bounds__(256)
+k_out_conv(const float *x, int C, int L, const float *w, float bias, int K, int dil, int64_t cut, float *out)
 {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= L || t < cut) return;
+    constexpr int W = 256 + OUT_HALO;
+    __shared__ float xs[16][W];
+    const int tl = threadIdx.x, t0 = blockIdx.x * 256, t = t0 + tl;
     const int pad = (K - 1) * dil;
     float s = bias;
-    for (int c = 0; c < C; c++)
-        for (int k = 0; k < K; k++) {
-            const int p = t + k * dil - pad;
-            if (p >= 0) s += x[(size_t)c * L + p] * w[c * K + k];
+    for (int c0 = 0; c0 < C; c0 += 16) {
+        const int nc = min(16, C - c0);
+        __syncthreads();
+#pragma unroll 4
+        for (int i = tl; i < 16 * W; i += 256) {
+            const int cc = i / W, j = i - cc * W, p = t0 - pad + j;
+            const bool ok = cc < nc && p >= 0 && p < L;
+            xs[cc][j] = *(ok ? x + (size_t)(c0 + cc) * L + p : k_zero);
         }
+        __syncthreads();
+        for (int cc = 0; cc < nc; cc++) {
+            const float *wr = w + (size_t)(c0 + cc) * K;
+            for (int k = 0; k < K; k++) s += xs[cc][tl + k * dil] * wr[k];
+        }
+    }
+    if (t >= L || t < cut) return;
     out[t - cut] = s < -1.0f ? -1.0f : (s > 1.0f ? 1.0f : s);
 }
 
@@ -629,8 +672,13 @@ __global__ void k_snake(const float *x, int C, int L, const float *alpha, const 
 
 #define DCHK(x) do { hipError_t e_ = (x); if (e_ != hipSuccess) return e_; } while (0)
 
-static int conv_mb(int M)
+// Row-tile height 16 * MB: 96 rows when they divide M (the Vocos channel
+// counts 1536 ... 96), else 64 / 32 / 16.  The 96-row tile is built for
+// the tap-major path only (every large conv); 128 rows would spill at two
+// workgroups per CU.
+static int conv_mb(int M, bool tm)
 {
+    if (tm && M % 96 == 0) return 6;
     return M >= 64 ? 4 : (M >= 32 ? 2 : 1);
 }
 
@@ -639,6 +687,9 @@ static void conv_launch(int mb, dim3 grid, const float *A, int M, int Kd, const 
                         const GemmGeo &g, hipStream_t s)
 {
     switch (mb) {
+    case 6:
+        if constexpr (TM) hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g);
+        break;
     case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
     case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
     default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
@@ -664,7 +715,8 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
 {
     const int Kd = in.IC * in.K;
     if (M < 1 || N < 1 || Kd < 1 || nph < 1 || (EPI == CE_SWIGLU && (M & 1))) return hipErrorInvalidValue;
-    const int mb = conv_mb(M);
+    const bool tm = conv_tap_major(in.IC, in.K);
+    const int mb = conv_mb(M, tm);
     GemmGeo g{};
     g.tm = (M + 16 * mb - 1) / (16 * mb);
     g.tn = (N + CGN - 1) / CGN;
@@ -675,7 +727,7 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
     g.ks = (nch + g.cps - 1) / g.cps;   // no empty slice
     g.part = ws.part;
     const dim3 grid(g.tm * g.tn * nph * g.ks);
-    if (conv_tap_major(in.IC, in.K))
+    if (tm)
         conv_launch<EPI, true>(mb, grid, A, M, Kd, in, o, N, g, s);
     else
         conv_launch<EPI, false>(mb, grid, A, M, Kd, in, o, N, g, s);
@@ -744,14 +796,18 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
-        hipLaunchKernelGGL(k_rope_cf, dim3((T + 63) / 64, 2 * d.n_heads), dim3(64), 0, s, ws.d, d.n_heads,
-                           d.head_dim, T, d.rope_cos, d.rope_sin, d.rope_rows);
-        DCHK(hipGetLastError());
+        if (!att_tile) {   // the tiled kernel applies RoPE while staging
+            hipLaunchKernelGGL(k_rope_cf, dim3((T + 63) / 64, 2 * d.n_heads), dim3(64), 0, s, ws.d, d.n_heads,
+                               d.head_dim, T, d.rope_cos, d.rope_sin, d.rope_rows);
+            DCHK(hipGetLastError());
+        }
         const dim3 ag((T + ATT_QB - 1) / ATT_QB, d.n_heads);
         if (att_tile && d.head_dim == 64)
-            hipLaunchKernelGGL(k_dec_attn_tile<64>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window, ws.e);
+            hipLaunchKernelGGL(k_dec_attn_tile<64>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window,
+                               d.rope_cos, d.rope_sin, d.rope_rows, ws.e);
         else if (att_tile)
-            hipLaunchKernelGGL(k_dec_attn_tile<16>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window, ws.e);
+            hipLaunchKernelGGL(k_dec_attn_tile<16>, ag, dim3(256), att_lds, s, ws.d, d.n_heads, T, d.window,
+                               d.rope_cos, d.rope_sin, d.rope_rows, ws.e);
         else if (d.head_dim == 64)
             hipLaunchKernelGGL(k_dec_attn<64>, dim3((T + 63) / 64, d.n_heads), dim3(64), 0, s, ws.d, d.n_heads, T,
                                d.window, ws.e);

@@ -1501,6 +1501,8 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
     d.voc = c->dec_voc.data();
     d.n_voc = h->n_vocos_blocks;
     if (h->output_conv.in_channels != ch) return fail(c, QTTS_ERR_INVALID, "output conv input channels");
+    if ((h->output_conv.kernel_size - 1) * h->output_conv.dilation > 64)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "output conv reach (kernel-1)*dilation above 64");
     RCHK(upload_vec(c, A, h->final_snake_alpha, (size_t)ch, &d.final_alpha));
     RCHK(upload_vec(c, A, h->final_snake_beta, (size_t)ch, &d.final_beta));
     RCHK(upload_vec(c, A, h->output_conv.weight, (size_t)ch * h->output_conv.kernel_size, &d.out_w));
