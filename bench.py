@@ -326,7 +326,7 @@ def main():
         log("GEMV sweep: " + ", ".join(f"{k} {v['gbs']:.0f} GB/s" for k, v in kernels["q4_gemv_shapes"].items()))
 
     if not args.no_decoder:
-        kernels["speech_decoder"] = time_decoder(synth, qtts, 0 if args.no_cpu else 8)
+        kernels["speech_decoder"] = time_decoder(synth, qtts, 0 if args.no_cpu else 120)
 
     cpu = None
     if not args.no_cpu:

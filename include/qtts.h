@@ -242,10 +242,12 @@ int qtts_embed_lookup_q4(qtts_ctx *ctx, const qtts_w *w, int64_t row,
 int qtts_model_upload(qtts_ctx *ctx, const qtts_talker_host *talker,
                       const qtts_predictor_host *predictor);
 
-/* Read the talker and predictor sections of a `.qora-tts` file (QTTS v1,
- * Q4 format byte) straight into the context.  Replaces `save::load_model`
- * (save.rs:262-298) -> `load_talker` / `load_predictor` (save.rs:300-409);
- * the decoder and speaker sections after them are not read. */
+/* Read a `.qora-tts` file (QTTS v1, Q4 format byte) straight into the
+ * context: talker and predictor, then the speech decoder when the file goes
+ * on past the predictor.  Replaces `save::load_model` (save.rs:262-298) ->
+ * `load_talker` / `load_predictor` / `load_decoder_weights`
+ * (save.rs:300-552); the speaker-encoder section after them is not read.
+ * A malformed section fails with QTTS_ERR_IO before anything is uploaded. */
 int qtts_model_load_qtts(qtts_ctx *ctx, const char *path);
 
 /* Shapes of the uploaded model (hidden, vocab, ...); 0 on success. */
@@ -362,6 +364,13 @@ int qtts_build_icl_block(qtts_ctx *ctx, const uint32_t *ref_tokens, int64_t n_re
  * kernel = stride or 2 * stride and padding 0 (the model's 2x / 8,5,4,3x
  * stages), head_dim 64 or 16.  Replaces a previously uploaded decoder. */
 int qtts_decoder_upload(qtts_ctx *ctx, const qtts_decoder_host *decoder);
+
+/* Shape of the uploaded decoder: codebooks per frame (n_rest + 1), codes
+ * per codebook, and output samples per frame (the product of the upsampling
+ * strides: 1920 for the 12 Hz tokenizer).  QTTS_ERR_STATE without one.  No
+ * reference counterpart (the reference reads these off its Vecs). */
+int qtts_decoder_dims(qtts_ctx *ctx, int32_t *n_codebooks, int32_t *codebook_size,
+                      int64_t *samples_per_frame);
 
 /* `decode_to_audio` (decoder.rs:395-574): codes [n_codebooks][n_frames]
  * (codebook-major, n_codebooks = n_rest + 1), optional warmup codes

@@ -1,5 +1,5 @@
-// qtts_loader.cpp — reads the talker and predictor sections of a
-// `.qora-tts` model file straight into a context.
+// qtts_loader.cpp — reads the talker, predictor and speech-decoder sections
+// of a `.qora-tts` model file straight into a context.
 //
 // Stream layout (save.rs:23-137, gemv.rs:595-687), all little-endian:
 //   "QTTS" u32 version=1 u8 format (1 = Q4)
@@ -15,7 +15,22 @@
 //            f32v rope_cos rope_sin
 //   W    = u64 k, u64 n, u64 len + bytes (packed), u64 len + len*2 (f16 scales)
 //   f16v = u64 len + len*2 bytes;  f32v = u64 len + len*4 bytes
-// The decoder and speaker-encoder sections that follow are not read.
+//   speech decoder (save.rs:171-260; read when bytes follow the predictor):
+//            u32 hidden n_heads head_dim inter sliding_window codebook_dim,
+//            f32v first_codebook first_output_proj, u32 n_rest,
+//            f32v rest[n_rest], f32v rest_output_proj, C pre_conv,
+//            f32v tf_input_w tf_input_b, u32 n_tf, per layer f32v q k v o
+//            gate up down input_norm post_norm attn_scale mlp_scale,
+//            f32v tf_norm tf_output_w tf_output_b, u32 n_up, per stage
+//            u32 channels, CT conv_t, DW dw_conv, f32v norm_w norm_b pw1_w
+//            pw1_b pw2_w pw2_b gamma, C vocos_init, u32 n_blocks, per block
+//            f32v pre_alpha pre_beta, CT upsample, u32 n_res, per residual
+//            f32v a1_alpha a1_beta, C conv1, f32v a2_alpha a2_beta, C conv2;
+//            f32v final_alpha final_beta, C output_conv, f32v rope_cos rope_sin
+//   C  = u32 in out kernel stride padding dilation, f32v weight bias
+//   CT = u32 in out kernel stride padding, f32v weight bias
+//   DW = u32 channels kernel padding, f32v weight bias
+// The speaker-encoder section that may follow is not read.
 #include "../../include/qtts.h"
 
 #include <fcntl.h>
@@ -86,6 +101,202 @@ struct Reader {
     }
 };
 
+// f32 vectors of the decoder section, copied out of the mapping into
+// 4-byte-aligned storage (the stream has no alignment).
+struct F32Store {
+    std::vector<std::vector<float>> bufs;
+    const float *take(Reader &r, uint64_t expect, uint64_t *got = nullptr)
+    {
+        uint64_t n = 0;
+        const uint8_t *d = r.vec(4, &n);
+        if (!r.ok || (expect && n != expect) || n == 0) {
+            r.ok = false;
+            return nullptr;
+        }
+        if (got) *got = n;
+        bufs.emplace_back(n);
+        memcpy(bufs.back().data(), d, n * 4);
+        return bufs.back().data();
+    }
+};
+
+uint64_t u32v(Reader &r) { return r.get<uint32_t>(); }
+
+void read_conv(Reader &r, F32Store &st, qtts_conv1d_host &c)
+{
+    c.in_channels = (int32_t)u32v(r);
+    c.out_channels = (int32_t)u32v(r);
+    c.kernel_size = (int32_t)u32v(r);
+    c.stride = (int32_t)u32v(r);
+    c.padding = (int32_t)u32v(r);
+    c.dilation = (int32_t)u32v(r);
+    if (!r.ok || c.in_channels < 1 || c.out_channels < 1 || c.kernel_size < 1 || c.in_channels > (1 << 16) ||
+        c.out_channels > (1 << 16) || c.kernel_size > 64) {
+        r.ok = false;
+        return;
+    }
+    c.weight = st.take(r, (uint64_t)c.out_channels * c.in_channels * c.kernel_size);
+    c.bias = st.take(r, (uint64_t)c.out_channels);
+}
+
+void read_convt(Reader &r, F32Store &st, qtts_convt1d_host &c)
+{
+    c.in_channels = (int32_t)u32v(r);
+    c.out_channels = (int32_t)u32v(r);
+    c.kernel_size = (int32_t)u32v(r);
+    c.stride = (int32_t)u32v(r);
+    c.padding = (int32_t)u32v(r);
+    if (!r.ok || c.in_channels < 1 || c.out_channels < 1 || c.kernel_size < 1 || c.in_channels > (1 << 16) ||
+        c.out_channels > (1 << 16) || c.kernel_size > 64) {
+        r.ok = false;
+        return;
+    }
+    c.weight = st.take(r, (uint64_t)c.in_channels * c.out_channels * c.kernel_size);
+    c.bias = st.take(r, (uint64_t)c.out_channels);
+}
+
+void read_dw(Reader &r, F32Store &st, qtts_dwconv_host &c)
+{
+    c.channels = (int32_t)u32v(r);
+    c.kernel_size = (int32_t)u32v(r);
+    c.padding = (int32_t)u32v(r);
+    if (!r.ok || c.channels < 1 || c.kernel_size < 1 || c.channels > (1 << 16) || c.kernel_size > 64) {
+        r.ok = false;
+        return;
+    }
+    c.weight = st.take(r, (uint64_t)c.channels * c.kernel_size);
+    c.bias = st.take(r, (uint64_t)c.channels);
+}
+
+// Everything a decoder host descriptor points at.
+struct DecoderParts {
+    F32Store st;
+    std::vector<const float *> rest;
+    std::vector<qtts_dec_layer_host> layers;
+    std::vector<qtts_upsample_host> ups;
+    std::vector<std::vector<qtts_vocos_res_host>> res;
+    std::vector<qtts_vocos_block_host> blocks;
+};
+
+// load_decoder_weights (save.rs:446-552); sizes the reference derives from
+// vector lengths (codebook size, vq dim, ConvNeXt width) are derived the
+// same way and every vector's length is checked against them.
+bool read_decoder(Reader &r, DecoderParts &P, qtts_decoder_host &d)
+{
+    F32Store &st = P.st;
+    d.hidden = (int32_t)u32v(r);
+    d.n_heads = (int32_t)u32v(r);
+    d.head_dim = (int32_t)u32v(r);
+    d.inter = (int32_t)u32v(r);
+    d.sliding_window = (int32_t)u32v(r);
+    d.codebook_dim = (int32_t)u32v(r);
+    if (!r.ok || d.hidden < 1 || d.hidden > 65536 || d.n_heads < 1 || d.n_heads > 1024 || d.head_dim < 2 ||
+        d.head_dim > 1024 || d.inter < 1 || d.inter > (1 << 20) || d.codebook_dim < 1 || d.codebook_dim > 65536)
+        return false;
+    const uint64_t D = (uint64_t)d.codebook_dim, H = (uint64_t)d.hidden, A = (uint64_t)d.n_heads * d.head_dim;
+    const uint64_t I = (uint64_t)d.inter;
+    uint64_t cbl = 0, pl = 0;
+    d.first_codebook = st.take(r, 0, &cbl);
+    d.first_output_proj = st.take(r, 0, &pl);
+    if (!r.ok || cbl % D || pl % D) return false;
+    d.codebook_size = (int32_t)(cbl / D);
+    d.vq_dim = (int32_t)(pl / D);
+    const uint32_t n_rest = r.get<uint32_t>();
+    if (!r.ok || n_rest > 15) return false;
+    P.rest.resize(n_rest);
+    for (auto &c : P.rest) c = st.take(r, cbl);
+    d.rest_codebooks = P.rest.data();
+    d.n_rest = (int32_t)n_rest;
+    d.rest_output_proj = st.take(r, pl);
+    read_conv(r, st, d.pre_conv);
+    if (!r.ok) return false;
+    d.latent = d.pre_conv.out_channels;
+    const uint64_t LAT = (uint64_t)d.latent;
+    d.tf_input_w = st.take(r, LAT * H);
+    d.tf_input_b = st.take(r, H);
+    const uint32_t n_tf = r.get<uint32_t>();
+    if (!r.ok || n_tf > 256) return false;
+    P.layers.resize(n_tf);
+    for (auto &L : P.layers) {
+        L.q_proj = st.take(r, H * A);
+        L.k_proj = st.take(r, H * A);
+        L.v_proj = st.take(r, H * A);
+        L.o_proj = st.take(r, A * H);
+        L.gate_proj = st.take(r, H * I);
+        L.up_proj = st.take(r, H * I);
+        L.down_proj = st.take(r, I * H);
+        L.input_norm = st.take(r, H);
+        L.post_attn_norm = st.take(r, H);
+        L.attn_scale = st.take(r, H);
+        L.mlp_scale = st.take(r, H);
+    }
+    d.tf_layers = P.layers.data();
+    d.n_tf_layers = (int32_t)n_tf;
+    d.tf_norm = st.take(r, H);
+    d.tf_output_w = st.take(r, H * LAT);
+    d.tf_output_b = st.take(r, LAT);
+    const uint32_t n_up = r.get<uint32_t>();
+    if (!r.ok || n_up > 16) return false;
+    P.ups.resize(n_up);
+    for (auto &U : P.ups) {
+        U.channels = (int32_t)u32v(r);
+        if (!r.ok || U.channels < 1 || U.channels > 65536) return false;
+        const uint64_t ch = (uint64_t)U.channels;
+        read_convt(r, st, U.conv_t);
+        read_dw(r, st, U.dw_conv);
+        U.norm_w = st.take(r, ch);
+        U.norm_b = st.take(r, ch);
+        uint64_t w1 = 0;
+        U.pw1_w = st.take(r, 0, &w1);
+        if (!r.ok || w1 % ch) return false;
+        U.inner = (int32_t)(w1 / ch);
+        U.pw1_b = st.take(r, (uint64_t)U.inner);
+        U.pw2_w = st.take(r, (uint64_t)U.inner * ch);
+        U.pw2_b = st.take(r, ch);
+        U.gamma = st.take(r, ch);
+    }
+    d.upsample = P.ups.data();
+    d.n_upsample = (int32_t)n_up;
+    read_conv(r, st, d.vocos_init);
+    const uint32_t n_vb = r.get<uint32_t>();
+    if (!r.ok || n_vb > 16) return false;
+    P.blocks.resize(n_vb);
+    P.res.resize(n_vb);
+    int32_t ch = d.vocos_init.out_channels;
+    for (uint32_t b = 0; b < n_vb; b++) {
+        qtts_vocos_block_host &B = P.blocks[b];
+        B.pre_snake_alpha = st.take(r, (uint64_t)ch);
+        B.pre_snake_beta = st.take(r, (uint64_t)ch);
+        read_convt(r, st, B.upsample);
+        if (!r.ok) return false;
+        ch = B.upsample.out_channels;
+        const uint32_t n_res = r.get<uint32_t>();
+        if (!r.ok || n_res > 16) return false;
+        P.res[b].resize(n_res);
+        for (auto &R : P.res[b]) {
+            R.act1_alpha = st.take(r, (uint64_t)ch);
+            R.act1_beta = st.take(r, (uint64_t)ch);
+            read_conv(r, st, R.conv1);
+            R.act2_alpha = st.take(r, (uint64_t)ch);
+            R.act2_beta = st.take(r, (uint64_t)ch);
+            read_conv(r, st, R.conv2);
+        }
+        B.residuals = P.res[b].data();
+        B.n_residuals = (int32_t)n_res;
+    }
+    d.vocos_blocks = P.blocks.data();
+    d.n_vocos_blocks = (int32_t)n_vb;
+    d.final_snake_alpha = st.take(r, (uint64_t)ch);
+    d.final_snake_beta = st.take(r, (uint64_t)ch);
+    read_conv(r, st, d.output_conv);
+    uint64_t nc = 0, ns = 0;
+    d.rope_cos = st.take(r, 0, &nc);
+    d.rope_sin = st.take(r, 0, &ns);
+    if (!r.ok || nc != ns || nc % (uint64_t)(d.head_dim / 2)) return false;
+    d.rope_max_pos = (int64_t)(nc / (d.head_dim / 2));
+    return true;
+}
+
 void read_layer(Reader &r, qtts_layer_host &L, uint64_t head_dim, uint64_t hidden)
 {
     L.q_proj = r.weight();
@@ -123,6 +334,8 @@ extern "C" int qtts_model_load_qtts(qtts_ctx *ctx, const char *path)
     std::vector<qtts_q4_host> emb, heads;
     qtts_talker_host t{};
     qtts_predictor_host p{};
+    DecoderParts dparts;
+    qtts_decoder_host dec{};
     do {
         const uint8_t *magic = r.bytes(4);                       // save.rs:265-269
         if (!r.ok || memcmp(magic, "QTTS", 4) != 0) break;
@@ -197,7 +410,12 @@ extern "C" int qtts_model_load_qtts(qtts_ctx *ctx, const char *path)
         p.n_groups = (int32_t)nemb;
         p.inter = (int32_t)pl[0].gate_proj.n;
         p.vocab = (int32_t)heads[0].n;
+        // speech decoder, when the file goes on (a malformed section fails
+        // the load before anything is uploaded)
+        const bool has_decoder = r.p < r.end;
+        if (has_decoder && !read_decoder(r, dparts, dec)) break;
         rc = qtts_model_upload(ctx, &t, &p);
+        if (rc == QTTS_OK && has_decoder) rc = qtts_decoder_upload(ctx, &dec);
     } while (0);
     munmap(map, (size_t)sb.st_size);
     return rc;

@@ -1545,6 +1545,21 @@ extern "C" int qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_host *d)
 // to fill the GPU; long ones have columns enough and do not split.
 static constexpr size_t DEC_PART_FLOATS = (size_t)16 << 20;
 
+extern "C" int qtts_decoder_dims(qtts_ctx *c, int32_t *n_codebooks, int32_t *codebook_size,
+                                 int64_t *samples_per_frame)
+{
+    if (!c || !n_codebooks || !codebook_size || !samples_per_frame) return QTTS_ERR_INVALID;
+    if (!c->has_decoder) return fail(c, QTTS_ERR_STATE, "no speech decoder uploaded");
+    const DecoderDev &d = c->dec;
+    int64_t factor = 1;
+    for (int u = 0; u < d.n_up; u++) factor *= d.up[u].conv_t.stride;
+    for (int b = 0; b < d.n_voc; b++) factor *= d.voc[b].up.stride;
+    *n_codebooks = d.n_rest + 1;
+    *codebook_size = d.codebook_size;
+    *samples_per_frame = factor;
+    return QTTS_OK;
+}
+
 static int ensure_dec_ws(qtts_ctx *c, int frames)
 {
     if (frames <= c->dws.cap_frames) return QTTS_OK;

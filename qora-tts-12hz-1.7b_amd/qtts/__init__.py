@@ -75,6 +75,7 @@ SIGNATURES = {
     "qtts_build_icl_block": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                               c_void_p, c_int], c_int),
     "qtts_decoder_upload": ([c_void_p, POINTER(DecoderHost)], c_int),
+    "qtts_decoder_dims": ([c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int64)], c_int),
     "qtts_decode_to_audio": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int64),
                               c_int], c_int),
     "qtts_predictor_chain": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
@@ -207,6 +208,8 @@ class Context:
 
     def load_qtts(self, path):
         self._check(self.lib.qtts_model_load_qtts(self.h, os.fsencode(path)))
+        if self.has_decoder():
+            self.dec_codebooks = self.decoder_dims()[0]
         self.dims()
 
     def dims(self):
@@ -320,6 +323,16 @@ class Context:
         h, keep = decoder_host(decoder)
         self._check(self.lib.qtts_decoder_upload(self.h, ctypes.byref(h)))
         self.dec_codebooks = len(decoder.rest_codebooks) + 1
+
+    def decoder_dims(self):
+        """(codebooks per frame, codes per codebook, samples per frame)."""
+        n, cs, spf = c_int32(), c_int32(), c_int64()
+        self._check(self.lib.qtts_decoder_dims(self.h, byref(n), byref(cs), byref(spf)))
+        return n.value, cs.value, spf.value
+
+    def has_decoder(self):
+        n, cs, spf = c_int32(), c_int32(), c_int64()
+        return self.lib.qtts_decoder_dims(self.h, byref(n), byref(cs), byref(spf)) == OK
 
     def decode_to_audio(self, codes, warmup=None):
         """decode_to_audio (decoder.rs:395-574): codes [n_codebooks][T],

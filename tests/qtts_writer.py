@@ -17,8 +17,10 @@ qtts_model_load_qtts.  Little-endian throughout:
     W    = u64 k, u64 n, u64 len + packed bytes, u64 len + len f16 scales
     f16v = u64 len + len * 2 bytes;  f32v = u64 len + len * 4 bytes
 
-The speech-decoder and speaker-encoder sections that follow in a real file
-are not written: the device loader stops after the predictor.
+With `decoder`, the speech-decoder section follows (save.rs:139-260:
+config u32s, codebooks, pre-conv, transformer, upsamplers, Vocos, output
+conv, RoPE tables; convolutions as u32 shape fields then f32v weight and
+bias).  The speaker-encoder section of a real file is not written.
 """
 import struct
 
@@ -69,7 +71,76 @@ def _layer(f, L):
     _f16v(f, L.post_attn_norm)
 
 
-def write_qtts(path, talker, predictor, format_id=1, mrope_section=(24, 20, 20)):
+def _conv(f, c):
+    for v in (c.in_channels, c.out_channels, c.kernel_size, c.stride, c.padding, c.dilation):
+        _u32(f, v)
+    _f32v(f, c.weight.reshape(-1))
+    _f32v(f, c.bias)
+
+
+def _convt(f, c):
+    for v in (c.in_channels, c.out_channels, c.kernel_size, c.stride, c.padding):
+        _u32(f, v)
+    _f32v(f, c.weight.reshape(-1))
+    _f32v(f, c.bias)
+
+
+def _dw(f, c):
+    for v in (c.channels, c.kernel_size, c.padding):
+        _u32(f, v)
+    _f32v(f, c.weight.reshape(-1))
+    _f32v(f, c.bias)
+
+
+def _decoder(f, d):
+    for v in (d.hidden, d.n_heads, d.head_dim, d.inter, d.sliding_window, d.codebook_dim):
+        _u32(f, v)
+    _f32v(f, d.first_codebook.reshape(-1))
+    _f32v(f, d.first_output_proj.reshape(-1))
+    _u32(f, len(d.rest_codebooks))
+    for cb in d.rest_codebooks:
+        _f32v(f, cb.reshape(-1))
+    _f32v(f, d.rest_output_proj.reshape(-1))
+    _conv(f, d.pre_conv)
+    _f32v(f, d.tf_input_w.reshape(-1))
+    _f32v(f, d.tf_input_b)
+    _u32(f, len(d.tf_layers))
+    for L in d.tf_layers:
+        for v in (L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj, L.up_proj, L.down_proj, L.input_norm,
+                  L.post_attn_norm, L.attn_scale, L.mlp_scale):
+            _f32v(f, v.reshape(-1))
+    _f32v(f, d.tf_norm)
+    _f32v(f, d.tf_output_w.reshape(-1))
+    _f32v(f, d.tf_output_b)
+    _u32(f, len(d.upsample))
+    for u in d.upsample:
+        _u32(f, u.channels)
+        _convt(f, u.conv_t)
+        _dw(f, u.dw_conv)
+        for v in (u.norm_w, u.norm_b, u.pw1_w, u.pw1_b, u.pw2_w, u.pw2_b, u.gamma):
+            _f32v(f, v.reshape(-1))
+    _conv(f, d.vocos_init)
+    _u32(f, len(d.vocos_blocks))
+    for b in d.vocos_blocks:
+        _f32v(f, b.pre_snake_alpha)
+        _f32v(f, b.pre_snake_beta)
+        _convt(f, b.upsample)
+        _u32(f, len(b.residuals))
+        for r in b.residuals:
+            _f32v(f, r.act1_alpha)
+            _f32v(f, r.act1_beta)
+            _conv(f, r.conv1)
+            _f32v(f, r.act2_alpha)
+            _f32v(f, r.act2_beta)
+            _conv(f, r.conv2)
+    _f32v(f, d.final_snake_alpha)
+    _f32v(f, d.final_snake_beta)
+    _conv(f, d.output_conv)
+    _f32v(f, d.rope_cos.reshape(-1))
+    _f32v(f, d.rope_sin.reshape(-1))
+
+
+def write_qtts(path, talker, predictor, format_id=1, mrope_section=(24, 20, 20), decoder=None):
     t, p = talker, predictor
     with open(path, "wb") as f:
         f.write(b"QTTS")
@@ -108,3 +179,5 @@ def write_qtts(path, talker, predictor, format_id=1, mrope_section=(24, 20, 20))
         _f16v(f, p.final_norm)
         _f32v(f, p.rope_cos.reshape(-1))
         _f32v(f, p.rope_sin.reshape(-1))
+        if decoder is not None:
+            _decoder(f, decoder)

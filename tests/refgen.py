@@ -25,6 +25,13 @@ class XRng:
         return s
 
 
+def rvec(st, n, mag):
+    """rvec of the reference's conv tests (conv.rs:707-711):
+    ((xrng % 2000) as f32 / 1000 - 1) * mag, in f32."""
+    r = np.fromiter((st.next() % 2000 for _ in range(n)), dtype=np.float32, count=n)
+    return (r / np.float32(1000.0) - np.float32(1.0)) * np.float32(mag)
+
+
 def rbytes(st, n):
     return np.array([st.next() & 0xFF for _ in range(n)], dtype=np.uint8)
 

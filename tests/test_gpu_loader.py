@@ -1,7 +1,8 @@
-"""`.qora-tts` loading (save.rs:262-409 -> qtts_model_load_qtts): a model
+"""`.qora-tts` loading (save.rs:262-552 -> qtts_model_load_qtts): a model
 written in the reference's stream layout by tests/qtts_writer.py and loaded
 from the file behaves bit-for-bit like the same weights uploaded from
-memory, and malformed files fail with the documented status."""
+memory -- talker, predictor and speech decoder -- and malformed files fail
+with the documented status before anything is uploaded."""
 import os
 
 import numpy as np
@@ -73,3 +74,52 @@ def test_malformed_files(ctx_factory, model_file, tmp_path):
     with pytest.raises(qtts.QttsError) as e:
         c.load_qtts(str(tmp_path / "missing.qora-tts"))
     assert e.value.code == qtts.ERR_IO
+
+
+def small_decoder():
+    return synth.make_decoder(seed=41, latent=64, hidden=64, n_heads=4, head_dim=16, inter=128, n_tf_layers=2,
+                              codebook_size=64, codebook_dim=32, vq_dim=32, vocos=(48, 32, 24, 16, 8),
+                              rope_max_pos=512)
+
+
+@pytest.fixture(scope="module")
+def full_file(tmp_path_factory):
+    t = synth.make_talker(seed=311, n_layers=1, text_vocab=256, rope_max_pos=256)
+    p = synth.make_predictor(seed=312, n_layers=5, rope_max_pos=64)
+    d = small_decoder()
+    path = str(tmp_path_factory.mktemp("qtts") / "full.qora-tts")
+    write_qtts(path, t, p, decoder=d)
+    return path, t, p, d
+
+
+def test_loaded_decoder_matches_upload(ctx_factory, full_file):
+    path, t, p, d = full_file
+    a, b = ctx_factory(256), ctx_factory(256)
+    a.upload_decoder(d)
+    b.load_qtts(path)
+    assert b.decoder_dims() == a.decoder_dims() == (16, d.codebook_size, d.upsample_factor)
+    rng = np.random.Generator(np.random.PCG64(32))
+    codes = rng.integers(0, d.codebook_size, (16, 25))
+    warm = rng.integers(0, d.codebook_size, (16, 7))
+    assert np.array_equal(bits(a.decode_to_audio(codes, warm)), bits(b.decode_to_audio(codes, warm)))
+    # the talker and predictor of the same file still load as before
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    a.upload_model(t, p)
+    assert np.array_equal(bits(a.forward_with_embedding(emb, 0)), bits(b.forward_with_embedding(emb, 0)))
+
+
+def test_malformed_decoder_section(ctx_factory, full_file, tmp_path):
+    path, t, p, d = full_file
+    data = open(path, "rb").read()
+    write_qtts(str(tmp_path / "head.qora-tts"), t, p)
+    head = len(open(tmp_path / "head.qora-tts", "rb").read())   # where the decoder section starts
+    assert data[:head] == open(tmp_path / "head.qora-tts", "rb").read()
+    c = ctx_factory(256)
+    for name, blob in (("cut_config", data[:head + 10]), ("cut_middle", data[:(head + len(data)) // 2]),
+                       ("cut_rope", data[:len(data) - 3])):
+        f = tmp_path / f"{name}.qora-tts"
+        f.write_bytes(blob)
+        with pytest.raises(qtts.QttsError) as e:
+            c.load_qtts(str(f))
+        assert e.value.code == qtts.ERR_IO, name
+        assert not c.has_decoder(), name

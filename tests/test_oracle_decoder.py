@@ -28,6 +28,68 @@ def test_warmup_trim_len_known_answers():
     assert O.warmup_trim_len(10, 10, 50) == 50
 
 
+def bits32(v):
+    return int(np.float32(v).view(np.uint32))
+
+
+def test_reference_transpose_dw_goldens():
+    """The reference's own bit-exact goldens (test_transpose_dw_golden,
+    conv.rs:772-823): a 192 -> 96 transposed conv (kernel 4, stride 3,
+    padding 1) over 3000 positions and a 96-channel depthwise conv (kernel
+    7, causal) over 20000, inputs from its xorshift generator (seed 777):
+    sums, three sampled output bits each and the 64-point sweep hash."""
+    from refgen import XRng, rvec
+    st = XRng(777)
+    inp = rvec(st, 192 * 3000, 1.0).reshape(192, 3000)
+    w = rvec(st, 192 * 96 * 4, 0.2).reshape(192, 96, 4)
+    b = rvec(st, 96, 0.1)
+    y = O.conv_transpose1d(inp, synth.ConvT1d(w, b, 192, 96, 4, 3, 1)).reshape(-1)
+    assert y.size == 96 * ((3000 - 1) * 3 - 2 + 4)
+    assert abs(float(y.sum(dtype=np.float64)) - 10309.475586) < 1.0
+    assert bits32(y[0]) == bits32(0.11413957)
+    assert bits32(y[12345]) == bits32(0.30676275)
+    assert bits32(y[-1]) == bits32(0.7365111)
+    step = y.size // 64
+    acc = 0
+    for n in range(0, 64 * step, step):
+        acc = (acc + bits32(y[n]) * (n + 1)) % (1 << 64)
+    assert acc == 59818250823433361
+    inp2 = rvec(st, 96 * 20000, 1.0).reshape(96, 20000)
+    w2 = rvec(st, 96 * 7, 0.2).reshape(96, 7)
+    b2 = rvec(st, 96, 0.1)
+    y2 = O.depthwise_conv1d(inp2, synth.DwConv(w2, b2, 96, 7, 6)).reshape(-1)
+    assert abs(float(y2.sum(dtype=np.float64)) - -3754.235596) < 1.0
+    assert bits32(y2[0]) == bits32(0.030722003)
+    assert bits32(y2[765432]) == bits32(-0.250796)
+    assert bits32(y2[-1]) == bits32(-0.10229)
+
+
+def test_reference_gemm_bitexact_cases():
+    """test_f32_gemm_bitexact (conv.rs:713-757): f32_gemm_bias equals the
+    reference's naive same-order loop (bias first, k ascending, exact zeros
+    of A skipped so a -0.0 bias keeps its sign) bit for bit, on its three
+    shapes and xorshift inputs (seed 4242), with its planted zeros."""
+    from refgen import XRng, rvec
+    st = XRng(4242)
+    for m, n, k in ((7, 13, 11), (64, 97, 48), (128, 482, 256)):
+        a = rvec(st, m * k, 1.0)
+        b = rvec(st, k * n, 0.5).reshape(k, n)
+        bias = rvec(st, m, 0.1)
+        a[0] = 0.0
+        a[1] = -0.0
+        bias[0] = -0.0
+        a = a.reshape(m, k)
+        expect = np.repeat(bias[:, None], n, axis=1).astype(np.float32)
+        for kk in range(k):
+            col = a[:, kk:kk + 1]
+            expect = np.where(col == 0.0, expect, expect + col * b[kk][None, :]).astype(np.float32)
+        got = O.gemm_bias(a, b, bias)
+        assert np.array_equal(got.view(np.uint32), expect.view(np.uint32)), (m, n, k)
+    # the -0.0 bias survives a row whose A entries are all zero
+    z = O.gemm_bias(np.zeros((1, 3), np.float32), np.ones((3, 2), np.float32), np.array([-0.0], np.float32))
+    assert np.signbit(z).all()
+
+
 def test_conv_kernels_vs_f64():
     rng = np.random.Generator(np.random.PCG64(5))
     x = rng.standard_normal((24, 50)).astype(np.float32)
