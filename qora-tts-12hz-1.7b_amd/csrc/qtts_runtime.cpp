@@ -1604,7 +1604,8 @@ extern "C" int qtts_decode_to_audio(qtts_ctx *c, const uint32_t *codes, int64_t 
     for (int u = 0; u < d.n_up; u++) factor *= d.up[u].conv_t.stride;
     for (int b = 0; b < d.n_voc; b++) factor *= d.voc[b].up.stride;
     const int64_t len = T * factor;
-    // warmup_trim_len (decoder.rs:661-666)
+    if (len > INT32_MAX) return fail(c, QTTS_ERR_CAPACITY, "%lld samples exceed one decode", (long long)len);
+    // warmup_trim_len (decoder.rs:651-656)
     const int64_t cut = n_warmup ? std::min<int64_t>(n_warmup * len / T, len) : 0;
     const int64_t n = len - cut;
     if (!audio || capacity < n) {
@@ -1623,10 +1624,9 @@ extern "C" int qtts_decode_to_audio(qtts_ctx *c, const uint32_t *codes, int64_t 
     HIPCHK(c, hipMemcpyAsync(c->dws.codes, all.data(), all.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
                              c->stream));
     float *out = audio;
-    DevScratch tmp;
-    if (!(flags & QTTS_DEVICE_PTRS)) {
-        HIPCHK(c, hipMalloc(&tmp.p, (size_t)n * sizeof(float)));
-        out = (float *)tmp.p;
+    if (!(flags & QTTS_DEVICE_PTRS)) {   // stage the samples in the context's I/O buffer
+        RCHK(ensure_io(c, n));
+        out = c->d_io;
     }
     HIPCHK(c, enqueue_decode(d, c->dws, c->dws.codes, (int)T, cut, out, c->stream));
     if (!(flags & QTTS_DEVICE_PTRS))
