@@ -7,7 +7,7 @@ matrix-core sums in another order than the reference's loops; the clamp to
 [-1, 1] is the same).  Size-independent checks: warmup trimming equals
 decoding the concatenation and dropping `warmup_trim_len` samples (bit for
 bit, same kernels and sizes), and a decoder is causal, so a prefix of the
-frames decodes to a prefix of the samples.
+frames decodes to a prefix of the samples (within 1e-5).
 """
 import numpy as np
 import pytest
@@ -79,15 +79,20 @@ def test_warmup_is_trimmed_concatenation(ctx, small):
     assert np.array_equal(got.view(np.uint32), full[cut:].view(np.uint32))
 
 
+CAUSAL_TOL = 1e-5
+
+
 def test_decode_is_causal(ctx, small):
     """Every stage is causal (causal convs, left-looking attention window,
     right-cropped transposed convs), so frames past t leave samples up to t
-    unchanged -- bit for bit, since no kernel's per-sample arithmetic
-    depends on the number of frames."""
+    unchanged.  Within 1e-5 of the peak rather than bitwise: how a short
+    stage splits its contraction across workgroups depends on the launch
+    size, so two lengths may add the same products in another order."""
     codes = codes_for(small, 64, 4300)
     full = ctx.decode_to_audio(codes)
     head = ctx.decode_to_audio(codes[:, :40])
-    assert np.array_equal(head.view(np.uint32), full[:head.size].view(np.uint32))
+    ok, e = close(head, full[:head.size], rel=CAUSAL_TOL)
+    assert ok, f"rel err {e}"
 
 
 def test_decode_edges(ctx, small):
@@ -112,13 +117,23 @@ def test_decode_without_decoder(ctx_factory):
     assert e.value.code == qtts.ERR_STATE
 
 
-def test_decode_full_dims_vs_oracle(ctx_factory):
+@pytest.fixture(scope="module")
+def full():
+    return synth.make_decoder(seed=7)
+
+
+@pytest.fixture(scope="module")
+def full_ctx(ctx_factory, full):
+    c = ctx_factory(64)
+    c.upload_decoder(full)
+    return c
+
+
+def test_decode_full_dims_vs_oracle(full_ctx, full):
     """The 12 Hz tokenizer's decoder shapes (16 codebooks of 2048 x 256, an
     8-layer 512-wide transformer, 1024-channel upsamplers, Vocos 1536 -> 96,
     1920 samples per frame) on 6 frames after 3 warmup frames."""
-    d = synth.make_decoder(seed=7)
-    c = ctx_factory(64)
-    c.upload_decoder(d)
+    d, c = full, full_ctx
     codes, warm = codes_for(d, 6, 4600), codes_for(d, 3, 4601)
     ref = O.decode_to_audio(d, codes, warmup=warm, threads=16)
     got = c.decode_to_audio(codes, warmup=warm)
@@ -126,3 +141,30 @@ def test_decode_full_dims_vs_oracle(ctx_factory):
     ok, e = close(got, ref)
     assert ok, f"rel err {e}"
     assert np.abs(ref).max() > 0.05            # a live signal, not a clamp or zeros
+
+
+def test_decode_full_dims_longer_vs_oracle(full_ctx, full):
+    """80 frames at the full shapes: the transformer (one position per
+    frame) runs past its 72-position window, and the short stages split
+    their contraction differently than at 9 frames."""
+    d, c = full, full_ctx
+    codes = codes_for(d, 80, 4700)
+    ref = O.decode_to_audio(d, codes, threads=16)
+    got = c.decode_to_audio(codes)
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+
+
+def test_decode_full_dims_properties(full_ctx, full):
+    """Warmup trim (bit-identical: same length, same kernels) and causality
+    (within 1e-5, see test_decode_is_causal) at the full shapes, at lengths
+    past the attention window (120 and 80 frames)."""
+    d, c = full, full_ctx
+    codes, warm = codes_for(d, 100, 4800), codes_for(d, 20, 4801)
+    whole = c.decode_to_audio(np.concatenate([warm, codes], axis=1))
+    got = c.decode_to_audio(codes, warmup=warm)
+    cut = O.warmup_trim_len(20, 120, whole.size)
+    assert np.array_equal(got.view(np.uint32), whole[cut:].view(np.uint32))
+    head = c.decode_to_audio(np.concatenate([warm, codes], axis=1)[:, :80])
+    ok, e = close(head, whole[:head.size], rel=CAUSAL_TOL)
+    assert ok, f"rel err {e}"
