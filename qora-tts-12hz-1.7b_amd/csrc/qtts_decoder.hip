@@ -33,7 +33,7 @@ constexpr int CGN = 128, CGK = 32, CLD = CGK + 4;
 // Read (never written) in place of out-of-range taps; a plain global
 // (not const) so that selecting between it and an activation pointer
 // stays in the global address space.
-__device__ float k_zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+__device__ __attribute__((aligned(16))) float k_zero[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 
 enum ConvEpi : int {
     CE_STORE = 0,        // y = acc + bias
@@ -162,29 +162,16 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         f32x4 b[4];
     };
     auto fetch = [&](Fetch &f, int k0) {
+        // Out-of-range rows, chunk tails and taps read k_zero: selecting the
+        // address rather than the value keeps every load unconditional (a
+        // select on the value lets the compiler sink each load into a
+        // branch of its own, or compute both sides, and wait on it there).
+        // Kd is a multiple of 4 (conv_gemm checks), so a quad is in or out.
 #pragma unroll
         for (int j = 0; j < NA; j++) {
             const int kk = k0 + akk[j];
-            if ((Kd & 3) == 0 && kk + 3 < Kd) {   // rows 16-byte aligned
-                f.a[j] = ld4(arow[j] + kk);
-            } else {
-                f32x4 v;
-                v.x = arow[j][min(kk, Kd - 1)];
-                v.y = arow[j][min(kk + 1, Kd - 1)];
-                v.z = arow[j][min(kk + 2, Kd - 1)];
-                v.w = arow[j][min(kk + 3, Kd - 1)];
-                v.x = kk < Kd ? v.x : 0.0f;
-                v.y = kk + 1 < Kd ? v.y : 0.0f;
-                v.z = kk + 2 < Kd ? v.z : 0.0f;
-                v.w = kk + 3 < Kd ? v.w : 0.0f;
-                f.a[j] = v;
-            }
-            f.a[j] = aok[j] ? f.a[j] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            f.a[j] = ld4((aok[j] && kk < Kd) ? arow[j] + kk : k_zero);
         }
-        // Out-of-range taps read k_zero: selecting the address rather than
-        // the value keeps every load unconditional (a select on the value
-        // lets the compiler sink each load into a branch of its own and
-        // wait on it there).
         if (TM) {
             const int tap = k0 / in.IC, icb = k0 - tap * in.IC;
             const int p = pos0 + tap * in.dil - in.pad;
@@ -714,7 +701,7 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
                             hipStream_t s, int nph = 1)
 {
     const int Kd = in.IC * in.K;
-    if (M < 1 || N < 1 || Kd < 1 || nph < 1 || (EPI == CE_SWIGLU && (M & 1))) return hipErrorInvalidValue;
+    if (M < 1 || N < 1 || Kd < 1 || (Kd & 3) || nph < 1 || (EPI == CE_SWIGLU && (M & 1))) return hipErrorInvalidValue;
     const bool tm = conv_tap_major(in.IC, in.K);
     const int mb = conv_mb(M, tm);
     GemmGeo g{};

@@ -1323,6 +1323,7 @@ static int upload_conv(qtts_ctx *c, const qtts_conv1d_host &h, DecConv *d)
         return fail(c, QTTS_ERR_INVALID, "bad conv1d descriptor");
     if (h.stride != 1) return fail(c, QTTS_ERR_UNSUPPORTED, "strided conv1d not used by the decoder");
     const int IC = h.in_channels, OC = h.out_channels, K = h.kernel_size;
+    if ((IC * K) % 4) return fail(c, QTTS_ERR_UNSUPPORTED, "conv1d in_channels*kernel %d not a multiple of 4", IC * K);
     d->ic = IC;
     d->oc = OC;
     d->k = K;
@@ -1349,6 +1350,7 @@ static int upload_convt(qtts_ctx *c, const qtts_convt1d_host &h, DecConvT *d)
         return fail(c, QTTS_ERR_UNSUPPORTED, "conv_transpose1d needs kernel = stride or 2*stride, padding 0");
     const int IC = h.in_channels, OC = h.out_channels, K = h.kernel_size, S = h.stride;
     const int taps = K / S;
+    if ((IC * taps) % 4) return fail(c, QTTS_ERR_UNSUPPORTED, "conv_transpose1d in_channels*taps not a multiple of 4");
     const bool tm = conv_tap_major(IC, taps);
     std::vector<float> p((size_t)S * OC * IC * taps);
     for (int r = 0; r < S; r++)
@@ -1377,6 +1379,8 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
     const int LAT = h->latent, AD = NH * HD;
     if (H < 1 || NH < 1 || (HD != 64 && HD != 16) || I < 1 || D < 1 || V < 1 || LAT < 1 || h->sliding_window < 1)
         return fail(c, QTTS_ERR_UNSUPPORTED, "decoder shape not supported (head_dim %d)", HD);
+    if (H % 4 || I % 4 || D % 2 || LAT % 4)   // matrix-core contractions run in quads
+        return fail(c, QTTS_ERR_UNSUPPORTED, "decoder widths must be multiples of 4");
     if (h->n_rest < 0 || h->n_rest > 15 || h->codebook_size < 1 || !h->first_codebook || !h->first_output_proj ||
         (h->n_rest && (!h->rest_codebooks || !h->rest_output_proj)))
         return fail(c, QTTS_ERR_INVALID, "decoder codebooks");
@@ -1445,7 +1449,7 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
         const qtts_upsample_host &U = h->upsample[u];
         DecUpsample &o = c->dec_up[u];
         if (U.channels != ch || U.conv_t.in_channels != ch || U.conv_t.out_channels != ch ||
-            U.dw_conv.channels != ch || U.inner < 1)
+            U.dw_conv.channels != ch || U.inner < 1 || U.inner % 4)
             return fail(c, QTTS_ERR_INVALID, "upsample stage %d shapes", u);
         RCHK(upload_convt(c, U.conv_t, &o.conv_t));
         RCHK(upload_vec(c, A, U.dw_conv.weight, (size_t)ch * U.dw_conv.kernel_size, &o.dw_w));
