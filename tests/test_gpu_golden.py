@@ -1,0 +1,108 @@
+"""The HIP path against the committed golden fixtures (tests/golden/, the
+oracle's outputs on seeded inputs; inputs regenerated here from the seeds in
+manifest.json and checked against their recorded digests).  Bars as in the
+other parity tests: GEMV, step and decoder outputs within 1e-3 of the
+reference's scale; codes exact on the first predictor input and >= 99%
+overall; greedy frames >= 99% teacher-forced."""
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+
+import make_golden as G  # noqa: E402
+import qtts  # noqa: E402
+from qtts import synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+MANIFEST = json.load(open(os.path.join(HERE, "golden", "manifest.json")))
+TOL = 1e-3
+
+
+def fixture(name):
+    return np.load(os.path.join(HERE, "golden", name + ".npz"))
+
+
+def close(got, ref, rel=TOL):
+    ref = np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), np.sqrt((ref ** 2).mean()), 1e-30)
+    err = np.abs(np.asarray(got, np.float64) - ref).max()
+    return err <= rel * scale, err / scale
+
+
+@pytest.fixture(scope="module")
+def loaded(ctx_factory):
+    t, p = G.models()
+    assert G.digest((t, p)) == MANIFEST["fixtures"]["talker_step"]["model"], "synthetic model generator drifted"
+    c = ctx_factory(1024)
+    c.upload_model(t, p)
+    return c, t
+
+
+def test_gemv_golden(ctx_factory):
+    c = ctx_factory(64)
+    w, x, cases = G.gemv_inputs()
+    f = fixture("gemv")
+    assert G.digest((w, x)) == MANIFEST["fixtures"]["gemv"]["inputs"]["config1"]
+    dw = c.upload(w)
+    ok, e = close(c.gemv(dw, x), f["config1_y"])
+    dw.free()
+    assert ok, f"config 1: rel err {e}"
+    for name, (cx, cw) in cases.items():
+        dw = c.upload(cw)
+        ok, e = close(c.gemv(dw, cx), f[name + "_y"])
+        dw.free()
+        assert ok, f"{name}: rel err {e}"
+
+
+def test_talker_step_golden(loaded):
+    c, t = loaded
+    K, V, emb = G.talker_step_inputs(t)
+    f = fixture("talker_step")
+    c.kv_reset()
+    c.kv_load(K, V)
+    out = c.forward_with_embedding(emb, 512)
+    k, v = c.kv_gather(0)
+    c.kv_reset()
+    for name, got in (("hidden", out[: t.hidden]), ("logits", out[t.hidden:]), ("k_new", k[512]), ("v_new", v[512])):
+        ok, e = close(got, f[name])
+        assert ok, f"{name}: rel err {e}"
+
+
+def test_predictor_golden(loaded):
+    c, t = loaded
+    ref = fixture("predictor")["codes"]
+    got = np.stack([c.generate_acoustic_codes(th, c.embed_codec_token(sem)) for th, sem in G.predictor_inputs(t)])
+    assert np.array_equal(got[0], ref[0]), f"{got[0]} vs {ref[0]}"
+    assert (got == ref).mean() >= 0.99
+
+
+def test_greedy_frames_golden(loaded):
+    """200 greedy frames, each fed the recorded codes of the frame before."""
+    c, t = loaded
+    ref = fixture("greedy_frames")["codes"]
+    X = G.greedy_prompt(t)
+    c.kv_reset()
+    hid = c.prefill_talker_raw_from(X, 0)
+    logits = c.apply_codec_head(hid)
+    c.gen_set_text(None, c.embed_text_token(3))
+    c.gen_begin(logits, hid, 16, 42, qtts.sample_params(top_k=1, eos_enabled=False))
+    pred = c.gen_frames_forced(ref)
+    c.kv_reset()
+    agree = (pred == ref).mean()
+    assert agree >= 0.99, f"agreement {agree:.4f}"
+
+
+def test_decoder_golden(ctx_factory):
+    d = synth.make_decoder(**G.DECODER)
+    assert G.digest(d) == MANIFEST["fixtures"]["decoder"]["model"]
+    codes, warm = G.decoder_inputs(d)
+    c = ctx_factory(64)
+    c.upload_decoder(d)
+    ok, e = close(c.decode_to_audio(codes, warm), fixture("decoder")["audio"])
+    assert ok, f"rel err {e}"
