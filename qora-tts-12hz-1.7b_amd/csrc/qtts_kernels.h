@@ -41,6 +41,7 @@ struct PredictorDev {
     Q4Tiled proj;
     const float *proj_bias;
     const float *proj_rows;              // [n_groups-1][emb rows][hidden] projected embedding rows, or null
+    const float *qkv_rows;               // [n_groups-1][emb rows][layers[0].qkv.npad] their layer-0 q|k|v, or null
     const Q4Tiled *heads;                // host array [n_groups]
     Q4Rows emb_rows;                     // [n_groups][rows][...] contiguous
     const uint16_t *final_norm;
@@ -192,6 +193,8 @@ hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws,
 hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s);
 hipError_t enqueue_pred_row_tables(const PredictorDev &p, int n_tables, float *X, float *part, float *out,
                                    hipStream_t s);
+bool pred_qkv_tables_supported(const PredictorDev &p);
+hipError_t enqueue_pred_qkv_tables(const PredictorDev &p, int n_tables, float *part, float *out, hipStream_t s);
 bool gemm_supported(const Q4Tiled &w);
 hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s);
 hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,

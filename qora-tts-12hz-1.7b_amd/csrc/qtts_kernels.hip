@@ -589,8 +589,10 @@ struct ProCodeRowRms {
             const uint32_t fc = st->fcode[slot];
             f.pred = cand_argmax(cand, ncand, f.nan);
             f.used = force ? fc : f.pred;
-        } else {
+        } else if (st) {
             f.pred = f.used = st->used[slot];
+        } else {
+            f.pred = f.used = blockIdx.y;   // table build: one row per grid row
         }
         const float *row = table + (size_t)min(f.used, (uint32_t)(rows - 1)) * k;
 #pragma unroll
@@ -1468,8 +1470,16 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
 // appends the new K (normed, roped) and V (raw) to the cache; no workgroup
 // of the same launch reads those entries back from memory.
 // Needs T == 256, KC == 512 and exactly MS qkv k-slices.
-template <int NB, int MS>
+//
+// TAB (layer 0 of steps 1..14): q|k|v come from a table row instead of the
+// partial sums, chosen by the code the previous head's argmax candidates
+// give (or the forced code), the table holding layer 0's q|k|v of every code
+// (slice sums, so MS = 1 reads the bits the partials would give); the
+// workgroup then records the code as the skipped q|k|v launch's prologue did
+// and the slice-0 workgroups write the layer's residual input row to x_out.
+template <int NB, int MS, bool TAB = false>
 struct ProPredAttn {
+    static_assert(!TAB || (NB == 1 && MS == 1), "table rows: one row, slice sums");
     static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
     static constexpr int HPW = 2;        // kv heads per workgroup
     static constexpr int NC4 = HPW * PRED_KV_CAP * (HEAD_DIM / 4) / 256;   // cached float4 per thread
@@ -1479,6 +1489,23 @@ struct ProPredAttn {
     const float *rope_cos, *rope_sin;
     int pos0;                // position of row 0
     float *Kc, *Vc;          // this layer's cache [PRED_KV_CAP][8][HEAD_DIM]
+    // TAB only
+    const float *tab;        // [rows][npad] q|k|v of each code
+    int rows;
+    const float2 *cand;      // previous head's argmax candidates
+    int ncand;
+    DevState *st;
+    int slot;
+    uint32_t *codes_api;
+    const float *xtab;       // [rows][xk] the layer's input row of each code
+    float *x_out;
+    int xk;
+
+    __device__ static uint32_t *code_lds()
+    {
+        __shared__ uint32_t code;
+        return &code;
+    }
 
     template <int T, int KC>
     struct Fetch {
@@ -1486,6 +1513,8 @@ struct ProPredAttn {
         uint32_t gq[2], gk[2];
         float cs[NB], sn[NB];
         f32x4 kc[NC4], vc[NC4];
+        uint32_t pred, used;
+        bool nan;
     };
     template <int T, int KC>
     __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
@@ -1503,11 +1532,24 @@ struct ProPredAttn {
         }
         const int qcol = (2 * h0 + wv) * HEAD_DIM + lane;
         const int kvcol = 16 * HEAD_DIM + (wv >> 1) * 8 * HEAD_DIM + (h0 + (wv & 1)) * HEAD_DIM + lane;
+        const float *pbase = part;
+        if constexpr (TAB) {
+            f.nan = false;
+            if (cand) {
+                const int force = st->force;
+                const uint32_t fc = st->fcode[slot];
+                f.pred = cand_argmax(cand, ncand, f.nan);
+                f.used = force ? fc : f.pred;
+            } else {
+                f.pred = f.used = st->used[slot];
+            }
+            pbase = tab + (size_t)min(f.used, (uint32_t)(rows - 1)) * npad;
+        }
 #pragma unroll
         for (int s = 0; s < MS; s++)
 #pragma unroll
             for (int b = 0; b < NB; b++) {
-                const float *pp = part + (s * NB + b) * npad;
+                const float *pp = pbase + (s * NB + b) * npad;
                 f.q[b][s][0] = pp[qcol];
                 f.q[b][s][1] = pp[qcol + 64];
                 f.kv[b][s][0] = pp[kvcol];
@@ -1532,6 +1574,18 @@ struct ProPredAttn {
         const int h0 = k0 / (2 * HEAD_DIM);
         const bool isk = wv < 2;
         const int jn = wv & 1;                       // kv head offset of this wave's k / v vector
+        if constexpr (TAB) {
+            if (t == 0) {
+                *code_lds() = f.used;                // read by finish, after the GEMV's barriers
+                if (cand && k0 == 0 && ctile == 0) {
+                    st->pred[slot] = f.pred;
+                    st->used[slot] = f.used;
+                    st->prev[slot] = f.used;
+                    if (f.nan) st->nan_flag = 1;
+                    if (codes_api) codes_api[slot - 1] = f.pred;
+                }
+            }
+        }
         // cached K / V rows into LDS
 #pragma unroll
         for (int u = 0; u < NC4; u++) {
@@ -1613,7 +1667,16 @@ struct ProPredAttn {
             xs[b * KC + wv * HEAD_DIM + lane + 64] = o1;
         }
     }
-    __device__ void finish(int s, int c, int nct) const {}
+    __device__ void finish(int s, int c, int nct) const
+    {
+        if constexpr (TAB) {
+            if (s != 0 || !x_out) return;
+            const float *row = xtab + (size_t)min(*code_lds(), (uint32_t)(rows - 1)) * xk;
+            const int per = (xk + nct - 1) / nct;
+            const int j0 = c * per, j1 = min(j0 + per, xk);
+            for (int j = j0 + threadIdx.x; j < j1; j += blockDim.x) x_out[j] = row[j];
+        }
+    }
 };
 
 // ---------------------------------------------------------------------------
@@ -2226,10 +2289,21 @@ static ProPredAttn<NB, MS> pred_attn_pro(const PredictorDev &p, const LayerDev &
 
 template <int NB>
 static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s,
-                             const ProCodeRowRms<1024> *row_in = nullptr)
+                             const ProCodeRowRms<1024> *row_in = nullptr, const float *qkv_tab = nullptr)
 {
     const LayerDev &L = p.layers[l];
     const int h = p.hidden;
+    if constexpr (NB == 1) {
+        if (row_in && qkv_tab) {
+            // layer 0's q|k|v read from the table inside the attention prologue
+            float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+            float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+            ProPredAttn<1, 1, true> pro{nullptr, 1, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
+                                        Kc, Vc, qkv_tab, row_in->rows, row_in->cand, row_in->ncand, row_in->st,
+                                        row_in->slot, row_in->codes_api, row_in->table, row_in->x_out, row_in->k};
+            return launch_gemv_then_mlp<1>(p, L, ws, pro, s);
+        }
+    }
     if (NB == 1 && row_in) {
         QCHK(launch_gemv<1>(L.qkv, *row_in, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
     } else {
@@ -2312,7 +2386,9 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
             const ProCodeRowRms<1024> row_in{p.proj_rows + (size_t)(g - 1) * p.emb_rows.rows * p.hidden,
                                              p.emb_rows.rows, cand, p.heads[g - 1].CT, st, g, codes_api,
                                              p.layers[0].input_norm, p.hidden, ws.pxb};
-            QCHK(pred_layer<1>(p, ws, 0, 1 + g, s, &row_in));
+            QCHK(pred_layer<1>(p, ws, 0, 1 + g, s, &row_in,
+                               p.qkv_rows ? p.qkv_rows + (size_t)(g - 1) * p.emb_rows.rows * p.layers[0].qkv.npad
+                                          : nullptr));
             for (int l = 1; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
             QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
             continue;
@@ -2357,6 +2433,31 @@ hipError_t enqueue_pred_row_tables(const PredictorDev &p, int n_tables, float *X
         QCHK(launch_gemv<1>(p.proj, ProPlainY{X, kin, kin}, EpiPartY{part, p.proj.npad, p.proj.S}, s, rows));
         hipLaunchKernelGGL(k_rows_from_parts, dim3((p.hidden + 255) / 256, rows), dim3(256), 0, s, part, p.proj.S,
                            p.proj.npad, p.proj_bias, p.hidden, out + (size_t)g * rows * p.hidden);
+        QCHK(hipGetLastError());
+    }
+    return hipSuccess;
+}
+
+// Layer 0's q|k|v of every row of the projected tables (rows of proj_rows
+// through the input RMSNorm and the q|k|v GEMV, the step's own prologue and
+// GEMV instance, slices summed in slice order as the attention prologue
+// sums them).  Scratch: part [rows][qkv.S][qkv.npad].
+bool pred_qkv_tables_supported(const PredictorDev &p)
+{
+    return p.proj_rows && pred_attn_fusable(p, p.layers[0]) && p.hidden <= 1024;
+}
+
+hipError_t enqueue_pred_qkv_tables(const PredictorDev &p, int n_tables, float *part, float *out, hipStream_t s)
+{
+    if (!pred_qkv_tables_supported(p)) return hipErrorInvalidValue;
+    const LayerDev &L = p.layers[0];
+    const int rows = p.emb_rows.rows;
+    for (int g = 0; g < n_tables; g++) {
+        const ProCodeRowRms<1024> pro{p.proj_rows + (size_t)g * rows * p.hidden, rows, nullptr, 0, nullptr, 0,
+                                      nullptr, L.input_norm, p.hidden, nullptr};
+        QCHK(launch_gemv<1>(L.qkv, pro, EpiPartY{part, L.qkv.npad, L.qkv.S}, s, rows));
+        hipLaunchKernelGGL(k_rows_from_parts, dim3((L.qkv.npad + 255) / 256, rows), dim3(256), 0, s, part, L.qkv.S,
+                           L.qkv.npad, (const float *)nullptr, L.qkv.npad, out + (size_t)g * rows * L.qkv.npad);
         QCHK(hipGetLastError());
     }
     return hipSuccess;

@@ -745,6 +745,7 @@ static int build_pred_rows(qtts_ctx *c)
 {
     PredictorDev &q = c->pm;
     q.proj_rows = nullptr;
+    q.qkv_rows = nullptr;
     const char *env = getenv("QTTS_PRED_ROWS");
     if (q.n_groups < 2 || q.hidden > 1024 || q.emb_rows.n != q.proj.k || (env && env[0] == '0')) return QTTS_OK;
     const int ntab = q.n_groups - 1, rows = q.emb_rows.rows;
@@ -762,6 +763,20 @@ static int build_pred_rows(qtts_ctx *c)
     hipFree(part);
     if (e != hipSuccess) return fail(c, QTTS_ERR_HIP, "predictor row tables: %s", hipGetErrorString(e));
     q.proj_rows = tab;
+    // layer 0's q|k|v of every table row (14 x 2048 x 4096 floats, 470 MB for
+    // the 1.7B predictor); QTTS_PRED_QKV_ROWS=0 keeps the per-step GEMV
+    q.qkv_rows = nullptr;
+    const char *qenv = getenv("QTTS_PRED_QKV_ROWS");
+    if ((qenv && qenv[0] == '0') || !pred_qkv_tables_supported(q)) return QTTS_OK;
+    const LayerDev &L0 = q.layers[0];
+    float *qtab = nullptr;
+    RCHK(dev_alloc(c, c->model_allocs, &qtab, (size_t)ntab * rows * L0.qkv.npad));
+    HIPCHK(c, hipMalloc(&part, (size_t)rows * L0.qkv.S * L0.qkv.npad * sizeof(float)));
+    e = enqueue_pred_qkv_tables(q, ntab, part, qtab, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    hipFree(part);
+    if (e != hipSuccess) return fail(c, QTTS_ERR_HIP, "predictor q|k|v tables: %s", hipGetErrorString(e));
+    q.qkv_rows = qtab;
     return QTTS_OK;
 }
 

@@ -329,36 +329,49 @@ def test_frames_free_running_sampled(loaded):
 
 
 def test_predictor_row_tables_bit_identical(ctx_factory, small_model, monkeypatch):
-    """Layer 0's input of predictor steps 1..14 read from the projected-row
-    tables (built at upload) carries the same bits as the per-step
-    projection GEMV (QTTS_PRED_ROWS=0): chain codes, sampled frames and the
-    final logits/hidden are identical."""
+    """Layer 0 of predictor steps 1..14 from the tables built at upload --
+    the projected embedding rows, and their layer-0 q|k|v read inside the
+    attention prologue -- carries the same bits as the per-step projection
+    and q|k|v GEMVs: contexts with both tables, with the row tables only
+    (QTTS_PRED_QKV_ROWS=0) and with neither (QTTS_PRED_ROWS=0) give identical
+    chain codes, free-running and teacher-forced frames, and final
+    logits/hidden."""
     t, p = small_model
-    a = ctx_factory(256)
-    a.upload_model(t, p)
-    monkeypatch.setenv("QTTS_PRED_ROWS", "0")
-    b = ctx_factory(256)
-    b.upload_model(t, p)
+    ctxs = []
+    for env in ({}, {"QTTS_PRED_QKV_ROWS": "0"}, {"QTTS_PRED_ROWS": "0"}):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        c = ctx_factory(256)
+        c.upload_model(t, p)
+        ctxs.append(c)
+        for k in env:
+            monkeypatch.delenv(k)
     rng = np.random.Generator(np.random.PCG64(81))
     for _ in range(3):
         th = rng.standard_normal(t.hidden).astype(np.float32)
-        sem = a.embed_codec_token(int(rng.integers(0, 3072)))
-        assert np.array_equal(a.generate_acoustic_codes(th, sem), b.generate_acoustic_codes(th, sem))
+        sem = ctxs[0].embed_codec_token(int(rng.integers(0, 3072)))
+        ref = ctxs[2].generate_acoustic_codes(th, sem)
+        for c in ctxs[:2]:
+            assert np.array_equal(c.generate_acoustic_codes(th, sem), ref)
     X = rng.standard_normal((16, t.hidden)).astype(np.float32)
     params = qtts.sample_params(eos_enabled=False)
     outs = []
-    for c in (a, b):
+    for c in ctxs:
         h = c.prefill_talker_raw_from(X, 0)
         c.gen_set_text(None, c.embed_text_token(3))
         c.gen_begin(c.apply_codec_head(h), h, 16, 42, params)
         codes, _ = c.gen_frames(24)
         lg, hd, pos, rng_state = c.gen_state()
-        outs.append((codes, lg, hd, pos, rng_state))
-    assert np.array_equal(outs[0][0], outs[1][0])
-    assert np.array_equal(bits(outs[0][1]), bits(outs[1][1])) and np.array_equal(bits(outs[0][2]), bits(outs[1][2]))
-    assert outs[0][3:] == outs[1][3:]
-    a.close()
-    b.close()
+        c.kv_truncate(16)
+        c.gen_begin(c.apply_codec_head(h), h, 16, 42, params)
+        forced = c.gen_frames_forced(codes[::-1].copy())
+        outs.append((codes, forced, lg, hd, pos, rng_state))
+    for o in outs[:2]:
+        assert np.array_equal(o[0], outs[2][0]) and np.array_equal(o[1], outs[2][1])
+        assert np.array_equal(bits(o[2]), bits(outs[2][2])) and np.array_equal(bits(o[3]), bits(outs[2][3]))
+        assert o[4:] == outs[2][4:]
+    for c in ctxs:
+        c.close()
 
 
 @pytest.mark.parametrize("tiles", [{"TGU": "14", "PGU": "16"}, {"TGU": "11", "PGU": "12", "PO": "11"},
