@@ -407,6 +407,37 @@ int qtts_sample_token(qtts_ctx *ctx, const float *logits, int64_t n,
                       int64_t n_prev, uint64_t *rng, float temperature,
                       uint32_t *out);
 
+/* ---- legacy loop (generate.rs:107-250) -------------------------------- */
+
+/* `prefill_talker` (talker.rs:487-508): each id embedded as a text token
+ * (is_text != 0: the text projection) or a codec token, then
+ * prefill_talker_raw over a fresh cache (positions 0..n-1).  hidden_out
+ * gets the final-normed hidden of the last row. */
+int qtts_prefill_tokens(qtts_ctx *ctx, const uint32_t *ids, const uint8_t *is_text,
+                        int64_t n, float *hidden_out, int flags);
+
+/* `predict_codes` (code_predictor.rs:126-216): the legacy, non-autoregressive
+ * predictor step -- project the talker hidden, run the predictor's layers
+ * over a cache kept across calls (the new row sits at the cache length),
+ * final norm, then every lm head: logits [n_groups][vocab].
+ * qtts_predict_codes_reset empties that cache (a new utterance; the
+ * reference allocates a fresh one, generate.rs:129). */
+int qtts_predict_codes(qtts_ctx *ctx, const float *talker_hidden, float *logits,
+                       int flags);
+int qtts_predict_codes_reset(qtts_ctx *ctx);
+
+/* The legacy loop's sampler (generate.rs:185-217): apply_repetition_penalty
+ * over the n_prev previous tokens when repetition_penalty > 1
+ * (generate.rs:87-98), then sample_top_k (generate.rs:50-84): temperature
+ * <= 0 takes the last maximum; otherwise the top_k logits in descending
+ * order, exp((l - max) / T) normalised, one `simple_rand` draw.  Equal
+ * logits keep index order (the reference's unstable sort leaves it open).
+ * QTTS_ERR_INVALID for top_k < 1 with temperature > 0, QTTS_ERR_NAN for a
+ * NaN logit.  Host buffers; n <= 4096. */
+int qtts_sample_top_k(qtts_ctx *ctx, const float *logits, int64_t n, float temperature,
+                      int32_t top_k, const uint32_t *prev, int64_t n_prev,
+                      float repetition_penalty, uint64_t *rng, uint32_t *out);
+
 /* ---- frame loop (generate_new.rs:606-675) ----------------------------- */
 
 /* Start a generation: the prefill's logits [vocab] and final-normed hidden

@@ -69,6 +69,9 @@ _SIG = {
     "oq_argmax_last": ([c_void_p, c_int64], c_uint32),
     "oq_sample_token": ([c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64, POINTER(c_uint64), c_float,
                          POINTER(c_uint32)], c_int),
+    "oq_predict_codes": ([POINTER(PredictorHost), c_void_p, POINTER(OqKv), c_void_p], c_int),
+    "oq_sample_top_k": ([c_void_p, c_int64, c_float, c_int64, c_void_p, c_int64, c_float, POINTER(c_uint64),
+                         POINTER(c_uint32)], c_int),
     "oq_frame": ([POINTER(TalkerHost), POINTER(PredictorHost), POINTER(OqKv), POINTER(OqKv), POINTER(OqGen),
                   POINTER(SampleParams), c_void_p, c_void_p, POINTER(c_int32), c_void_p], c_int),
     "od_set_threads": ([c_int], None),
@@ -231,6 +234,20 @@ def sample_token(logits, params, prev, rng, temperature):
     return out.value, s.value
 
 
+def sample_top_k(logits, temperature, top_k, prev, penalty, rng):
+    """The legacy loop's sampler (generate.rs:185-217): (token, rng) or
+    raises with the status (QTTS_ERR_INVALID for top_k 0, _NAN)."""
+    lg = f32(logits)
+    pv = np.ascontiguousarray(prev, dtype=np.uint32)
+    s = c_uint64(rng)
+    out = c_uint32()
+    rc = lib().oq_sample_top_k(ptr(lg), lg.size, temperature, top_k, ptr(pv) if pv.size else None, pv.size, penalty,
+                               byref(s), byref(out))
+    if rc != 0:
+        raise RuntimeError(f"oracle sample_top_k rc={rc}")
+    return out.value, s.value
+
+
 # ---------------------------------------------------------------------------
 # model-level oracle
 # ---------------------------------------------------------------------------
@@ -244,12 +261,15 @@ class Model:
         self.ph, self._kp = hostdesc.predictor_host(predictor)
         self.tkv = lib().oq_kv_new(len(talker.layers), talker.n_kv_heads, talker.head_dim, kv_cap)
         self.pkv = lib().oq_kv_new(len(predictor.layers), predictor.n_kv_heads, predictor.head_dim, 16)
+        # the legacy predictor's cache, kept across predict_codes calls
+        self.lkv = lib().oq_kv_new(len(predictor.layers), predictor.n_kv_heads, predictor.head_dim, kv_cap)
 
     def close(self):
         if self.tkv:
             lib().oq_kv_free(self.tkv)
             lib().oq_kv_free(self.pkv)
-            self.tkv = self.pkv = None
+            lib().oq_kv_free(self.lkv)
+            self.tkv = self.pkv = self.lkv = None
 
     def __del__(self):
         try:
@@ -319,6 +339,17 @@ class Model:
         if rc:
             raise RuntimeError(f"oracle predictor rc={rc}")
         return codes
+
+    def predict_codes(self, th):
+        """predict_codes (code_predictor.rs:126-216): logits [n_groups][vocab]."""
+        out = np.empty((len(self.p.lm_heads), self.p.vocab), np.float32)
+        rc = lib().oq_predict_codes(byref(self.ph), ptr(f32(th)), self.lkv, ptr(out))
+        if rc:
+            raise RuntimeError(f"oracle predict_codes rc={rc}")
+        return out
+
+    def predict_codes_reset(self):
+        lib().oq_kv_reset(self.lkv)
 
     def acoustic_embed_sum(self, codes):
         c = np.ascontiguousarray(codes, dtype=np.uint32)

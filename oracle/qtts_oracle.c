@@ -813,6 +813,28 @@ int oq_predictor_chain(const qtts_predictor_host *p, const float *th,
     return rc;
 }
 
+/* predict_codes (code_predictor.rs:126-216), the legacy loop's predictor
+ * (generate.rs:210-213): project the talker hidden, run the layers over a
+ * cache that persists across calls (the position of the new row is the
+ * cache length, RoPE at that offset), final norm, then every lm head:
+ * logits [n_groups][vocab]. */
+int oq_predict_codes(const qtts_predictor_host *p, const float *th, oq_kv *kv, float *logits)
+{
+    const int64_t h = p->hidden;
+    layer_dims d = pred_dims(p);
+    if (kv->len[0] >= kv->cap) return QTTS_ERR_CAPACITY;
+    float *x = (float *)malloc(h * sizeof(float));
+    float *hid = (float *)malloc(h * sizeof(float));
+    project_input(p, th, x);                           /* :135 */
+    for (int32_t l = 0; l < p->n_layers; l++)          /* :137-199 */
+        layer_decode(&d, &p->layers[l], x, kv, l, kv->len[l]);
+    oq_rms_norm_f16(x, p->final_norm, h, hid);         /* :202 */
+    for (int32_t g = 0; g < p->n_groups; g++)          /* :205-208 */
+        oq_gemv_q4(hid, &p->lm_heads[g], logits + (size_t)g * p->vocab);
+    free(x); free(hid);
+    return QTTS_OK;
+}
+
 /* get_acoustic_embeddings_sum (code_predictor.rs:287-300). */
 void oq_acoustic_embed_sum(const qtts_predictor_host *p, const uint32_t *codes,
                            int32_t n, float *out)
@@ -921,6 +943,60 @@ int oq_sample_token(const float *logits, int64_t n,
         if (rr < cs) { res = (uint32_t)i; break; }
     }
     free(s);
+    *out = res;
+    return QTTS_OK;
+}
+
+/* The legacy loop's sampler (generate.rs:185-217): apply_repetition_penalty
+ * (generate.rs:87-98) over every previous token when penalty > 1, then
+ * sample_top_k (generate.rs:50-84): temperature <= 0 -> the last maximum
+ * (max_by); else the top_k logits in descending order, probabilities
+ * exp((l - max) / T) normalised by their sequential sum, and the first
+ * index whose running sum passes simple_rand.  The reference orders equal
+ * logits with an unstable sort; here ties keep index order.  top_k 0 (a
+ * panic in the reference) is QTTS_ERR_INVALID, a NaN QTTS_ERR_NAN. */
+int oq_sample_top_k(const float *logits, int64_t n, float temperature, int64_t top_k,
+                    const uint32_t *prev, int64_t n_prev, float penalty, uint64_t *rng,
+                    uint32_t *out)
+{
+    if (n < 1) return QTTS_ERR_INVALID;
+    float *s = (float *)malloc((size_t)n * sizeof(float));
+    memcpy(s, logits, (size_t)n * sizeof(float));
+    if (penalty > 1.0f) {
+        for (int64_t i = 0; i < n_prev; i++) {
+            const uint32_t t = prev[i];
+            if ((int64_t)t < n) {
+                if (s[t] > 0.0f) s[t] /= penalty;
+                else s[t] *= penalty;
+            }
+        }
+    }
+    if (any_nan(s, n)) { free(s); return QTTS_ERR_NAN; }
+    if (temperature <= 0.0f) {
+        *out = oq_argmax_last(s, n);
+        free(s);
+        return QTTS_OK;
+    }
+    const int64_t k = top_k < n ? top_k : n;
+    if (k < 1) { free(s); return QTTS_ERR_INVALID; }
+    ranked *r = (ranked *)malloc((size_t)n * sizeof(ranked));
+    ranked *tmp = (ranked *)malloc((size_t)n * sizeof(ranked));
+    for (int64_t i = 0; i < n; i++) { r[i].i = i; r[i].p = s[i]; }
+    sort_desc_stable(r, n, tmp);
+    float *pr = (float *)malloc((size_t)k * sizeof(float));
+    const float mx = r[0].p;
+    for (int64_t i = 0; i < k; i++) pr[i] = expf((r[i].p - mx) / temperature);
+    float sum = 0.0f;
+    for (int64_t i = 0; i < k; i++) sum += pr[i];
+    for (int64_t i = 0; i < k; i++) pr[i] /= sum;
+    const float rr = oq_simple_rand(rng);
+    float cs = 0.0f;
+    uint32_t res = (uint32_t)r[k - 1].i;
+    for (int64_t i = 0; i < k; i++) {
+        cs += pr[i];
+        if (rr < cs) { res = (uint32_t)r[i].i; break; }
+    }
+    free(s); free(r); free(tmp); free(pr);
     *out = res;
     return QTTS_OK;
 }

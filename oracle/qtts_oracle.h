@@ -120,6 +120,10 @@ uint32_t oq_argmax_last(const float *v, int64_t n); /* code_predictor.rs:335 */
 /* -- sampler ------------------------------------------------------------- */
 /* generate_new.rs:771-862.  Returns QTTS_ERR_NAN where Rust would panic
  * (partial_cmp().unwrap() on NaN). */
+int  oq_predict_codes(const qtts_predictor_host *p, const float *th, oq_kv *kv, float *logits);
+int oq_sample_top_k(const float *logits, int64_t n, float temperature, int64_t top_k,
+                    const uint32_t *prev, int64_t n_prev, float penalty, uint64_t *rng,
+                    uint32_t *out);
 int oq_sample_token(const float *logits, int64_t n,
                     const qtts_sample_params *p, const uint32_t *prev,
                     int64_t n_prev, uint64_t *rng, float temperature,

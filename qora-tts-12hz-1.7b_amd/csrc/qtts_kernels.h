@@ -183,6 +183,8 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
                                    const uint32_t *forced, uint32_t *codes_api, hipStream_t s);
 hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
                          const uint32_t *forced, hipStream_t s);
+hipError_t enqueue_sample_top_k(const float *logits, int n, float temperature, int top_k, const uint32_t *prev,
+                                int n_prev, float penalty, uint64_t *rng, uint32_t *out, int *status, hipStream_t s);
 hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &a, uint64_t *rng_dev,
                               uint32_t *out_dev, DevState *st, hipStream_t s);
 hipError_t enqueue_kv_gather(const KvPaged &kv, int layer, int len, float *K, float *V, hipStream_t s);

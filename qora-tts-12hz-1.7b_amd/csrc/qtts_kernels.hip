@@ -2482,6 +2482,130 @@ hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Worksp
     return enqueue_talker_step(m, ws, st, 1, s);
 }
 
+// The legacy loop's sampler (generate.rs:185-217): apply_repetition_penalty
+// (generate.rs:87-98, every previous token in order, when penalty > 1), then
+// sample_top_k (generate.rs:50-84).  One workgroup: temperature <= 0 takes
+// the last maximum; otherwise a bitonic sort of (logit desc, index asc) in
+// LDS (the reference's unstable sort leaves the order of equal logits
+// open), then thread 0 forms exp((l - max) / T) over the top k, their
+// sequential sum, the normalised running sum and the draw.  status: 0,
+// -1 (top_k < 1: the reference indexes an empty list), -7 (NaN).
+constexpr int LEG_N = 4096;
+
+__global__ void __launch_bounds__(1024)
+k_sample_top_k(const float *logits, int n, float temperature, int top_k, const uint32_t *prev, int n_prev,
+               float penalty, uint64_t *rng, uint32_t *out, int *status)
+{
+    __shared__ float v[LEG_N];
+    __shared__ int ix[LEG_N];
+    __shared__ int nanf;
+    __shared__ float bv[32];
+    __shared__ int bi[32];
+    const int t = threadIdx.x;
+    if (t == 0) nanf = 0;
+    for (int i = t; i < LEG_N; i += 1024) {
+        v[i] = i < n ? logits[i] : -INFINITY;
+        ix[i] = i;
+    }
+    __syncthreads();
+    if (t == 0 && penalty > 1.0f) {
+        for (int i = 0; i < n_prev; i++) {
+            const uint32_t tok = prev[i];
+            if (tok < (uint32_t)n) {
+                const float x = v[tok];
+                v[tok] = x > 0.0f ? x / penalty : x * penalty;
+            }
+        }
+    }
+    __syncthreads();
+    bool mynan = false;
+    for (int i = t; i < n; i += 1024) mynan |= isnan(v[i]);
+    if (mynan) nanf = 1;
+    __syncthreads();
+    if (nanf) {
+        if (t == 0) *status = -7;
+        return;
+    }
+    if (temperature <= 0.0f) {
+        // max_by: the last index among equal maxima
+        float best = -INFINITY;
+        int bidx = -1;
+        for (int i = t; i < n; i += 1024)
+            if (bidx < 0 || !(best > v[i])) { best = v[i]; bidx = i; }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int oi = __shfl_xor(bidx, o);
+            if (oi >= 0 && (bidx < 0 || ov > best || (ov == best && oi > bidx))) { best = ov; bidx = oi; }
+        }
+        if ((t & 63) == 0) { bv[t >> 6] = best; bi[t >> 6] = bidx; }
+        __syncthreads();
+        if (t == 0) {
+            float b = bv[0];
+            int j = bi[0];
+            for (int w = 1; w < 16; w++)
+                if (bi[w] >= 0 && (j < 0 || bv[w] > b || (bv[w] == b && bi[w] > j))) { b = bv[w]; j = bi[w]; }
+            *out = (uint32_t)j;
+            *status = 0;
+        }
+        return;
+    }
+    // bitonic sort of all LEG_N slots into (value desc, index asc)
+    for (int size = 2; size <= LEG_N; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = t; i < LEG_N; i += 1024) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const float a = v[i], b = v[j];
+                    const int ia = ix[i], ib = ix[j];
+                    const bool a_first = a > b || (a == b && ia < ib);
+                    const bool up = (i & size) == 0;
+                    if (up != a_first) {
+                        v[i] = b; v[j] = a;
+                        ix[i] = ib; ix[j] = ia;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (t == 0) {
+        const int k = top_k < n ? top_k : n;
+        if (k < 1) {
+            *status = -1;
+            return;
+        }
+        // probabilities over the top k reuse the sorted values' slots
+        const float mx = v[0];
+        for (int i = 0; i < k; i++) v[i] = expf((v[i] - mx) / temperature);
+        float sum = 0.0f;
+        for (int i = 0; i < k; i++) sum += v[i];
+        for (int i = 0; i < k; i++) v[i] /= sum;
+        uint64_t rs = *rng;
+        const float r = simple_rand_dev(rs);
+        *rng = rs;
+        float cs = 0.0f;
+        int res = ix[k - 1];
+        for (int i = 0; i < k; i++) {
+            cs += v[i];
+            if (r < cs) {
+                res = ix[i];
+                break;
+            }
+        }
+        *out = (uint32_t)res;
+        *status = 0;
+    }
+}
+
+hipError_t enqueue_sample_top_k(const float *logits, int n, float temperature, int top_k, const uint32_t *prev,
+                                int n_prev, float penalty, uint64_t *rng, uint32_t *out, int *status, hipStream_t s)
+{
+    if (n < 1 || n > LEG_N) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_sample_top_k, dim3(1), dim3(1024), 0, s, logits, n, temperature, top_k, prev, n_prev,
+                       penalty, rng, out, status);
+    return hipGetLastError();
+}
+
 hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &a, uint64_t *rng_dev,
                               uint32_t *out_dev, DevState *st, hipStream_t s)
 {

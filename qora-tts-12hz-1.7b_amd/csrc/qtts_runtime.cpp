@@ -50,6 +50,14 @@ struct qtts_ctx {
     uint32_t *d_codes_api = nullptr;                 // [16]
     uint64_t *d_rng_api = nullptr;
     uint32_t *d_prev_api = nullptr;                  // [4096]
+
+    // legacy loop (generate.rs): the predictor's cache kept across
+    // predict_codes calls, and small device buffers
+    float *lkv = nullptr;                            // model allocation: [layers][pages][2][8][64][128]
+    int32_t *lkv_ptab = nullptr;                     // identity page table
+    float *leg_buf = nullptr;                        // side row + logits
+    int *d_status = nullptr;
+    int64_t lkv_len = 0;
     float *d_io = nullptr;                           // API staging, 2 rows of max(hidden,vocab,4096)
     float *d_io2 = nullptr;
     int64_t io_floats = 0;
@@ -400,7 +408,8 @@ extern "C" int qtts_ctx_create(int device, int64_t kv_capacity, qtts_ctx **out)
               hipHostMalloc(&c->h_ring, sizeof(uint32_t) * RING_FRAMES * 16 * 2, hipHostMallocDefault) == hipSuccess &&
               hipMalloc(&c->d_codes_api, sizeof(uint32_t) * 16) == hipSuccess &&
               hipMalloc(&c->d_rng_api, sizeof(uint64_t)) == hipSuccess &&
-              hipMalloc(&c->d_prev_api, sizeof(uint32_t) * 4096) == hipSuccess;
+              hipMalloc(&c->d_prev_api, sizeof(uint32_t) * 4096) == hipSuccess &&
+              hipMalloc(&c->d_status, sizeof(int) * 2) == hipSuccess;
     if (!ok) {
         qtts_ctx_destroy(c);
         return QTTS_ERR_OOM;
@@ -416,6 +425,9 @@ static void free_model(qtts_ctx *c)
 {
     drop_graph(c);
     free_list(c->model_allocs);
+    c->lkv = c->leg_buf = nullptr;                   // were model allocations
+    c->lkv_ptab = nullptr;
+    c->lkv_len = 0;
     free_list(c->ws_allocs);
     if (c->pf_mem) hipFree(c->pf_mem);   // sized for the model's hidden / inter
     c->pf_mem = nullptr;
@@ -443,6 +455,7 @@ extern "C" void qtts_ctx_destroy(qtts_ctx *c)
     if (c->h_ring) hipHostFree(c->h_ring);
     if (c->d_codes_api) hipFree(c->d_codes_api);
     if (c->d_rng_api) hipFree(c->d_rng_api);
+    if (c->d_status) hipFree(c->d_status);
     if (c->d_prev_api) hipFree(c->d_prev_api);
     if (c->stream) hipStreamDestroy(c->stream);
     delete c;
@@ -1713,6 +1726,153 @@ extern "C" int qtts_sample_token(qtts_ctx *c, const float *logits, int64_t n, co
     HIPCHK(c, hipMemcpyAsync(out, c->d_codes_api, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (back.nan_flag) return fail(c, QTTS_ERR_NAN, "NaN in sampler input");
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// legacy loop (generate.rs:107-250)
+// ---------------------------------------------------------------------------
+
+extern "C" int qtts_sample_top_k(qtts_ctx *c, const float *logits, int64_t n, float temperature, int32_t top_k,
+                                 const uint32_t *prev, int64_t n_prev, float repetition_penalty, uint64_t *rng,
+                                 uint32_t *out)
+{
+    if (!c || !logits || !rng || !out || n <= 0 || n_prev < 0 || (n_prev > 0 && !prev)) return QTTS_ERR_INVALID;
+    if (n > 4096) return fail(c, QTTS_ERR_UNSUPPORTED, "sampler supports n <= 4096");
+    hipSetDevice(c->device);
+    RCHK(ensure_io(c, std::max<int64_t>(8192, n_prev)));
+    HIPCHK(c, hipMemcpyAsync(c->d_io, logits, n * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    uint32_t *d_prev = (uint32_t *)c->d_io2;
+    if (n_prev) HIPCHK(c, hipMemcpyAsync(d_prev, prev, n_prev * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(c->d_rng_api, rng, sizeof(uint64_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, enqueue_sample_top_k(c->d_io, (int)n, temperature, top_k, d_prev, (int)n_prev, repetition_penalty,
+                                   c->d_rng_api, c->d_codes_api, c->d_status, c->stream));
+    int status = 0;
+    HIPCHK(c, hipMemcpyAsync(&status, c->d_status, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(rng, c->d_rng_api, sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipMemcpyAsync(out, c->d_codes_api, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (status == -7) return fail(c, QTTS_ERR_NAN, "NaN in sampler input");
+    if (status == -1) return fail(c, QTTS_ERR_INVALID, "top_k must be at least 1 when temperature > 0");
+    return QTTS_OK;
+}
+
+// The legacy predictor's cache: the talker step's paged layout for the
+// predictor's layers, pages in identity order (no prefix sharing here).
+static int ensure_legacy(qtts_ctx *c)
+{
+    if (c->lkv) return QTTS_OK;
+    const PredictorDev &p = c->pm;
+    const int n_pages = (int)(c->kv_cap / KV_PAGE);
+    float *kv = nullptr, *buf = nullptr;
+    RCHK(dev_alloc(c, c->model_allocs, &kv, (size_t)p.n_layers * n_pages * 2 * 8 * KV_PAGE * HEAD_DIM));
+    RCHK(dev_alloc(c, c->model_allocs, &buf, (size_t)p.hidden + (size_t)p.n_groups * p.vocab));
+    std::vector<int32_t> id(MAX_CHUNKS);
+    for (int i = 0; i < MAX_CHUNKS; i++) id[i] = i;
+    const int32_t *pt = nullptr;
+    RCHK(upload_vec(c, c->model_allocs, id.data(), id.size(), &pt));
+    c->lkv = kv;
+    c->leg_buf = buf;
+    c->lkv_ptab = const_cast<int32_t *>(pt);
+    c->lkv_len = 0;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_predict_codes_reset(qtts_ctx *c)
+{
+    NEED_MODEL(c);
+    c->lkv_len = 0;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_predict_codes(qtts_ctx *c, const float *talker_hidden, float *logits, int flags)
+{
+    NEED_MODEL(c);
+    if (!talker_hidden || !logits) return QTTS_ERR_INVALID;
+    hipSetDevice(c->device);
+    RCHK(ensure_legacy(c));
+    const TalkerDev &m = c->tm;
+    const PredictorDev &p = c->pm;
+    const int64_t pos = c->lkv_len;
+    if (pos >= c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "legacy predictor cache full (%lld)", (long long)pos);
+    if (pos >= p.rope_rows) return fail(c, QTTS_ERR_CAPACITY, "position beyond the predictor's RoPE table");
+    // project_input (code_predictor.rs:135) into the step input row
+    RCHK(ensure_io(c, m.hidden));
+    RCHK(stage_in(c, talker_hidden, m.hidden, c->d_io, flags));
+    HIPCHK(c, enqueue_gemv_store(p.proj, c->d_io, c->ws.x, p.proj_bias, c->ws.part_proj, c->stream));
+    // the layers through the talker step's kernels: a view of the predictor
+    TalkerDev v = m;
+    v.n_layers = p.n_layers;
+    v.hidden = p.hidden;
+    v.inter = p.inter;
+    v.vocab = p.vocab;
+    v.layers = p.layers;
+    v.final_norm = p.final_norm;
+    v.rope_cos = p.rope_cos;
+    v.rope_sin = p.rope_sin;
+    v.rope_rows = p.rope_rows;
+    v.kv = KvPaged{c->lkv, c->lkv_ptab, (int32_t)(c->kv_cap / KV_PAGE)};
+    HIPCHK(c, enqueue_talker_row(v, c->ws, c->st_gen, pos, (int)pos, c->stream));
+    // final norm (code_predictor.rs:202) into `side`, then every head
+    float *side = c->leg_buf, *out = c->leg_buf + p.hidden;
+    v.codec_head = p.heads[0];
+    HIPCHK(c, enqueue_final_norm(v, c->ws, side, c->stream));
+    for (int g = 0; g < p.n_groups; g++) {
+        v.codec_head = p.heads[g];
+        HIPCHK(c, enqueue_codec_head(v, c->ws, side, out + (size_t)g * p.vocab, c->stream));
+    }
+    RCHK(stage_out(c, out, (int64_t)p.n_groups * p.vocab, logits, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    c->lkv_len = pos + 1;
+    return QTTS_OK;
+}
+
+extern "C" int qtts_prefill_tokens(qtts_ctx *c, const uint32_t *ids, const uint8_t *is_text, int64_t n,
+                                   float *hidden_out, int flags)
+{
+    NEED_MODEL(c);
+    if (!ids || !is_text || n < 1 || !hidden_out) return QTTS_ERR_INVALID;
+    const TalkerDev &m = c->tm;
+    std::vector<uint32_t> tid, cid;
+    std::vector<int64_t> tpos, cpos;
+    for (int64_t i = 0; i < n; i++) {
+        if (is_text[i]) {
+            if ((int64_t)ids[i] >= m.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", ids[i]);
+            tid.push_back(ids[i]);
+            tpos.push_back(i);
+        } else {
+            if ((int64_t)ids[i] >= m.codec_rows.rows) return fail(c, QTTS_ERR_INVALID, "codec token %u out of range", ids[i]);
+            cid.push_back(ids[i]);
+            cpos.push_back(i);
+        }
+    }
+    hipSetDevice(c->device);
+    const int H = m.hidden;
+    const int64_t nt = (int64_t)tid.size(), nc = (int64_t)cid.size();
+    DevScratch buf;
+    const size_t rows_f = (size_t)(n + nt + nc + 1) * H, scr_f = (size_t)nt * (m.text_hidden + m.text_fc1.n);
+    HIPCHK(c, hipMalloc(&buf.p, (rows_f + scr_f) * sizeof(float) + (size_t)n * sizeof(uint32_t)));
+    float *X = (float *)buf.p, *trows = X + (size_t)n * H, *crows = trows + (size_t)nt * H;
+    float *hid = crows + (size_t)nc * H, *scratch = hid + H;
+    uint32_t *d_tid = (uint32_t *)(scratch + scr_f), *d_cid = d_tid + nt;
+    // embed_text_token / embed_codec_token per position (talker.rs:497-504)
+    if (nt) {
+        HIPCHK(c, hipMemcpyAsync(d_tid, tid.data(), nt * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+        RCHK(text_rows(c, d_tid, (int)nt, trows, scratch));
+    }
+    if (nc) {
+        HIPCHK(c, hipMemcpyAsync(d_cid, cid.data(), nc * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_cid, (int)nc, crows, H, c->stream));
+    }
+    for (int64_t i = 0; i < nt; i++)
+        HIPCHK(c, hipMemcpyAsync(X + tpos[i] * H, trows + i * H, H * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    for (int64_t i = 0; i < nc; i++)
+        HIPCHK(c, hipMemcpyAsync(X + cpos[i] * H, crows + i * H, H * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    // prefill_talker_raw over a fresh cache (talker.rs:506-507)
+    RCHK(qtts_kv_reset(c));
+    RCHK(qtts_talker_prefill(c, X, n, 0, hid, flags | QTTS_DEVICE_PTRS));
+    RCHK(stage_out(c, hid, H, hidden_out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
     return QTTS_OK;
 }
 

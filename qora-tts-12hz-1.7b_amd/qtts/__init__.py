@@ -82,6 +82,11 @@ SIGNATURES = {
     "qtts_acoustic_embed_sum": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_sample_token": ([c_void_p, c_void_p, c_int64, POINTER(SampleParams), c_void_p, c_int64,
                            POINTER(c_uint64), c_float, POINTER(c_uint32)], c_int),
+    "qtts_prefill_tokens": ([c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_predict_codes": ([c_void_p, c_void_p, c_void_p, c_int], c_int),
+    "qtts_predict_codes_reset": ([c_void_p], c_int),
+    "qtts_sample_top_k": ([c_void_p, c_void_p, c_int64, c_float, c_int32, c_void_p, c_int64, c_float,
+                           POINTER(c_uint64), POINTER(c_uint32)], c_int),
     "qtts_gen_begin": ([c_void_p, c_void_p, c_void_p, c_int64, c_uint64, POINTER(SampleParams)], c_int),
     "qtts_gen_set_text": ([c_void_p, c_void_p, c_int64, c_void_p], c_int),
     "qtts_gen_frames": ([c_void_p, c_int64, c_void_p, POINTER(c_int64), POINTER(c_int32)], c_int),
@@ -351,6 +356,34 @@ class Context:
         self._check(self.lib.qtts_decode_to_audio(self.h, ptr(c), c.shape[1], ptr(w) if nw else None, nw, ptr(out),
                                                   out.size, ctypes.byref(n), 0))
         return out[:n.value]
+
+    # ---- legacy loop (generate.rs) ----------------------------------------------
+    def prefill_tokens(self, ids, is_text):
+        """prefill_talker (talker.rs:487-508) over a fresh cache."""
+        ids = np.ascontiguousarray(ids, np.uint32).reshape(-1)
+        it = np.ascontiguousarray(is_text, np.uint8).reshape(-1)
+        out = np.empty(self.hidden, np.float32)
+        self._check(self.lib.qtts_prefill_tokens(self.h, ptr(ids), ptr(it), ids.size, ptr(out), 0))
+        return out
+
+    def predict_codes(self, talker_hidden):
+        """predict_codes (code_predictor.rs:126-216): [n_groups][vocab] logits."""
+        th = _f32(talker_hidden, self.hidden)
+        out = np.empty((self.n_groups, self.p_vocab), np.float32)
+        self._check(self.lib.qtts_predict_codes(self.h, ptr(th), ptr(out), 0))
+        return out
+
+    def predict_codes_reset(self):
+        self._check(self.lib.qtts_predict_codes_reset(self.h))
+
+    def sample_top_k(self, logits, temperature, top_k, prev, penalty, rng):
+        """The legacy sampler (generate.rs:185-217): (token, rng)."""
+        lg = _f32(logits)
+        pv = np.ascontiguousarray(prev, np.uint32).reshape(-1)
+        s, out = c_uint64(rng), c_uint32()
+        self._check(self.lib.qtts_sample_top_k(self.h, ptr(lg), lg.size, temperature, top_k, ptr(pv) if pv.size else None,
+                                               pv.size, penalty, byref(s), byref(out)))
+        return out.value, s.value
 
     def generate_acoustic_codes(self, talker_hidden, semantic_embed):
         th = _f32(talker_hidden, self.hidden)

@@ -182,5 +182,17 @@ class Predictor64:
             out.append(h @ self.heads[g])
         return out
 
+    def predict_logits(self, talker_hiddens):
+        """predict_codes (code_predictor.rs:126-216) over successive calls:
+        call t projects hidden t, runs the layers at position t against the
+        cache the earlier calls left, and returns every head's logits."""
+        K = [[] for _ in self.layers]
+        V = [[] for _ in self.layers]
+        out = []
+        for t, th in enumerate(talker_hiddens):
+            h = self._hidden(self.project(th), t, K, V)
+            out.append([h @ w for w in self.heads])
+        return out
+
     def embed_sum(self, codes):
         return sum(row(self.p.codec_embeddings[g], int(c)) for g, c in enumerate(codes))

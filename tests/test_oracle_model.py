@@ -110,6 +110,64 @@ def test_predictor_chain_teacher_forced(models):
             assert _consistent_argmax(int(codes_f[g]), logits_f[g]), f"forced trial {trial} group {g}"
 
 
+def test_predict_codes_legacy(models):
+    """predict_codes (code_predictor.rs:126-216): four successive calls, the
+    cache carried from call to call (RoPE at the cache length), all 15
+    heads' logits against the float64 model; a reset starts over."""
+    t, p, om, ft, fp = models
+    rng = np.random.Generator(np.random.PCG64(41))
+    hs = [rng.standard_normal(512).astype(np.float32) for _ in range(4)]
+    om.predict_codes_reset()
+    got = [om.predict_codes(h) for h in hs]
+    ref = fp.predict_logits(hs)
+    for i in range(4):
+        for g in range(15):
+            assert rel_err(got[i][g], ref[i][g]) <= REL, f"call {i} head {g}"
+    # the first call's logits depend on position 0 only: after a reset, equal
+    om.predict_codes_reset()
+    assert np.array_equal(om.predict_codes(hs[0]), got[0])
+    om.predict_codes_reset()
+
+
+def test_sample_top_k_legacy_known_answers():
+    """sample_top_k and apply_repetition_penalty (generate.rs:50-98): the
+    answers the definitions fix."""
+    # temperature <= 0: the last of equal maxima (max_by), one draw not taken
+    assert O.sample_top_k([1.0, 3.0, 3.0, 2.0], 0.0, 50, [], 1.0, 7) == (2, 7)
+    # top_k 1: the maximum whatever the draw; the generator advances once
+    tok, rng = O.sample_top_k([0.5, 4.0, 1.0], 0.9, 1, [], 1.0, 7)
+    assert tok == 1 and rng == O.simple_rand(7)[1]
+    # penalty > 1 divides a positive logit, multiplies a negative one, once per
+    # occurrence; penalty <= 1 is not applied (generate.rs:188-190)
+    assert O.sample_top_k([2.0, 1.5], 0.0, 2, [0], 2.0, 1)[0] == 1
+    assert O.sample_top_k([2.0, 1.7], 0.0, 2, [0], 1.1, 1)[0] == 0
+    assert O.sample_top_k([2.0, 1.7], 0.0, 2, [0, 0], 1.1, 1)[0] == 1
+    assert O.sample_top_k([-1.0, -1.5], 0.0, 2, [1], 2.0, 1)[0] == 0
+    assert O.sample_top_k([-1.0, -1.5], 0.0, 2, [0], 2.0, 1)[0] == 1
+    assert O.sample_top_k([2.0, 1.5], 0.0, 2, [0], 0.5, 1)[0] == 0
+    with pytest.raises(RuntimeError):
+        O.sample_top_k([1.0, 2.0], 1.0, 0, [], 1.0, 1)     # top_k 0: the reference indexes an empty list
+
+
+def test_sample_top_k_legacy_distribution():
+    """Draws follow the top-k softmax at temperature T: only the k largest
+    logits are drawn, with frequencies exp((l - max) / T) normalised
+    (4000 draws, 5-sigma bands)."""
+    logits = np.array([2.0, 0.5, 1.2, -1.0, 1.9, 0.0], np.float32)
+    T, k, n = 0.8, 3, 4000
+    top = np.argsort(-logits, kind="stable")[:k]
+    p = np.exp((logits[top].astype(np.float64) - logits[top].max()) / T)
+    p /= p.sum()
+    counts = np.zeros(len(logits))
+    rng = 12345
+    for _ in range(n):
+        tok, rng = O.sample_top_k(logits, T, k, [], 1.0, rng)
+        counts[tok] += 1
+    assert counts[np.setdiff1d(np.arange(len(logits)), top)].sum() == 0
+    for j, pj in zip(top, p):
+        assert abs(counts[j] / n - pj) <= 5 * np.sqrt(pj * (1 - pj) / n), (j, counts[j] / n, pj)
+
+
 def test_acoustic_embed_sum(models):
     t, p, om, ft, fp = models
     codes = np.random.Generator(np.random.PCG64(5)).integers(0, 2048, 15).astype(np.uint32)
