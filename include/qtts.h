@@ -484,7 +484,14 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
  *   kind 2: plain float4 copy of 256 MiB (no model needed), the HBM
  *           calibration point for byte counters;
  *   kind 3: predictor attention + o-proj, one row at position 8;
- *   kind 4: one whole predictor layer step, one row at position 8. */
+ *   kind 4: one whole predictor layer step, one row at position 8;
+ *   kind 5: the frame without its talker step (sampler, predictor chain,
+ *           combine), captured alone and replayed; *bytes = the predictor's
+ *           Q4 weight bytes;
+ *   kind 6: the talker step alone (28 layers + codec head), captured and
+ *           replayed from the current KV length (QTTS_ERR_CAPACITY without
+ *           room for iters + 1 positions); *bytes = its Q4 weight bytes.
+ * Kinds 5 and 6 restore the generation state afterwards. */
 int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
                      double *avg_us, double *bytes);
 

@@ -69,6 +69,9 @@ __device__ __forceinline__ float wave_max_dpp(float v)
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p; }
+// streaming read (no reuse within the frame): the non-temporal hint evicts
+// less of the last-level cache than an ordinary load
+__device__ __forceinline__ f32x4 ld4nt(const float *p) { return __builtin_nontemporal_load((const f32x4 *)p); }
 
 __device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
 {

@@ -181,6 +181,9 @@ hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const flo
 hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, const Workspace &ws,
                                    DevState *st, const float *hidden, const float *sem,
                                    const uint32_t *forced, uint32_t *codes_api, hipStream_t s);
+// The frame up to the talker step: sampler, predictor chain, combine.
+hipError_t enqueue_frame_codes(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
+                               const uint32_t *forced, hipStream_t s);
 hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
                          const uint32_t *forced, hipStream_t s);
 hipError_t enqueue_sample_top_k(const float *logits, int n, float temperature, int top_k, const uint32_t *prev,

@@ -1283,9 +1283,9 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
         f32x4 kk[8], vv[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) kk[i] = ld4(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
+        for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
 #pragma unroll
-        for (int i = 0; i < 8; i++) vv[i] = ld4(Vp + (vt0 + i) * HEAD_DIM + vd);
+        for (int i = 0; i < 8; i++) vv[i] = ld4nt(Vp + (vt0 + i) * HEAD_DIM + vd);
         // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92)
         float qv = qp[0], kvv = kp[0];
 #pragma unroll
@@ -2465,8 +2465,8 @@ hipError_t enqueue_pred_qkv_tables(const PredictorDev &p, int n_tables, float *p
 
 // One frame (generate_new.rs:606-675): sample code 0, predictor chain,
 // fuse embeddings + text, talker step, record.
-hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
-                         const uint32_t *forced, hipStream_t s)
+hipError_t enqueue_frame_codes(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
+                               const uint32_t *forced, hipStream_t s)
 {
     SampleArgs none{};
     hipLaunchKernelGGL(k_sampler, dim3(1), dim3(SAMP_T), 0, s, ws.logits, m.vocab, st, 0, none,
@@ -2478,7 +2478,13 @@ hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Worksp
                        p.emb_rows, p.n_groups, st, ws.text, ws.pad, ws.x, m.hidden,
                        head_cand(p, gl) ? (const float2 *)(ws.cand + gl * MAX_CAND) : (const float2 *)nullptr,
                        p.heads[gl].CT);
-    QCHK(hipGetLastError());
+    return hipGetLastError();
+}
+
+hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
+                         const uint32_t *forced, hipStream_t s)
+{
+    QCHK(enqueue_frame_codes(m, p, ws, st, forced, s));
     return enqueue_talker_step(m, ws, st, 1, s);
 }
 

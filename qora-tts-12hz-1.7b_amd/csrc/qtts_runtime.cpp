@@ -2127,6 +2127,55 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
                              [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->stream); },
                              avg_us);
     }
+    if (kind == 5 || kind == 6) {
+        // the frame's two halves, each captured alone and replayed back to
+        // back: 5 = sampler + predictor chain + combine (the predictor's
+        // weights stay warm in the last-level cache between replays), 6 =
+        // the talker step (KV appended from the current length).  The
+        // generation state is restored afterwards.
+        const PredictorDev &p = c->pm;
+        const int64_t n = (int64_t)iters + 1;
+        if (kind == 6 && (c->h_st->kv_len + n > c->kv_cap || c->h_st->position + n > m.rope_rows))
+            return fail(c, QTTS_ERR_CAPACITY, "no room in the KV cache to time %d talker steps", iters);
+        hipSetDevice(c->device);
+        DevState saved;
+        HIPCHK(c, hipMemcpyAsync(&saved, c->st_gen, sizeof saved, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        double w = 0.0;
+        if (kind == 5) {
+            for (int l = 0; l < p.n_layers; l++) {
+                const LayerDev &L = p.layers[l];
+                w += (double)(L.qkv.k * L.qkv.n + L.o.k * L.o.n + L.gate_up.k * L.gate_up.n + L.down.k * L.down.n);
+            }
+            for (int g = 0; g < p.n_groups; g++) w += (double)p.heads[g].k * p.heads[g].n;
+            w += (double)p.proj.k * p.proj.n;
+        } else {
+            for (int l = 0; l < m.n_layers; l++) {
+                const LayerDev &L = m.layers[l];
+                w += (double)(L.qkv.k * L.qkv.n + L.o.k * L.o.n + L.gate_up.k * L.gate_up.n + L.down.k * L.down.n);
+            }
+            w += (double)m.codec_head.k * m.codec_head.n;
+        }
+        *bytes = w * 0.5625;
+        hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
+        HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        const hipError_t e = kind == 5 ? enqueue_frame_codes(m, p, c->ws, c->st_gen, c->d_forced, c->stream)
+                                       : enqueue_talker_step(m, c->ws, c->st_gen, 0, c->stream);
+        const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+        if (e != hipSuccess || e2 != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            return fail(c, QTTS_ERR_HIP, "capture failed: %s / %s", hipGetErrorString(e), hipGetErrorString(e2));
+        }
+        const hipError_t e3 = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (e3 != hipSuccess) return fail(c, QTTS_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e3));
+        const int rc = time_launches(c, iters, [&](int) { return hipGraphLaunch(ge, c->stream); }, avg_us);
+        hipGraphExecDestroy(ge);
+        HIPCHK(c, hipMemcpyAsync(c->st_gen, &saved, sizeof saved, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        return rc;
+    }
     if (kind == 3 || kind == 4) {
         // predictor, one row at position 8 (a mid-chain step), cycling the layers
         const PredictorDev &p = c->pm;
