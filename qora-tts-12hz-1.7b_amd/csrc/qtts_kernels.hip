@@ -42,7 +42,7 @@ __device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t m)
 }
 
 // ---------------------------------------------------------------------------
-// block-wide reductions (deterministic tree order)
+// wave-wide sum (deterministic butterfly order)
 // ---------------------------------------------------------------------------
 
 __device__ __forceinline__ float wave_sum(float v)
@@ -50,62 +50,6 @@ __device__ __forceinline__ float wave_sum(float v)
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
     return v;
-}
-
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
-}
-
-__device__ float block_sum(float v, float *scratch)
-{
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int nw = (blockDim.x + 63) >> 6;
-    v = wave_sum(v);
-    __syncthreads();
-    if (lane == 0) scratch[wv] = v;
-    __syncthreads();
-    float r = 0.0f;
-    for (int i = 0; i < nw; i++) r += scratch[i];
-    return r;
-}
-
-__device__ float block_max(float v, float *scratch)
-{
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int nw = (blockDim.x + 63) >> 6;
-    v = wave_max(v);
-    __syncthreads();
-    if (lane == 0) scratch[wv] = v;
-    __syncthreads();
-    float r = -INFINITY;
-    for (int i = 0; i < nw; i++) r = fmaxf(r, scratch[i]);
-    return r;
-}
-
-// Exclusive prefix sum of one int per thread over the block (thread order).
-__device__ int block_excl_scan(int v, int *scratch, int *total)
-{
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int nw = (blockDim.x + 63) >> 6;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-    }
-    __syncthreads();
-    if (lane == 63) scratch[wv] = x;
-    __syncthreads();
-    int base = 0, tot = 0;
-    for (int i = 0; i < nw; i++) {
-        if (i < wv) base += scratch[i];
-        tot += scratch[i];
-    }
-    if (total) *total = tot;
-    return base + x - v;
 }
 
 template <int CTRL>
@@ -1815,16 +1759,21 @@ __global__ void k_silu(float *x, int n)
 }
 
 // ---------------------------------------------------------------------------
-// sampler (sample_token, generate_new.rs:771-862) in one workgroup.
-// Top-k keeps the k largest probabilities with ties broken by lower index
-// (Rust's stable sort): a 4-pass radix select finds the k-th largest value,
+// sampler (sample_token, generate_new.rs:771-862) in one workgroup of four
+// waves.  Thread t holds entries 16t..16t+15 in registers, so "index order"
+// is thread order then register order.  The repetition penalty is applied
+// per history entry (a count per token, the same division repeated); top-k
+// keeps the k largest probabilities with ties broken by lower index (Rust's
+// stable sort): a radix select over the probability bits (8 bits a pass,
+// per-wave histograms, the bin scan on one wave) finds the k-th largest,
 // then equal values are admitted in index order.  Top-p sorts the kept
 // entries (bitonic, rank = (p desc, index asc)).  The draw walks nonzero
 // probabilities in index order.
 // ---------------------------------------------------------------------------
 
 constexpr int SAMP_MAX = 4096;
-constexpr int SAMP_T = 1024;
+constexpr int SAMP_T = 256;
+constexpr int SAMP_E = SAMP_MAX / SAMP_T;        // entries per thread
 
 __device__ __forceinline__ bool rank_before(float pa, int ia, float pb, int ib)
 {
@@ -1865,68 +1814,69 @@ struct SampleArgs {
     int n_prev;
 };
 
-// Keeps the top_k largest entries of p[0..n) (p >= 0, no NaN), zeroing the
-// rest; among equal values the lower indices are kept.
-__device__ void topk_select(float *p, int n, int top_k, int *hist, int *iscratch)
+// Exclusive prefix sum of one int per lane in lane order; *total = the
+// wave's sum.
+__device__ __forceinline__ int wave_excl_scan(int v, int *total)
 {
-    __shared__ uint32_t prefix_s, mask_s;
-    __shared__ int need_s;
-    const int t = threadIdx.x;
-    if (t == 0) { prefix_s = 0; mask_s = 0; need_s = top_k; }
-    __syncthreads();
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        for (int i = t; i < 256; i += blockDim.x) hist[i] = 0;
-        __syncthreads();
-        const uint32_t prefix = prefix_s, mask = mask_s;
-        for (int i = t; i < n; i += blockDim.x) {
-            const uint32_t b = __float_as_uint(p[i]);
-            if ((b & mask) == prefix) atomicAdd(&hist[(b >> shift) & 0xFF], 1);
-        }
-        __syncthreads();
-        // bins in descending order: thread t < 256 owns bin 255 - t; the bin
-        // holding the need-th largest is where the running count crosses need
-        const int need = need_s;
-        const int hv = t < 256 ? hist[255 - t] : 0;
-        const int above = block_excl_scan(hv, iscratch, nullptr);
-        if (t < 256 && above < need && above + hv >= need) {
-            prefix_s = prefix | ((uint32_t)(255 - t) << shift);
-            mask_s = mask | (0xFFu << shift);
-            need_s = need - above;
-        }
-        __syncthreads();
+    const int lane = threadIdx.x & 63;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
     }
-    // thr: bits of the k-th largest value; need_eq: how many entries equal
-    // to it stay (the lowest indices)
-    const uint32_t thr = prefix_s;
-    const int need_eq = need_s;
-    const int per = (n + blockDim.x - 1) / blockDim.x;
-    const int i0 = t * per, i1 = min(i0 + per, n);
-    int eq = 0;
-    for (int i = i0; i < i1; i++) eq += __float_as_uint(p[i]) == thr;
-    int before = block_excl_scan(eq, iscratch, nullptr);
-    for (int i = i0; i < i1; i++) {
-        const uint32_t b = __float_as_uint(p[i]);
-        bool keep = b > thr;
-        if (b == thr) keep = before++ < need_eq;
-        if (!keep) p[i] = 0.0f;
-    }
+    *total = __shfl(x, 63);
+    return x - v;
+}
+
+// Four-wave block helpers, one barrier each.  Every call site passes its own
+// 4-slot scratch, so no barrier is needed before the scratch is reused.
+__device__ __forceinline__ int blk4_excl_scan(int v, int *wsum, int *total)
+{
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int wt;
+    const int x = wave_excl_scan(v, &wt);
+    if (lane == 0) wsum[wv] = wt;
     __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int s = wsum[i];
+        base += i < wv ? s : 0;
+        tot += s;
+    }
+    if (total) *total = tot;
+    return base + x;
+}
+
+__device__ __forceinline__ float blk4_sum(float v, float *red)
+{
+    v = wave_sum_dpp(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __forceinline__ float blk4_max(float v, float *red)
+{
+    v = wave_max_dpp(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 __global__ void __launch_bounds__(SAMP_T)
 k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, uint64_t *rng_api,
           uint32_t *out_api, const uint32_t *forced)
 {
-    __shared__ float p[SAMP_MAX];
-    __shared__ float kp[SAMP_MAX];
-    __shared__ int ki[SAMP_MAX];
-    __shared__ float scratch[16];
-    __shared__ int iscratch[16];
-    __shared__ int hist[256];
-    __shared__ int nanf;
-    __shared__ int cutoff_s;
-    const int t = threadIdx.x;
+    __shared__ __align__(16) float kp[SAMP_MAX];
+    __shared__ __align__(16) int ki[SAMP_MAX];
+    __shared__ __align__(16) int hist[2][4][256];
+    __shared__ float redf[4][4];
+    __shared__ int redi[4][4];
+    __shared__ uint32_t sel_prefix, sel_mask;
+    __shared__ int sel_need, sel_done, cutoff_s;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     if (mode == 0 && st->stop) return;
     float temp, top_p, rep;
     int top_k, n_prev;
@@ -1939,45 +1889,64 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
         temp = api.temperature; top_p = api.top_p; rep = api.rep; top_k = api.top_k;
         prev = api.prev; n_prev = api.n_prev;
     }
-    if (t == 0) nanf = 0;
-    for (int i = t; i < n; i += blockDim.x) p[i] = logits[i];
-    __syncthreads();
-    if (t == 0 && rep != 1.0f) {
-        for (int i = 0; i < n_prev; i++) {
-            const uint32_t tok = prev[i];
-            if (tok < (uint32_t)n) {
-                const float v = p[tok];
-                p[tok] = v > 0.0f ? v / rep : v * rep;
-            }
+    const int i0 = t * SAMP_E;
+    float v[SAMP_E];
+    if (i0 + SAMP_E <= n && ((uintptr_t)logits & 15) == 0) {
+#pragma unroll
+        for (int q = 0; q < SAMP_E / 4; q++) {
+            const f32x4 a = ld4(logits + i0 + 4 * q);
+            v[4 * q] = a.x; v[4 * q + 1] = a.y; v[4 * q + 2] = a.z; v[4 * q + 3] = a.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) {
+            const float x = logits[min(i0 + e, n - 1)];
+            v[e] = i0 + e < n ? x : -INFINITY;
         }
     }
-    __syncthreads();
+    // repetition penalty (generate_new.rs:776-785): once per history entry
+    if (rep != 1.0f && n_prev > 0) {
+        for (int i = t; i < n; i += SAMP_T) ki[i] = 0;
+        __syncthreads();
+        for (int j = t; j < n_prev; j += SAMP_T) {
+            const uint32_t tok = prev[j];
+            if (tok < (uint32_t)n) atomicAdd(&ki[tok], 1);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) {
+            const int c = i0 + e < n ? ki[i0 + e] : 0;
+            for (int k = 0; k < c; k++) v[e] = v[e] > 0.0f ? v[e] / rep : v[e] * rep;
+        }
+    }
+    // temperature, softmax
     const bool use_t = temp != 1.0f && temp > 0.0f;
     float mx = -INFINITY;
-    for (int i = t; i < n; i += blockDim.x) {
-        float v = p[i];
-        if (use_t) v = v / temp;
-        p[i] = v;
-        mx = fmaxf(mx, v);
+#pragma unroll
+    for (int e = 0; e < SAMP_E; e++) {
+        if (use_t) v[e] = v[e] / temp;
+        mx = fmaxf(mx, v[e]);
     }
-    mx = block_max(mx, scratch);
+    mx = blk4_max(mx, redf[0]);
     float sum = 0.0f;
-    for (int i = t; i < n; i += blockDim.x) {
-        const float e = expf(p[i] - mx);
-        p[i] = e;
-        sum += e;
+#pragma unroll
+    for (int e = 0; e < SAMP_E; e++) {
+        const float ex = i0 + e < n ? expf(v[e] - mx) : 0.0f;
+        v[e] = ex;
+        sum += ex;
     }
-    sum = block_sum(sum, scratch);
-    for (int i = t; i < n; i += blockDim.x) {
-        const float v = p[i] / sum;
-        if (isnan(v)) nanf = 1;
-        p[i] = v;
+    sum = blk4_sum(sum, redf[1]);
+    int nan_l = 0;
+#pragma unroll
+    for (int e = 0; e < SAMP_E; e++) {
+        const float q = v[e] / sum;
+        nan_l |= (i0 + e < n) && isnan(q);
+        v[e] = i0 + e < n ? q : 0.0f;
     }
-    __syncthreads();
 
     const bool do_k = top_k > 0 && top_k < n;
     const bool do_p = top_p > 0.0f && top_p < 1.0f;
-    if ((do_k || do_p) && nanf) {        // Rust panics in partial_cmp().unwrap()
+    if (__syncthreads_or(nan_l) && (do_k || do_p)) {   // Rust panics in partial_cmp().unwrap()
         if (t == 0) {
             st->nan_flag = 1;
             if (mode == 0) st->stop = 1; else *out_api = 0;
@@ -1985,27 +1954,88 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
         return;
     }
     if (do_k) {
-        topk_select(p, n, top_k, hist, iscratch);
-        float s2 = 0.0f;
-        for (int i = t; i < n; i += blockDim.x) s2 += p[i];
-        s2 = block_sum(s2, scratch);
-        if (s2 > 0.0f)
-            for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s2;
+        uint32_t key[SAMP_E];
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) key[e] = __float_as_uint(v[e]);
+        for (int i = t; i < 4 * 256; i += SAMP_T) (&hist[0][0][0])[i] = 0;
+        if (t == 0) { sel_prefix = 0; sel_mask = 0; sel_need = top_k; sel_done = 0; }
         __syncthreads();
+        for (int pass = 0; pass < 4; pass++) {
+            const int shift = 24 - 8 * pass;
+            const uint32_t prefix = sel_prefix, mask = sel_mask;
+            int *h = &hist[pass & 1][wv][0];
+#pragma unroll
+            for (int e = 0; e < SAMP_E; e++)
+                if (i0 + e < n && (key[e] & mask) == prefix) atomicAdd(&h[(key[e] >> shift) & 0xFF], 1);
+            for (int i = t; i < 4 * 256; i += SAMP_T) (&hist[(pass + 1) & 1][0][0])[i] = 0;
+            __syncthreads();
+            if (wv == 0) {
+                // lane l scans bins 255-4l down to 252-4l; the bin holding
+                // the need-th largest is where the running count crosses need
+                const int b0 = 252 - 4 * lane;
+                int c[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int w = 0; w < 4; w++) {
+                    const int4 q = *(const int4 *)&hist[pass & 1][w][b0];
+                    c[0] += q.w; c[1] += q.z; c[2] += q.y; c[3] += q.x;
+                }
+                int wt;
+                int above = wave_excl_scan((c[0] + c[1]) + (c[2] + c[3]), &wt);
+                const int need = sel_need;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (above < need && above + c[q] >= need) {
+                        sel_prefix = prefix | ((uint32_t)(b0 + 3 - q) << shift);
+                        sel_mask = mask | (0xFFu << shift);
+                        sel_need = need - above;
+                        sel_done = above + c[q] == need;
+                    }
+                    above += c[q];
+                }
+            }
+            __syncthreads();
+            if (sel_done) break;
+        }
+        // keep entries above the selected bits, and the first sel_need equal
+        // to them in index order
+        const uint32_t prefix = sel_prefix, mask = sel_mask;
+        const int need = sel_need;
+        int eq = 0;
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) eq += (i0 + e < n) && (key[e] & mask) == prefix;
+        int before = blk4_excl_scan(eq, redi[0], nullptr);
+        float s2 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) {
+            bool keep = false;
+            if (i0 + e < n) {
+                const uint32_t km = key[e] & mask;
+                keep = km > prefix;
+                if (km == prefix) keep = before++ < need;
+            }
+            if (!keep) v[e] = 0.0f;
+            s2 += v[e];
+        }
+        s2 = blk4_sum(s2, redf[2]);
+        if (s2 > 0.0f)
+#pragma unroll
+            for (int e = 0; e < SAMP_E; e++) v[e] = v[e] / s2;
     }
     if (do_p) {
         // rank the nonzero entries (after top-k at most top_k of them)
-        const int per = (n + blockDim.x - 1) / blockDim.x;
-        const int i0 = t * per, i1 = min(i0 + per, n);
+        uint8_t *drop = (uint8_t *)&hist[0][0][0];
         int c = 0;
-        for (int i = i0; i < i1; i++) c += p[i] != 0.0f;
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) c += v[e] != 0.0f;
         int tot = 0;
-        int o = block_excl_scan(c, iscratch, &tot);
-        for (int i = i0; i < i1; i++)
-            if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
+        int o = blk4_excl_scan(c, redi[1], &tot);
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++)
+            if (v[e] != 0.0f) { kp[o] = v[e]; ki[o] = i0 + e; o++; }
         int N = 1;
         while (N < tot) N <<= 1;
-        for (int i = tot + t; i < N; i += blockDim.x) { kp[i] = -1.0f; ki[i] = 0x7fffffff; }
+        for (int i = tot + t; i < N; i += SAMP_T) { kp[i] = -1.0f; ki[i] = 0x7fffffff; }
+        for (int i = t; i < n; i += SAMP_T) drop[i] = 0;
         __syncthreads();
         bitonic_sort_desc(kp, ki, N);
         if (t == 0) {
@@ -2018,33 +2048,45 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
             cutoff_s = cutoff < 1 ? 1 : cutoff;
         }
         __syncthreads();
-        for (int r = cutoff_s + t; r < tot; r += blockDim.x) p[ki[r]] = 0.0f;
+        for (int r = cutoff_s + t; r < tot; r += SAMP_T) drop[ki[r]] = 1;
         __syncthreads();
         float s3 = 0.0f;
-        for (int i = t; i < n; i += blockDim.x) s3 += p[i];
-        s3 = block_sum(s3, scratch);
+#pragma unroll
+        for (int e = 0; e < SAMP_E; e++) {
+            if (i0 + e < n && drop[i0 + e]) v[e] = 0.0f;
+            s3 += v[e];
+        }
+        s3 = blk4_sum(s3, redf[3]);
         if (s3 > 0.0f)
-            for (int i = t; i < n; i += blockDim.x) p[i] = p[i] / s3;
-        __syncthreads();
+#pragma unroll
+            for (int e = 0; e < SAMP_E; e++) v[e] = v[e] / s3;
     }
     // compact nonzero probabilities in index order, then the cumulative draw
-    const int per = (n + blockDim.x - 1) / blockDim.x;
-    const int i0 = t * per, i1 = min(i0 + per, n);
     int c = 0;
-    for (int i = i0; i < i1; i++) c += p[i] != 0.0f;
+#pragma unroll
+    for (int e = 0; e < SAMP_E; e++) c += v[e] != 0.0f;
     int total = 0;
-    int o = block_excl_scan(c, iscratch, &total);
-    for (int i = i0; i < i1; i++)
-        if (p[i] != 0.0f) { kp[o] = p[i]; ki[o] = i; o++; }
+    int o = blk4_excl_scan(c, redi[2], &total);
+#pragma unroll
+    for (int e = 0; e < SAMP_E; e++)
+        if (v[e] != 0.0f) { kp[o] = v[e]; ki[o] = i0 + e; o++; }
     __syncthreads();
     if (t == 0) {
         uint64_t rs = mode == 0 ? st->rng : *rng_api;
         const float r = simple_rand_dev(rs);
         float cs = 0.0f;
         uint32_t res = 0;
-        for (int k = 0; k < total; k++) {
-            cs += kp[k];
-            if (r < cs) { res = (uint32_t)ki[k]; break; }
+        bool found = false;
+        for (int k = 0; k < total && !found; k += 4) {
+            const f32x4 q = *(const f32x4 *)&kp[k];
+            const float qv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (!found && k + j < total) {
+                    cs += qv[j];
+                    if (r < cs) { res = (uint32_t)ki[k + j]; found = true; }
+                }
+            }
         }
         if (mode == 0) {
             st->rng = rs;

@@ -276,6 +276,36 @@ def test_sampler_matches_oracle(ctx, top_k, top_p, temp, rep):
     assert mismatch <= 1
 
 
+@pytest.mark.parametrize("n,top_k,top_p,temp,rep,n_prev,ties", [
+    (37, 5, 1.0, 0.9, 1.05, 16, False),       # ragged n: one thread holds a partial range
+    (4096, 4095, 1.0, 0.8, 1.3, 16, False),   # the largest n, top-k of all but one
+    (3072, 50, 1.0, 0.9, 1.2, 1000, False),   # long history, many repeats per token
+    (3072, 20, 0.9, 1.0, 1.0, 0, True),       # heavy ties: 8 distinct logits
+    (3072, 1, 1.0, 0.9, 1.05, 16, True),      # greedy among ties: the lowest index
+    (1000, 0, 1.0, 0.0, 1.05, 16, False),     # T <= 0 is softmax at T = 1, no top-k
+])
+def test_sampler_edges_match_oracle(ctx, n, top_k, top_p, temp, rep, n_prev, ties):
+    """The sampler on the edges of its layout (entries per thread, the
+    radix select's ties and early exit, the history count) against the
+    oracle; selections are exact, a draw may differ where the CDF's float
+    rounding differs (expf bits), at most once per 20 draws."""
+    rng = np.random.Generator(np.random.PCG64(1000 + n + top_k))
+    params = qtts.sample_params(temperature=temp, top_k=top_k, top_p=top_p, repetition_penalty=rep)
+    mismatch = 0
+    s_gpu = s_cpu = 7
+    for i in range(20):
+        if ties:
+            lg = (rng.integers(0, 8, n) * 0.5).astype(np.float32)
+        else:
+            lg = (rng.standard_normal(n) * 3).astype(np.float32)
+        prev = rng.integers(0, min(n, 64) if n_prev > 16 else n, n_prev).astype(np.uint32)
+        a, s_gpu = ctx.sample_token(lg, params, prev, s_gpu, temp)
+        b, s_cpu = O.sample_token(lg, params, prev, s_cpu, temp)
+        assert s_gpu == s_cpu
+        mismatch += a != b
+    assert mismatch <= (0 if top_k == 1 else 1)
+
+
 def test_frames_teacher_forced_greedy(loaded):
     """200 greedy frames (top_k 1), each fed the oracle's previous codes;
     >= 99% of the 16 x 200 codes agree."""
