@@ -8,7 +8,7 @@ recorded in manifest.json (numpy PCG64 through qtts.synth and
 tests/refgen.py), and a SHA-256 prefix of every input array is recorded so a
 drift of the generators is caught before any comparison.
 
-  gemv.npz            the BASELINE GEMV (k 2048 -> n 6144, seed 1) and the
+  gemv.npz            the GEMV k 2048 -> n 6144 (seed 1) and the
                       reference's own differential cases (gemv.rs:756-861),
                       gemv_q4_scalar order
   talker_step.npz     one talker layer at the 1.7B shapes, KV N(0,1) to 512,
@@ -141,12 +141,12 @@ def main():
     manifest = {"oracle_workers": WORKERS, "oracle_threads": THREADS, "fixtures": {}}
 
     w, x, cases = gemv_inputs()
-    out = {"config1_y": O.gemv_scalar(x, w)}
+    out = {"gemv_2048x6144_y": O.gemv_scalar(x, w)}
     for name, (cx, cw) in cases.items():
         out[name + "_y"] = O.gemv_scalar(cx, cw)
     np.savez(os.path.join(HERE, "gemv.npz"), **out)
     manifest["fixtures"]["gemv"] = {
-        "inputs": {"config1": digest((w, x)), **{k: digest(v) for k, v in cases.items()}},
+        "inputs": {"gemv_2048x6144": digest((w, x)), **{k: digest(v) for k, v in cases.items()}},
         "tolerance": "1e-3 * max(max|ref|, rms(ref))"}
 
     t, p = models()

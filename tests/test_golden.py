@@ -43,9 +43,9 @@ def test_gemv_fixture():
     O.set_workers(MANIFEST["oracle_workers"], MANIFEST["oracle_threads"])
     w, x, cases = G.gemv_inputs()
     rec = MANIFEST["fixtures"]["gemv"]["inputs"]
-    assert G.digest((w, x)) == rec["config1"]
+    assert G.digest((w, x)) == rec["gemv_2048x6144"]
     f = fixture("gemv")
-    assert same_bits(O.gemv_scalar(x, w), f["config1_y"])
+    assert same_bits(O.gemv_scalar(x, w), f["gemv_2048x6144_y"])
     for name, (cx, cw) in cases.items():
         assert G.digest((cx, cw)) == rec[name], name
         assert same_bits(O.gemv_scalar(cx, cw), f[name + "_y"]), name

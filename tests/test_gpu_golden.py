@@ -48,9 +48,9 @@ def test_gemv_golden(ctx_factory):
     c = ctx_factory(64)
     w, x, cases = G.gemv_inputs()
     f = fixture("gemv")
-    assert G.digest((w, x)) == MANIFEST["fixtures"]["gemv"]["inputs"]["config1"]
+    assert G.digest((w, x)) == MANIFEST["fixtures"]["gemv"]["inputs"]["gemv_2048x6144"]
     dw = c.upload(w)
-    ok, e = close(c.gemv(dw, x), f["config1_y"])
+    ok, e = close(c.gemv(dw, x), f["gemv_2048x6144_y"])
     dw.free()
     assert ok, f"config 1: rel err {e}"
     for name, (cx, cw) in cases.items():
