@@ -1,0 +1,114 @@
+"""The frame loop's stops and errors (generate_new.rs:583-675).  EOS ends
+generation before the EOS frame is emitted: the reference breaks before
+pushing it (generate_new.rs:617-621).  A full KV cache, NaN logits and calls
+out of order return their statuses and leave the context usable."""
+import numpy as np
+import pytest
+
+import oracle as O
+import qtts
+from qtts import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def model():
+    t = synth.make_talker(seed=701, n_layers=2, text_vocab=256, rope_max_pos=1024)
+    p = synth.make_predictor(seed=702, n_layers=5, rope_max_pos=64)
+    return t, p
+
+
+def begin(ctx, t, n, params, edit_logits=None, seed=42):
+    X = np.random.Generator(np.random.PCG64(71)).standard_normal((n, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    hid = ctx.prefill_talker_raw_from(X, 0)
+    lg = ctx.apply_codec_head(hid)
+    if edit_logits is not None:
+        lg = edit_logits(lg.copy())
+    ctx.gen_set_text(None, ctx.embed_text_token(3))
+    ctx.gen_begin(lg, hid, n, seed, params)
+    return X, hid, lg
+
+
+def test_eos_on_the_first_frame(ctx_factory, model):
+    t, p = model
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+
+    def eos_wins(lg):
+        lg[2150] = 1e4
+        return lg
+    params = qtts.sample_params(eos_enabled=True)
+    X, hid, lg = begin(c, t, 16, params, eos_wins)
+    codes, eos = c.gen_frames(10)
+    assert eos and codes.shape[0] == 0 and c.kv_len() == 16
+    codes, eos = c.gen_frames(10)                  # stays stopped
+    assert eos and codes.shape[0] == 0
+    om = O.Model(t, p, kv_cap=256)
+    om.prefill(X, 0)
+    om.gen_begin(lg, hid, 16, 42)
+    _, oeos = om.frame(params, c.embed_text_token(3))
+    om.close()
+    assert oeos
+
+
+def test_eos_mid_run_stops_before_the_frame(ctx_factory, model):
+    """Frames sampled without EOS, then the same run with the EOS id set to
+    the first code 0 that frame k introduces: exactly frames 0..k-1 come
+    back, identical, and the flag is set."""
+    t, p = model
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+    begin(c, t, 16, qtts.sample_params(eos_enabled=False))
+    free, eos = c.gen_frames(24)
+    assert not eos and free.shape[0] == 24
+    first = {}
+    for f, code in enumerate(free[:, 0]):
+        first.setdefault(int(code), f)
+    k, x = max((f, code) for code, f in first.items() if f > 0)
+    begin(c, t, 16, qtts.sample_params(eos_enabled=True, codec_eos_id=x))
+    got, eos = c.gen_frames(24)
+    assert eos and got.shape[0] == k
+    assert np.array_equal(got, free[:k])
+    assert c.kv_len() == 16 + k
+
+
+def test_kv_capacity(ctx_factory, model):
+    """A batch that would overflow the cache is refused before it runs; the
+    frames that fit still run afterwards; the next one is refused."""
+    t, p = model
+    c = ctx_factory(128)
+    c.upload_model(t, p)
+    begin(c, t, 100, qtts.sample_params(eos_enabled=False))
+    with pytest.raises(qtts.QttsError) as e:
+        c.gen_frames(64)
+    assert e.value.code == qtts.ERR_CAPACITY
+    assert c.kv_len() == 100
+    codes, eos = c.gen_frames(28)
+    assert codes.shape[0] == 28 and not eos and c.kv_len() == 128
+    with pytest.raises(qtts.QttsError) as e:
+        c.gen_frames(1)
+    assert e.value.code == qtts.ERR_CAPACITY
+
+
+def test_nan_logits_and_order(ctx_factory, model):
+    t, p = model
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+    with pytest.raises(qtts.QttsError) as e:
+        c.gen_frames(4)                            # before gen_begin
+    assert e.value.code == qtts.ERR_STATE
+
+    def poison(lg):
+        lg[7] = np.nan
+        return lg
+    begin(c, t, 16, qtts.sample_params(eos_enabled=False), poison)
+    with pytest.raises(qtts.QttsError) as e:
+        c.gen_frames(4)
+    assert e.value.code == qtts.ERR_NAN
+    # a fresh start on the same context works
+    begin(c, t, 16, qtts.sample_params(eos_enabled=False))
+    codes, eos = c.gen_frames(3)
+    assert codes.shape[0] == 3 and not eos
+    assert c.gen_frames(0)[0].shape[0] == 0
