@@ -171,7 +171,8 @@ struct ProPlain {
 // sums are wave-uniform loads.  The cache length is read in the fetch stage
 // (a scalar load) and the pages after the weights are in flight.
 struct ProAttnCombine {
-    static constexpr int PF = 8;   // pages of P.V fetched ahead of the weights
+    static constexpr int PF = 16;  // pages of P.V fetched ahead of the weights
+    static constexpr int PB = 24;  // pages of P.V loaded together after them (PF + k*PB never straddles page 64)
     const float *am, *al;    // [16 heads][MAX_CHUNKS] page max / exp-sum
     const float *aacc;       // [MAX_CHUNKS][16][128] page P.V
     const DevState *st;
@@ -187,6 +188,7 @@ struct ProAttnCombine {
     __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
         static_assert(KC % T == 0 && KC % HEAD_DIM == 0 && MAX_CHUNKS == 128, "rows per thread, pages per lane");
+        static_assert(PF + 2 * PB == 64, "a block of pages never straddles page 64");
         const int lane = threadIdx.x & 63;
         f.L = (slot_ovr >= 0 ? slot_ovr : st->kv_len) + 1;
 #pragma unroll
@@ -223,15 +225,15 @@ struct ProAttnCombine {
                 o = j < C ? fmaf(wc, f.a[e][j], o) : o;
             }
             const float *ah = aacc + (size_t)h * HEAD_DIM + d;
-            for (int c0 = PF; c0 < C; c0 += 8) {
-                float av[8];
+            for (int c0 = PF; c0 < C; c0 += PB) {
+                float av[PB];
 #pragma unroll
-                for (int j = 0; j < 8; j++) av[j] = ah[(size_t)min(c0 + j, C - 1) * 16 * HEAD_DIM];
+                for (int j = 0; j < PB; j++) av[j] = ah[(size_t)min(c0 + j, C - 1) * 16 * HEAD_DIM];
+                const float wb = c0 < 64 ? w0 : w1;
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
+                for (int j = 0; j < PB; j++) {
                     const int c = c0 + j;
-                    const float wc = c < 64 ? lane_value(w0, c & 63) : lane_value(w1, c & 63);
-                    o = c < C ? fmaf(wc, av[j], o) : o;
+                    o = c < C ? fmaf(lane_value(wb, c & 63), av[j], o) : o;
                 }
             }
             xs[i] = row < 16 * HEAD_DIM ? o / Ls : 0.0f;
