@@ -250,6 +250,25 @@ int qtts_model_upload(qtts_ctx *ctx, const qtts_talker_host *talker,
  * A malformed section fails with QTTS_ERR_IO before anything is uploaded. */
 int qtts_model_load_qtts(qtts_ctx *ctx, const char *path);
 
+/* RoPE tables for a container that does not hold them: the talker's
+ * multimodal tables (rope::build_mrope_tables, rope.rs:11-41) and the
+ * predictor's standard ones (loader.rs:869-881), [max_pos][head_dim/2]. */
+typedef struct qtts_rope_tables {
+    const float *talker_cos, *talker_sin;
+    int64_t talker_max_pos;
+    const float *pred_cos, *pred_sin;
+    int64_t pred_max_pos;
+} qtts_rope_tables;
+
+/* Read the older "QORA-TTS-Q4" named-tensor container straight into the
+ * context: talker and predictor.  Replaces `load_talker_binary` /
+ * `load_code_predictor_binary` (loader.rs:724-882, container read by
+ * loader.rs:47-127).  Shapes come from the tensors (layer and codebook
+ * counts from the names present); the RoPE tables from `rope`.  A missing
+ * or malformed tensor fails with QTTS_ERR_IO, an F16 linear weight with
+ * QTTS_ERR_UNSUPPORTED, before anything is uploaded. */
+int qtts_model_load_qora_q4(qtts_ctx *ctx, const char *path, const qtts_rope_tables *rope);
+
 /* Shapes of the uploaded model (hidden, vocab, ...); 0 on success. */
 int qtts_model_dims(qtts_ctx *ctx, int32_t *talker_hidden,
                     int32_t *talker_vocab, int32_t *talker_layers,

@@ -420,3 +420,256 @@ extern "C" int qtts_model_load_qtts(qtts_ctx *ctx, const char *path)
     munmap(map, (size_t)sb.st_size);
     return rc;
 }
+
+// ---------------------------------------------------------------------------
+// The older "QORA-TTS-Q4" container (loader.rs:47-127 read, 724-882 mapped):
+//   16-byte header starting "QORA-TTS-Q4", u32 version, u32 n_tensors, then
+//   per tensor: u32 name_len + name, u32 rank + u32 dims[rank], u8 format,
+//     format 1 (Q4): u32 n_scales + f16 scales, u32 n_packed + bytes
+//     format 0 (F16): u32 n_values + f16 values
+//   little-endian.  Linear weights and embeddings are stored [in][out]
+//   (shape [k, n]) in the F1 layout; norms and biases are F16 vectors.
+// The file holds no configuration or RoPE tables: the shapes come from the
+// tensors, and the tables from the caller (the reference builds them from
+// config.json, loader.rs:770-775 and 869-881).
+// ---------------------------------------------------------------------------
+
+#include <map>
+#include <string>
+
+namespace {
+
+struct LegacyTensor {
+    std::vector<uint32_t> shape;
+    uint8_t format = 0;
+    const uint16_t *f16 = nullptr;   // scales (Q4) or values (F16)
+    uint64_t n16 = 0;
+    const uint8_t *packed = nullptr;
+    uint64_t npacked = 0;
+};
+
+bool read_legacy_tensors(Reader &r, std::map<std::string, LegacyTensor> &m)
+{
+    const uint8_t *hdr = r.bytes(16);
+    if (!r.ok || memcmp(hdr, "QORA-TTS-Q4", 11) != 0) return false;
+    (void)r.get<uint32_t>();                                   // version
+    const uint32_t nt = r.get<uint32_t>();
+    if (!r.ok || nt > (1u << 20)) return false;
+    for (uint32_t i = 0; i < nt; i++) {
+        const uint32_t nl = r.get<uint32_t>();
+        const uint8_t *nm = r.bytes(nl);
+        const uint32_t rank = r.get<uint32_t>();
+        if (!r.ok || rank > 8) return false;
+        LegacyTensor t;
+        for (uint32_t d = 0; d < rank; d++) t.shape.push_back(r.get<uint32_t>());
+        t.format = r.get<uint8_t>();
+        t.n16 = r.get<uint32_t>();
+        t.f16 = (const uint16_t *)r.bytes(t.n16 * 2);
+        if (t.format == 1) {
+            t.npacked = r.get<uint32_t>();
+            t.packed = r.bytes(t.npacked);
+        } else if (t.format != 0) {
+            return false;
+        }
+        if (!r.ok) return false;
+        m[std::string((const char *)nm, nl)] = std::move(t);
+    }
+    return true;
+}
+
+struct LegacyModel {
+    std::map<std::string, LegacyTensor> m;
+    std::vector<std::vector<float>> f32;   // F16 biases widened to f32
+    int status = QTTS_OK;                  // first problem met
+    void fail(int s) { if (status == QTTS_OK) status = s; }
+    const LegacyTensor *find(const std::string &k)
+    {
+        auto it = m.find(k);
+        if (it == m.end()) { fail(QTTS_ERR_IO); return nullptr; }
+        return &it->second;
+    }
+    // binary_to_weight (loader.rs:148-170); F16 weights are not on the device path
+    qtts_q4_host weight(const std::string &k)
+    {
+        qtts_q4_host w{};
+        const LegacyTensor *t = find(k);
+        if (!t) return w;
+        if (t->shape.size() != 2) { fail(QTTS_ERR_IO); return w; }
+        if (t->format != 1) { fail(QTTS_ERR_UNSUPPORTED); return w; }
+        w.k = t->shape[0];
+        w.n = t->shape[1];
+        if (w.k <= 0 || w.n <= 0 || w.n % 32 || t->npacked != (uint64_t)(w.k * (w.n / 2)) ||
+            t->n16 != (uint64_t)(w.k * (w.n / 32))) {
+            fail(QTTS_ERR_IO);
+            return w;
+        }
+        w.packed = t->packed;
+        w.scales = t->f16;
+        return w;
+    }
+    // binary_to_f16 (loader.rs:139-145)
+    const uint16_t *f16v(const std::string &k, uint64_t expect)
+    {
+        const LegacyTensor *t = find(k);
+        if (!t) return nullptr;
+        if (t->format != 0 || t->n16 != expect) { fail(QTTS_ERR_IO); return nullptr; }
+        return t->f16;
+    }
+    // binary_to_f32 (loader.rs:130-136): f16 -> f32 is exact
+    const float *f32v(const std::string &k, uint64_t expect)
+    {
+        const uint16_t *h = f16v(k, expect);
+        if (!h) return nullptr;
+        f32.emplace_back(expect);
+        for (uint64_t i = 0; i < expect; i++) {
+            uint16_t b;
+            memcpy(&b, h + i, 2);
+            f32.back()[i] = half_to_float(b);
+        }
+        return f32.back().data();
+    }
+    static float half_to_float(uint16_t h)
+    {
+        const uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 0x1F, f = h & 0x3FF;
+        uint32_t bits;
+        if (e == 0) {
+            if (f == 0) {
+                bits = s;
+            } else {                               // subnormal: renormalise
+                int sh = 0;
+                uint32_t ff = f;
+                while (!(ff & 0x400)) { ff <<= 1; sh++; }
+                bits = s | ((uint32_t)(113 - sh) << 23) | ((ff & 0x3FF) << 13);
+            }
+        } else if (e == 31) {
+            bits = s | 0x7F800000u | (f << 13);
+        } else {
+            bits = s | ((e + 112) << 23) | (f << 13);
+        }
+        float v;
+        memcpy(&v, &bits, 4);
+        return v;
+    }
+    void layer(const std::string &pre, qtts_layer_host &L, int64_t hidden)
+    {
+        L.q_proj = weight(pre + ".self_attn.q_proj.weight");
+        L.k_proj = weight(pre + ".self_attn.k_proj.weight");
+        L.v_proj = weight(pre + ".self_attn.v_proj.weight");
+        L.o_proj = weight(pre + ".self_attn.o_proj.weight");
+        const LegacyTensor *qn = find(pre + ".self_attn.q_norm.weight");
+        const uint64_t hd = qn ? qn->n16 : 0;
+        L.q_norm = f16v(pre + ".self_attn.q_norm.weight", hd);
+        L.k_norm = f16v(pre + ".self_attn.k_norm.weight", hd);
+        L.gate_proj = weight(pre + ".mlp.gate_proj.weight");
+        L.up_proj = weight(pre + ".mlp.up_proj.weight");
+        L.down_proj = weight(pre + ".mlp.down_proj.weight");
+        L.input_norm = f16v(pre + ".input_layernorm.weight", (uint64_t)hidden);
+        L.post_attn_norm = f16v(pre + ".post_attention_layernorm.weight", (uint64_t)hidden);
+    }
+    int count(const std::string &pre, const std::string &post, int max)
+    {
+        int n = 0;
+        while (n < max && m.count(pre + std::to_string(n) + post)) n++;
+        return n;
+    }
+};
+
+}  // namespace
+
+extern "C" int qtts_model_load_qora_q4(qtts_ctx *ctx, const char *path, const qtts_rope_tables *rope)
+{
+    if (!ctx || !path || !rope || !rope->talker_cos || !rope->talker_sin || !rope->pred_cos || !rope->pred_sin ||
+        rope->talker_max_pos <= 0 || rope->pred_max_pos <= 0)
+        return QTTS_ERR_INVALID;
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) return QTTS_ERR_IO;
+    struct stat sb;
+    if (fstat(fd, &sb) != 0 || sb.st_size < 24) {
+        close(fd);
+        return QTTS_ERR_IO;
+    }
+    void *map = mmap(nullptr, (size_t)sb.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (map == MAP_FAILED) return QTTS_ERR_IO;
+    Reader r{(const uint8_t *)map, (const uint8_t *)map + sb.st_size};
+    LegacyModel M;
+    int rc = QTTS_ERR_IO;
+    std::vector<qtts_layer_host> tl, pl;
+    std::vector<qtts_q4_host> emb, heads;
+    qtts_talker_host t{};
+    qtts_predictor_host p{};
+    do {
+        if (!read_legacy_tensors(r, M.m)) break;
+        // talker (load_talker_binary, loader.rs:724-799)
+        const std::string tp = "talker.model.layers.";
+        t.n_layers = M.count(tp, ".self_attn.q_proj.weight", 256);
+        if (t.n_layers == 0) break;
+        const qtts_q4_host q0 = M.weight(tp + "0.self_attn.q_proj.weight");
+        const qtts_q4_host k0 = M.weight(tp + "0.self_attn.k_proj.weight");
+        const LegacyTensor *qn0 = M.find(tp + "0.self_attn.q_norm.weight");
+        if (M.status != QTTS_OK || !qn0 || qn0->n16 == 0) break;
+        t.hidden = (int32_t)q0.k;
+        t.head_dim = (int32_t)qn0->n16;
+        t.n_heads = (int32_t)(q0.n / t.head_dim);
+        t.n_kv_heads = (int32_t)(k0.n / t.head_dim);
+        tl.resize(t.n_layers);
+        for (int i = 0; i < t.n_layers; i++) M.layer(tp + std::to_string(i), tl[i], t.hidden);
+        t.layers = tl.data();
+        t.codec_embedding = M.weight("talker.model.codec_embedding.weight");
+        t.text_embedding = M.weight("talker.model.text_embedding.weight");
+        t.text_fc1 = M.weight("talker.text_projection.linear_fc1.weight");
+        t.text_fc1_bias = M.f32v("talker.text_projection.linear_fc1.bias", (uint64_t)t.text_fc1.n);
+        t.text_fc2 = M.weight("talker.text_projection.linear_fc2.weight");
+        t.text_fc2_bias = M.f32v("talker.text_projection.linear_fc2.bias", (uint64_t)t.text_fc2.n);
+        t.codec_head = M.weight("talker.codec_head.weight");
+        t.final_norm = M.f16v("talker.model.norm.weight", (uint64_t)t.hidden);
+        t.text_hidden = (int32_t)t.text_embedding.n;
+        t.inter = (int32_t)tl[0].gate_proj.n;
+        t.vocab = (int32_t)t.codec_head.n;
+        t.rope_cos = rope->talker_cos;
+        t.rope_sin = rope->talker_sin;
+        t.rope_max_pos = rope->talker_max_pos;
+        // code predictor (load_code_predictor_binary, loader.rs:801-882)
+        const std::string cp = "talker.code_predictor.";
+        p.n_layers = M.count(cp + "model.layers.", ".self_attn.q_proj.weight", 64);
+        p.n_groups = M.count(cp + "model.codec_embedding.", ".weight", 64);
+        if (M.status != QTTS_OK || p.n_layers == 0 || p.n_groups == 0 ||
+            M.count(cp + "lm_head.", ".weight", 64) != p.n_groups)
+            break;
+        if (M.m.count(cp + "small_to_mtp_projection.weight")) {
+            p.has_input_proj = 1;
+            p.input_proj = M.weight(cp + "small_to_mtp_projection.weight");
+            p.input_proj_bias = M.f32v(cp + "small_to_mtp_projection.bias", (uint64_t)p.input_proj.n);
+        }
+        const qtts_q4_host pq0 = M.weight(cp + "model.layers.0.self_attn.q_proj.weight");
+        const qtts_q4_host pk0 = M.weight(cp + "model.layers.0.self_attn.k_proj.weight");
+        const LegacyTensor *pqn0 = M.find(cp + "model.layers.0.self_attn.q_norm.weight");
+        if (M.status != QTTS_OK || !pqn0 || pqn0->n16 == 0) break;
+        p.hidden = (int32_t)pq0.k;
+        p.head_dim = (int32_t)pqn0->n16;
+        p.n_heads = (int32_t)(pq0.n / p.head_dim);
+        p.n_kv_heads = (int32_t)(pk0.n / p.head_dim);
+        emb.resize(p.n_groups);
+        heads.resize(p.n_groups);
+        for (int g = 0; g < p.n_groups; g++) {
+            emb[g] = M.weight(cp + "model.codec_embedding." + std::to_string(g) + ".weight");
+            heads[g] = M.weight(cp + "lm_head." + std::to_string(g) + ".weight");
+        }
+        pl.resize(p.n_layers);
+        for (int i = 0; i < p.n_layers; i++) M.layer(cp + "model.layers." + std::to_string(i), pl[i], p.hidden);
+        p.final_norm = M.f16v(cp + "model.norm.weight", (uint64_t)p.hidden);
+        p.layers = pl.data();
+        p.codec_embeddings = emb.data();
+        p.lm_heads = heads.data();
+        p.inter = (int32_t)pl[0].gate_proj.n;
+        p.vocab = (int32_t)heads[0].n;
+        p.rope_cos = rope->pred_cos;
+        p.rope_sin = rope->pred_sin;
+        p.rope_max_pos = rope->pred_max_pos;
+        if (M.status != QTTS_OK) break;
+        rc = qtts_model_upload(ctx, &t, &p);
+    } while (0);
+    if (rc == QTTS_ERR_IO && M.status != QTTS_OK) rc = M.status;
+    munmap(map, (size_t)sb.st_size);
+    return rc;
+}

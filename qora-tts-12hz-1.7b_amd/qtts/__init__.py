@@ -24,6 +24,13 @@ import numpy as np
 from . import hostdesc
 from .hostdesc import DecoderHost, PredictorHost, Q4Host, SampleParams, TalkerHost, decoder_host, ptr, sample_params
 
+
+class RopeTables(ctypes.Structure):
+    """qtts_rope_tables (include/qtts.h)."""
+    _fields_ = [("talker_cos", c_void_p), ("talker_sin", c_void_p), ("talker_max_pos", c_int64),
+                ("pred_cos", c_void_p), ("pred_sin", c_void_p), ("pred_max_pos", c_int64)]
+
+
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "libqtts_hip.so")
 
@@ -53,6 +60,7 @@ SIGNATURES = {
     "qtts_embed_lookup_q4": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
     "qtts_model_upload": ([c_void_p, POINTER(TalkerHost), POINTER(PredictorHost)], c_int),
     "qtts_model_load_qtts": ([c_void_p, c_char_p], c_int),
+    "qtts_model_load_qora_q4": ([c_void_p, c_char_p, c_void_p], c_int),
     "qtts_model_dims": ([c_void_p] + [POINTER(c_int32)] * 6, c_int),
     "qtts_talker_step": ([c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int], c_int),
     "qtts_talker_decode_token": ([c_void_p, c_uint32, c_int, c_int64, c_void_p, c_int], c_int),
@@ -215,6 +223,15 @@ class Context:
         self._check(self.lib.qtts_model_load_qtts(self.h, os.fsencode(path)))
         if self.has_decoder():
             self.dec_codebooks = self.decoder_dims()[0]
+        self.dims()
+
+    def load_qora_q4(self, path, talker_rope, pred_rope):
+        """The older "QORA-TTS-Q4" container (loader.rs:724-882); the RoPE
+        tables come from the caller as (cos, sin) pairs [max_pos][head_dim/2]."""
+        tc, ts = (np.ascontiguousarray(a, np.float32) for a in talker_rope)
+        pc, ps = (np.ascontiguousarray(a, np.float32) for a in pred_rope)
+        rt = RopeTables(tc.ctypes.data, ts.ctypes.data, tc.shape[0], pc.ctypes.data, ps.ctypes.data, pc.shape[0])
+        self._check(self.lib.qtts_model_load_qora_q4(self.h, os.fsencode(path), byref(rt)))
         self.dims()
 
     def dims(self):

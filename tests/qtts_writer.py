@@ -181,3 +181,69 @@ def write_qtts(path, talker, predictor, format_id=1, mrope_section=(24, 20, 20),
         _f32v(f, p.rope_sin.reshape(-1))
         if decoder is not None:
             _decoder(f, decoder)
+
+
+def _f16_bits(v):
+    return np.ascontiguousarray(np.asarray(v, np.float32).astype(np.float16)).view(np.uint16)
+
+
+def write_qora_q4(path, talker, predictor, f16_weights=()):
+    """The older "QORA-TTS-Q4" named-tensor container (loader.rs:47-127),
+    with the tensor names load_talker_binary / load_code_predictor_binary
+    map (loader.rs:724-882).  Biases are stored as F16, as the container
+    holds them; names in `f16_weights` are written in the F16 format (which
+    the device path refuses)."""
+    t, p = talker, predictor
+    items = []
+
+    def q4(name, w):
+        items.append((name, [w.k, w.n], w))
+
+    def f16(name, v):
+        items.append((name, [len(v)], _f16_bits(v) if np.asarray(v).dtype != np.uint16 else np.asarray(v, np.uint16)))
+
+    def layer(pre, L):
+        for nm, w in (("self_attn.q_proj", L.q_proj), ("self_attn.k_proj", L.k_proj), ("self_attn.v_proj", L.v_proj),
+                      ("self_attn.o_proj", L.o_proj), ("mlp.gate_proj", L.gate_proj), ("mlp.up_proj", L.up_proj),
+                      ("mlp.down_proj", L.down_proj)):
+            q4(f"{pre}.{nm}.weight", w)
+        f16(f"{pre}.self_attn.q_norm.weight", L.q_norm)
+        f16(f"{pre}.self_attn.k_norm.weight", L.k_norm)
+        f16(f"{pre}.input_layernorm.weight", L.input_norm)
+        f16(f"{pre}.post_attention_layernorm.weight", L.post_attn_norm)
+
+    for i, L in enumerate(t.layers):
+        layer(f"talker.model.layers.{i}", L)
+    q4("talker.model.codec_embedding.weight", t.codec_embedding)
+    q4("talker.model.text_embedding.weight", t.text_embedding)
+    q4("talker.text_projection.linear_fc1.weight", t.text_fc1)
+    f16("talker.text_projection.linear_fc1.bias", t.text_fc1_bias)
+    q4("talker.text_projection.linear_fc2.weight", t.text_fc2)
+    f16("talker.text_projection.linear_fc2.bias", t.text_fc2_bias)
+    q4("talker.codec_head.weight", t.codec_head)
+    f16("talker.model.norm.weight", t.final_norm)
+    q4("talker.code_predictor.small_to_mtp_projection.weight", p.input_proj)
+    f16("talker.code_predictor.small_to_mtp_projection.bias", p.input_proj_bias)
+    for g, w in enumerate(p.codec_embeddings):
+        q4(f"talker.code_predictor.model.codec_embedding.{g}.weight", w)
+    for i, L in enumerate(p.layers):
+        layer(f"talker.code_predictor.model.layers.{i}", L)
+    for g, w in enumerate(p.lm_heads):
+        q4(f"talker.code_predictor.lm_head.{g}.weight", w)
+    f16("talker.code_predictor.model.norm.weight", p.final_norm)
+    with open(path, "wb") as f:
+        f.write(b"QORA-TTS-Q4" + bytes(5))
+        f.write(struct.pack("<II", 1, len(items)))
+        for name, shape, data in items:
+            nb = name.encode()
+            f.write(struct.pack("<I", len(nb)) + nb)
+            f.write(struct.pack("<I", len(shape)) + b"".join(struct.pack("<I", d) for d in shape))
+            if hasattr(data, "packed") and name not in f16_weights:
+                sc = np.ascontiguousarray(data.scales, np.uint16).reshape(-1)
+                pk = np.ascontiguousarray(data.packed, np.uint8).reshape(-1)
+                f.write(bytes([1]) + struct.pack("<I", sc.size) + sc.tobytes() + struct.pack("<I", pk.size) + pk.tobytes())
+            elif hasattr(data, "packed"):
+                vals = _f16_bits(np.zeros(data.k * data.n, np.float32))
+                f.write(bytes([0]) + struct.pack("<I", vals.size) + vals.tobytes())
+            else:
+                f.write(bytes([0]) + struct.pack("<I", data.size) + data.tobytes())

@@ -11,7 +11,7 @@ import pytest
 import oracle as O
 import qtts
 from qtts import synth
-from qtts_writer import write_qtts
+from qtts_writer import write_qora_q4, write_qtts
 
 pytestmark = pytest.mark.gpu
 
@@ -123,3 +123,53 @@ def test_malformed_decoder_section(ctx_factory, full_file, tmp_path):
             c.load_qtts(str(f))
         assert e.value.code == qtts.ERR_IO, name
         assert not c.has_decoder(), name
+
+
+def test_qora_q4_container(ctx_factory, tmp_path):
+    """The older named-tensor container (loader.rs:47-127 read, 724-882
+    mapped): the same weights, biases rounded to f16 as the container stores
+    them, behave bit for bit like an upload; a bad header, a truncated file,
+    a missing lm head and an F16 linear weight fail with their statuses."""
+    from dataclasses import replace
+    r16 = lambda v: np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+    t = synth.make_talker(seed=321, n_layers=2, text_vocab=256, rope_max_pos=512)
+    p = synth.make_predictor(seed=322, n_layers=5, rope_max_pos=64)
+    t = replace(t, text_fc1_bias=r16(t.text_fc1_bias), text_fc2_bias=r16(t.text_fc2_bias))
+    p = replace(p, input_proj_bias=r16(p.input_proj_bias))
+    path = str(tmp_path / "legacy.qora-tts")
+    write_qora_q4(path, t, p)
+    ropes = ((t.rope_cos, t.rope_sin), (p.rope_cos, p.rope_sin))
+    a, b = ctx_factory(512), ctx_factory(512)
+    a.upload_model(t, p)
+    b.load_qora_q4(path, *ropes)
+    assert b.dims() == a.dims() == (t.hidden, t.vocab, len(t.layers), p.hidden, p.vocab, len(p.lm_heads))
+    rng = np.random.Generator(np.random.PCG64(33))
+    X = rng.standard_normal((12, t.hidden)).astype(np.float32)
+    ha, hb = a.prefill_talker_raw_from(X, 0), b.prefill_talker_raw_from(X, 0)
+    assert np.array_equal(bits(ha), bits(hb))
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    assert np.array_equal(bits(a.forward_with_embedding(emb, 12)), bits(b.forward_with_embedding(emb, 12)))
+    for tok in (0, 200):
+        assert np.array_equal(bits(a.embed_text_token(tok)), bits(b.embed_text_token(tok)))
+    sem = a.embed_codec_token(1500)
+    assert np.array_equal(a.generate_acoustic_codes(ha, sem), b.generate_acoustic_codes(hb, sem))
+
+    data = open(path, "rb").read()
+    c = ctx_factory(256)
+    bad = {"bad_header": (b"QORA-TTS-Q5" + data[11:], qtts.ERR_IO),
+           "truncated": (data[: len(data) // 2], qtts.ERR_IO),
+           "empty": (b"", qtts.ERR_IO)}
+    for name, (blob, code) in bad.items():
+        f = tmp_path / f"{name}.qora-tts"
+        f.write_bytes(blob)
+        with pytest.raises(qtts.QttsError) as e:
+            c.load_qora_q4(str(f), *ropes)
+        assert e.value.code == code, name
+    write_qora_q4(str(tmp_path / "short.qora-tts"), t, replace(p, lm_heads=p.lm_heads[:-1]))
+    with pytest.raises(qtts.QttsError) as e:
+        c.load_qora_q4(str(tmp_path / "short.qora-tts"), *ropes)
+    assert e.value.code == qtts.ERR_IO
+    write_qora_q4(str(tmp_path / "f16.qora-tts"), t, p, f16_weights={"talker.codec_head.weight"})
+    with pytest.raises(qtts.QttsError) as e:
+        c.load_qora_q4(str(tmp_path / "f16.qora-tts"), *ropes)
+    assert e.value.code == qtts.ERR_UNSUPPORTED
