@@ -264,6 +264,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape GEMV sweep")
     ap.add_argument("--decoder-only", action="store_true", help="time only the speech decoder")
     ap.add_argument("--no-decoder", action="store_true", help="skip the speech decoder")
+    ap.add_argument("--no-icl", action="store_true", help="skip the ICL workload (400-row prompt + 512 frames)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -364,7 +365,7 @@ def main():
 
     lg, hd, _, _ = ctx.gen_state()
     kernels["icl_prefill"] = time_prefill(ctx, args.layers)   # rewrites the KV cache
-    if args.layers == 28:
+    if args.layers == 28 and not args.no_icl:
         kernels["icl_decode"] = time_icl_decode(ctx, params, pad)
     if not args.no_sweep:
         kernels["q4_gemv_shapes"] = gemv_sweep(ctx, synth)
