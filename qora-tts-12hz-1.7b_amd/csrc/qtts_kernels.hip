@@ -1197,9 +1197,7 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
               const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
               int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
-    __shared__ float ssq[4][2];
-    __shared__ float qn[2][HEAD_DIM], kvn[2][HEAD_DIM];
-    __shared__ float qr[2][HEAD_DIM], knew[HEAD_DIM];
+    __shared__ float qr[2][HEAD_DIM], knew[HEAD_DIM], vnew[HEAD_DIM];
     __shared__ float pr[2][KV_PAGE];
     __shared__ float wred[4][2][2];
     __shared__ float ored[4][2][HEAD_DIM];
@@ -1215,16 +1213,20 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         const int c = item >> 3, h = item & 7;
         const int ntok = min(KV_PAGE, L - c * KV_PAGE);
         __syncthreads();                           // LDS of the previous item is free
-        // ---- loads: q / k-or-v partials, gammas, rope, then the page
-        float qp[RES_MAX_S], kp[RES_MAX_S];
+        // ---- loads: the wave's vector of the step (wave 0, 1: q heads 2h,
+        // 2h+1; wave 2: k head h; wave 3: v head h), lane l holding dims l
+        // and l+64 (a rotate-half pair), its gammas and RoPE values, then the page
+        const int base = (wv < 2 ? 2 * h + wv : 16 + 8 * (wv - 2) + h) * HEAD_DIM + lane;
+        float xa[RES_MAX_S], xb[RES_MAX_S];
 #pragma unroll
         for (int s = 0; s < RES_MAX_S; s++) {
-            const float *p = part + (size_t)min(s, S - 1) * npad;
-            qp[s] = p[(2 * h + sel) * HEAD_DIM + d];
-            kp[s] = p[16 * HEAD_DIM + sel * 8 * HEAD_DIM + h * HEAD_DIM + d];
+            const float *p = part + (size_t)min(s, S - 1) * npad + base;
+            xa[s] = p[0];
+            xb[s] = p[64];
         }
-        const uint32_t gq = qn_g[d], gk = kn_g[d];
-        const float cs = rope_cos[pos * 64 + (d & 63)], sn = rope_sin[pos * 64 + (d & 63)];
+        const uint16_t *gam = wv < 2 ? qn_g : kn_g;
+        const uint32_t ga = gam[lane], gb = gam[lane + 64];
+        const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
         const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
         const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
         f32x4 kk[8], vv[8];
@@ -1232,38 +1234,49 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
 #pragma unroll
         for (int i = 0; i < 8; i++) vv[i] = ld4nt(Vp + (vt0 + i) * HEAD_DIM + vd);
-        // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92)
-        float qv = qp[0], kvv = kp[0];
+        // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92) in
+        // registers: the sum of squares is the dims 0..63 wave sum plus the
+        // dims 64..127 wave sum, in that order
+        float a = xa[0], b = xb[0];
 #pragma unroll
         for (int s = 1; s < RES_MAX_S; s++) {
-            qv = s < S ? qv + qp[s] : qv;
-            kvv = s < S ? kvv + kp[s] : kvv;
+            a = s < S ? a + xa[s] : a;
+            b = s < S ? b + xb[s] : b;
         }
         for (int s = RES_MAX_S; s < S; s++) {
-            const float *p = part + (size_t)s * npad;
-            qv += p[(2 * h + sel) * HEAD_DIM + d];
-            kvv += p[16 * HEAD_DIM + sel * 8 * HEAD_DIM + h * HEAD_DIM + d];
+            const float *p = part + (size_t)s * npad + base;
+            a += p[0];
+            b += p[64];
         }
-        const float q2 = wave_sum_dpp(qv * qv), k2 = wave_sum_dpp(kvv * kvv);
-        if (lane == 0) { ssq[wv][0] = q2; ssq[wv][1] = k2; }
-        __syncthreads();
-        const float sq = ssq[2 * sel][0] + ssq[2 * sel + 1][0];
-        const float sk = ssq[0][1] + ssq[1][1];
-        qn[sel][d] = qv * (1.0f / sqrtf(sq / 128.0f + 1e-6f)) * h2f(gq);
-        kvn[sel][d] = sel ? kvv : kvv * (1.0f / sqrtf(sk / 128.0f + 1e-6f)) * h2f(gk);
-        __syncthreads();
-        qr[sel][d] = d < 64 ? qn[sel][d] * cs - qn[sel][d + 64] * sn : qn[sel][d] * cs + qn[sel][d - 64] * sn;
-        if (!sel) knew[d] = d < 64 ? kvn[0][d] * cs - kvn[0][d + 64] * sn : kvn[0][d] * cs + kvn[0][d - 64] * sn;
+        if (wv < 3) {
+            const float ss = wave_sum_dpp(a * a) + wave_sum_dpp(b * b);
+            const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
+            const float na = a * r * h2f(ga), nb = b * r * h2f(gb);
+            const float ra = na * cs - nb * sn, rb = nb * cs + na * sn;
+            float *dst = wv < 2 ? qr[wv] : knew;
+            dst[lane] = ra;
+            dst[lane + 64] = rb;
+            a = ra;
+            b = rb;
+        } else {
+            vnew[lane] = a;
+            vnew[lane + 64] = b;
+        }
+        if (c == C - 1 && wv >= 2) {
+            // append (talker.rs:299-302): K normed and roped, V raw
+            float *row = kv_ptr(kv, layer, slot, h, wv - 2);
+            row[lane] = a;
+            row[lane + 64] = b;
+        }
         __syncthreads();
         if (c == C - 1) {
-            // append (talker.rs:299-302), then patch the stale row in registers
-            kv_ptr(kv, layer, slot, h, sel)[d] = sel ? kvn[1][d] : knew[d];
+            // patch the stale row in registers (the page was read before the append)
             const int ts = slot - c * KV_PAGE;
             if (tk == ts) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) kk[i] = *(const f32x4 *)&knew[kq * 32 + 4 * i];
             }
-            const f32x4 vn = *(const f32x4 *)&kvn[1][vd];
+            const f32x4 vn = *(const f32x4 *)&vnew[vd];
 #pragma unroll
             for (int i = 0; i < 8; i++) vv[i] = vt0 + i == ts ? vn : vv[i];
         }
