@@ -510,7 +510,9 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
  *   kind 6: the talker step alone (28 layers + codec head), captured and
  *           replayed from the current KV length (QTTS_ERR_CAPACITY without
  *           room for iters + 1 positions); *bytes = its Q4 weight bytes.
- * Kinds 5 and 6 restore the generation state afterwards. */
+ * Kinds 5 and 6 restore the generation state afterwards (counters, the
+ * next frame's logits and hidden), so frames generated after the call are
+ * those that would have followed without it. */
 int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
                      double *avg_us, double *bytes);
 

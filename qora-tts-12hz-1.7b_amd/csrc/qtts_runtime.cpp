@@ -2138,8 +2138,12 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         if (kind == 6 && (c->h_st->kv_len + n > c->kv_cap || c->h_st->position + n > m.rope_rows))
             return fail(c, QTTS_ERR_CAPACITY, "no room in the KV cache to time %d talker steps", iters);
         hipSetDevice(c->device);
+        // the generation state: counters, the next frame's logits and hidden
         DevState saved;
+        std::vector<float> lg(m.vocab), hd(m.hidden);
         HIPCHK(c, hipMemcpyAsync(&saved, c->st_gen, sizeof saved, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(lg.data(), c->ws.logits, lg.size() * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipMemcpyAsync(hd.data(), c->ws.hidden, hd.size() * sizeof(float), hipMemcpyDeviceToHost, c->stream));
         HIPCHK(c, hipStreamSynchronize(c->stream));
         double w = 0.0;
         if (kind == 5) {
@@ -2173,6 +2177,8 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         const int rc = time_launches(c, iters, [&](int) { return hipGraphLaunch(ge, c->stream); }, avg_us);
         hipGraphExecDestroy(ge);
         HIPCHK(c, hipMemcpyAsync(c->st_gen, &saved, sizeof saved, hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(c->ws.logits, lg.data(), lg.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
+        HIPCHK(c, hipMemcpyAsync(c->ws.hidden, hd.data(), hd.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
         HIPCHK(c, hipStreamSynchronize(c->stream));
         return rc;
     }

@@ -112,3 +112,22 @@ def test_nan_logits_and_order(ctx_factory, model):
     codes, eos = c.gen_frames(3)
     assert codes.shape[0] == 3 and not eos
     assert c.gen_frames(0)[0].shape[0] == 0
+
+
+def test_frame_half_timing_between_frames(ctx_factory, model):
+    """qtts_time_kernel kinds 5 and 6 (each half of the frame replayed alone)
+    called in the middle of a generation leave it as it was: the frames that
+    follow are the ones an undisturbed run produces."""
+    t, p = model
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+    params = qtts.sample_params(eos_enabled=False)
+    begin(c, t, 16, params)
+    ref, _ = c.gen_frames(8)
+    begin(c, t, 16, params)
+    a, _ = c.gen_frames(4)
+    c.time_kernel(5, 3)
+    c.time_kernel(6, 3)
+    b, _ = c.gen_frames(4)
+    assert np.array_equal(np.concatenate([a, b]), ref)
+    assert c.kv_len() == 16 + 8
