@@ -265,6 +265,8 @@ def main():
     ap.add_argument("--decoder-only", action="store_true", help="time only the speech decoder")
     ap.add_argument("--no-decoder", action="store_true", help="skip the speech decoder")
     ap.add_argument("--no-icl", action="store_true", help="skip the ICL workload (400-row prompt + 512 frames)")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="time only the talker decode attention at KV 2048 (and the copy calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -291,6 +293,19 @@ def main():
         pf = time_prefill(ctx, args.layers)
         ctx.close()
         print(json.dumps({"prefill": pf}), flush=True)
+        return
+    if args.attention_only:
+        # 2048 cached positions from a prefill of N(0,1) rows, then one decode
+        # step's attention per layer (appending at 2048, attending 2049)
+        X = np.random.Generator(np.random.PCG64(7)).standard_normal((2048, talker.hidden)).astype(np.float32)
+        ctx.prefill_talker_raw_from(X, 0)
+        a_us, a_bytes = ctx.time_kernel(1, 4 * args.layers)
+        c_us, c_bytes = ctx.time_kernel(2, 20)
+        ctx.close()
+        print(json.dumps({"talker_attention": {"kv": 2049, "us": round(a_us, 2), "bytes": int(a_bytes),
+                                               "gbs": round(a_bytes / a_us / 1e3, 1)},
+                          "float4_copy_256MiB": {"us": round(c_us, 2), "gbs": round(c_bytes / c_us / 1e3, 1)}}),
+              flush=True)
         return
 
     rng = np.random.Generator(np.random.PCG64(42))
