@@ -66,6 +66,42 @@ __device__ __forceinline__ float wave_max_dpp(float v)
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// ---------------------------------------------------------------------------
+// gfx950 lane swaps on the VALU (no LDS crossbar round trip).  Of the
+// builtins' two results, the first holds operand a's even 16-lane rows
+// (32-lane halves) and b's even rows in the odd positions, the second a's
+// odd rows in the even positions and b's odd rows.
+// ---------------------------------------------------------------------------
+
+// Sum of the swap's two results.  Both pass through an empty register
+// constraint first: used directly in one add, the compiler reads the first
+// result twice.
+__device__ __forceinline__ float swap_pair_sum(unsigned a, unsigned b)
+{
+    asm volatile("" : "+v"(a), "+v"(b));
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+
+// v + (v of lane ^ 32).  The second operand is the same value passed through
+// an empty register copy, so the compiler cannot fold the two operands.
+__device__ __forceinline__ float add_xor32(float v)
+{
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    unsigned w;
+    asm volatile("" : "=v"(w) : "0"(u));
+    const auto r = __builtin_amdgcn_permlane32_swap(u, w, false, false);
+    return swap_pair_sum(r[0], r[1]);
+}
+
+// Lanes in even 16-lane rows return lo + (lo of lane ^ 16), lanes in odd
+// rows hi + (hi of lane ^ 16): one halving step of a reduce-scatter.
+__device__ __forceinline__ float add_xor16_split(float lo, float hi)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, lo),
+                                                    __builtin_bit_cast(unsigned, hi), false, false);
+    return swap_pair_sum(r[0], r[1]);
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p; }

@@ -838,7 +838,7 @@ __device__ __forceinline__ void rs_dpp_step(float (&v)[NB][32], bool sel)
 
 // Reduce-scatter of 32 column sums held by all 64 lanes of a wave.  Partner
 // masks in order: lane^15 (row_mirror), ^7 (row_half_mirror), ^3 and ^1
-// (quad permutes), ^16 (swizzle), then ^32 adds the last value; each mask
+// (quad permutes), ^16 (row swap), then ^32 adds the last value; each mask
 // leaves the bits chosen by earlier steps unchanged, so partners always hold
 // the same columns.  Lanes l and l^32 end with column wave_rs_col(l).
 template <int NB>
@@ -848,14 +848,8 @@ __device__ __forceinline__ void wave_rs32(float (&v)[NB][32], int lane)
     rs_dpp_step<8, 0x141, NB>(v, lane & 4);
     rs_dpp_step<4, 0x1B, NB>(v, lane & 2);
     rs_dpp_step<2, 0xB1, NB>(v, lane & 1);
-    const bool s16 = lane & 16;
 #pragma unroll
-    for (int b = 0; b < NB; b++) {
-        const float send = s16 ? v[b][0] : v[b][1];
-        const float keep = s16 ? v[b][1] : v[b][0];
-        v[b][0] = keep + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, send), 0x401F));
-        v[b][0] += __shfl_xor(v[b][0], 32);
-    }
+    for (int b = 0; b < NB; b++) v[b][0] = add_xor32(add_xor16_split(v[b][0], v[b][1]));
 }
 
 __device__ __forceinline__ int wave_rs_col(int lane)
@@ -1320,10 +1314,8 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             a1.z = ok ? fmaf(p1, v.z, a1.z) : a1.z; a1.w = ok ? fmaf(p1, v.w, a1.w) : a1.w;
         }
         // rows 8*(t/32): lanes l and l^32 of a wave hold the same dims
-        a0.x += __shfl_xor(a0.x, 32); a0.y += __shfl_xor(a0.y, 32);
-        a0.z += __shfl_xor(a0.z, 32); a0.w += __shfl_xor(a0.w, 32);
-        a1.x += __shfl_xor(a1.x, 32); a1.y += __shfl_xor(a1.y, 32);
-        a1.z += __shfl_xor(a1.z, 32); a1.w += __shfl_xor(a1.w, 32);
+        a0.x = add_xor32(a0.x); a0.y = add_xor32(a0.y); a0.z = add_xor32(a0.z); a0.w = add_xor32(a0.w);
+        a1.x = add_xor32(a1.x); a1.y = add_xor32(a1.y); a1.z = add_xor32(a1.z); a1.w = add_xor32(a1.w);
         if (lane < 32) {
             *(f32x4 *)&ored[wv][0][vd] = a0;
             *(f32x4 *)&ored[wv][1][vd] = a1;
