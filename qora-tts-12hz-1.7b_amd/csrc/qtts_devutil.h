@@ -109,11 +109,16 @@ __device__ __forceinline__ f32x4 ld4(const float *p) { return *(const f32x4 *)p;
 // less of the last-level cache than an ordinary load
 __device__ __forceinline__ f32x4 ld4nt(const float *p) { return __builtin_nontemporal_load((const f32x4 *)p); }
 
+// row `row` of physical page `pg`
+__device__ __forceinline__ float *kv_page_ptr(const KvPaged &kv, int layer, int pg, int row, int h, int isv)
+{
+    const size_t blk = ((size_t)layer * kv.n_phys + pg) * 2 + isv;
+    return kv.base + ((blk * 8 + h) * KV_PAGE + row) * HEAD_DIM;
+}
+
 __device__ __forceinline__ float *kv_ptr(const KvPaged &kv, int layer, int pos, int h, int isv)
 {
-    const int pg = kv.ptab[pos / KV_PAGE];
-    const size_t blk = ((size_t)layer * kv.n_phys + pg) * 2 + isv;
-    return kv.base + ((blk * 8 + h) * KV_PAGE + (pos % KV_PAGE)) * HEAD_DIM;
+    return kv_page_ptr(kv, layer, kv.ptab[pos / KV_PAGE], pos % KV_PAGE, h, isv);
 }
 
 // ---------------------------------------------------------------------------

@@ -1196,6 +1196,11 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
     __shared__ float wred[4][2][2];
     __shared__ float ored[4][2][HEAD_DIM];
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127, sel = t >> 7;
+    // the page-table entry of this workgroup's first page (an entry of the
+    // table for every workgroup of the launch) is read beside the sequence
+    // length; the page itself only once the length shows it is in use
+    const int pg0 = kv.ptab[min((int)(blockIdx.x >> 3), MAX_CHUNKS - 1)];
+    asm volatile("" ::: "memory");               // keeps the load above the length's
     const int slot = slot_ovr >= 0 ? slot_ovr : st->kv_len;
     const int64_t pos = pos_ovr >= 0 ? pos_ovr : st->position;
     const int L = slot + 1;
@@ -1221,8 +1226,9 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         const uint16_t *gam = wv < 2 ? qn_g : kn_g;
         const uint32_t ga = gam[lane], gb = gam[lane + 64];
         const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
-        const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0);
-        const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1);
+        const int pg = item == (int)blockIdx.x ? pg0 : kv.ptab[c];
+        const float *Kp = kv_page_ptr(kv, layer, pg, 0, h, 0);
+        const float *Vp = kv_page_ptr(kv, layer, pg, 0, h, 1);
         f32x4 kk[8], vv[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
