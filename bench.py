@@ -1,20 +1,25 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X decode path: codec frames/s, batch 1.
+"""Benchmark of the MI355X decode path: codec frames/s, batch 1, at KV 2048.
 
 Workload (one "step" = one frame): the full 28-layer Talker (hidden 2048,
 16/8 heads, FFN 6144, codec vocab 3072) plus the 5-layer code predictor
 (15 codebooks), random Q4 weights, a synthetic prompt of 64 text ids
 (uniform in [0, 151936)) embedded through the text projection and
-prefilled at positions 0..63, then --steps frames decoded with the KV cache
-growing from 64 (2048 frames: 64 -> 2112), top-k 50, temperature 0.9,
-repetition penalty 1.05, seed 42, EOS disabled (random weights can emit it).
+prefilled at positions 0..63, then the frame loop with top-k 50,
+temperature 0.9, repetition penalty 1.05, seed 42, EOS disabled (random
+weights can emit it).  The loop runs untimed from KV 64 to KV 2048 (the
+last --warmup of those frames are the warm-up), then --steps frames are
+timed from KV 2048 (64 steps: KV 2048 -> 2112, the last frames of the
+2048-frame workload).  The whole loop's average from KV 64 is reported
+beside it.
 
 Printed as one JSON line: frames/s over the timed frames (whole job, inputs
 resident in HBM); the roofline of the Q4 GEMV k=2048 -> n=6144 on a rotating
-pool of 64 weights (HIP events around back-to-back launches); the talker
-gate|up and attention kernels and a float4 copy (with --stream, the same
-GEMV kernel streaming a 113 MB weight); and the oracle's CPU frame rate on a
-bounded sample as the CPU baseline.
+pool of 64 weights (HIP events around back-to-back launches), with a
+streaming read of the same bytes as its attainable single-launch bound; the
+same GEMV kernel streaming a 113 MB weight; the talker gate|up and attention
+kernels and a float4 copy; and the oracle's CPU frame rate on a bounded
+sample at KV 2048 as the CPU baseline.
 """
 import argparse
 import json
@@ -31,6 +36,8 @@ HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix peak
 ICL_ROWS = 400                 # ICL prompt positions (text + reference codes)
 TTS_PAD = 151671          # generate_new.rs:28
+PROMPT = 64                    # prompt positions
+KV_HEADLINE = 2048             # KV length the headline frames start from
 
 
 # The standalone GEMV's kernel instance (tile G1_T256: one 32-column group x
@@ -253,13 +260,13 @@ def time_decoder(synth, qtts, cpu_frames=0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048, help="timed frames (KV grows from 64)")
+    ap.add_argument("--steps", type=int, default=64, help=f"timed frames from KV {KV_HEADLINE}")
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--gemv-copies", type=int, default=64)
-    ap.add_argument("--stream", action="store_true", help="also time the Q4 GEMV on a 2048 x 98304 weight")
+    ap.add_argument("--no-stream", action="store_true", help="skip the Q4 GEMV on a 2048 x 98304 weight")
     ap.add_argument("--prefill-only", action="store_true", help="time only the matrix-core prefill")
     ap.add_argument("--no-sweep", action="store_true", help="skip the per-shape GEMV sweep")
     ap.add_argument("--decoder-only", action="store_true", help="time only the speech decoder")
@@ -271,6 +278,10 @@ def main():
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               f"(one utterance's decode is a serial chain; independent text chunks would each take one GPU)", file=sys.stderr)
+        sys.exit(2)
+
+    if args.steps < 1 or KV_HEADLINE + args.steps > 8192:
+        print(f"--steps must be in 1..{8192 - KV_HEADLINE} (the cache holds 8192 positions)", file=sys.stderr)
         sys.exit(2)
 
     import qtts
@@ -285,7 +296,8 @@ def main():
     pred = synth.make_predictor(seed=2)
     log(f"synthetic model generated in {time.time() - t_gen:.1f}s")
 
-    ctx = qtts.Context(0, kv_capacity=4096)
+    cap = -(-(KV_HEADLINE + args.steps) // 64) * 64
+    ctx = qtts.Context(0, kv_capacity=max(cap, 4096))
     t_up = time.time()
     ctx.upload_model(talker, pred)
     log(f"uploaded in {time.time() - t_up:.1f}s")
@@ -309,21 +321,32 @@ def main():
         return
 
     rng = np.random.Generator(np.random.PCG64(42))
-    ids = rng.integers(0, 151936, 64)
+    ids = rng.integers(0, 151936, PROMPT)
     prompt = np.stack([ctx.embed_text_token(int(i)) for i in ids])
     pad = ctx.embed_text_token(TTS_PAD)
     ctx.gen_set_text(None, pad)
     hidden = ctx.prefill_talker_raw_from(prompt, 0)
     logits = ctx.apply_codec_head(hidden)
     params = qtts.sample_params(eos_enabled=False)
-    log("prefill done (64 positions)")
+    log(f"prefill done ({PROMPT} positions)")
 
-    # warm-up frames, then rewind the KV cache to the prompt
-    ctx.gen_begin(logits, hidden, 64, 42, params)
-    ctx.gen_frames(args.warmup)
-    ctx.kv_truncate(64)
-    ctx.gen_begin(logits, hidden, 64, 42, params)
+    # the frame loop from KV 64: untimed up to KV 2048 (its last --warmup
+    # frames are the warm-up), then --steps timed frames from KV 2048
+    warm = min(args.warmup, KV_HEADLINE - PROMPT)
+    ramp = KV_HEADLINE - PROMPT - warm
+    ctx.gen_begin(logits, hidden, PROMPT, 42, params)
     ctx.lib.qtts_sync(ctx.h)
+    t_ramp = time.perf_counter()
+    done, _ = ctx.gen_frames(ramp)
+    ctx.lib.qtts_sync(ctx.h)
+    t_ramp = time.perf_counter() - t_ramp
+    t_warm = time.perf_counter()
+    done2, _ = ctx.gen_frames(warm)
+    ctx.lib.qtts_sync(ctx.h)
+    t_warm = time.perf_counter() - t_warm
+    kv_start = ctx.kv_len()
+    assert kv_start == KV_HEADLINE and done.shape[0] + done2.shape[0] == KV_HEADLINE - PROMPT, kv_start
+    log(f"frames KV {PROMPT} -> {kv_start}: {(ramp + warm) / (t_ramp + t_warm):.1f} frames/s")
 
     t0 = time.perf_counter()
     codes, eos = ctx.gen_frames(args.steps)
@@ -331,7 +354,11 @@ def main():
     dt = time.perf_counter() - t0
     frames = codes.shape[0]
     fps = frames / dt
-    log(f"{frames} frames in {dt:.3f}s -> {fps:.1f} frames/s (KV 64 -> {64 + frames})")
+    log(f"{frames} frames in {dt:.4f}s -> {fps:.1f} frames/s (KV {kv_start} -> {kv_start + frames})")
+    loop_frames = ramp + warm + frames
+    loop = {"kv_start": PROMPT, "kv_end": kv_start + frames, "frames": loop_frames,
+            "frames_per_s": round(loop_frames / (t_ramp + t_warm + dt), 2),
+            "note": "the whole frame loop from the prompt, untimed ramp + warm-up + the timed frames"}
 
     # kernels at the final KV length (~2112): HIP events around back-to-back launches
     gu_us, gu_bytes = ctx.time_kernel(0, 4 * args.layers)
@@ -342,7 +369,8 @@ def main():
 
     # Q4 GEMV k=2048 -> n=6144 (the dominant kernel family: k_gemv is ~3/4 of
     # the frame's GPU time) over a pool of distinct weights (> 256 MB
-    # last-level cache), then the same kernel streaming a 113 MB weight
+    # last-level cache); a streaming read of the same bytes in one launch
+    # (its attainable bound); then the same kernel streaming a 113 MB weight
     grng = np.random.Generator(np.random.PCG64(1))
     pool = [ctx.upload(synth.q4_random(grng, 2048, 6144)) for _ in range(args.gemv_copies)]
     g_us, g_bytes = ctx.time_gemv(pool, 4 * args.gemv_copies)
@@ -350,11 +378,16 @@ def main():
         w.free()
     g_gbs = g_bytes / (g_us * 1e-6) / 1e9
     log(f"Q4 GEMV 2048x6144: {g_us:.2f}us/launch, {g_gbs:.0f} GB/s")
+    r_us, r_bytes = ctx.time_kernel(7, 256)
+    log(f"streaming read of the same {int(r_bytes)} B: {r_us:.2f}us/launch ({r_bytes / r_us / 1e3:.0f} GB/s)")
     traffic, traffic_src = measured_traffic(GEMV_KERNEL)
     roof = {"bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(g_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": f"{GEMV_KERNEL} (Q4 GEMV k=2048 -> n=6144, tile 1 group x 2048 rows)",
-            "avg_us": round(g_us, 3), "bytes_per_launch": int(g_bytes), "traffic_source": traffic_src}
+            "avg_us": round(g_us, 3), "bytes_per_launch": int(g_bytes), "traffic_source": traffic_src,
+            "attainable": {"what": "streaming read of the same bytes in one launch (64 rotating 7.1 MB buffers)",
+                           "us": round(r_us, 3), "gbs": round(r_bytes / r_us / 1e3, 1),
+                           "gemv_over_read": round(g_us / r_us, 3)}}
     kernels = {
         "talker_gate_up_rmsnorm": {"us": round(gu_us, 2), "gbs": round(gu_bytes / gu_us / 1e3, 1),
                                    "bytes": int(gu_bytes)},
@@ -363,10 +396,10 @@ def main():
         "float4_copy_256MiB": {"us": round(cp_us, 2), "gbs": round(cp_bytes / cp_us / 1e3, 1),
                                "bytes": int(cp_bytes)},
     }
-    if args.stream:
+    if not args.no_stream:
         # the same kernel streaming one 113 MB weight per launch (4 copies);
-        # opt-in, so the default run's profile line for the kernel covers the
-        # 2048 x 6144 launches alone
+        # --no-stream leaves it out, so that a profile's line for the kernel
+        # covers the 2048 x 6144 launches alone
         big = synth.q4_random(grng, 2048, 98304)
         pool = [ctx.upload(big) for _ in range(4)]
         s_us, s_bytes = ctx.time_gemv(pool, 32)
@@ -392,12 +425,12 @@ def main():
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline (oracle)")
-        cpu = cpu_baseline(talker, pred, lg, hd, pad, 2048, args.cpu_seconds)
+        cpu = cpu_baseline(talker, pred, lg, hd, pad, KV_HEADLINE, args.cpu_seconds)
         cpu["gemv_2048x6144"] = cpu_gemv()
         cpu["host"] = host_info()
         log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads; GEMV {cpu['gemv_2048x6144']}")
 
-    avg_bytes = float(np.mean([frame_bytes(64 + i) for i in range(frames)])) if args.layers == 28 else None
+    avg_bytes = float(np.mean([frame_bytes(kv_start + i) for i in range(frames)])) if args.layers == 28 else None
     frame_roof = None if avg_bytes is None else {
         "bound": "hbm", "bytes_per_frame_avg": int(avg_bytes), "bytes_per_frame_kv2048": frame_bytes(2048),
         "achieved": round(fps * avg_bytes / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -416,9 +449,11 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded random Q4 weights of the 1.7B shapes; random prompt ids)",
-        "config": {"workload": f"full frame loop: {args.layers}-layer talker + 5-layer predictor, 64-token prompt, "
-                               f"{frames} frames, KV 64->{64 + frames}, top-k 50, T 0.9, seed 42",
-                   "kv_start": 64, "kv_end": 64 + frames, "parallelism": "single GPU"},
+        "config": {"workload": f"frame loop at KV {kv_start}: {args.layers}-layer talker + 5-layer predictor, "
+                               f"64-token prompt, frames from KV 64 untimed to {kv_start}, then {frames} timed "
+                               f"frames KV {kv_start}->{kv_start + frames}, top-k 50, T 0.9, seed 42",
+                   "kv_start": kv_start, "kv_end": kv_start + frames, "parallelism": "single GPU"},
+        "frame_loop_from_prompt": loop,
         "roofline": roof,
         "frame_roofline": frame_roof,
         "kernels": kernels,

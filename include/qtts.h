@@ -509,7 +509,11 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
  *           Q4 weight bytes;
  *   kind 6: the talker step alone (28 layers + codec head), captured and
  *           replayed from the current KV length (QTTS_ERR_CAPACITY without
- *           room for iters + 1 positions); *bytes = its Q4 weight bytes.
+ *           room for iters + 1 positions); *bytes = its Q4 weight bytes;
+ *   kind 7: a streaming read of 7,110,656 B (the Q4 GEMV k=2048 -> n=6144's
+ *           bytes) in one launch, cycling 64 buffers (455 MB, beyond the
+ *           last-level cache; no model needed): the attainable time of a
+ *           single launch that moves those bytes.
  * Kinds 5 and 6 restore the generation state afterwards (counters, the
  * next frame's logits and hidden), so frames generated after the call are
  * those that would have followed without it. */

@@ -1195,7 +1195,7 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
     __shared__ float pr[2][KV_PAGE];
     __shared__ float wred[4][2][2];
     __shared__ float ored[4][2][HEAD_DIM];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127, sel = t >> 7;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127;
     // the page-table entry of this workgroup's first page (an entry of the
     // table for every workgroup of the launch) is read beside the sequence
     // length; the page itself only once the length shows it is in use
@@ -2747,6 +2747,37 @@ hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s)
     const int64_t n4 = n / 4;
     const int64_t grid = (n4 + 256 * 8 - 1) / (256 * 8);
     hipLaunchKernelGGL(k_copy_f4, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4 *)src, (u32x4 *)dst, n4);
+    return hipGetLastError();
+}
+
+// Streaming read of n4 16-byte words, 8 loads per thread in flight, as the
+// GEMV issues its weight tile: the attainable time of one launch that only
+// has to move the same bytes.  The loaded words are folded into one value
+// that is stored only if it equals `never` (the host passes a value the
+// data cannot fold to), so the loads stay and nothing is written.
+__global__ void __launch_bounds__(256) k_read_f4(const u32x4 *__restrict__ src, int64_t n4, uint32_t never,
+                                                 uint32_t *sink)
+{
+    constexpr int U = 8;
+    const int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int64_t i = base + (int64_t)u * 256;
+        v[u] = __builtin_nontemporal_load(src + (i < n4 ? i : n4 - 1));
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    if (acc == never) sink[0] = acc;
+}
+
+hipError_t enqueue_read(const float *src, int64_t n, uint32_t never, uint32_t *sink, hipStream_t s)
+{
+    if (n <= 0 || n % 4) return hipErrorInvalidValue;
+    const int64_t n4 = n / 4;
+    const int64_t grid = (n4 + 256 * 8 - 1) / (256 * 8);
+    hipLaunchKernelGGL(k_read_f4, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4 *)src, n4, never, sink);
     return hipGetLastError();
 }
 

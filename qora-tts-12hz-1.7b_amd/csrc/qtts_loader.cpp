@@ -353,7 +353,9 @@ extern "C" int qtts_model_load_qtts(qtts_ctx *ctx, const char *path)
         t.head_dim = (int32_t)r.get<uint32_t>();
         (void)r.get<uint32_t>();                                 // n_kv_groups
         const uint32_t nsec = r.get<uint32_t>();
-        if (!r.ok || nsec > 16 || t.n_layers <= 0 || t.n_layers > 256 || t.head_dim <= 0) break;
+        // the device kernels are built for 128-wide heads (both models' head_dim);
+        // anything else is refused before the layers are read
+        if (!r.ok || nsec > 16 || t.n_layers <= 0 || t.n_layers > 256 || t.head_dim != 128) break;
         for (uint32_t i = 0; i < nsec; i++) (void)r.get<uint32_t>();
         tl.resize(t.n_layers);
         for (auto &L : tl) read_layer(r, L, t.head_dim, t.hidden);
@@ -382,7 +384,7 @@ extern "C" int qtts_model_load_qtts(qtts_ctx *ctx, const char *path)
         p.head_dim = (int32_t)r.get<uint32_t>();
         (void)r.get<uint32_t>();
         const uint8_t has_proj = r.get<uint8_t>();
-        if (!r.ok || p.n_layers <= 0 || p.n_layers > 64 || p.head_dim <= 0) break;
+        if (!r.ok || p.n_layers <= 0 || p.n_layers > 64 || p.head_dim != 128) break;
         p.has_input_proj = has_proj == 1;
         if (p.has_input_proj) {
             p.input_proj = r.weight();

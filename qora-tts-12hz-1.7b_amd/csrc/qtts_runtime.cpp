@@ -67,6 +67,8 @@ struct qtts_ctx {
 
     float *d_copy = nullptr;                         // copy-calibration buffers, 2 x copy_floats
     int64_t copy_floats = 0;
+    float *d_read = nullptr;                         // streaming-read bound: READ_POOL buffers of READ_BYTES
+    uint32_t *d_sink = nullptr;
 
     PrefillWs pf{};                                  // batched-prefill rows (allocated on first use)
     void *pf_mem = nullptr;
@@ -447,6 +449,8 @@ extern "C" void qtts_ctx_destroy(qtts_ctx *c)
     if (c->d_io) hipFree(c->d_io);
     if (c->d_io2) hipFree(c->d_io2);
     if (c->d_copy) hipFree(c->d_copy);
+    if (c->d_read) hipFree(c->d_read);
+    if (c->d_sink) hipFree(c->d_sink);
     free_list(c->dec_allocs);
     if (c->dws_mem) hipFree(c->dws_mem);
     if (c->st_gen) hipFree(c->st_gen);
@@ -1185,6 +1189,11 @@ extern "C" int qtts_prefix_attach(qtts_ctx *c, const qtts_prefix *p)
         page_drop(c, c->seq_ptab[i]);
         c->seq_ptab[i] = pg;
     }
+    // Pages past the prefix may still be shared with another kept prefix
+    // (attaching a shorter prefix over a longer one's pages): the steps and
+    // frames that follow append there without a copy-on-write check, so
+    // they get private pages now.
+    RCHK(seq_unshare_from(c, p->len));
     RCHK(push_ptab(c));
     c->gen_started = false;
     c->h_st->kv_len = (int32_t)p->len;
@@ -2107,6 +2116,24 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         *bytes = 2.0 * n * sizeof(float);
         return time_launches(c, iters, [&](int) { return enqueue_copy(c->d_copy, c->d_copy + n, n, c->stream); },
                              avg_us);
+    }
+    if (kind == 7) {
+        // streaming read of the Q4 GEMV's bytes (k=2048 -> n=6144: 7,110,656 B)
+        // in one launch, cycling 64 buffers (455 MB, beyond the 256 MB
+        // last-level cache): the attainable time of a launch that moves the
+        // GEMV's bytes and nothing else
+        constexpr int64_t READ_BYTES = 7110656, READ_POOL = 64;
+        hipSetDevice(c->device);
+        if (!c->d_read) {
+            HIPCHK(c, hipMalloc(&c->d_read, READ_BYTES * READ_POOL));
+            HIPCHK(c, hipMalloc(&c->d_sink, sizeof(uint32_t)));
+            HIPCHK(c, hipMemsetAsync(c->d_read, 0, READ_BYTES * READ_POOL, c->stream));
+        }
+        *bytes = (double)READ_BYTES;
+        // zero words fold to 0, never to 1: the sink is never written
+        return time_launches(c, iters, [&](int i) {
+            return enqueue_read(c->d_read + (i % READ_POOL) * (READ_BYTES / 4), READ_BYTES / 4, 1u, c->d_sink, c->stream);
+        }, avg_us);
     }
     NEED_MODEL(c);
     const TalkerDev &m = c->tm;

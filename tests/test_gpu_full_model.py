@@ -24,13 +24,13 @@ def close(got, ref, rel=1e-3):
 
 @pytest.fixture(scope="module")
 def full(ctx_factory):
-    t = synth.make_talker(seed=801, text_vocab=256, rope_max_pos=1024)
+    t = synth.make_talker(seed=801, text_vocab=256, rope_max_pos=4096)
     p = synth.make_predictor(seed=802, rope_max_pos=64)
     assert len(t.layers) == 28 and t.hidden == 2048 and len(p.layers) == 5 and p.hidden == 1024
-    c = ctx_factory(1024)
+    c = ctx_factory(4096)
     c.upload_model(t, p)
     O.set_workers(16, 8)
-    om = O.Model(t, p, kv_cap=1024)
+    om = O.Model(t, p, kv_cap=4096)
     yield c, om, t, p
     om.close()
 
@@ -57,3 +57,36 @@ def test_full_model_prefill_and_frames(full):
     agree = (pred == ref).mean()
     assert agree >= 0.99, f"agreement {agree:.4f}"
     assert c.kv_len() == 16 + FRAMES
+
+
+def test_full_model_sampled_frames_kv2048(full):
+    c, om, t, p = full
+    L, n_frames = 2048, 16
+    print(f"28-layer frames from KV {L}", flush=True)
+    rng = np.random.Generator(np.random.PCG64(82))
+    n = len(t.layers)
+    K = rng.standard_normal((n, L, 8, 128), dtype=np.float32)
+    V = rng.standard_normal((n, L, 8, 128), dtype=np.float32)
+    c.kv_load(K, V)
+    om.kv_load(K, V)
+    del K, V
+    hid = rng.standard_normal(t.hidden).astype(np.float32)
+    logits = om.codec_head(hid)
+    pad = om.embed_text_token(3)
+    params = qtts.sample_params(eos_enabled=False)    # top-k 50, T 0.9, penalty 1.05
+    c.gen_set_text(None, pad)
+    om.gen_begin(logits, hid, L, 42)
+    c.gen_begin(logits, hid, L, 42, params)
+    ref = np.stack([om.frame(params, pad)[0] for _ in range(n_frames)])
+    pred = c.gen_frames_forced(ref)
+    assert np.array_equal(pred[:, 0], ref[:, 0]), f"sampled codes {pred[:, 0]} vs {ref[:, 0]}"
+    agree = (pred[:, 1:] == ref[:, 1:]).mean()
+    assert agree >= 0.99, f"predictor codes agree {agree:.4f}"
+    lg, hd, pos, rng_state = c.gen_state()
+    assert pos == L + n_frames and c.kv_len() == L + n_frames
+    assert rng_state == om.gen.rng
+    ok_h, eh = close(hd, om.g_hidden)
+    ok_l, el = close(lg, om.g_logits)
+    assert ok_h and ok_l, f"after {n_frames} frames: hidden rel err {eh}, logits {el}"
+    c.kv_reset()
+    om.kv_reset()

@@ -65,6 +65,11 @@ def test_malformed_files(ctx_factory, model_file, tmp_path):
         "f16_format": (data[:8] + bytes([0]) + data[9:], qtts.ERR_UNSUPPORTED),
         "empty": (b"", qtts.ERR_IO),
     }
+    # talker head_dim (u32 at byte 29: magic, version, format, then n_layers,
+    # hidden, text_hidden, n_heads, n_kv_heads): 1 once divided by zero in
+    # the RoPE table check; every width but 128 is refused with a status
+    for hd in (0, 1, 2, 64, 256):
+        cases[f"head_dim_{hd}"] = (data[:29] + hd.to_bytes(4, "little") + data[33:], qtts.ERR_IO)
     for name, (blob, code) in cases.items():
         f = tmp_path / f"{name}.qora-tts"
         f.write_bytes(blob)

@@ -431,3 +431,46 @@ def test_alternative_tiles_step_and_chain(ctx_factory, small_model, tiles, monke
     assert (got == ref).mean() >= 14 / 15, f"{tiles}: codes {got} vs {ref}"
     om.close()
     c.close()
+
+
+def test_onset_temperature_schedule(loaded):
+    """frame_temperature (generate_new.rs:82-88): frames 0..2 sample at the
+    onset temperature 0.3, later frames at 0.9.  Eight teacher-forced frames
+    in two calls (2 + 6, the boundary inside the onset window) sample the
+    oracle's code 0 draw for draw, so the frame count carries across calls;
+    the same seed without the onset samples other codes (the test can tell
+    the schedule from its absence)."""
+    ctx, om, t, p = loaded
+    params = qtts.sample_params(eos_enabled=False, onset_frames=3, onset_temperature=0.3)
+    plain = qtts.sample_params(eos_enabled=False)
+    rng = np.random.Generator(np.random.PCG64(13))
+    X = rng.standard_normal((16, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    hid = om.prefill(X, 0)
+    ctx.prefill_talker_raw_from(X, 0)
+    logits = om.codec_head(hid)
+    pad = om.embed_text_token(3)
+    ctx.gen_set_text(None, pad)
+
+    def oracle_frames(prm, n=8):
+        om.kv_reset()
+        om.prefill(X, 0)
+        om.gen_begin(logits, hid, 16, 42)
+        return np.stack([om.frame(prm, pad)[0] for _ in range(n)])
+
+    ref_plain = oracle_frames(plain)
+    ref = oracle_frames(params)
+    assert not np.array_equal(ref[:3, 0], ref_plain[:3, 0])
+    ctx.gen_begin(logits, hid, 16, 42, params)
+    pred = np.concatenate([ctx.gen_frames_forced(ref[:2]), ctx.gen_frames_forced(ref[2:])])
+    assert np.array_equal(pred[:, 0], ref[:, 0]), f"code 0: {pred[:, 0]} vs {ref[:, 0]}"
+    assert (pred[:, 1:] == ref[:, 1:]).mean() >= 0.99
+    # free-running, also split inside the onset window: the first frames
+    # match the oracle's onset run
+    ctx.kv_truncate(16)
+    ctx.gen_begin(logits, hid, 16, 42, params)
+    got = np.concatenate([ctx.gen_frames(2)[0], ctx.gen_frames(2)[0]])
+    assert np.array_equal(got, ref[:4]), f"{got[:, 0]} vs {ref[:4, 0]}"
+    ctx.kv_reset()
+    om.kv_reset()

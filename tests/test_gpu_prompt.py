@@ -170,6 +170,46 @@ def test_prefix_then_frames(ctx, model):
     ctx.kv_reset()
 
 
+def test_shorter_prefix_over_longer(ctx, model):
+    """Attach a 200-position prefix A, then a 64-position prefix B: the
+    sequence's pages past B's end were A's.  Steps and frames after B write
+    positions 64..150 into private pages, so A is untouched: attaching A
+    again and prefilling a suffix equals one full prefill bit for bit."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3350))
+    XA = rng.standard_normal((200, t.hidden)).astype(np.float32)
+    XB = rng.standard_normal((64, t.hidden)).astype(np.float32)
+    suf = rng.standard_normal((50, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    h_ref = ctx.prefill_talker_raw_from(np.concatenate([XA, suf]), 0, path="mfma")
+    kv_ref = [ctx.kv_gather(l) for l in range(len(t.layers))]
+    ctx.kv_reset()
+    ctx.prefill_talker_raw_from(XA, 0, path="mfma")
+    a = ctx.prefix_capture()
+    ctx.kv_reset()
+    hb = ctx.prefill_talker_raw_from(XB, 0, path="mfma")
+    b = ctx.prefix_capture()
+    ctx.prefix_attach(a)
+    ctx.prefix_attach(b)
+    assert ctx.kv_len() == 64
+    for i in range(3):
+        ctx.forward_with_embedding(rng.standard_normal(t.hidden).astype(np.float32), 64 + i)
+    pad = ctx.embed_text_tokens([TTS_PAD])[0]
+    ctx.gen_set_text(None, pad)
+    ctx.gen_begin(ctx.apply_codec_head(hb), hb, 67, 42, qtts.sample_params(eos_enabled=False))
+    codes, _ = ctx.gen_frames(84)
+    assert codes.shape[0] == 84 and ctx.kv_len() == 151
+    ctx.prefix_attach(a)
+    h = ctx.prefill_talker_raw_from(suf, 200, path="mfma")
+    assert np.array_equal(bits(h), bits(h_ref))
+    for l in range(len(t.layers)):
+        k, v = ctx.kv_gather(l)
+        assert np.array_equal(bits(k), bits(kv_ref[l][0])) and np.array_equal(bits(v), bits(kv_ref[l][1]))
+    a.free()
+    b.free()
+    ctx.kv_reset()
+
+
 def test_prefix_pool_capacity(ctx_factory, model):
     """kv_capacity 256: 4 sequence pages + 4 spare.  A kept prefix pins its
     pages; once the sequence has unshared them the pool is exhausted and a
