@@ -230,6 +230,19 @@ int qtts_gemv_q4(qtts_ctx *ctx, const qtts_w *w, const float *x, float *y,
 int qtts_gemm_q4(qtts_ctx *ctx, const qtts_w *w, const float *X, int64_t rows,
                  float *Y, int flags);
 
+/* qtts_gemm_q4 on DEVICE pointers X [rows][k] and Y [rows][n] that
+ * allocates nothing: no reference counterpart.  For callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops).  The GEMV passes' split-K partial sums use a 4 MiB device array
+ * held by the library on each GPU until the process ends; a weight whose
+ * passes need more (S * 2 * npad floats, S = ceil(k / 2048) for the
+ * default tile) is refused with QTTS_ERR_CAPACITY.  Only enqueues on the
+ * context stream (no synchronisation; qtts_sync or the stream from
+ * qtts_stream orders the results).  Calls that overlap on one GPU share
+ * that array and race.  flags: QTTS_PATH_* as for qtts_gemm_q4. */
+int qtts_gemm_q4_noalloc(qtts_ctx *ctx, const qtts_w *w, const float *X,
+                         int64_t rows, float *Y, int flags);
+
 /* out[n] = dequantised row `row`.  Replaces `embed_lookup_q4`
  * (gemv.rs:415-437); exact in f32. */
 int qtts_embed_lookup_q4(qtts_ctx *ctx, const qtts_w *w, int64_t row,

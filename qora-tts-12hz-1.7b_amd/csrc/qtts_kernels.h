@@ -170,6 +170,7 @@ hipError_t enqueue_embed_row(const Q4Rows &e, const uint32_t *code_dev, uint32_t
                              hipStream_t st);
 hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *codes, float *out, hipStream_t st);
 hipError_t enqueue_silu(float *x, int n, hipStream_t st);
+hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStream_t st);
 
 hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
                                hipStream_t s);

@@ -2227,6 +2227,21 @@ hipError_t enqueue_silu(float *x, int n, hipStream_t st)
     return hipGetLastError();
 }
 
+// Columns c0..c1-1 of rows [rows][ld] set to zero (a fill kernel rather than
+// a memset node, so the call can sit in a captured graph).
+__global__ void k_zero_cols(float *Y, int ld, int c0, int c1)
+{
+    const int j = c0 + blockIdx.x * blockDim.x + threadIdx.x;
+    if (j < c1) Y[(size_t)blockIdx.y * ld + j] = 0.0f;
+}
+
+hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStream_t st)
+{
+    if (rows <= 0 || c1 <= c0) return hipSuccess;
+    hipLaunchKernelGGL(k_zero_cols, dim3((c1 - c0 + 255) / 256, rows), dim3(256), 0, st, Y, ld, c0, c1);
+    return hipGetLastError();
+}
+
 hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *codes, float *out,
                              hipStream_t st)
 {

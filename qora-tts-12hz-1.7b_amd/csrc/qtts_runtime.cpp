@@ -13,6 +13,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -64,6 +65,8 @@ struct qtts_ctx {
 
     hipGraphExec_t frame_exec = nullptr;
     bool gen_started = false;
+
+    float *scratch = nullptr;                        // this device's copy of `scratch` (qtts_gemm_q4_noalloc)
 
     float *d_copy = nullptr;                         // copy-calibration buffers, 2 x copy_floats
     int64_t copy_floats = 0;
@@ -384,6 +387,35 @@ static void drop_graph(qtts_ctx *c)
     c->frame_exec = nullptr;
 }
 
+// ---------------------------------------------------------------------------
+// scratch of the allocation-free entry point (qtts_gemm_q4_noalloc): the
+// split-K partial sums of its GEMV passes live in this file-scope device
+// array, one copy per GPU, held until the process ends.  Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in):
+// its device address is looked up once per device, with that device
+// current, when the first context on the device is created.
+// ---------------------------------------------------------------------------
+
+constexpr size_t SCRATCH_FLOATS = (size_t)1 << 20;    // 4 MiB
+constexpr int SCRATCH_MAX_DEVICES = 64;
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+static std::mutex g_scratch_mu;
+static float *g_scratch_dev[SCRATCH_MAX_DEVICES];      // device address of `scratch` per device
+
+static hipError_t scratch_address(int device, float **out)
+{
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (device < 0 || device >= SCRATCH_MAX_DEVICES) return hipErrorInvalidDevice;
+    if (!g_scratch_dev[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_dev[device] = (float *)p;
+    }
+    *out = g_scratch_dev[device];
+    return hipSuccess;
+}
+
 extern "C" int qtts_ctx_create(int device, int64_t kv_capacity, qtts_ctx **out)
 {
     if (!out) return QTTS_ERR_INVALID;
@@ -401,6 +433,11 @@ extern "C" int qtts_ctx_create(int device, int64_t kv_capacity, qtts_ctx **out)
         return QTTS_ERR_HIP;
     }
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return QTTS_ERR_HIP;
+    }
+    if (scratch_address(device, &c->scratch) != hipSuccess) {
+        hipStreamDestroy(c->stream);
         delete c;
         return QTTS_ERR_HIP;
     }
@@ -596,6 +633,36 @@ extern "C" int qtts_gemm_q4(qtts_ctx *c, const qtts_w *w, const float *X, int64_
         HIPCHK(c, enqueue_gemv_rows(w->t, c->d_io, (int)rows, c->d_io2, w->part, c->stream));
     RCHK(stage_out(c, c->d_io2, rows * w->t.n, Y, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// qtts_gemm_q4 on device rows, allocating nothing: the GEMV passes' partial
+// sums go to this device's `scratch` (its address looked up when the
+// context was created), the ragged columns are cleared by a fill kernel,
+// and nothing is staged, so the call only enqueues kernels on the context
+// stream and returns.  Calls that overlap on one GPU (other contexts,
+// other host threads) share the array and race.
+extern "C" int qtts_gemm_q4_noalloc(qtts_ctx *c, const qtts_w *w, const float *X, int64_t rows, float *Y,
+                                    int flags)
+{
+    if (!c || !w || !X || !Y || rows < 0) return QTTS_ERR_INVALID;
+    if (rows == 0) return QTTS_OK;
+    if (rows > (1 << 24)) return fail(c, QTTS_ERR_CAPACITY, "at most %d rows", 1 << 24);
+    if (!c->scratch) return fail(c, QTTS_ERR_STATE, "no scratch address for device %d", c->device);
+    hipSetDevice(c->device);
+    const Q4Tiled &t = w->t;
+    if (use_mfma(flags, rows) && gemm_supported(t)) {
+        HIPCHK(c, enqueue_gemm_rows(t, X, (int)rows, Y, t.n, c->stream));
+    } else {
+        const size_t need = (size_t)t.S * 2 * t.npad;
+        if (need > SCRATCH_FLOATS)
+            return fail(c, QTTS_ERR_CAPACITY, "this weight's GEMV passes need %zu floats of scratch; the maximum is %zu",
+                        need, SCRATCH_FLOATS);
+        HIPCHK(c, enqueue_gemv_rows(t, X, (int)rows, Y, c->scratch, c->stream));
+    }
+    // columns past the last full group are zero (gemv.rs:255)
+    const int full = (t.n / 32) * 32;
+    HIPCHK(c, enqueue_zero_cols(Y, (int)rows, t.n, full, t.n, c->stream));
     return QTTS_OK;
 }
 

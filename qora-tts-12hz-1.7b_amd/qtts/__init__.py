@@ -57,6 +57,7 @@ SIGNATURES = {
     "qtts_q4_free": ([c_void_p, c_void_p], c_int),
     "qtts_gemv_q4": ([c_void_p, c_void_p, c_void_p, c_void_p, c_int], c_int),
     "qtts_gemm_q4": ([c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_gemm_q4_noalloc": ([c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
     "qtts_embed_lookup_q4": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
     "qtts_model_upload": ([c_void_p, POINTER(TalkerHost), POINTER(PredictorHost)], c_int),
     "qtts_model_load_qtts": ([c_void_p, c_char_p], c_int),
@@ -205,6 +206,16 @@ class Context:
         Y = np.empty((X.shape[0], w.n), np.float32)
         self._check(self.lib.qtts_gemm_q4(self.h, w.h, ptr(X), X.shape[0], ptr(Y), _PATH_FLAGS[path]))
         return Y
+
+    def gemm_noalloc(self, w, X_dev, rows, Y_dev, path=None):
+        """`gemm` on device addresses X_dev [rows][k] and Y_dev [rows][n]
+        with nothing allocated (qtts_gemm_q4_noalloc); enqueues only, call
+        sync() before reading Y."""
+        self._check(self.lib.qtts_gemm_q4_noalloc(self.h, w.h, c_void_p(X_dev), rows, c_void_p(Y_dev),
+                                                  _PATH_FLAGS[path]))
+
+    def sync(self):
+        self._check(self.lib.qtts_sync(self.h))
 
     def embed_lookup(self, w, row):
         """`embed_lookup_q4` (gemv.rs:415)."""
