@@ -1182,20 +1182,43 @@ __device__ __forceinline__ float qkv_head_prologue(const float *part, int S, int
 // (talker.rs:299-302) and patches that row in its registers (the page was
 // read before the append).  Writes per (page, query head) the max score, the
 // exp-sum and the unnormalised P.V.
-// Thread t: K rows t/4 (dims 32*(t%4)..+32); V dims 4*(t%32)..+4 of rows
-// 8*(t/32)..+8.
+//
+// Wave w owns page rows 16w..16w+15; lane l holds dims 4(l%32)..+4 of rows
+// 16w + 8(l/32) + i, i = 0..7, of both K and V, so every load instruction
+// reads two whole 512-byte rows.  A row's score is the sum of 32 lanes'
+// 4-dim partial dot products: a reduce-scatter over those lanes leaves the
+// score of (head (l>>3)&1, row i = l&7) in lanes l and l^16.  Each wave
+// forms its own softmax pieces (max, exp, sum, P.V over its 16 rows); one
+// barrier then merges the four waves, rescaled to the page maximum.
 // ---------------------------------------------------------------------------
+
+// One halving step of a reduce-scatter of N values across lanes: keep the
+// upper half when `sel`, adding the partner's copy (DPP exchange CTRL).
+template <int H, int CTRL, int N>
+__device__ __forceinline__ void rs_step_n(float (&v)[N], bool sel)
+{
+#pragma unroll
+    for (int j = 0; j < H; j++) {
+        const float lo = v[j] + dpp_mov<CTRL>(v[j]);
+        const float hi = v[j + H] + dpp_mov<CTRL>(v[j + H]);
+        v[j] = sel ? hi : lo;
+    }
+}
 
 __global__ void __launch_bounds__(256, 2)
 k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
               const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
               int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
-    __shared__ float qr[2][HEAD_DIM], knew[HEAD_DIM], vnew[HEAD_DIM];
-    __shared__ float pr[2][KV_PAGE];
-    __shared__ float wred[4][2][2];
-    __shared__ float ored[4][2][HEAD_DIM];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, d = t & 127;
+    __shared__ __attribute__((aligned(16))) float qr[2][HEAD_DIM];
+    __shared__ __attribute__((aligned(16))) float knew[HEAD_DIM];
+    __shared__ __attribute__((aligned(16))) float vnew[HEAD_DIM];
+    __shared__ __attribute__((aligned(16))) float pw[4][2][2][8];   // [wave][head][half][row] probabilities
+    __shared__ float wml[4][2][2];                                   // [wave][head][max, sum]
+    __shared__ __attribute__((aligned(16))) float ored[4][2][HEAD_DIM];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int half = lane >> 5, dl = lane & 31, d4 = 4 * dl;
+    const int row0 = 16 * wv + 8 * half;           // this lane's rows row0 + i, i = 0..7
     // the page-table entry of this workgroup's first page (an entry of the
     // table for every workgroup of the launch) is read beside the sequence
     // length; the page itself only once the length shows it is in use
@@ -1206,8 +1229,6 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
     const int L = slot + 1;
     const int C = (L + KV_PAGE - 1) / KV_PAGE;
     const float scale = 1.0f / sqrtf(128.0f);
-    const int tk = t >> 2, kq = t & 3;             // K: row, quarter of the dims
-    const int vd = (t & 31) * 4, vt0 = (t >> 5) * 8; // V: 4 dims, 8 rows
     for (int item = blockIdx.x; item < 8 * C; item += gridDim.x) {
         const int c = item >> 3, h = item & 7;
         const int ntok = min(KV_PAGE, L - c * KV_PAGE);
@@ -1227,13 +1248,13 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         const uint32_t ga = gam[lane], gb = gam[lane + 64];
         const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
         const int pg = item == (int)blockIdx.x ? pg0 : kv.ptab[c];
-        const float *Kp = kv_page_ptr(kv, layer, pg, 0, h, 0);
-        const float *Vp = kv_page_ptr(kv, layer, pg, 0, h, 1);
+        const float *Kp = kv_page_ptr(kv, layer, pg, row0, h, 0) + d4;
+        const float *Vp = kv_page_ptr(kv, layer, pg, row0, h, 1) + d4;
         f32x4 kk[8], vv[8];
 #pragma unroll
-        for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + tk * HEAD_DIM + kq * 32 + 4 * i);
+        for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + i * HEAD_DIM);
 #pragma unroll
-        for (int i = 0; i < 8; i++) vv[i] = ld4nt(Vp + (vt0 + i) * HEAD_DIM + vd);
+        for (int i = 0; i < 8; i++) vv[i] = ld4nt(Vp + i * HEAD_DIM);
         // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92) in
         // registers: the sum of squares is the dims 0..63 wave sum plus the
         // dims 64..127 wave sum, in that order
@@ -1272,69 +1293,78 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         if (c == C - 1) {
             // patch the stale row in registers (the page was read before the append)
             const int ts = slot - c * KV_PAGE;
-            if (tk == ts) {
+            const f32x4 kn = *(const f32x4 *)&knew[d4], vn = *(const f32x4 *)&vnew[d4];
 #pragma unroll
-                for (int i = 0; i < 8; i++) kk[i] = *(const f32x4 *)&knew[kq * 32 + 4 * i];
+            for (int i = 0; i < 8; i++) {
+                kk[i] = row0 + i == ts ? kn : kk[i];
+                vv[i] = row0 + i == ts ? vn : vv[i];
             }
-            const f32x4 vn = *(const f32x4 *)&vnew[vd];
-#pragma unroll
-            for (int i = 0; i < 8; i++) vv[i] = vt0 + i == ts ? vn : vv[i];
         }
-        // ---- scores of row tk for both query heads
-        float d0 = 0.0f, d1 = 0.0f;
+        // ---- 4-dim partial scores of the lane's 8 rows, both query heads,
+        // then the reduce-scatter over the half's 32 lanes (partner masks 15,
+        // 7, 3, 1 by DPP, then 16 by a row swap)
+        const f32x4 q0 = *(const f32x4 *)&qr[0][d4], q1 = *(const f32x4 *)&qr[1][d4];
+        float sc[16];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const f32x4 a = *(const f32x4 *)&qr[0][kq * 32 + 4 * i];
-            const f32x4 b = *(const f32x4 *)&qr[1][kq * 32 + 4 * i];
             const f32x4 k = kk[i];
-            d0 = fmaf(a.x, k.x, fmaf(a.y, k.y, fmaf(a.z, k.z, fmaf(a.w, k.w, d0))));
-            d1 = fmaf(b.x, k.x, fmaf(b.y, k.y, fmaf(b.z, k.z, fmaf(b.w, k.w, d1))));
+            sc[i] = fmaf(q0.x, k.x, fmaf(q0.y, k.y, fmaf(q0.z, k.z, q0.w * k.w)));
+            sc[8 + i] = fmaf(q1.x, k.x, fmaf(q1.y, k.y, fmaf(q1.z, k.z, q1.w * k.w)));
         }
-        d0 += dpp_mov<0xB1>(d0);
-        d0 += dpp_mov<0x4E>(d0);
-        d1 += dpp_mov<0xB1>(d1);
-        d1 += dpp_mov<0x4E>(d1);
-        const bool valid = tk < ntok;
-        const float s0 = valid ? d0 * scale : -INFINITY, s1 = valid ? d1 * scale : -INFINITY;
-        // ---- softmax_raw pieces over the page (gemv.rs:471-482)
-        const float mw0 = wave_max_dpp(s0), mw1 = wave_max_dpp(s1);
-        if (lane == 0) { wred[wv][0][0] = mw0; wred[wv][1][0] = mw1; }
-        __syncthreads();
-        const float m0 = fmaxf(fmaxf(wred[0][0][0], wred[1][0][0]), fmaxf(wred[2][0][0], wred[3][0][0]));
-        const float m1 = fmaxf(fmaxf(wred[0][1][0], wred[1][1][0]), fmaxf(wred[2][1][0], wred[3][1][0]));
-        const float e0 = valid ? expf(s0 - m0) : 0.0f, e1 = valid ? expf(s1 - m1) : 0.0f;
-        const float lw0 = wave_sum_dpp(kq == 0 ? e0 : 0.0f), lw1 = wave_sum_dpp(kq == 0 ? e1 : 0.0f);
-        if (lane == 0) { wred[wv][0][1] = lw0; wred[wv][1][1] = lw1; }
-        if (kq == 0) { pr[0][tk] = e0; pr[1][tk] = e1; }
-        __syncthreads();
-        // ---- P.V over this thread's 8 rows and 4 dims, both heads
+        rs_step_n<8, 0x140, 16>(sc, lane & 8);
+        rs_step_n<4, 0x141, 16>(sc, lane & 4);
+        rs_step_n<2, 0x1B, 16>(sc, lane & 2);
+        rs_step_n<1, 0xB1, 16>(sc, lane & 1);
+        const float dot = add_xor16_split(sc[0], sc[0]);
+        const int hh = (lane >> 3) & 1, ri = lane & 7, row = row0 + ri;
+        const bool valid = row < ntok;
+        const float sv = valid ? dot * scale : -INFINITY;
+        // ---- softmax_raw pieces over the wave's rows (gemv.rs:471-482)
+        const float m0 = wave_max_dpp(hh == 0 ? sv : -INFINITY), m1 = wave_max_dpp(hh == 1 ? sv : -INFINITY);
+        const float e = valid ? expf(sv - (hh ? m1 : m0)) : 0.0f;
+        const bool first = (lane & 16) == 0;       // one of the two lanes holding each value
+        const float l0 = wave_sum_dpp(first && hh == 0 ? e : 0.0f), l1 = wave_sum_dpp(first && hh == 1 ? e : 0.0f);
+        if (first) pw[wv][hh][half][ri] = e;
+        if (lane == 0) { wml[wv][0][0] = m0; wml[wv][0][1] = l0; wml[wv][1][0] = m1; wml[wv][1][1] = l1; }
+        __builtin_amdgcn_wave_barrier();
+        // ---- P.V over the lane's 8 rows and 4 dims, both heads
+        const f32x4 pa0 = *(const f32x4 *)&pw[wv][0][half][0], pa1 = *(const f32x4 *)&pw[wv][0][half][4];
+        const f32x4 pb0 = *(const f32x4 *)&pw[wv][1][half][0], pb1 = *(const f32x4 *)&pw[wv][1][half][4];
+        const float p0[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
+        const float p1[8] = {pb0.x, pb0.y, pb0.z, pb0.w, pb1.x, pb1.y, pb1.z, pb1.w};
         f32x4 a0 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const bool ok = vt0 + i < ntok;              // rows past the page's end may hold anything
-            const float p0 = pr[0][vt0 + i], p1 = pr[1][vt0 + i];
+            const bool ok = row0 + i < ntok;             // rows past the page's end may hold anything
             const f32x4 v = vv[i];
-            a0.x = ok ? fmaf(p0, v.x, a0.x) : a0.x; a0.y = ok ? fmaf(p0, v.y, a0.y) : a0.y;
-            a0.z = ok ? fmaf(p0, v.z, a0.z) : a0.z; a0.w = ok ? fmaf(p0, v.w, a0.w) : a0.w;
-            a1.x = ok ? fmaf(p1, v.x, a1.x) : a1.x; a1.y = ok ? fmaf(p1, v.y, a1.y) : a1.y;
-            a1.z = ok ? fmaf(p1, v.z, a1.z) : a1.z; a1.w = ok ? fmaf(p1, v.w, a1.w) : a1.w;
+            a0.x = ok ? fmaf(p0[i], v.x, a0.x) : a0.x; a0.y = ok ? fmaf(p0[i], v.y, a0.y) : a0.y;
+            a0.z = ok ? fmaf(p0[i], v.z, a0.z) : a0.z; a0.w = ok ? fmaf(p0[i], v.w, a0.w) : a0.w;
+            a1.x = ok ? fmaf(p1[i], v.x, a1.x) : a1.x; a1.y = ok ? fmaf(p1[i], v.y, a1.y) : a1.y;
+            a1.z = ok ? fmaf(p1[i], v.z, a1.z) : a1.z; a1.w = ok ? fmaf(p1[i], v.w, a1.w) : a1.w;
         }
-        // rows 8*(t/32): lanes l and l^32 of a wave hold the same dims
+        // the two halves hold the same dims of rows 8 apart
         a0.x = add_xor32(a0.x); a0.y = add_xor32(a0.y); a0.z = add_xor32(a0.z); a0.w = add_xor32(a0.w);
         a1.x = add_xor32(a1.x); a1.y = add_xor32(a1.y); a1.z = add_xor32(a1.z); a1.w = add_xor32(a1.w);
         if (lane < 32) {
-            *(f32x4 *)&ored[wv][0][vd] = a0;
-            *(f32x4 *)&ored[wv][1][vd] = a1;
+            *(f32x4 *)&ored[wv][0][d4] = a0;
+            *(f32x4 *)&ored[wv][1][d4] = a1;
         }
         __syncthreads();
         {
-            const int hh = t >> 7;
-            const float o = (ored[0][hh][d] + ored[1][hh][d]) + (ored[2][hh][d] + ored[3][hh][d]);
-            aacc[((size_t)c * 16 + 2 * h + hh) * HEAD_DIM + d] = o;
+            // the four waves merged at the page maximum, in wave order
+            const int oh = t >> 7, d = t & 127;
+            const float M = fmaxf(fmaxf(wml[0][oh][0], wml[1][oh][0]), fmaxf(wml[2][oh][0], wml[3][oh][0]));
+            float o = 0.0f, ls = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float f = expf(wml[w][oh][0] - M);   // 0 for a wave with no valid row
+                o = fmaf(f, ored[w][oh][d], o);
+                ls = fmaf(f, wml[w][oh][1], ls);
+            }
+            aacc[((size_t)c * 16 + 2 * h + oh) * HEAD_DIM + d] = o;
             if (d == 0) {
-                am[(2 * h + hh) * MAX_CHUNKS + c] = hh ? m1 : m0;
-                al[(2 * h + hh) * MAX_CHUNKS + c] = hh ? (wred[0][1][1] + wred[1][1][1]) + (wred[2][1][1] + wred[3][1][1])
-                                             : (wred[0][0][1] + wred[1][0][1]) + (wred[2][0][1] + wred[3][0][1]);
+                am[(2 * h + oh) * MAX_CHUNKS + c] = M;
+                al[(2 * h + oh) * MAX_CHUNKS + c] = ls;
             }
         }
     }
