@@ -106,8 +106,10 @@ def host_info():
 
 
 def cpu_gemv(seconds=3.0):
-    """The oracle's restatement of gemv_q4 (AVX2 kernel + chunk/pool policy)
-    on the 2048 x 6144 GEMV: min(nproc, 16) workers and one thread."""
+    """The oracle's restatement of gemv_q4 (chunk/pool policy) on the
+    2048 x 6144 GEMV: min(nproc, 16) workers and one thread, with the inner
+    kernel the reference picks on this host (gemv.rs:230-243: AVX-512 when
+    present) and with the AVX2 kernel beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     from qtts import synth
@@ -116,27 +118,36 @@ def cpu_gemv(seconds=3.0):
     x = rng.standard_normal(2048).astype(np.float32)
     nbytes = 2048 * 6144 * 0.5625 + 4 * 2048 + 4 * 6144
     res = {}
-    for label, workers in (("pool", min(os.cpu_count() or 1, 16)), ("one_thread", 1)):
-        oracle.set_workers(workers, workers)
-        oracle.gemv(x, w)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds / 2:
+    isas = [oracle.set_isa(None)]
+    if isas[0] != "avx2" and oracle.set_isa("avx2"):
+        isas.append("avx2")
+    for isa in isas:
+        oracle.set_isa(None if isa == isas[0] else isa)
+        for label, workers in (("pool", min(os.cpu_count() or 1, 16)), ("one_thread", 1)):
+            oracle.set_workers(workers, workers)
             oracle.gemv(x, w)
-            n += 1
-        us = (time.perf_counter() - t0) / n * 1e6
-        res[label] = {"threads": workers, "us": round(us, 1), "gbs": round(nbytes / us / 1e3, 2)}
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < seconds / (2 * len(isas)):
+                oracle.gemv(x, w)
+                n += 1
+            us = (time.perf_counter() - t0) / n * 1e6
+            key = label if isa == isas[0] else f"{label}_{isa}"
+            res[key] = {"threads": workers, "isa": isa, "us": round(us, 1), "gbs": round(nbytes / us / 1e3, 2)}
+    oracle.set_isa(None)
     return res
 
 
-def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds):
-    """Oracle (C restatement of the reference's AVX2 CPU path, gemv pool of
-    min(nproc, 16) workers) timed on a bounded sample: frames at KV ~kv_len
-    after a synthetic N(0,1) KV prefill."""
+def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds, isa=None):
+    """Oracle (C restatement of the reference's CPU path, gemv pool of
+    min(nproc, 16) workers, the inner GEMV kernel the reference picks on this
+    host or `isa`) timed on a bounded sample: frames at KV ~kv_len after a
+    synthetic N(0,1) KV prefill."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     import qtts
     workers = min(os.cpu_count() or 1, 16)
     oracle.set_workers(workers, workers)
+    used_isa = oracle.set_isa(isa)
     om = oracle.Model(talker, pred, kv_cap=kv_len + 64)
     rng = np.random.Generator(np.random.PCG64(7))
     L = len(talker.layers)
@@ -155,9 +166,10 @@ def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds):
         if el >= seconds or n >= 64:
             break
     om.close()
-    return {"value": n / el, "unit": "frames/s", "cores": workers, "kind": "port",
+    oracle.set_isa(None)
+    return {"value": n / el, "unit": "frames/s", "cores": workers, "kind": "port", "isa": used_isa,
             "sample": f"{n} frames of the 28-layer talker + 5-layer predictor at KV {kv_len}..{kv_len + n} "
-                      f"(synthetic N(0,1) KV prefill), {el:.1f} s"}
+                      f"(synthetic N(0,1) KV prefill), {el:.1f} s, {used_isa} GEMV kernel"}
 
 
 def time_prefill(ctx, layers):
@@ -462,6 +474,9 @@ def main():
     if not args.no_cpu:
         log("timing the CPU baseline (oracle)")
         cpu = cpu_baseline(talker, pred, lg, hd, pad, KV_HEADLINE, args.cpu_seconds)
+        if cpu["isa"] != "avx2":
+            a2 = cpu_baseline(talker, pred, lg, hd, pad, KV_HEADLINE, args.cpu_seconds / 2, isa="avx2")
+            cpu["avx2"] = {"value": a2["value"], "sample": a2["sample"]}
         cpu["gemv_2048x6144"] = cpu_gemv()
         cpu["host"] = host_info()
         log(f"cpu baseline {cpu['value']:.3f} frames/s on {cpu['cores']} threads; GEMV {cpu['gemv_2048x6144']}")

@@ -40,6 +40,9 @@ _SIG = {
     "oq_simple_rand": ([POINTER(c_uint64)], c_float),
     "oq_gemv_q4_scalar": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], None),
     "oq_gemv_q4_avx2": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], c_int),
+    "oq_gemv_q4_avx512": ([c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p], c_int),
+    "oq_set_isa": ([c_int], c_int),
+    "oq_get_isa": ([], c_int),
     "oq_set_workers": ([c_int, c_int], None),
     "oq_get_workers": ([], c_int),
     "oq_gemv_q4": ([c_void_p, POINTER(Q4Host), c_void_p], None),
@@ -130,6 +133,30 @@ def gemv_avx2(x, w, k0=0, k1=None):
     out = np.empty(w.n, np.float32)
     ok = lib().oq_gemv_q4_avx2(ptr(x), ptr(w.packed), ptr(w.scales), w.n, k0, w.k if k1 is None else k1, ptr(out))
     return out if ok else None
+
+
+def gemv_avx512(x, w, k0=0, k1=None):
+    """gemv_q4_avx512 (simd.rs:203-269); None when the host lacks AVX-512."""
+    x = f32(x)
+    out = np.empty(w.n, np.float32)
+    ok = lib().oq_gemv_q4_avx512(ptr(x), ptr(w.packed), ptr(w.scales), w.n, k0, w.k if k1 is None else k1, ptr(out))
+    return out if ok else None
+
+
+ISA_NAMES = {0: "scalar", 1: "avx2", 2: "avx512f"}
+
+
+def set_isa(isa=None):
+    """Inner GEMV kernel of the chunked GEMV: None for the reference's own
+    choice (gemv.rs:230-243: AVX-512, else AVX2, else scalar), or "scalar",
+    "avx2", "avx512f".  Returns the ISA in use, None if the host lacks it."""
+    code = -1 if isa is None else {v: k for k, v in ISA_NAMES.items()}[isa]
+    r = lib().oq_set_isa(code)
+    return None if r < 0 else ISA_NAMES[r]
+
+
+def get_isa():
+    return ISA_NAMES[lib().oq_get_isa()]
 
 
 def set_workers(workers=16, threads=0):

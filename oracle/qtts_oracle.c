@@ -192,18 +192,97 @@ int oq_gemv_q4_avx2(const float *x, const uint8_t *packed,
     return 1;
 }
 
-/* The inner kernel the chunked GEMV calls (gemv.rs:230-243 picks the SIMD
- * kernel; all of them are bit-identical to the scalar one). */
+/* gemv_q4_avx512 (simd.rs:203-269): per group the 16-entry table
+ * lut = (q - 8) * s as one 16-lane product, the low and high nibbles of the
+ * 16 packed bytes looked up in it, then interleaved back to column order
+ * (lanes 0,16,1,17,... and 8,24,9,25,...) and added to the outputs. */
+__attribute__((target("avx512f")))
+static void gemv_q4_avx512_impl(const float *x, const uint8_t *packed,
+                                const uint16_t *scales, int64_t n, int64_t k0,
+                                int64_t k1, float *out)
+{
+    const int64_t groups = n / GROUP;
+    const int64_t row_bytes = groups * PACKED_PER_GROUP;
+    memset(out, 0, (size_t)n * sizeof(float));
+    float fac[16];
+    int32_t il_first[16], il_second[16];
+    for (int i = 0; i < 16; i++) {
+        fac[i] = (float)(i - 8);
+        il_first[i] = (i & 1) ? 16 + i / 2 : i / 2;        /* lo[i/2] or hi[i/2]       */
+        il_second[i] = (i & 1) ? 24 + i / 2 : 8 + i / 2;   /* lo[8+i/2] or hi[8+i/2]   */
+    }
+    const __m512 factors = _mm512_loadu_ps(fac);
+    const __m512i ilo = _mm512_loadu_si512((const void *)il_first);
+    const __m512i ihi = _mm512_loadu_si512((const void *)il_second);
+    const __m512i mask = _mm512_set1_epi32(0x0F);
+    for (int64_t ki = k0; ki < k1; ki++) {
+        const float xv = x[ki];
+        if (xv == 0.0f) continue;
+        const int64_t sb = ki * groups;
+        const int64_t pb = ki * row_bytes;
+        for (int64_t g = 0; g < groups; g++) {
+            const float s = oq_f16_to_f32(scales[sb + g]) * xv;
+            if (s == 0.0f) continue;
+            const __m512 lut = _mm512_mul_ps(factors, _mm512_set1_ps(s));
+            const __m128i bytes =
+                _mm_loadu_si128((const __m128i *)(packed + pb + g * PACKED_PER_GROUP));
+            const __m512i b32 = _mm512_cvtepu8_epi32(bytes);
+            const __m512 lov = _mm512_permutexvar_ps(_mm512_and_epi32(b32, mask), lut);
+            const __m512 hiv = _mm512_permutexvar_ps(_mm512_srli_epi32(b32, 4), lut);
+            const __m512 first = _mm512_permutex2var_ps(lov, ilo, hiv);
+            const __m512 second = _mm512_permutex2var_ps(lov, ihi, hiv);
+            float *o = out + g * GROUP;
+            _mm512_storeu_ps(o, _mm512_add_ps(_mm512_loadu_ps(o), first));
+            _mm512_storeu_ps(o + 16, _mm512_add_ps(_mm512_loadu_ps(o + 16), second));
+        }
+    }
+}
+
+static int host_has_avx512(void)
+{
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f");
+}
+
+int oq_gemv_q4_avx512(const float *x, const uint8_t *packed,
+                      const uint16_t *scales, int64_t n, int64_t k0, int64_t k1,
+                      float *out)
+{
+    if (!host_has_avx512()) return 0;
+    gemv_q4_avx512_impl(x, packed, scales, n, k0, k1, out);
+    return 1;
+}
+
+/* ISA of the inner kernel: -1 as gemv_q4_inner picks it (gemv.rs:230-243:
+ * AVX-512 when the host has it, else AVX2, else scalar), or forced to
+ * OQ_ISA_SCALAR / OQ_ISA_AVX2 / OQ_ISA_AVX512 (when the host has it).  All
+ * three are bit-identical to the scalar kernel. */
+static int g_isa = -1;
+
+int oq_set_isa(int isa)
+{
+    if (isa == OQ_ISA_AVX512 && !host_has_avx512()) return -1;
+    if (isa == OQ_ISA_AVX2 && !host_has_avx2()) return -1;
+    g_isa = isa;
+    return oq_get_isa();
+}
+
+int oq_get_isa(void)
+{
+    if (g_isa >= 0) return g_isa;
+    return host_has_avx512() ? OQ_ISA_AVX512 : host_has_avx2() ? OQ_ISA_AVX2 : OQ_ISA_SCALAR;
+}
+
+/* The inner kernel the chunked GEMV calls. */
 static void gemv_inner(const float *x, const uint8_t *packed,
                        const uint16_t *scales, int64_t n, int64_t k0,
                        int64_t k1, float *out)
 {
-    static int avx2 = -1;
-    if (avx2 < 0) avx2 = host_has_avx2();
-    if (avx2)
-        gemv_q4_avx2_impl(x, packed, scales, n, k0, k1, out);
-    else
-        oq_gemv_q4_scalar(x, packed, scales, n, k0, k1, out);
+    switch (oq_get_isa()) {
+    case OQ_ISA_AVX512: gemv_q4_avx512_impl(x, packed, scales, n, k0, k1, out); break;
+    case OQ_ISA_AVX2: gemv_q4_avx2_impl(x, packed, scales, n, k0, k1, out); break;
+    default: oq_gemv_q4_scalar(x, packed, scales, n, k0, k1, out); break;
+    }
 }
 
 /* ---- persistent chunk pool (gpool.rs:17-66 restated with pthreads) ---- */

@@ -42,6 +42,14 @@ void oq_gemv_q4_scalar(const float *x, const uint8_t *packed,
 int  oq_gemv_q4_avx2(const float *x, const uint8_t *packed,
                      const uint16_t *scales, int64_t n, int64_t k0,
                      int64_t k1, float *out);
+/* gemv_q4_avx512 (simd.rs:203-269); 0 when the host lacks AVX-512. */
+int  oq_gemv_q4_avx512(const float *x, const uint8_t *packed,
+                       const uint16_t *scales, int64_t n, int64_t k0, int64_t k1,
+                       float *out);
+/* Inner-kernel ISA of the chunked GEMV (gemv.rs:230-243). */
+enum { OQ_ISA_SCALAR = 0, OQ_ISA_AVX2 = 1, OQ_ISA_AVX512 = 2 };
+int  oq_set_isa(int isa);     /* -1 restores the reference's choice; returns the ISA in use or -1 */
+int  oq_get_isa(void);
 /* gemv.rs:290-346 chunk policy.  `workers` is the pool size the policy
  * assumes (the reference's gpool::num_workers(), gpool.rs:29-34) and
  * `threads` the OS threads that execute chunks (0/1 = run in this thread).

@@ -37,6 +37,63 @@ def test_avx2_matches_scalar_sparse(k, n, seed, iz, sz):
     assert np.array_equal(bits(ya), bits(O.gemv_scalar(x, w)))
 
 
+@pytest.mark.parametrize("k,n,seed", refgen.SHAPE_CASES)
+def test_avx512_matches_scalar_shapes(k, n, seed):
+    # simd.rs:203-269 is bit-identical to the scalar kernel, as its AVX2 sibling
+    x, w = refgen.case(k, n, seed)
+    ya = O.gemv_avx512(x, w)
+    if ya is None:
+        pytest.skip("host has no AVX-512")
+    assert np.array_equal(bits(ya), bits(O.gemv_scalar(x, w)))
+
+
+@pytest.mark.parametrize("k,n,seed,iz,sz", refgen.SPARSE_CASES)
+def test_avx512_matches_scalar_sparse(k, n, seed, iz, sz):
+    x, w = refgen.case(k, n, seed, iz, sz)
+    ya = O.gemv_avx512(x, w)
+    if ya is None:
+        pytest.skip("host has no AVX-512")
+    assert np.array_equal(bits(ya), bits(O.gemv_scalar(x, w)))
+
+
+def test_avx512_interleave_order():
+    # one-hot rows: column j of the output is exactly (nibble_j - 8) * s, so a
+    # wrong lane of the interleave (lo/hi or first/second half) moves a value
+    rng = np.random.Generator(np.random.PCG64(5))
+    w = synth.q4_random(rng, 3, 96)
+    for r in range(3):
+        x = np.zeros(3, np.float32)
+        x[r] = 1.0
+        ya = O.gemv_avx512(x, w)
+        if ya is None:
+            pytest.skip("host has no AVX-512")
+        nib = np.empty(96, np.int64)
+        nib[0::2] = w.packed[r] & 15
+        nib[1::2] = w.packed[r] >> 4
+        sc = np.repeat(np.ascontiguousarray(w.scales[r]).view(np.float16).astype(np.float32), 32)
+        assert np.array_equal(bits(ya), bits((nib - 8).astype(np.float32) * sc))
+
+
+def test_isa_dispatch_and_chunked_gemv_agree():
+    # gemv.rs:230-243 picks AVX-512 first; every ISA gives the chunked GEMV
+    # the same bits (the kernels are bit-identical per k-range)
+    rng = np.random.Generator(np.random.PCG64(6))
+    w = synth.q4_random(rng, 2048, 1024)
+    x = rng.standard_normal(2048).astype(np.float32)
+    O.set_workers(8, 8)
+    try:
+        default = O.set_isa(None)
+        assert default == ("avx512f" if O.gemv_avx512(x[:1], synth.q4_random(rng, 1, 32)) is not None
+                           else "avx2" if O.gemv_avx2(x[:1], synth.q4_random(rng, 1, 32)) is not None else "scalar")
+        ref = O.gemv(x, w)
+        for isa in ("scalar", "avx2", "avx512f"):
+            if O.set_isa(isa) is None:
+                continue
+            assert np.array_equal(bits(O.gemv(x, w)), bits(ref)), isa
+    finally:
+        O.set_isa(None)
+
+
 def test_subrange_chunks():
     # gemv.rs:777-810: chunked AVX2 == chunked scalar exactly, ~ full within 1e-3
     st = refgen.XRng(21)
