@@ -387,6 +387,42 @@ int qtts_build_icl_block(qtts_ctx *ctx, const uint32_t *ref_tokens, int64_t n_re
                          const uint32_t *text_tokens, int64_t n_text,
                          const uint32_t *ref_codes, int64_t n_frames,
                          float *icl_out, float *remainder_out, int flags);
+/* `build_prefill_head` (generate_new.rs:222-237) on the device: the
+ * chunk-independent head, out [9][hidden].  Rows 0-2 are the text rows of
+ * IM_START, ASSISTANT, NEWLINE (`build_role_prefix`, :91-97).  With a
+ * voice embedding (`build_codec_prefix_voice`, :200-223): codec rows of
+ * THINK, THINK_BOS, language_id, THINK_EOS + the TTS_PAD text row, then
+ * voice[j] + TTS_PAD[j] for j < min(voice_len, hidden) (zero past it),
+ * then CODEC_PAD + TTS_BOS.  With voice null (`build_codec_prefix_builtin`,
+ * :226-238): codec rows of THINK, THINK_BOS, language_id, THINK_EOS,
+ * speaker_id, CODEC_PAD under the overlay [TTS_PAD x5, TTS_BOS].  voice is
+ * a host or device float buffer as flags say. */
+int qtts_build_prefill_head(qtts_ctx *ctx, uint32_t speaker_id, uint32_t language_id,
+                            const float *voice, int64_t voice_len, float *out, int flags);
+/* `build_icl_prefix` (generate_new.rs:244-280) on the device: the first
+ * n_ref pairs of the ICL block, out [n_ref][hidden], bit-identical to those
+ * rows of qtts_build_icl_block; a ref token past the last frame meets
+ * CODEC_PAD.  ref_codes [16][n_frames], ids and codes in host memory. */
+int qtts_build_icl_prefix(qtts_ctx *ctx, const uint32_t *ref_tokens, int64_t n_ref,
+                          const uint32_t *ref_codes, int64_t n_frames, float *out, int flags);
+/* `build_trailing_text` (generate_new.rs:756-767): the text rows of
+ * tokens[1..n) then TTS_EOS, out [max(n - 1, 0) + 1][hidden]. */
+int qtts_build_trailing_text(qtts_ctx *ctx, const uint32_t *tokens, int64_t n, float *out, int flags);
+/* `prefill_custom_voice` (generate_new.rs:361-476) on the device: the
+ * prompt is the 9 head rows (qtts_build_prefill_head), then the ICL rows
+ * (icl_rows [n_icl][hidden], voice-cloning head only) or, without them and
+ * with text, CODEC_BOS + the first text token's row.  The KV cache is reset
+ * and the prompt prefilled from position 0, then the codec head: hidden_out
+ * [hidden], logits_out [vocab], and *position_out the frame loop's first
+ * position (9 + n_icl, else 10, or 9 with no text; generate_new.rs:560-565).
+ * flags: QTTS_DEVICE_PTRS for the float buffers, QTTS_PATH_* for the
+ * prefill. */
+int qtts_prefill_custom_voice(qtts_ctx *ctx, const uint32_t *text_tokens, int64_t n_text,
+                              uint32_t speaker_id, uint32_t language_id,
+                              const float *voice, int64_t voice_len,
+                              const float *icl_rows, int64_t n_icl,
+                              float *hidden_out, float *logits_out, int64_t *position_out,
+                              int flags);
 
 /* ---- speech decoder --------------------------------------------------- */
 

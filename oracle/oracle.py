@@ -77,6 +77,16 @@ _SIG = {
                          POINTER(c_uint32)], c_int),
     "oq_frame": ([POINTER(TalkerHost), POINTER(PredictorHost), POINTER(OqKv), POINTER(OqKv), POINTER(OqGen),
                   POINTER(SampleParams), c_void_p, c_void_p, POINTER(c_int32), c_void_p], c_int),
+    "oq_frame_temperature": ([POINTER(SampleParams), c_int64], c_float),
+    "oq_build_prefill_head": ([POINTER(TalkerHost), c_uint32, c_uint32, c_void_p, c_int64, c_void_p], None),
+    "oq_icl_layout": ([c_int64, c_int64, c_int64, POINTER(c_int64), POINTER(c_int64)], None),
+    "oq_build_icl_block": ([POINTER(TalkerHost), POINTER(PredictorHost), c_void_p, c_int64, c_void_p, c_int64,
+                            c_void_p, c_int64, c_void_p, c_void_p], None),
+    "oq_build_icl_prefix": ([POINTER(TalkerHost), POINTER(PredictorHost), c_void_p, c_int64, c_void_p, c_int64,
+                             c_void_p], None),
+    "oq_build_trailing_text": ([POINTER(TalkerHost), c_void_p, c_int64, c_void_p], None),
+    "oq_prefill_custom_voice": ([POINTER(TalkerHost), c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_int64,
+                                 c_void_p, c_int64, POINTER(OqKv), c_void_p, c_void_p, c_void_p], c_int64),
     "od_set_threads": ([c_int], None),
     "od_causal_conv1d": ([c_void_p, c_int64, POINTER(Conv1dHost), c_void_p], None),
     "od_conv_transpose1d": ([c_void_p, c_int64, POINTER(ConvT1dHost), c_void_p], c_int64),
@@ -157,6 +167,18 @@ def set_isa(isa=None):
 
 def get_isa():
     return ISA_NAMES[lib().oq_get_isa()]
+
+
+def frame_temperature(params, frame_idx):
+    """frame_temperature (generate_new.rs:82-88)."""
+    return lib().oq_frame_temperature(byref(params), frame_idx)
+
+
+def icl_layout(n_ref, n_text, n_frames):
+    """icl_block_layout (generate_new.rs:120-128): (icl_len, remainder_len)."""
+    a, b = c_int64(), c_int64()
+    lib().oq_icl_layout(n_ref, n_text, n_frames, byref(a), byref(b))
+    return a.value, b.value
 
 
 def set_workers(workers=16, threads=0):
@@ -383,6 +405,62 @@ class Model:
         out = np.empty(self.t.hidden, np.float32)
         lib().oq_acoustic_embed_sum(byref(self.ph), ptr(c), c.size, ptr(out))
         return out
+
+    # prompt construction (generate_new.rs:82-476) ----------------------------
+    def build_prefill_head(self, speaker_id, language_id, voice=None):
+        """build_prefill_head (generate_new.rs:222-237): [9][hidden]."""
+        out = np.empty((9, self.t.hidden), np.float32)
+        v = None if voice is None else f32(voice)
+        lib().oq_build_prefill_head(byref(self.th), speaker_id, language_id, ptr(v) if v is not None else None,
+                                    0 if v is None else v.size, ptr(out))
+        return out
+
+    def build_icl_block(self, ref_tokens, text_tokens, ref_codes):
+        """build_icl_block (generate_new.rs:140-195): (icl, remainder)."""
+        rt = np.ascontiguousarray(ref_tokens, np.uint32)
+        tt = np.ascontiguousarray(text_tokens, np.uint32)
+        codes = np.ascontiguousarray(ref_codes, np.uint32).reshape(16, -1)
+        icl_len, rem_len = icl_layout(rt.size, tt.size, codes.shape[1])
+        icl = np.empty((icl_len, self.t.hidden), np.float32)
+        rem = np.empty((rem_len, self.t.hidden), np.float32)
+        lib().oq_build_icl_block(byref(self.th), byref(self.ph), ptr(rt) if rt.size else None, rt.size,
+                                 ptr(tt) if tt.size else None, tt.size, ptr(codes), codes.shape[1], ptr(icl),
+                                 ptr(rem) if rem_len else None)
+        return icl, rem
+
+    def build_icl_prefix(self, ref_tokens, ref_codes):
+        """build_icl_prefix (generate_new.rs:244-280): [len(ref_tokens)][hidden]."""
+        rt = np.ascontiguousarray(ref_tokens, np.uint32)
+        codes = np.ascontiguousarray(ref_codes, np.uint32).reshape(16, -1)
+        out = np.empty((rt.size, self.t.hidden), np.float32)
+        lib().oq_build_icl_prefix(byref(self.th), byref(self.ph), ptr(rt), rt.size, ptr(codes), codes.shape[1],
+                                  ptr(out))
+        return out
+
+    def build_trailing_text(self, tokens):
+        """build_trailing_text (generate_new.rs:756-767)."""
+        tk = np.ascontiguousarray(tokens, np.uint32)
+        out = np.empty((max(tk.size - 1, 0) + 1, self.t.hidden), np.float32)
+        lib().oq_build_trailing_text(byref(self.th), ptr(tk) if tk.size else None, tk.size, ptr(out))
+        return out
+
+    def prefill_custom_voice(self, text_tokens, speaker_id, language_id, voice=None, icl_rows=None):
+        """prefill_custom_voice (generate_new.rs:361-476) from position 0:
+        (hidden, logits, position, prompt rows)."""
+        tt = np.ascontiguousarray(text_tokens, np.uint32)
+        v = None if voice is None else f32(voice)
+        icl = None if icl_rows is None else f32(icl_rows).reshape(-1, self.t.hidden)
+        n = 9 + (icl.shape[0] if icl is not None else int(tt.size > 0))
+        rows = np.empty((n, self.t.hidden), np.float32)
+        hid = np.empty(self.t.hidden, np.float32)
+        lg = np.empty(self.t.vocab, np.float32)
+        pos = lib().oq_prefill_custom_voice(byref(self.th), ptr(tt) if tt.size else None, tt.size, speaker_id,
+                                            language_id, ptr(v) if v is not None else None,
+                                            0 if v is None else v.size, ptr(icl) if icl is not None else None,
+                                            0 if icl is None else icl.shape[0], self.tkv, ptr(hid), ptr(lg), ptr(rows))
+        if pos < 0:
+            raise RuntimeError(f"oracle prefill_custom_voice rc={pos}")
+        return hid, lg, int(pos), rows
 
     # frame loop ---------------------------------------------------------------
     def gen_begin(self, logits, hidden, position, seed):

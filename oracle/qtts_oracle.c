@@ -1129,3 +1129,226 @@ int oq_frame(const qtts_talker_host *t, const qtts_predictor_host *p,
     free(sem); free(sum); free(res);
     return rc;
 }
+
+/* ===================================================================== */
+/* prompt construction (generate_new.rs:82-476)                           */
+/* ===================================================================== */
+
+/* special ids (generate_new.rs:25-36) */
+enum {
+    OQ_IM_START = 151644, OQ_ASSISTANT = 77091, OQ_NEWLINE = 198,
+    OQ_TTS_PAD = 151671, OQ_TTS_BOS = 151672, OQ_TTS_EOS = 151673,
+    OQ_CODEC_THINK = 2154, OQ_CODEC_THINK_BOS = 2156, OQ_CODEC_THINK_EOS = 2157,
+    OQ_CODEC_PAD = 2148, OQ_CODEC_BOS = 2149
+};
+
+/* frame_temperature (generate_new.rs:82-88). */
+float oq_frame_temperature(const qtts_sample_params *sp, int64_t frame_idx)
+{
+    return frame_idx < sp->onset_frames ? sp->onset_temperature : sp->temperature;
+}
+
+/* out = a + b, element by element (add_embed, generate_new.rs:130-132). */
+static void add_rows(const float *a, const float *b, int64_t n, float *out)
+{
+    for (int64_t j = 0; j < n; j++) out[j] = a[j] + b[j];
+}
+
+/* build_prefill_head (generate_new.rs:222-237): build_role_prefix (:91-97),
+ * then build_codec_prefix_voice (:200-223) with a voice embedding or
+ * build_codec_prefix_builtin (:226-238, overlay build_tts_pad_bos :100-108)
+ * without.  out: [9][hidden]. */
+void oq_build_prefill_head(const qtts_talker_host *t, uint32_t speaker_id, uint32_t language_id,
+                           const float *voice, int64_t voice_len, float *out)
+{
+    const int64_t H = t->hidden;
+    float *pad = (float *)malloc(H * sizeof(float));
+    float *bos = (float *)malloc(H * sizeof(float));
+    float *ce = (float *)malloc(H * sizeof(float));
+    oq_embed_text_token(t, OQ_IM_START, out);
+    oq_embed_text_token(t, OQ_ASSISTANT, out + H);
+    oq_embed_text_token(t, OQ_NEWLINE, out + 2 * H);
+    oq_embed_text_token(t, OQ_TTS_PAD, pad);
+    oq_embed_text_token(t, OQ_TTS_BOS, bos);
+    if (voice) {
+        const uint32_t codec[4] = {OQ_CODEC_THINK, OQ_CODEC_THINK_BOS, language_id, OQ_CODEC_THINK_EOS};
+        for (int i = 0; i < 4; i++) {
+            oq_embed_codec_token(t, codec[i], ce);
+            add_rows(ce, pad, H, out + (3 + i) * H);
+        }
+        float *p4 = out + 7 * H;
+        memset(p4, 0, H * sizeof(float));
+        const int64_t m = voice_len < H ? voice_len : H;
+        for (int64_t j = 0; j < m; j++) p4[j] = voice[j] + pad[j];
+        oq_embed_codec_token(t, OQ_CODEC_PAD, ce);
+        add_rows(ce, bos, H, out + 8 * H);
+    } else {
+        const uint32_t codec[6] = {OQ_CODEC_THINK, OQ_CODEC_THINK_BOS, language_id, OQ_CODEC_THINK_EOS,
+                                   speaker_id, OQ_CODEC_PAD};
+        for (int i = 0; i < 6; i++) {
+            oq_embed_codec_token(t, codec[i], ce);
+            add_rows(ce, i < 5 ? pad : bos, H, out + (3 + i) * H);
+        }
+    }
+    free(pad); free(bos); free(ce);
+}
+
+/* icl_block_layout (generate_new.rs:120-128). */
+void oq_icl_layout(int64_t n_ref, int64_t n_text, int64_t n_frames, int64_t *icl_len, int64_t *rem_len)
+{
+    const int64_t text_len = n_ref + n_text + 1, codec_len = n_frames + 1;
+    *icl_len = codec_len;
+    *rem_len = text_len > codec_len ? text_len - codec_len : 0;
+}
+
+/* codec_full row f of the ICL block: CODEC_BOS for f = 0, else the talker
+ * codec row of ref_codes[0][f-1] += the predictor rows of codes 1..15
+ * (generate_new.rs:159-172).  codes: [16][n_frames]. */
+static void codec_full_row(const qtts_talker_host *t, const qtts_predictor_host *p, const uint32_t *codes,
+                           int64_t n_frames, int64_t f, float *row, float *tmp)
+{
+    const int64_t H = t->hidden;
+    if (f == 0) {
+        oq_embed_codec_token(t, OQ_CODEC_BOS, row);
+        return;
+    }
+    oq_embed_codec_token(t, codes[f - 1], row);
+    for (int g = 1; g < 16; g++) {
+        oq_embed_lookup_q4(&p->codec_embeddings[g - 1], codes[(size_t)g * n_frames + f - 1], H, tmp);
+        for (int64_t j = 0; j < H; j++) row[j] += tmp[j];
+    }
+}
+
+/* build_icl_block (generate_new.rs:140-195): icl [icl_len][H], remainder
+ * [rem_len][H] (NULL when rem_len is 0). */
+void oq_build_icl_block(const qtts_talker_host *t, const qtts_predictor_host *p, const uint32_t *ref_tokens,
+                        int64_t n_ref, const uint32_t *text_tokens, int64_t n_text, const uint32_t *codes,
+                        int64_t n_frames, float *icl, float *rem)
+{
+    const int64_t H = t->hidden, text_len = n_ref + n_text + 1, codec_len = n_frames + 1;
+    float *pad = (float *)malloc(H * sizeof(float));
+    float *txt = (float *)malloc(H * sizeof(float));
+    float *cod = (float *)malloc(H * sizeof(float));
+    float *tmp = (float *)malloc(H * sizeof(float));
+    oq_embed_text_token(t, OQ_TTS_PAD, pad);
+    for (int64_t i = 0; i < (text_len > codec_len ? text_len : codec_len); i++) {
+        /* text_full[i]: ref ++ text ++ [tts_eos] */
+        const int have_text = i < text_len;
+        if (have_text) {
+            const uint32_t tok = i < n_ref ? ref_tokens[i] : i < n_ref + n_text ? text_tokens[i - n_ref] : OQ_TTS_EOS;
+            oq_embed_text_token(t, tok, txt);
+        }
+        if (i < codec_len) {
+            codec_full_row(t, p, codes, n_frames, i, cod, tmp);
+            add_rows(have_text ? txt : pad, cod, H, icl + i * H);
+        } else {
+            memcpy(rem + (i - codec_len) * H, txt, H * sizeof(float));
+        }
+    }
+    free(pad); free(txt); free(cod); free(tmp);
+}
+
+/* build_icl_prefix (generate_new.rs:244-280): the first n_ref pairs of the
+ * ICL block, text row + codec_full row (CODEC_PAD past the frames). */
+void oq_build_icl_prefix(const qtts_talker_host *t, const qtts_predictor_host *p, const uint32_t *ref_tokens,
+                         int64_t n_ref, const uint32_t *codes, int64_t n_frames, float *out)
+{
+    const int64_t H = t->hidden;
+    float *txt = (float *)malloc(H * sizeof(float));
+    float *cod = (float *)malloc(H * sizeof(float));
+    float *tmp = (float *)malloc(H * sizeof(float));
+    for (int64_t i = 0; i < n_ref; i++) {
+        oq_embed_text_token(t, ref_tokens[i], txt);
+        if (i == 0 || i - 1 < n_frames)
+            codec_full_row(t, p, codes, n_frames, i, cod, tmp);
+        else
+            oq_embed_codec_token(t, OQ_CODEC_PAD, cod);
+        add_rows(txt, cod, H, out + i * H);
+    }
+    free(txt); free(cod); free(tmp);
+}
+
+/* build_trailing_text (generate_new.rs:756-767): text rows of tokens
+ * 1..n-1, then TTS_EOS.  out: [max(n - 1, 0) + 1][H]. */
+void oq_build_trailing_text(const qtts_talker_host *t, const uint32_t *tokens, int64_t n, float *out)
+{
+    const int64_t H = t->hidden;
+    int64_t r = 0;
+    for (int64_t i = 1; i < n; i++) oq_embed_text_token(t, tokens[i], out + (r++) * H);
+    oq_embed_text_token(t, OQ_TTS_EOS, out + r * H);
+}
+
+/* prefill_custom_voice (generate_new.rs:361-476): the prompt rows, written
+ * out step by step as that function writes them (role prefix; with a voice
+ * embedding four codec+TTS_PAD rows, voice+TTS_PAD, PAD+TTS_BOS, then the
+ * ICL rows or BOS+first text; without, the built-in speaker's six rows
+ * under the [TTS_PAD x5, TTS_BOS] overlay, then BOS+first text), prefilled
+ * into kv from position 0, then the codec head.  Returns the position the
+ * frame loop starts from (generate_new.rs:560-565), or a negative status. */
+int64_t oq_prefill_custom_voice(const qtts_talker_host *t, const uint32_t *text_tokens, int64_t n_text,
+                                uint32_t speaker_id, uint32_t language_id, const float *voice, int64_t voice_len,
+                                const float *icl_rows, int64_t n_icl, oq_kv *kv, float *hidden_out,
+                                float *logits_out, float *rows_out)
+{
+    const int64_t H = t->hidden;
+    const int has_first = !icl_rows && n_text > 0;
+    const int64_t n = 9 + (icl_rows ? n_icl : has_first);
+    float *x = (float *)malloc((size_t)n * H * sizeof(float));
+    float *pad = (float *)malloc(H * sizeof(float));
+    float *bos = (float *)malloc(H * sizeof(float));
+    float *e = (float *)malloc(H * sizeof(float));
+    oq_embed_text_token(t, OQ_IM_START, x);
+    oq_embed_text_token(t, OQ_ASSISTANT, x + H);
+    oq_embed_text_token(t, OQ_NEWLINE, x + 2 * H);
+    int64_t r = 3;
+    if (voice) {
+        const uint32_t prefix_codec[4] = {OQ_CODEC_THINK, OQ_CODEC_THINK_BOS, language_id, OQ_CODEC_THINK_EOS};
+        oq_embed_text_token(t, OQ_TTS_PAD, pad);
+        oq_embed_text_token(t, OQ_TTS_BOS, bos);
+        for (int i = 0; i < 4; i++) {
+            oq_embed_codec_token(t, prefix_codec[i], e);
+            for (int64_t j = 0; j < H; j++) x[r * H + j] = e[j] + pad[j];
+            r++;
+        }
+        for (int64_t j = 0; j < H; j++) x[r * H + j] = 0.0f;
+        for (int64_t j = 0; j < (voice_len < H ? voice_len : H); j++) x[r * H + j] = voice[j] + pad[j];
+        r++;
+        oq_embed_codec_token(t, OQ_CODEC_PAD, e);
+        for (int64_t j = 0; j < H; j++) x[r * H + j] = e[j] + bos[j];
+        r++;
+        if (icl_rows) {
+            memcpy(x + r * H, icl_rows, (size_t)n_icl * H * sizeof(float));
+            r += n_icl;
+        }
+    } else {
+        const uint32_t codec[6] = {OQ_CODEC_THINK, OQ_CODEC_THINK_BOS, language_id, OQ_CODEC_THINK_EOS,
+                                   speaker_id, OQ_CODEC_PAD};
+        oq_embed_text_token(t, OQ_TTS_PAD, pad);
+        oq_embed_text_token(t, OQ_TTS_BOS, bos);
+        for (int i = 0; i < 6; i++) {
+            oq_embed_codec_token(t, codec[i], x + r * H);
+            const float *ov = i < 5 ? pad : bos;
+            for (int64_t j = 0; j < H; j++) x[r * H + j] += ov[j];
+            r++;
+        }
+    }
+    if (has_first) {
+        float *first = (float *)malloc(H * sizeof(float));
+        oq_embed_codec_token(t, OQ_CODEC_BOS, e);
+        oq_embed_text_token(t, text_tokens[0], first);
+        for (int64_t j = 0; j < H; j++) x[r * H + j] = e[j] + first[j];
+        r++;
+        free(first);
+    }
+    int rc = QTTS_OK;
+    if (r != n) rc = QTTS_ERR_INVALID;   /* ICL rows without a voice embedding: not a reference layout */
+    if (rc == QTTS_OK) {
+        oq_kv_reset(kv);
+        rc = oq_talker_prefill(t, x, n, kv, 0, hidden_out);
+    }
+    if (rc == QTTS_OK) oq_codec_head(t, hidden_out, logits_out);
+    if (rc == QTTS_OK && rows_out) memcpy(rows_out, x, (size_t)n * H * sizeof(float));
+    free(x); free(pad); free(bos); free(e);
+    if (rc != QTTS_OK) return rc;
+    return icl_rows ? 9 + n_icl : (n_text > 0 ? 10 : 9);
+}

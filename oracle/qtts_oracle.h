@@ -155,6 +155,31 @@ int oq_frame(const qtts_talker_host *t, const qtts_predictor_host *p,
              const float *text_add, uint32_t *codes_out, int32_t *eos,
              const uint32_t *forced);
 
+/* -- prompt construction (generate_new.rs:82-476) ------------------------ */
+float oq_frame_temperature(const qtts_sample_params *sp, int64_t frame_idx);   /* :82-88 */
+/* build_prefill_head (:222-237): role prefix + codec header, [9][hidden];
+ * voice NULL -> the built-in speaker's header. */
+void oq_build_prefill_head(const qtts_talker_host *t, uint32_t speaker_id, uint32_t language_id,
+                           const float *voice, int64_t voice_len, float *out);
+void oq_icl_layout(int64_t n_ref, int64_t n_text, int64_t n_frames, int64_t *icl_len,
+                   int64_t *rem_len);                                          /* :120-128 */
+/* build_icl_block (:140-195): codes [16][n_frames]. */
+void oq_build_icl_block(const qtts_talker_host *t, const qtts_predictor_host *p, const uint32_t *ref_tokens,
+                        int64_t n_ref, const uint32_t *text_tokens, int64_t n_text, const uint32_t *codes,
+                        int64_t n_frames, float *icl, float *rem);
+/* build_icl_prefix (:244-280): [n_ref][hidden]. */
+void oq_build_icl_prefix(const qtts_talker_host *t, const qtts_predictor_host *p, const uint32_t *ref_tokens,
+                         int64_t n_ref, const uint32_t *codes, int64_t n_frames, float *out);
+/* build_trailing_text (:756-767): [max(n-1, 0) + 1][hidden]. */
+void oq_build_trailing_text(const qtts_talker_host *t, const uint32_t *tokens, int64_t n, float *out);
+/* prefill_custom_voice (:361-476) into kv from position 0; returns the
+ * frame loop's start position (:560-565) or a negative status.  rows_out
+ * (NULL or [position rows][hidden]) receives the prompt rows. */
+int64_t oq_prefill_custom_voice(const qtts_talker_host *t, const uint32_t *text_tokens, int64_t n_text,
+                                uint32_t speaker_id, uint32_t language_id, const float *voice, int64_t voice_len,
+                                const float *icl_rows, int64_t n_icl, oq_kv *kv, float *hidden_out,
+                                float *logits_out, float *rows_out);
+
 /* -- speech decoder (qtts_decoder.c; decoder.rs, conv.rs) -------------------- */
 void    od_set_threads(int n);
 void    od_causal_conv1d(const float *in, int64_t in_len, const qtts_conv1d_host *w,

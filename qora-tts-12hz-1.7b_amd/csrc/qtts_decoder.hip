@@ -19,6 +19,7 @@
 #include "qtts_device.h"
 #include "qtts_kernels.h"
 #include "qtts_devutil.h"
+#include "qtts_mfma.h"
 
 #include <algorithm>
 
@@ -28,7 +29,7 @@ namespace qtts {
 // implicit-GEMM convolution
 // ---------------------------------------------------------------------------
 
-constexpr int CGN = 128, CGK = 32, CLD = CGK + 4;
+constexpr int CGN = MFMA_N, CGK = MFMA_K, CLD = MFMA_LD;
 
 // Read (never written) in place of out-of-range taps; a plain global
 // (not const) so that selecting between it and an activation pointer
@@ -214,63 +215,15 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     };
 
     const int r16 = lane & 15, q = lane >> 4;
+    const int cb[2] = {2 * wv, 2 * wv + 1};      // wave w owns 16-column blocks 2w, 2w + 1
     f32x4 acc[MB][2];
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mfma = [&](int buf) {
-#pragma unroll
-        for (int kk = 0; kk < CGK / 16; kk++) {
-            f32x4 av[MB], bv[2];
-#pragma unroll
-            for (int i = 0; i < MB; i++) av[i] = *(const f32x4 *)&As[buf][(16 * i + r16) * CLD + 16 * kk + 4 * q];
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (2 * wv + j) + r16) * CLD + 16 * kk + 4 * q];
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-#pragma unroll
-                for (int i = 0; i < MB; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    Fetch fa, fb;
-    fetch(fa, kb);
-    if (nch > 1) fetch(fb, kb + CGK);
-    stage(fa, 0);
-    __syncthreads();
-    int c = 0;
-    for (; c + 3 < nch; c += 2) {
-        fetch(fa, kb + (c + 2) * CGK);
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        fetch(fb, kb + (c + 3) * CGK);
-        mfma(1);
-        stage(fa, 0);
-        __syncthreads();
-    }
-    if (c + 2 < nch) {
-        fetch(fa, kb + (c + 2) * CGK);
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        mfma(1);
-        stage(fa, 0);
-        __syncthreads();
-        mfma(0);
-    } else if (c + 1 < nch) {
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        mfma(1);
-    } else {
-        mfma(0);
-    }
+    mfma_pipeline<Fetch>(
+        nch, [&](Fetch &f, int c) { fetch(f, kb + c * CGK); }, stage,
+        [&](int buf) { mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane); });
 
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
     if (g.ks > 1) {

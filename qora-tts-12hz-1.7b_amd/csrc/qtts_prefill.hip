@@ -21,6 +21,7 @@
 #include "qtts_device.h"
 #include "qtts_kernels.h"
 #include "qtts_devutil.h"
+#include "qtts_mfma.h"
 
 #include <algorithm>
 
@@ -72,7 +73,7 @@ k_row_inv(const float *X, int ld, int M, int K, float *inv)
 // LDS load (As is [row][k], Bs is [column][k]).
 // ---------------------------------------------------------------------------
 
-constexpr int GN = 128, GK = 32, GLD = GK + 4;
+constexpr int GN = MFMA_N, GK = MFMA_K, GLD = MFMA_LD;
 
 enum GemmEpi : int { GEMM_STORE = 0, GEMM_PART = 1, GEMM_SWIGLU = 2, GEMM_BIAS = 3, GEMM_BIAS_SILU = 4 };
 
@@ -213,68 +214,18 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         }
     };
 
-    // compute roles
+    // compute roles: wave w owns 16-column blocks cb0 and cb0 + 2
     const int r16 = lane & 15, q = lane >> 4;
     const int cb0 = (wv & 1) + 4 * (wv >> 1);
+    const int cb[2] = {cb0, cb0 + 2};
     f32x4 acc[MB][2];
 #pragma unroll
     for (int i = 0; i < MB; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mfma = [&](int buf) {
-#pragma unroll
-        for (int kk = 0; kk < GK / 16; kk++) {
-            f32x4 av[MB], bv[2];
-#pragma unroll
-            for (int i = 0; i < MB; i++) av[i] = *(const f32x4 *)&As[buf][(16 * i + r16) * GLD + 16 * kk + 4 * q];
-#pragma unroll
-            for (int j = 0; j < 2; j++)
-                bv[j] = *(const f32x4 *)&Bs[buf][(16 * (cb0 + 2 * j) + r16) * GLD + 16 * kk + 4 * q];
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-#pragma unroll
-                for (int i = 0; i < MB; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    // Two register sets of fetched chunks: chunk c's loads are issued two
-    // chunks ahead of its MFMAs, one chunk ahead of its dequantisation into
-    // LDS, so no wait on memory sits between MFMAs.  Chunks c0.. alternate
-    // LDS buffers 0/1 and register sets fa/fb (c1 - c0 >= 2).
-    Fetch fa, fb;
-    fetch(fa, c0 * GK);
-    fetch(fb, (c0 + 1) * GK);
-    stage(fa, 0);
-    __syncthreads();
-    int c = c0;
-    for (; c + 3 < c1; c += 2) {
-        fetch(fa, (c + 2) * GK);
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        fetch(fb, (c + 3) * GK);
-        mfma(1);
-        stage(fa, 0);
-        __syncthreads();
-    }
-    if (c + 2 < c1) {
-        fetch(fa, (c + 2) * GK);
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        mfma(1);
-        stage(fa, 0);
-        __syncthreads();
-        mfma(0);
-    } else {
-        mfma(0);
-        stage(fb, 1);
-        __syncthreads();
-        mfma(1);
-    }
+    mfma_pipeline<Fetch>(
+        c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage,
+        [&](int buf) { mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane); });
 
     // epilogue: element e of acc[i][j] is row 16i + 4q + e of the tile,
     // column 128nt + 16(cb0 + 2j) + r16

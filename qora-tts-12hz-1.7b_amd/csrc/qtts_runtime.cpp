@@ -116,6 +116,8 @@ constexpr int PREFILL_MAX_ROWS = 1024;   // rows per prefill chunk
 
 // special ids of the prompt layout (generate_new.rs:25-36)
 constexpr uint32_t TTS_PAD_ID = 151671, TTS_EOS_ID = 151673, CODEC_BOS_ID = 2149;
+constexpr uint32_t IM_START_ID = 151644, ASSISTANT_ID = 77091, NEWLINE_ID = 198, TTS_BOS_ID = 151672;
+constexpr uint32_t CODEC_THINK_ID = 2154, CODEC_THINK_BOS_ID = 2156, CODEC_THINK_EOS_ID = 2157, CODEC_PAD_ID = 2148;
 
 // ---------------------------------------------------------------------------
 // error helpers
@@ -1404,6 +1406,166 @@ extern "C" int qtts_build_icl_block(qtts_ctx *c, const uint32_t *ref_tokens, int
     RCHK(stage_out(c, icl, (int64_t)f_icl, icl_out, flags));
     if (rem_len) RCHK(stage_out(c, text + (size_t)icl_len * H, rem_len * (int64_t)H, remainder_out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+// Floats of device scratch text_rows needs for n text ids.
+static size_t text_scratch_floats(const TalkerDev &m, int64_t n) { return (size_t)n * (m.text_hidden + m.text_fc1.n); }
+
+static int check_text_ids(qtts_ctx *c, const uint32_t *ids, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++)
+        if ((int64_t)ids[i] >= c->tm.text_rows.rows) return fail(c, QTTS_ERR_INVALID, "text token %u out of range", ids[i]);
+    return QTTS_OK;
+}
+
+// The 9 head rows of the prompt into out [9][H] (device): build_role_prefix
+// (generate_new.rs:91-97), then build_codec_prefix_voice (:200-223) when a
+// voice embedding is given, else build_codec_prefix_builtin (:226-238, the
+// overlay of build_tts_pad_bos :100-108).  Each row is one two-operand sum
+// (codec row + text row, or the voice row + TTS_PAD) or a text row.
+// voice: device, voice_len floats (rows past min(voice_len, H) stay zero in
+// the voice row, as generate_new.rs:211-214 leaves them).
+static int head_rows(qtts_ctx *c, uint32_t speaker_id, uint32_t language_id, const float *voice, int64_t voice_len,
+                     float *out)
+{
+    const TalkerDev &m = c->tm;
+    const size_t H = m.hidden;
+    const uint32_t tids[5] = {IM_START_ID, ASSISTANT_ID, NEWLINE_ID, TTS_PAD_ID, TTS_BOS_ID};
+    const uint32_t cids[6] = {CODEC_THINK_ID, CODEC_THINK_BOS_ID, language_id, CODEC_THINK_EOS_ID,
+                              voice ? CODEC_PAD_ID : speaker_id, CODEC_PAD_ID};
+    RCHK(check_text_ids(c, tids, 5));
+    for (uint32_t t : cids)
+        if ((int64_t)t >= m.codec_rows.rows) return fail(c, QTTS_ERR_INVALID, "codec token %u out of range", t);
+    DevScratch buf;
+    HIPCHK(c, hipMalloc(&buf.p, (11 * H + text_scratch_floats(m, 5)) * sizeof(float) + 11 * sizeof(uint32_t)));
+    float *T = (float *)buf.p, *C = T + 5 * H, *scr = C + 6 * H;
+    uint32_t *d_ids = (uint32_t *)(scr + text_scratch_floats(m, 5));
+    HIPCHK(c, hipMemcpyAsync(d_ids, tids, sizeof tids, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_ids + 5, cids, sizeof cids, hipMemcpyHostToDevice, c->stream));
+    RCHK(text_rows(c, d_ids, 5, T, scr));
+    HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_ids + 5, 6, C, (int)H, c->stream));
+    const int64_t vm = voice ? std::min<int64_t>(voice_len, (int64_t)H) : 0;
+    if (voice && vm > 0)
+        HIPCHK(c, hipMemcpyAsync(C + 4 * H, voice, vm * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(out, T, 3 * H * sizeof(float), hipMemcpyDeviceToDevice, c->stream));
+    // rows 3..7: codec (or voice) row + TTS_PAD; row 8: CODEC_PAD + TTS_BOS
+    HIPCHK(c, enqueue_add_rows(T + 3 * H, 0, C, (int)H, out + 3 * H, (int)H, 5, (int)H, c->stream));
+    HIPCHK(c, enqueue_add_rows(T + 4 * H, 0, C + 5 * H, (int)H, out + 8 * H, (int)H, 1, (int)H, c->stream));
+    if (voice) HIPCHK(c, enqueue_zero_cols(out + 7 * H, 1, (int)H, (int)vm, (int)H, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_build_prefill_head(qtts_ctx *c, uint32_t speaker_id, uint32_t language_id, const float *voice,
+                                       int64_t voice_len, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (!out || voice_len < 0) return QTTS_ERR_INVALID;
+    const size_t H = c->tm.hidden;
+    DevScratch buf;
+    HIPCHK(c, hipMalloc(&buf.p, (9 * H + (voice ? (size_t)voice_len : 0) + 1) * sizeof(float)));
+    float *rows = (float *)buf.p, *v = rows + 9 * H;
+    if (voice && voice_len) RCHK(stage_in(c, voice, voice_len, v, flags));
+    RCHK(head_rows(c, speaker_id, language_id, voice ? v : nullptr, voice_len, rows));
+    RCHK(stage_out(c, rows, (int64_t)(9 * H), out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_build_icl_prefix(qtts_ctx *c, const uint32_t *ref_tokens, int64_t n_ref,
+                                     const uint32_t *ref_codes, int64_t n_frames, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (n_ref < 0 || n_frames < 1 || (n_ref && (!ref_tokens || !out)) || !ref_codes) return QTTS_ERR_INVALID;
+    if (n_ref == 0) return QTTS_OK;
+    const TalkerDev &m = c->tm;
+    const PredictorDev &p = c->pm;
+    if (p.n_groups != 15 || p.emb_rows.n != m.hidden)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "ICL rows need 15 predictor tables of the talker width");
+    RCHK(check_text_ids(c, ref_tokens, n_ref));
+    for (int64_t i = 0; i < 16 * n_frames; i++)
+        if (ref_codes[i] >= (uint32_t)p.emb_rows.rows || (i < n_frames && ref_codes[i] >= (uint32_t)m.codec_rows.rows))
+            return fail(c, QTTS_ERR_INVALID, "reference code %u out of range", ref_codes[i]);
+    const size_t H = m.hidden;
+    // codec side of pair i: CODEC_BOS, frames 0.. (generate_new.rs:255-275),
+    // CODEC_PAD for a ref token past the last frame
+    const int64_t nf = std::min<int64_t>(n_ref - 1, n_frames), npad = n_ref - 1 - nf;
+    DevScratch buf;
+    HIPCHK(c, hipMalloc(&buf.p, (3 * (size_t)n_ref * H + text_scratch_floats(m, n_ref)) * sizeof(float) +
+                                    (n_ref + 16 * n_frames + 2) * sizeof(uint32_t)));
+    float *text = (float *)buf.p, *codec = text + n_ref * H, *rows = codec + n_ref * H, *scr = rows + n_ref * H;
+    uint32_t *d_ids = (uint32_t *)(scr + text_scratch_floats(m, n_ref)), *d_codes = d_ids + n_ref;
+    const uint32_t special[2] = {CODEC_BOS_ID, CODEC_PAD_ID};
+    HIPCHK(c, hipMemcpyAsync(d_ids, ref_tokens, n_ref * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_codes, ref_codes, 16 * n_frames * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipMemcpyAsync(d_codes + 16 * n_frames, special, sizeof special, hipMemcpyHostToDevice, c->stream));
+    RCHK(text_rows(c, d_ids, (int)n_ref, text, scr));
+    HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_codes + 16 * n_frames, 1, codec, (int)H, c->stream));
+    if (nf > 0)
+        HIPCHK(c, enqueue_codec_frame_rows(m.codec_rows, p.emb_rows, 15, d_codes, (int)n_frames, codec + H, (int)H,
+                                           c->stream));
+    for (int64_t i = 0; i < npad; i++)
+        HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_codes + 16 * n_frames + 1, 1, codec + (1 + nf + i) * H, (int)H,
+                                      c->stream));
+    HIPCHK(c, enqueue_add_rows(text, (int)H, codec, (int)H, rows, (int)H, (int)n_ref, (int)H, c->stream));
+    RCHK(stage_out(c, rows, n_ref * (int64_t)H, out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return QTTS_OK;
+}
+
+extern "C" int qtts_build_trailing_text(qtts_ctx *c, const uint32_t *tokens, int64_t n, float *out, int flags)
+{
+    NEED_MODEL(c);
+    if (n < 0 || (n && !tokens) || !out) return QTTS_ERR_INVALID;
+    std::vector<uint32_t> ids(tokens + std::min<int64_t>(n, 1), tokens + n);
+    ids.push_back(TTS_EOS_ID);
+    return qtts_embed_text_tokens(c, ids.data(), (int64_t)ids.size(), out, flags);
+}
+
+extern "C" int qtts_prefill_custom_voice(qtts_ctx *c, const uint32_t *text_tokens, int64_t n_text,
+                                         uint32_t speaker_id, uint32_t language_id, const float *voice,
+                                         int64_t voice_len, const float *icl_rows, int64_t n_icl, float *hidden_out,
+                                         float *logits_out, int64_t *position_out, int flags)
+{
+    NEED_MODEL(c);
+    if (n_text < 0 || (n_text && !text_tokens) || voice_len < 0 || n_icl < 0 || (n_icl && !icl_rows) ||
+        !hidden_out || !logits_out || !position_out)
+        return QTTS_ERR_INVALID;
+    if (icl_rows && !voice)
+        return fail(c, QTTS_ERR_INVALID, "ICL rows follow the voice-cloning head only (generate_new.rs:413-431)");
+    const TalkerDev &m = c->tm;
+    const size_t H = m.hidden;
+    const bool first = !icl_rows && n_text > 0;
+    const int64_t n = 9 + (icl_rows ? n_icl : (first ? 1 : 0));
+    if (first) RCHK(check_text_ids(c, text_tokens, 1));
+    if (first && (int64_t)CODEC_BOS_ID >= m.codec_rows.rows) return fail(c, QTTS_ERR_INVALID, "no CODEC_BOS row");
+    if (n > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "prompt of %lld rows beyond the KV cache", (long long)n);
+    DevScratch buf;
+    HIPCHK(c, hipMalloc(&buf.p, ((size_t)(n + 2) * H + (voice ? (size_t)voice_len : 0) + m.vocab +
+                                 text_scratch_floats(m, 1)) * sizeof(float) + 2 * sizeof(uint32_t)));
+    float *X = (float *)buf.p, *row = X + (size_t)n * H, *v = row + 2 * H, *lg = v + (voice ? voice_len : 0);
+    float *scr = lg + m.vocab;
+    uint32_t *d_ids = (uint32_t *)(scr + text_scratch_floats(m, 1));
+    if (voice && voice_len) RCHK(stage_in(c, voice, voice_len, v, flags));
+    RCHK(head_rows(c, speaker_id, language_id, voice ? v : nullptr, voice_len, X));
+    if (icl_rows) {
+        RCHK(stage_in(c, icl_rows, n_icl * (int64_t)H, X + 9 * H, flags));
+    } else if (first) {
+        // CODEC_BOS + the first text token (generate_new.rs:423-431, 453-461)
+        const uint32_t ids[2] = {text_tokens[0], CODEC_BOS_ID};
+        HIPCHK(c, hipMemcpyAsync(d_ids, ids, sizeof ids, hipMemcpyHostToDevice, c->stream));
+        RCHK(text_rows(c, d_ids, 1, row, scr));
+        HIPCHK(c, enqueue_gather_rows(m.codec_rows, d_ids + 1, 1, row + H, (int)H, c->stream));
+        HIPCHK(c, enqueue_add_rows(row + H, (int)H, row, (int)H, X + 9 * H, (int)H, 1, (int)H, c->stream));
+    }
+    RCHK(qtts_kv_reset(c));
+    RCHK(qtts_talker_prefill(c, X, n, 0, row, flags | QTTS_DEVICE_PTRS));
+    HIPCHK(c, enqueue_codec_head(m, c->ws, row, lg, c->stream));
+    RCHK(stage_out(c, row, (int64_t)H, hidden_out, flags));
+    RCHK(stage_out(c, lg, m.vocab, logits_out, flags));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    *position_out = icl_rows ? 9 + n_icl : (n_text > 0 ? 10 : 9);
     return QTTS_OK;
 }
 

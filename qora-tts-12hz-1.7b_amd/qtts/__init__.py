@@ -83,6 +83,11 @@ SIGNATURES = {
     "qtts_embed_text_tokens": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
     "qtts_build_icl_block": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p,
                               c_void_p, c_int], c_int),
+    "qtts_build_prefill_head": ([c_void_p, c_uint32, c_uint32, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_build_icl_prefix": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_build_trailing_text": ([c_void_p, c_void_p, c_int64, c_void_p, c_int], c_int),
+    "qtts_prefill_custom_voice": ([c_void_p, c_void_p, c_int64, c_uint32, c_uint32, c_void_p, c_int64, c_void_p,
+                                   c_int64, c_void_p, c_void_p, POINTER(c_int64), c_int], c_int),
     "qtts_decoder_upload": ([c_void_p, POINTER(DecoderHost)], c_int),
     "qtts_decoder_dims": ([c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int64)], c_int),
     "qtts_decode_to_audio": ([c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, POINTER(c_int64),
@@ -349,6 +354,45 @@ class Context:
                                                   ptr(t) if t.size else None, t.size, ptr(codes), codes.shape[1],
                                                   ptr(icl), ptr(rem) if rem_len else None, 0))
         return icl, rem
+
+    def build_prefill_head(self, speaker_id, language_id, voice=None):
+        """build_prefill_head (generate_new.rs:222-237): [9][hidden]."""
+        v = None if voice is None else _f32(voice)
+        out = np.empty((9, self.hidden), np.float32)
+        self._check(self.lib.qtts_build_prefill_head(self.h, speaker_id, language_id, ptr(v) if v is not None else None,
+                                                     0 if v is None else v.size, ptr(out), 0))
+        return out
+
+    def build_icl_prefix(self, ref_tokens, ref_codes):
+        """build_icl_prefix (generate_new.rs:244-280): [len(ref_tokens)][hidden]."""
+        r = np.ascontiguousarray(ref_tokens, np.uint32).reshape(-1)
+        codes = np.ascontiguousarray(ref_codes, np.uint32).reshape(16, -1)
+        out = np.empty((r.size, self.hidden), np.float32)
+        self._check(self.lib.qtts_build_icl_prefix(self.h, ptr(r) if r.size else None, r.size, ptr(codes),
+                                                   codes.shape[1], ptr(out), 0))
+        return out
+
+    def build_trailing_text(self, tokens):
+        """build_trailing_text (generate_new.rs:756-767)."""
+        t = np.ascontiguousarray(tokens, np.uint32).reshape(-1)
+        out = np.empty((max(t.size - 1, 0) + 1, self.hidden), np.float32)
+        self._check(self.lib.qtts_build_trailing_text(self.h, ptr(t) if t.size else None, t.size, ptr(out), 0))
+        return out
+
+    def prefill_custom_voice(self, text_tokens, speaker_id, language_id, voice=None, icl_rows=None, path=None):
+        """prefill_custom_voice (generate_new.rs:361-476) from position 0:
+        (hidden, logits, position)."""
+        t = np.ascontiguousarray(text_tokens, np.uint32).reshape(-1)
+        v = None if voice is None else _f32(voice)
+        icl = None if icl_rows is None else _f32(icl_rows).reshape(-1, self.hidden)
+        hid = np.empty(self.hidden, np.float32)
+        lg = np.empty(self.vocab, np.float32)
+        pos = c_int64()
+        self._check(self.lib.qtts_prefill_custom_voice(
+            self.h, ptr(t) if t.size else None, t.size, speaker_id, language_id, ptr(v) if v is not None else None,
+            0 if v is None else v.size, ptr(icl) if icl is not None else None, 0 if icl is None else icl.shape[0],
+            ptr(hid), ptr(lg), byref(pos), _PATH_FLAGS[path]))
+        return hid, lg, pos.value
 
     # ---- speech decoder -----------------------------------------------------
     def upload_decoder(self, decoder):

@@ -9,7 +9,13 @@
 - prefix capture / attach (TalkerPrefixCache, generate_new.rs:317-355,
   537-551): prefix + suffix prefill is bit-identical to one full prefill,
   hidden and every layer's cache, and the prefix survives the sequence
-  rewriting its cache (copy-on-write).
+  rewriting its cache (copy-on-write);
+- the prompt head (build_prefill_head, build_icl_prefix,
+  build_trailing_text, prefill_custom_voice; generate_new.rs:91-476): rows
+  bit-identical to the device's text rows plus the exact codec rows in the
+  reference's arrangement, within the bar of the oracle, and the reference's
+  prefix-cache path (head + ICL prefix kept, block suffix prefilled) equal
+  to prefill_custom_voice over the whole prompt bit for bit.
 """
 import numpy as np
 import pytest
@@ -232,3 +238,124 @@ def test_prefix_pool_capacity(ctx_factory, model):
     assert c.kv_len() == 100
     b.free()
     c.close()
+
+
+IM_START, ASSISTANT, NEWLINE, TTS_BOS = 151644, 77091, 198, 151672
+THINK, THINK_BOS, THINK_EOS, CODEC_PAD = 2154, 2156, 2157, 2148
+
+
+@pytest.mark.parametrize("voice_len", [None, 2048, 1000])
+def test_prefill_head(ctx, model, om, voice_len):
+    """build_prefill_head (generate_new.rs:222-237) on the device: bit for
+    bit the device's own text rows plus the exact codec rows in the
+    reference's arrangement, and within the bar of the oracle's head."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3500))
+    voice = None if voice_len is None else rng.standard_normal(voice_len).astype(np.float32)
+    spk, lang = 3000, 2055
+    head = ctx.build_prefill_head(spk, lang, voice)
+    T = ctx.embed_text_tokens([IM_START, ASSISTANT, NEWLINE, TTS_PAD, TTS_BOS])
+    c = om.embed_codec_token
+    exp = [T[0], T[1], T[2]]
+    codec = [THINK, THINK_BOS, lang, THINK_EOS]
+    exp += [c(k) + T[3] for k in codec]
+    if voice is None:
+        exp += [c(spk) + T[3], c(CODEC_PAD) + T[4]]
+    else:
+        m = min(voice_len, t.hidden)
+        v4 = np.zeros(t.hidden, np.float32)
+        v4[:m] = voice[:m] + T[3][:m]
+        exp += [v4, c(CODEC_PAD) + T[4]]
+    assert np.array_equal(bits(head), bits(np.stack(exp)))
+    ref = om.build_prefill_head(spk, lang, voice)
+    for i in range(9):
+        ok, e = close(head[i], ref[i])
+        assert ok, f"row {i}: rel err {e}"
+
+
+@pytest.mark.parametrize("n_ref,n_text,n_frames", [(8, 8, 23), (30, 30, 23), (5, 3, 3)])
+def test_icl_prefix_is_the_blocks_head(ctx, n_ref, n_text, n_frames):
+    """build_icl_prefix on the device is bit-identical to the ICL block's
+    first n_ref rows (the prefix cache depends on it); with more ref tokens
+    than frames the tail pairs meet CODEC_PAD."""
+    rng = np.random.Generator(np.random.PCG64(3600 + n_ref))
+    ref = rng.integers(0, 151936, n_ref)
+    text = rng.integers(0, 151936, n_text)
+    codes = rng.integers(0, 2048, (16, n_frames))
+    icl, _ = ctx.build_icl_block(ref, text, codes)
+    pre = ctx.build_icl_prefix(ref, codes)
+    k = min(n_ref, icl.shape[0])
+    assert np.array_equal(bits(pre[:k]), bits(icl[:k]))
+    if n_ref > n_frames + 1:
+        T = ctx.embed_text_tokens(ref)
+        pad = ctx.embed_codec_token(CODEC_PAD)
+        for i in range(n_frames + 1, n_ref):
+            assert np.array_equal(bits(pre[i]), bits(T[i] + pad))
+
+
+def test_trailing_text(ctx):
+    rng = np.random.Generator(np.random.PCG64(3700))
+    toks = rng.integers(0, 151936, 6)
+    tr = ctx.build_trailing_text(toks)
+    assert np.array_equal(bits(tr), bits(ctx.embed_text_tokens(list(toks[1:]) + [TTS_EOS])))
+    assert np.array_equal(bits(ctx.build_trailing_text([])), bits(ctx.embed_text_tokens([TTS_EOS])))
+
+
+@pytest.mark.parametrize("case", ["voice_icl", "voice_text", "builtin_text", "builtin_empty"])
+def test_prefill_custom_voice(ctx, model, case):
+    """prefill_custom_voice (generate_new.rs:361-476) on the device against
+    the oracle: hidden and logits within the bar, the same start position."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3800))
+    voice = rng.standard_normal(t.hidden).astype(np.float32) if case.startswith("voice") else None
+    text = [] if case == "builtin_empty" else rng.integers(0, 151936, 12)
+    icl = None
+    if case == "voice_icl":
+        ref = rng.integers(0, 151936, 20)
+        codes = rng.integers(0, 2048, (16, 30))
+        icl, _ = ctx.build_icl_block(ref, text, codes)
+    om = O.Model(t, p, kv_cap=128)
+    try:
+        hid, lg, pos = ctx.prefill_custom_voice(text, 3000, 2055, voice, icl)
+        ohid, olg, opos, _ = om.prefill_custom_voice(text, 3000, 2055, voice, icl)
+    finally:
+        om.close()
+    assert pos == opos and ctx.kv_len() == pos
+    ok_h, eh = close(hid, ohid)
+    ok_l, el = close(lg, olg)
+    assert ok_h and ok_l, f"{case}: hidden rel err {eh}, logits {el}"
+    ctx.kv_reset()
+
+
+def test_prefix_cache_path_bit_identical(ctx, model):
+    """The reference's prefix cache (build_talker_prefix, generate_new.rs:
+    330-355, then the suffix path :537-551): head + ICL prefix prefilled and
+    kept, then attached and the block's rows past the prefix prefilled, gives
+    the hidden, logits and cache of prefill_custom_voice over the whole
+    prompt bit for bit."""
+    t, p = model
+    rng = np.random.Generator(np.random.PCG64(3900))
+    voice = rng.standard_normal(t.hidden).astype(np.float32)
+    ref = rng.integers(0, 151936, 25)
+    text = rng.integers(0, 151936, 40)
+    codes = rng.integers(0, 2048, (16, 50))
+    icl, rem = ctx.build_icl_block(ref, text, codes)
+    hid, lg, pos = ctx.prefill_custom_voice(text, 0, 2055, voice, icl, path="mfma")
+    kv_full = [ctx.kv_gather(l) for l in range(len(t.layers))]
+    head = ctx.build_prefill_head(0, 2055, voice)
+    pre = ctx.build_icl_prefix(ref, codes)
+    assert qtts.prefix_suffix_split(icl.shape[0], len(ref), 9 + len(ref)) == icl.shape[0] - len(ref)
+    ctx.kv_reset()
+    ctx.prefill_talker_raw_from(np.concatenate([head, pre]), 0, path="mfma")
+    pfx = ctx.prefix_capture()
+    ctx.kv_reset()
+    ctx.prefix_attach(pfx)
+    h2 = ctx.prefill_talker_raw_from(icl[len(ref):], pfx.len, path="mfma")
+    assert ctx.kv_len() == pos == 9 + icl.shape[0]
+    assert np.array_equal(bits(h2), bits(hid))
+    assert np.array_equal(bits(ctx.apply_codec_head(h2)), bits(lg))
+    for l in range(len(t.layers)):
+        k, v = ctx.kv_gather(l)
+        assert np.array_equal(bits(k), bits(kv_full[l][0])) and np.array_equal(bits(v), bits(kv_full[l][1]))
+    pfx.free()
+    ctx.kv_reset()
