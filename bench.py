@@ -289,8 +289,11 @@ def main():
     ap.add_argument("--frames-only", action="store_true",
                     help=f"only --steps frames from KV {KV_HEADLINE}, the cache filled by a prefill of N(0,1) rows "
                          f"(for kernel profiles of the frame at the headline KV)")
+    ap.add_argument("--frames-kv", type=int, default=KV_HEADLINE,
+                    help=f"--frames-only: the cached positions the frames start from (default {KV_HEADLINE})")
     ap.add_argument("--gemv-only", action="store_true",
-                    help="only the Q4 GEMV 2048 x 6144 over its weight pool and the same-bytes streaming read")
+                    help="only the Q4 GEMV 2048 x 6144 over its weight pool, the same-bytes streaming read "
+                         "and the float4 copy (the counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -313,7 +316,10 @@ def main():
     pred = synth.make_predictor(seed=2)
     log(f"synthetic model generated in {time.time() - t_gen:.1f}s")
 
-    cap = min(8192, -(-(KV_HEADLINE + args.steps + args.warmup) // 64) * 64)
+    if not 1 <= args.frames_kv <= 8192 - args.steps - args.warmup:
+        print(f"--frames-kv {args.frames_kv}: the cache holds at most 8192 positions", file=sys.stderr)
+        sys.exit(2)
+    cap = min(8192, -(-(max(KV_HEADLINE, args.frames_kv) + args.steps + args.warmup) // 64) * 64)
     ctx = qtts.Context(0, kv_capacity=max(cap, 4096))
     t_up = time.time()
     ctx.upload_model(talker, pred)
@@ -344,25 +350,28 @@ def main():
         for w in pool:
             w.free()
         r_us, r_bytes = ctx.time_kernel(7, 256)
+        c_us, c_bytes = ctx.time_kernel(2, 20)
         ctx.close()
         print(json.dumps({"q4_gemv_2048x6144": {"us": round(g_us, 3), "gbs": round(g_bytes / g_us / 1e3, 1)},
-                          "read_same_bytes": {"us": round(r_us, 3), "gbs": round(r_bytes / r_us / 1e3, 1)}}),
+                          "read_same_bytes": {"us": round(r_us, 3), "gbs": round(r_bytes / r_us / 1e3, 1)},
+                          "float4_copy_256MiB": {"us": round(c_us, 2), "gbs": round(c_bytes / c_us / 1e3, 1)}}),
               flush=True)
         return
     if args.frames_only:
-        X = np.random.Generator(np.random.PCG64(7)).standard_normal((KV_HEADLINE, talker.hidden)).astype(np.float32)
+        kv = args.frames_kv
+        X = np.random.Generator(np.random.PCG64(7)).standard_normal((kv, talker.hidden)).astype(np.float32)
         hid = ctx.prefill_talker_raw_from(X, 0)
         del X
         pad = ctx.embed_text_token(TTS_PAD)
         ctx.gen_set_text(None, pad)
-        ctx.gen_begin(ctx.apply_codec_head(hid), hid, KV_HEADLINE, 42, qtts.sample_params(eos_enabled=False))
+        ctx.gen_begin(ctx.apply_codec_head(hid), hid, kv, 42, qtts.sample_params(eos_enabled=False))
         ctx.gen_frames(args.warmup)
         ctx.lib.qtts_sync(ctx.h)
         t0 = time.perf_counter()
         codes, _ = ctx.gen_frames(args.steps)
         ctx.lib.qtts_sync(ctx.h)
         dt = time.perf_counter() - t0
-        kv0 = KV_HEADLINE + args.warmup
+        kv0 = kv + args.warmup
         ctx.close()
         print(json.dumps({"frames": codes.shape[0], "kv_start": kv0, "kv_end": kv0 + codes.shape[0],
                           "frames_per_s": round(codes.shape[0] / dt, 2)}), flush=True)
