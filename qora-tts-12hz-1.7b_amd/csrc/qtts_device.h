@@ -2,6 +2,7 @@
 // host runtime of the MI355X decode path.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace qtts {
@@ -91,6 +92,8 @@ struct DevState {
     int32_t top_k, onset_frames, eos_enabled;
     uint32_t eos_id;
 };
+// the decode attention reads position and kv_len as one 16-byte load
+static_assert(offsetof(DevState, position) == 0 && offsetof(DevState, kv_len) == 8, "DevState head");
 
 constexpr int KV_PAGE = 64;          // talker KV positions per page
 constexpr int HEAD_DIM = 128;

@@ -7,6 +7,12 @@
 namespace qtts {
 
 constexpr int MAX_CHUNKS = 128;          // KV pages per sequence (8192 positions)
+// Talker decode attention: pages per workgroup (four waves per page), the
+// unit of the page merge in the o-proj's prologue.  One page per workgroup
+// below ATTN_LONG_KV cached positions, two from there on (fewer, longer
+// work items, and half the partials for the merge to read).
+constexpr int ATTN_LONG_KV = 1024;
+inline int attn_pages(int64_t kv_len) { return kv_len >= ATTN_LONG_KV ? 2 : 1; }
 constexpr int RING_FRAMES = 64;          // frames per host synchronisation, max
 constexpr int MAX_CAND = 64;             // lm-head column tiles reduced by one wave
 
@@ -54,7 +60,7 @@ struct Workspace {
     float *xa, *xb;    // talker residual stream, ping-pong [hidden]
     float *pxa, *pxb;  // predictor residual rows, ping-pong [2][p.hidden]
     float *pin;        // predictor API input rows [2][t.hidden]
-    float *am, *al;    // attention chunk max / sum [MAX_CHUNKS][16]
+    float *am, *al;    // attention chunk max / sum [16][MAX_CHUNKS], a chunk = 1 or 2 pages
     float *aacc;       // attention chunk P.V [MAX_CHUNKS][16][128]
     float *attn;       // talker attention output [16*128]
     float *pattn;      // predictor attention output [2][16*128]
@@ -69,7 +75,7 @@ struct Workspace {
     float *pad;        // tts_pad row [hidden]
     uint32_t *ring_pred, *ring_used;      // [RING_FRAMES][16]
     float2 *cand;      // lm-head argmax candidates [16 heads][MAX_CAND] (value, index bits)
-    int attn_grid;
+    int attn_grid;     // attention workgroups at one page each (8 per page of the capacity)
 };
 
 // Buffers of the batched prefill, rows of one prompt chunk.
@@ -172,10 +178,10 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
 hipError_t enqueue_silu(float *x, int n, hipStream_t st);
 hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStream_t st);
 
-hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
+hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode, int attn_pg,
                                hipStream_t s);
 hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,
-                              int slot, hipStream_t s);
+                              int slot, int attn_pg, hipStream_t s);
 hipError_t enqueue_final_norm(const TalkerDev &m, const Workspace &ws, float *hidden_out, hipStream_t s);
 hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const float *hidden, float *logits,
                               hipStream_t s);
@@ -186,7 +192,7 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
 hipError_t enqueue_frame_codes(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
                                const uint32_t *forced, hipStream_t s);
 hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
-                         const uint32_t *forced, hipStream_t s);
+                         const uint32_t *forced, int attn_pg, hipStream_t s);
 hipError_t enqueue_sample_top_k(const float *logits, int n, float temperature, int top_k, const uint32_t *prev,
                                 int n_prev, float penalty, uint64_t *rng, uint32_t *out, int *status, hipStream_t s);
 hipError_t enqueue_sample_api(const float *logits, int n, const SampleArgsHost &a, uint64_t *rng_dev,
@@ -223,6 +229,6 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
 double decode_flops(const DecoderDev &d, int T);
 hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l, hipStream_t s);
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
-                               hipStream_t s);
+                               const DevState *st, int attn_pg, hipStream_t s);
 
 }  // namespace qtts

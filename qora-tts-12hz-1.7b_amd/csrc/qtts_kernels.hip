@@ -170,11 +170,14 @@ struct ProPlain {
 // tile's k-slice; the rows of a wave share one head, so the page maxima and
 // sums are wave-uniform loads.  The cache length is read in the fetch stage
 // (a scalar load) and the pages after the weights are in flight.
+template <int PG>
 struct ProAttnCombine {
-    static constexpr int PF = 16;  // pages of P.V fetched ahead of the weights
-    static constexpr int PB = 24;  // pages of P.V loaded together after them (PF + k*PB never straddles page 64)
-    const float *am, *al;    // [16 heads][MAX_CHUNKS] page max / exp-sum
-    const float *aacc;       // [MAX_CHUNKS][16][128] page P.V
+    // chunks of P.V fetched ahead of the weights: 16 one-page chunks (KV 1024,
+    // where two-page chunks take over), 20 two-page chunks (KV 2560)
+    static constexpr int PF = PG == 1 ? 16 : 20;
+    static constexpr int PB = (64 - PF) / 2;  // chunks loaded together after them (PF + k*PB never straddles 64)
+    const float *am, *al;    // [16 heads][MAX_CHUNKS] chunk max / exp-sum (a chunk: PG pages)
+    const float *aacc;       // [MAX_CHUNKS][16][128] chunk P.V
     const DevState *st;
     int slot_ovr;            // >= 0: the row's KV slot (prefill rows), else st->kv_len
     template <int T, int KC>
@@ -207,13 +210,13 @@ struct ProAttnCombine {
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
         const int lane = threadIdx.x & 63;
-        const int C = (f.L + KV_PAGE - 1) / KV_PAGE;
+        const int C = (f.L + KV_PAGE * PG - 1) / (KV_PAGE * PG);
         const bool v0 = lane < C, v1 = lane + 64 < C;
 #pragma unroll
         for (int e = 0; e < KC / T; e++) {
             const int i = threadIdx.x + e * T, row = k0 + i;
             const int h = __builtin_amdgcn_readfirstlane(min(row / HEAD_DIM, 15)), d = row & (HEAD_DIM - 1);
-            // lane j holds pages j and j + 64
+            // lane j holds chunks j and j + 64
             const float m0 = v0 ? f.m[e][0] : -INFINITY, m1 = v1 ? f.m[e][1] : -INFINITY;
             const float M = wave_max_dpp(fmaxf(m0, m1));
             const float w0 = v0 ? expf(m0 - M) : 0.0f, w1 = v1 ? expf(m1 - M) : 0.0f;
@@ -1187,22 +1190,25 @@ __device__ __forceinline__ float qkv_head_prologue(const float *part, int S, int
 
 // ---------------------------------------------------------------------------
 // talker decode attention, split over 64-position pages (flash-decoding).
-// Work item (page c, kv head h): both query heads 2h, 2h+1 share one pass
-// over the page's K and V (GQA, talker.rs:310).  All global loads are issued
-// first (q/k/v partial sums, then the page's K and V as 16-byte loads), so
-// the q/k/v prologue (QK-norm, RoPE) runs while the page streams in.  The
-// item owning the newest position appends K (normed, roped) and V (raw)
-// (talker.rs:299-302) and patches that row in its registers (the page was
-// read before the append).  Writes per (page, query head) the max score, the
-// exp-sum and the unnormalised P.V.
+// Work item (chunk g of PG pages, kv head h): both query heads 2h, 2h+1
+// share one pass over the pages' K and V (GQA, talker.rs:310).  All global
+// loads are issued first (q/k/v partial sums, then the pages' K and V as
+// 16-byte loads), so the q/k/v prologue (QK-norm, RoPE) runs while the pages
+// stream in.  The item owning the newest position appends K (normed, roped)
+// and V (raw) (talker.rs:299-302) and patches that row in its registers (the
+// page was read before the append).  Writes per (chunk, query head) the max
+// score, the exp-sum and the unnormalised P.V.
 //
-// Wave w owns page rows 16w..16w+15; lane l holds dims 4(l%32)..+4 of rows
-// 16w + 8(l/32) + i, i = 0..7, of both K and V, so every load instruction
-// reads two whole 512-byte rows.  A row's score is the sum of 32 lanes'
-// 4-dim partial dot products: a reduce-scatter over those lanes leaves the
-// score of (head (l>>3)&1, row i = l&7) in lanes l and l^16.  Each wave
-// forms its own softmax pieces (max, exp, sum, P.V over its 16 rows); one
-// barrier then merges the four waves, rescaled to the page maximum.
+// Four waves per page: wave w takes page PG*g + w/4 and its rows
+// 16(w%4)..+15; lane l holds dims 4(l%32)..+4 of rows 16(w%4) + 8(l/32) + i,
+// i = 0..7, of both K and V, so every load instruction reads two whole
+// 512-byte rows.  A row's score is the sum of 32 lanes' 4-dim partial dot
+// products: a reduce-scatter over those lanes leaves the score of (head
+// (l>>3)&1, row i = l&7) in lanes l and l^16.  Each wave forms its own
+// softmax pieces (max, exp, sum, P.V over its 16 rows); one barrier then
+// merges the waves, rescaled to the chunk maximum.  A wave whose page is past
+// the cache's end re-reads the rows of the chunk's first page (same lines,
+// no extra HBM traffic) and masks every row.
 // ---------------------------------------------------------------------------
 
 // One halving step of a reduce-scatter of N values across lanes: keep the
@@ -1218,38 +1224,56 @@ __device__ __forceinline__ void rs_step_n(float (&v)[N], bool sel)
     }
 }
 
-__global__ void __launch_bounds__(256, 2)
+template <int PG>
+__global__ void __launch_bounds__(256 * PG, 2 / PG)
 k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
               const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
               int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
+    static_assert(PG == 1 || PG == 2, "one or two pages per workgroup");
+    constexpr int NWV = 4 * PG;
     __shared__ __attribute__((aligned(16))) float qr[2][HEAD_DIM];
     __shared__ __attribute__((aligned(16))) float knew[HEAD_DIM];
     __shared__ __attribute__((aligned(16))) float vnew[HEAD_DIM];
-    __shared__ __attribute__((aligned(16))) float pw[4][2][2][8];   // [wave][head][half][row] probabilities
-    __shared__ float wml[4][2][2];                                   // [wave][head][max, sum]
-    __shared__ __attribute__((aligned(16))) float ored[4][2][HEAD_DIM];
-    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    __shared__ __attribute__((aligned(16))) float pw[NWV][2][2][8];   // [wave][head][half][row] probabilities
+    __shared__ float wml[NWV][2][2];                                   // [wave][head][max, sum]
+    __shared__ __attribute__((aligned(16))) float ored[NWV][2][HEAD_DIM];
+    const int t = threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wp = wv >> 2, wq = wv & 3;           // page of the chunk, row block of the page
     const int half = lane >> 5, dl = lane & 31, d4 = 4 * dl;
-    const int row0 = 16 * wv + 8 * half;           // this lane's rows row0 + i, i = 0..7
-    // the page-table entry of this workgroup's first page (an entry of the
-    // table for every workgroup of the launch) is read beside the sequence
-    // length; the page itself only once the length shows it is in use
-    const int pg0 = kv.ptab[min((int)(blockIdx.x >> 3), MAX_CHUNKS - 1)];
-    asm volatile("" ::: "memory");               // keeps the load above the length's
-    const int slot = slot_ovr >= 0 ? slot_ovr : st->kv_len;
-    const int64_t pos = pos_ovr >= 0 ? pos_ovr : st->position;
+    const int row0 = 16 * wq + 8 * half;           // this lane's rows row0 + i, i = 0..7
+    // the page-table entries of this workgroup's chunk (the wave's page and
+    // the chunk's first page; the grid never exceeds the table) are read
+    // beside the sequence length; the pages themselves only once the length
+    // shows which are in use
+    const int g = blockIdx.x >> 3, h = blockIdx.x & 7;
+    const int c = PG * g + wp;                     // this wave's page
+    const int pgw = kv.ptab[min(c, MAX_CHUNKS - 1)];
+    const int pgf = kv.ptab[min(PG * g, MAX_CHUNKS - 1)];
+    asm volatile("" ::: "memory");               // keeps the loads above the length's
+    // position and length in one load (the device state's first 16 bytes),
+    // so the RoPE values do not wait a second round trip
+    const u32x4 sv = *(const u32x4 *)st;
+    // the other arguments now, not after the length's wait
+    asm volatile("" ::"s"(part), "s"(qn_g), "s"(kn_g), "s"(rope_cos), "s"(rope_sin), "s"(kv.base), "s"(aacc),
+                 "s"(am), "s"(al), "s"(S), "s"(npad), "s"(layer), "s"(kv.n_phys));
+    const int slot = slot_ovr >= 0 ? slot_ovr : (int)sv[2];
+    const int64_t pos = pos_ovr >= 0 ? pos_ovr : (int64_t)(((uint64_t)sv[1] << 32) | sv[0]);
     const int L = slot + 1;
-    const int C = (L + KV_PAGE - 1) / KV_PAGE;
+    const int C = (L + KV_PAGE - 1) / KV_PAGE;     // pages in use
+    // the grid covers the capacity: chunks past the length exit (the whole
+    // workgroup, before any barrier)
+    if (PG * g >= C) return;
     const float scale = 1.0f / sqrtf(128.0f);
-    for (int item = blockIdx.x; item < 8 * C; item += gridDim.x) {
-        const int c = item >> 3, h = item & 7;
-        const int ntok = min(KV_PAGE, L - c * KV_PAGE);
-        __syncthreads();                           // LDS of the previous item is free
-        // ---- loads: the wave's vector of the step (wave 0, 1: q heads 2h,
-        // 2h+1; wave 2: k head h; wave 3: v head h), lane l holding dims l
-        // and l+64 (a rotate-half pair), its gammas and RoPE values, then the page
-        const int base = (wv < 2 ? 2 * h + wv : 16 + 8 * (wv - 2) + h) * HEAD_DIM + lane;
+    {
+        const bool live = c < C;
+        const int ntok = live ? min(KV_PAGE, L - c * KV_PAGE) : 0;
+        const bool last = g == (C - 1) / PG;       // the chunk holding the newest position
+        // ---- loads: the vector of the step (waves w%4 = 0, 1: q heads 2h,
+        // 2h+1; 2: k head h; 3: v head h; waves past the first page load the
+        // same and only read LDS), lane l holding dims l and l+64 (a
+        // rotate-half pair), its gammas and RoPE values, then the page
+        const int base = (wq < 2 ? 2 * h + wq : 16 + 8 * (wq - 2) + h) * HEAD_DIM + lane;
         float xa[RES_MAX_S], xb[RES_MAX_S];
 #pragma unroll
         for (int s = 0; s < RES_MAX_S; s++) {
@@ -1257,10 +1281,10 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             xa[s] = p[0];
             xb[s] = p[64];
         }
-        const uint16_t *gam = wv < 2 ? qn_g : kn_g;
+        const uint16_t *gam = wq < 2 ? qn_g : kn_g;
         const uint32_t ga = gam[lane], gb = gam[lane + 64];
         const float cs = rope_cos[pos * 64 + lane], sn = rope_sin[pos * 64 + lane];
-        const int pg = item == (int)blockIdx.x ? pg0 : kv.ptab[c];
+        const int pg = live ? pgw : pgf;
         const float *Kp = kv_page_ptr(kv, layer, pg, row0, h, 0) + d4;
         const float *Vp = kv_page_ptr(kv, layer, pg, row0, h, 1) + d4;
         f32x4 kk[8], vv[8];
@@ -1268,6 +1292,9 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         for (int i = 0; i < 8; i++) kk[i] = ld4nt(Kp + i * HEAD_DIM);
 #pragma unroll
         for (int i = 0; i < 8; i++) vv[i] = ld4nt(Vp + i * HEAD_DIM);
+        // nothing below may be scheduled above the page loads: a wait for the
+        // step's vectors there would hold the pages back a round trip
+        __builtin_amdgcn_sched_barrier(0);
         // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92) in
         // registers: the sum of squares is the dims 0..63 wave sum plus the
         // dims 64..127 wave sum, in that order
@@ -1282,25 +1309,23 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             a += p[0];
             b += p[64];
         }
-        if (wv < 3) {
+        if (wq < 3) {
             const float ss = wave_sum_dpp(a * a) + wave_sum_dpp(b * b);
             const float r = 1.0f / sqrtf(ss / 128.0f + 1e-6f);
             const float na = a * r * h2f(ga), nb = b * r * h2f(gb);
-            const float ra = na * cs - nb * sn, rb = nb * cs + na * sn;
-            float *dst = wv < 2 ? qr[wv] : knew;
-            dst[lane] = ra;
-            dst[lane + 64] = rb;
-            a = ra;
-            b = rb;
-        } else {
-            vnew[lane] = a;
-            vnew[lane + 64] = b;
+            a = na * cs - nb * sn;
+            b = nb * cs + na * sn;
         }
-        if (c == C - 1 && wv >= 2) {
-            // append (talker.rs:299-302): K normed and roped, V raw
-            float *row = kv_ptr(kv, layer, slot, h, wv - 2);
-            row[lane] = a;
-            row[lane + 64] = b;
+        if (wv < 4) {
+            float *dst = wq < 2 ? qr[wq] : wq == 2 ? knew : vnew;
+            dst[lane] = a;
+            dst[lane + 64] = b;
+            if (last && wv >= 2) {
+                // append (talker.rs:299-302): K normed and roped, V raw
+                float *row = kv_ptr(kv, layer, slot, h, wv - 2);
+                row[lane] = a;
+                row[lane + 64] = b;
+            }
         }
         __syncthreads();
         if (c == C - 1) {
@@ -1363,21 +1388,23 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             *(f32x4 *)&ored[wv][1][d4] = a1;
         }
         __syncthreads();
-        {
-            // the four waves merged at the page maximum, in wave order
+        if (t < 2 * HEAD_DIM) {
+            // the waves merged at the chunk maximum, in wave order
             const int oh = t >> 7, d = t & 127;
-            const float M = fmaxf(fmaxf(wml[0][oh][0], wml[1][oh][0]), fmaxf(wml[2][oh][0], wml[3][oh][0]));
+            float M = wml[0][oh][0];
+#pragma unroll
+            for (int w = 1; w < NWV; w++) M = fmaxf(M, wml[w][oh][0]);
             float o = 0.0f, ls = 0.0f;
 #pragma unroll
-            for (int w = 0; w < 4; w++) {
+            for (int w = 0; w < NWV; w++) {
                 const float f = expf(wml[w][oh][0] - M);   // 0 for a wave with no valid row
                 o = fmaf(f, ored[w][oh][d], o);
                 ls = fmaf(f, wml[w][oh][1], ls);
             }
-            aacc[((size_t)c * 16 + 2 * h + oh) * HEAD_DIM + d] = o;
+            aacc[((size_t)g * 16 + 2 * h + oh) * HEAD_DIM + d] = o;
             if (d == 0) {
-                am[(2 * h + oh) * MAX_CHUNKS + c] = M;
-                al[(2 * h + oh) * MAX_CHUNKS + c] = ls;
+                am[(2 * h + oh) * MAX_CHUNKS + g] = M;
+                al[(2 * h + oh) * MAX_CHUNKS + g] = ls;
             }
         }
     }
@@ -2310,8 +2337,23 @@ static hipError_t swiglu_down(const LayerDev &L, const Workspace &ws, const ProG
 // One talker layer, decode (talker.rs:274-350).  The residual stream enters
 // as base (+ the previous layer's down partials) and leaves as ws.xa plus
 // this layer's down partials.
+// The decode attention over one or two pages per workgroup, and the o-proj
+// that merges its chunks.
+template <int PG>
+static hipError_t talker_attn_o(const TalkerDev &m, const Workspace &ws, const LayerDev &L, int l,
+                                const DevState *st, int64_t pos_ovr, int slot_ovr, hipStream_t s)
+{
+    const int grid = 8 * ((ws.attn_grid / 8 + PG - 1) / PG);
+    hipLaunchKernelGGL(k_talker_attn<PG>, dim3(grid), dim3(256 * PG), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
+                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
+                       ws.al, ws.aacc);
+    QCHK(hipGetLastError());
+    return launch_gemv<1>(L.o, ProAttnCombine<PG>{ws.am, ws.al, ws.aacc, st, slot_ovr},
+                          EpiPart<1>{ws.part_o, L.o.npad}, s);
+}
+
 static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, const float *x_in,
-                               const DevState *st, int64_t pos_ovr, int slot_ovr, hipStream_t s)
+                               const DevState *st, int64_t pos_ovr, int slot_ovr, int attn_pg, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
     const LayerDev *P = l > 0 ? &m.layers[l - 1] : nullptr;
@@ -2321,12 +2363,9 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
                                   P ? P->down.npad : 0, nullptr, L.input_norm, H, ws.xb, nullptr};
     QCHK(launch_gemv<1>(L.qkv, pre_attn, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
     // 2. QK-norm, RoPE, KV append, split-K attention over the pages
-    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
-                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
-                       ws.al, ws.aacc);
-    QCHK(hipGetLastError());
     // 3. o_proj -> partials, the pages merged in its prologue
-    QCHK(launch_gemv<1>(L.o, ProAttnCombine{ws.am, ws.al, ws.aacc, st, slot_ovr}, EpiPart<1>{ws.part_o, L.o.npad}, s));
+    QCHK(attn_pg == 2 ? talker_attn_o<2>(m, ws, L, l, st, pos_ovr, slot_ovr, s)
+                      : talker_attn_o<1>(m, ws, L, l, st, pos_ovr, slot_ovr, s));
     // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
     const ProResidRms<1, 2048> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
     return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);
@@ -2344,10 +2383,10 @@ static hipError_t talker_head(const TalkerDev &m, const Workspace &ws, float *si
 
 // forward_with_embedding (talker.rs:263-360) on the input ws.x: 28 layers,
 // final norm (hidden -> ws.hid_work), codec head, then k_step_end.
-hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode,
+hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode, int attn_pg,
                                hipStream_t s)
 {
-    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, -1, -1, s));
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, -1, -1, attn_pg, s));
     QCHK(talker_head(m, ws, ws.hid_work, s));
     hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1024), 0, s, ws.part_head, m.codec_head.S,
                        m.codec_head.npad, m.vocab, ws.hid_work, m.hidden, ws.logits, ws.hidden, st,
@@ -2357,9 +2396,9 @@ hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState
 
 // One prefill row: RoPE at pos, KV slot `slot`, no codec head.
 hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,
-                              int slot, hipStream_t s)
+                              int slot, int attn_pg, hipStream_t s)
 {
-    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, pos, slot, s));
+    for (int l = 0; l < m.n_layers; l++) QCHK(talker_layer(m, ws, l, ws.x, st, pos, slot, attn_pg, s));
     return hipSuccess;
 }
 
@@ -2595,10 +2634,10 @@ hipError_t enqueue_frame_codes(const TalkerDev &m, const PredictorDev &p, const 
 }
 
 hipError_t enqueue_frame(const TalkerDev &m, const PredictorDev &p, const Workspace &ws, DevState *st,
-                         const uint32_t *forced, hipStream_t s)
+                         const uint32_t *forced, int attn_pg, hipStream_t s)
 {
     QCHK(enqueue_frame_codes(m, p, ws, st, forced, s));
-    return enqueue_talker_step(m, ws, st, 1, s);
+    return enqueue_talker_step(m, ws, st, 1, attn_pg, s);
 }
 
 // The legacy loop's sampler (generate.rs:185-217): apply_repetition_penalty
@@ -2850,14 +2889,19 @@ hipError_t enqueue_gateup_timing(const TalkerDev &m, const Workspace &ws, int l,
 }
 
 hipError_t enqueue_attn_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
-                               hipStream_t s)
+                               const DevState *st, int attn_pg, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
     // a decode step's attention: appends at the free slot `slot` (beyond the
     // cached length, so cached positions are untouched) and attends slot+1
-    hipLaunchKernelGGL(k_talker_attn, dim3(ws.attn_grid), dim3(256), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
-                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, (const DevState *)nullptr, pos, slot, l, m.kv,
-                       ws.am, ws.al, ws.aacc);
+    if (attn_pg == 2) {
+        hipLaunchKernelGGL(k_talker_attn<2>, dim3(8 * ((ws.attn_grid / 8 + 1) / 2)), dim3(512), 0, s, ws.part_qkv,
+                           L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos, slot, l, m.kv,
+                           ws.am, ws.al, ws.aacc);
+    } else {
+        hipLaunchKernelGGL(k_talker_attn<1>, dim3(ws.attn_grid), dim3(256), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
+                           L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos, slot, l, m.kv, ws.am, ws.al, ws.aacc);
+    }
     return hipGetLastError();
 }
 

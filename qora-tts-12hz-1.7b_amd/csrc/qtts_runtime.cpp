@@ -63,7 +63,7 @@ struct qtts_ctx {
     float *d_io2 = nullptr;
     int64_t io_floats = 0;
 
-    hipGraphExec_t frame_exec = nullptr;
+    hipGraphExec_t frame_exec[2] = {nullptr, nullptr};   // one and two attention pages per workgroup
     bool gen_started = false;
 
     float *scratch = nullptr;                        // this device's copy of `scratch` (qtts_gemm_q4_noalloc)
@@ -385,8 +385,10 @@ static void free_list(std::vector<void *> &l)
 
 static void drop_graph(qtts_ctx *c)
 {
-    if (c->frame_exec) hipGraphExecDestroy(c->frame_exec);
-    c->frame_exec = nullptr;
+    for (auto &e : c->frame_exec) {
+        if (e) hipGraphExecDestroy(e);
+        e = nullptr;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -992,7 +994,7 @@ static int talker_step_staged(qtts_ctx *c, int64_t position, float *hidden_out, 
 {
     c->h_st->position = position;
     HIPCHK(c, hipMemcpyAsync(&c->st_gen->position, &c->h_st->position, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
-    HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, c->stream));
+    HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, attn_pages(c->h_st->kv_len), c->stream));
     RCHK(stage_out(c, c->ws.hidden, c->tm.hidden, hidden_out, flags));
     RCHK(stage_out(c, c->ws.logits, c->tm.vocab, logits_out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1072,7 +1074,8 @@ extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int
     } else {
         for (int64_t t = 0; t < seq; t++) {
             RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
-            HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t), c->stream));
+            HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t),
+                                         attn_pages(start_pos + t), c->stream));
         }
         HIPCHK(c, enqueue_final_norm(c->tm, c->ws, c->ws.hid_work, c->stream));
     }
@@ -2050,7 +2053,7 @@ extern "C" int qtts_predict_codes(qtts_ctx *c, const float *talker_hidden, float
     v.rope_sin = p.rope_sin;
     v.rope_rows = p.rope_rows;
     v.kv = KvPaged{c->lkv, c->lkv_ptab, (int32_t)(c->kv_cap / KV_PAGE)};
-    HIPCHK(c, enqueue_talker_row(v, c->ws, c->st_gen, pos, (int)pos, c->stream));
+    HIPCHK(c, enqueue_talker_row(v, c->ws, c->st_gen, pos, (int)pos, attn_pages(pos), c->stream));
     // final norm (code_predictor.rs:202) into `side`, then every head
     float *side = c->leg_buf, *out = c->leg_buf + p.hidden;
     v.codec_head = p.heads[0];
@@ -2118,21 +2121,24 @@ extern "C" int qtts_prefill_tokens(qtts_ctx *c, const uint32_t *ids, const uint8
 // frame loop
 // ---------------------------------------------------------------------------
 
-static int build_frame_graph(qtts_ctx *c)
+// The frame graph of the attention variant `pg` (pages per workgroup),
+// captured on first use.
+static int build_frame_graph(qtts_ctx *c, int pg)
 {
-    if (c->frame_exec) return QTTS_OK;
+    hipGraphExec_t &exec = c->frame_exec[pg - 1];
+    if (exec) return QTTS_OK;
     hipGraph_t g = nullptr;
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
-    const hipError_t e = enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, c->stream);
+    const hipError_t e = enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, pg, c->stream);
     const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
     if (e != hipSuccess || e2 != hipSuccess) {
         if (g) hipGraphDestroy(g);
         return fail(c, QTTS_ERR_HIP, "frame capture failed: %s / %s", hipGetErrorString(e), hipGetErrorString(e2));
     }
-    const hipError_t e3 = hipGraphInstantiate(&c->frame_exec, g, nullptr, nullptr, 0);
+    const hipError_t e3 = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
     hipGraphDestroy(g);
     if (e3 != hipSuccess) {
-        c->frame_exec = nullptr;
+        exec = nullptr;
         return fail(c, QTTS_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e3));
     }
     return QTTS_OK;
@@ -2200,7 +2206,6 @@ static bool use_graph()
 static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done, int32_t *eos, bool forced)
 {
     const bool graph = use_graph();
-    if (graph) RCHK(build_frame_graph(c));
     int64_t emitted = 0;
     *eos = 0;
     while (emitted < n) {
@@ -2212,9 +2217,20 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
         c->h_st->ring_base = c->h_st->frame_idx;
         HIPCHK(c, hipMemcpyAsync(&c->st_gen->ring_base, &c->h_st->ring_base, sizeof(int32_t), hipMemcpyHostToDevice,
                                  c->stream));
+        // frame f's talker step attends kv_len + f + 1 positions (frames after
+        // a stop are no-ops whichever variant runs them); the batch's graphs
+        // are captured before its first launch
+        if (graph) {
+            RCHK(build_frame_graph(c, attn_pages(c->h_st->kv_len)));
+            RCHK(build_frame_graph(c, attn_pages(c->h_st->kv_len + batch - 1)));
+        }
         for (int64_t f = 0; f < batch; f++) {
-            if (graph) HIPCHK(c, hipGraphLaunch(c->frame_exec, c->stream));
-            else HIPCHK(c, enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, c->stream));
+            const int pg = attn_pages(c->h_st->kv_len + f);
+            if (graph) {
+                HIPCHK(c, hipGraphLaunch(c->frame_exec[pg - 1], c->stream));
+            } else {
+                HIPCHK(c, enqueue_frame(c->tm, c->pm, c->ws, c->st_gen, c->d_forced, pg, c->stream));
+            }
         }
         HIPCHK(c, hipMemcpyAsync(c->h_ring, c->ws.ring_pred, sizeof(uint32_t) * batch * 16, hipMemcpyDeviceToHost,
                                  c->stream));
@@ -2380,7 +2396,10 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         const int64_t pos = std::min<int64_t>(c->h_st->position, m.rope_rows - 1);
         *bytes = (double)(slot + 1) * 8 * HEAD_DIM * 4 * 2 + 16.0 * HEAD_DIM * 4 * 3;
         return time_launches(c, iters,
-                             [&](int i) { return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->stream); },
+                             [&](int i) {
+                                 return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->st_api,
+                                                            attn_pages(slot), c->stream);
+                             },
                              avg_us);
     }
     if (kind == 5 || kind == 6) {
@@ -2421,7 +2440,8 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         hipGraphExec_t ge = nullptr;
         HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         const hipError_t e = kind == 5 ? enqueue_frame_codes(m, p, c->ws, c->st_gen, c->d_forced, c->stream)
-                                       : enqueue_talker_step(m, c->ws, c->st_gen, 0, c->stream);
+                                       : enqueue_talker_step(m, c->ws, c->st_gen, 0, attn_pages(c->h_st->kv_len),
+                                                             c->stream);
         const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
         if (e != hipSuccess || e2 != hipSuccess) {
             if (g) hipGraphDestroy(g);
