@@ -324,6 +324,9 @@ def main():
     t_up = time.time()
     ctx.upload_model(talker, pred)
     log(f"uploaded in {time.time() - t_up:.1f}s")
+    # what the model holds on the device; the predictor's upload-time tables
+    # (projected code rows and their layer-0 q|k|v) are read one row per step
+    mem = {k: round(v / 2**20, 1) for k, v in ctx.device_bytes().items()}
     if args.prefill_only:
         pf = time_prefill(ctx, args.layers)
         ctx.close()
@@ -516,6 +519,7 @@ def main():
         "frame_loop_from_prompt": loop,
         "roofline": roof,
         "frame_roofline": frame_roof,
+        "device_memory_mb": mem,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

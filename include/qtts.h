@@ -597,6 +597,22 @@ int qtts_time_prefill(qtts_ctx *ctx, int64_t rows, int32_t what, int32_t iters,
 int qtts_time_decode(qtts_ctx *ctx, int64_t n_frames, int32_t iters,
                      double *avg_us, double *flops);
 
+/* Device memory the uploaded model holds, in bytes.  No reference
+ * counterpart (the reference keeps its weights in host memory): a
+ * measurement helper so a caller can see what the upload-time tables cost
+ * against the weights they stand in for. */
+typedef struct {
+    int64_t talker_q4;            /* talker Q4 tiles: layers, codec head, text projection */
+    int64_t predictor_q4;         /* predictor Q4 tiles: layers, lm heads, input projection */
+    int64_t predictor_row_tables; /* projected code-embedding rows of steps 1..14 (f32), 0 if off */
+    int64_t predictor_qkv_tables; /* their layer-0 q|k|v rows (f32), 0 if off */
+    int64_t embedding_rows;       /* Q4 embedding tables kept row-major (text, codec, predictor) */
+    int64_t kv_pool;              /* talker KV page pool (f32), 2 x capacity */
+    int64_t device_used;          /* total minus free device memory (hipMemGetInfo) */
+} qtts_mem_report;
+
+int qtts_device_bytes(qtts_ctx *ctx, qtts_mem_report *out);
+
 #ifdef __cplusplus
 }
 #endif

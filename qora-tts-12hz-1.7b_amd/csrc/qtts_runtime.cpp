@@ -2562,3 +2562,39 @@ extern "C" int qtts_time_gemv(qtts_ctx *c, const qtts_w *const *ws, int32_t n_w,
         },
         avg_us);
 }
+
+// ---------------------------------------------------------------------------
+// device memory of the uploaded model
+// ---------------------------------------------------------------------------
+
+static int64_t tiled_bytes(const Q4Tiled &w) { return (int64_t)w.S * w.CT * w.tile_bytes; }
+static int64_t rows_bytes(const Q4Rows &e) { return (int64_t)e.rows * e.G * (16 + 2); }
+
+extern "C" int qtts_device_bytes(qtts_ctx *c, qtts_mem_report *out)
+{
+    NEED_MODEL(c);
+    if (!out) return QTTS_ERR_INVALID;
+    memset(out, 0, sizeof *out);
+    const TalkerDev &m = c->tm;
+    const PredictorDev &p = c->pm;
+    for (int l = 0; l < m.n_layers; l++) {
+        const LayerDev &L = m.layers[l];
+        out->talker_q4 += tiled_bytes(L.qkv) + tiled_bytes(L.o) + tiled_bytes(L.gate_up) + tiled_bytes(L.down);
+    }
+    out->talker_q4 += tiled_bytes(m.codec_head) + tiled_bytes(m.text_fc1) + tiled_bytes(m.text_fc2);
+    for (int l = 0; l < p.n_layers; l++) {
+        const LayerDev &L = p.layers[l];
+        out->predictor_q4 += tiled_bytes(L.qkv) + tiled_bytes(L.o) + tiled_bytes(L.gate_up) + tiled_bytes(L.down);
+    }
+    for (int g = 0; g < p.n_groups; g++) out->predictor_q4 += tiled_bytes(p.heads[g]);
+    out->predictor_q4 += tiled_bytes(p.proj);
+    const int64_t ntab = p.n_groups - 1, rows = p.emb_rows.rows;
+    if (p.proj_rows) out->predictor_row_tables = ntab * rows * p.hidden * (int64_t)sizeof(float);
+    if (p.qkv_rows) out->predictor_qkv_tables = ntab * rows * p.layers[0].qkv.npad * (int64_t)sizeof(float);
+    out->embedding_rows = rows_bytes(m.codec_rows) + rows_bytes(m.text_rows) + p.n_groups * rows_bytes(p.emb_rows);
+    out->kv_pool = (int64_t)m.n_layers * m.kv.n_phys * 2 * 8 * KV_PAGE * HEAD_DIM * (int64_t)sizeof(float);
+    size_t fr = 0, tot = 0;
+    HIPCHK(c, hipMemGetInfo(&fr, &tot));
+    out->device_used = (int64_t)(tot - fr);
+    return QTTS_OK;
+}

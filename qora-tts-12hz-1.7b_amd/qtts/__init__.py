@@ -107,6 +107,7 @@ SIGNATURES = {
     "qtts_gen_frames_forced": ([c_void_p, c_int64, c_void_p, c_void_p], c_int),
     "qtts_gen_state": ([c_void_p, c_void_p, c_void_p, POINTER(c_int64), POINTER(c_uint64)], c_int),
     "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
+    "qtts_device_bytes": ([c_void_p, c_void_p], c_int),
     "qtts_time_gemv": ([c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_prefill": ([c_void_p, c_int64, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_decode": ([c_void_p, c_int64, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
@@ -513,6 +514,16 @@ class Context:
         return lg, hd, pos.value, rng.value
 
     # ---- measurement ----------------------------------------------------------
+    MEM_FIELDS = ("talker_q4", "predictor_q4", "predictor_row_tables", "predictor_qkv_tables", "embedding_rows",
+                  "kv_pool", "device_used")
+
+    def device_bytes(self):
+        """The device memory the uploaded model holds, bytes per part
+        (qtts_mem_report)."""
+        out = (c_int64 * len(self.MEM_FIELDS))()
+        self._check(self.lib.qtts_device_bytes(self.h, out))
+        return dict(zip(self.MEM_FIELDS, (int(v) for v in out)))
+
     def time_kernel(self, kind, iters):
         us, b = c_double(), c_double()
         self._check(self.lib.qtts_time_kernel(self.h, kind, iters, byref(us), byref(b)))

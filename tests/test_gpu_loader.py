@@ -178,3 +178,30 @@ def test_qora_q4_container(ctx_factory, tmp_path):
     with pytest.raises(qtts.QttsError) as e:
         c.load_qora_q4(str(tmp_path / "f16.qora-tts"), *ropes)
     assert e.value.code == qtts.ERR_UNSUPPORTED
+
+
+def test_device_bytes_report(ctx_factory):
+    """qtts_device_bytes: each part from the shapes of what was uploaded."""
+    t = synth.make_talker(seed=171, n_layers=2, text_vocab=256)
+    p = synth.make_predictor(seed=172, n_layers=2)
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+    r = c.device_bytes()
+    q4 = lambda w: w.nbytes                 # nibbles + an f16 scale per 32 columns
+    talker = sum(q4(w) for L in t.layers for w in (L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj,
+                                                   L.up_proj, L.down_proj))
+    talker += q4(t.codec_head) + q4(t.text_fc1) + q4(t.text_fc2)
+    pred = sum(q4(w) for L in p.layers for w in (L.q_proj, L.k_proj, L.v_proj, L.o_proj, L.gate_proj,
+                                                 L.up_proj, L.down_proj))
+    pred += sum(q4(h) for h in p.lm_heads) + q4(p.input_proj)
+    # tiles pad k to whole slices and n to whole groups, never below the weights
+    assert talker <= r["talker_q4"] <= 1.25 * talker
+    assert pred <= r["predictor_q4"] <= 1.25 * pred
+    ntab, rows = len(p.lm_heads) - 1, p.codec_embeddings[0].k
+    assert r["predictor_row_tables"] == ntab * rows * p.hidden * 4
+    assert r["predictor_qkv_tables"] >= ntab * rows * 4096 * 4
+    emb = q4(t.codec_embedding) + q4(t.text_embedding) + sum(q4(e) for e in p.codec_embeddings)
+    assert r["embedding_rows"] == emb
+    assert r["kv_pool"] == len(t.layers) * 2 * (256 // 64) * 2 * 8 * 64 * 128 * 4
+    parts = sum(v for k, v in r.items() if k != "device_used")
+    assert r["device_used"] >= parts
