@@ -569,6 +569,15 @@ int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
 int qtts_time_kernel(qtts_ctx *ctx, int32_t kind, int32_t iters,
                      double *avg_us, double *bytes);
 
+/* Launch mode of the timing calls above and below: 0 (default) launches
+ * each timed kernel from the context stream; 1 captures the `iters`
+ * launches once into a graph and replays it (one warm-up replay, then four
+ * between the events; the average is over all replayed launches), which
+ * is how the frame loop runs its kernels.  Kinds 5 and 6 replay their own
+ * graph either way; the whole-prefill and speech-decoder timings always
+ * launch from the stream.  No reference counterpart. */
+int qtts_time_graph(qtts_ctx *ctx, int32_t on);
+
 /* Same for the standalone Q4 GEMV, cycling through `n_w` uploaded weights
  * of one shape (a pool larger than the 256 MB last-level cache measures
  * HBM, not cache). */

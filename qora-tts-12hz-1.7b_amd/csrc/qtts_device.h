@@ -86,7 +86,7 @@ struct DevState {
     int32_t n_text;          // trailing text rows
     int32_t ring_base;       // frame_idx of ring slot 0
     int32_t forced_base;     // frame_idx of forced row 0
-    int32_t pad0;
+    int32_t sync_err;        // a bounded cross-workgroup wait ran out (results invalid)
     // sampler parameters
     float temperature, top_p, rep_penalty, onset_temperature;
     int32_t top_k, onset_frames, eos_enabled;

@@ -76,6 +76,8 @@ struct Workspace {
     uint32_t *ring_pred, *ring_used;      // [RING_FRAMES][16]
     float2 *cand;      // lm-head argmax candidates [16 heads][MAX_CAND] (value, index bits)
     int attn_grid;     // attention workgroups at one page each (8 per page of the capacity)
+    uint64_t *ll_qkv;  // talker q|k|v as (epoch, value) words [S][npad], fused q|k|v + attention launch
+    uint32_t *ll_seq;  // epoch counter of those words (advanced by each talker o-proj launch)
 };
 
 // Buffers of the batched prefill, rows of one prompt chunk.
@@ -178,6 +180,10 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
 hipError_t enqueue_silu(float *x, int n, hipStream_t st);
 hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStream_t st);
 
+// True when every talker layer runs its q|k|v GEMV and decode attention as
+// one launch (two pages per attention work item at every length); the
+// caller then passes attn_pg = 2 for every step.
+bool talker_fused_attn(const TalkerDev &m);
 hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode, int attn_pg,
                                hipStream_t s);
 hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,

@@ -180,6 +180,7 @@ struct ProAttnCombine {
     const float *aacc;       // [MAX_CHUNKS][16][128] chunk P.V
     const DevState *st;
     int slot_ovr;            // >= 0: the row's KV slot (prefill rows), else st->kv_len
+    uint32_t *seq;           // advanced once per launch: the next q|k|v + attention launch's epoch
     template <int T, int KC>
     struct Fetch {
         int L;
@@ -242,7 +243,10 @@ struct ProAttnCombine {
             xs[i] = row < 16 * HEAD_DIM ? o / Ls : 0.0f;
         }
     }
-    __device__ void finish(int s, int c, int nct) const {}
+    __device__ void finish(int s, int c, int nct) const
+    {
+        if (seq && s == 0 && c == 0 && threadIdx.x == 0) *seq = *seq + 1;
+    }
 };
 
 // Residual update + RMSNorm (gemv.rs:445-454):
@@ -712,6 +716,23 @@ struct EpiPart {
     }
 };
 
+// Column sums stored as (epoch, value) words for a consumer in the same
+// launch (k_talker_qkv_attn): one 8-byte system-scope store per column, the
+// epoch (*seq + 1) in the high half, so a word and its epoch arrive
+// together and no fence is needed.
+struct EpiLL {
+    uint64_t *ll;            // [S][npad]
+    int npad;
+    const uint32_t *seq;
+    uint32_t epoch;          // *seq + 1, read by the kernel at its start
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
+    {
+        __hip_atomic_store(ll + (size_t)s * npad + c * C + cc, ((uint64_t)epoch << 32) | __float_as_uint(y(cc)),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+};
+
 // Row blockIdx.y of a batch of single rows: the per-row arithmetic of NB = 1
 // (used to build the predictor's projected-row tables at upload).
 struct ProPlainY {
@@ -886,8 +907,11 @@ __device__ __forceinline__ void rs_steps(float (&v)[NB][32], int lane, int &base
     }
 }
 
+// One tile of the GEMV on workgroup `item` (one workgroup per tile): the
+// body of k_gemv, and of the fused launches that host GEMV tiles beside
+// other work.
 template <int T, int GB, int R, int NB, class Pro, class Epi>
-__global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
+__device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, const Epi &epi, int item)
 {
     constexpr int P = T / GB;
     constexpr int KC = R * P;
@@ -910,7 +934,6 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
 
     {
         // launch_gemv starts exactly one workgroup per tile
-        const int item = blockIdx.x;
         if (item >= items) return;
         const int s = item / w.CT, c = item - s * w.CT;
         const uint8_t *tile = w.data + (size_t)item * w.tile_bytes;
@@ -1060,6 +1083,12 @@ __global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
         }
         pro.finish(s, c, w.CT);
     }
+}
+
+template <int T, int GB, int R, int NB, class Pro, class Epi>
+__global__ void __launch_bounds__(T) k_gemv(Q4Tiled w, Pro pro, Epi epi)
+{
+    gemv_tile<T, GB, R, NB>(w, pro, epi, blockIdx.x);
 }
 
 // A prologue that only supports one workgroup size declares it as
@@ -1224,11 +1253,25 @@ __device__ __forceinline__ void rs_step_n(float (&v)[N], bool sel)
     }
 }
 
-template <int PG>
-__global__ void __launch_bounds__(256 * PG, 2 / PG)
-k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
-              const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
-              int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
+// The q|k|v of the step arrive either as the q|k|v GEMV's k-slice partials
+// (`part`, written by an earlier launch) or, when the GEMV runs in the same
+// launch (LL), as (epoch, value) words `ll[s][col]` that its tiles store
+// with system-scope atomics: the attention workgroups poll their words
+// after issuing the page loads, so the pages stream in while the GEMV is
+// still running.  A word is current when its epoch is *seq + 1; the o-proj
+// launch that follows advances *seq, so words of an earlier launch never
+// match.  Polls are bounded: past LL_SPIN_MAX (milliseconds, against the
+// few microseconds the GEMV takes) the workgroup records sync_err in the
+// device state and finishes with whatever it read; once sync_err is set,
+// later launches do not wait at all.
+constexpr int LL_SPIN_MAX = 1 << 14;
+
+template <int PG, bool LL>
+__device__ __forceinline__ void
+talker_attn_body(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
+                 const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
+                 int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc,
+                 const uint64_t *ll, const uint32_t *seq, int bid)
 {
     static_assert(PG == 1 || PG == 2, "one or two pages per workgroup");
     constexpr int NWV = 4 * PG;
@@ -1246,7 +1289,7 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
     // the chunk's first page; the grid never exceeds the table) are read
     // beside the sequence length; the pages themselves only once the length
     // shows which are in use
-    const int g = blockIdx.x >> 3, h = blockIdx.x & 7;
+    const int g = bid >> 3, h = bid & 7;
     const int c = PG * g + wp;                     // this wave's page
     const int pgw = kv.ptab[min(c, MAX_CHUNKS - 1)];
     const int pgf = kv.ptab[min(PG * g, MAX_CHUNKS - 1)];
@@ -1257,6 +1300,12 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
     // the other arguments now, not after the length's wait
     asm volatile("" ::"s"(part), "s"(qn_g), "s"(kn_g), "s"(rope_cos), "s"(rope_sin), "s"(kv.base), "s"(aacc),
                  "s"(am), "s"(al), "s"(S), "s"(npad), "s"(layer), "s"(kv.n_phys));
+    uint32_t epoch = 0;
+    bool give_up = false;
+    if constexpr (LL) {
+        epoch = *seq + 1;
+        give_up = st->sync_err != 0;
+    }
     const int slot = slot_ovr >= 0 ? slot_ovr : (int)sv[2];
     const int64_t pos = pos_ovr >= 0 ? pos_ovr : (int64_t)(((uint64_t)sv[1] << 32) | sv[0]);
     const int L = slot + 1;
@@ -1275,11 +1324,13 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         // rotate-half pair), its gammas and RoPE values, then the page
         const int base = (wq < 2 ? 2 * h + wq : 16 + 8 * (wq - 2) + h) * HEAD_DIM + lane;
         float xa[RES_MAX_S], xb[RES_MAX_S];
+        if constexpr (!LL) {
 #pragma unroll
-        for (int s = 0; s < RES_MAX_S; s++) {
-            const float *p = part + (size_t)min(s, S - 1) * npad + base;
-            xa[s] = p[0];
-            xb[s] = p[64];
+            for (int s = 0; s < RES_MAX_S; s++) {
+                const float *p = part + (size_t)min(s, S - 1) * npad + base;
+                xa[s] = p[0];
+                xb[s] = p[64];
+            }
         }
         const uint16_t *gam = wq < 2 ? qn_g : kn_g;
         const uint32_t ga = gam[lane], gb = gam[lane + 64];
@@ -1295,6 +1346,33 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
         // nothing below may be scheduled above the page loads: a wait for the
         // step's vectors there would hold the pages back a round trip
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LL) {
+            // the step's vector from the GEMV tiles of this launch: waves of
+            // the second page only read LDS and skip the wait
+            for (int s = 0; s < RES_MAX_S; s++) { xa[s] = 0.0f; xb[s] = 0.0f; }
+            if (wv < 4) {
+                for (int it = 0;; it++) {
+                    bool ok = true;
+#pragma unroll
+                    for (int s = 0; s < RES_MAX_S; s++) {
+                        if (s < S) {
+                            const uint64_t *p = ll + (size_t)s * npad + base;
+                            const uint64_t wa = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                            const uint64_t wb = __hip_atomic_load(p + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                            ok = ok && (uint32_t)(wa >> 32) == epoch && (uint32_t)(wb >> 32) == epoch;
+                            xa[s] = __uint_as_float((uint32_t)wa);
+                            xb[s] = __uint_as_float((uint32_t)wb);
+                        }
+                    }
+                    if (__all(ok) || give_up) break;
+                    if (it >= LL_SPIN_MAX) {
+                        if (lane == 0) const_cast<DevState *>(st)->sync_err = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+        }
         // ---- QK-norm (talker.rs:286-297) and RoPE (rope.rs:79-92) in
         // registers: the sum of squares is the dims 0..63 wave sum plus the
         // dims 64..127 wave sum, in that order
@@ -1304,10 +1382,12 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             a = s < S ? a + xa[s] : a;
             b = s < S ? b + xb[s] : b;
         }
-        for (int s = RES_MAX_S; s < S; s++) {
-            const float *p = part + (size_t)s * npad + base;
-            a += p[0];
-            b += p[64];
+        if constexpr (!LL) {
+            for (int s = RES_MAX_S; s < S; s++) {
+                const float *p = part + (size_t)s * npad + base;
+                a += p[0];
+                b += p[64];
+            }
         }
         if (wq < 3) {
             const float ss = wave_sum_dpp(a * a) + wave_sum_dpp(b * b);
@@ -1408,6 +1488,41 @@ k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const ui
             }
         }
     }
+}
+
+// q|k|v GEMV and decode attention in one launch (two pages per attention
+// workgroup): workgroups [0, nq) are the GEMV's tiles, storing their column
+// sums as (epoch, value) words; the rest are the attention's work items,
+// which issue their page loads at once and then wait for their words.  The
+// GEMV tiles come first in the grid, and workgroups are dispatched in index
+// order, so every tile an attention workgroup waits for has been dispatched
+// before it and never waits itself.
+template <int T, int GB, int R>
+__global__ void __launch_bounds__(512, 1)
+k_talker_qkv_attn(Q4Tiled wq, ProResidRms<1, 2048> pro, EpiLL epi, int nq, const uint16_t *qn_g,
+                  const uint16_t *kn_g, const float *rope_cos, const float *rope_sin, const DevState *st,
+                  int64_t pos_ovr, int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
+{
+    static_assert(T == 512, "the attention side runs 512 threads (two pages)");
+    if ((int)blockIdx.x < nq) {
+        // the epoch loaded now, waited for only by the epilogue
+        EpiLL e = epi;
+        e.epoch = *epi.seq + 1;
+        gemv_tile<T, GB, R, 1>(wq, pro, e, blockIdx.x);
+        return;
+    }
+    talker_attn_body<2, true>(nullptr, wq.S, epi.npad, qn_g, kn_g, rope_cos, rope_sin, st, pos_ovr, slot_ovr,
+                              layer, kv, am, al, aacc, epi.ll, epi.seq, blockIdx.x - nq);
+}
+
+template <int PG>
+__global__ void __launch_bounds__(256 * PG, 2 / PG)
+k_talker_attn(const float *part, int S, int npad, const uint16_t *qn_g, const uint16_t *kn_g,
+              const float *rope_cos, const float *rope_sin, const DevState *st, int64_t pos_ovr,
+              int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
+{
+    talker_attn_body<PG, false>(part, S, npad, qn_g, kn_g, rope_cos, rope_sin, st, pos_ovr, slot_ovr, layer, kv, am,
+                                al, aacc, nullptr, nullptr, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2341,15 +2456,43 @@ static hipError_t swiglu_down(const LayerDev &L, const Workspace &ws, const ProG
 // that merges its chunks.
 template <int PG>
 static hipError_t talker_attn_o(const TalkerDev &m, const Workspace &ws, const LayerDev &L, int l,
-                                const DevState *st, int64_t pos_ovr, int slot_ovr, hipStream_t s)
+                                const DevState *st, int64_t pos_ovr, int slot_ovr, bool fused, hipStream_t s)
 {
-    const int grid = 8 * ((ws.attn_grid / 8 + PG - 1) / PG);
-    hipLaunchKernelGGL(k_talker_attn<PG>, dim3(grid), dim3(256 * PG), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
-                       L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
-                       ws.al, ws.aacc);
-    QCHK(hipGetLastError());
-    return launch_gemv<1>(L.o, ProAttnCombine<PG>{ws.am, ws.al, ws.aacc, st, slot_ovr},
+    if (!fused) {
+        const int grid = 8 * ((ws.attn_grid / 8 + PG - 1) / PG);
+        hipLaunchKernelGGL(k_talker_attn<PG>, dim3(grid), dim3(256 * PG), 0, s, ws.part_qkv, L.qkv.S, L.qkv.npad,
+                           L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, st, pos_ovr, slot_ovr, l, m.kv, ws.am,
+                           ws.al, ws.aacc);
+        QCHK(hipGetLastError());
+    }
+    return launch_gemv<1>(L.o, ProAttnCombine<PG>{ws.am, ws.al, ws.aacc, st, slot_ovr, ws.ll_seq},
                           EpiPart<1>{ws.part_o, L.o.npad}, s);
+}
+
+// The q|k|v GEMV and the two-page attention share one launch when the q|k|v
+// weight has the tile the fused kernel is built for (QTTS_FUSED_ATTN=0
+// keeps them apart).  Fused, two pages per work item is faster at every
+// length (KV 80-336: 507 frames/s unfused with one page, 517 fused with
+// two; KV 2064-2320: 492 unfused, 510 fused).
+static bool fused_attn_on()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_FUSED_ATTN");
+        return !(v && *v == '0');
+    }();
+    return on;
+}
+
+static bool qkv_attn_fusable(const LayerDev &L)
+{
+    return L.qkv.cfg == TILE_G1_T512_R2 && L.qkv.S <= RES_MAX_S && L.qkv.npad >= 32 * HEAD_DIM && fused_attn_on();
+}
+
+bool talker_fused_attn(const TalkerDev &m)
+{
+    for (int l = 0; l < m.n_layers; l++)
+        if (!qkv_attn_fusable(m.layers[l])) return false;
+    return m.n_layers > 0;
 }
 
 static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, const float *x_in,
@@ -2361,11 +2504,23 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
     // 1. residual + RMSNorm + fused q|k|v GEMV -> partials
     const ProResidRms<1, 2048> pre_attn{l == 0 ? x_in : ws.xa, H, P ? ws.part_down : nullptr, P ? P->down.S : 0, 1, 0,
                                   P ? P->down.npad : 0, nullptr, L.input_norm, H, ws.xb, nullptr};
-    QCHK(launch_gemv<1>(L.qkv, pre_attn, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
+    const bool fused = attn_pg == 2 && qkv_attn_fusable(L);
+    if (fused) {
+        // 1-2 in one launch: the GEMV's tiles, then the attention's work items
+        constexpr TileShape ts = tile_shape(TILE_G1_T512_R2);
+        const int nq = L.qkv.S * L.qkv.CT;
+        const int na = 8 * ((ws.attn_grid / 8 + 1) / 2);
+        hipLaunchKernelGGL((k_talker_qkv_attn<ts.T, ts.GB, ts.R>), dim3(nq + na), dim3(ts.T), 0, s, L.qkv, pre_attn,
+                           EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq, 0}, nq, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin,
+                           st, pos_ovr, slot_ovr, l, m.kv, ws.am, ws.al, ws.aacc);
+        QCHK(hipGetLastError());
+    } else {
+        QCHK(launch_gemv<1>(L.qkv, pre_attn, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
+    }
     // 2. QK-norm, RoPE, KV append, split-K attention over the pages
     // 3. o_proj -> partials, the pages merged in its prologue
-    QCHK(attn_pg == 2 ? talker_attn_o<2>(m, ws, L, l, st, pos_ovr, slot_ovr, s)
-                      : talker_attn_o<1>(m, ws, L, l, st, pos_ovr, slot_ovr, s));
+    QCHK(attn_pg == 2 ? talker_attn_o<2>(m, ws, L, l, st, pos_ovr, slot_ovr, fused, s)
+                      : talker_attn_o<1>(m, ws, L, l, st, pos_ovr, slot_ovr, fused, s));
     // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
     const ProResidRms<1, 2048> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
     return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);

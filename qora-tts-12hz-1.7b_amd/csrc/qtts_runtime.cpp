@@ -72,6 +72,7 @@ struct qtts_ctx {
     int64_t copy_floats = 0;
     float *d_read = nullptr;                         // streaming-read bound: READ_POOL buffers of READ_BYTES
     uint32_t *d_sink = nullptr;
+    bool time_graph = false;                         // qtts_time_*: launches captured in a graph and replayed
 
     PrefillWs pf{};                                  // batched-prefill rows (allocated on first use)
     void *pf_mem = nullptr;
@@ -719,6 +720,12 @@ static int alloc_workspace(qtts_ctx *c)
     RCHK(dev_alloc(c, A, &w.pv, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.h, 2 * (size_t)std::max(m.inter, p.inter)));
     RCHK(dev_alloc(c, A, &w.part_qkv, pq));
+    size_t lq = 0;
+    for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
+    RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
+    RCHK(dev_alloc(c, A, &w.ll_seq, 1));
+    HIPCHK(c, hipMemset(w.ll_qkv, 0, sizeof(uint64_t) * std::max<size_t>(lq, 32)));
+    HIPCHK(c, hipMemset(w.ll_seq, 0, sizeof(uint32_t)));
     RCHK(dev_alloc(c, A, &w.part_o, po));
     RCHK(dev_alloc(c, A, &w.part_gu, pg));
     RCHK(dev_alloc(c, A, &w.part_down, pd));
@@ -989,15 +996,34 @@ extern "C" int qtts_model_dims(qtts_ctx *c, int32_t *th, int32_t *tv, int32_t *t
 // talker
 // ---------------------------------------------------------------------------
 
+// A bounded cross-workgroup wait that ran out (the fused q|k|v + attention
+// launch) leaves sync_err set in the device state: reported once, then
+// cleared.
+static int check_sync(qtts_ctx *c)
+{
+    int32_t e = 0;
+    HIPCHK(c, hipMemcpyAsync(&e, &c->st_gen->sync_err, sizeof e, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (!e) return QTTS_OK;
+    const int32_t z = 0;
+    HIPCHK(c, hipMemcpy(&c->st_gen->sync_err, &z, sizeof z, hipMemcpyHostToDevice));
+    c->h_st->sync_err = 0;
+    return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (q|k|v + attention launch)");
+}
+
+// Pages per attention work item for a talker step at cached length kv.
+static int step_pages(const qtts_ctx *c, int64_t kv) { return talker_fused_attn(c->tm) ? 2 : attn_pages(kv); }
+
 // One talker step on the input already in ws.x.
 static int talker_step_staged(qtts_ctx *c, int64_t position, float *hidden_out, float *logits_out, int flags)
 {
     c->h_st->position = position;
     HIPCHK(c, hipMemcpyAsync(&c->st_gen->position, &c->h_st->position, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
-    HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, attn_pages(c->h_st->kv_len), c->stream));
+    HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, step_pages(c, c->h_st->kv_len), c->stream));
     RCHK(stage_out(c, c->ws.hidden, c->tm.hidden, hidden_out, flags));
     RCHK(stage_out(c, c->ws.logits, c->tm.vocab, logits_out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    RCHK(check_sync(c));
     c->h_st->kv_len += 1;
     c->h_st->position = position + 1;
     return QTTS_OK;
@@ -1075,9 +1101,10 @@ extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int
         for (int64_t t = 0; t < seq; t++) {
             RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
             HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t),
-                                         attn_pages(start_pos + t), c->stream));
+                                         step_pages(c, start_pos + t), c->stream));
         }
         HIPCHK(c, enqueue_final_norm(c->tm, c->ws, c->ws.hid_work, c->stream));
+        RCHK(check_sync(c));
     }
     RCHK(stage_out(c, c->ws.hid_work, H, hidden_out, flags));
     c->h_st->kv_len = (int32_t)(start_pos + seq);
@@ -2221,11 +2248,11 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
         // a stop are no-ops whichever variant runs them); the batch's graphs
         // are captured before its first launch
         if (graph) {
-            RCHK(build_frame_graph(c, attn_pages(c->h_st->kv_len)));
-            RCHK(build_frame_graph(c, attn_pages(c->h_st->kv_len + batch - 1)));
+            RCHK(build_frame_graph(c, step_pages(c, c->h_st->kv_len)));
+            RCHK(build_frame_graph(c, step_pages(c, c->h_st->kv_len + batch - 1)));
         }
         for (int64_t f = 0; f < batch; f++) {
-            const int pg = attn_pages(c->h_st->kv_len + f);
+            const int pg = step_pages(c, c->h_st->kv_len + f);
             if (graph) {
                 HIPCHK(c, hipGraphLaunch(c->frame_exec[pg - 1], c->stream));
             } else {
@@ -2241,6 +2268,10 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
         if (got < 0 || got > batch) return fail(c, QTTS_ERR_STATE, "frame counter out of step");
         if (pred_out) memcpy(pred_out + emitted * 16, c->h_ring, sizeof(uint32_t) * got * 16);
         emitted += got;
+        if (c->h_st->sync_err) {
+            *done = emitted;
+            RCHK(check_sync(c));
+        }
         if (c->h_st->nan_flag) {
             *done = emitted;
             return fail(c, QTTS_ERR_NAN, "NaN logits during generation");
@@ -2325,24 +2356,58 @@ extern "C" int qtts_gen_state(qtts_ctx *c, float *logits, float *hidden, int64_t
 // Average launch duration: one event pair around `iters` back-to-back
 // launches on the context stream (a warm-up launch first), so the figure is
 // the kernel plus the dispatch gap, without per-event overhead.
-static int time_launches(qtts_ctx *c, int32_t iters, const std::function<hipError_t(int)> &launch, double *avg_us)
+//
+// In graph mode (qtts_time_graph) the `iters` launches are captured once into
+// a graph, which is replayed once to warm up and then GRAPH_REPLAYS times
+// between the events: the launches then run as the frame loop runs its
+// kernels, from a replayed graph.  Launchers that replay a graph themselves
+// pass allow_graph = false.
+static int time_launches(qtts_ctx *c, int32_t iters, const std::function<hipError_t(int)> &launch, double *avg_us,
+                         bool allow_graph = true)
 {
+    constexpr int GRAPH_REPLAYS = 4;
+    const bool graph = allow_graph && c->time_graph;
     hipEvent_t e0, e1;
     HIPCHK(c, hipEventCreate(&e0));
     HIPCHK(c, hipEventCreate(&e1));
     int rc = QTTS_OK;
-    hipError_t err = launch(0);
-    if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
-    for (int i = 0; i < iters && err == hipSuccess; i++) err = launch(i);
+    hipError_t err = hipSuccess;
+    hipGraphExec_t ge = nullptr;
+    if (graph) {
+        hipGraph_t g = nullptr;
+        err = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+        if (err == hipSuccess) {
+            for (int i = 0; i < iters && err == hipSuccess; i++) err = launch(i);
+            const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
+            if (err == hipSuccess) err = e2;
+        }
+        if (err == hipSuccess) err = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        if (g) hipGraphDestroy(g);
+        if (err == hipSuccess) err = hipGraphLaunch(ge, c->stream);
+        if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+        for (int r = 0; r < GRAPH_REPLAYS && err == hipSuccess; r++) err = hipGraphLaunch(ge, c->stream);
+    } else {
+        err = launch(0);
+        if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+        for (int i = 0; i < iters && err == hipSuccess; i++) err = launch(i);
+    }
     if (err == hipSuccess) err = hipEventRecord(e1, c->stream);
     if (err == hipSuccess) err = hipEventSynchronize(e1);
     float ms = 0.0f;
     if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
     if (err != hipSuccess) rc = fail(c, QTTS_ERR_HIP, "kernel timing: %s", hipGetErrorString(err));
+    if (ge) hipGraphExecDestroy(ge);
     hipEventDestroy(e0);
     hipEventDestroy(e1);
-    *avg_us = ms * 1000.0 / iters;
+    *avg_us = ms * 1000.0 / ((double)iters * (graph ? GRAPH_REPLAYS : 1));
     return rc;
+}
+
+extern "C" int qtts_time_graph(qtts_ctx *c, int32_t on)
+{
+    if (!c || (on != 0 && on != 1)) return QTTS_ERR_INVALID;
+    c->time_graph = on != 0;
+    return QTTS_OK;
 }
 
 extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double *avg_us, double *bytes)
@@ -2440,7 +2505,7 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         hipGraphExec_t ge = nullptr;
         HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
         const hipError_t e = kind == 5 ? enqueue_frame_codes(m, p, c->ws, c->st_gen, c->d_forced, c->stream)
-                                       : enqueue_talker_step(m, c->ws, c->st_gen, 0, attn_pages(c->h_st->kv_len),
+                                       : enqueue_talker_step(m, c->ws, c->st_gen, 0, step_pages(c, c->h_st->kv_len),
                                                              c->stream);
         const hipError_t e2 = hipStreamEndCapture(c->stream, &g);
         if (e != hipSuccess || e2 != hipSuccess) {
@@ -2450,7 +2515,7 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         const hipError_t e3 = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         hipGraphDestroy(g);
         if (e3 != hipSuccess) return fail(c, QTTS_ERR_HIP, "graph instantiate: %s", hipGetErrorString(e3));
-        const int rc = time_launches(c, iters, [&](int) { return hipGraphLaunch(ge, c->stream); }, avg_us);
+        const int rc = time_launches(c, iters, [&](int) { return hipGraphLaunch(ge, c->stream); }, avg_us, false);
         hipGraphExecDestroy(ge);
         HIPCHK(c, hipMemcpyAsync(c->st_gen, &saved, sizeof saved, hipMemcpyHostToDevice, c->stream));
         HIPCHK(c, hipMemcpyAsync(c->ws.logits, lg.data(), lg.size() * sizeof(float), hipMemcpyHostToDevice, c->stream));
@@ -2512,7 +2577,7 @@ extern "C" int qtts_time_prefill(qtts_ctx *c, int64_t rows, int32_t what, int32_
         hipError_t e = hipMemcpyAsync(c->pf.x, src, (size_t)M * H * sizeof(float), hipMemcpyDeviceToDevice, c->stream);
         if (e != hipSuccess) return e;
         return enqueue_talker_prefill(m, c->pf, M, 0, c->ws.hid_work, c->stream);
-    }, avg_us);
+    }, avg_us, false);
     c->h_st->kv_len = 0;
     c->h_st->position = 0;
     HIPCHK(c, hipMemcpyAsync(c->st_gen, c->h_st, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
@@ -2544,7 +2609,7 @@ extern "C" int qtts_time_decode(qtts_ctx *c, int64_t n_frames, int32_t iters, do
     RCHK(ensure_io(c, (int64_t)T * factor));
     *flops = decode_flops(d, T);
     return time_launches(c, iters, [&](int) { return enqueue_decode(d, c->dws, c->dws.codes, T, 0, c->d_io, c->stream); },
-                         avg_us);
+                         avg_us, false);
 }
 
 extern "C" int qtts_time_gemv(qtts_ctx *c, const qtts_w *const *ws, int32_t n_w, int32_t iters, double *avg_us,

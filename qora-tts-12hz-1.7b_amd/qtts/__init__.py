@@ -108,6 +108,7 @@ SIGNATURES = {
     "qtts_gen_state": ([c_void_p, c_void_p, c_void_p, POINTER(c_int64), POINTER(c_uint64)], c_int),
     "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_device_bytes": ([c_void_p, c_void_p], c_int),
+    "qtts_time_graph": ([c_void_p, c_int32], c_int),
     "qtts_time_gemv": ([c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_prefill": ([c_void_p, c_int64, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_time_decode": ([c_void_p, c_int64, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
@@ -528,6 +529,11 @@ class Context:
         us, b = c_double(), c_double()
         self._check(self.lib.qtts_time_kernel(self.h, kind, iters, byref(us), byref(b)))
         return us.value, b.value
+
+    def time_graph(self, on):
+        """Timing calls launch from a replayed graph (True) or from the
+        stream (False, the default)."""
+        self._check(self.lib.qtts_time_graph(self.h, 1 if on else 0))
 
     def time_gemv(self, weights, iters):
         arr = (c_void_p * len(weights))(*[w.h for w in weights])

@@ -11,6 +11,11 @@ the o-proj's weights, KV 2560) and 21 (the first 22-chunk block after them);
 frame loop's last); 8192 positions (the largest cache).  A frame loop crosses
 the KV-1024 switch inside one batch of frames.
 
+By default the q|k|v GEMV and the attention run as one launch, two pages
+per work item at every length; a q|k|v tile other than the fused kernel's
+(QTTS_TILE_TQKV) keeps them apart, with one page per work item below
+KV 1024.  Both paths are checked.
+
 Bars: hidden, logits and the appended K/V row within 1e-3 of the scale
 (f32 accumulation in another order); the L loaded rows bit-exact.
 """
@@ -38,12 +43,18 @@ def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.fixture(scope="module")
-def long_model(ctx_factory):
+# q|k|v tiles: the fused launch's (the default) and one the unfused kernels take
+FUSED, UNFUSED = "15", "13"
+
+
+@pytest.fixture(scope="module", params=[FUSED, UNFUSED], ids=["fused", "unfused"])
+def long_model(ctx_factory, request):
     t = synth.make_talker(seed=131, n_layers=2, text_vocab=256, rope_max_pos=CAP)
     p = synth.make_predictor(seed=132, n_layers=2)
     c = ctx_factory(CAP)
-    c.upload_model(t, p)
+    with pytest.MonkeyPatch.context() as mp:
+        mp.setenv("QTTS_TILE_TQKV", request.param)
+        c.upload_model(t, p)
     O.set_workers(16, 8)
     om = O.Model(t, p, kv_cap=CAP)
     yield c, om, t
@@ -97,10 +108,11 @@ def test_steps_across_page_boundary(long_model):
 
 
 def test_frames_across_attention_switch(long_model):
-    """Sampled frames teacher-forced from KV 1018 to 1030 in one batch: the
-    frames before KV 1024 replay the one-page attention graph, those after the
-    two-page one; codes, generator state and the final hidden/logits against
-    the oracle's frame loop (generate_new.rs:606-675)."""
+    """Sampled frames teacher-forced from KV 1018 to 1030 in one batch: when
+    the launches are apart, the frames before KV 1024 replay the one-page
+    attention graph and those after the two-page one (fused, every frame
+    replays the two-page graph); codes, generator state and the final
+    hidden/logits against the oracle's frame loop (generate_new.rs:606-675)."""
     c, om, t = long_model
     L, n_frames = 1018, 12
     rng = np.random.Generator(np.random.PCG64(1401))
