@@ -270,6 +270,7 @@ struct ProResidRms {
     int k;
     float *x_out;
     float *side;
+    uint32_t *seq;           // when set: advanced once per launch (the epoch of a fused launch before it)
     __device__ static float *xf_lds()
     {
         __shared__ float xf[NB * KMAX];
@@ -372,6 +373,7 @@ struct ProResidRms {
     // after the tile: slice-0 workgroups store their share of x / normed x
     __device__ void finish(int s, int c, int nct) const
     {
+        if (seq && s == 0 && c == 0 && threadIdx.x == 0) *seq = *seq + 1;
         if (s != 0 || (!x_out && !side)) return;
         const float *xf = xf_lds();
         const int per = (k + nct - 1) / nct;
@@ -1619,9 +1621,15 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
 // (slice sums, so MS = 1 reads the bits the partials would give); the
 // workgroup then records the code as the skipped q|k|v launch's prologue did
 // and the slice-0 workgroups write the layer's residual input row to x_out.
-template <int NB, int MS, bool TAB = false>
+//
+// LL (q|k|v GEMV in the same launch, k_pred_qkv_attn_o): q|k|v arrive as the
+// GEMV tiles' (epoch, value) words ll[s][col] instead of partial sums; the
+// fetch issues everything else, and the load stage polls the words (bounded,
+// as in the talker's fused launch) once the weights are in flight.
+template <int NB, int MS, bool TAB = false, bool LL = false>
 struct ProPredAttn {
     static_assert(!TAB || (NB == 1 && MS == 1), "table rows: one row, slice sums");
+    static_assert(!LL || (!TAB && NB == 1), "words: one row, no table");
     static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
     static constexpr int HPW = 2;        // kv heads per workgroup
     static constexpr int NC4 = HPW * PRED_KV_CAP * (HEAD_DIM / 4) / 256;   // cached float4 per thread
@@ -1642,6 +1650,9 @@ struct ProPredAttn {
     const float *xtab;       // [rows][xk] the layer's input row of each code
     float *x_out;
     int xk;
+    // LL only (st above takes sync_err)
+    const uint64_t *ll;      // [S][npad] q|k|v words
+    const uint32_t *seq;
 
     __device__ static uint32_t *code_lds()
     {
@@ -1657,6 +1668,8 @@ struct ProPredAttn {
         f32x4 kc[NC4], vc[NC4];
         uint32_t pred, used;
         bool nan;
+        uint32_t epoch;
+        int give_up;
     };
     template <int T, int KC>
     __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
@@ -1687,16 +1700,21 @@ struct ProPredAttn {
             }
             pbase = tab + (size_t)min(f.used, (uint32_t)(rows - 1)) * npad;
         }
+        if constexpr (LL) {
+            f.epoch = *seq + 1;
+            f.give_up = st->sync_err;
+        } else {
 #pragma unroll
-        for (int s = 0; s < MS; s++)
+            for (int s = 0; s < MS; s++)
 #pragma unroll
-            for (int b = 0; b < NB; b++) {
-                const float *pp = pbase + (s * NB + b) * npad;
-                f.q[b][s][0] = pp[qcol];
-                f.q[b][s][1] = pp[qcol + 64];
-                f.kv[b][s][0] = pp[kvcol];
-                f.kv[b][s][1] = pp[kvcol + 64];
-            }
+                for (int b = 0; b < NB; b++) {
+                    const float *pp = pbase + (s * NB + b) * npad;
+                    f.q[b][s][0] = pp[qcol];
+                    f.q[b][s][1] = pp[qcol + 64];
+                    f.kv[b][s][0] = pp[kvcol];
+                    f.kv[b][s][1] = pp[kvcol + 64];
+                }
+        }
         f.gq[0] = qn_g[lane];
         f.gq[1] = qn_g[lane + 64];
         f.gk[0] = kn_g[lane];
@@ -1738,14 +1756,50 @@ struct ProPredAttn {
             }
         }
         const float gq0 = h2f(f.gq[0]), gq1 = h2f(f.gq[1]), gk0 = h2f(f.gk[0]), gk1 = h2f(f.gk[1]);
+        float wq[NB][MS][2], wkv[NB][MS][2];
+        if constexpr (LL) {
+            const int qcol = (2 * h0 + wv) * HEAD_DIM + lane;
+            const int kvcol = 16 * HEAD_DIM + (wv >> 1) * 8 * HEAD_DIM + (h0 + (wv & 1)) * HEAD_DIM + lane;
+            for (int it = 0;; it++) {
+                bool ok = true;
+#pragma unroll
+                for (int s = 0; s < MS; s++) {
+                    const uint64_t *pp = ll + (size_t)s * npad;
+                    const uint64_t w0 = __hip_atomic_load(pp + qcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    const uint64_t w1 = __hip_atomic_load(pp + qcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    const uint64_t w2 = __hip_atomic_load(pp + kvcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    const uint64_t w3 = __hip_atomic_load(pp + kvcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    ok = ok && (uint32_t)(w0 >> 32) == f.epoch && (uint32_t)(w1 >> 32) == f.epoch &&
+                         (uint32_t)(w2 >> 32) == f.epoch && (uint32_t)(w3 >> 32) == f.epoch;
+                    wq[0][s][0] = __uint_as_float((uint32_t)w0);
+                    wq[0][s][1] = __uint_as_float((uint32_t)w1);
+                    wkv[0][s][0] = __uint_as_float((uint32_t)w2);
+                    wkv[0][s][1] = __uint_as_float((uint32_t)w3);
+                }
+                if (__all(ok) || f.give_up) break;
+                if (it >= LL_SPIN_MAX) {
+                    if (lane == 0) st->sync_err = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int s = 0; s < MS; s++) {
+                    wq[b][s][0] = f.q[b][s][0]; wq[b][s][1] = f.q[b][s][1];
+                    wkv[b][s][0] = f.kv[b][s][0]; wkv[b][s][1] = f.kv[b][s][1];
+                }
+        }
 #pragma unroll
         for (int b = 0; b < NB; b++) {
             // k-slice sums in slice order
-            float q0 = f.q[b][0][0], q1 = f.q[b][0][1], v0 = f.kv[b][0][0], v1 = f.kv[b][0][1];
+            float q0 = wq[b][0][0], q1 = wq[b][0][1], v0 = wkv[b][0][0], v1 = wkv[b][0][1];
 #pragma unroll
             for (int s = 1; s < MS; s++) {
-                q0 += f.q[b][s][0]; q1 += f.q[b][s][1];
-                v0 += f.kv[b][s][0]; v1 += f.kv[b][s][1];
+                q0 += wq[b][s][0]; q1 += wq[b][s][1];
+                v0 += wkv[b][s][0]; v1 += wkv[b][s][1];
             }
             // QK-norm over the head's 128 dims (talker.rs:89-99; code_predictor.rs:84-93)
             const float iq = 1.0f / sqrtf(wave_sum_dpp(q0 * q0 + q1 * q1) / 128.0f + 1e-6f);
@@ -2594,9 +2648,47 @@ static ProPredAttn<NB, MS> pred_attn_pro(const PredictorDev &p, const LayerDev &
                                pos0, Kc, Vc};
 }
 
+// Predictor q|k|v GEMV and attention + o-proj in one launch (one row):
+// workgroups [0, nq) are the q|k|v tiles, storing (epoch, value) words; the
+// rest are the o-proj tiles, whose prologue issues its cache, gamma and
+// weight loads at once and attends when its words arrive.  The q|k|v tiles
+// come first in the grid, so every tile an o-proj workgroup waits for has
+// been dispatched before it and never waits itself.  The gate|up launch that
+// follows advances the epoch.
+template <int MS>
+__global__ void __launch_bounds__(256)
+k_pred_qkv_attn_o(Q4Tiled wq, ProResidRms<1, 1024> pq, EpiLL eq, int nq, Q4Tiled wo,
+                  ProPredAttn<1, MS, false, true> po, EpiPart<1> eo)
+{
+    if ((int)blockIdx.x < nq) {
+        EpiLL e = eq;
+        e.epoch = *eq.seq + 1;
+        gemv_tile<256, 1, 2, 1>(wq, pq, e, blockIdx.x);
+        return;
+    }
+    gemv_tile<256, 1, 2, 1>(wo, po, eo, blockIdx.x - nq);
+}
+
+// QTTS_FUSED_PRED=0 keeps the predictor's q|k|v and attention + o-proj apart.
+static bool fused_pred_on()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_FUSED_PRED");
+        return !(v && *v == '0');
+    }();
+    return on;
+}
+
+static bool pred_qkv_attn_fusable(const PredictorDev &p, const LayerDev &L)
+{
+    return fused_pred_on() && pred_attn_fusable(p, L) && L.qkv.cfg == TILE_G1_T256_R2 &&
+           L.o.cfg == TILE_G1_T256_R2 && L.qkv.S == 2;
+}
+
 template <int NB>
 static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s,
-                             const ProCodeRowRms<1024> *row_in = nullptr, const float *qkv_tab = nullptr)
+                             const ProCodeRowRms<1024> *row_in = nullptr, const float *qkv_tab = nullptr,
+                             DevState *st = nullptr)
 {
     const LayerDev &L = p.layers[l];
     const int h = p.hidden;
@@ -2611,6 +2703,8 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
             return launch_gemv_then_mlp<1>(p, L, ws, pro, s);
         }
     }
+    float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
+    float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     if (NB == 1 && row_in) {
         QCHK(launch_gemv<1>(L.qkv, *row_in, EpiPart<1>{ws.part_qkv, L.qkv.npad}, s));
     } else {
@@ -2619,10 +2713,26 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
                                            L.input_norm, h, ws.pxb, nullptr}
                    : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
                                            p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
+        if constexpr (NB == 1) {
+            if (st && pred_qkv_attn_fusable(p, L)) {
+                // q|k|v and attention + o-proj in one launch; the gate|up launch advances the epoch
+                const ProPredAttn<1, 2, false, true> po{nullptr, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm,
+                                                        p.rope_cos, p.rope_sin, pos0, Kc, Vc, nullptr, 0, nullptr,
+                                                        0, st, 0, nullptr, nullptr, nullptr, 0, ws.ll_qkv,
+                                                        ws.ll_seq};
+                const int nq = L.qkv.S * L.qkv.CT, no = L.o.S * L.o.CT;
+                hipLaunchKernelGGL(k_pred_qkv_attn_o<2>, dim3(nq + no), dim3(256), 0, s, L.qkv, pre_attn,
+                                   EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq, 0}, nq, L.o, po,
+                                   EpiPart<1>{ws.part_o, L.o.npad});
+                QCHK(hipGetLastError());
+                ProResidRms<1, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, h,
+                                             ws.pxa, nullptr};
+                pre_mlp.seq = ws.ll_seq;
+                return swiglu_down<1>(L, ws, pre_mlp, p.inter, s);
+            }
+        }
         QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
     }
-    float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
-    float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
     if (pred_attn_fusable(p, L)) {
         // attention inside the o-proj prologue
         switch (L.qkv.S) {
@@ -2696,7 +2806,7 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
             QCHK(pred_layer<1>(p, ws, 0, 1 + g, s, &row_in,
                                p.qkv_rows ? p.qkv_rows + (size_t)(g - 1) * p.emb_rows.rows * p.layers[0].qkv.npad
                                           : nullptr));
-            for (int l = 1; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
+            for (int l = 1; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s, nullptr, nullptr, st));
             QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
             continue;
         }
@@ -2709,7 +2819,7 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
                                 EpiPart<1>{ws.part_proj, p.proj.npad}, s));
         else
             QCHK(launch_gemv<1>(p.proj, ProEmbed{e, &st->used[g]}, EpiPart<1>{ws.part_proj, p.proj.npad}, s));
-        for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s));
+        for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<1>(p, ws, l, 1 + g, s, nullptr, nullptr, st));
         QCHK(pred_head(p, ws, st, g, 1, 0, forced, codes_api, s));
     }
     // API calls resolve the last code here; a frame's combine does it itself

@@ -722,6 +722,7 @@ static int alloc_workspace(qtts_ctx *c)
     RCHK(dev_alloc(c, A, &w.part_qkv, pq));
     size_t lq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
+    for (const LayerDev &L : c->players) upd(lq, L.qkv, 1);
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
     RCHK(dev_alloc(c, A, &w.ll_seq, 1));
     HIPCHK(c, hipMemset(w.ll_qkv, 0, sizeof(uint64_t) * std::max<size_t>(lq, 32)));
@@ -1008,7 +1009,7 @@ static int check_sync(qtts_ctx *c)
     const int32_t z = 0;
     HIPCHK(c, hipMemcpy(&c->st_gen->sync_err, &z, sizeof z, hipMemcpyHostToDevice));
     c->h_st->sync_err = 0;
-    return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (q|k|v + attention launch)");
+    return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (fused q|k|v + attention launch)");
 }
 
 // Pages per attention work item for a talker step at cached length kv.
@@ -1957,6 +1958,7 @@ extern "C" int qtts_predictor_chain(qtts_ctx *c, const float *th, const float *s
     HIPCHK(c, hipMemcpyAsync(&back, c->st_api, sizeof(DevState), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (back.nan_flag) return fail(c, QTTS_ERR_NAN, "NaN logits in the predictor");
+    if (back.sync_err) return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (predictor q|k|v + attention launch)");
     return QTTS_OK;
 }
 
