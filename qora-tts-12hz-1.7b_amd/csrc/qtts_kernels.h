@@ -16,6 +16,14 @@ inline int attn_pages(int64_t kv_len) { return kv_len >= ATTN_LONG_KV ? 2 : 1; }
 constexpr int RING_FRAMES = 64;          // frames per host synchronisation, max
 constexpr int MAX_CAND = 64;             // lm-head column tiles reduced by one wave
 
+// Epoch counters of the fused launches.  A launch of one kind reads its
+// counter at its start and stamps its words with counter + 1; a launch that
+// always runs between two launches of that kind, and never reads that
+// counter, advances it: the talker o-proj advances LL_TQKV and LL_TMLP, the
+// predictor's attention + o-proj launches advance LL_PMLP, the predictor's
+// MLP launch (fused or its gate|up) advances LL_PQKV.
+enum LlKind { LL_TQKV = 0, LL_PQKV = 1, LL_PMLP = 2, LL_TMLP = 3, LL_KINDS = 4 };
+
 struct KvPaged {
     float *base;           // [layers][n_phys][2 (K,V)][8 heads][64 pos][128]
     const int32_t *ptab;   // logical page -> physical page
@@ -76,8 +84,13 @@ struct Workspace {
     uint32_t *ring_pred, *ring_used;      // [RING_FRAMES][16]
     float2 *cand;      // lm-head argmax candidates [16 heads][MAX_CAND] (value, index bits)
     int attn_grid;     // attention workgroups at one page each (8 per page of the capacity)
-    uint64_t *ll_qkv;  // talker q|k|v as (epoch, value) words [S][npad], fused q|k|v + attention launch
-    uint32_t *ll_seq;  // epoch counter of those words (advanced by each talker o-proj launch)
+    // (epoch, value) words handed between the two halves of a fused launch,
+    // one buffer per kind of launch, and the epoch counter of each kind
+    uint64_t *ll_qkv;  // talker q|k|v [S][npad] (q|k|v GEMV + attention)
+    uint64_t *ll_pqkv; // predictor q|k|v [S][npad] (q|k|v GEMV + attention + o-proj)
+    uint64_t *ll_th;   // talker silu(gate)*up [inter] (gate|up + down)
+    uint64_t *ll_ph;   // predictor silu(gate)*up [inter] (gate|up + down)
+    uint32_t *ll_seq;  // [LL_KINDS] epoch counters, indexed by LlKind
 };
 
 // Buffers of the batched prefill, rows of one prompt chunk.
@@ -184,6 +197,10 @@ hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStre
 // one launch (two pages per attention work item at every length); the
 // caller then passes attn_pg = 2 for every step.
 bool talker_fused_attn(const TalkerDev &m);
+// True unless QTTS_FUSED_MLP=0: gate|up and down run as one launch where the
+// tiles allow (single-slice gate|up); the predictor's gate|up then takes a
+// single-slice tile.
+bool fused_mlp_enabled();
 hipError_t enqueue_talker_step(const TalkerDev &m, const Workspace &ws, DevState *st, int frame_mode, int attn_pg,
                                hipStream_t s);
 hipError_t enqueue_talker_row(const TalkerDev &m, const Workspace &ws, const DevState *st, int64_t pos,

@@ -41,6 +41,13 @@ __device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t m)
     return r;
 }
 
+// Bound on the polls of a workgroup waiting for (epoch, value) words from
+// another workgroup of the same launch: past it (milliseconds, against the
+// few microseconds a producer takes) the workgroup records sync_err in the
+// device state and finishes with whatever it read; once sync_err is set,
+// later launches do not wait at all.
+constexpr int LL_SPIN_MAX = 1 << 14;
+
 // ---------------------------------------------------------------------------
 // wave-wide sum (deterministic butterfly order)
 // ---------------------------------------------------------------------------
@@ -180,7 +187,7 @@ struct ProAttnCombine {
     const float *aacc;       // [MAX_CHUNKS][16][128] chunk P.V
     const DevState *st;
     int slot_ovr;            // >= 0: the row's KV slot (prefill rows), else st->kv_len
-    uint32_t *seq;           // advanced once per launch: the next q|k|v + attention launch's epoch
+    uint32_t *seq;           // the epoch counters: LL_TQKV and LL_TMLP advanced once per launch
     template <int T, int KC>
     struct Fetch {
         int L;
@@ -245,7 +252,10 @@ struct ProAttnCombine {
     }
     __device__ void finish(int s, int c, int nct) const
     {
-        if (seq && s == 0 && c == 0 && threadIdx.x == 0) *seq = *seq + 1;
+        if (seq && s == 0 && c == 0 && threadIdx.x == 0) {
+            seq[LL_TQKV] = seq[LL_TQKV] + 1;
+            seq[LL_TMLP] = seq[LL_TMLP] + 1;
+        }
     }
 };
 
@@ -733,6 +743,75 @@ struct EpiLL {
         __hip_atomic_store(ll + (size_t)s * npad + c * C + cc, ((uint64_t)epoch << 32) | __float_as_uint(y(cc)),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+};
+
+// silu(gate) * up of an interleaved single-slice gate|up tile (EpiSwiglu)
+// stored as (epoch, value) words for the down projection's tiles in the
+// same launch (k_mlp).
+struct EpiSwigluLL {
+    uint64_t *ll;            // [inter]
+    const uint32_t *seq;
+    uint32_t epoch;          // *seq + 1, read by the kernel at its start
+    template <class Y>
+    __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
+    {
+        if ((cc & 63) < 32) {
+            const int j = (c * C + cc) >> 6;
+            const float h = silu_f(y(cc)) * y(cc + 32);
+            __hip_atomic_store(ll + j * 32 + (cc & 31), ((uint64_t)epoch << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+};
+
+// GEMV input rows k0.. from (epoch, value) words that producer tiles of the
+// same launch store (k_mlp's down projection): fetch reads the epoch, load
+// polls the slice's words (bounded, as every such wait) once the weights are
+// in flight.  Rows past n read as 0.
+struct ProLL {
+    const uint64_t *ll;
+    int n;
+    const uint32_t *seq;
+    DevState *st;
+    template <int T, int KC>
+    struct Fetch {
+        uint32_t epoch;
+        int give_up;
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        f.epoch = *seq + 1;
+        f.give_up = st->sync_err;
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        constexpr int U = (KC + T - 1) / T;
+        float v[U];
+        for (int it = 0;; it++) {
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int r = k0 + (int)threadIdx.x + u * T;
+                const uint64_t w = __hip_atomic_load(ll + min(r, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                ok = ok && (r >= n || (uint32_t)(w >> 32) == f.epoch);
+                v[u] = r < n ? __uint_as_float((uint32_t)w) : 0.0f;
+            }
+            if (__all(ok) || f.give_up) break;
+            if (it >= LL_SPIN_MAX) {
+                if ((threadIdx.x & 63) == 0) st->sync_err = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = threadIdx.x + u * T;
+            if (i < KC) xs[i] = v[u];
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const {}
 };
 
 // Row blockIdx.y of a batch of single rows: the per-row arithmetic of NB = 1
@@ -1262,11 +1341,7 @@ __device__ __forceinline__ void rs_step_n(float (&v)[N], bool sel)
 // after issuing the page loads, so the pages stream in while the GEMV is
 // still running.  A word is current when its epoch is *seq + 1; the o-proj
 // launch that follows advances *seq, so words of an earlier launch never
-// match.  Polls are bounded: past LL_SPIN_MAX (milliseconds, against the
-// few microseconds the GEMV takes) the workgroup records sync_err in the
-// device state and finishes with whatever it read; once sync_err is set,
-// later launches do not wait at all.
-constexpr int LL_SPIN_MAX = 1 << 14;
+// match.  Polls are bounded (LL_SPIN_MAX).
 
 template <int PG, bool LL>
 __device__ __forceinline__ void
@@ -1653,6 +1728,7 @@ struct ProPredAttn {
     // LL only (st above takes sync_err)
     const uint64_t *ll;      // [S][npad] q|k|v words
     const uint32_t *seq;
+    uint32_t *adv;           // an epoch counter advanced once per launch (the MLP launch's), or null
 
     __device__ static uint32_t *code_lds()
     {
@@ -1865,6 +1941,7 @@ struct ProPredAttn {
     }
     __device__ void finish(int s, int c, int nct) const
     {
+        if (adv && s == 0 && c == 0 && threadIdx.x == 0) *adv = *adv + 1;
         if constexpr (TAB) {
             if (s != 0 || !x_out) return;
             const float *row = xtab + (size_t)min(*code_lds(), (uint32_t)(rows - 1)) * xk;
@@ -2488,12 +2565,86 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
     return hipGetLastError();
 }
 
+// gate|up and down in one launch (one row): workgroups [0, ng) are the
+// gate|up tiles (single slice, interleaved groups), storing silu(gate) * up
+// as (epoch, value) words; the rest are the down projection's tiles, which
+// issue their weight loads at once and take their k-slice of the words when
+// they arrive.  The gate|up tiles come first in the grid, so every tile a
+// down workgroup waits for has been dispatched before it and never waits.
+template <int GBG, int RG, int RD, int KMAX>
+__global__ void __launch_bounds__(512)
+k_mlp(Q4Tiled wg, ProResidRms<1, KMAX> pg, EpiSwigluLL eg, int ng, Q4Tiled wd, ProLL pd, EpiPart<1> ed)
+{
+    if ((int)blockIdx.x < ng) {
+        EpiSwigluLL e = eg;
+        e.epoch = *eg.seq + 1;
+        gemv_tile<512, GBG, RG, 1>(wg, pg, e, blockIdx.x);
+        return;
+    }
+    gemv_tile<512, 1, RD, 1>(wd, pd, ed, blockIdx.x - ng);
+}
+
+// The words and epoch of a fused gate|up + down launch.
+struct MlpFuse {
+    uint64_t *ll;
+    uint32_t *seq;
+    DevState *st;
+};
+
+// QTTS_FUSED_MLP=0 keeps gate|up and down apart.
+static bool fused_mlp_on()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_FUSED_MLP");
+        return !(v && *v == '0');
+    }();
+    return on;
+}
+
+bool fused_mlp_enabled() { return fused_mlp_on(); }
+
+// Tile pairs k_mlp is built for: the talker's (gate|up 2 groups x 2048 rows,
+// down 4 rows per thread) and the predictor's (2 groups x 1024 rows, down 2
+// rows per thread), 512 threads each.
+template <int KMAX>
+static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProResidRms<1, KMAX> &pro_gu, int inter,
+                             const MlpFuse &fz, hipStream_t s)
+{
+    const int ng = L.gate_up.S * L.gate_up.CT, nd = L.down.S * L.down.CT;
+    const EpiSwigluLL eg{fz.ll, fz.seq, 0};
+    const ProLL pd{fz.ll, inter, fz.seq, fz.st};
+    const EpiPart<1> ed{ws.part_down, L.down.npad};
+    if (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4)
+        hipLaunchKernelGGL((k_mlp<2, 8, 4, KMAX>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng, L.down,
+                           pd, ed);
+    else if (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2)
+        hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng, L.down,
+                           pd, ed);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+static bool mlp_fusable(const LayerDev &L)
+{
+    if (!fused_mlp_on() || L.gate_up.S != 1) return false;
+    return (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4) ||
+           (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2);
+}
+
 // gate|up then down: h = silu(gate) * up written by the gate|up epilogue when
-// the gate|up weight is one slice, else formed in the down prologue.
+// the gate|up weight is one slice, else formed in the down prologue; with
+// `fz` and tiles k_mlp is built for, both in one launch.
 template <int NB, class ProGU>
 static hipError_t swiglu_down(const LayerDev &L, const Workspace &ws, const ProGU &pro_gu, int inter,
-                              hipStream_t s)
+                              hipStream_t s, const MlpFuse *fz = nullptr)
 {
+    if constexpr (NB == 1 && std::is_same<ProGU, ProResidRms<1, 1024>>::value) {
+        if (fz && mlp_fusable(L)) return launch_mlp<1024>(L, ws, pro_gu, inter, *fz, s);
+    }
+    if constexpr (NB == 1 && std::is_same<ProGU, ProResidRms<1, 2048>>::value) {
+        if (fz && mlp_fusable(L)) return launch_mlp<2048>(L, ws, pro_gu, inter, *fz, s);
+    }
     if (L.gate_up.S == 1 && tile_shape(L.gate_up.cfg).GB % 2 == 0) {
         QCHK(launch_gemv<NB>(L.gate_up, pro_gu, EpiSwiglu<NB>{ws.h, inter}, s));
         return launch_gemv<NB>(L.down, ProPlain<NB>{ws.h, inter, inter}, EpiPart<NB>{ws.part_down, L.down.npad}, s);
@@ -2565,7 +2716,7 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
         const int nq = L.qkv.S * L.qkv.CT;
         const int na = 8 * ((ws.attn_grid / 8 + 1) / 2);
         hipLaunchKernelGGL((k_talker_qkv_attn<ts.T, ts.GB, ts.R>), dim3(nq + na), dim3(ts.T), 0, s, L.qkv, pre_attn,
-                           EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq, 0}, nq, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin,
+                           EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq + LL_TQKV, 0}, nq, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin,
                            st, pos_ovr, slot_ovr, l, m.kv, ws.am, ws.al, ws.aacc);
         QCHK(hipGetLastError());
     } else {
@@ -2577,7 +2728,8 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
                       : talker_attn_o<1>(m, ws, L, l, st, pos_ovr, slot_ovr, fused, s));
     // 5-6. residual + RMSNorm + gate|up, SiLU * up, down -> partials
     const ProResidRms<1, 2048> pre_mlp{ws.xb, H, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, H, ws.xa, nullptr};
-    return swiglu_down<1>(L, ws, pre_mlp, m.inter, s);
+    const MlpFuse fz{ws.ll_th, ws.ll_seq + LL_TMLP, const_cast<DevState *>(st)};
+    return swiglu_down<1>(L, ws, pre_mlp, m.inter, s, st ? &fz : nullptr);
 }
 
 // Final norm of the residual (talker.rs:352-353) into `side` + codec-head
@@ -2630,7 +2782,7 @@ hipError_t enqueue_codec_head(const TalkerDev &m, const Workspace &ws, const flo
 // projection partials + bias.
 template <int NB, class Pro>
 static hipError_t launch_gemv_then_mlp(const PredictorDev &p, const LayerDev &L, const Workspace &ws,
-                                       const Pro &pro, hipStream_t s);
+                                       const Pro &pro, hipStream_t s, DevState *st = nullptr);
 
 // The fused attention prologue covers 2 kv heads per workgroup of 256
 // threads: o-proj tiles of 256 threads and 512 rows, 16 / 8 heads of 128.
@@ -2645,7 +2797,22 @@ static ProPredAttn<NB, MS> pred_attn_pro(const PredictorDev &p, const LayerDev &
                                          float *Kc, float *Vc)
 {
     return ProPredAttn<NB, MS>{ws.part_qkv, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin,
-                               pos0, Kc, Vc};
+                               pos0, Kc, Vc, nullptr, 0, nullptr, 0, nullptr, 0, nullptr, nullptr, nullptr, 0,
+                               nullptr, nullptr, ws.ll_seq + LL_PMLP};
+}
+
+// The predictor MLP after the attention + o-proj: residual + RMSNorm,
+// gate|up, down (one launch when fusable and `st` takes the wait errors).
+// Its gate|up advances the LL_PQKV epoch.
+template <int NB>
+static hipError_t pred_mlp(const PredictorDev &p, const LayerDev &L, const Workspace &ws, hipStream_t s,
+                           DevState *st)
+{
+    const int h = p.hidden;
+    ProResidRms<NB, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
+    pre_mlp.seq = ws.ll_seq + LL_PQKV;
+    const MlpFuse fz{ws.ll_ph, ws.ll_seq + LL_PMLP, st};
+    return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s, st ? &fz : nullptr);
 }
 
 // Predictor q|k|v GEMV and attention + o-proj in one launch (one row):
@@ -2699,8 +2866,9 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
             float *Vc = ws.pv + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
             ProPredAttn<1, 1, true> pro{nullptr, 1, L.qkv.npad, L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0,
                                         Kc, Vc, qkv_tab, row_in->rows, row_in->cand, row_in->ncand, row_in->st,
-                                        row_in->slot, row_in->codes_api, row_in->table, row_in->x_out, row_in->k};
-            return launch_gemv_then_mlp<1>(p, L, ws, pro, s);
+                                        row_in->slot, row_in->codes_api, row_in->table, row_in->x_out, row_in->k,
+                                        nullptr, nullptr, ws.ll_seq + LL_PMLP};
+            return launch_gemv_then_mlp<1>(p, L, ws, pro, s, row_in->st);
         }
     }
     float *Kc = ws.pk + (size_t)l * PRED_KV_CAP * 8 * HEAD_DIM;
@@ -2718,17 +2886,14 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
                 // q|k|v and attention + o-proj in one launch; the gate|up launch advances the epoch
                 const ProPredAttn<1, 2, false, true> po{nullptr, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm,
                                                         p.rope_cos, p.rope_sin, pos0, Kc, Vc, nullptr, 0, nullptr,
-                                                        0, st, 0, nullptr, nullptr, nullptr, 0, ws.ll_qkv,
-                                                        ws.ll_seq};
+                                                        0, st, 0, nullptr, nullptr, nullptr, 0, ws.ll_pqkv,
+                                                        ws.ll_seq + LL_PQKV, ws.ll_seq + LL_PMLP};
                 const int nq = L.qkv.S * L.qkv.CT, no = L.o.S * L.o.CT;
                 hipLaunchKernelGGL(k_pred_qkv_attn_o<2>, dim3(nq + no), dim3(256), 0, s, L.qkv, pre_attn,
-                                   EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq, 0}, nq, L.o, po,
+                                   EpiLL{ws.ll_pqkv, L.qkv.npad, ws.ll_seq + LL_PQKV, 0}, nq, L.o, po,
                                    EpiPart<1>{ws.part_o, L.o.npad});
                 QCHK(hipGetLastError());
-                ProResidRms<1, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, 1, 0, L.o.npad, nullptr, L.post_norm, h,
-                                             ws.pxa, nullptr};
-                pre_mlp.seq = ws.ll_seq;
-                return swiglu_down<1>(L, ws, pre_mlp, p.inter, s);
+                return pred_mlp<1>(p, L, ws, s, st);
             }
         }
         QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
@@ -2736,27 +2901,26 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
     if (pred_attn_fusable(p, L)) {
         // attention inside the o-proj prologue
         switch (L.qkv.S) {
-        case 1: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 1>(p, L, ws, pos0, Kc, Vc), s);
-        case 2: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 2>(p, L, ws, pos0, Kc, Vc), s);
-        case 3: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 3>(p, L, ws, pos0, Kc, Vc), s);
-        default: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 4>(p, L, ws, pos0, Kc, Vc), s);
+        case 1: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 1>(p, L, ws, pos0, Kc, Vc), s, st);
+        case 2: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 2>(p, L, ws, pos0, Kc, Vc), s, st);
+        case 3: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 3>(p, L, ws, pos0, Kc, Vc), s, st);
+        default: return launch_gemv_then_mlp<NB>(p, L, ws, pred_attn_pro<NB, 4>(p, L, ws, pos0, Kc, Vc), s, st);
         }
     }
     hipLaunchKernelGGL(k_pred_attn, dim3(p.n_kv_heads), dim3(256), 0, s, ws.part_qkv, L.qkv.S, NB, L.qkv.npad,
                        L.q_norm, L.k_norm, p.rope_cos, p.rope_sin, pos0, Kc, Vc, ws.pattn);
     QCHK(hipGetLastError());
+    // this o-proj does not advance the MLP epoch: the MLP stays two launches
     const int qd = p.n_heads * HEAD_DIM;
-    return launch_gemv_then_mlp<NB>(p, L, ws, ProPlain<NB>{ws.pattn, qd, qd}, s);
+    return launch_gemv_then_mlp<NB>(p, L, ws, ProPlain<NB>{ws.pattn, qd, qd}, s, nullptr);
 }
 
 template <int NB, class Pro>
 static hipError_t launch_gemv_then_mlp(const PredictorDev &p, const LayerDev &L, const Workspace &ws,
-                                       const Pro &pro, hipStream_t s)
+                                       const Pro &pro, hipStream_t s, DevState *st)
 {
-    const int h = p.hidden;
     QCHK(launch_gemv<NB>(L.o, pro, EpiPart<NB>{ws.part_o, L.o.npad}, s));
-    const ProResidRms<NB, 1024> pre_mlp{ws.pxb, h, ws.part_o, L.o.S, NB, 0, L.o.npad, nullptr, L.post_norm, h, ws.pxa, nullptr};
-    return swiglu_down<NB>(L, ws, pre_mlp, p.inter, s);
+    return pred_mlp<NB>(p, L, ws, s, st);
 }
 
 // A single-slice lm head whose column tiles fit one wave writes per-tile

@@ -193,7 +193,10 @@ static int default_cfg(const char *role, int64_t k)
     if (r == "TO" || r == "PQKV" || r == "PO" || r == "PPROJ") return TILE_G1_T256_R2;   // KC 512
     if (r == "HEAD" || r == "PHEAD") return TILE_G1_T256_R4;                    // KC 1024
     if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;            // one slice, SiLU epilogue
-    if (r == "PGU") return k <= 1024 ? TILE_G2_T256_R4 : TILE_G2_T512;          // 2 slices, SwiGLU in the down prologue
+    if (r == "PGU") {
+        if (k <= 1024 && fused_mlp_enabled()) return TILE_G2_T512_R4;           // one slice: gate|up + down in one launch
+        return k <= 1024 ? TILE_G2_T256_R4 : TILE_G2_T512;                      // 2 slices, SwiGLU in the down prologue
+    }
     if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
     if (r == "PDOWN") return TILE_G1_T512_R2;                                   // KC 1024
     if (r == "GEMV") return TILE_G1_T256;                                       // standalone Q4 GEMV
@@ -720,13 +723,20 @@ static int alloc_workspace(qtts_ctx *c)
     RCHK(dev_alloc(c, A, &w.pv, (size_t)p.n_layers * PRED_KV_CAP * 8 * HEAD_DIM));
     RCHK(dev_alloc(c, A, &w.h, 2 * (size_t)std::max(m.inter, p.inter)));
     RCHK(dev_alloc(c, A, &w.part_qkv, pq));
-    size_t lq = 0;
+    size_t lq = 0, lpq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
-    for (const LayerDev &L : c->players) upd(lq, L.qkv, 1);
+    for (const LayerDev &L : c->players) upd(lpq, L.qkv, 1);
+    const size_t lth = (size_t)m.inter, lph = (size_t)p.inter;
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
-    RCHK(dev_alloc(c, A, &w.ll_seq, 1));
+    RCHK(dev_alloc(c, A, &w.ll_pqkv, lpq));
+    RCHK(dev_alloc(c, A, &w.ll_th, lth));
+    RCHK(dev_alloc(c, A, &w.ll_ph, lph));
+    RCHK(dev_alloc(c, A, &w.ll_seq, LL_KINDS));
     HIPCHK(c, hipMemset(w.ll_qkv, 0, sizeof(uint64_t) * std::max<size_t>(lq, 32)));
-    HIPCHK(c, hipMemset(w.ll_seq, 0, sizeof(uint32_t)));
+    HIPCHK(c, hipMemset(w.ll_pqkv, 0, sizeof(uint64_t) * std::max<size_t>(lpq, 32)));
+    HIPCHK(c, hipMemset(w.ll_th, 0, sizeof(uint64_t) * std::max<size_t>(lth, 32)));
+    HIPCHK(c, hipMemset(w.ll_ph, 0, sizeof(uint64_t) * std::max<size_t>(lph, 32)));
+    HIPCHK(c, hipMemset(w.ll_seq, 0, sizeof(uint32_t) * LL_KINDS));
     RCHK(dev_alloc(c, A, &w.part_o, po));
     RCHK(dev_alloc(c, A, &w.part_gu, pg));
     RCHK(dev_alloc(c, A, &w.part_down, pd));
