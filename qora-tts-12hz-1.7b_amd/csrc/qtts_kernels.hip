@@ -732,24 +732,28 @@ struct EpiPart {
 // launch (k_talker_qkv_attn): one 8-byte system-scope store per column, the
 // epoch (*seq + 1) in the high half, so a word and its epoch arrive
 // together and no fence is needed.
+template <int NB = 1>
 struct EpiLL {
-    uint64_t *ll;            // [S][npad]
+    uint64_t *ll;            // [S][NB][npad]
     int npad;
     const uint32_t *seq;
     uint32_t epoch;          // *seq + 1, read by the kernel at its start
     template <class Y>
     __device__ void operator()(int s, int b, int c, int cc, int C, const Y &y) const
     {
-        __hip_atomic_store(ll + (size_t)s * npad + c * C + cc, ((uint64_t)epoch << 32) | __float_as_uint(y(cc)),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(ll + ((size_t)s * NB + b) * npad + c * C + cc,
+                           ((uint64_t)epoch << 32) | __float_as_uint(y(cc)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
     }
 };
 
 // silu(gate) * up of an interleaved single-slice gate|up tile (EpiSwiglu)
 // stored as (epoch, value) words for the down projection's tiles in the
 // same launch (k_mlp).
+template <int NB = 1>
 struct EpiSwigluLL {
-    uint64_t *ll;            // [inter]
+    uint64_t *ll;            // [NB][ld]
+    int ld;                  // inter
     const uint32_t *seq;
     uint32_t epoch;          // *seq + 1, read by the kernel at its start
     template <class Y>
@@ -758,8 +762,8 @@ struct EpiSwigluLL {
         if ((cc & 63) < 32) {
             const int j = (c * C + cc) >> 6;
             const float h = silu_f(y(cc)) * y(cc + 32);
-            __hip_atomic_store(ll + j * 32 + (cc & 31), ((uint64_t)epoch << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(ll + (size_t)b * ld + j * 32 + (cc & 31), ((uint64_t)epoch << 32) | __float_as_uint(h),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
 };
@@ -768,8 +772,9 @@ struct EpiSwigluLL {
 // same launch store (k_mlp's down projection): fetch reads the epoch, load
 // polls the slice's words (bounded, as every such wait) once the weights are
 // in flight.  Rows past n read as 0.
+template <int NB = 1>
 struct ProLL {
-    const uint64_t *ll;
+    const uint64_t *ll;      // [NB][n]
     int n;
     const uint32_t *seq;
     DevState *st;
@@ -787,14 +792,16 @@ struct ProLL {
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
-        constexpr int U = (KC + T - 1) / T;
+        constexpr int U = (NB * KC + T - 1) / T;
         float v[U];
         for (int it = 0;; it++) {
             bool ok = true;
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                const int r = k0 + (int)threadIdx.x + u * T;
-                const uint64_t w = __hip_atomic_load(ll + min(r, n - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const int i = min((int)threadIdx.x + u * T, NB * KC - 1);
+                const int b = i / KC, r = k0 + (i - b * KC);
+                const uint64_t w = __hip_atomic_load(ll + (size_t)b * n + min(r, n - 1), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_SYSTEM);
                 ok = ok && (r >= n || (uint32_t)(w >> 32) == f.epoch);
                 v[u] = r < n ? __uint_as_float((uint32_t)w) : 0.0f;
             }
@@ -808,7 +815,7 @@ struct ProLL {
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int i = threadIdx.x + u * T;
-            if (i < KC) xs[i] = v[u];
+            if (i < NB * KC) xs[i] = v[u];
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -1576,14 +1583,14 @@ talker_attn_body(const float *part, int S, int npad, const uint16_t *qn_g, const
 // before it and never waits itself.
 template <int T, int GB, int R>
 __global__ void __launch_bounds__(512, 1)
-k_talker_qkv_attn(Q4Tiled wq, ProResidRms<1, 2048> pro, EpiLL epi, int nq, const uint16_t *qn_g,
+k_talker_qkv_attn(Q4Tiled wq, ProResidRms<1, 2048> pro, EpiLL<1> epi, int nq, const uint16_t *qn_g,
                   const uint16_t *kn_g, const float *rope_cos, const float *rope_sin, const DevState *st,
                   int64_t pos_ovr, int slot_ovr, int layer, KvPaged kv, float *am, float *al, float *aacc)
 {
     static_assert(T == 512, "the attention side runs 512 threads (two pages)");
     if ((int)blockIdx.x < nq) {
         // the epoch loaded now, waited for only by the epilogue
-        EpiLL e = epi;
+        EpiLL<1> e = epi;
         e.epoch = *epi.seq + 1;
         gemv_tile<T, GB, R, 1>(wq, pro, e, blockIdx.x);
         return;
@@ -1704,7 +1711,7 @@ k_pred_attn(const float *part, int S, int NB, int npad, const uint16_t *qn_g, co
 template <int NB, int MS, bool TAB = false, bool LL = false>
 struct ProPredAttn {
     static_assert(!TAB || (NB == 1 && MS == 1), "table rows: one row, slice sums");
-    static_assert(!LL || (!TAB && NB == 1), "words: one row, no table");
+    static_assert(!LL || !TAB, "words or a table row, not both");
     static constexpr int kOnlyT = 256;   // launch_gemv instantiates 256-thread tiles only
     static constexpr int HPW = 2;        // kv heads per workgroup
     static constexpr int NC4 = HPW * PRED_KV_CAP * (HEAD_DIM / 4) / 256;   // cached float4 per thread
@@ -1839,19 +1846,23 @@ struct ProPredAttn {
             for (int it = 0;; it++) {
                 bool ok = true;
 #pragma unroll
-                for (int s = 0; s < MS; s++) {
-                    const uint64_t *pp = ll + (size_t)s * npad;
-                    const uint64_t w0 = __hip_atomic_load(pp + qcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    const uint64_t w1 = __hip_atomic_load(pp + qcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    const uint64_t w2 = __hip_atomic_load(pp + kvcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    const uint64_t w3 = __hip_atomic_load(pp + kvcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    ok = ok && (uint32_t)(w0 >> 32) == f.epoch && (uint32_t)(w1 >> 32) == f.epoch &&
-                         (uint32_t)(w2 >> 32) == f.epoch && (uint32_t)(w3 >> 32) == f.epoch;
-                    wq[0][s][0] = __uint_as_float((uint32_t)w0);
-                    wq[0][s][1] = __uint_as_float((uint32_t)w1);
-                    wkv[0][s][0] = __uint_as_float((uint32_t)w2);
-                    wkv[0][s][1] = __uint_as_float((uint32_t)w3);
-                }
+                for (int s = 0; s < MS; s++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        const uint64_t *pp = ll + ((size_t)s * NB + b) * npad;
+                        const uint64_t w0 = __hip_atomic_load(pp + qcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        const uint64_t w1 =
+                            __hip_atomic_load(pp + qcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        const uint64_t w2 = __hip_atomic_load(pp + kvcol, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        const uint64_t w3 =
+                            __hip_atomic_load(pp + kvcol + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        ok = ok && (uint32_t)(w0 >> 32) == f.epoch && (uint32_t)(w1 >> 32) == f.epoch &&
+                             (uint32_t)(w2 >> 32) == f.epoch && (uint32_t)(w3 >> 32) == f.epoch;
+                        wq[b][s][0] = __uint_as_float((uint32_t)w0);
+                        wq[b][s][1] = __uint_as_float((uint32_t)w1);
+                        wkv[b][s][0] = __uint_as_float((uint32_t)w2);
+                        wkv[b][s][1] = __uint_as_float((uint32_t)w3);
+                    }
                 if (__all(ok) || f.give_up) break;
                 if (it >= LL_SPIN_MAX) {
                     if (lane == 0) st->sync_err = 1;
@@ -2571,17 +2582,17 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
 // issue their weight loads at once and take their k-slice of the words when
 // they arrive.  The gate|up tiles come first in the grid, so every tile a
 // down workgroup waits for has been dispatched before it and never waits.
-template <int GBG, int RG, int RD, int KMAX>
+template <int GBG, int RG, int RD, int KMAX, int NB>
 __global__ void __launch_bounds__(512)
-k_mlp(Q4Tiled wg, ProResidRms<1, KMAX> pg, EpiSwigluLL eg, int ng, Q4Tiled wd, ProLL pd, EpiPart<1> ed)
+k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled wd, ProLL<NB> pd, EpiPart<NB> ed)
 {
     if ((int)blockIdx.x < ng) {
-        EpiSwigluLL e = eg;
+        EpiSwigluLL<NB> e = eg;
         e.epoch = *eg.seq + 1;
-        gemv_tile<512, GBG, RG, 1>(wg, pg, e, blockIdx.x);
+        gemv_tile<512, GBG, RG, NB>(wg, pg, e, blockIdx.x);
         return;
     }
-    gemv_tile<512, 1, RD, 1>(wd, pd, ed, blockIdx.x - ng);
+    gemv_tile<512, 1, RD, NB>(wd, pd, ed, blockIdx.x - ng);
 }
 
 // The words and epoch of a fused gate|up + down launch.
@@ -2606,20 +2617,20 @@ bool fused_mlp_enabled() { return fused_mlp_on(); }
 // Tile pairs k_mlp is built for: the talker's (gate|up 2 groups x 2048 rows,
 // down 4 rows per thread) and the predictor's (2 groups x 1024 rows, down 2
 // rows per thread), 512 threads each.
-template <int KMAX>
-static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProResidRms<1, KMAX> &pro_gu, int inter,
+template <int NB, int KMAX>
+static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProResidRms<NB, KMAX> &pro_gu, int inter,
                              const MlpFuse &fz, hipStream_t s)
 {
     const int ng = L.gate_up.S * L.gate_up.CT, nd = L.down.S * L.down.CT;
-    const EpiSwigluLL eg{fz.ll, fz.seq, 0};
-    const ProLL pd{fz.ll, inter, fz.seq, fz.st};
-    const EpiPart<1> ed{ws.part_down, L.down.npad};
+    const EpiSwigluLL<NB> eg{fz.ll, inter, fz.seq, 0};
+    const ProLL<NB> pd{fz.ll, inter, fz.seq, fz.st};
+    const EpiPart<NB> ed{ws.part_down, L.down.npad};
     if (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4)
-        hipLaunchKernelGGL((k_mlp<2, 8, 4, KMAX>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng, L.down,
-                           pd, ed);
+        hipLaunchKernelGGL((k_mlp<2, 8, 4, KMAX, NB>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
+                           L.down, pd, ed);
     else if (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2)
-        hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng, L.down,
-                           pd, ed);
+        hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX, NB>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
+                           L.down, pd, ed);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2639,11 +2650,11 @@ template <int NB, class ProGU>
 static hipError_t swiglu_down(const LayerDev &L, const Workspace &ws, const ProGU &pro_gu, int inter,
                               hipStream_t s, const MlpFuse *fz = nullptr)
 {
-    if constexpr (NB == 1 && std::is_same<ProGU, ProResidRms<1, 1024>>::value) {
-        if (fz && mlp_fusable(L)) return launch_mlp<1024>(L, ws, pro_gu, inter, *fz, s);
+    if constexpr (std::is_same<ProGU, ProResidRms<NB, 1024>>::value) {
+        if (fz && mlp_fusable(L)) return launch_mlp<NB, 1024>(L, ws, pro_gu, inter, *fz, s);
     }
     if constexpr (NB == 1 && std::is_same<ProGU, ProResidRms<1, 2048>>::value) {
-        if (fz && mlp_fusable(L)) return launch_mlp<2048>(L, ws, pro_gu, inter, *fz, s);
+        if (fz && mlp_fusable(L)) return launch_mlp<1, 2048>(L, ws, pro_gu, inter, *fz, s);
     }
     if (L.gate_up.S == 1 && tile_shape(L.gate_up.cfg).GB % 2 == 0) {
         QCHK(launch_gemv<NB>(L.gate_up, pro_gu, EpiSwiglu<NB>{ws.h, inter}, s));
@@ -2716,7 +2727,7 @@ static hipError_t talker_layer(const TalkerDev &m, const Workspace &ws, int l, c
         const int nq = L.qkv.S * L.qkv.CT;
         const int na = 8 * ((ws.attn_grid / 8 + 1) / 2);
         hipLaunchKernelGGL((k_talker_qkv_attn<ts.T, ts.GB, ts.R>), dim3(nq + na), dim3(ts.T), 0, s, L.qkv, pre_attn,
-                           EpiLL{ws.ll_qkv, L.qkv.npad, ws.ll_seq + LL_TQKV, 0}, nq, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin,
+                           EpiLL<1>{ws.ll_qkv, L.qkv.npad, ws.ll_seq + LL_TQKV, 0}, nq, L.q_norm, L.k_norm, m.rope_cos, m.rope_sin,
                            st, pos_ovr, slot_ovr, l, m.kv, ws.am, ws.al, ws.aacc);
         QCHK(hipGetLastError());
     } else {
@@ -2822,18 +2833,18 @@ static hipError_t pred_mlp(const PredictorDev &p, const LayerDev &L, const Works
 // come first in the grid, so every tile an o-proj workgroup waits for has
 // been dispatched before it and never waits itself.  The gate|up launch that
 // follows advances the epoch.
-template <int MS>
+template <int MS, int NB>
 __global__ void __launch_bounds__(256)
-k_pred_qkv_attn_o(Q4Tiled wq, ProResidRms<1, 1024> pq, EpiLL eq, int nq, Q4Tiled wo,
-                  ProPredAttn<1, MS, false, true> po, EpiPart<1> eo)
+k_pred_qkv_attn_o(Q4Tiled wq, ProResidRms<NB, 1024> pq, EpiLL<NB> eq, int nq, Q4Tiled wo,
+                  ProPredAttn<NB, MS, false, true> po, EpiPart<NB> eo)
 {
     if ((int)blockIdx.x < nq) {
-        EpiLL e = eq;
+        EpiLL<NB> e = eq;
         e.epoch = *eq.seq + 1;
-        gemv_tile<256, 1, 2, 1>(wq, pq, e, blockIdx.x);
+        gemv_tile<256, 1, 2, NB>(wq, pq, e, blockIdx.x);
         return;
     }
-    gemv_tile<256, 1, 2, 1>(wo, po, eo, blockIdx.x - nq);
+    gemv_tile<256, 1, 2, NB>(wo, po, eo, blockIdx.x - nq);
 }
 
 // QTTS_FUSED_PRED=0 keeps the predictor's q|k|v and attention + o-proj apart.
@@ -2881,20 +2892,18 @@ static hipError_t pred_layer(const PredictorDev &p, const Workspace &ws, int l, 
                                            L.input_norm, h, ws.pxb, nullptr}
                    : ProResidRms<NB, 1024>{ws.pxa, h, ws.part_down, p.layers[l - 1].down.S, NB, 0,
                                            p.layers[l - 1].down.npad, nullptr, L.input_norm, h, ws.pxb, nullptr};
-        if constexpr (NB == 1) {
-            if (st && pred_qkv_attn_fusable(p, L)) {
-                // q|k|v and attention + o-proj in one launch; the gate|up launch advances the epoch
-                const ProPredAttn<1, 2, false, true> po{nullptr, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm,
-                                                        p.rope_cos, p.rope_sin, pos0, Kc, Vc, nullptr, 0, nullptr,
-                                                        0, st, 0, nullptr, nullptr, nullptr, 0, ws.ll_pqkv,
-                                                        ws.ll_seq + LL_PQKV, ws.ll_seq + LL_PMLP};
-                const int nq = L.qkv.S * L.qkv.CT, no = L.o.S * L.o.CT;
-                hipLaunchKernelGGL(k_pred_qkv_attn_o<2>, dim3(nq + no), dim3(256), 0, s, L.qkv, pre_attn,
-                                   EpiLL{ws.ll_pqkv, L.qkv.npad, ws.ll_seq + LL_PQKV, 0}, nq, L.o, po,
-                                   EpiPart<1>{ws.part_o, L.o.npad});
-                QCHK(hipGetLastError());
-                return pred_mlp<1>(p, L, ws, s, st);
-            }
+        if (st && pred_qkv_attn_fusable(p, L)) {
+            // q|k|v and attention + o-proj in one launch; the gate|up launch advances the epoch
+            const ProPredAttn<NB, 2, false, true> po{nullptr, L.qkv.S, L.qkv.npad, L.q_norm, L.k_norm,
+                                                     p.rope_cos, p.rope_sin, pos0, Kc, Vc, nullptr, 0, nullptr,
+                                                     0, st, 0, nullptr, nullptr, nullptr, 0, ws.ll_pqkv,
+                                                     ws.ll_seq + LL_PQKV, ws.ll_seq + LL_PMLP};
+            const int nq = L.qkv.S * L.qkv.CT, no = L.o.S * L.o.CT;
+            hipLaunchKernelGGL((k_pred_qkv_attn_o<2, NB>), dim3(nq + no), dim3(256), 0, s, L.qkv, pre_attn,
+                               EpiLL<NB>{ws.ll_pqkv, L.qkv.npad, ws.ll_seq + LL_PQKV, 0}, nq, L.o, po,
+                               EpiPart<NB>{ws.part_o, L.o.npad});
+            QCHK(hipGetLastError());
+            return pred_mlp<NB>(p, L, ws, s, st);
         }
         QCHK(launch_gemv<NB>(L.qkv, pre_attn, EpiPart<NB>{ws.part_qkv, L.qkv.npad}, s));
     }
@@ -2958,7 +2967,7 @@ hipError_t enqueue_predictor_chain(const PredictorDev &p, const TalkerDev &m, co
         QCHK(launch_gemv<2>(p.proj, ProHidEmbed{hidden, m.codec_rows, &st->used[0], m.hidden},
                             EpiPart<2>{ws.part_proj, p.proj.npad}, s));
     }
-    for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, 0, s));
+    for (int l = 0; l < p.n_layers; l++) QCHK(pred_layer<2>(p, ws, l, 0, s, nullptr, nullptr, st));
     QCHK(pred_head(p, ws, st, 0, 2, 1, forced, codes_api, s));           // :247-248
     for (int g = 1; g < p.n_groups; g++) {
         if (p.proj_rows) {

@@ -725,8 +725,8 @@ static int alloc_workspace(qtts_ctx *c)
     RCHK(dev_alloc(c, A, &w.part_qkv, pq));
     size_t lq = 0, lpq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
-    for (const LayerDev &L : c->players) upd(lpq, L.qkv, 1);
-    const size_t lth = (size_t)m.inter, lph = (size_t)p.inter;
+    for (const LayerDev &L : c->players) upd(lpq, L.qkv, 2);
+    const size_t lth = (size_t)m.inter, lph = 2 * (size_t)p.inter;   // predictor words: up to 2 rows
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
     RCHK(dev_alloc(c, A, &w.ll_pqkv, lpq));
     RCHK(dev_alloc(c, A, &w.ll_th, lth));
