@@ -420,15 +420,30 @@ def main():
             "frames_per_s": round(loop_frames / (t_ramp + t_warm + dt), 2),
             "note": "the whole frame loop from the prompt, untimed ramp + warm-up + the timed frames"}
 
-    # kernels at the final KV length (~2112): HIP events around back-to-back launches
+    # the frame's two halves, each captured alone and replayed (the state is
+    # restored afterwards): the talker step at KV ~2112, and the sampler +
+    # predictor chain + combine
+    tk_us, tk_bytes = ctx.time_kernel(6, 16)
+    pc_us, pc_bytes = ctx.time_kernel(5, 16)
+    log(f"talker step {tk_us:.1f}us, sampler + predictor chain + combine {pc_us:.1f}us")
+    split = {"talker_step_us": round(tk_us, 1), "talker_step_weight_bytes": int(tk_bytes),
+             "predictor_chain_us": round(pc_us, 1), "predictor_weight_bytes": int(pc_bytes),
+             "note": "each half of the frame captured alone and replayed back to back (KV ~2112); "
+                     "the whole frame is slower than the sum by the predictor weights falling out "
+                     "of the last-level cache between frames"}
+
+    # kernels at the final KV length (~2112): HIP events around back-to-back
+    # launches.  These two are the component kernels timed alone: in the frame
+    # the attention shares a launch with the q|k|v GEMV, and the gate|up one
+    # with the down projection.
     gu_us, gu_bytes = ctx.time_kernel(0, 4 * args.layers)
     at_us, at_bytes = ctx.time_kernel(1, 4 * args.layers)
     cp_us, cp_bytes = ctx.time_kernel(2, 20)
     log(f"gate|up {gu_us:.2f}us ({gu_bytes / gu_us / 1e3:.0f} GB/s), attention {at_us:.2f}us "
         f"({at_bytes / at_us / 1e3:.0f} GB/s), float4 copy 256 MiB {cp_bytes / cp_us / 1e3:.0f} GB/s")
 
-    # Q4 GEMV k=2048 -> n=6144 (the dominant kernel family: k_gemv is ~3/4 of
-    # the frame's GPU time) over a pool of distinct weights (> 256 MB
+    # Q4 GEMV k=2048 -> n=6144 (the GEMV tiles run inside every launch of
+    # the frame) over a pool of distinct weights (> 256 MB
     # last-level cache); a streaming read of the same bytes in one launch
     # (its attainable bound); then the same kernel streaming a 113 MB weight
     grng = np.random.Generator(np.random.PCG64(1))
@@ -520,6 +535,7 @@ def main():
         "roofline": roof,
         "frame_roofline": frame_roof,
         "device_memory_mb": mem,
+        "frame_split": split,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }
