@@ -34,6 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, "qora-tts-12hz-1.7b_amd"))
 
 HBM_PEAK_GBS = 8000.0
 F32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense f32 matrix peak
+F16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
 ICL_ROWS = 400                 # ICL prompt positions (text + reference codes)
 TTS_PAD = 151671          # generate_new.rs:28
 PROMPT = 64                    # prompt positions
@@ -175,7 +176,12 @@ def cpu_baseline(talker, pred, logits, hidden, pad, kv_len, seconds, isa=None):
 def time_prefill(ctx, layers):
     """The ICL-prompt prefill on the matrix cores: the gate|up GEMM alone
     (cycling the layers) and the whole 400-position prefill, as achieved
-    TFLOP/s against the f32 MFMA peak."""
+    TFLOP/s of the algorithmic (f32-accurate) work against the f32 MFMA
+    peak.  The GEMMs issue that work as three f16 matrix products per pair of
+    split operands (QTTS_GEMM_F32=1: f32 matrix instructions instead), so
+    `f16_mfma_issue` gives 3x the GEMM's algorithmic rate against the dense
+    f16 MFMA peak."""
+    f32 = os.environ.get("QTTS_GEMM_F32", "0") not in ("", "0")
     g_us, g_fl = ctx.time_prefill(ICL_ROWS, 0, 4 * layers)
     p_us, p_fl = ctx.time_prefill(ICL_ROWS, 1, 3)
     g_tf, p_tf = g_fl / g_us / 1e6, p_fl / p_us / 1e6
@@ -185,8 +191,12 @@ def time_prefill(ctx, layers):
             "frac_f32_mfma": round(p_tf / F32_MFMA_PEAK_TFLOPS, 4), "flops": p_fl,
             "gate_up_gemm": {"shape": f"[{ICL_ROWS} x 2048] x [2048 x 12288], SwiGLU epilogue", "us": round(g_us, 2),
                              "tflops": round(g_tf, 2), "frac_f32_mfma": round(g_tf / F32_MFMA_PEAK_TFLOPS, 4),
+                             "f16_mfma_issue": None if f32 else round(3 * g_tf / F16_MFMA_PEAK_TFLOPS, 4),
                              "flops": g_fl},
-            "peak_tflops": F32_MFMA_PEAK_TFLOPS, "dtype": "f32 (v_mfma_f32_16x16x4_f32)"}
+            "peak_tflops": F32_MFMA_PEAK_TFLOPS,
+            "dtype": "f32 (v_mfma_f32_16x16x4_f32)" if f32 else
+                     "f32-accurate: operands split into f16 hi + lo, hi*hi + hi*lo + lo*hi on "
+                     "v_mfma_f32_16x16x32_f16 with f32 accumulation"}
 
 
 ICL_FRAMES = 512               # decode frames after the ICL prompt (KV 400 -> 912)

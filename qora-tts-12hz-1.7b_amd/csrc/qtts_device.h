@@ -59,6 +59,7 @@ struct Q4Tiled {
     int32_t tile_bytes;
     int32_t npad;          // G * 32
     int32_t interleave;    // 1: two fused weights alternate by group (a0 b0 a1 b1 ...)
+    int32_t bshift;        // split-f16 matrix path: dequantised weights scaled by 2^bshift (-1: not usable)
 };
 
 // Row-major Q4 (the reference layout) kept for embedding lookups.

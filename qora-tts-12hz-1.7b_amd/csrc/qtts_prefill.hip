@@ -107,14 +107,77 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
     scale = (const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + t * ts.R + r;
 }
 
-template <int MB, int EPI, bool NORM>
+// X3: the contraction on v_mfma_f32_16x16x32_f16 in three products per
+// pair of operands.  Each staged value v is split into hi = f16(v) and
+// lo = f16(v - hi): hi + lo carries 22 bits of v's 24, and a dequantised
+// weight (a 4-bit integer times an f16 scale, 15 significant bits) is
+// exactly hi + lo.  acc += Ahi Bhi + Ahi Blo + Alo Bhi (f32 accumulation,
+// the products exact); the dropped Alo Blo is below 2^-22 of each term.
+// Per chunk of 32 that is 3 matrix instructions of 8192 multiply-adds
+// where the f32 path issues 8 of 1024.  The staged tiles are f16 rows of
+// HLD halves (80 bytes: a lane's 16-byte read of 8 halves at 16q bytes).
+constexpr int HLD = GK + 8;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+template <int MB>
+__device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float16 *Ah, const _Float16 *Al,
+                                              const _Float16 *Bh, const _Float16 *Bl, const int (&cb)[2], int lane)
+{
+    // v_mfma_f32_16x16x32_f16: lane l holds A row l%16 and B column l%16 at
+    // k = 8(l/16)..+7; result element e is row 4(l/16) + e, column l%16
+    const int r16 = lane & 15, q = lane >> 4;
+    half8 ah[MB], al[MB], bh[2], bl[2];
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        ah[i] = *(const half8 *)&Ah[(16 * i + r16) * HLD + 8 * q];
+        al[i] = *(const half8 *)&Al[(16 * i + r16) * HLD + 8 * q];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        bh[j] = *(const half8 *)&Bh[(16 * cb[j] + r16) * HLD + 8 * q];
+        bl[j] = *(const half8 *)&Bl[(16 * cb[j] + r16) * HLD + 8 * q];
+    }
+    // the small terms first, then the leading one; each pass over all
+    // 2*MB accumulators, so consecutive instructions never share one
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
+}
+
+// hi + lo = v to 22 bits.  v is made opaque first: otherwise the compiler
+// folds a product feeding the conversion into one mixed-precision FMA
+// (v_fma_mix) for hi, rounding the exact product once, while lo is formed
+// from the f32-rounded product, and the two disagree by an f16 ulp.
+__device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo)
+{
+    asm volatile("" : "+v"(v));
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+template <int MB, int EPI, bool NORM, bool X3>
 __global__ void __launch_bounds__(256, 2)
 k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * GK / 4 + 255) / 256;   // 16-byte A slots per thread
-    __shared__ __attribute__((aligned(16))) float As[2][BM * GLD];
-    __shared__ __attribute__((aligned(16))) float Bs[2][GN * GLD];
+    constexpr int F32_BYTES = 2 * (BM + GN) * GLD * 4, X3_BYTES = 2 * 2 * (BM + GN) * HLD * 2;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
+    // f32: As[2][BM*GLD], Bs[2][GN*GLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [GN*HLD]
+    float(*As)[BM * GLD] = (float(*)[BM * GLD])lds;
+    float(*Bs)[GN * GLD] = (float(*)[GN * GLD])(lds + 2 * BM * GLD * 4);
+    const auto xa = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * (BM + GN) * HLD; };
+    const auto xb = [&](int buf, int hl) { return xa(buf, hl) + (size_t)BM * HLD; };
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     // Workgroups are dealt round-robin to the 8 XCDs: give each XCD a
     // contiguous run of tiles (row blocks fastest) so the row blocks that
@@ -159,6 +222,10 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         gt[h] = gc - gct[h] * ts.GB;
     }
 
+    // X3: the weights are staged times 2^bshift (their split's low half a
+    // normal f16) and the sums scaled back by 2^-bshift (both exact)
+    const float bscale = X3 ? __builtin_ldexpf(1.0f, w.bshift) : 1.0f;
+
     // tile position of (pt, group): one group per wave when wave_groups,
     // else groups interleaved by thread -- one formula for both
     const int tA = wave_groups ? 1 : ts.GB, tB = wave_groups ? 64 : 1;
@@ -202,15 +269,37 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
                 x.z *= h2f(f.rg[j][1] & 0xFFFFu);
                 x.w *= h2f(f.rg[j][1] >> 16);
             }
-            *(f32x4 *)&As[buf][aoff[j]] = x;
+            if constexpr (X3) {
+                // row aoff / GLD, halves 4 (slot % 8)..+3
+                const int r = aoff[j] / GLD, kk = aoff[j] - r * GLD;
+                _Float16 h0, h1, h2, h3, l0, l1, l2, l3;
+                split_f16(x.x, h0, l0);
+                split_f16(x.y, h1, l1);
+                split_f16(x.z, h2, l2);
+                split_f16(x.w, h3, l3);
+                *(half4 *)&xa(buf, 0)[r * HLD + kk] = half4{h0, h1, h2, h3};
+                *(half4 *)&xa(buf, 1)[r * HLD + kk] = half4{l0, l1, l2, l3};
+            } else {
+                *(f32x4 *)&As[buf][aoff[j]] = x;
+            }
         }
         // 8 columns 32*g + 8*qw + c, c = 0..7: byte c/2, low nibble even c
-        float *bp = &Bs[buf][(32 * gi + 8 * qw) * GLD + kr];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const float sc = h2f(f.rs[h]);
+            const float sc = X3 ? h2f(f.rs[h]) * bscale : h2f(f.rs[h]);
 #pragma unroll
-            for (int c = 0; c < 8; c++) bp[(64 * h + c) * GLD] = (float)((int)((f.rb[h] >> (4 * c)) & 15u) - 8) * sc;
+            for (int c = 0; c < 8; c++) {
+                const float v = (float)((int)((f.rb[h] >> (4 * c)) & 15u) - 8) * sc;
+                const int col = 32 * gi + 8 * qw + 64 * h + c;
+                if constexpr (X3) {
+                    _Float16 hi, lo;
+                    split_f16(v, hi, lo);
+                    xb(buf, 0)[col * HLD + kr] = hi;
+                    xb(buf, 1)[col * HLD + kr] = lo;
+                } else {
+                    Bs[buf][col * GLD + kr] = v;
+                }
+            }
         }
     };
 
@@ -224,9 +313,20 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     mfma_pipeline<Fetch>(
-        c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage,
-        [&](int buf) { mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane); });
+        c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage, [&](int buf) {
+            if constexpr (X3)
+                mfma_chunk_x3<MB>(acc, xa(buf, 0), xa(buf, 1), xb(buf, 0), xb(buf, 1), cb, lane);
+            else
+                mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane);
+        });
 
+    if constexpr (X3) {
+        const float unscale = __builtin_ldexpf(1.0f, -w.bshift);
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] *= unscale;
+    }
     // epilogue: element e of acc[i][j] is row 16i + 4q + e of the tile,
     // column 128nt + 16(cb0 + 2j) + r16
     float *Y = o.Y + (EPI == GEMM_PART ? (size_t)sl * o.slice_stride : 0);
@@ -535,14 +635,32 @@ static int part_slices(const Q4Tiled &w)
     return S;
 }
 
+// The split-f16 contraction unless QTTS_GEMM_F32=1 (f32 matrix instructions).
+static bool gemm_x3()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_GEMM_F32");
+        return !(v && *v && *v != '0');
+    }();
+    return on;
+}
+
 template <int MB, int EPI>
 static hipError_t launch_gemm_mb(const GemmA &a, const Q4Tiled &w, const GemmOut &o, int S, hipStream_t s)
 {
     const int tm = (a.M + 16 * MB - 1) / (16 * MB), tn = (w.G * 32 + GN - 1) / GN;
-    if (a.inv)
-        hipLaunchKernelGGL((k_gemm_q4<MB, EPI, true>), dim3(tm * tn * S), dim3(256), 0, s, a, w, o, tm, S);
-    else
-        hipLaunchKernelGGL((k_gemm_q4<MB, EPI, false>), dim3(tm * tn * S), dim3(256), 0, s, a, w, o, tm, S);
+    const dim3 grid(tm * tn * S);
+    if (gemm_x3() && w.bshift >= 0) {
+        if (a.inv)
+            hipLaunchKernelGGL((k_gemm_q4<MB, EPI, true, true>), grid, dim3(256), 0, s, a, w, o, tm, S);
+        else
+            hipLaunchKernelGGL((k_gemm_q4<MB, EPI, false, true>), grid, dim3(256), 0, s, a, w, o, tm, S);
+    } else {
+        if (a.inv)
+            hipLaunchKernelGGL((k_gemm_q4<MB, EPI, true, false>), grid, dim3(256), 0, s, a, w, o, tm, S);
+        else
+            hipLaunchKernelGGL((k_gemm_q4<MB, EPI, false, false>), grid, dim3(256), 0, s, a, w, o, tm, S);
+    }
     return hipGetLastError();
 }
 

@@ -207,6 +207,13 @@ static int role_cfg(const char *role, int64_t k) { return env_tile(role, default
 
 static void parallel_for(int64_t n, const std::function<void(int64_t, int64_t)> &fn);
 
+static float f16_to_f32(uint16_t h)
+{
+    _Float16 v;
+    memcpy(&v, &h, sizeof v);
+    return (float)v;
+}
+
 // interleave = true (two sources of equal width): groups alternate a0 b0 a1
 // b1 ..., so a tile of an even number of groups holds matching pairs.
 static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vector<SrcW> &srcs, int cfg,
@@ -293,6 +300,18 @@ static int build_tiled(qtts_ctx *c, std::vector<void *> &allocs, const std::vect
     d.tile_bytes = (int32_t)tile_bytes;
     d.npad = (int32_t)(G * 32);
     d.interleave = interleave ? 1 : 0;
+    // The split-f16 matrix path scales the dequantised weights by 2^bshift so
+    // that the low half of each split stays a normal f16: the largest
+    // |(nibble - 8) * scale| * 2^bshift must stay below 2^15.
+    float smax = 0.0f;
+    for (const SrcW &w : srcs)
+        for (int64_t i = 0; i < w.k * (w.n / 32); i++) smax = std::max(smax, std::fabs(f16_to_f32(w.scales[i])));
+    d.bshift = -1;
+    for (int b = 12; b >= 0; b--)
+        if (8.0f * smax * std::ldexp(1.0f, b) < 32768.0f) {
+            d.bshift = b;
+            break;
+        }
     *out = d;
     if (mem_out) *mem_out = mem;
     return QTTS_OK;
