@@ -119,6 +119,15 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
 constexpr int HLD = GK + 8;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+
+// (w & m) | o, kept opaque so the masked word is consumed as two f16 halves
+__device__ __forceinline__ uint32_t and_or_opaque(uint32_t w, uint32_t m, uint32_t o)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(m), "s"(o));   // one scalar operand (VOP3)
+    return r;
+}
 
 template <int MB>
 __device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float16 *Ah, const _Float16 *Al,
@@ -154,15 +163,37 @@ __device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float1
         for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
 }
 
-// hi + lo = v to 22 bits.  v is made opaque first: otherwise the compiler
-// folds a product feeding the conversion into one mixed-precision FMA
-// (v_fma_mix) for hi, rounding the exact product once, while lo is formed
-// from the f32-rounded product, and the two disagree by an f16 ulp.
-__device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo)
+// x * g with g the low (HI = 0) or high f16 half of a register: one
+// v_fma_mix_f32 with a -0 addend, the product rounded once to f32 as a
+// multiply rounds it (sign of a zero product kept)
+template <int HI>
+__device__ __forceinline__ float mul_f16_half(uint32_t g, float x, float nz)
 {
-    asm volatile("" : "+v"(v));
-    hi = (_Float16)v;
-    lo = (_Float16)(v - (float)hi);
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(g), "v"(x), "v"(nz));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(g), "v"(x), "v"(nz));
+    return r;
+}
+
+// hi = f16(v), lo = f16(v - hi) of two values, as packed pairs: hi by
+// v_cvt_pk_f16_f32 (RNE), lo by v_fma_mixlo/mixhi_f16 (hi * -1 + v, the
+// exact remainder rounded once to f16).  v is made opaque first: otherwise
+// the compiler folds a product feeding the conversion into one
+// mixed-precision FMA (v_fma_mix) for hi, rounding the exact product once,
+// while lo is formed from the f32-rounded product, and the two disagree by
+// an f16 ulp.
+__device__ __forceinline__ void split_f16_pair(float v0, float v1, uint32_t &hi, uint32_t &lo)
+{
+    asm volatile("" : "+v"(v0), "+v"(v1));
+    const h16x2 h = {(_Float16)v0, (_Float16)v1};
+    hi = __builtin_bit_cast(uint32_t, h);
+    uint32_t r;
+    asm("" : "=v"(r));   // both halves are written below: no initial value needed
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v0));
+    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v1));
+    lo = r;
 }
 
 template <int MB, int EPI, bool NORM, bool X3>
@@ -208,14 +239,18 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         akk[j] = 4 * (slot & 7);
         amul[j] = m < a.M ? (NORM ? a.inv[min(m, a.M - 1)] : 1.0f) : 0.0f;
     }
-    // B staging: bytes 4*qw..+4 of row kr, groups 4*nt + gi and + 2 (groups
-    // past G stage zeros)
-    const int kr = t & 31, qw = (t >> 5) & 3, gi = t >> 7;
+    // B staging: bytes 4*qw..+4 (8 columns) of the tiled rows; groups past
+    // G stage zeros.  f32: row kr of groups 4*nt + gi and + 2.  X3: rows kr
+    // and kr + 1 of group 4*nt + gi (one wave per group), so the two rows'
+    // values of a column leave as one 4-byte LDS write.
+    const int kr = X3 ? 2 * (t & 15) : (t & 31);
+    const int qw = X3 ? (t >> 4) & 3 : (t >> 5) & 3;
+    const int gi = X3 ? t >> 6 : t >> 7;
     int gt[2], gct[2];
     bool gok[2];
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-        const int g = 4 * nt + gi + 2 * h;
+        const int g = 4 * nt + gi + (X3 ? 0 : 2 * h);
         gok[h] = g < w.G;
         const int gc = min(g, w.G - 1);
         gct[h] = gc / ts.GB;
@@ -244,13 +279,14 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
                 f.rg[j][1] = gv.y;
             }
         }
-        // k = k0 + kr: slice s, row r, position pt of the tiled layout;
-        // k0 is a multiple of 32, so only P = 16 splits a chunk over rows
+        // k = k0 + kr (+ h on X3): slice s, row r, position pt of the tiled
+        // layout; k0 is a multiple of 32, so only P = 16 splits a chunk over
+        // rows
         const int s = k0 / w.KC, rr0 = k0 - s * w.KC, r0 = rr0 / P, pt0 = rr0 - r0 * P;
-        const int ptk = pt0 + kr;
-        const int r = P < 32 ? r0 + (ptk >> 4) : r0, pt = P < 32 ? (ptk & 15) : ptk;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            const int ptk = pt0 + kr + (X3 ? h : 0);
+            const int r = P < 32 ? r0 + (ptk >> 4) : r0, pt = P < 32 ? (ptk & 15) : ptk;
             const int tt = (pt >> 6) * 64 * ts.GB + (pt & 63) * tA + gt[h] * tB;
             const uint8_t *tile = w.data + (size_t)(s * w.CT + gct[h]) * w.tile_bytes;
             const uint32_t word = *(const uint32_t *)(tile + ((size_t)r * ts.T + tt) * 16 + 4 * qw);
@@ -263,41 +299,66 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 #pragma unroll
         for (int j = 0; j < NA; j++) {
             f32x4 x = f.ra[j] * amul[j];
-            if (NORM) {
-                x.x *= h2f(f.rg[j][0] & 0xFFFFu);
-                x.y *= h2f(f.rg[j][0] >> 16);
-                x.z *= h2f(f.rg[j][1] & 0xFFFFu);
-                x.w *= h2f(f.rg[j][1] >> 16);
-            }
             if constexpr (X3) {
+                if (NORM) {
+                    // (x * inv) * gamma, gamma read as f16 from its register
+                    const float nz = -0.0f;
+                    x.x = mul_f16_half<0>(f.rg[j][0], x.x, nz);
+                    x.y = mul_f16_half<1>(f.rg[j][0], x.y, nz);
+                    x.z = mul_f16_half<0>(f.rg[j][1], x.z, nz);
+                    x.w = mul_f16_half<1>(f.rg[j][1], x.w, nz);
+                }
                 // row aoff / GLD, halves 4 (slot % 8)..+3
                 const int r = aoff[j] / GLD, kk = aoff[j] - r * GLD;
-                _Float16 h0, h1, h2, h3, l0, l1, l2, l3;
-                split_f16(x.x, h0, l0);
-                split_f16(x.y, h1, l1);
-                split_f16(x.z, h2, l2);
-                split_f16(x.w, h3, l3);
-                *(half4 *)&xa(buf, 0)[r * HLD + kk] = half4{h0, h1, h2, h3};
-                *(half4 *)&xa(buf, 1)[r * HLD + kk] = half4{l0, l1, l2, l3};
+                uint32_t h01, l01, h23, l23;
+                split_f16_pair(x.x, x.y, h01, l01);
+                split_f16_pair(x.z, x.w, h23, l23);
+                *(uint2 *)&xa(buf, 0)[r * HLD + kk] = uint2{h01, h23};
+                *(uint2 *)&xa(buf, 1)[r * HLD + kk] = uint2{l01, l23};
             } else {
+                if (NORM) {
+                    x.x *= h2f(f.rg[j][0] & 0xFFFFu);
+                    x.y *= h2f(f.rg[j][0] >> 16);
+                    x.z *= h2f(f.rg[j][1] & 0xFFFFu);
+                    x.w *= h2f(f.rg[j][1] >> 16);
+                }
                 *(f32x4 *)&As[buf][aoff[j]] = x;
             }
         }
         // 8 columns 32*g + 8*qw + c, c = 0..7: byte c/2, low nibble even c
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const float sc = X3 ? h2f(f.rs[h]) * bscale : h2f(f.rs[h]);
+        if constexpr (X3) {
+            // Rows kr, kr + 1 interleaved by bytes: p01 = [r0.b0, r0.b1,
+            // r1.b0, r1.b1], p23 likewise, so (p >> 4c') & 0x000F000F
+            // holds column c's nibble of both rows.  Two values per packed
+            // f16 operation: | 0x64006400 gives 1024 + nib, adding -1032
+            // leaves nib - 8 exactly; hi = f16(n8 * s) is the f16 rounding
+            // of the exact product (4 + 11 significant bits), as
+            // f16(f32(n8) * s) is, and lo = f16(n8 * s - hi) in one fused
+            // operation is the rounding of the exact remainder, as
+            // f16(f32 product - hi) is.
+            const uint32_t p01 = __builtin_amdgcn_perm(f.rb[1], f.rb[0], 0x05040100u);
+            const uint32_t p23 = __builtin_amdgcn_perm(f.rb[1], f.rb[0], 0x07060302u);
+            // the rows' scales times 2^bshift: exact (a power-of-two multiple)
+            const h16x2 sp = {(_Float16)(h2f(f.rs[0]) * bscale), (_Float16)(h2f(f.rs[1]) * bscale)};
+            const h16x2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
 #pragma unroll
             for (int c = 0; c < 8; c++) {
-                const float v = (float)((int)((f.rb[h] >> (4 * c)) & 15u) - 8) * sc;
-                const int col = 32 * gi + 8 * qw + 64 * h + c;
-                if constexpr (X3) {
-                    _Float16 hi, lo;
-                    split_f16(v, hi, lo);
-                    xb(buf, 0)[col * HLD + kr] = hi;
-                    xb(buf, 1)[col * HLD + kr] = lo;
-                } else {
-                    Bs[buf][col * GLD + kr] = v;
+                const uint32_t pw = (c < 4 ? p01 : p23) >> (4 * (c & 3));
+                const h16x2 n8 = __builtin_bit_cast(h16x2, and_or_opaque(pw, 0x000F000Fu, 0x64006400u)) + off;
+                const h16x2 hi = n8 * sp;
+                const h16x2 lo = __builtin_elementwise_fma(n8, sp, -hi);
+                const int col = 32 * gi + 8 * qw + c;
+                *(h16x2 *)&xb(buf, 0)[col * HLD + kr] = hi;
+                *(h16x2 *)&xb(buf, 1)[col * HLD + kr] = lo;
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float sc = h2f(f.rs[h]);
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const float v = (float)((int)((f.rb[h] >> (4 * c)) & 15u) - 8) * sc;
+                    Bs[buf][(32 * gi + 8 * qw + 64 * h + c) * GLD + kr] = v;
                 }
             }
         }
