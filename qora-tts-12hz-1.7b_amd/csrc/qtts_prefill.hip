@@ -117,6 +117,10 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
 // where the f32 path issues 8 of 1024.  The staged tiles are f16 rows of
 // HLD halves (80 bytes: a lane's 16-byte read of 8 halves at 16q bytes).
 constexpr int HLD = GK + 8;
+// The B tile's 16-column blocks are BPAD halves apart beyond their rows, so
+// the four 8-column groups a wave writes at once (8 rows = 160 dwords apart
+// otherwise: the same banks two by two) start on banks 0, 32, 16, 48.
+constexpr int BPAD = 32;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
@@ -144,8 +148,8 @@ __device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float1
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        bh[j] = *(const half8 *)&Bh[(16 * cb[j] + r16) * HLD + 8 * q];
-        bl[j] = *(const half8 *)&Bl[(16 * cb[j] + r16) * HLD + 8 * q];
+        bh[j] = *(const half8 *)&Bh[(16 * cb[j] + r16) * HLD + cb[j] * BPAD + 8 * q];
+        bl[j] = *(const half8 *)&Bl[(16 * cb[j] + r16) * HLD + cb[j] * BPAD + 8 * q];
     }
     // the small terms first, then the leading one; each pass over all
     // 2*MB accumulators, so consecutive instructions never share one
@@ -202,12 +206,13 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * GK / 4 + 255) / 256;   // 16-byte A slots per thread
-    constexpr int F32_BYTES = 2 * (BM + GN) * GLD * 4, X3_BYTES = 2 * 2 * (BM + GN) * HLD * 2;
+    constexpr int XSTRIDE = BM * HLD + GN * HLD + (GN / 16) * BPAD;   // halves per (buffer, half) on X3
+    constexpr int F32_BYTES = 2 * (BM + GN) * GLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
     __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
     // f32: As[2][BM*GLD], Bs[2][GN*GLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [GN*HLD]
     float(*As)[BM * GLD] = (float(*)[BM * GLD])lds;
     float(*Bs)[GN * GLD] = (float(*)[GN * GLD])(lds + 2 * BM * GLD * 4);
-    const auto xa = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * (BM + GN) * HLD; };
+    const auto xa = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * XSTRIDE; };
     const auto xb = [&](int buf, int hl) { return xa(buf, hl) + (size_t)BM * HLD; };
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     // Workgroups are dealt round-robin to the 8 XCDs: give each XCD a
@@ -226,14 +231,17 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 
     // A staging: slot i = t + 256 j (clamped: spare threads repeat the last
     // slot) covers row i / 8, floats 4 (i % 8)..+4 of the chunk.  Rows past
-    // M load row M-1 and stage zeros.
+    // M load row M-1 and stage zeros.  On X3 the rows of each 16-row block
+    // are taken in 4 x 4 transposed order, so the 4 rows of one 32-lane
+    // half of a write are 4 apart (80 dwords: disjoint bank ranges).
     const float *arow[NA];
     int aoff[NA], akk[NA];
     float amul[NA];
 #pragma unroll
     for (int j = 0; j < NA; j++) {
         const int slot = min(t + 256 * j, BM * GK / 4 - 1);
-        const int r = slot >> 3, m = m0 + r;
+        const int rr = slot >> 3;
+        const int r = X3 ? (rr & ~15) | ((rr & 3) << 2) | ((rr >> 2) & 3) : rr, m = m0 + r;
         arow[j] = a.A + (size_t)min(m, a.M - 1) * a.lda + 4 * (slot & 7);
         aoff[j] = r * GLD + 4 * (slot & 7);
         akk[j] = 4 * (slot & 7);
@@ -348,8 +356,8 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
                 const h16x2 hi = n8 * sp;
                 const h16x2 lo = __builtin_elementwise_fma(n8, sp, -hi);
                 const int col = 32 * gi + 8 * qw + c;
-                *(h16x2 *)&xb(buf, 0)[col * HLD + kr] = hi;
-                *(h16x2 *)&xb(buf, 1)[col * HLD + kr] = lo;
+                *(h16x2 *)&xb(buf, 0)[col * HLD + (col >> 4) * BPAD + kr] = hi;
+                *(h16x2 *)&xb(buf, 1)[col * HLD + (col >> 4) * BPAD + kr] = lo;
             }
         } else {
 #pragma unroll
