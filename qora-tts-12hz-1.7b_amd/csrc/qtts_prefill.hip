@@ -636,6 +636,188 @@ k_prefill_attn(const float *q, int ldq, int M, int64_t start, KvPaged kv, int la
 // 75 / 62 / 76 / 140 us per layer (the per-page chain and the occupancy bind)
 constexpr int PREFILL_ATTN_QB = 2;
 
+// ---------------------------------------------------------------------------
+// The same causal attention on the matrix cores.  Workgroup (block of 8
+// rows, kv head h): 16 queries, query i = (row i/2, head 2h + i%2).  Wave w
+// takes positions 16w..16w+15 of every 64-position page and keeps its own
+// online softmax (max, sum, output) per query; the four waves are merged
+// once at the end, in wave order.  Per page and wave:
+//   S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = the wave's 16 K rows, B = the
+//        16 queries; lane l then holds query l%16 at positions 4(l/16)..+3,
+//   which is the B operand of
+//   O^T += V^T P^T on v_mfma_f32_16x16x16_f16 (A = V^T: dims 16t + l%16 at
+//        the same 4 positions), so the probabilities never leave the lane
+//        and the softmax statistics of a query stay in its lanes.
+// Every product is split f16 (hi*hi + hi*lo + lo*hi, f32 accumulation), as
+// in the GEMM.  Cache rows at or past the block's length may hold anything:
+// their scores are replaced by -inf and their V values by 0 (selects).  A
+// query's result depends only on its own row and position, not on the
+// block it shares, so a prompt prefilled in pieces matches one prefilled
+// whole bit for bit.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void split8(const f32x4 &a, const f32x4 &b, half8 &hi, half8 &lo)
+{
+    uint32_t h[4], l[4];
+    split_f16_pair(a.x, a.y, h[0], l[0]);
+    split_f16_pair(a.z, a.w, h[1], l[1]);
+    split_f16_pair(b.x, b.y, h[2], l[2]);
+    split_f16_pair(b.z, b.w, h[3], l[3]);
+    hi = __builtin_bit_cast(half8, uint4{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(half8, uint4{l[0], l[1], l[2], l[3]});
+}
+
+__device__ __forceinline__ void split4(float a, float b, float c, float d, half4 &hi, half4 &lo)
+{
+    uint32_t h[2], l[2];
+    split_f16_pair(a, b, h[0], l[0]);
+    split_f16_pair(c, d, h[1], l[1]);
+    hi = __builtin_bit_cast(half4, uint2{h[0], h[1]});
+    lo = __builtin_bit_cast(half4, uint2{l[0], l[1]});
+}
+
+__global__ void __launch_bounds__(256)
+k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int layer, float *out, int ldo)
+{
+    constexpr int QR = 8;
+    __shared__ float smax[4][16], ssum[4][16];
+    __shared__ __attribute__((aligned(16))) float so[4][16][HEAD_DIM + 4];
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6, r16 = lane & 15, qd = lane >> 4;
+    const int m0 = blockIdx.x * QR, h = blockIdx.y;
+    const int nq = min(QR, M - m0);
+    const int Lmax = (int)(start + m0 + nq);     // positions 0..Lmax-1 hold the block's keys
+    const int C = (Lmax + KV_PAGE - 1) / KV_PAGE;
+    const float scale = 1.0f / sqrtf(128.0f);
+    // this lane's query: row r16/2 of the block, head 2h + r16%2
+    const int qrow = r16 >> 1;
+    const int qpos = (int)start + m0 + qrow;
+
+    // Q as the B operand of S^T: dims 32c + 8qd..+7 of the lane's query
+    half8 qh[4], ql[4];
+    {
+        const bool ok = qrow < nq;
+        const float *qp = q + (size_t)(m0 + min(qrow, nq - 1)) * ldq + (2 * h + (r16 & 1)) * HEAD_DIM + 8 * qd;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            f32x4 a = ld4(qp + 32 * c), b = ld4(qp + 32 * c + 4);
+            const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
+            split8(ok ? a : z, ok ? b : z, qh[c], ql[c]);
+        }
+    }
+    // K rows p0 + r16 (dims 32c + 8qd..+7) and V rows p0 + 4qd + kk (dims
+    // 16t + r16) of page c, p0 = 64c + 16w
+    auto load_kv = [&](int c, f32x4 (&kr)[8], float (&vr)[32]) {
+        const float *Kp = kv_ptr(kv, layer, c * KV_PAGE, h, 0) + (16 * wv + r16) * HEAD_DIM + 8 * qd;
+        const float *Vp = kv_ptr(kv, layer, c * KV_PAGE, h, 1) + (16 * wv + 4 * qd) * HEAD_DIM + r16;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            kr[2 * i] = ld4(Kp + 32 * i);
+            kr[2 * i + 1] = ld4(Kp + 32 * i + 4);
+        }
+#pragma unroll
+        for (int tt = 0; tt < 8; tt++)
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) vr[tt * 4 + kk] = Vp[kk * HEAD_DIM + 16 * tt];
+    };
+    float mrun = -INFINITY, lrun = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int tt = 0; tt < 8; tt++) o[tt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 kn[8];
+    float vn[32];
+    load_kv(0, kn, vn);
+    for (int c = 0; c < C; c++) {
+        f32x4 kr[8];
+        float vr[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) kr[i] = kn[i];
+#pragma unroll
+        for (int i = 0; i < 32; i++) vr[i] = vn[i];
+        if (c + 1 < C) load_kv(c + 1, kn, vn);
+        const int p0 = c * KV_PAGE + 16 * wv;
+        // scores S^T[position p0 + 4qd + e][query r16]
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            half8 kh, kl;
+            split8(kr[2 * i], kr[2 * i + 1], kh, kl);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[i], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[i], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[i], s, 0, 0, 0);
+        }
+        // causal mask, the wave's online softmax for query r16 (its four
+        // lanes r16 + 16j combine by lane swaps, in a fixed order)
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) sc[e] = p0 + 4 * qd + e <= qpos ? s[e] * scale : -INFINITY;
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(mrun, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : expf(mrun - mn);
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) p[e] = sc[e] == -INFINITY ? 0.0f : expf(sc[e] - mn);
+        float ps = (p[0] + p[1]) + (p[2] + p[3]);
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        lrun = lrun * alpha + ps;
+        mrun = mn;
+        half4 ph, pl;
+        split4(p[0], p[1], p[2], p[3], ph, pl);
+        // O^T[dim 16t + 4qd + e][query r16] += V^T P^T
+#pragma unroll
+        for (int tt = 0; tt < 8; tt++) {
+            float v[4];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) v[kk] = p0 + 4 * qd + kk < Lmax ? vr[tt * 4 + kk] : 0.0f;
+            half4 vh, vl;
+            split4(v[0], v[1], v[2], v[3], vh, vl);
+            f32x4 a = o[tt] * alpha;
+            a = __builtin_amdgcn_mfma_f32_16x16x16f16(vl, ph, a, 0, 0, 0);
+            a = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, pl, a, 0, 0, 0);
+            o[tt] = __builtin_amdgcn_mfma_f32_16x16x16f16(vh, ph, a, 0, 0, 0);
+        }
+    }
+    // merge the waves: weights exp(m_w - max_w m_w), in wave order
+    if (qd == 0) {
+        smax[wv][r16] = mrun;
+        ssum[wv][r16] = lrun;
+    }
+#pragma unroll
+    for (int tt = 0; tt < 8; tt++) *(f32x4 *)&so[wv][r16][16 * tt + 4 * qd] = o[tt];
+    __syncthreads();
+    const int qi = t >> 4, d0 = 8 * (t & 15), row = qi >> 1;
+    if (row < nq) {
+        const float mm = fmaxf(fmaxf(smax[0][qi], smax[1][qi]), fmaxf(smax[2][qi], smax[3][qi]));
+        float wgt[4], l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            wgt[w] = smax[w][qi] == -INFINITY ? 0.0f : expf(smax[w][qi] - mm);
+            l = fmaf(wgt[w], ssum[w][qi], l);
+        }
+        const float inv = 1.0f / l;
+        float *op = out + (size_t)(m0 + row) * ldo + (2 * h + (qi & 1)) * HEAD_DIM + d0;
+#pragma unroll
+        for (int j = 0; j < 8; j += 4) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < 4; w++) acc += wgt[w] * *(const f32x4 *)&so[w][qi][d0 + j];
+            *(f32x4 *)(op + j) = acc * inv;
+        }
+    }
+}
+
+// the matrix-core attention unless QTTS_PREFILL_ATTN_VALU=1
+static bool prefill_attn_mx()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_PREFILL_ATTN_VALU");
+        return !(v && *v && *v != '0');
+    }();
+    return on;
+}
+
 // final-normed hidden of one row (talker.rs:477-481)
 __global__ void __launch_bounds__(256)
 k_final_rms(const float *x, const uint16_t *gamma, int H, float *out)
@@ -845,8 +1027,12 @@ hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M
         hipLaunchKernelGGL(k_prefill_qkv_post, dim3(M, 8), dim3(256), 0, s, pw.part, S, (size_t)M * ld, ld, M, start,
                            L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, m.kv, l, pw.q, A);
         PCHK(hipGetLastError());
-        hipLaunchKernelGGL(k_prefill_attn<PREFILL_ATTN_QB>, dim3((M + PREFILL_ATTN_QB - 1) / PREFILL_ATTN_QB, 8), dim3(256),
-                           0, s, pw.q, A, M, start, m.kv, l, pw.attn, A);
+        if (prefill_attn_mx())
+            hipLaunchKernelGGL(k_prefill_attn_mx, dim3((M + 7) / 8, 8), dim3(256), 0, s, pw.q, A, M, start, m.kv, l,
+                               pw.attn, A);
+        else
+            hipLaunchKernelGGL(k_prefill_attn<PREFILL_ATTN_QB>, dim3((M + PREFILL_ATTN_QB - 1) / PREFILL_ATTN_QB, 8),
+                               dim3(256), 0, s, pw.q, A, M, start, m.kv, l, pw.attn, A);
         PCHK(hipGetLastError());
         // o-proj, residual, post-attention norm
         PCHK(gemm_parts(GemmA{pw.attn, A, nullptr, nullptr, M}, L.o, pw, &S, &ld, s));

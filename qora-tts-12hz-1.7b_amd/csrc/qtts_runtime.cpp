@@ -2491,10 +2491,13 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         if (slot + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "no free KV slot to time attention");
         const int64_t pos = std::min<int64_t>(c->h_st->position, m.rope_rows - 1);
         *bytes = (double)(slot + 1) * 8 * HEAD_DIM * 4 * 2 + 16.0 * HEAD_DIM * 4 * 3;
+        // pages per work item: the step's choice, or QTTS_ATTN_PAGES (1, 2)
+        const char *pe = getenv("QTTS_ATTN_PAGES");
+        const int pg = (pe && (atoi(pe) == 1 || atoi(pe) == 2)) ? atoi(pe) : attn_pages(slot);
         return time_launches(c, iters,
                              [&](int i) {
-                                 return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->st_api,
-                                                            attn_pages(slot), c->stream);
+                                 return enqueue_attn_timing(m, c->ws, i % m.n_layers, slot, pos, c->st_api, pg,
+                                                            c->stream);
                              },
                              avg_us);
     }
