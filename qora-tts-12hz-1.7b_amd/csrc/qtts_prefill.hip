@@ -5,18 +5,20 @@
 //   k_row_inv            1/rms of every residual row         gemv.rs:445-454
 //   k_gemm_q4 (store)    [M x 2048] x [2048 x 4096] q|k|v    talker.rs:392-400
 //   k_prefill_qkv_post   QK-norm, RoPE, K/V append           talker.rs:402-425
-//   k_prefill_attn       causal attention over the cache     talker.rs:427-458
+//   k_prefill_attn_mx    causal attention over the cache     talker.rs:427-458
 //   k_gemm_q4 (add)      x += attn x o_proj                  talker.rs:460-461
 //   k_row_inv            post-attention norm
 //   k_gemm_q4 (swiglu)   silu(gate) * up, gate|up fused      talker.rs:464-472
 //   k_gemm_q4 (add)      x += h x down_proj                  talker.rs:473-474
 // then k_final_rms on the last row (talker.rs:477-481).
 //
-// k_gemm_q4 contracts on v_mfma_f32_16x16x4_f32: f32 operands and f32
-// accumulation, the arithmetic the reference's gemm_q4 (gemv.rs:349-412)
-// does on the CPU, so results agree to f32 rounding.  The weight is read
-// from the same tiled Q4 layout the decode GEMV streams (no second copy in
-// HBM) and dequantised into LDS once per 64-row block of the prompt.
+// k_gemm_q4 contracts f32 operands with f32 accumulation, the arithmetic
+// the reference's gemm_q4 (gemv.rs:349-412) does on the CPU: by default on
+// the f16 matrix cores with every operand split into f16 hi + lo (three
+// products, f32-accurate; see X3 below), or on v_mfma_f32_16x16x4_f32
+// (QTTS_GEMM_F32=1).  The weight is read from the same tiled Q4 layout the
+// decode GEMV streams (no second copy in HBM) and dequantised into LDS once
+// per row tile of the prompt.
 
 #include "qtts_device.h"
 #include "qtts_kernels.h"
