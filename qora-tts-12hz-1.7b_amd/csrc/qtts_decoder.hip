@@ -120,14 +120,22 @@ struct GemmGeo {
     float *part;
 };
 
-template <int MB, int EPI, bool TM>
+// X3: the split-f16 contraction (qtts_mfma.h): weights and gathered inputs
+// staged as f16 hi + lo, three f16 matrix products per pair, f32
+// accumulation; otherwise v_mfma_f32_16x16x4_f32 on f32 operands.
+template <int MB, int EPI, bool TM, bool X3>
 __global__ void __launch_bounds__(256, 2)
 k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo g)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * CGK / 4 + 255) / 256;
-    __shared__ __attribute__((aligned(16))) float As[2][BM * CLD];
-    __shared__ __attribute__((aligned(16))) float Bs[2][CGN * CLD];
+    constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * (BM + CGN) * MFMA_HLD * 2;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
+    // f32: As[2][BM*CLD], Bs[2][CGN*CLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [CGN*HLD]
+    float(*As)[BM * CLD] = (float(*)[BM * CLD])lds;
+    float(*Bs)[CGN * CLD] = (float(*)[CGN * CLD])(lds + 2 * BM * CLD * 4);
+    const auto ha = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * (BM + CGN) * MFMA_HLD; };
+    const auto hb = [&](int buf, int hl) { return ha(buf, hl) + (size_t)BM * MFMA_HLD; };
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int tiles = g.tm * g.tn, tile = blockIdx.x % tiles, rest = blockIdx.x / tiles;
     const int ph = rest % g.nph, slice = rest / g.nph;
@@ -208,10 +216,30 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         }
     };
     auto stage = [&](const Fetch &f, int buf) {
+        if constexpr (X3) {
 #pragma unroll
-        for (int j = 0; j < NA; j++) *(f32x4 *)&As[buf][aoff[j]] = f.a[j];
+            for (int j = 0; j < NA; j++) {
+                const int r = aoff[j] / CLD, kk = aoff[j] - r * CLD;
+                uint32_t h01, l01, h23, l23;
+                split_f16_pair(f.a[j].x, f.a[j].y, h01, l01);
+                split_f16_pair(f.a[j].z, f.a[j].w, h23, l23);
+                *(uint2 *)&ha(buf, 0)[r * MFMA_HLD + kk] = uint2{h01, h23};
+                *(uint2 *)&ha(buf, 1)[r * MFMA_HLD + kk] = uint2{l01, l23};
+            }
 #pragma unroll
-        for (int i = 0; i < 4; i++) *(f32x4 *)&Bs[buf][bcol * CLD + 4 * (bq + 2 * i)] = f.b[i];
+            for (int i = 0; i < 4; i++) {
+                uint32_t h01, l01, h23, l23;
+                split_f16_pair(f.b[i].x, f.b[i].y, h01, l01);
+                split_f16_pair(f.b[i].z, f.b[i].w, h23, l23);
+                *(uint2 *)&hb(buf, 0)[bcol * MFMA_HLD + 4 * (bq + 2 * i)] = uint2{h01, h23};
+                *(uint2 *)&hb(buf, 1)[bcol * MFMA_HLD + 4 * (bq + 2 * i)] = uint2{l01, l23};
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NA; j++) *(f32x4 *)&As[buf][aoff[j]] = f.a[j];
+#pragma unroll
+            for (int i = 0; i < 4; i++) *(f32x4 *)&Bs[buf][bcol * CLD + 4 * (bq + 2 * i)] = f.b[i];
+        }
     };
 
     const int r16 = lane & 15, q = lane >> 4;
@@ -223,7 +251,12 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     mfma_pipeline<Fetch>(
         nch, [&](Fetch &f, int c) { fetch(f, kb + c * CGK); }, stage,
-        [&](int buf) { mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane); });
+        [&](int buf) {
+            if constexpr (X3)
+                mfma_chunk_x3<MB>(acc, ha(buf, 0), ha(buf, 1), hb(buf, 0), hb(buf, 1), cb, lane);
+            else
+                mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane);
+        });
 
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
     if (g.ks > 1) {
@@ -622,18 +655,39 @@ static int conv_mb(int M, bool tm)
     return M >= 64 ? 4 : (M >= 32 ? 2 : 1);
 }
 
+// the split-f16 contraction unless QTTS_DEC_F32=1
+static bool dec_x3()
+{
+    static const bool on = [] {
+        const char *v = getenv("QTTS_DEC_F32");
+        return !(v && *v && *v != '0');
+    }();
+    return on;
+}
+
+template <int EPI, bool TM, bool X3>
+static void conv_launch_x(int mb, dim3 grid, const float *A, int M, int Kd, const ConvIn &in, const ConvOut &o, int N,
+                          const GemmGeo &g, hipStream_t s)
+{
+    switch (mb) {
+    case 6:
+        if constexpr (TM)
+            hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g);
+        break;
+    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    }
+}
+
 template <int EPI, bool TM>
 static void conv_launch(int mb, dim3 grid, const float *A, int M, int Kd, const ConvIn &in, const ConvOut &o, int N,
                         const GemmGeo &g, hipStream_t s)
 {
-    switch (mb) {
-    case 6:
-        if constexpr (TM) hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g);
-        break;
-    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
-    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
-    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
-    }
+    if (dec_x3())
+        conv_launch_x<EPI, TM, true>(mb, grid, A, M, Kd, in, o, N, g, s);
+    else
+        conv_launch_x<EPI, TM, false>(mb, grid, A, M, Kd, in, o, N, g, s);
 }
 
 // Contraction slices: split K while the launch has fewer than 2 workgroups

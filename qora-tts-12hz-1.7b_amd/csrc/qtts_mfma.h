@@ -1,4 +1,4 @@
-// qtts_mfma.h — the f32 matrix-core main loop shared by the prefill GEMM
+// qtts_mfma.h — the matrix-core main loop shared by the prefill GEMM
 // (qtts_prefill.hip, k_gemm_q4) and the speech decoder's implicit-GEMM
 // convolutions (qtts_decoder.hip, k_conv_gemm).
 //
@@ -38,6 +38,74 @@ __device__ __forceinline__ void mfma_chunk(f32x4 (&acc)[MB][2], const float *As,
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][e], bv[j][e], acc[i][j], 0, 0, 0);
     }
+}
+
+// The split-f16 form of the contraction (f32-accurate on the f16 matrix
+// cores): each staged value v is stored as hi = f16(v) and lo = f16(v - hi)
+// in rows of MFMA_HLD halves (80 bytes: a lane's 16-byte read of 8 halves
+// at 16q bytes), and acc += Ahi Bhi + Ahi Blo + Alo Bhi on
+// v_mfma_f32_16x16x32_f16 with f32 accumulation (the dropped Alo Blo is
+// below 2^-22 of each term).
+constexpr int MFMA_HLD = MFMA_K + 8;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+
+// hi = f16(v), lo = f16(v - hi) of two values, as packed pairs: hi by
+// v_cvt_pk_f16_f32 (RNE), lo by v_fma_mixlo/mixhi_f16 (hi * -1 + v, the
+// exact remainder rounded once to f16).  v is made opaque first: otherwise
+// the compiler folds a product feeding the conversion into one
+// mixed-precision FMA (v_fma_mix) for hi, rounding the exact product once,
+// while lo is formed from the f32-rounded product, and the two disagree by
+// an f16 ulp.
+__device__ __forceinline__ void split_f16_pair(float v0, float v1, uint32_t &hi, uint32_t &lo)
+{
+    asm volatile("" : "+v"(v0), "+v"(v1));
+    const h16x2 h = {(_Float16)v0, (_Float16)v1};
+    hi = __builtin_bit_cast(uint32_t, h);
+    uint32_t r;
+    asm("" : "=v"(r));   // both halves are written below: no initial value needed
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v0));
+    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v1));
+    lo = r;
+}
+
+// acc[i][j] += the split-f16 products over one staged chunk: A rows
+// 16i..16i+15 (Ah, Al), B columns 16*cb[j]..+15 (Bh, Bl; the column block
+// cb at BP extra halves per block).  Element e of acc[i][j] is row
+// 16i + 4q + e, column 16*cb[j] + r16, as with mfma_chunk.
+template <int MB, int BP = 0>
+__device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float16 *Ah, const _Float16 *Al,
+                                              const _Float16 *Bh, const _Float16 *Bl, const int (&cb)[2], int lane)
+{
+    // v_mfma_f32_16x16x32_f16: lane l holds A row l%16 and B column l%16 at
+    // k = 8(l/16)..+7; result element e is row 4(l/16) + e, column l%16
+    const int r16 = lane & 15, q = lane >> 4;
+    half8 ah[MB], al[MB], bh[2], bl[2];
+#pragma unroll
+    for (int i = 0; i < MB; i++) {
+        ah[i] = *(const half8 *)&Ah[(16 * i + r16) * MFMA_HLD + 8 * q];
+        al[i] = *(const half8 *)&Al[(16 * i + r16) * MFMA_HLD + 8 * q];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        bh[j] = *(const half8 *)&Bh[(16 * cb[j] + r16) * MFMA_HLD + cb[j] * BP + 8 * q];
+        bl[j] = *(const half8 *)&Bl[(16 * cb[j] + r16) * MFMA_HLD + cb[j] * BP + 8 * q];
+    }
+    // the small terms first, then the leading one; each pass over all
+    // 2*MB accumulators, so consecutive instructions never share one
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
 }
 
 // The double-buffered schedule over nch >= 1 chunks.  fetch(f, c) issues

@@ -118,14 +118,11 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
 // Per chunk of 32 that is 3 matrix instructions of 8192 multiply-adds
 // where the f32 path issues 8 of 1024.  The staged tiles are f16 rows of
 // HLD halves (80 bytes: a lane's 16-byte read of 8 halves at 16q bytes).
-constexpr int HLD = GK + 8;
+constexpr int HLD = MFMA_HLD;
 // The B tile's 16-column blocks are BPAD halves apart beyond their rows, so
 // the four 8-column groups a wave writes at once (8 rows = 160 dwords apart
 // otherwise: the same banks two by two) start on banks 0, 32, 16, 48.
 constexpr int BPAD = 32;
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 
 // (w & m) | o, kept opaque so the masked word is consumed as two f16 halves
 __device__ __forceinline__ uint32_t and_or_opaque(uint32_t w, uint32_t m, uint32_t o)
@@ -133,40 +130,6 @@ __device__ __forceinline__ uint32_t and_or_opaque(uint32_t w, uint32_t m, uint32
     uint32_t r;
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(m), "s"(o));   // one scalar operand (VOP3)
     return r;
-}
-
-template <int MB>
-__device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float16 *Ah, const _Float16 *Al,
-                                              const _Float16 *Bh, const _Float16 *Bl, const int (&cb)[2], int lane)
-{
-    // v_mfma_f32_16x16x32_f16: lane l holds A row l%16 and B column l%16 at
-    // k = 8(l/16)..+7; result element e is row 4(l/16) + e, column l%16
-    const int r16 = lane & 15, q = lane >> 4;
-    half8 ah[MB], al[MB], bh[2], bl[2];
-#pragma unroll
-    for (int i = 0; i < MB; i++) {
-        ah[i] = *(const half8 *)&Ah[(16 * i + r16) * HLD + 8 * q];
-        al[i] = *(const half8 *)&Al[(16 * i + r16) * HLD + 8 * q];
-    }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        bh[j] = *(const half8 *)&Bh[(16 * cb[j] + r16) * HLD + cb[j] * BPAD + 8 * q];
-        bl[j] = *(const half8 *)&Bl[(16 * cb[j] + r16) * HLD + cb[j] * BPAD + 8 * q];
-    }
-    // the small terms first, then the leading one; each pass over all
-    // 2*MB accumulators, so consecutive instructions never share one
-#pragma unroll
-    for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < MB; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
 }
 
 // x * g with g the low (HI = 0) or high f16 half of a register: one
@@ -181,25 +144,6 @@ __device__ __forceinline__ float mul_f16_half(uint32_t g, float x, float nz)
     else
         asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(g), "v"(x), "v"(nz));
     return r;
-}
-
-// hi = f16(v), lo = f16(v - hi) of two values, as packed pairs: hi by
-// v_cvt_pk_f16_f32 (RNE), lo by v_fma_mixlo/mixhi_f16 (hi * -1 + v, the
-// exact remainder rounded once to f16).  v is made opaque first: otherwise
-// the compiler folds a product feeding the conversion into one
-// mixed-precision FMA (v_fma_mix) for hi, rounding the exact product once,
-// while lo is formed from the f32-rounded product, and the two disagree by
-// an f16 ulp.
-__device__ __forceinline__ void split_f16_pair(float v0, float v1, uint32_t &hi, uint32_t &lo)
-{
-    asm volatile("" : "+v"(v0), "+v"(v1));
-    const h16x2 h = {(_Float16)v0, (_Float16)v1};
-    hi = __builtin_bit_cast(uint32_t, h);
-    uint32_t r;
-    asm("" : "=v"(r));   // both halves are written below: no initial value needed
-    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v0));
-    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v1));
-    lo = r;
 }
 
 template <int MB, int EPI, bool NORM, bool X3>
@@ -386,7 +330,7 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     mfma_pipeline<Fetch>(
         c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage, [&](int buf) {
             if constexpr (X3)
-                mfma_chunk_x3<MB>(acc, xa(buf, 0), xa(buf, 1), xb(buf, 0), xb(buf, 1), cb, lane);
+                mfma_chunk_x3<MB, BPAD>(acc, xa(buf, 0), xa(buf, 1), xb(buf, 0), xb(buf, 1), cb, lane);
             else
                 mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane);
         });
