@@ -122,19 +122,26 @@ struct GemmGeo {
 
 // X3: the split-f16 contraction (qtts_mfma.h): weights and gathered inputs
 // staged as f16 hi + lo, three f16 matrix products per pair, f32
-// accumulation; otherwise v_mfma_f32_16x16x4_f32 on f32 operands.
+// accumulation; otherwise v_mfma_f32_16x16x4_f32 on f32 operands.  On X3
+// a B lane stages 16 consecutive k of its column (quads 4bq..4bq+3, two
+// 16-byte writes per half: 16 columns 20 dwords apart cover the 64 banks
+// once), and the A rows of each 16-row block are staged in 4 x 4
+// transposed order (the 4 rows of a half-wave write 80 dwords apart,
+// disjoint bank ranges).
+
 template <int MB, int EPI, bool TM, bool X3>
 __global__ void __launch_bounds__(256, 2)
 k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo g)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * CGK / 4 + 255) / 256;
-    constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * (BM + CGN) * MFMA_HLD * 2;
+    constexpr int XSTRIDE = (BM + CGN) * MFMA_HLD;   // halves per (buffer, half) on X3
+    constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
     __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
     // f32: As[2][BM*CLD], Bs[2][CGN*CLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [CGN*HLD]
     float(*As)[BM * CLD] = (float(*)[BM * CLD])lds;
     float(*Bs)[CGN * CLD] = (float(*)[CGN * CLD])(lds + 2 * BM * CLD * 4);
-    const auto ha = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * (BM + CGN) * MFMA_HLD; };
+    const auto ha = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * XSTRIDE; };
     const auto hb = [&](int buf, int hl) { return ha(buf, hl) + (size_t)BM * MFMA_HLD; };
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
     const int tiles = g.tm * g.tn, tile = blockIdx.x % tiles, rest = blockIdx.x / tiles;
@@ -154,13 +161,14 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
 #pragma unroll
     for (int j = 0; j < NA; j++) {
         const int slot = min(t + 256 * j, BM * CGK / 4 - 1);
-        const int r = slot >> 3, m = m0 + r;
+        const int rr = slot >> 3;
+        const int r = X3 ? (rr & ~15) | ((rr & 3) << 2) | ((rr >> 2) & 3) : rr, m = m0 + r;
         aok[j] = m < M;
         arow[j] = A + (size_t)min(m, M - 1) * Kd;
         aoff[j] = r * CLD + 4 * (slot & 7);
         akk[j] = 4 * (slot & 7);
     }
-    // B: column n0 + (t & 127); k quads kq, kq + 2, kq + 4, kq + 6 of the chunk
+    // B: column n0 + (t & 127); k quads bq, bq + 2, bq + 4, bq + 6 of the chunk (X3: 4bq..4bq+3)
     const int bcol = t & 127, bq = t >> 7;
     const int pos0 = n0 + bcol;
     const bool bcok = pos0 < N;
@@ -188,7 +196,7 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
             const float *xp = xb + min(max(p, 0), in.L_in - 1);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int ic = icb + 4 * (bq + 2 * i);
+                const int ic = icb + 4 * (X3 ? 4 * bq + i : bq + 2 * i);
                 const float *row = xp + (size_t)ic * in.ldx;
                 float v[4];
 #pragma unroll
@@ -201,7 +209,7 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int kq = bq + 2 * i;
+                const int kq = X3 ? 4 * bq + i : bq + 2 * i;
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
@@ -227,12 +235,14 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
                 *(uint2 *)&ha(buf, 1)[r * MFMA_HLD + kk] = uint2{l01, l23};
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                uint32_t h01, l01, h23, l23;
-                split_f16_pair(f.b[i].x, f.b[i].y, h01, l01);
-                split_f16_pair(f.b[i].z, f.b[i].w, h23, l23);
-                *(uint2 *)&hb(buf, 0)[bcol * MFMA_HLD + 4 * (bq + 2 * i)] = uint2{h01, h23};
-                *(uint2 *)&hb(buf, 1)[bcol * MFMA_HLD + 4 * (bq + 2 * i)] = uint2{l01, l23};
+            for (int i = 0; i < 4; i += 2) {
+                uint32_t h[4], l[4];
+                split_f16_pair(f.b[i].x, f.b[i].y, h[0], l[0]);
+                split_f16_pair(f.b[i].z, f.b[i].w, h[1], l[1]);
+                split_f16_pair(f.b[i + 1].x, f.b[i + 1].y, h[2], l[2]);
+                split_f16_pair(f.b[i + 1].z, f.b[i + 1].w, h[3], l[3]);
+                *(uint4 *)&hb(buf, 0)[bcol * MFMA_HLD + 4 * (4 * bq + i)] = uint4{h[0], h[1], h[2], h[3]};
+                *(uint4 *)&hb(buf, 1)[bcol * MFMA_HLD + 4 * (4 * bq + i)] = uint4{l[0], l[1], l[2], l[3]};
             }
         } else {
 #pragma unroll
