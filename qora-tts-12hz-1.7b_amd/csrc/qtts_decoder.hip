@@ -668,11 +668,10 @@ static int conv_mb(int M, bool tm)
 // the split-f16 contraction unless QTTS_DEC_F32=1
 static bool dec_x3()
 {
-    static const bool on = [] {
-        const char *v = getenv("QTTS_DEC_F32");
-        return !(v && *v && *v != '0');
-    }();
-    return on;
+    // read at every launch (a few hundred ns), so a caller or test can switch
+    // paths between calls
+    const char *v = getenv("QTTS_DEC_F32");
+    return !(v && *v && *v != '0');
 }
 
 template <int EPI, bool TM, bool X3>

@@ -757,11 +757,10 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
 // the matrix-core attention unless QTTS_PREFILL_ATTN_VALU=1
 static bool prefill_attn_mx()
 {
-    static const bool on = [] {
-        const char *v = getenv("QTTS_PREFILL_ATTN_VALU");
-        return !(v && *v && *v != '0');
-    }();
-    return on;
+    // read at every launch (a few hundred ns), so a caller or test can switch
+    // paths between calls
+    const char *v = getenv("QTTS_PREFILL_ATTN_VALU");
+    return !(v && *v && *v != '0');
 }
 
 // final-normed hidden of one row (talker.rs:477-481)
@@ -835,11 +834,10 @@ static int part_slices(const Q4Tiled &w)
 // The split-f16 contraction unless QTTS_GEMM_F32=1 (f32 matrix instructions).
 static bool gemm_x3()
 {
-    static const bool on = [] {
-        const char *v = getenv("QTTS_GEMM_F32");
-        return !(v && *v && *v != '0');
-    }();
-    return on;
+    // read at every launch (a few hundred ns), so a caller or test can switch
+    // paths between calls
+    const char *v = getenv("QTTS_GEMM_F32");
+    return !(v && *v && *v != '0');
 }
 
 template <int MB, int EPI>

@@ -61,6 +61,19 @@ def test_decode_small_vs_oracle(ctx, small, T):
     assert ok, f"T={T}: rel err {e}"
 
 
+def test_decode_f32_instructions_vs_oracle(ctx, small, monkeypatch):
+    """The f32-instruction convolutions (QTTS_DEC_F32=1) kept beside the
+    split-f16 ones: against the oracle, and against the default path."""
+    codes = codes_for(small, 40, 4050)
+    ref = O.decode_to_audio(small, codes, threads=16)
+    default = ctx.decode_to_audio(codes)
+    monkeypatch.setenv("QTTS_DEC_F32", "1")
+    got = ctx.decode_to_audio(codes)
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+    assert close(got, default)[0]
+
+
 def test_decode_small_warmup_vs_oracle(ctx, small):
     codes, warm = codes_for(small, 30, 4100), codes_for(small, 12, 4101)
     ref = O.decode_to_audio(small, codes, warmup=warm, threads=16)

@@ -151,6 +151,43 @@ def test_prefill_mfma_single_row_and_paths(loaded):
     om.kv_reset()
 
 
+@pytest.mark.parametrize("env", ["QTTS_GEMM_F32", "QTTS_PREFILL_ATTN_VALU"])
+def test_prefill_fallback_paths(loaded, env, monkeypatch):
+    """The f32-instruction GEMM (QTTS_GEMM_F32=1) and the VALU attention
+    (QTTS_PREFILL_ATTN_VALU=1) kept beside the split-f16 matrix-core kernels:
+    each against the oracle on a prefill over a cached prefix, and against
+    the default path within the same bar."""
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(2350))
+    A = rng.standard_normal((70, t.hidden)).astype(np.float32)
+    B = rng.standard_normal((90, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    om.kv_reset()
+    ref_a, ref_b = om.prefill(A, 0), om.prefill(B, 70)
+    ctx.prefill_talker_raw_from(A, 0, path="mfma")
+    default = ctx.prefill_talker_raw_from(B, 70, path="mfma")
+    ctx.kv_reset()
+    monkeypatch.setenv(env, "1")
+    ok, e = close(ctx.prefill_talker_raw_from(A, 0, path="mfma"), ref_a)
+    assert ok, f"{env}: prefix rel err {e}"
+    got = ctx.prefill_talker_raw_from(B, 70, path="mfma")
+    ok, e = close(got, ref_b)
+    assert ok, f"{env}: suffix rel err {e}"
+    assert close(got, default)[0]
+    check_kv(ctx, om, len(t.layers), 160)
+    if env == "QTTS_GEMM_F32":
+        w = synth.q4_random(rng, 2048, 4096)
+        X = rng.standard_normal((40, 2048)).astype(np.float32)
+        dw = ctx.upload(w)
+        Y = ctx.gemm(dw, X, path="mfma")
+        dw.free()
+        R = O.gemm(X, w)
+        for r in range(40):
+            assert close(Y[r], R[r])[0], f"f32 GEMM row {r}"
+    ctx.kv_reset()
+    om.kv_reset()
+
+
 def test_prefill_chunked(ctx_factory):
     """More rows than one prefill chunk (1024): the second chunk attends to
     the first through the cache."""
