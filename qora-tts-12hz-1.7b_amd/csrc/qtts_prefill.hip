@@ -119,6 +119,9 @@ __device__ __forceinline__ void tiled_word(const Q4Tiled &w, TileShape ts, int k
 // where the f32 path issues 8 of 1024.  The staged tiles are f16 rows of
 // HLD halves (80 bytes: a lane's 16-byte read of 8 halves at 16q bytes).
 constexpr int HLD = MFMA_HLD;
+// word 3 of a raw buffer descriptor on this GPU family (untyped dword
+// access, no swizzle, offsets checked against the record count in bytes)
+constexpr int BUF_RSRC_W3 = 0x00020000;
 // The B tile's 16-column blocks are BPAD halves apart beyond their rows, so
 // the four 8-column groups a wave writes at once (8 rows = 160 dwords apart
 // otherwise: the same banks two by two) start on banks 0, 32, 16, 48.
@@ -180,7 +183,9 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     // M load row M-1 and stage zeros.  On X3 the rows of each 16-row block
     // are taken in 4 x 4 transposed order, so the 4 rows of one 32-lane
     // half of a write are 4 apart (80 dwords: disjoint bank ranges).
-    const float *arow[NA];
+    // aoffg: byte offset of the slot in A, unsigned 32 bits, so each load
+    // takes the chunk's wave-uniform base in scalar registers plus this
+    uint32_t aoffg[NA];
     int aoff[NA], akk[NA];
     float amul[NA];
 #pragma unroll
@@ -188,7 +193,7 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         const int slot = min(t + 256 * j, BM * GK / 4 - 1);
         const int rr = slot >> 3;
         const int r = X3 ? (rr & ~15) | ((rr & 3) << 2) | ((rr >> 2) & 3) : rr, m = m0 + r;
-        arow[j] = a.A + (size_t)min(m, a.M - 1) * a.lda + 4 * (slot & 7);
+        aoffg[j] = (uint32_t)(min(m, a.M - 1) * a.lda + 4 * (slot & 7)) * 4u;
         aoff[j] = r * GLD + 4 * (slot & 7);
         akk[j] = 4 * (slot & 7);
         amul[j] = m < a.M ? (NORM ? a.inv[min(m, a.M - 1)] : 1.0f) : 0.0f;
@@ -199,7 +204,9 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     // values of a column leave as one 4-byte LDS write.
     const int kr = X3 ? 2 * (t & 15) : (t & 31);
     const int qw = X3 ? (t >> 4) & 3 : (t >> 5) & 3;
-    const int gi = X3 ? t >> 6 : t >> 7;
+    // gi is the same across a wave: read it as a scalar, so the tile
+    // addresses below come from the scalar unit
+    const int gi = __builtin_amdgcn_readfirstlane(X3 ? t >> 6 : t >> 7);
     int gt[2], gct[2];
     bool gok[2];
 #pragma unroll
@@ -218,6 +225,25 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     // tile position of (pt, group): one group per wave when wave_groups,
     // else groups interleaved by thread -- one formula for both
     const int tA = wave_groups ? 1 : ts.GB, tB = wave_groups ? 64 : 1;
+    // With P >= 32 (every tile but 8 groups x 128 threads) a chunk's 32 rows
+    // lie in one tile row r0 and one 64-position block (pt0 is a multiple of
+    // 32), so tt = ttu(k0) + (kr [+ h]) * tA + gt * tB: a wave-uniform part
+    // per chunk and this constant thread part.
+    uint32_t thr_w[2], thr_s[2];   // byte offsets of the word and the scale from the chunk's base
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const uint32_t tt = (uint32_t)((kr + (X3 ? h : 0)) * tA + gt[h] * tB);
+        thr_w[h] = tt * 16u + 4u * (uint32_t)qw;
+        thr_s[h] = tt * (uint32_t)ts.R * 2u;
+    }
+    // A and the tiled weight are read through buffer descriptors: the
+    // chunk's wave-uniform offset goes in a scalar register (soffset), the
+    // thread's byte offset is a constant vector register, so a chunk's loads
+    // need no per-chunk vector address arithmetic
+    const __amdgpu_buffer_rsrc_t rsA =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.A, (short)0, (int)((size_t)a.M * a.lda * 4), BUF_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t rsW =
+        __builtin_amdgcn_make_buffer_rsrc((void *)w.data, (short)0, (int)((size_t)w.S * w.CT * w.tile_bytes), BUF_RSRC_W3);
     struct Fetch {
         f32x4 ra[NA];
         uint32_t rg[NA][2];
@@ -226,7 +252,7 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     auto fetch = [&](Fetch &f, int k0) {
 #pragma unroll
         for (int j = 0; j < NA; j++) {
-            f.ra[j] = ld4(arow[j] + k0);
+            f.ra[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsA, aoffg[j], k0 * 4, 0));
             if (NORM) {
                 const uint2 gv = *(const uint2 *)(a.gamma + k0 + akk[j]);
                 f.rg[j][0] = gv.x;
@@ -239,12 +265,21 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         const int s = k0 / w.KC, rr0 = k0 - s * w.KC, r0 = rr0 / P, pt0 = rr0 - r0 * P;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int ptk = pt0 + kr + (X3 ? h : 0);
-            const int r = P < 32 ? r0 + (ptk >> 4) : r0, pt = P < 32 ? (ptk & 15) : ptk;
-            const int tt = (pt >> 6) * 64 * ts.GB + (pt & 63) * tA + gt[h] * tB;
-            const uint8_t *tile = w.data + (size_t)(s * w.CT + gct[h]) * w.tile_bytes;
-            const uint32_t word = *(const uint32_t *)(tile + ((size_t)r * ts.T + tt) * 16 + 4 * qw);
-            const uint16_t sc = *((const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + tt * ts.R + r);
+            uint32_t word;
+            uint16_t sc;
+            if (P >= 32) {
+                const int ttu = (pt0 >> 6) * 64 * ts.GB + (pt0 & 63) * tA;
+                const int tb = (s * w.CT + gct[h]) * w.tile_bytes;
+                word = __builtin_amdgcn_raw_buffer_load_b32(rsW, thr_w[h], tb + (r0 * ts.T + ttu) * 16, 0);
+                sc = __builtin_amdgcn_raw_buffer_load_b16(rsW, thr_s[h], tb + ts.R * ts.T * 16 + (ttu * ts.R + r0) * 2, 0);
+            } else {
+                const uint8_t *tile = w.data + (size_t)(s * w.CT + gct[h]) * w.tile_bytes;
+                const int ptk = pt0 + kr + (X3 ? h : 0);
+                const int r = r0 + (ptk >> 4), pt = ptk & 15;
+                const int tt = (pt >> 6) * 64 * ts.GB + (pt & 63) * tA + gt[h] * tB;
+                word = *(const uint32_t *)(tile + ((size_t)r * ts.T + tt) * 16 + 4 * qw);
+                sc = *((const uint16_t *)(tile + (size_t)ts.R * ts.T * 16) + tt * ts.R + r);
+            }
             f.rb[h] = gok[h] ? word : 0x88888888u;
             f.rs[h] = gok[h] ? (uint32_t)sc : 0u;
         }
