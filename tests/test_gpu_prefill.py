@@ -151,6 +151,34 @@ def test_prefill_mfma_single_row_and_paths(loaded):
     om.kv_reset()
 
 
+def test_prefill_pieces_bit_identical_across_groups(loaded):
+    """Each row's attention walks its pages, and each wave its fixed position
+    quarter of a page, in the same order whatever rows share the launch: a
+    500-row prompt prefilled whole and as 300 + 200 rows (and as 37 + 463)
+    gives the same last hidden and the same cache, bit for bit, and matches
+    the oracle."""
+    ctx, om, t, p = loaded
+    rng = np.random.Generator(np.random.PCG64(2360))
+    X = rng.standard_normal((500, t.hidden)).astype(np.float32)
+    ctx.kv_reset()
+    whole = ctx.prefill_talker_raw_from(X, 0, path="mfma")
+    kv_whole = [ctx.kv_gather(l) for l in range(len(t.layers))]
+    om.kv_reset()
+    ok, e = close(whole, om.prefill(X, 0))
+    assert ok, f"rel err {e}"
+    om.kv_reset()
+    for cut in (300, 37):
+        ctx.kv_reset()
+        ctx.prefill_talker_raw_from(X[:cut], 0, path="mfma")
+        h = ctx.prefill_talker_raw_from(X[cut:], cut, path="mfma")
+        assert np.array_equal(h.view(np.uint32), whole.view(np.uint32)), f"cut {cut}: hidden differs"
+        for l in range(len(t.layers)):
+            k, v = ctx.kv_gather(l)
+            assert np.array_equal(k.view(np.uint32), kv_whole[l][0].view(np.uint32)), f"cut {cut} layer {l} K"
+            assert np.array_equal(v.view(np.uint32), kv_whole[l][1].view(np.uint32)), f"cut {cut} layer {l} V"
+    ctx.kv_reset()
+
+
 @pytest.mark.parametrize("env", ["QTTS_GEMM_F32", "QTTS_PREFILL_ATTN_VALU"])
 def test_prefill_fallback_paths(loaded, env, monkeypatch):
     """The f32-instruction GEMM (QTTS_GEMM_F32=1) and the VALU attention
