@@ -1148,19 +1148,26 @@ __device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, cons
             // the lost interleaving costs more than the earlier start.
             if constexpr (R >= 4) __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (!WAVE_GROUPS) {
 #pragma unroll
-        for (int b = 0; b < NB; b++) {
-            const float off = -8.0f * asum[b];
+            for (int b = 0; b < NB; b++) {
+                const float off = -8.0f * asum[b];
 #pragma unroll
-            for (int j = 0; j < 32; j++) acc[b][j] += off;
+                for (int j = 0; j < 32; j++) acc[b][j] += off;
+            }
         }
 
         if constexpr (WAVE_GROUPS) {
+            // the whole wave holds one group: its -8 * sum(a) offset is added
+            // once to each column sum, not to every lane's 32 partials
+            float off[NB];
+#pragma unroll
+            for (int b = 0; b < NB; b++) off[b] = -8.0f * wave_sum_dpp(asum[b]);
             wave_rs32<NB>(acc, lane);
             if (lane < 32) {
                 const int col = wave_rs_col(lane);
 #pragma unroll
-                for (int b = 0; b < NB; b++) red[(wv * NB + b) * 32 + col] = acc[b][0];
+                for (int b = 0; b < NB; b++) red[(wv * NB + b) * 32 + col] = acc[b][0] + off[b];
             }
             __syncthreads();
             // column sums straight from the per-wave partials, waves in fixed order
