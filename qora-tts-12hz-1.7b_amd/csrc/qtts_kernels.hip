@@ -331,6 +331,21 @@ struct ProResidRms {
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
+        norm_rows<T, KC>(f, k0, [&](int b, int u, int r, float v) { xs[b * KC + r] = v; });
+    }
+    // With one group per tile (P == T, ph == t) the rows thread t normalises
+    // for the LDS tile, k0 + t + u * T, are exactly its own GEMV rows: they go
+    // straight into its registers, without the LDS tile and its barrier.
+    static constexpr bool kOwnRows = true;
+    template <int T, int KC, int R>
+    __device__ void load_own(const Fetch<T, KC> &f, float (&xv)[R][NB], int k0) const
+    {
+        static_assert(Fetch<T, KC>::UG == R, "one gamma per own row");
+        norm_rows<T, KC>(f, k0, [&](int b, int u, int r, float v) { xv[u][b] = v; });
+    }
+    template <int T, int KC, class Put>
+    __device__ void norm_rows(const Fetch<T, KC> &f, int k0, const Put &put) const
+    {
         constexpr int NW = T / 64;
         __shared__ float wss[NB][NW];
         constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
@@ -379,7 +394,7 @@ struct ProResidRms {
 #pragma unroll
             for (int u = 0; u < UG; u++) {
                 const int r = t + u * T;
-                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * h2f(f.g[u]) : 0.0f;
+                if (r < KC) put(b, u, r, (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * h2f(f.g[u]) : 0.0f);
             }
         }
     }
@@ -999,6 +1014,13 @@ __device__ __forceinline__ void rs_steps(float (&v)[NB][32], int lane, int &base
     }
 }
 
+// A prologue that can leave each thread's own rows in its registers when
+// the tile has one group (P == T) declares `kOwnRows` and load_own.
+template <class P, class = void>
+struct OwnRows { static constexpr bool v = false; };
+template <class P>
+struct OwnRows<P, std::void_t<decltype(P::kOwnRows)>> { static constexpr bool v = P::kOwnRows; };
+
 // One tile of the GEMV on workgroup `item` (one workgroup per tile): the
 // body of k_gemv, and of the fused launches that host GEMV tiles beside
 // other work.  MIX picks the inner loop: v_fma_mix_f32 on f16-subnormal
@@ -1057,8 +1079,14 @@ __device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, cons
         for (int r = 0; r < R; r++)
             q[r] = __builtin_nontemporal_load((const u32x4 *)(tile + ((size_t)r * T + t) * 16));
 
-        pro.template load<T, KC>(pf, xs, s * KC, c);
-        __syncthreads();
+        constexpr bool OWN = OwnRows<Pro>::v && GB == 1 && WAVE_GROUPS;   // ph == t, P == T
+        float xv[R][NB];
+        if constexpr (OWN) {
+            pro.template load_own<T, KC, R>(pf, xv, s * KC);
+        } else {
+            pro.template load<T, KC>(pf, xs, s * KC, c);
+            __syncthreads();
+        }
 
         float acc[NB][32];
         float asum[NB];
@@ -1069,11 +1097,12 @@ __device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, cons
             for (int j = 0; j < 32; j++) acc[b][j] = 0.0f;
         }
         // the inputs of every row read from LDS before the first row waits
-        float xv[R][NB];
+        if constexpr (!OWN) {
 #pragma unroll
-        for (int r = 0; r < R; r++)
+            for (int r = 0; r < R; r++)
 #pragma unroll
-            for (int b = 0; b < NB; b++) xv[r][b] = xs[b * KC + r * P + ph];
+                for (int b = 0; b < NB; b++) xv[r][b] = xs[b * KC + r * P + ph];
+        }
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const uint32_t sw = sc[r >> 1];
