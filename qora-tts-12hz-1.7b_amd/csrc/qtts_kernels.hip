@@ -2120,15 +2120,30 @@ k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, DevState *st, const float *
         }
     }
     if (j >= H) return;
-    const float sem = q4_row_value(tcodec, st->used[0], j);
-    float sum = 0.0f;
-    for (int g = 0; g < n_groups; g++) {
-        Q4Rows e = cpemb;
-        e.packed += (size_t)g * e.rows * e.G * 16;
-        e.scales += (size_t)g * e.rows * e.G;
-        const uint32_t code = (cand_last && g == n_groups - 1) ? last : st->used[g + 1];
-        sum += q4_row_value(e, code, j);
+    // n_groups is 1..15 (checked at upload).  Every code and row value is
+    // loaded first (group indices clamped, so each load is unconditional),
+    // then summed in group order.
+    constexpr int MAXG = 15;
+    uint32_t code[MAXG];
+#pragma unroll
+    for (int g = 0; g < MAXG; g++) {
+        const int gg = min(g, n_groups - 1);
+        code[g] = (cand_last && gg == n_groups - 1) ? last : st->used[gg + 1];
     }
+    const float sem = q4_row_value(tcodec, st->used[0], j);
+    float val[MAXG];
+#pragma unroll
+    for (int g = 0; g < MAXG; g++) {
+        const int gg = min(g, n_groups - 1);
+        Q4Rows e = cpemb;
+        e.packed += (size_t)gg * e.rows * e.G * 16;
+        e.scales += (size_t)gg * e.rows * e.G;
+        val[g] = q4_row_value(e, code[g], j);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < MAXG; g++)
+        if (g < n_groups) sum += val[g];
     float v = sem + sum;
     const int f = st->frame_idx;
     const float *tr = (f < st->n_text) ? text + (size_t)f * H : pad;
