@@ -673,7 +673,7 @@ static void layer_prefill(const layer_dims *d, const qtts_layer_host *lw,
 {
     const int64_t H = d->hidden, qd = d->n_heads * d->hd, kd = d->n_kv * d->hd;
     const int64_t I = d->inter;
-    float *xn = (float *)malloc((size_t)seq * H * sizeof(float));
+    float *xn = (float *)calloc((size_t)seq * H, sizeof(float));
     float *q = (float *)malloc((size_t)seq * qd * sizeof(float));
     float *k = (float *)malloc((size_t)seq * kd * sizeof(float));
     float *v = (float *)malloc((size_t)seq * kd * sizeof(float));
