@@ -220,6 +220,20 @@ struct ProAttnCombine {
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
+        merge<T, KC>(f, k0, [&](int e, int i, float v) { xs[i] = v; });
+    }
+    // Thread t merges rows k0 + t + e * T, which on a one-group tile are its
+    // own GEMV rows: they go straight into its registers (no LDS, no barrier).
+    static constexpr bool kOwnRows = true;
+    template <int T, int KC, int R>
+    __device__ void load_own(const Fetch<T, KC> &f, float (&xv)[R][1], int k0) const
+    {
+        static_assert(KC / T == R, "one group per tile");
+        merge<T, KC>(f, k0, [&](int e, int i, float v) { xv[e][0] = v; });
+    }
+    template <int T, int KC, class Put>
+    __device__ void merge(const Fetch<T, KC> &f, int k0, const Put &put) const
+    {
         const int lane = threadIdx.x & 63;
         const int C = (f.L + KV_PAGE * PG - 1) / (KV_PAGE * PG);
         const bool v0 = lane < C, v1 = lane + 64 < C;
@@ -250,7 +264,7 @@ struct ProAttnCombine {
                     o = c < C ? fmaf(lane_value(wb, c & 63), av[j], o) : o;
                 }
             }
-            xs[i] = row < 16 * HEAD_DIM ? o / Ls : 0.0f;
+            put(e, i, row < 16 * HEAD_DIM ? o / Ls : 0.0f);
         }
     }
     __device__ void finish(int s, int c, int nct) const
