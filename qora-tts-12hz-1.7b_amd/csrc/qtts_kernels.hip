@@ -315,15 +315,30 @@ struct ProResidRms {
         f32x4 base[NB][U];
         f32x4 part[NB][RES_MAX_S][U];
         f32x4 bias[U];
-        uint32_t g[UG];
+        uint32_t g[4 * UG];   // UG for the LDS tile; a thread's own R rows (R = GB * UG, GB <= 4)
     };
     template <int T, int KC>
     __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
     {
-        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
-        const int k4 = k >> 2, t = threadIdx.x;
+        constexpr int UG = Fetch<T, KC>::UG;
 #pragma unroll
-        for (int u = 0; u < UG; u++) f.g[u] = gamma[min(k0 + t + u * T, k - 1)];
+        for (int u = 0; u < UG; u++) f.g[u] = gamma[min(k0 + (int)threadIdx.x + u * T, k - 1)];
+        fetch_rows<T, KC>(f);
+    }
+    // The gammas of the thread's own GEMV rows k0 + r * P + ph instead.
+    template <int T, int KC, int R, int P>
+    __device__ void fetch_own(Fetch<T, KC> &f, int k0, int ph) const
+    {
+        static_assert(R <= 4 * Fetch<T, KC>::UG, "own-row gammas");
+#pragma unroll
+        for (int r = 0; r < R; r++) f.g[r] = gamma[min(k0 + r * P + ph, k - 1)];
+        fetch_rows<T, KC>(f);
+    }
+    template <int T, int KC>
+    __device__ void fetch_rows(Fetch<T, KC> &f) const
+    {
+        constexpr int U = Fetch<T, KC>::U;
+        const int k4 = k >> 2, t = threadIdx.x;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
 #pragma unroll
@@ -345,24 +360,43 @@ struct ProResidRms {
     template <int T, int KC>
     __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
     {
-        norm_rows<T, KC>(f, k0, [&](int b, int u, int r, float v) { xs[b * KC + r] = v; });
+        constexpr int UG = Fetch<T, KC>::UG;
+        float iv[NB];
+        stage<T, KC>(f, iv);
+        const float *xf = xf_lds();
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int u = 0; u < UG; u++) {
+                const int r = t + u * T;
+                if (r < KC) xs[b * KC + r] = (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv[b] * h2f(f.g[u]) : 0.0f;
+            }
     }
-    // With one group per tile (P == T, ph == t) the rows thread t normalises
-    // for the LDS tile, k0 + t + u * T, are exactly its own GEMV rows: they go
-    // straight into its registers, without the LDS tile and its barrier.
-    static constexpr bool kOwnRows = true;
-    template <int T, int KC, int R>
-    __device__ void load_own(const Fetch<T, KC> &f, float (&xv)[R][NB], int k0) const
+    // Each thread normalises its own GEMV rows k0 + r * P + ph straight from
+    // the staged row into its registers: no LDS tile, no second barrier.
+    static constexpr bool kOwnRowsAny = true;
+    template <int T, int KC, int R, int P>
+    __device__ void load_own(const Fetch<T, KC> &f, float (&xv)[R][NB], int k0, int ph) const
     {
-        static_assert(Fetch<T, KC>::UG == R, "one gamma per own row");
-        norm_rows<T, KC>(f, k0, [&](int b, int u, int r, float v) { xv[u][b] = v; });
+        float iv[NB];
+        stage<T, KC>(f, iv);
+        const float *xf = xf_lds();
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const int row = k0 + r * P + ph;
+                xv[r][b] = row < k ? xf[b * KMAX + row] * iv[b] * h2f(f.g[r]) : 0.0f;
+            }
     }
-    template <int T, int KC, class Put>
-    __device__ void norm_rows(const Fetch<T, KC> &f, int k0, const Put &put) const
+    // The residual row(s) summed and staged in LDS, and 1 / rms of each.
+    template <int T, int KC>
+    __device__ void stage(const Fetch<T, KC> &f, float (&ivs)[NB]) const
     {
         constexpr int NW = T / 64;
         __shared__ float wss[NB][NW];
-        constexpr int U = Fetch<T, KC>::U, UG = Fetch<T, KC>::UG;
+        constexpr int U = Fetch<T, KC>::U;
         float *xf = xf_lds();
         const int k4 = k >> 2, t = threadIdx.x;
         float ssb[NB];
@@ -405,11 +439,7 @@ struct ProResidRms {
             for (int i = 0; i < NW; i++) tot += wss[b][i];
             const float iv = 1.0f / sqrtf(tot / (float)k + 1e-6f);
             if (t == 0) inv_lds()[b] = iv;
-#pragma unroll
-            for (int u = 0; u < UG; u++) {
-                const int r = t + u * T;
-                if (r < KC) put(b, u, r, (k0 + r < k) ? xf[b * KMAX + k0 + r] * iv * h2f(f.g[u]) : 0.0f);
-            }
+            ivs[b] = iv;
         }
     }
     // after the tile: slice-0 workgroups store their share of x / normed x
@@ -1035,6 +1065,14 @@ struct OwnRows { static constexpr bool v = false; };
 template <class P>
 struct OwnRows<P, std::void_t<decltype(P::kOwnRows)>> { static constexpr bool v = P::kOwnRows; };
 
+// A prologue that can leave each thread's own rows k0 + r * P + ph in its
+// registers on any tile with one group per wave declares `kOwnRowsAny` and
+// fetch_own / load_own<T, KC, R, P>.
+template <class P, class = void>
+struct OwnRowsAny { static constexpr bool v = false; };
+template <class P>
+struct OwnRowsAny<P, std::void_t<decltype(P::kOwnRowsAny)>> { static constexpr bool v = P::kOwnRowsAny; };
+
 // One tile of the GEMV on workgroup `item` (one workgroup per tile): the
 // body of k_gemv, and of the fused launches that host GEMV tiles beside
 // other work.  MIX picks the inner loop: v_fma_mix_f32 on f16-subnormal
@@ -1069,8 +1107,12 @@ __device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, cons
         const uint8_t *tile = w.data + (size_t)item * w.tile_bytes;
         // the prologue's loads first, then the weight stream: the prologue's
         // waits then leave the weights in flight
+        constexpr bool OWN_ANY = OwnRowsAny<Pro>::v && WAVE_GROUPS;
         typename Pro::template Fetch<T, KC> pf;
-        pro.template fetch<T, KC>(pf, s * KC, c);
+        if constexpr (OWN_ANY)
+            pro.template fetch_own<T, KC, R, P>(pf, s * KC, ph);
+        else
+            pro.template fetch<T, KC>(pf, s * KC, c);
         asm volatile("" ::: "memory");
         // the scales before the nibble rows: loads retire in issue order, so
         // row r's arithmetic then waits for rows 0..r only, not the whole tile
@@ -1093,9 +1135,11 @@ __device__ __forceinline__ void gemv_tile(const Q4Tiled &w, const Pro &pro, cons
         for (int r = 0; r < R; r++)
             q[r] = __builtin_nontemporal_load((const u32x4 *)(tile + ((size_t)r * T + t) * 16));
 
-        constexpr bool OWN = OwnRows<Pro>::v && GB == 1 && WAVE_GROUPS;   // ph == t, P == T
+        constexpr bool OWN = OWN_ANY || (OwnRows<Pro>::v && GB == 1 && WAVE_GROUPS);   // GB == 1: ph == t, P == T
         float xv[R][NB];
-        if constexpr (OWN) {
+        if constexpr (OWN_ANY) {
+            pro.template load_own<T, KC, R, P>(pf, xv, s * KC, ph);
+        } else if constexpr (OWN) {
             pro.template load_own<T, KC, R>(pf, xv, s * KC);
         } else {
             pro.template load<T, KC>(pf, xs, s * KC, c);
