@@ -239,7 +239,8 @@ int qtts_gemm_q4(qtts_ctx *ctx, const qtts_w *w, const float *X, int64_t rows,
  * default tile) is refused with QTTS_ERR_CAPACITY.  Only enqueues on the
  * context stream (no synchronisation; qtts_sync or the stream from
  * qtts_stream orders the results).  Calls that overlap on one GPU share
- * that array and race.  flags: QTTS_PATH_* as for qtts_gemm_q4. */
+ * that array and race.  At most 2^20 rows per call (QTTS_ERR_CAPACITY
+ * beyond).  flags: QTTS_PATH_* as for qtts_gemm_q4. */
 int qtts_gemm_q4_noalloc(qtts_ctx *ctx, const qtts_w *w, const float *X,
                          int64_t rows, float *Y, int flags);
 
@@ -538,6 +539,18 @@ int qtts_gen_frames_forced(qtts_ctx *ctx, int64_t n_frames,
  * RNG state (host copies). */
 int qtts_gen_state(qtts_ctx *ctx, float *logits, float *hidden,
                    int64_t *position, uint64_t *rng);
+
+/* Test hook, no reference counterpart (the reference has no device waits):
+ * the next call that runs fused launches (talker step or row prefill, frame
+ * batch, predictor chain, legacy predictor step) starts from the state a
+ * bounded cross-workgroup wait leaves when it runs out.  Its fused launches
+ * skip their waits (every kernel exits normally, outputs invalid) and the
+ * call returns QTTS_ERR_HIP; the one after it runs normally.  A talker step
+ * that fails so keeps its cache length and position; a frame batch has
+ * counted and cached the frames it ran, so the caller truncates the cache
+ * (qtts_kv_truncate) and begins again (qtts_gen_begin), as after a real
+ * timeout. */
+int qtts_debug_force_sync_err(qtts_ctx *ctx);
 
 /* ---- measurement ------------------------------------------------------ */
 

@@ -22,6 +22,7 @@
 #include "qtts_kernels.h"
 #include "qtts_devutil.h"
 
+#include <algorithm>
 #include <math.h>
 
 #include <type_traits>
@@ -2712,16 +2713,19 @@ hipError_t enqueue_silu(float *x, int n, hipStream_t st)
 
 // Columns c0..c1-1 of rows [rows][ld] set to zero (a fill kernel rather than
 // a memset node, so the call can sit in a captured graph).
-__global__ void k_zero_cols(float *Y, int ld, int c0, int c1)
+__global__ void k_zero_cols(float *Y, int rows, int ld, int c0, int c1)
 {
     const int j = c0 + blockIdx.x * blockDim.x + threadIdx.x;
-    if (j < c1) Y[(size_t)blockIdx.y * ld + j] = 0.0f;
+    if (j >= c1) return;
+    for (int r = blockIdx.y; r < rows; r += gridDim.y) Y[(size_t)r * ld + j] = 0.0f;
 }
 
 hipError_t enqueue_zero_cols(float *Y, int rows, int ld, int c0, int c1, hipStream_t st)
 {
     if (rows <= 0 || c1 <= c0) return hipSuccess;
-    hipLaunchKernelGGL(k_zero_cols, dim3((c1 - c0 + 255) / 256, rows), dim3(256), 0, st, Y, ld, c0, c1);
+    // rows beyond the grid's y limit are taken by a row loop
+    const int gy = std::min(rows, 65535);
+    hipLaunchKernelGGL(k_zero_cols, dim3((c1 - c0 + 255) / 256, gy), dim3(256), 0, st, Y, rows, ld, c0, c1);
     return hipGetLastError();
 }
 

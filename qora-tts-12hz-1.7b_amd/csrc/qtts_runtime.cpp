@@ -65,6 +65,7 @@ struct qtts_ctx {
 
     hipGraphExec_t frame_exec[2] = {nullptr, nullptr};   // one and two attention pages per workgroup
     bool gen_started = false;
+    bool force_sync_err = false;                     // qtts_debug_force_sync_err: armed for the next call
 
     float *scratch = nullptr;                        // this device's copy of `scratch` (qtts_gemm_q4_noalloc)
 
@@ -674,7 +675,9 @@ extern "C" int qtts_gemm_q4_noalloc(qtts_ctx *c, const qtts_w *w, const float *X
 {
     if (!c || !w || !X || !Y || rows < 0) return QTTS_ERR_INVALID;
     if (rows == 0) return QTTS_OK;
-    if (rows > (1 << 24)) return fail(c, QTTS_ERR_CAPACITY, "at most %d rows", 1 << 24);
+    // 2^20 rows keep every launch's grid within the device's limits (the
+    // matrix-core GEMM's row tiles x column tiles x 256 threads below 2^32)
+    if (rows > (1 << 20)) return fail(c, QTTS_ERR_CAPACITY, "at most %d rows", 1 << 20);
     if (!c->scratch) return fail(c, QTTS_ERR_STATE, "no scratch address for device %d", c->device);
     hipSetDevice(c->device);
     const Q4Tiled &t = w->t;
@@ -1026,9 +1029,10 @@ extern "C" int qtts_model_dims(qtts_ctx *c, int32_t *th, int32_t *tv, int32_t *t
 // talker
 // ---------------------------------------------------------------------------
 
-// A bounded cross-workgroup wait that ran out (the fused q|k|v + attention
-// launch) leaves sync_err set in the device state: reported once, then
-// cleared.
+// A bounded cross-workgroup wait that ran out (a fused launch: q|k|v +
+// attention, gate|up + down) leaves sync_err set in the device state:
+// reported once, then cleared.  The launches after it skipped their waits,
+// so the outputs of the call are invalid.
 static int check_sync(qtts_ctx *c)
 {
     int32_t e = 0;
@@ -1038,22 +1042,46 @@ static int check_sync(qtts_ctx *c)
     const int32_t z = 0;
     HIPCHK(c, hipMemcpy(&c->st_gen->sync_err, &z, sizeof z, hipMemcpyHostToDevice));
     c->h_st->sync_err = 0;
-    return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (fused q|k|v + attention launch)");
+    return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out (fused launch): outputs of this call are invalid");
+}
+
+// qtts_debug_force_sync_err armed: the state `st` of the call about to
+// launch gets the flag a wait that ran out leaves (the call's fused
+// launches then skip their waits).
+static int arm_sync_err(qtts_ctx *c, DevState *st)
+{
+    if (!c->force_sync_err) return QTTS_OK;
+    c->force_sync_err = false;
+    if (st == c->st_gen) c->h_st->sync_err = 1;
+    const int32_t one = 1;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(&st->sync_err, &one, sizeof one, hipMemcpyHostToDevice));
+    return QTTS_OK;
 }
 
 // Pages per attention work item for a talker step at cached length kv.
 static int step_pages(const qtts_ctx *c, int64_t kv) { return talker_fused_attn(c->tm) ? 2 : attn_pages(kv); }
 
-// One talker step on the input already in ws.x.
+// One talker step on the input already in ws.x.  A step whose waits ran
+// out reports QTTS_ERR_HIP and leaves the cache length and position where
+// they were (the device's counters are rolled back; the row it appended
+// lies past the length and is overwritten by the next step).
 static int talker_step_staged(qtts_ctx *c, int64_t position, float *hidden_out, float *logits_out, int flags)
 {
     c->h_st->position = position;
     HIPCHK(c, hipMemcpyAsync(&c->st_gen->position, &c->h_st->position, sizeof(int64_t), hipMemcpyHostToDevice, c->stream));
+    RCHK(arm_sync_err(c, c->st_gen));
     HIPCHK(c, enqueue_talker_step(c->tm, c->ws, c->st_gen, 0, step_pages(c, c->h_st->kv_len), c->stream));
     RCHK(stage_out(c, c->ws.hidden, c->tm.hidden, hidden_out, flags));
     RCHK(stage_out(c, c->ws.logits, c->tm.vocab, logits_out, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    RCHK(check_sync(c));
+    const int rs = check_sync(c);
+    if (rs != QTTS_OK) {
+        const std::string msg = c->err;
+        RCHK(write_state(c));
+        c->err = msg;
+        return rs;
+    }
     c->h_st->kv_len += 1;
     c->h_st->position = position + 1;
     return QTTS_OK;
@@ -1128,6 +1156,7 @@ extern "C" int qtts_talker_prefill(qtts_ctx *c, const float *X, int64_t seq, int
             HIPCHK(c, enqueue_talker_prefill(c->tm, c->pf, rows, start_pos + r0, c->ws.hid_work, c->stream));
         }
     } else {
+        RCHK(arm_sync_err(c, c->st_gen));
         for (int64_t t = 0; t < seq; t++) {
             RCHK(stage_in(c, X + t * H, H, c->ws.x, flags));
             HIPCHK(c, enqueue_talker_row(c->tm, c->ws, c->st_gen, start_pos + t, (int)(start_pos + t),
@@ -1979,6 +2008,7 @@ extern "C" int qtts_predictor_chain(qtts_ctx *c, const float *th, const float *s
     RCHK(stage_in(c, sem, H, c->d_io2, flags));
     DevState z{};
     HIPCHK(c, hipMemcpyAsync(c->st_api, &z, sizeof(DevState), hipMemcpyHostToDevice, c->stream));
+    RCHK(arm_sync_err(c, c->st_api));
     HIPCHK(c, enqueue_predictor_chain(c->pm, c->tm, c->ws, c->st_api, c->d_io, c->d_io2, nullptr, c->d_codes_api,
                                       c->stream));
     HIPCHK(c, hipMemcpyAsync(codes_out, c->d_codes_api, sizeof(uint32_t) * c->pm.n_groups, hipMemcpyDeviceToHost,
@@ -2111,6 +2141,7 @@ extern "C" int qtts_predict_codes(qtts_ctx *c, const float *talker_hidden, float
     v.rope_sin = p.rope_sin;
     v.rope_rows = p.rope_rows;
     v.kv = KvPaged{c->lkv, c->lkv_ptab, (int32_t)(c->kv_cap / KV_PAGE)};
+    RCHK(arm_sync_err(c, c->st_gen));
     HIPCHK(c, enqueue_talker_row(v, c->ws, c->st_gen, pos, (int)pos, attn_pages(pos), c->stream));
     // final norm (code_predictor.rs:202) into `side`, then every head
     float *side = c->leg_buf, *out = c->leg_buf + p.hidden;
@@ -2122,6 +2153,7 @@ extern "C" int qtts_predict_codes(qtts_ctx *c, const float *talker_hidden, float
     }
     RCHK(stage_out(c, out, (int64_t)p.n_groups * p.vocab, logits, flags));
     HIPCHK(c, hipStreamSynchronize(c->stream));
+    RCHK(check_sync(c));   // a wait that ran out: the cache keeps its length
     c->lkv_len = pos + 1;
     return QTTS_OK;
 }
@@ -2267,7 +2299,11 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
     int64_t emitted = 0;
     *eos = 0;
     while (emitted < n) {
-        const int64_t batch = std::min<int64_t>(n - emitted, RING_FRAMES);
+        // direct launches (QTTS_NO_GRAPH=1) synchronise after every frame
+        // (a profiled process once crashed on the host queueing 64 frames of
+        // direct launches, ~28k dispatches, between synchronisations; no
+        // cause was found in this code)
+        const int64_t batch = std::min<int64_t>(n - emitted, graph ? RING_FRAMES : 1);
         if (c->h_st->kv_len + batch > c->kv_cap)
             return fail(c, QTTS_ERR_CAPACITY, "talker KV cache full at %d positions", c->h_st->kv_len);
         if (c->h_st->position + batch > c->tm.rope_rows)
@@ -2282,6 +2318,7 @@ static int run_frames(qtts_ctx *c, int64_t n, uint32_t *pred_out, int64_t *done,
             RCHK(build_frame_graph(c, step_pages(c, c->h_st->kv_len)));
             RCHK(build_frame_graph(c, step_pages(c, c->h_st->kv_len + batch - 1)));
         }
+        RCHK(arm_sync_err(c, c->st_gen));
         for (int64_t f = 0; f < batch; f++) {
             const int pg = step_pages(c, c->h_st->kv_len + f);
             if (graph) {
@@ -2377,6 +2414,18 @@ extern "C" int qtts_gen_state(qtts_ctx *c, float *logits, float *hidden, int64_t
     if (hidden) HIPCHK(c, hipMemcpy(hidden, c->ws.hidden, sizeof(float) * c->tm.hidden, hipMemcpyDeviceToHost));
     if (position) *position = c->h_st->position;
     if (rng) *rng = c->h_st->rng;
+    return QTTS_OK;
+}
+
+// Test hook: the next call that runs fused launches (talker step or row
+// prefill, frame batch, predictor chain, legacy predictor step) starts from
+// the state a bounded wait leaves when it runs out, so its fused launches
+// take no wait at all (each workgroup reads the flag at its start and skips
+// its polls: every kernel exits normally) and it reports QTTS_ERR_HIP once.
+extern "C" int qtts_debug_force_sync_err(qtts_ctx *c)
+{
+    NEED_MODEL(c);
+    c->force_sync_err = true;
     return QTTS_OK;
 }
 

@@ -106,6 +106,7 @@ SIGNATURES = {
     "qtts_gen_frames": ([c_void_p, c_int64, c_void_p, POINTER(c_int64), POINTER(c_int32)], c_int),
     "qtts_gen_frames_forced": ([c_void_p, c_int64, c_void_p, c_void_p], c_int),
     "qtts_gen_state": ([c_void_p, c_void_p, c_void_p, POINTER(c_int64), POINTER(c_uint64)], c_int),
+    "qtts_debug_force_sync_err": ([c_void_p], c_int),
     "qtts_time_kernel": ([c_void_p, c_int32, c_int32, POINTER(c_double), POINTER(c_double)], c_int),
     "qtts_device_bytes": ([c_void_p, c_void_p], c_int),
     "qtts_time_graph": ([c_void_p, c_int32], c_int),
@@ -513,6 +514,11 @@ class Context:
         pos, rng = c_int64(), c_uint64()
         self._check(self.lib.qtts_gen_state(self.h, ptr(lg), ptr(hd), byref(pos), byref(rng)))
         return lg, hd, pos.value, rng.value
+
+    def debug_force_sync_err(self):
+        """Leave the state of a cross-workgroup wait that ran out: the next
+        step / frame batch / chain call returns QTTS_ERR_HIP once."""
+        self._check(self.lib.qtts_debug_force_sync_err(self.h))
 
     # ---- measurement ----------------------------------------------------------
     MEM_FIELDS = ("talker_q4", "predictor_q4", "predictor_row_tables", "predictor_qkv_tables", "embedding_rows",

@@ -131,3 +131,64 @@ def test_frame_half_timing_between_frames(ctx_factory, model):
     b, _ = c.gen_frames(4)
     assert np.array_equal(np.concatenate([a, b]), ref)
     assert c.kv_len() == 16 + 8
+
+
+def test_wait_give_up_reported_then_recovers(ctx_factory, model):
+    """The give-up path of the fused launches' bounded waits, forced from the
+    host (qtts_debug_force_sync_err: the next call starts with the flag a
+    wait sets when it runs out, so every workgroup skips its polls and each
+    kernel exits normally).  The talker step, a frame batch, the predictor
+    chain and the legacy predictor step each return QTTS_ERR_HIP, and the
+    same call repeated is correct: against the oracle, or bit-identical to
+    an undisturbed run."""
+    t, p = model
+    c = ctx_factory(256)
+    c.upload_model(t, p)
+    om = O.Model(t, p, kv_cap=256)
+    rng = np.random.Generator(np.random.PCG64(7100))
+    K = rng.standard_normal((len(t.layers), 40, 8, 128)).astype(np.float32)
+    V = rng.standard_normal((len(t.layers), 40, 8, 128)).astype(np.float32)
+    c.kv_load(K, V)
+    om.kv_load(K, V)
+    emb = rng.standard_normal(t.hidden).astype(np.float32)
+    c.debug_force_sync_err()
+    with pytest.raises(qtts.QttsError) as e:
+        c.forward_with_embedding(emb, 40)
+    assert e.value.code == qtts.ERR_HIP
+    assert c.kv_len() == 40
+    got, ref = c.forward_with_embedding(emb, 40), om.forward_with_embedding(emb, 40)
+    scale = max(np.abs(ref).max(), 1e-30)
+    assert np.abs(got.astype(np.float64) - ref).max() <= 1e-3 * scale
+    assert c.kv_len() == 41
+    om.close()
+
+    th = rng.standard_normal(t.hidden).astype(np.float32)
+    sem = c.embed_codec_token(77)
+    codes = c.generate_acoustic_codes(th, sem)
+    c.debug_force_sync_err()
+    with pytest.raises(qtts.QttsError) as e:
+        c.generate_acoustic_codes(th, sem)
+    assert e.value.code == qtts.ERR_HIP
+    assert np.array_equal(c.generate_acoustic_codes(th, sem), codes)
+
+    c.predict_codes_reset()
+    lg = c.predict_codes(th)
+    c.predict_codes_reset()
+    c.debug_force_sync_err()
+    with pytest.raises(qtts.QttsError) as e:
+        c.predict_codes(th)
+    assert e.value.code == qtts.ERR_HIP
+    assert np.array_equal(c.predict_codes(th).view(np.uint32), lg.view(np.uint32))
+
+    params = qtts.sample_params(eos_enabled=False)
+    begin(c, t, 16, params)
+    ref_frames, _ = c.gen_frames(6)
+    begin(c, t, 16, params)
+    c.debug_force_sync_err()
+    with pytest.raises(qtts.QttsError) as e:
+        c.gen_frames(6)
+    assert e.value.code == qtts.ERR_HIP
+    begin(c, t, 16, params)                        # truncate and begin again
+    assert c.kv_len() == 16
+    got, _ = c.gen_frames(6)
+    assert np.array_equal(got, ref_frames)
