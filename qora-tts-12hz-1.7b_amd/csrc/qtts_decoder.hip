@@ -118,6 +118,7 @@ __device__ __forceinline__ void epi_swiglu(const ConvOut &o, int m, size_t col, 
 struct GemmGeo {
     int tm, tn, nph, ks, cps;   // cps: 32-wide chunks per slice
     float *part;
+    int32_t *range_flag;        // X3: set when a workgroup's staged inputs leave the split's range
 };
 
 // X3: the split-f16 contraction (qtts_mfma.h): weights and gathered inputs
@@ -137,7 +138,10 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     constexpr int NA = (BM * CGK / 4 + 255) / 256;
     constexpr int XSTRIDE = (BM + CGN) * MFMA_HLD;   // halves per (buffer, half) on X3
     constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
+    constexpr int TILE_BYTES = X3 ? X3_BYTES : F32_BYTES;
+    // the staging tiles first (their bank layout assumes the block's base),
+    // then the range check's per-wave maxima
+    __shared__ __attribute__((aligned(16))) unsigned char lds[TILE_BYTES + 16];
     // f32: As[2][BM*CLD], Bs[2][CGN*CLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [CGN*HLD]
     float(*As)[BM * CLD] = (float(*)[BM * CLD])lds;
     float(*Bs)[CGN * CLD] = (float(*)[CGN * CLD])(lds + 2 * BM * CLD * 4);
@@ -223,8 +227,13 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
             }
         }
     };
+    // X3: largest |input| this thread stages (the range check below)
+    float bmax = 0.0f;
     auto stage = [&](const Fetch &f, int buf) {
         if constexpr (X3) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                bmax = fmaxf(bmax, fmaxf(fmaxf(fabsf(f.b[i].x), fabsf(f.b[i].y)), fmaxf(fabsf(f.b[i].z), fabsf(f.b[i].w))));
 #pragma unroll
             for (int j = 0; j < NA; j++) {
                 const int r = aoff[j] / CLD, kk = aoff[j] - r * CLD;
@@ -268,6 +277,18 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
                 mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane);
         });
 
+    // The split holds an input as f16 hi + lo: f32-accurate below the f16
+    // maximum and, through lo, to 2^-25 absolute.  A workgroup whose inputs
+    // reach 65504, or are all below 2^-14 but not zero, flags the decode,
+    // which the host then repeats on the f32 matrix path.
+    if constexpr (X3) {
+        float *wmx = (float *)(lds + TILE_BYTES);
+        const float m = wave_max_dpp(bmax);
+        if (lane == 0) wmx[wv] = m;
+        __syncthreads();
+        const float mx = fmaxf(fmaxf(wmx[0], wmx[1]), fmaxf(wmx[2], wmx[3]));
+        if (t == 0 && g.range_flag && (!(mx < 65504.0f) || (mx > 0.0f && mx < 0x1p-14f))) *g.range_flag = 1;
+    }
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
     if (g.ks > 1) {
         float *pp = g.part + ((size_t)slice * g.nph + ph) * M * N;
@@ -691,9 +712,9 @@ static void conv_launch_x(int mb, dim3 grid, const float *A, int M, int Kd, cons
 
 template <int EPI, bool TM>
 static void conv_launch(int mb, dim3 grid, const float *A, int M, int Kd, const ConvIn &in, const ConvOut &o, int N,
-                        const GemmGeo &g, hipStream_t s)
+                        const GemmGeo &g, bool f32, hipStream_t s)
 {
-    if (dec_x3())
+    if (!f32 && dec_x3())
         conv_launch_x<EPI, TM, true>(mb, grid, A, M, Kd, in, o, N, g, s);
     else
         conv_launch_x<EPI, TM, false>(mb, grid, A, M, Kd, in, o, N, g, s);
@@ -729,11 +750,12 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
     g.cps = (nch + g.ks - 1) / g.ks;
     g.ks = (nch + g.cps - 1) / g.cps;   // no empty slice
     g.part = ws.part;
+    g.range_flag = ws.range_flag;
     const dim3 grid(g.tm * g.tn * nph * g.ks);
     if (tm)
-        conv_launch<EPI, true>(mb, grid, A, M, Kd, in, o, N, g, s);
+        conv_launch<EPI, true>(mb, grid, A, M, Kd, in, o, N, g, ws.f32, s);
     else
-        conv_launch<EPI, false>(mb, grid, A, M, Kd, in, o, N, g, s);
+        conv_launch<EPI, false>(mb, grid, A, M, Kd, in, o, N, g, ws.f32, s);
     DCHK(hipGetLastError());
     if (g.ks > 1) {
         const int64_t n = (int64_t)nph * (EPI == CE_SWIGLU ? M / 2 : M) * N;
@@ -779,6 +801,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
                           float *audio, hipStream_t s)
 {
     if (T < 1 || T > ws.cap_frames) return hipErrorInvalidValue;
+    if (ws.range_flag) DCHK(hipMemsetAsync(ws.range_flag, 0, sizeof(int32_t), s));
     const int D = d.codebook_dim, V = d.vq_dim, H = d.hidden, A = d.n_heads * d.head_dim, I = d.inter;
     const int LAT = d.latent;
     // 1. VQ -> [V][T]

@@ -35,6 +35,13 @@ struct KvPaged {
 struct LayerDev {
     Q4Tiled qkv, o, gate_up, down;
     const uint16_t *q_norm, *k_norm, *input_norm, *post_norm;
+    // matrix-core prefill: the staging powers of two (shift = 14 -
+    // ceil(log2(bound))) of the normed rows (bound sqrt(hidden) * max|gamma|
+    // of the input / post norm) and of the attention's q and k (after
+    // QK-norm and RoPE: sqrt(128) * max|gamma|) and v (sqrt(hidden) *
+    // max|input gamma| * the largest column 2-norm of v_proj); the
+    // attention's are 0 while the bound lies in [2^-4, 2^14]
+    int in_shift, post_shift, q_shift, k_shift, v_shift;
 };
 
 struct TalkerDev {
@@ -101,6 +108,7 @@ struct PrefillWs {
     float *h;          // silu(gate)*up rows [cap_rows][inter]
     float *part;       // k-slice partial sums of a projection [cap_rows * prefill_part_floats]
     float *inv;        // per-row 1/rms [cap_rows]
+    float *rmax;       // per-row largest |x| of a GEMM input by column slots [cap_rows][prefill_rmax_slots]
     int cap_rows;
 };
 
@@ -167,13 +175,16 @@ struct DecoderDev {
     int out_k, out_dil;
     const float *rope_cos, *rope_sin;
     int64_t rope_rows;
+    bool weights_f32;                     // a weight matrix outside the split-f16 range: f32 matrix path
 };
 struct DecoderWs {
     float *a, *b, *c, *d, *e;             // each floats_per_frame * cap_frames
     float *part;                          // split-K partial sums
     size_t part_cap;                      // floats in part
     uint32_t *codes;                      // [n_rest + 1][cap_frames]
+    int32_t *range_flag;                  // set by a split-f16 convolution whose inputs left its range
     int cap_frames;
+    bool f32;                             // this decode on the f32 matrix path
 };
 
 struct SampleArgsHost {
@@ -232,11 +243,17 @@ hipError_t enqueue_pred_row_tables(const PredictorDev &p, int n_tables, float *X
 bool pred_qkv_tables_supported(const PredictorDev &p);
 hipError_t enqueue_pred_qkv_tables(const PredictorDev &p, int n_tables, float *part, float *out, hipStream_t s);
 bool gemm_supported(const Q4Tiled &w);
-hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s);
+hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, float *rmax,
+                             hipStream_t s);
 hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,
-                             int ldy, hipStream_t s);
+                             int ldy, float *rmax, hipStream_t s);
 bool prefill_supported(const TalkerDev &m);
 int64_t prefill_part_floats(const TalkerDev &m);
+int64_t prefill_rmax_slots(const TalkerDev &m);
+int norm_shift(const uint16_t *gamma_host, int n);
+int bound_shift(double bound);
+int attn_shift(double bound);
+double f16_max_abs(const uint16_t *h, int n);
 hipError_t enqueue_gather_rows(const Q4Rows &e, const uint32_t *ids, int n, float *out, int ld, hipStream_t s);
 hipError_t enqueue_codec_frame_rows(const Q4Rows &tcodec, const Q4Rows &pemb, int n_groups, const uint32_t *codes,
                                     int n_frames, float *out, int ld, hipStream_t s);

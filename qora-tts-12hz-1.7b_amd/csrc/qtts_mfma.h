@@ -58,16 +58,32 @@ typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 // mixed-precision FMA (v_fma_mix) for hi, rounding the exact product once,
 // while lo is formed from the f32-rounded product, and the two disagree by
 // an f16 ulp.
+//
+// The compiler's hazard checks do not see through inline asm: a matrix
+// instruction may read lo too soon after the asm wrote it (a VALU write read
+// as an MFMA source needs wait states on this GPU, which nothing inserts for
+// an asm write).  REG = true, for results that feed a matrix instruction
+// straight from registers, forms lo in plain code instead: v - f32(hi) is
+// exact in f32 (v and hi agree in all but their last 13 bits), so its one
+// rounding to f16 gives the bits of the fused form, and the compiler sees
+// every write.  Staged through LDS (REG = false), the LDS write and the
+// barrier lie between the asm and any matrix instruction.
+template <bool REG = false>
 __device__ __forceinline__ void split_f16_pair(float v0, float v1, uint32_t &hi, uint32_t &lo)
 {
     asm volatile("" : "+v"(v0), "+v"(v1));
     const h16x2 h = {(_Float16)v0, (_Float16)v1};
     hi = __builtin_bit_cast(uint32_t, h);
-    uint32_t r;
-    asm("" : "=v"(r));   // both halves are written below: no initial value needed
-    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v0));
-    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v1));
-    lo = r;
+    if constexpr (REG) {
+        const h16x2 l = {(_Float16)(v0 - (float)h.x), (_Float16)(v1 - (float)h.y)};
+        lo = __builtin_bit_cast(uint32_t, l);
+    } else {
+        uint32_t r;
+        asm("" : "=v"(r));   // both halves are written below: no initial value needed
+        asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v0));
+        asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(r) : "v"(hi), "v"(v1));
+        lo = r;
+    }
 }
 
 // acc[i][j] += the split-f16 products over one staged chunk: A rows
@@ -108,17 +124,35 @@ __device__ __forceinline__ void mfma_chunk_x3(f32x4 (&acc)[MB][2], const _Float1
         for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh[j], acc[i][j], 0, 0, 0);
 }
 
+// The power of two 2^s that takes a largest magnitude mx into [2^14, 2^15).
+// Staged times 2^s, no value of a row reaches the f16 maximum, values above
+// 2^-17 of mx keep 22 bits in hi + lo, and smaller ones are off by at most
+// 2^-39 of mx (lo's subnormal step).  0 for zero, inf and NaN (those
+// propagate as in f32); |s| <= 100, so 2^s and 2^-s are normal floats.
+__device__ __forceinline__ int range_shift(float mx)
+{
+    if (!(mx > 0.0f) || mx == __builtin_huge_valf()) return 0;
+    int e;
+    (void)__builtin_frexpf(mx, &e);              // mx in [2^(e-1), 2^e)
+    return max(-100, min(100, 15 - e));
+}
+
 // The double-buffered schedule over nch >= 1 chunks.  fetch(f, c) issues
 // chunk c's global loads into register set f, stage(f, buf) writes a
 // register set into LDS buffer buf, mma(buf) runs the MFMAs of buffer buf.
 // Two register sets alternate, so chunk c's loads are issued two chunks
 // before its MFMAs and one before its staging, and no wait on memory sits
 // between MFMAs; chunks alternate LDS buffers 0 and 1.
-template <class F, class FetchFn, class StageFn, class MmaFn>
-__device__ __forceinline__ void mfma_pipeline(int nch, FetchFn &&fetch, StageFn &&stage, MmaFn &&mma)
+//
+// pre() runs once after chunk 0's loads are issued and before chunk 1's:
+// per-tile set-up that waits on loads issued before the pipeline (they are
+// older than chunk 0's, so the wait leaves chunk 0 in flight).
+template <class F, class FetchFn, class StageFn, class PreFn, class MmaFn>
+__device__ __forceinline__ void mfma_pipeline(int nch, FetchFn &&fetch, StageFn &&stage, PreFn &&pre, MmaFn &&mma)
 {
     F fa, fb;
     fetch(fa, 0);
+    pre();
     if (nch > 1) fetch(fb, 1);
     stage(fa, 0);
     __syncthreads();
@@ -150,6 +184,12 @@ __device__ __forceinline__ void mfma_pipeline(int nch, FetchFn &&fetch, StageFn 
     } else {
         mma(0);
     }
+}
+
+template <class F, class FetchFn, class StageFn, class MmaFn>
+__device__ __forceinline__ void mfma_pipeline(int nch, FetchFn &&fetch, StageFn &&stage, MmaFn &&mma)
+{
+    mfma_pipeline<F>(nch, fetch, stage, [] {}, mma);
 }
 
 }  // namespace qtts

@@ -26,6 +26,7 @@
 #include "qtts_mfma.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace qtts {
 
@@ -85,6 +86,14 @@ struct GemmA {
     const float *inv;        // per-row 1/rms, or null
     const uint16_t *gamma;   // [K] f16, or null
     int M;
+    // The range of the split-f16 staging (X3).  Rows without a norm: rmax
+    // [M][rslots] holds the largest |A| of each row over slots of rw columns
+    // (slot s: k in [s rw, (s+1) rw)), or is null (rows staged as they are).
+    // Rows with a norm: nshift, a power of two that takes the bound of
+    // |x * inv * gamma| (sqrt(K) * max|gamma|) into [2^13, 2^14].
+    const float *rmax;
+    int rslots, rw;
+    int nshift;
 };
 
 struct GemmOut {
@@ -92,6 +101,8 @@ struct GemmOut {
     int ldy, ncols;
     const float *bias;       // GEMM_BIAS*: [ncols]
     size_t slice_stride;     // GEMM_PART: floats between the slices' blocks
+    float *rmax;             // GEMM_SWIGLU: largest |output| per (row, 64-column tile) [rows][rslots], or null
+    int rslots;
 };
 
 // Address of the 16-byte word and the scale of (row k, group g) in the
@@ -157,7 +168,13 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     constexpr int NA = (BM * GK / 4 + 255) / 256;   // 16-byte A slots per thread
     constexpr int XSTRIDE = BM * HLD + GN * HLD + (GN / 16) * BPAD;   // halves per (buffer, half) on X3
     constexpr int F32_BYTES = 2 * (BM + GN) * GLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[X3 ? X3_BYTES : F32_BYTES];
+    constexpr int TILE_BYTES = X3 ? X3_BYTES : F32_BYTES;
+    // one LDS block: the staging tiles first (their bank layout assumes the
+    // block's base), then the per-row factors that undo the staging scales
+    // (X3) and the SwiGLU epilogue's per-wave row maxima
+    __shared__ __attribute__((aligned(16))) unsigned char lds[TILE_BYTES + BM * 4 + 4 * BM * 4];
+    float *rsc = (float *)(lds + TILE_BYTES);
+    float(*wmx)[BM] = (float(*)[BM])(lds + TILE_BYTES + BM * 4);
     // f32: As[2][BM*GLD], Bs[2][GN*GLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [GN*HLD]
     float(*As)[BM * GLD] = (float(*)[BM * GLD])lds;
     float(*Bs)[GN * GLD] = (float(*)[GN * GLD])(lds + 2 * BM * GLD * 4);
@@ -185,9 +202,25 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
     // half of a write are 4 apart (80 dwords: disjoint bank ranges).
     // aoffg: byte offset of the slot in A, unsigned 32 bits, so each load
     // takes the chunk's wave-uniform base in scalar registers plus this
+    // X3 range: row r is staged times 2^sh(r), sh chosen so that the row's
+    // largest |value| over this slice's columns lies in [2^14, 2^15) (from
+    // rmax) or below the norm's static bound (nshift); the f16 halves then
+    // neither overflow nor go subnormal where the value is not tiny against
+    // the row.  The sums are scaled back by 2^-(sh + bshift) per row in the
+    // epilogue.  Both scalings are exact.  The loads the staging factors need
+    // (1/rms, the rows' slots) are issued here and used in `pre`, after the
+    // first chunk's loads are issued: waiting for them does not hold those
+    // back.
     uint32_t aoffg[NA];
-    int aoff[NA], akk[NA];
-    float amul[NA];
+    int aoff[NA], akk[NA], arow[NA];
+    float amul[NA], ainv[NA];
+    float arv[NA][2];               // two of the row's slots over this slice (rows without a norm, X3)
+    const int s0 = a.rmax ? (c0 * GK) / a.rw : 0, s1 = a.rmax ? (c1 * GK - 1) / a.rw : 0;
+    // A row's 8 slots of a chunk sit in 8 consecutive lanes (8 | 256, and the
+    // clamped slots fill whole groups of 8): lane e8 of the group reads the
+    // row's slots s0 + 2 e8 and s0 + 2 e8 + 1 (the launcher checks that a
+    // slice spans at most 16), and the group takes their maximum by DPP
+    const int e8 = t & 7;
 #pragma unroll
     for (int j = 0; j < NA; j++) {
         const int slot = min(t + 256 * j, BM * GK / 4 - 1);
@@ -196,8 +229,41 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         aoffg[j] = (uint32_t)(min(m, a.M - 1) * a.lda + 4 * (slot & 7)) * 4u;
         aoff[j] = r * GLD + 4 * (slot & 7);
         akk[j] = 4 * (slot & 7);
-        amul[j] = m < a.M ? (NORM ? a.inv[min(m, a.M - 1)] : 1.0f) : 0.0f;
+        arow[j] = (slot & 7) == 0 ? r : -1;      // the thread that records the row's factor
+        ainv[j] = NORM ? a.inv[min(m, a.M - 1)] : 1.0f;
+        if constexpr (X3 && !NORM) {
+            if (a.rmax) {
+                const float *rp = a.rmax + (size_t)min(m, a.M - 1) * a.rslots;
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const int sl = s0 + 2 * e8 + u;
+                    const float v = rp[min(sl, s1)];
+                    arv[j][u] = sl <= s1 ? v : 0.0f;
+                }
+            }
+        }
     }
+    auto pre = [&]() {
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            const int m = m0 + (aoff[j] / GLD);
+            int sh = 0;
+            if constexpr (X3) {
+                if (NORM) {
+                    sh = a.nshift;
+                } else if (a.rmax) {
+                    float mx = fmaxf(arv[j][0], arv[j][1]);
+                    mx = fmaxf(mx, dpp_mov<0xB1>(mx));    // lane ^ 1
+                    mx = fmaxf(mx, dpp_mov<0x4E>(mx));    // lane ^ 2
+                    mx = fmaxf(mx, dpp_mov<0x141>(mx));   // the other quad of the 8 (half-row mirror)
+                    sh = range_shift(mx);
+                }
+            }
+            const float p2 = __builtin_ldexpf(1.0f, sh);
+            amul[j] = m < a.M ? (NORM ? ainv[j] * p2 : p2) : 0.0f;
+            if (arow[j] >= 0) rsc[arow[j]] = __builtin_ldexpf(1.0f, -(sh + (X3 ? w.bshift : 0)));
+        }
+    };
     // B staging: bytes 4*qw..+4 (8 columns) of the tiled rows; groups past
     // G stage zeros.  f32: row kr of groups 4*nt + gi and + 2.  X3: rows kr
     // and kr + 1 of group 4*nt + gi (one wave per group), so the two rows'
@@ -363,7 +429,7 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
 #pragma unroll
         for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     mfma_pipeline<Fetch>(
-        c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage, [&](int buf) {
+        c1 - c0, [&](Fetch &f, int c) { fetch(f, (c0 + c) * GK); }, stage, pre, [&](int buf) {
             if constexpr (X3)
                 mfma_chunk_x3<MB, BPAD>(acc, xa(buf, 0), xa(buf, 1), xb(buf, 0), xb(buf, 1), cb, lane);
             else
@@ -371,15 +437,50 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
         });
 
     if constexpr (X3) {
-        const float unscale = __builtin_ldexpf(1.0f, -w.bshift);
+        // rsc was written before the pipeline's first barrier
 #pragma unroll
         for (int i = 0; i < MB; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[i][j] *= unscale;
+            for (int e = 0; e < 4; e++) {
+                const float u = rsc[16 * i + 4 * q + e];
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j][e] *= u;
+            }
     }
     // epilogue: element e of acc[i][j] is row 16i + 4q + e of the tile,
     // column 128nt + 16(cb0 + 2j) + r16
     float *Y = o.Y + (EPI == GEMM_PART ? (size_t)sl * o.slice_stride : 0);
+    if constexpr (EPI == GEMM_SWIGLU) {
+        // groups (4nt, 4nt+1) and (4nt+2, 4nt+3) are (gate, up) pairs
+        const int col = 32 * (2 * nt + (wv >> 1)) + 16 * (wv & 1) + r16;
+        float vmax[MB][4];
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + 16 * i + 4 * q + e;
+                const float v = silu_f(acc[i][0][e]) * acc[i][1][e];
+                if (m < a.M && col < o.ncols) Y[(size_t)m * o.ldy + col] = v;
+                vmax[i][e] = col < o.ncols ? fabsf(v) : 0.0f;
+            }
+        // largest |silu(g) u| of each row over this tile's 64 output columns
+        // (the range of the down projection's staging): over a wave's 16
+        // columns by DPP, then over the four waves through LDS
+        if (o.rmax) {
+#pragma unroll
+            for (int i = 0; i < MB; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float v = row_max16(vmax[i][e]);   // the 16 lanes r16 of this q form one DPP row
+                    if (r16 == 0) wmx[wv][16 * i + 4 * q + e] = v;
+                }
+            __syncthreads();
+            if (t < BM && m0 + t < a.M)
+                o.rmax[(size_t)(m0 + t) * o.rslots + nt] =
+                    fmaxf(fmaxf(wmx[0][t], wmx[1][t]), fmaxf(wmx[2][t], wmx[3][t]));
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MB; i++) {
 #pragma unroll
@@ -387,11 +488,7 @@ k_gemm_q4(GemmA a, Q4Tiled w, GemmOut o, int tm, int S)
             const int m = m0 + 16 * i + 4 * q + e;
             if (m >= a.M) continue;
             float *yr = Y + (size_t)m * o.ldy;
-            if (EPI == GEMM_SWIGLU) {
-                // groups (4nt, 4nt+1) and (4nt+2, 4nt+3) are (gate, up) pairs
-                const int col = 32 * (2 * nt + (wv >> 1)) + 16 * (wv & 1) + r16;
-                if (col < o.ncols) yr[col] = silu_f(acc[i][0][e]) * acc[i][1][e];
-            } else {
+            {
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int col = GN * nt + 16 * (cb0 + 2 * j) + r16;
@@ -637,13 +734,14 @@ constexpr int PREFILL_ATTN_QB = 2;
 // whole bit for bit.
 // ---------------------------------------------------------------------------
 
+// (results straight into matrix instructions: the register form of the split)
 __device__ __forceinline__ void split8(const f32x4 &a, const f32x4 &b, half8 &hi, half8 &lo)
 {
     uint32_t h[4], l[4];
-    split_f16_pair(a.x, a.y, h[0], l[0]);
-    split_f16_pair(a.z, a.w, h[1], l[1]);
-    split_f16_pair(b.x, b.y, h[2], l[2]);
-    split_f16_pair(b.z, b.w, h[3], l[3]);
+    split_f16_pair<true>(a.x, a.y, h[0], l[0]);
+    split_f16_pair<true>(a.z, a.w, h[1], l[1]);
+    split_f16_pair<true>(b.x, b.y, h[2], l[2]);
+    split_f16_pair<true>(b.z, b.w, h[3], l[3]);
     hi = __builtin_bit_cast(half8, uint4{h[0], h[1], h[2], h[3]});
     lo = __builtin_bit_cast(half8, uint4{l[0], l[1], l[2], l[3]});
 }
@@ -651,14 +749,22 @@ __device__ __forceinline__ void split8(const f32x4 &a, const f32x4 &b, half8 &hi
 __device__ __forceinline__ void split4(float a, float b, float c, float d, half4 &hi, half4 &lo)
 {
     uint32_t h[2], l[2];
-    split_f16_pair(a, b, h[0], l[0]);
-    split_f16_pair(c, d, h[1], l[1]);
+    split_f16_pair<true>(a, b, h[0], l[0]);
+    split_f16_pair<true>(c, d, h[1], l[1]);
     hi = __builtin_bit_cast(half4, uint2{h[0], h[1]});
     lo = __builtin_bit_cast(half4, uint2{l[0], l[1]});
 }
 
+// Split range: with SC, q, K and V are staged times 2^sq, 2^sk, 2^sv, static
+// powers of two from the layer's bounds (the QK-norm gammas, the input norm
+// and v_proj) for a layer whose bounds leave [2^-4, 2^14], so their f16
+// halves neither overflow nor go subnormal; the scores are scaled back by
+// 2^-(sq + sk), the output by 2^-sv (exact).  Layers within that band run
+// without the scalings (SC false).
+template <bool SC>
 __global__ void __launch_bounds__(256)
-k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int layer, float *out, int ldo)
+k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int layer, float *out, int ldo,
+                  float *rmax, int rslots, int sq, int sk, int sv)
 {
     constexpr int QR = 8;
     __shared__ float smax[4][16], ssum[4][16];
@@ -678,13 +784,20 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
     {
         const bool ok = qrow < nq;
         const float *qp = q + (size_t)(m0 + min(qrow, nq - 1)) * ldq + (2 * h + (r16 & 1)) * HEAD_DIM + 8 * qd;
+        const float pq = __builtin_ldexpf(1.0f, sq);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             f32x4 a = ld4(qp + 32 * c), b = ld4(qp + 32 * c + 4);
+            if constexpr (SC) {
+                a *= pq;
+                b *= pq;
+            }
             const f32x4 z = {0.0f, 0.0f, 0.0f, 0.0f};
             split8(ok ? a : z, ok ? b : z, qh[c], ql[c]);
         }
     }
+    const float pk = __builtin_ldexpf(1.0f, sk), pv = __builtin_ldexpf(1.0f, sv);
+    const float uqk = __builtin_ldexpf(1.0f, -(sq + sk)), uv = __builtin_ldexpf(1.0f, -sv);
     // K rows p0 + r16 (dims 32c + 8qd..+7) and V rows p0 + 4qd + kk (dims
     // 16t + r16) of page c, p0 = 64c + 16w
     auto load_kv = [&](int c, f32x4 (&kr)[8], float (&vr)[32]) {
@@ -721,7 +834,10 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             half8 kh, kl;
-            split8(kr[2 * i], kr[2 * i + 1], kh, kl);
+            if constexpr (SC)
+                split8(kr[2 * i] * pk, kr[2 * i + 1] * pk, kh, kl);
+            else
+                split8(kr[2 * i], kr[2 * i + 1], kh, kl);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[i], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[i], s, 0, 0, 0);
             s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[i], s, 0, 0, 0);
@@ -730,7 +846,7 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
         // lanes r16 + 16j combine by lane swaps, in a fixed order)
         float sc[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) sc[e] = p0 + 4 * qd + e <= qpos ? s[e] * scale : -INFINITY;
+        for (int e = 0; e < 4; e++) sc[e] = p0 + 4 * qd + e <= qpos ? (SC ? s[e] * uqk : s[e]) * scale : -INFINITY;
         float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
@@ -751,7 +867,7 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
         for (int tt = 0; tt < 8; tt++) {
             float v[4];
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++) v[kk] = p0 + 4 * qd + kk < Lmax ? vr[tt * 4 + kk] : 0.0f;
+            for (int kk = 0; kk < 4; kk++) v[kk] = p0 + 4 * qd + kk < Lmax ? (SC ? vr[tt * 4 + kk] * pv : vr[tt * 4 + kk]) : 0.0f;
             half4 vh, vl;
             split4(v[0], v[1], v[2], v[3], vh, vl);
             f32x4 a = o[tt] * alpha;
@@ -779,14 +895,53 @@ k_prefill_attn_mx(const float *q, int ldq, int M, int64_t start, KvPaged kv, int
         }
         const float inv = 1.0f / l;
         float *op = out + (size_t)(m0 + row) * ldo + (2 * h + (qi & 1)) * HEAD_DIM + d0;
+        float mx = 0.0f;
+        // (the sums of P V times 2^sv, merged, divided by l, scaled back)
 #pragma unroll
         for (int j = 0; j < 8; j += 4) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int w = 0; w < 4; w++) acc += wgt[w] * *(const f32x4 *)&so[w][qi][d0 + j];
-            *(f32x4 *)(op + j) = acc * inv;
+            acc = SC ? (acc * inv) * uv : acc * inv;
+            *(f32x4 *)(op + j) = acc;
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(acc.x), fabsf(acc.y)), fmaxf(fabsf(acc.z), fabsf(acc.w))));
         }
+        // the largest |output| of the row over its two heads (the range of
+        // the o-projection's staging): the row's 32 lanes are one half-wave
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        mx = fmaxf(mx, __shfl_xor(mx, 8));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        if (rmax && (t & 31) == 0) rmax[(size_t)(m0 + row) * rslots + h] = mx;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Largest |x| of each row over slots of rw columns: out[m][s] = max over k in
+// [s rw, min((s+1) rw, K)) of |X[m][k]|.  One wave per (row, slot).  The
+// range of the split-f16 staging for GEMM rows no kernel of the chain
+// measured on the way out.
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+k_row_absmax(const float *X, int ld, int M, int K, int rw, int rslots, float *out)
+{
+    const int lane = threadIdx.x & 63;
+    const int id = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (id >= M * rslots) return;
+    const int m = id / rslots, sl = id - m * rslots;
+    const float *x = X + (size_t)m * ld;
+    const int k1 = min((sl + 1) * rw, K);
+    float mx = 0.0f;
+    for (int k = sl * rw + lane; k < k1; k += 64) mx = fmaxf(mx, fabsf(x[k]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    mx = fmaxf(mx, __shfl_xor(mx, 4));
+    mx = fmaxf(mx, __shfl_xor(mx, 8));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (lane == 0) out[(size_t)m * rslots + sl] = mx;
 }
 
 // the matrix-core attention unless QTTS_PREFILL_ATTN_VALU=1
@@ -894,10 +1049,25 @@ static hipError_t launch_gemm_mb(const GemmA &a, const Q4Tiled &w, const GemmOut
     return hipGetLastError();
 }
 
+// The staging-range slots of every k-slice fit the GEMM's reads: at most 16
+// slots per slice (two per lane of a row's 8), all within the row.
+static bool rmax_fits(const GemmA &a, int K, int S)
+{
+    if (!a.rmax) return true;
+    if (a.rslots < 1 || a.rw < 1 || (int64_t)a.rslots * a.rw < K) return false;
+    const int nch = K / GK;
+    for (int sl = 0; sl < S; sl++) {
+        const int c0 = sl * nch / S, c1 = (sl + 1) * nch / S;
+        if ((c1 * GK - 1) / a.rw - (c0 * GK) / a.rw >= 16) return false;
+    }
+    return true;
+}
+
 template <int EPI>
 static hipError_t launch_gemm(const GemmA &a, const Q4Tiled &w, const GemmOut &o, int S, hipStream_t s)
 {
     if (!gemm_shape_ok(w, w.k) || a.M < 1 || a.lda % 4 || S < 1 || S > w.k / (2 * GK)) return hipErrorInvalidValue;
+    if (!rmax_fits(a, w.k, S) || (o.rmax && o.rslots < (w.G * 32 + GN - 1) / GN)) return hipErrorInvalidValue;
     if (EPI == GEMM_SWIGLU && (!w.interleave || w.G % 4)) return hipErrorInvalidValue;
     if ((EPI == GEMM_BIAS || EPI == GEMM_BIAS_SILU) && !o.bias) return hipErrorInvalidValue;
     if (EPI != GEMM_PART && S != 1) return hipErrorInvalidValue;
@@ -916,21 +1086,37 @@ bool gemm_supported(const Q4Tiled &w)
     return gemm_shape_ok(w, w.k);
 }
 
-hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, hipStream_t s)
+static hipError_t row_absmax(const float *X, int ld, int M, int K, int rw, int rslots, float *out, hipStream_t s)
 {
-    const GemmA a{X, w.k, nullptr, nullptr, rows};
+    const int n = M * rslots;
+    hipLaunchKernelGGL(k_row_absmax, dim3((n + 3) / 4), dim3(256), 0, s, X, ld, M, K, rw, rslots, out);
+    return hipGetLastError();
+}
+
+// Rows of any magnitude (gemm_q4 takes any finite input, gemv.rs:349-412):
+// each row's largest |x| first (rmax, rows floats), for the staging's range.
+hipError_t enqueue_gemm_rows(const Q4Tiled &w, const float *X, int rows, float *Y, int ldy, float *rmax,
+                             hipStream_t s)
+{
+    if (gemm_x3()) PCHK(row_absmax(X, w.k, rows, w.k, w.k, 1, rmax, s));
+    const GemmA a{X, w.k, nullptr, nullptr, rows, rmax, 1, w.k, 0};
     return launch_gemm<GEMM_STORE>(a, w, GemmOut{Y, ldy, std::min(ldy, w.G * 32), nullptr, 0}, 1, s);
 }
 
 // Y = X W + bias, optionally through SiLU (the text projection's fc1 / fc2,
-// talker.rs:105-116, over a batch of rows).
+// talker.rs:105-116, over a batch of rows).  rmax: rows floats, as above.
 hipError_t enqueue_gemm_bias(const Q4Tiled &w, const float *X, int rows, const float *bias, bool silu, float *Y,
-                             int ldy, hipStream_t s)
+                             int ldy, float *rmax, hipStream_t s)
 {
-    const GemmA a{X, w.k, nullptr, nullptr, rows};
+    if (gemm_x3()) PCHK(row_absmax(X, w.k, rows, w.k, w.k, 1, rmax, s));
+    const GemmA a{X, w.k, nullptr, nullptr, rows, rmax, 1, w.k, 0};
     const GemmOut o{Y, ldy, std::min(ldy, w.n), bias, 0};
     return silu ? launch_gemm<GEMM_BIAS_SILU>(a, w, o, 1, s) : launch_gemm<GEMM_BIAS>(a, w, o, 1, s);
 }
+
+// Slots of the down projection's input range: one per 64 output columns of
+// the gate|up GEMM (one column tile).
+static int down_rslots(const TalkerDev &m) { return ((m.inter + 63) / 64 + 3) & ~3; }
 
 bool prefill_supported(const TalkerDev &m)
 {
@@ -944,6 +1130,49 @@ bool prefill_supported(const TalkerDev &m)
             return false;
     }
     return true;
+}
+
+// Column slots per prompt row of the staging-range buffer (PrefillWs.rmax):
+// 8 for the o-projection's input (one per kv head), one per 64 columns for
+// the down projection's.
+int64_t prefill_rmax_slots(const TalkerDev &m) { return std::max<int64_t>(8, down_rslots(m)); }
+
+// The staging power of two of rows normed with this gamma (f16 bit
+// patterns, on the host): |x * inv * gamma| <= sqrt(n) * max|gamma|, since
+// |x_k| * inv <= sqrt(n); the shift takes that bound into [2^13, 2^14].
+// Largest finite |value| of n f16 bit patterns (inf / NaN skipped: they
+// give no finite bound and propagate as in f32).
+double f16_max_abs(const uint16_t *h, int n)
+{
+    double g = 0.0;
+    for (int k = 0; k < n; k++) {
+        const uint16_t a = h[k] & 0x7FFFu;
+        if (a >= 0x7C00u) continue;
+        const int e = a >> 10, f = a & 0x3FF;
+        g = std::max(g, e ? std::ldexp(1024.0 + f, e - 25) : std::ldexp((double)f, -24));
+    }
+    return g;
+}
+
+// The power of two that takes a bound on |values| into [2^13, 2^14].
+int bound_shift(double bound)
+{
+    if (!(bound > 0.0) || !std::isfinite(bound)) return 0;
+    return std::max(-100, std::min(100, 14 - (int)std::ceil(std::log2(bound))));
+}
+
+// The attention's staging shifts: none while the bound lies in [2^-4, 2^14]
+// (the values' f16 halves then neither overflow nor lose precision against
+// the bound), else the shift that takes it into [2^13, 2^14].
+int attn_shift(double bound)
+{
+    if (bound >= 0x1p-4 && bound <= 0x1p14) return 0;
+    return bound_shift(bound);
+}
+
+int norm_shift(const uint16_t *gamma_host, int n)
+{
+    return bound_shift(std::sqrt((double)n) * f16_max_abs(gamma_host, n));
 }
 
 // Floats per prompt row of the k-slice partials buffer.
@@ -976,8 +1205,9 @@ hipError_t enqueue_row_inv(const float *X, int ld, int M, int K, float *inv, hip
 hipError_t enqueue_gemm_gateup(const TalkerDev &m, const PrefillWs &pw, int l, int M, hipStream_t s)
 {
     const LayerDev &L = m.layers[l];
-    return launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, m.hidden, pw.inv, L.post_norm, M}, L.gate_up,
-                                    GemmOut{pw.h, m.inter, m.inter, nullptr, 0}, 1, s);
+    return launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, m.hidden, pw.inv, L.post_norm, M, nullptr, 0, 0, L.post_shift},
+                                    L.gate_up, GemmOut{pw.h, m.inter, m.inter, nullptr, 0, pw.rmax, down_rslots(m)},
+                                    1, s);
 }
 
 // A projection into k-slice partials: slice s of row m at part[s * M * ld +
@@ -1002,26 +1232,36 @@ hipError_t enqueue_talker_prefill(const TalkerDev &m, const PrefillWs &pw, int M
     for (int l = 0; l < m.n_layers; l++) {
         const LayerDev &L = m.layers[l];
         // q|k|v (input norm fused), QK-norm + RoPE + KV append, attention
-        PCHK(gemm_parts(GemmA{pw.x, H, pw.inv, L.input_norm, M}, L.qkv, pw, &S, &ld, s));
+        PCHK(gemm_parts(GemmA{pw.x, H, pw.inv, L.input_norm, M, nullptr, 0, 0, L.in_shift}, L.qkv, pw, &S, &ld, s));
         hipLaunchKernelGGL(k_prefill_qkv_post, dim3(M, 8), dim3(256), 0, s, pw.part, S, (size_t)M * ld, ld, M, start,
                            L.q_norm, L.k_norm, m.rope_cos, m.rope_sin, m.kv, l, pw.q, A);
         PCHK(hipGetLastError());
-        if (prefill_attn_mx())
-            hipLaunchKernelGGL(k_prefill_attn_mx, dim3((M + 7) / 8, 8), dim3(256), 0, s, pw.q, A, M, start, m.kv, l,
-                               pw.attn, A);
-        else
+        // attention rows, and each row's largest |value| per kv head's two
+        // q heads (the o-projection's staging range: 8 slots of 256)
+        if (prefill_attn_mx()) {
+            if (L.q_shift || L.k_shift || L.v_shift)
+                hipLaunchKernelGGL(k_prefill_attn_mx<true>, dim3((M + 7) / 8, 8), dim3(256), 0, s, pw.q, A, M, start,
+                                   m.kv, l, pw.attn, A, pw.rmax, 8, L.q_shift, L.k_shift, L.v_shift);
+            else
+                hipLaunchKernelGGL(k_prefill_attn_mx<false>, dim3((M + 7) / 8, 8), dim3(256), 0, s, pw.q, A, M, start,
+                                   m.kv, l, pw.attn, A, pw.rmax, 8, 0, 0, 0);
+        } else {
             hipLaunchKernelGGL(k_prefill_attn<PREFILL_ATTN_QB>, dim3((M + PREFILL_ATTN_QB - 1) / PREFILL_ATTN_QB, 8),
                                dim3(256), 0, s, pw.q, A, M, start, m.kv, l, pw.attn, A);
+            PCHK(hipGetLastError());
+            PCHK(row_absmax(pw.attn, A, M, A, 2 * HEAD_DIM, 8, pw.rmax, s));
+        }
         PCHK(hipGetLastError());
         // o-proj, residual, post-attention norm
-        PCHK(gemm_parts(GemmA{pw.attn, A, nullptr, nullptr, M}, L.o, pw, &S, &ld, s));
+        PCHK(gemm_parts(GemmA{pw.attn, A, nullptr, nullptr, M, pw.rmax, 8, 2 * HEAD_DIM, 0}, L.o, pw, &S, &ld, s));
         hipLaunchKernelGGL(k_resid_add_inv, dim3(M), dim3(256), 0, s, pw.x, H, pw.part, S, (size_t)M * ld, ld, H,
                            pw.inv);
         PCHK(hipGetLastError());
-        // gate|up with SwiGLU, down, residual, next layer's input norm
-        PCHK(launch_gemm<GEMM_SWIGLU>(GemmA{pw.x, H, pw.inv, L.post_norm, M}, L.gate_up,
-                                      GemmOut{pw.h, m.inter, m.inter, nullptr, 0}, 1, s));
-        PCHK(gemm_parts(GemmA{pw.h, m.inter, nullptr, nullptr, M}, L.down, pw, &S, &ld, s));
+        // gate|up with SwiGLU (and the down projection's staging range per
+        // 64 columns), down, residual, next layer's input norm
+        PCHK(enqueue_gemm_gateup(m, pw, l, M, s));
+        PCHK(gemm_parts(GemmA{pw.h, m.inter, nullptr, nullptr, M, pw.rmax, down_rslots(m), 64, 0}, L.down, pw, &S,
+                        &ld, s));
         hipLaunchKernelGGL(k_resid_add_inv, dim3(M), dim3(256), 0, s, pw.x, H, pw.part, S, (size_t)M * ld, ld, H,
                            pw.inv);
         PCHK(hipGetLastError());

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -62,6 +63,8 @@ struct qtts_ctx {
     float *d_io = nullptr;                           // API staging, 2 rows of max(hidden,vocab,4096)
     float *d_io2 = nullptr;
     int64_t io_floats = 0;
+    float *d_rmax = nullptr;                         // per-row largest |x| of a GEMM's rows (staging range)
+    int64_t rmax_rows = 0;
 
     hipGraphExec_t frame_exec[2] = {nullptr, nullptr};   // one and two attention pages per workgroup
     bool gen_started = false;
@@ -370,6 +373,26 @@ static int upload_vec(qtts_ctx *c, std::vector<void *> &allocs, const T *src, si
 
 static SrcW src_of(const qtts_q4_host &w) { return SrcW{w.packed, w.scales, w.k, w.n}; }
 
+// Largest 2-norm of a column of a Q4 weight (dequantised, in double).
+static double q4_max_col_norm(const qtts_q4_host &w)
+{
+    if (!w.packed || !w.scales || w.n < 32) return 0.0;
+    const int64_t G = w.n / 32;
+    std::vector<double> ss((size_t)G * 32, 0.0);
+    for (int64_t k = 0; k < w.k; k++)
+        for (int64_t g = 0; g < G; g++) {
+            const double sc = f16_max_abs(&w.scales[k * G + g], 1);   // |scale|: only squares are summed
+            const uint8_t *p = w.packed + (k * G + g) * 16;
+            for (int j = 0; j < 32; j++) {
+                const double v = (double)((int)((p[j >> 1] >> (4 * (j & 1))) & 15) - 8) * sc;
+                ss[(size_t)g * 32 + j] += v * v;
+            }
+        }
+    double m = 0.0;
+    for (double v : ss) m = std::max(m, v);
+    return std::sqrt(m);
+}
+
 static int upload_layer(qtts_ctx *c, const qtts_layer_host &L, int hidden, int head_dim, LayerDev *out,
                         bool predictor)
 {
@@ -390,6 +413,12 @@ static int upload_layer(qtts_ctx *c, const qtts_layer_host &L, int hidden, int h
     RCHK(upload_vec(c, A, L.k_norm, head_dim, &out->k_norm));
     RCHK(upload_vec(c, A, L.input_norm, hidden, &out->input_norm));
     RCHK(upload_vec(c, A, L.post_attn_norm, hidden, &out->post_norm));
+    out->in_shift = norm_shift(L.input_norm, hidden);
+    out->post_shift = norm_shift(L.post_attn_norm, hidden);
+    out->q_shift = attn_shift(std::sqrt((double)head_dim) * f16_max_abs(L.q_norm, head_dim));
+    out->k_shift = attn_shift(std::sqrt((double)head_dim) * f16_max_abs(L.k_norm, head_dim));
+    out->v_shift = attn_shift(std::sqrt((double)hidden) * f16_max_abs(L.input_norm, hidden) *
+                              q4_max_col_norm(L.v_proj));
     if (L.q_proj.n != 16 * HEAD_DIM || L.k_proj.n != 8 * HEAD_DIM || L.v_proj.n != 8 * HEAD_DIM)
         return fail(c, QTTS_ERR_UNSUPPORTED, "device path expects 16 q heads / 8 kv heads of 128");
     if (L.o_proj.n != hidden || L.down_proj.n != hidden || L.q_proj.k != hidden)
@@ -513,6 +542,7 @@ extern "C" void qtts_ctx_destroy(qtts_ctx *c)
     if (c->d_forced) hipFree(c->d_forced);
     if (c->d_io) hipFree(c->d_io);
     if (c->d_io2) hipFree(c->d_io2);
+    if (c->d_rmax) hipFree(c->d_rmax);
     if (c->d_copy) hipFree(c->d_copy);
     if (c->d_read) hipFree(c->d_read);
     if (c->d_sink) hipFree(c->d_sink);
@@ -553,6 +583,19 @@ static int ensure_io(qtts_ctx *c, int64_t floats)
     return QTTS_OK;
 }
 
+// One float per GEMM row for the rows' largest |x| (grown on demand).
+static int ensure_rmax(qtts_ctx *c, int64_t rows)
+{
+    if (rows <= c->rmax_rows) return QTTS_OK;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (c->d_rmax) hipFree(c->d_rmax);
+    c->d_rmax = nullptr;
+    c->rmax_rows = 0;
+    HIPCHK(c, hipMalloc(&c->d_rmax, (size_t)rows * sizeof(float)));
+    c->rmax_rows = rows;
+    return QTTS_OK;
+}
+
 // Row buffers of the batched prefill for `rows` rows (grown on demand).
 static int ensure_prefill(qtts_ctx *c, int rows)
 {
@@ -561,7 +604,8 @@ static int ensure_prefill(qtts_ctx *c, int rows)
     c->pf_mem = nullptr;
     c->pf = PrefillWs{};
     const int64_t H = c->tm.hidden, A = 16 * HEAD_DIM, I = c->tm.inter, P = prefill_part_floats(c->tm);
-    const int64_t per_row = H + A + A + I + P + 1;
+    const int64_t RS = prefill_rmax_slots(c->tm);
+    const int64_t per_row = H + A + A + I + P + 1 + RS;
     float *base = nullptr;
     HIPCHK(c, hipMalloc(&base, (size_t)rows * per_row * sizeof(float)));
     c->pf_mem = base;
@@ -570,7 +614,8 @@ static int ensure_prefill(qtts_ctx *c, int rows)
     c->pf.attn = c->pf.q + rows * A;
     c->pf.h = c->pf.attn + rows * A;
     c->pf.part = c->pf.h + rows * I;
-    c->pf.inv = c->pf.part + rows * P;
+    c->pf.rmax = c->pf.part + rows * P;   // 16-byte aligned: every width before it is a multiple of 4
+    c->pf.inv = c->pf.rmax + rows * RS;
     c->pf.cap_rows = rows;
     return QTTS_OK;
 }
@@ -655,8 +700,10 @@ extern "C" int qtts_gemm_q4(qtts_ctx *c, const qtts_w *w, const float *X, int64_
     RCHK(ensure_io(c, std::max<int64_t>(rows * w->t.k, rows * w->t.npad)));
     RCHK(stage_in(c, X, rows * w->t.k, c->d_io, flags));
     HIPCHK(c, hipMemsetAsync(c->d_io2, 0, rows * w->t.n * sizeof(float), c->stream));
-    if (use_mfma(flags, rows) && gemm_supported(w->t))
-        HIPCHK(c, enqueue_gemm_rows(w->t, c->d_io, (int)rows, c->d_io2, w->t.n, c->stream));
+    if (use_mfma(flags, rows) && gemm_supported(w->t)) {
+        RCHK(ensure_rmax(c, rows));
+        HIPCHK(c, enqueue_gemm_rows(w->t, c->d_io, (int)rows, c->d_io2, w->t.n, c->d_rmax, c->stream));
+    }
     else
         HIPCHK(c, enqueue_gemv_rows(w->t, c->d_io, (int)rows, c->d_io2, w->part, c->stream));
     RCHK(stage_out(c, c->d_io2, rows * w->t.n, Y, flags));
@@ -677,12 +724,15 @@ extern "C" int qtts_gemm_q4_noalloc(qtts_ctx *c, const qtts_w *w, const float *X
     if (rows == 0) return QTTS_OK;
     // 2^20 rows keep every launch's grid within the device's limits (the
     // matrix-core GEMM's row tiles x column tiles x 256 threads below 2^32)
+    static_assert((size_t)1 << 20 <= SCRATCH_FLOATS, "one float of scratch per row for the rows' ranges");
     if (rows > (1 << 20)) return fail(c, QTTS_ERR_CAPACITY, "at most %d rows", 1 << 20);
     if (!c->scratch) return fail(c, QTTS_ERR_STATE, "no scratch address for device %d", c->device);
     hipSetDevice(c->device);
     const Q4Tiled &t = w->t;
     if (use_mfma(flags, rows) && gemm_supported(t)) {
-        HIPCHK(c, enqueue_gemm_rows(t, X, (int)rows, Y, t.n, c->stream));
+        // the rows' largest |x| (the staging range) in the scratch array:
+        // rows <= 2^20 = its size
+        HIPCHK(c, enqueue_gemm_rows(t, X, (int)rows, Y, t.n, c->scratch, c->stream));
     } else {
         const size_t need = (size_t)t.S * 2 * t.npad;
         if (need > SCRATCH_FLOATS)
@@ -1409,9 +1459,10 @@ static int text_rows(qtts_ctx *c, const uint32_t *d_ids, int n, float *out, floa
     Q4Rows e = m.text_rows;
     e.n = m.text_hidden;
     float *raw = scratch, *h1 = scratch + (size_t)n * m.text_hidden;
+    RCHK(ensure_rmax(c, n));
     HIPCHK(c, enqueue_gather_rows(e, d_ids, n, raw, m.text_hidden, c->stream));
-    HIPCHK(c, enqueue_gemm_bias(m.text_fc1, raw, n, m.text_fc1_bias, true, h1, m.text_fc1.n, c->stream));
-    HIPCHK(c, enqueue_gemm_bias(m.text_fc2, h1, n, m.text_fc2_bias, false, out, m.hidden, c->stream));
+    HIPCHK(c, enqueue_gemm_bias(m.text_fc1, raw, n, m.text_fc1_bias, true, h1, m.text_fc1.n, c->d_rmax, c->stream));
+    HIPCHK(c, enqueue_gemm_bias(m.text_fc2, h1, n, m.text_fc2_bias, false, out, m.hidden, c->d_rmax, c->stream));
     return QTTS_OK;
 }
 
@@ -1662,10 +1713,22 @@ extern "C" int qtts_prefill_custom_voice(qtts_ctx *c, const uint32_t *text_token
 // speech decoder
 // ---------------------------------------------------------------------------
 
+// The split-f16 convolutions hold a weight as f16 hi + lo: f32-accurate for
+// every |w| below the f16 maximum, and (through lo) to 2^-25 absolute
+// below 2^-14.  A matrix outside that (any |w| >= 65504, or all of it below
+// 2^-14 but not zero) sends the whole decoder to the f32 matrix path.
+static void note_gemm_weights(qtts_ctx *c, const float *w, size_t n)
+{
+    float mx = 0.0f;
+    for (size_t i = 0; i < n; i++) mx = std::max(mx, std::fabs(w[i]));
+    if (!(mx < 65504.0f) || (mx > 0.0f && mx < 0x1p-14f)) c->dec.weights_f32 = true;
+}
+
 // Host matrix [k][n] (input-major) -> device [n][k] (the GEMM's A operand).
 static int upload_t(qtts_ctx *c, const float *src, int k, int n, const float **out)
 {
     if (!src) return fail(c, QTTS_ERR_INVALID, "null matrix in decoder descriptor");
+    note_gemm_weights(c, src, (size_t)k * n);
     std::vector<float> t((size_t)k * n);
     for (int i = 0; i < k; i++)
         for (int j = 0; j < n; j++) t[(size_t)j * k + i] = src[(size_t)i * n + j];
@@ -1683,6 +1746,7 @@ static int upload_conv(qtts_ctx *c, const qtts_conv1d_host &h, DecConv *d)
     d->oc = OC;
     d->k = K;
     d->dil = h.dilation;
+    note_gemm_weights(c, h.weight, (size_t)OC * IC * K);
     if (K > 1 && conv_tap_major(IC, K)) {   // [out][in][k] -> [out][k][in]
         std::vector<float> w((size_t)OC * IC * K);
         for (int o = 0; o < OC; o++)
@@ -1722,6 +1786,7 @@ static int upload_convt(qtts_ctx *c, const qtts_convt1d_host &h, DecConvT *d)
     d->oc = OC;
     d->stride = S;
     d->taps = taps;
+    note_gemm_weights(c, p.data(), p.size());
     RCHK(upload_vec(c, c->dec_allocs, p.data(), p.size(), &d->phases));
     return upload_vec(c, c->dec_allocs, h.bias, (size_t)OC, &d->b);
 }
@@ -1741,6 +1806,7 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
         return fail(c, QTTS_ERR_INVALID, "decoder codebooks");
     if (h->output_conv.out_channels != 1 || h->pre_conv.in_channels != V || h->pre_conv.out_channels != LAT)
         return fail(c, QTTS_ERR_INVALID, "decoder conv shapes");
+    d.weights_f32 = false;
     d.hidden = H; d.n_heads = NH; d.head_dim = HD; d.inter = I; d.window = h->sliding_window;
     d.codebook_dim = D; d.codebook_size = h->codebook_size; d.vq_dim = V; d.latent = LAT; d.n_rest = h->n_rest;
     const size_t cb = (size_t)h->codebook_size * D;
@@ -1758,6 +1824,7 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
                 vp[(size_t)v * 2 * D + k] = h->first_output_proj[(size_t)k * V + v];
                 if (h->n_rest) vp[(size_t)v * 2 * D + D + k] = h->rest_output_proj[(size_t)k * V + v];
             }
+        note_gemm_weights(c, vp.data(), vp.size());
         RCHK(upload_vec(c, A, vp.data(), vp.size(), &d.vq_proj));
     }
     RCHK(upload_conv(c, h->pre_conv, &d.pre_conv));
@@ -1781,6 +1848,8 @@ static int upload_decoder(qtts_ctx *c, const qtts_decoder_host *h)
                 gu[(size_t)(2 * j + 1) * H + k] = L.up_proj[(size_t)k * I + j];
             }
         }
+        note_gemm_weights(c, qkv.data(), qkv.size());
+        note_gemm_weights(c, gu.data(), gu.size());
         RCHK(upload_vec(c, A, qkv.data(), qkv.size(), &o.qkv));
         RCHK(upload_vec(c, A, gu.data(), gu.size(), &o.gate_up));
         RCHK(upload_t(c, L.o_proj, AD, H, &o.o));
@@ -1928,7 +1997,7 @@ static int ensure_dec_ws(qtts_ctx *c, int frames)
     const size_t per = (size_t)c->dec_floats_per_frame * frames;
     const size_t part = DEC_PART_FLOATS;
     void *m = nullptr;
-    HIPCHK(c, hipMalloc(&m, (5 * per + part) * sizeof(float) + (size_t)16 * frames * sizeof(uint32_t)));
+    HIPCHK(c, hipMalloc(&m, (5 * per + part) * sizeof(float) + (size_t)16 * frames * sizeof(uint32_t) + 256));
     c->dws_mem = m;
     float *f = (float *)m;
     c->dws.a = f;
@@ -1939,6 +2008,7 @@ static int ensure_dec_ws(qtts_ctx *c, int frames)
     c->dws.part = f + 5 * per;
     c->dws.part_cap = part;
     c->dws.codes = (uint32_t *)(f + 5 * per + part);
+    c->dws.range_flag = (int32_t *)(c->dws.codes + (size_t)16 * frames);
     c->dws.cap_frames = frames;
     return QTTS_OK;
 }
@@ -1987,7 +2057,20 @@ extern "C" int qtts_decode_to_audio(qtts_ctx *c, const uint32_t *codes, int64_t 
         RCHK(ensure_io(c, n));
         out = c->d_io;
     }
+    // on the split-f16 convolutions unless a weight matrix is outside their
+    // range; inputs outside it (flagged by the convolutions) repeat the
+    // decode on the f32 matrix path
+    c->dws.f32 = d.weights_f32;
     HIPCHK(c, enqueue_decode(d, c->dws, c->dws.codes, (int)T, cut, out, c->stream));
+    int32_t range = 0;
+    HIPCHK(c, hipMemcpyAsync(&range, c->dws.range_flag, sizeof range, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (range && !c->dws.f32) {
+        c->dws.f32 = true;
+        const hipError_t e = enqueue_decode(d, c->dws, c->dws.codes, (int)T, cut, out, c->stream);
+        c->dws.f32 = false;
+        HIPCHK(c, e);
+    }
     if (!(flags & QTTS_DEVICE_PTRS))
         HIPCHK(c, hipMemcpyAsync(audio, out, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -2677,6 +2760,7 @@ extern "C" int qtts_time_decode(qtts_ctx *c, int64_t n_frames, int32_t iters, do
     const DecoderDev &d = c->dec;
     const int T = (int)n_frames, ncb = d.n_rest + 1;
     RCHK(ensure_dec_ws(c, T));
+    c->dws.f32 = d.weights_f32;
     // synthetic codes from a fixed LCG, uniform over the codebook
     std::vector<uint32_t> codes((size_t)ncb * T);
     uint64_t x = 0x9E3779B97F4A7C15ull;

@@ -5,8 +5,10 @@ Checked through the C ABI against qtts_gemm_q4 on the same weight and rows:
 two calls in a row on the same device buffers, the second with fewer rows
 (the scratch keeps the first call's contents), on both paths (GEMV passes
 and the matrix-core GEMM) and on a ragged n; bit-identical, since both run
-the same kernels in the same order, and within 1e-3 of the oracle.  A
-weight whose passes need more scratch than the array holds is refused.
+the same kernels in the same order, and within 1e-3 of the oracle; rows far
+outside the f16 range on the matrix cores (their largest |x| staged in the
+same array).  A weight whose passes need more scratch than the array holds
+is refused.
 The device buffers are the caller's, allocated here with hipMalloc.
 """
 import ctypes
@@ -84,6 +86,41 @@ def test_gemm_noalloc_matches_gemm(ctx_factory, k, n, rows, path):
             for i in range(2):
                 scale = max(np.abs(R[i]).max(), np.sqrt((R[i].astype(np.float64) ** 2).mean()))
                 assert np.abs(Y[i] - R[i]).max() <= 1e-3 * scale
+    finally:
+        dx.free()
+        dy.free()
+        dw.free()
+
+
+def test_gemm_noalloc_extreme_rows(ctx_factory):
+    """Rows far outside the f16 range on the matrix cores: the rows' largest
+    |x| (the staging range) go to the scratch array too; bit-identical to
+    qtts_gemm_q4 on two calls in a row, the second with fewer rows."""
+    c = ctx_factory(256)
+    h = hip()
+    assert h.hipSetDevice(0) == 0
+    rng = np.random.Generator(np.random.PCG64(1234))
+    k, n = 2048, 4096
+    w = synth.q4_random(rng, k, n)
+    dw = c.upload(w)
+    X = rng.standard_normal((24, k)).astype(np.float32)
+    X[0] *= 1e5
+    X[1] *= 1e-6
+    X[2, 5] = 1e5
+    X[20] *= 3e4
+    dx, dy = DevBuf(h, X.nbytes), DevBuf(h, X.shape[0] * n * 4)
+    try:
+        for r in (24, 18):
+            Xr = X[:r]
+            ref = c.gemm(dw, Xr, path="mfma")
+            dx.put(Xr)
+            c.gemm_noalloc(dw, dx.ptr.value, r, dy.ptr.value, path="mfma")
+            c.sync()
+            Y = dy.get((r, n))
+            assert np.array_equal(bits(Y), bits(ref)), f"rows {r}: differs from qtts_gemm_q4"
+        R = O.gemm(X[:3], w)
+        for i in range(3):
+            assert np.abs(Y[i].astype(np.float64) - R[i]).max() <= 1e-3 * np.abs(R[i]).max()
     finally:
         dx.free()
         dy.free()
