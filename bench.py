@@ -63,6 +63,36 @@ def measured_traffic(kernel):
     return None, None
 
 
+FUSED_FILE = os.path.join(ROOT, "profiles", "frame_fused_kernels_traffic.txt")
+
+
+def fused_profile():
+    """Per-launch rows of the committed profile of the frame's fused
+    launches (kernel trace + FETCH_SIZE / WRITE_SIZE / L2 counter passes of
+    bench.py --fused-only): {description: {avg_us, alg_bytes, counter_bytes,
+    ratio, frac, l2_hit}}, or {} when the summary is absent."""
+    rows = {}
+    try:
+        with open(FUSED_FILE) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) < 11 or not parts[-1].replace(".", "").isdigit():
+                    continue
+                try:
+                    n, avg, med = int(parts[-9]), float(parts[-8]), float(parts[-7])
+                    alg, cb = int(parts[-6].replace(",", "")), int(parts[-5].replace(",", ""))
+                    ratio, gbs, frac, l2 = (float(x) for x in parts[-4:])
+                except ValueError:
+                    continue
+                desc = " ".join(parts[:-9])
+                rows[desc] = {"dispatches": n, "avg_us": avg, "median_us": med, "alg_bytes": alg,
+                              "counter_bytes": cb, "traffic_ratio": ratio, "alg_gbs": gbs, "frac": frac,
+                              "l2_hit": l2}
+    except OSError:
+        pass
+    return rows
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -313,6 +343,10 @@ def main():
                          f"(for kernel profiles of the frame at the headline KV)")
     ap.add_argument("--frames-kv", type=int, default=KV_HEADLINE,
                     help=f"--frames-only: the cached positions the frames start from (default {KV_HEADLINE})")
+    ap.add_argument("--fused-only", action="store_true",
+                    help="only the frame's fused launches, standalone: one talker layer at KV 2048 (q|k|v + "
+                         "attention, o-proj, gate|up + down) and one predictor layer step (q|k|v + attention + "
+                         "o-proj, gate|up + down), cycling the layers, and the copy calibration (for counter passes)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the Q4 GEMV 2048 x 6144 over its weight pool, the same-bytes streaming read "
                          "and the float4 copy (the counter calibration)")
@@ -364,6 +398,24 @@ def main():
         ctx.close()
         print(json.dumps({"talker_attention": {"kv": 2049, "us": round(a_us, 2), "bytes": int(a_bytes),
                                                "gbs": round(a_bytes / a_us / 1e3, 1)},
+                          "float4_copy_256MiB": {"us": round(c_us, 2), "gbs": round(c_bytes / c_us / 1e3, 1)}}),
+              flush=True)
+        return
+
+    if args.fused_only:
+        # 2048 cached positions from a prefill of N(0,1) rows; the talker
+        # layer appends at 2048 and attends 2049, as the frame at KV 2048
+        X = np.random.Generator(np.random.PCG64(7)).standard_normal((2048, talker.hidden)).astype(np.float32)
+        ctx.prefill_talker_raw_from(X, 0)
+        del X
+        tl_us, tl_bytes = ctx.time_kernel(8, 4 * args.layers)
+        pl_us, pl_bytes = ctx.time_kernel(9, 4 * 5 * 14)
+        c_us, c_bytes = ctx.time_kernel(2, 20)
+        ctx.close()
+        print(json.dumps({"talker_layer_kv2049": {"launches": 3, "us": round(tl_us, 2), "bytes": int(tl_bytes),
+                                                  "gbs": round(tl_bytes / tl_us / 1e3, 1)},
+                          "predictor_layer_step": {"launches": 2, "us": round(pl_us, 2), "bytes": int(pl_bytes),
+                                                   "gbs": round(pl_bytes / pl_us / 1e3, 1)},
                           "float4_copy_256MiB": {"us": round(c_us, 2), "gbs": round(c_bytes / c_us / 1e3, 1)}}),
               flush=True)
         return
@@ -463,6 +515,30 @@ def main():
     cp_us, cp_bytes = ctx.time_kernel(2, 20)
     log(f"gate|up {gu_us:.2f}us ({gu_bytes / gu_us / 1e3:.0f} GB/s), attention {at_us:.2f}us "
         f"({at_bytes / at_us / 1e3:.0f} GB/s), float4 copy 256 MiB {cp_bytes / cp_us / 1e3:.0f} GB/s")
+    # the frame's fused launches standalone, as the frame runs them (direct
+    # launches, HIP events): one talker layer at the current KV (3 launches)
+    # and one predictor layer step (2 launches); per-launch durations and
+    # counter bytes from the committed profile of bench.py --fused-only
+    tl_us, tl_bytes = ctx.time_kernel(8, 4 * args.layers)
+    pl_us, pl_bytes = ctx.time_kernel(9, 280)
+    log(f"talker layer {tl_us:.2f}us ({tl_bytes / tl_us / 1e3:.0f} GB/s), predictor layer step {pl_us:.2f}us "
+        f"({pl_bytes / pl_us / 1e3:.0f} GB/s)")
+    prof = fused_profile()
+    pmlp = next((v for k, v in prof.items() if k.startswith("predictor gate|up")), None)
+    frame_kernels = {
+        "talker_layer": {"launches": 3, "kv": ctx.kv_len() + 1, "us": round(tl_us, 2), "bytes": int(tl_bytes),
+                         "gbs": round(tl_bytes / tl_us / 1e3, 1), "frac": round(tl_bytes / tl_us / 1e3 / HBM_PEAK_GBS, 4)},
+        "predictor_layer_step": {"launches": 2, "us": round(pl_us, 2), "bytes": int(pl_bytes),
+                                 "gbs": round(pl_bytes / pl_us / 1e3, 1),
+                                 "frac": round(pl_bytes / pl_us / 1e3 / HBM_PEAK_GBS, 4)},
+        "per_launch": prof, "source": os.path.relpath(FUSED_FILE, ROOT) if prof else None,
+    }
+    if pmlp:
+        frame_kernels["roofline"] = {
+            "bound": "hbm", "kernel": "k_mlp<2, 4, 2, 1024, 1> (predictor gate|up + down, one launch)",
+            "achieved": pmlp["alg_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": pmlp["frac"],
+            "traffic": pmlp["counter_bytes"], "avg_us": pmlp["avg_us"], "bytes_per_launch": pmlp["alg_bytes"],
+            "note": "from the committed kernel trace and counter passes (bench.py --fused-only)"}
 
     # Q4 GEMV k=2048 -> n=6144 (the GEMV tiles run inside every launch of
     # the frame) over a pool of distinct weights (> 256 MB
@@ -558,6 +634,7 @@ def main():
         "frame_roofline": frame_roof,
         "device_memory_mb": mem,
         "frame_split": split,
+        "frame_kernels": frame_kernels,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

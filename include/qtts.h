@@ -575,7 +575,15 @@ int qtts_debug_force_sync_err(qtts_ctx *ctx);
  *   kind 7: a streaming read of 7,110,656 B (the Q4 GEMV k=2048 -> n=6144's
  *           bytes) in one launch, cycling 64 buffers (455 MB, beyond the
  *           last-level cache; no model needed): the attainable time of a
- *           single launch that moves those bytes.
+ *           single launch that moves those bytes;
+ *   kind 8: one talker layer as the frame's step runs it (q|k|v + attention
+ *           in one launch, the o-proj, gate|up + down in one launch) at the
+ *           current length, appending at the free slot, cycling the layers;
+ *           *bytes = the layer's Q4 weights + the K/V read and appended;
+ *   kind 9: one predictor layer step as the chain runs it (q|k|v +
+ *           attention + o-proj in one launch, gate|up + down in the next),
+ *           one row at position 8, cycling the layers; *bytes = the layer's
+ *           Q4 weights + the cached K/V.
  * Kinds 5 and 6 restore the generation state afterwards (counters, the
  * next frame's logits and hidden), so frames generated after the call are
  * those that would have followed without it. */

@@ -236,6 +236,10 @@ hipError_t enqueue_kv_scatter(const KvPaged &kv, int layer, int len, const float
                               hipStream_t s);
 hipError_t enqueue_pred_attn_o_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
 hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, hipStream_t s);
+hipError_t enqueue_pred_layer_fused_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, DevState *st,
+                                           hipStream_t s);
+hipError_t enqueue_talker_layer_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
+                                       const DevState *st, hipStream_t s);
 hipError_t enqueue_copy(const float *src, float *dst, int64_t n, hipStream_t s);
 hipError_t enqueue_read(const float *src, int64_t n, uint32_t never, uint32_t *sink, hipStream_t s);
 hipError_t enqueue_pred_row_tables(const PredictorDev &p, int n_tables, float *X, float *part, float *out,

@@ -3421,6 +3421,25 @@ hipError_t enqueue_pred_layer_timing(const PredictorDev &p, const Workspace &ws,
     return pred_layer<1>(p, ws, l, pos0, s);
 }
 
+// One predictor layer step as the chain runs it (one row at pos0): q|k|v +
+// attention + o-proj in one launch, gate|up + down in the next, the bounded
+// waits reading st.
+hipError_t enqueue_pred_layer_fused_timing(const PredictorDev &p, const Workspace &ws, int l, int pos0, DevState *st,
+                                           hipStream_t s)
+{
+    return pred_layer<1>(p, ws, l, pos0, s, nullptr, nullptr, st);
+}
+
+// One talker layer as the frame's step runs it (q|k|v + attention in one
+// launch at two pages per work item, the o-proj with the page merge,
+// gate|up + down in one launch), appending at `slot` (past the cached
+// length: cached positions untouched) and attending slot + 1 positions.
+hipError_t enqueue_talker_layer_timing(const TalkerDev &m, const Workspace &ws, int l, int slot, int64_t pos,
+                                       const DevState *st, hipStream_t s)
+{
+    return talker_layer(m, ws, l, ws.x, st, pos, slot, 2, s);
+}
+
 // Plain 16-byte-per-lane copy, 8 loads per thread in flight; n % 4 == 0.
 __global__ void __launch_bounds__(256) k_copy_f4(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, int64_t n4)
 {

@@ -2689,6 +2689,43 @@ extern "C" int qtts_time_kernel(qtts_ctx *c, int32_t kind, int32_t iters, double
         HIPCHK(c, hipStreamSynchronize(c->stream));
         return rc;
     }
+    if (kind == 8 || kind == 9) {
+        // the fused launches as the frame runs them, cycling the layers: 8 =
+        // one talker layer (q|k|v + attention, o-proj, gate|up + down) at the
+        // current length, appending at the free slot kv_len; 9 = one
+        // predictor layer step (q|k|v + attention + o-proj, gate|up + down),
+        // one row at position 8.  The waits read the API state (cleared
+        // first); one that ran out is reported.
+        DevState z{};
+        HIPCHK(c, hipMemcpyAsync(c->st_api, &z, sizeof z, hipMemcpyHostToDevice, c->stream));
+        int rc;
+        if (kind == 8) {
+            const int slot = c->h_st->kv_len;
+            if (slot + 1 > c->kv_cap) return fail(c, QTTS_ERR_CAPACITY, "no free KV slot to time the talker layer");
+            if (!talker_fused_attn(m)) return fail(c, QTTS_ERR_UNSUPPORTED, "the talker's q|k|v tile is not the fused one");
+            const int64_t pos = std::min<int64_t>(c->h_st->position, m.rope_rows - 1);
+            const LayerDev &L = m.layers[0];
+            *bytes = (double)(L.qkv.k * L.qkv.n + L.o.k * L.o.n + L.gate_up.k * L.gate_up.n + L.down.k * L.down.n) *
+                         0.5625 + (double)(slot + 2) * 8 * HEAD_DIM * 4 * 2;
+            rc = time_launches(c, iters, [&](int i) {
+                return enqueue_talker_layer_timing(m, c->ws, i % m.n_layers, slot, pos, c->st_api, c->stream);
+            }, avg_us);
+        } else {
+            const PredictorDev &p = c->pm;
+            const LayerDev &L = p.layers[0];
+            *bytes = (double)(L.qkv.k * L.qkv.n + L.o.k * L.o.n + L.gate_up.k * L.gate_up.n + L.down.k * L.down.n) *
+                         0.5625 + 9.0 * 8 * HEAD_DIM * 4 * 2;
+            rc = time_launches(c, iters, [&](int i) {
+                return enqueue_pred_layer_fused_timing(p, c->ws, i % p.n_layers, 8, c->st_api, c->stream);
+            }, avg_us);
+        }
+        if (rc != QTTS_OK) return rc;
+        DevState back{};
+        HIPCHK(c, hipMemcpyAsync(&back, c->st_api, sizeof back, hipMemcpyDeviceToHost, c->stream));
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        if (back.sync_err) return fail(c, QTTS_ERR_HIP, "a cross-workgroup wait timed out while timing");
+        return QTTS_OK;
+    }
     if (kind == 3 || kind == 4) {
         // predictor, one row at position 8 (a mid-chain step), cycling the layers
         const PredictorDev &p = c->pm;

@@ -17,6 +17,16 @@ drift of the generators is caught before any comparison.
   greedy_frames.npz   200 greedy frames (top-k 1) after a 16-row prefill
   decoder.npz         the speech decoder (reduced widths) on 12 frames
                       after 4 warmup frames
+  icl28.npz           the ICL workload at full depth (28-layer talker):
+                      a voice-clone prompt of 9 + 400 rows (build_icl_block
+                      of 150 reference tokens, 269 text tokens and 399
+                      reference frames, prefill_custom_voice), then 32
+                      greedy frames fed the block's 20 remainder rows, then
+                      tts_pad: hidden, logits, K/V rows of layers 0, 13, 27,
+                      the frames' codes, the last frame's logits and hidden
+
+    python tests/golden/make_golden.py            every fixture
+    python tests/golden/make_golden.py icl28      icl28.npz only (minutes)
 """
 import hashlib
 import json
@@ -43,6 +53,10 @@ PREDICTOR = dict(seed=202, n_layers=5)
 DECODER = dict(seed=211, latent=64, hidden=64, n_heads=4, head_dim=16, inter=128, n_tf_layers=2, codebook_size=64,
                codebook_dim=32, vq_dim=32, vocos=(48, 32, 24, 16, 8), rope_max_pos=512)
 GREEDY_FRAMES = 200
+ICL28 = dict(talker=dict(seed=221, n_layers=28, rope_max_pos=2048), predictor=dict(seed=222, n_layers=5))
+ICL28_FRAMES = 32
+ICL28_KV = dict(layers=[0, 13, 27], positions=[0, 204, 408])
+TTS_PAD = 151671
 
 
 def digest(obj):
@@ -106,6 +120,58 @@ def decoder_inputs(d):
     return codes, warm
 
 
+def icl28_models():
+    return synth.make_talker(**ICL28["talker"]), synth.make_predictor(**ICL28["predictor"])
+
+
+def icl28_inputs():
+    """Reference tokens, text tokens, reference codes [16][399] and a voice
+    embedding: 150 + 269 + 1 text rows against 399 + 1 codec rows, so the
+    ICL block holds 400 rows and leaves 20 text rows as the remainder
+    (icl_block_layout, generate_new.rs:120-128)."""
+    rng = np.random.Generator(np.random.PCG64(2210))
+    ref = rng.integers(0, 151936, 150).astype(np.uint32)
+    text = rng.integers(0, 151936, 269).astype(np.uint32)
+    codes = rng.integers(0, 2048, (16, 399)).astype(np.uint32)
+    voice = rng.standard_normal(2048).astype(np.float32)
+    return ref, text, codes, voice
+
+
+def run_icl28(om):
+    """generate_speech's ICL path (generate_new.rs:479-675) on the oracle."""
+    ref, text, codes, voice = icl28_inputs()
+    om.kv_reset()
+    icl, rem = om.build_icl_block(ref, text, codes)
+    hid, lg, pos, _ = om.prefill_custom_voice(text, 0, 2055, voice, icl)
+    out = {"hidden": hid, "logits": lg, "position": np.int64(pos), "remainder_rows": np.int64(rem.shape[0])}
+    for l in ICL28_KV["layers"]:
+        k, v = om.kv_layer(l)
+        out[f"k_l{l}"] = k[ICL28_KV["positions"]]
+        out[f"v_l{l}"] = v[ICL28_KV["positions"]]
+    pad = om.embed_text_token(TTS_PAD)
+    om.gen_begin(lg, hid, pos, 42)
+    params = qtts.sample_params(top_k=1, eos_enabled=False)
+    out["codes"] = np.stack([om.frame(params, rem[f] if f < rem.shape[0] else pad)[0] for f in range(ICL28_FRAMES)])
+    out["final_logits"] = om.g_logits.copy()
+    out["final_hidden"] = om.g_hidden.copy()
+    om.kv_reset()
+    return out
+
+
+def write_icl28(manifest):
+    t, p = icl28_models()
+    om = O.Model(t, p, kv_cap=1024)
+    np.savez_compressed(os.path.join(HERE, "icl28.npz"), **run_icl28(om))
+    om.close()
+    manifest["fixtures"]["icl28"] = {"talker": ICL28["talker"], "predictor": ICL28["predictor"],
+                                     "model": digest((t, p)), "inputs": digest(icl28_inputs()),
+                                     "frames": ICL28_FRAMES, "seed": 42, "kv": ICL28_KV,
+                                     "speaker": 0, "language": 2055,
+                                     "bar": "hidden, logits, K/V rows and the last frame's logits and hidden within "
+                                            "1e-3 * max(max|ref|, rms(ref)); code 0 exact and >= 99% of the "
+                                            "codes, teacher-forced"}
+
+
 def run_talker_step(om, t):
     K, V, emb = talker_step_inputs(t)
     om.kv_reset()
@@ -136,8 +202,16 @@ def run_greedy(om, n_frames):
     return {"codes": codes}
 
 
-def main():
+def main(which=None):
     O.set_workers(WORKERS, THREADS)
+    if which == "icl28":
+        path = os.path.join(HERE, "manifest.json")
+        manifest = json.load(open(path))
+        write_icl28(manifest)
+        with open(path, "w") as f:
+            json.dump(manifest, f, indent=1, sort_keys=True)
+            f.write("\n")
+        return
     manifest = {"oracle_workers": WORKERS, "oracle_threads": THREADS, "fixtures": {}}
 
     w, x, cases = gemv_inputs()
@@ -172,10 +246,11 @@ def main():
     manifest["fixtures"]["decoder"] = {"decoder": {k: list(v) if isinstance(v, tuple) else v for k, v in DECODER.items()},
                                        "model": digest(d), "inputs": digest((codes, warm)),
                                        "tolerance": "1e-3 * max|ref|"}
+    write_icl28(manifest)
     with open(os.path.join(HERE, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1, sort_keys=True)
         f.write("\n")
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1] if len(sys.argv) > 1 else None)

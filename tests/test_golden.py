@@ -81,3 +81,18 @@ def test_decoder_fixture():
     assert G.digest((codes, warm)) == rec["inputs"]
     got = O.decode_to_audio(d, codes, warmup=warm, threads=MANIFEST["oracle_threads"])
     assert same_bits(got, fixture("decoder")["audio"])
+
+
+def test_icl28_fixture_inputs():
+    """The 28-layer ICL fixture: its seeded inputs still regenerate
+    (digest), and it holds what the GPU test reads.  Regenerating its
+    outputs takes the oracle about three minutes (make_golden.py icl28), so
+    this CPU check stops at the inputs."""
+    rec = MANIFEST["fixtures"]["icl28"]
+    assert G.digest(G.icl28_inputs()) == rec["inputs"]
+    f = fixture("icl28")
+    assert int(f["position"]) == 409 and int(f["remainder_rows"]) == 20
+    assert f["codes"].shape == (rec["frames"], 16) and f["hidden"].shape == (2048,) and f["logits"].shape == (3072,)
+    for l in rec["kv"]["layers"]:
+        assert f[f"k_l{l}"].shape == f[f"v_l{l}"].shape == (len(rec["kv"]["positions"]), 8, 128)
+    assert np.all(np.isfinite(f["final_logits"])) and np.all(np.isfinite(f["final_hidden"]))

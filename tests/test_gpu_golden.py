@@ -106,3 +106,47 @@ def test_decoder_golden(ctx_factory):
     c.upload_decoder(d)
     ok, e = close(c.decode_to_audio(codes, warm), fixture("decoder")["audio"])
     assert ok, f"rel err {e}"
+
+
+def test_icl28_golden(ctx_factory):
+    """The ICL workload at full depth against the oracle's fixture: the
+    voice-clone prompt built on the device (build_icl_block, the prompt head,
+    prefill_custom_voice on the matrix cores through all 28 layers), the
+    last hidden and logits and cached K/V rows of layers 0, 13 and 27, then
+    32 greedy frames fed the block's remainder rows as trailing text and
+    teacher-forced on the fixture's codes (talker.rs:379-482,
+    generate_new.rs:552-654)."""
+    m = MANIFEST["fixtures"]["icl28"]
+    t, p = G.icl28_models()
+    assert G.digest((t, p)) == m["model"], "synthetic model generator drifted"
+    ref_tok, text, codes, voice = G.icl28_inputs()
+    assert G.digest((ref_tok, text, codes, voice)) == m["inputs"]
+    f = fixture("icl28")
+    c = ctx_factory(1024)
+    c.upload_model(t, p)
+    del t, p
+    icl, rem = c.build_icl_block(ref_tok, text, codes)
+    assert icl.shape[0] == 400 and rem.shape[0] == int(f["remainder_rows"])
+    hid, lg, pos = c.prefill_custom_voice(text, m["speaker"], m["language"], voice, icl)
+    assert pos == int(f["position"]) == 409
+    for name, got in (("hidden", hid), ("logits", lg)):
+        ok, e = close(got, f[name])
+        assert ok, f"prompt {name}: rel err {e}"
+    for l in m["kv"]["layers"]:
+        k, v = c.kv_gather(l)
+        for name, got in ((f"k_l{l}", k[m["kv"]["positions"]]), (f"v_l{l}", v[m["kv"]["positions"]])):
+            for i, pos_i in enumerate(m["kv"]["positions"]):
+                ok, e = close(got[i], f[name][i])
+                assert ok, f"{name} position {pos_i}: rel err {e}"
+    ref = f["codes"]
+    c.gen_set_text(rem, c.embed_text_token(G.TTS_PAD))
+    c.gen_begin(lg, hid, pos, m["seed"], qtts.sample_params(top_k=1, eos_enabled=False))
+    pred = np.concatenate([c.gen_frames_forced(ref[:20]), c.gen_frames_forced(ref[20:])])
+    assert np.array_equal(pred[:, 0], ref[:, 0]), f"code 0: {pred[:, 0]} vs {ref[:, 0]}"
+    assert (pred[:, 1:] == ref[:, 1:]).mean() >= 0.99
+    lg2, hd2, pos2, _ = c.gen_state()
+    assert pos2 == 409 + ref.shape[0]
+    for name, got, want in (("logits", lg2, f["final_logits"]), ("hidden", hd2, f["final_hidden"])):
+        ok, e = close(got, want)
+        assert ok, f"after the frames, {name}: rel err {e}"
+    c.close()
