@@ -52,6 +52,25 @@ __device__ __forceinline__ uint32_t and_opaque(uint32_t w, uint32_t m)
 // later launches do not wait at all.
 constexpr int LL_SPIN_MAX = 1 << 14;
 
+// A second-stage workgroup of some fused launches holds back its own loads
+// for a fixed time so that the first stage's weight stream, which its
+// inputs depend on, is served first: HBM serves requests roughly in arrival
+// order, and weights a waiting tile fetched at once would only delay the
+// words it waits for.  Times are ticks of the 100 MHz real-time counter,
+// tuned on frames/s (MI355X, KV 64 and 2048): the talker's down tiles 2.5 us
+// (1.5-4 us swept), the predictor's o-proj tiles 0.7 us (0.2-1 us swept).
+// Holding the predictor's down tiles or the talker's attention items did not
+// help (the attention items' page reads are the larger stream).
+constexpr uint32_t HOLD_TALKER_DOWN = 250;
+constexpr uint32_t HOLD_PRED_O = 70;
+
+// Waits `ticks` of the real-time counter (bounded by the clock).
+__device__ __forceinline__ void stage_hold(uint32_t ticks)
+{
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(2);
+}
+
 // ---------------------------------------------------------------------------
 // wave-wide sum (deterministic butterfly order)
 // ---------------------------------------------------------------------------
@@ -2739,10 +2758,11 @@ hipError_t enqueue_embed_sum(const Q4Rows &cp, int n_groups, const uint32_t *cod
 // gate|up and down in one launch (one row): workgroups [0, ng) are the
 // gate|up tiles (single slice, interleaved groups), storing silu(gate) * up
 // as (epoch, value) words; the rest are the down projection's tiles, which
-// issue their weight loads at once and take their k-slice of the words when
-// they arrive.  The gate|up tiles come first in the grid, so every tile a
-// down workgroup waits for has been dispatched before it and never waits.
-template <int GBG, int RG, int RD, int KMAX, int NB>
+// issue their weight loads (after HOLD ticks) and take their k-slice of the
+// words when they arrive.  The gate|up tiles come first in the grid, so
+// every tile a down workgroup waits for has been dispatched before it and
+// never waits.
+template <int GBG, int RG, int RD, int KMAX, int NB, uint32_t HOLD>
 __global__ void __launch_bounds__(512)
 k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled wd, ProLL<NB> pd, EpiPart<NB> ed)
 {
@@ -2755,6 +2775,7 @@ k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled 
         gemv_tile<512, GBG, RG, NB, false>(wg, pg, e, blockIdx.x);
         return;
     }
+    if constexpr (HOLD > 0) stage_hold(HOLD);
     gemv_tile<512, 1, RD, NB, false>(wd, pd, ed, blockIdx.x - ng);
 }
 
@@ -2788,11 +2809,12 @@ static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProRe
     const EpiSwigluLL<NB> eg{fz.ll, inter, fz.seq, 0};
     const ProLL<NB> pd{fz.ll, inter, fz.seq, fz.st};
     const EpiPart<NB> ed{ws.part_down, L.down.npad};
+    constexpr uint32_t hold = KMAX == 2048 ? HOLD_TALKER_DOWN : 0;   // the talker's hidden size
     if (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4)
-        hipLaunchKernelGGL((k_mlp<2, 8, 4, KMAX, NB>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
+        hipLaunchKernelGGL((k_mlp<2, 8, 4, KMAX, NB, hold>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
                            L.down, pd, ed);
     else if (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2)
-        hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX, NB>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
+        hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX, NB, hold>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
                            L.down, pd, ed);
     else
         return hipErrorInvalidValue;
@@ -2992,7 +3014,7 @@ static hipError_t pred_mlp(const PredictorDev &p, const LayerDev &L, const Works
 // Predictor q|k|v GEMV and attention + o-proj in one launch (one row):
 // workgroups [0, nq) are the q|k|v tiles, storing (epoch, value) words; the
 // rest are the o-proj tiles, whose prologue issues its cache, gamma and
-// weight loads at once and attends when its words arrive.  The q|k|v tiles
+// weight loads (after HOLD_PRED_O ticks) and attends when its words arrive.  The q|k|v tiles
 // come first in the grid, so every tile an o-proj workgroup waits for has
 // been dispatched before it and never waits itself.  The gate|up launch that
 // follows advances the epoch.
@@ -3007,6 +3029,7 @@ k_pred_qkv_attn_o(Q4Tiled wq, ProResidRms<NB, 1024> pq, EpiLL<NB> eq, int nq, Q4
         gemv_tile<256, 1, 2, NB>(wq, pq, e, blockIdx.x);
         return;
     }
+    stage_hold(HOLD_PRED_O);
     gemv_tile<256, 1, 2, NB>(wo, po, eo, blockIdx.x - nq);
 }
 
