@@ -2290,6 +2290,7 @@ __global__ void k_silu(float *x, int n)
 constexpr int SAMP_MAX = 4096;
 constexpr int SAMP_T = 256;
 constexpr int SAMP_E = SAMP_MAX / SAMP_T;        // entries per thread
+static_assert(SAMP_MAX % 16 == 0, "the draw reads blocks of 16");
 
 __device__ __forceinline__ bool rank_before(float pa, int ia, float pb, int ib)
 {
@@ -2330,18 +2331,26 @@ struct SampleArgs {
     int n_prev;
 };
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_int(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, false);
+}
+
 // Exclusive prefix sum of one int per lane in lane order; *total = the
-// wave's sum.
+// wave's sum.  On the VALU: row shifts by 1, 2, 4 and 8 scan each 16-lane
+// row (lanes without a source add 0), then row_bcast:15 adds row r's total
+// to row r + 1 (rows 1 and 3) and row_bcast:31 adds lane 31 to rows 2 and 3.
 __device__ __forceinline__ int wave_excl_scan(int v, int *total)
 {
-    const int lane = threadIdx.x & 63;
     int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(x, o);
-        if (lane >= o) x += y;
-    }
-    *total = __shfl(x, 63);
+    x += dpp_int<0x111, 0xF>(x);
+    x += dpp_int<0x112, 0xF>(x);
+    x += dpp_int<0x114, 0xF>(x);
+    x += dpp_int<0x118, 0xF>(x);
+    x += dpp_int<0x142, 0xA>(x);
+    x += dpp_int<0x143, 0xC>(x);
+    *total = __builtin_amdgcn_readlane(x, 63);
     return x - v;
 }
 
@@ -2393,18 +2402,8 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
     __shared__ uint32_t sel_prefix, sel_mask;
     __shared__ int sel_need, sel_done, cutoff_s;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    if (mode == 0 && st->stop) return;
-    float temp, top_p, rep;
-    int top_k, n_prev;
-    const uint32_t *prev;
-    if (mode == 0) {
-        temp = st->frame_idx < st->onset_frames ? st->onset_temperature : st->temperature;
-        top_p = st->top_p; rep = st->rep_penalty; top_k = st->top_k;
-        prev = st->prev; n_prev = 16;
-    } else {
-        temp = api.temperature; top_p = api.top_p; rep = api.rep; top_k = api.top_k;
-        prev = api.prev; n_prev = api.n_prev;
-    }
+    // the logits and every state word the kernel reads are loaded up front
+    // (the logits buffer is valid whatever the state holds)
     const int i0 = t * SAMP_E;
     float v[SAMP_E];
     if (i0 + SAMP_E <= n && ((uintptr_t)logits & 15) == 0) {
@@ -2420,12 +2419,34 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
             v[e] = i0 + e < n ? x : -INFINITY;
         }
     }
+    float temp, top_p, rep;
+    int top_k, n_prev;
+    const uint32_t *prev;
+    uint64_t rs0;
+    uint32_t tok0;   // history entry t, for t < min(n_prev, SAMP_T)
+    int force = 0, eos_en = 0, fidx = 0, fbase = 0;
+    uint32_t eos_id = 0;
+    if (mode == 0) {
+        if (st->stop) return;
+        temp = st->frame_idx < st->onset_frames ? st->onset_temperature : st->temperature;
+        top_p = st->top_p; rep = st->rep_penalty; top_k = st->top_k;
+        prev = st->prev; n_prev = 16;
+        tok0 = st->prev[min(t, 15)];
+        rs0 = st->rng;
+        force = st->force; eos_en = st->eos_enabled; eos_id = st->eos_id;
+        fidx = st->frame_idx; fbase = st->forced_base;
+    } else {
+        temp = api.temperature; top_p = api.top_p; rep = api.rep; top_k = api.top_k;
+        prev = api.prev; n_prev = api.n_prev;
+        tok0 = n_prev > 0 ? prev[min(t, n_prev - 1)] : 0u;
+        rs0 = *rng_api;
+    }
     // repetition penalty (generate_new.rs:776-785): once per history entry
     if (rep != 1.0f && n_prev > 0) {
         for (int i = t; i < n; i += SAMP_T) ki[i] = 0;
         __syncthreads();
         for (int j = t; j < n_prev; j += SAMP_T) {
-            const uint32_t tok = prev[j];
+            const uint32_t tok = j < SAMP_T ? tok0 : prev[j];
             if (tok < (uint32_t)n) atomicAdd(&ki[tok], 1);
         }
         __syncthreads();
@@ -2588,35 +2609,45 @@ k_sampler(const float *logits, int n, DevState *st, int mode, SampleArgs api, ui
         if (v[e] != 0.0f) { kp[o] = v[e]; ki[o] = i0 + e; o++; }
     __syncthreads();
     if (t == 0) {
-        uint64_t rs = mode == 0 ? st->rng : *rng_api;
+        uint64_t rs = rs0;
         const float r = simple_rand_dev(rs);
         float cs = 0.0f;
         uint32_t res = 0;
         bool found = false;
-        for (int k = 0; k < total && !found; k += 4) {
-            const f32x4 q = *(const f32x4 *)&kp[k];
-            const float qv[4] = {q.x, q.y, q.z, q.w};
+        // blocks of 16 read together, then summed in index order without
+        // branches (entries past `total` are read, never summed: total <=
+        // SAMP_MAX, a multiple of 16)
+        for (int k = 0; k < total && !found; k += 16) {
+            f32x4 q[4];
+            int4 qi[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                if (!found && k + j < total) {
-                    cs += qv[j];
-                    if (r < cs) { res = (uint32_t)ki[k + j]; found = true; }
-                }
+                q[j] = *(const f32x4 *)&kp[k + 4 * j];
+                qi[j] = *(const int4 *)&ki[k + 4 * j];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const bool live = !found && k + j < total;
+                const float c2 = cs + q[j >> 2][j & 3];
+                const bool hit = live && r < c2;
+                cs = live ? c2 : cs;
+                res = hit ? (uint32_t)qi[j >> 2][j & 3] : res;
+                found = found || hit;
             }
         }
         if (mode == 0) {
             st->rng = rs;
             st->pred[0] = res;
             uint32_t used = res;
-            if (st->force && forced) {
+            if (force && forced) {
                 // this frame's forced codes, staged for the predictor chain
-                const uint32_t *fr = forced + (size_t)(st->frame_idx - st->forced_base) * 16;
+                const uint32_t *fr = forced + (size_t)(fidx - fbase) * 16;
                 for (int i = 0; i < 16; i++) st->fcode[i] = fr[i];
                 used = fr[0];
             }
             st->used[0] = used;
             st->prev[0] = used;
-            if (st->eos_enabled && !st->force && res == st->eos_id) { st->stop = 1; st->eos = 1; }
+            if (eos_en && !force && res == eos_id) { st->stop = 1; st->eos = 1; }
         } else {
             *rng_api = rs;
             *out_api = res;
