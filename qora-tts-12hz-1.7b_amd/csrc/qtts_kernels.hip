@@ -58,11 +58,14 @@ constexpr int LL_SPIN_MAX = 1 << 14;
 // order, and weights a waiting tile fetched at once would only delay the
 // words it waits for.  Times are ticks of the 100 MHz real-time counter,
 // tuned on frames/s (MI355X, KV 64 and 2048): the talker's down tiles 2.5 us
-// (1.5-4 us swept), the predictor's o-proj tiles 0.7 us (0.2-1 us swept).
-// Holding the predictor's down tiles or the talker's attention items did not
-// help (the attention items' page reads are the larger stream).
+// (1.5-4 us swept), the predictor's o-proj tiles 0.7 us (0.2-1 us swept),
+// the predictor's down tiles behind one-group gate|up tiles 0.8 us (0.3-3 us
+// swept; behind paired gate|up tiles a hold did not help).  Holding the
+// talker's attention items back did not help either (their page reads are
+// the larger stream).
 constexpr uint32_t HOLD_TALKER_DOWN = 250;
 constexpr uint32_t HOLD_PRED_O = 70;
+constexpr uint32_t HOLD_PRED_DOWN = 80;
 
 // Waits `ticks` of the real-time counter (bounded by the clock).
 __device__ __forceinline__ void stage_hold(uint32_t ticks)
@@ -898,6 +901,66 @@ struct ProLL {
         for (int u = 0; u < U; u++) {
             const int i = threadIdx.x + u * T;
             if (i < NB * KC) xs[i] = v[u];
+        }
+    }
+    __device__ void finish(int s, int c, int nct) const {}
+};
+
+// silu(gate) * up of the GEMV input rows k0.. from the raw gate|up column
+// sums that one-group producer tiles of the same launch store as (epoch,
+// value) words (EpiLL over the interleaved gate|up weight: group 2j holds
+// gate columns 32j..32j+31, group 2j + 1 the matching up columns).  The
+// product is formed as EpiSwigluLL and ProSwiglu form it.  Rows past n read
+// as 0.
+template <int NB = 1>
+struct ProSwigluLL {
+    const uint64_t *ll;      // [NB][npad] gate|up words
+    int npad, n;             // words per row, rows of h (inter)
+    const uint32_t *seq;
+    DevState *st;
+    template <int T, int KC>
+    struct Fetch {
+        uint32_t epoch;
+        int give_up;
+    };
+    template <int T, int KC>
+    __device__ void fetch(Fetch<T, KC> &f, int k0, int ctile) const
+    {
+        f.epoch = *seq + 1;
+        f.give_up = st->sync_err;
+    }
+    template <int T, int KC>
+    __device__ void load(const Fetch<T, KC> &f, float *xs, int k0, int ctile) const
+    {
+        constexpr int U = (NB * KC + T - 1) / T;
+        float g[U], u[U];
+        for (int it = 0;; it++) {
+            bool ok = true;
+#pragma unroll
+            for (int q = 0; q < U; q++) {
+                const int i = min((int)threadIdx.x + q * T, NB * KC - 1);
+                const int b = i / KC, r = k0 + (i - b * KC), rr = min(r, n - 1);
+                const uint64_t *p = ll + (size_t)b * npad + (rr >> 5) * 64 + (rr & 31);
+                const uint64_t wg = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                const uint64_t wu = __hip_atomic_load(p + 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                ok = ok && (r >= n || ((uint32_t)(wg >> 32) == f.epoch && (uint32_t)(wu >> 32) == f.epoch));
+                g[q] = __uint_as_float((uint32_t)wg);
+                u[q] = __uint_as_float((uint32_t)wu);
+            }
+            if (__all(ok) || f.give_up) break;
+            if (it >= LL_SPIN_MAX) {
+                if ((threadIdx.x & 63) == 0) st->sync_err = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+#pragma unroll
+        for (int q = 0; q < U; q++) {
+            const int i = threadIdx.x + q * T;
+            if (i < NB * KC) {
+                const int b = i / KC, r = k0 + (i - b * KC);
+                xs[i] = r < n ? silu_f(g[q]) * u[q] : 0.0f;
+            }
         }
     }
     __device__ void finish(int s, int c, int nct) const {}
@@ -2810,6 +2873,25 @@ k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled 
     gemv_tile<512, 1, RD, NB, false>(wd, pd, ed, blockIdx.x - ng);
 }
 
+// The same on one-group gate|up tiles: a gate or an up group per tile, twice
+// the tiles of the paired layout, so twice the CUs stream the gate|up weight
+// (a 1024 x 6144 gate|up GEMV: 3.0 us on 192 one-group tiles, 3.6 us on 96
+// paired ones).  The tiles store their raw column sums as words and the
+// down tiles form silu(gate) * up from them (ProSwigluLL).
+template <int RG, int RD, int KMAX, int NB, uint32_t HOLD>
+__global__ void __launch_bounds__(512)
+k_mlp1(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiLL<NB> eg, int ng, Q4Tiled wd, ProSwigluLL<NB> pd, EpiPart<NB> ed)
+{
+    if ((int)blockIdx.x < ng) {
+        EpiLL<NB> e = eg;
+        e.epoch = *eg.seq + 1;
+        gemv_tile<512, 1, RG, NB, false>(wg, pg, e, blockIdx.x);
+        return;
+    }
+    if constexpr (HOLD > 0) stage_hold(HOLD);
+    gemv_tile<512, 1, RD, NB, false>(wd, pd, ed, blockIdx.x - ng);
+}
+
 // The words and epoch of a fused gate|up + down launch.
 struct MlpFuse {
     uint64_t *ll;
@@ -2847,6 +2929,11 @@ static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProRe
     else if (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2)
         hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX, NB, hold>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
                            L.down, pd, ed);
+    else if (L.gate_up.cfg == TILE_G1_T512_R2 && L.down.cfg == TILE_G1_T512_R2 && L.gate_up.interleave)
+        hipLaunchKernelGGL((k_mlp1<2, 2, KMAX, NB, KMAX == 2048 ? HOLD_TALKER_DOWN : HOLD_PRED_DOWN>), dim3(ng + nd),
+                           dim3(512), 0, s, L.gate_up, pro_gu,
+                           EpiLL<NB>{fz.ll, L.gate_up.npad, fz.seq, 0}, ng, L.down,
+                           ProSwigluLL<NB>{fz.ll, L.gate_up.npad, inter, fz.seq, fz.st}, ed);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -2856,7 +2943,8 @@ static bool mlp_fusable(const LayerDev &L)
 {
     if (!fused_mlp_on() || L.gate_up.S != 1) return false;
     return (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4) ||
-           (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2);
+           (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2) ||
+           (L.gate_up.cfg == TILE_G1_T512_R2 && L.down.cfg == TILE_G1_T512_R2 && L.gate_up.interleave);
 }
 
 // gate|up then down: h = silu(gate) * up written by the gate|up epilogue when

@@ -198,7 +198,7 @@ static int default_cfg(const char *role, int64_t k)
     if (r == "HEAD" || r == "PHEAD") return TILE_G1_T256_R4;                    // KC 1024
     if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;            // one slice, SiLU epilogue
     if (r == "PGU") {
-        if (k <= 1024 && fused_mlp_enabled()) return TILE_G2_T512_R4;           // one slice: gate|up + down in one launch
+        if (k <= 1024 && fused_mlp_enabled()) return TILE_G1_T512_R2;           // one slice, one group per tile: gate|up + down in one launch
         return k <= 1024 ? TILE_G2_T256_R4 : TILE_G2_T512;                      // 2 slices, SwiGLU in the down prologue
     }
     if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
@@ -798,7 +798,9 @@ static int alloc_workspace(qtts_ctx *c)
     size_t lq = 0, lpq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
     for (const LayerDev &L : c->players) upd(lpq, L.qkv, 2);
-    const size_t lth = (size_t)m.inter, lph = 2 * (size_t)p.inter;   // predictor words: up to 2 rows
+    // predictor words: up to 2 rows of silu(gate) * up, or of the raw gate|up
+    // column sums (one-group gate|up tiles)
+    const size_t lth = (size_t)m.inter, lph = 2 * 2 * (size_t)p.inter;
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
     RCHK(dev_alloc(c, A, &w.ll_pqkv, lpq));
     RCHK(dev_alloc(c, A, &w.ll_th, lth));
