@@ -305,12 +305,14 @@ struct ProAttnCombine {
 // Every workgroup rebuilds x in LDS; after the tile's GEMV, the slice-0
 // workgroups store x (the residual stream) to x_out and the normed vector to
 // side, each a share of the columns.  Consumer row b reads producer row
-// prow + b of NBP rows.  Needs k % 4 == 0 and k <= KMAX.  Up to RES_MAX_S
-// producer slices are fetched ahead; more are read in the load stage.
+// prow + b of NBP rows.  Needs k % 4 == 0 and k <= KMAX.  Up to MS producer
+// slices are fetched ahead (RES_MAX_S, or 6 at the predictor's width, whose
+// down projection leaves 6); more are read in the load stage.
 constexpr int RES_MAX_S = 4;
 
 template <int NB, int KMAX>
 struct ProResidRms {
+    static constexpr int MS = KMAX <= 1024 ? 6 : RES_MAX_S;
     const float *base;
     int ldb;
     const float *parts;
@@ -336,7 +338,7 @@ struct ProResidRms {
         static constexpr int U = (KMAX / 4 + T - 1) / T;   // float4 of a row per thread
         static constexpr int UG = (KC + T - 1) / T;         // gamma values per thread
         f32x4 base[NB][U];
-        f32x4 part[NB][RES_MAX_S][U];
+        f32x4 part[NB][MS][U];
         f32x4 bias[U];
         uint32_t g[4 * UG];   // UG for the LDS tile; a thread's own R rows (R = GB * UG, GB <= 4)
     };
@@ -370,7 +372,7 @@ struct ProResidRms {
                 if (base) f.base[b][u] = ld4(base + (size_t)b * ldb + 4 * i);
                 if (parts) {
 #pragma unroll
-                    for (int s = 0; s < RES_MAX_S; s++)
+                    for (int s = 0; s < MS; s++)
                         f.part[b][s][u] = ld4(parts + ((size_t)min(s, S - 1) * NBP + prow + b) * npad + 4 * i);
                 }
             }
@@ -433,9 +435,9 @@ struct ProResidRms {
                 if (parts) {
                     f32x4 a = f.part[b][0][u];
 #pragma unroll
-                    for (int s = 1; s < RES_MAX_S; s++)
+                    for (int s = 1; s < MS; s++)
                         if (s < S) a += f.part[b][s][u];
-                    for (int s = RES_MAX_S; s < S; s++)
+                    for (int s = MS; s < S; s++)
                         a += ld4(parts + ((size_t)s * NBP + prow + b) * npad + 4 * min(i, k4 - 1));
                     x = base ? f.base[b][u] + a : a;
                 } else if (base) {
@@ -2878,18 +2880,18 @@ k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled 
 // (a 1024 x 6144 gate|up GEMV: 3.0 us on 192 one-group tiles, 3.6 us on 96
 // paired ones).  The tiles store their raw column sums as words and the
 // down tiles form silu(gate) * up from them (ProSwigluLL).
-template <int RG, int RD, int KMAX, int NB, uint32_t HOLD>
-__global__ void __launch_bounds__(512)
+template <int T, int RG, int RD, int KMAX, int NB, uint32_t HOLD>
+__global__ void __launch_bounds__(T)
 k_mlp1(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiLL<NB> eg, int ng, Q4Tiled wd, ProSwigluLL<NB> pd, EpiPart<NB> ed)
 {
     if ((int)blockIdx.x < ng) {
         EpiLL<NB> e = eg;
         e.epoch = *eg.seq + 1;
-        gemv_tile<512, 1, RG, NB, false>(wg, pg, e, blockIdx.x);
+        gemv_tile<T, 1, RG, NB, false>(wg, pg, e, blockIdx.x);
         return;
     }
     if constexpr (HOLD > 0) stage_hold(HOLD);
-    gemv_tile<512, 1, RD, NB, false>(wd, pd, ed, blockIdx.x - ng);
+    gemv_tile<T, 1, RD, NB, false>(wd, pd, ed, blockIdx.x - ng);
 }
 
 // The words and epoch of a fused gate|up + down launch.
@@ -2930,8 +2932,13 @@ static hipError_t launch_mlp(const LayerDev &L, const Workspace &ws, const ProRe
         hipLaunchKernelGGL((k_mlp<2, 4, 2, KMAX, NB, hold>), dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu, eg, ng,
                            L.down, pd, ed);
     else if (L.gate_up.cfg == TILE_G1_T512_R2 && L.down.cfg == TILE_G1_T512_R2 && L.gate_up.interleave)
-        hipLaunchKernelGGL((k_mlp1<2, 2, KMAX, NB, KMAX == 2048 ? HOLD_TALKER_DOWN : HOLD_PRED_DOWN>), dim3(ng + nd),
-                           dim3(512), 0, s, L.gate_up, pro_gu,
+        hipLaunchKernelGGL((k_mlp1<512, 2, 2, KMAX, NB, KMAX == 2048 ? HOLD_TALKER_DOWN : HOLD_PRED_DOWN>),
+                           dim3(ng + nd), dim3(512), 0, s, L.gate_up, pro_gu,
+                           EpiLL<NB>{fz.ll, L.gate_up.npad, fz.seq, 0}, ng, L.down,
+                           ProSwigluLL<NB>{fz.ll, L.gate_up.npad, inter, fz.seq, fz.st}, ed);
+    else if (L.gate_up.cfg == TILE_G1_T256_R4 && L.down.cfg == TILE_G1_T256_R2 && L.gate_up.interleave)
+        hipLaunchKernelGGL((k_mlp1<256, 4, 2, KMAX, NB, KMAX == 2048 ? HOLD_TALKER_DOWN : HOLD_PRED_DOWN>),
+                           dim3(ng + nd), dim3(256), 0, s, L.gate_up, pro_gu,
                            EpiLL<NB>{fz.ll, L.gate_up.npad, fz.seq, 0}, ng, L.down,
                            ProSwigluLL<NB>{fz.ll, L.gate_up.npad, inter, fz.seq, fz.st}, ed);
     else
@@ -2944,7 +2951,8 @@ static bool mlp_fusable(const LayerDev &L)
     if (!fused_mlp_on() || L.gate_up.S != 1) return false;
     return (L.gate_up.cfg == TILE_G2_T512 && L.down.cfg == TILE_G1_T512_R4) ||
            (L.gate_up.cfg == TILE_G2_T512_R4 && L.down.cfg == TILE_G1_T512_R2) ||
-           (L.gate_up.cfg == TILE_G1_T512_R2 && L.down.cfg == TILE_G1_T512_R2 && L.gate_up.interleave);
+           (L.gate_up.cfg == TILE_G1_T512_R2 && L.down.cfg == TILE_G1_T512_R2 && L.gate_up.interleave) ||
+           (L.gate_up.cfg == TILE_G1_T256_R4 && L.down.cfg == TILE_G1_T256_R2 && L.gate_up.interleave);
 }
 
 // gate|up then down: h = silu(gate) * up written by the gate|up epilogue when

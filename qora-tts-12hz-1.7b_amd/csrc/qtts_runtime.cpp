@@ -198,11 +198,11 @@ static int default_cfg(const char *role, int64_t k)
     if (r == "HEAD" || r == "PHEAD") return TILE_G1_T256_R4;                    // KC 1024
     if (r == "TGU") return k <= 2048 ? TILE_G2_T512 : TILE_G2_T256;            // one slice, SiLU epilogue
     if (r == "PGU") {
-        if (k <= 1024 && fused_mlp_enabled()) return TILE_G1_T512_R2;           // one slice, one group per tile: gate|up + down in one launch
+        if (k <= 1024 && fused_mlp_enabled()) return TILE_G1_T256_R4;           // one slice, one group per tile: gate|up + down in one launch
         return k <= 1024 ? TILE_G2_T256_R4 : TILE_G2_T512;                      // 2 slices, SwiGLU in the down prologue
     }
     if (r == "TDOWN") return TILE_G1_T512_R4;                                   // KC 2048
-    if (r == "PDOWN") return TILE_G1_T512_R2;                                   // KC 1024
+    if (r == "PDOWN") return fused_mlp_enabled() ? TILE_G1_T256_R2 : TILE_G1_T512_R2;   // KC 512 (6 slices) / 1024
     if (r == "GEMV") return TILE_G1_T256;                                       // standalone Q4 GEMV
     return k <= 2048 ? TILE_G1_T256 : TILE_G8_T256;                             // text fc
 }
