@@ -798,8 +798,8 @@ static int alloc_workspace(qtts_ctx *c)
     size_t lq = 0, lpq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
     for (const LayerDev &L : c->players) upd(lpq, L.qkv, 2);
-    // predictor words: up to 2 rows of silu(gate) * up, or of the raw gate|up
-    // column sums (one-group gate|up tiles)
+    // silu(gate) * up words (talker), the raw gate|up column sums of the
+    // predictor's one-group gate|up tiles for up to 2 rows
     const size_t lth = (size_t)m.inter, lph = 2 * 2 * (size_t)p.inter;
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
     RCHK(dev_alloc(c, A, &w.ll_pqkv, lpq));
