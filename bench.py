@@ -535,7 +535,7 @@ def main():
     }
     if pmlp:
         frame_kernels["roofline"] = {
-            "bound": "hbm", "kernel": "k_mlp<2, 4, 2, 1024, 1, 0> (predictor gate|up + down, one launch)",
+            "bound": "hbm", "kernel": "k_mlp1<256, 4, 2, 1024, 1, 80> (predictor gate|up + down, one launch, one-group gate|up tiles)",
             "achieved": pmlp["alg_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": pmlp["frac"],
             "traffic": pmlp["counter_bytes"], "avg_us": pmlp["avg_us"], "bytes_per_launch": pmlp["alg_bytes"],
             "note": "from the committed kernel trace and counter passes (bench.py --fused-only)"}
