@@ -58,13 +58,13 @@ constexpr int LL_SPIN_MAX = 1 << 14;
 // order, and weights a waiting tile fetched at once would only delay the
 // words it waits for.  Times are ticks of the 100 MHz real-time counter,
 // tuned on frames/s (MI355X, KV 64 and 2048): the talker's down tiles 2.5 us
-// (1.5-4 us swept), the predictor's o-proj tiles 0.7 us (0.2-1 us swept),
+// (1.5-4 us swept), the predictor's o-proj tiles 1.0 us (0.2-2.2 us swept),
 // the predictor's down tiles behind one-group gate|up tiles 0.8 us (0.3-3 us
 // swept; behind paired gate|up tiles a hold did not help).  Holding the
 // talker's attention items back did not help either (their page reads are
 // the larger stream).
 constexpr uint32_t HOLD_TALKER_DOWN = 250;
-constexpr uint32_t HOLD_PRED_O = 70;
+constexpr uint32_t HOLD_PRED_O = 100;
 constexpr uint32_t HOLD_PRED_DOWN = 80;
 
 // Waits `ticks` of the real-time counter (bounded by the clock).
