@@ -798,9 +798,10 @@ static int alloc_workspace(qtts_ctx *c)
     size_t lq = 0, lpq = 0;
     for (const LayerDev &L : c->tlayers) upd(lq, L.qkv, 1);
     for (const LayerDev &L : c->players) upd(lpq, L.qkv, 2);
-    // silu(gate) * up words (talker), the raw gate|up column sums of the
-    // predictor's one-group gate|up tiles for up to 2 rows
-    const size_t lth = (size_t)m.inter, lph = 2 * 2 * (size_t)p.inter;
+    // silu(gate) * up words, or the raw gate|up column sums (twice as many)
+    // when a one-group gate|up tile feeds the down tiles (the predictor's
+    // default, any role's tile override); the predictor's for up to 2 rows
+    const size_t lth = 2 * (size_t)m.inter, lph = 2 * 2 * (size_t)p.inter;
     RCHK(dev_alloc(c, A, &w.ll_qkv, lq));
     RCHK(dev_alloc(c, A, &w.ll_pqkv, lpq));
     RCHK(dev_alloc(c, A, &w.ll_th, lth));
