@@ -2862,13 +2862,14 @@ template <int GBG, int RG, int RD, int KMAX, int NB, uint32_t HOLD>
 __global__ void __launch_bounds__(512)
 k_mlp(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiSwigluLL<NB> eg, int ng, Q4Tiled wd, ProLL<NB> pd, EpiPart<NB> ed)
 {
-    // both tile kinds on the byte-convert inner loop: measured faster here
-    // (frames at KV 2048: 544.8 against 537.1 frames/s with v_fma_mix in
-    // both), although v_fma_mix is faster in the other GEMV launches
+    // the down tiles on the byte-convert inner loop, the gate|up tiles on
+    // v_fma_mix (same bits either way): frames at KV 2048 586.9 against
+    // 585.7 frames/s with both on byte converts and 584.7 with the down
+    // tiles on v_fma_mix too (the same split measured for k_mlp1)
     if ((int)blockIdx.x < ng) {
         EpiSwigluLL<NB> e = eg;
         e.epoch = *eg.seq + 1;
-        gemv_tile<512, GBG, RG, NB, false>(wg, pg, e, blockIdx.x);
+        gemv_tile<512, GBG, RG, NB, true>(wg, pg, e, blockIdx.x);
         return;
     }
     if constexpr (HOLD > 0) stage_hold(HOLD);
@@ -2887,7 +2888,7 @@ k_mlp1(Q4Tiled wg, ProResidRms<NB, KMAX> pg, EpiLL<NB> eg, int ng, Q4Tiled wd, P
     if ((int)blockIdx.x < ng) {
         EpiLL<NB> e = eg;
         e.epoch = *eg.seq + 1;
-        gemv_tile<T, 1, RG, NB, false>(wg, pg, e, blockIdx.x);
+        gemv_tile<T, 1, RG, NB, true>(wg, pg, e, blockIdx.x);
         return;
     }
     if constexpr (HOLD > 0) stage_hold(HOLD);
