@@ -10,14 +10,18 @@
 //   decode attention   talker.rs:304-331    (k_talker_attn + the o-proj's ProAttnCombine)
 //   SwiGLU             talker.rs:338-349    (EpiSwiglu / ProSwiglu)
 //   predictor layers   code_predictor.rs:345-513 (k_pred_attn et al.)
-//   argmax             code_predictor.rs:335-341 (k_argmax)
+//   argmax             code_predictor.rs:335-341 (EpiArgmax candidates, k_argmax)
 //   sample_token       generate_new.rs:771-862   (k_sampler)
 //   frame fusion       generate_new.rs:638-654   (k_combine)
 //
-// Every stage is one kernel; a frame is ~500 of them replayed from a HIP
-// graph.  Stages hand partial sums (one row per k-slice) to the next
-// stage, whose prologue reduces them in slice order, so no stage needs an
-// atomic or a device-wide fence.
+// A frame is 264 dependent launches replayed from a HIP graph.  Launches
+// hand partial sums (one row per k-slice) to the next launch, whose
+// prologue reduces them in slice order.  Inside the fused launches
+// (k_talker_qkv_attn, k_pred_qkv_attn_o, k_mlp, k_mlp1) the first stage's
+// workgroups hand their column sums to the second stage's as (epoch, value)
+// words, stored and polled with system-scope relaxed atomics and bounded
+// waits; no kernel uses a device-wide fence or a read-modify-write atomic
+// on global memory.
 #include "qtts_device.h"
 #include "qtts_kernels.h"
 #include "qtts_devutil.h"
