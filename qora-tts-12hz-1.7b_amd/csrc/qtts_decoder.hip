@@ -3,7 +3,9 @@
 //
 // Activations stay channel-first [channels][positions] as in the reference.
 // Every convolution, projection and pointwise layer is one implicit GEMM on
-// the f32 matrix cores (k_conv_gemm): rows = output channels, columns =
+// the matrix cores (k_conv_gemm; f32-accurate: operands split into f16 hi +
+// lo, three f16 products per pair, f32 accumulation; f32 matrix
+// instructions with QTTS_DEC_F32=1): rows = output channels, columns =
 // positions, contraction = input channels x taps, with the im2col gather
 // done while staging the activation tile:
 //   causal_conv1d        conv.rs:114-228   taps at t + j*dil - (K-1)*dil
