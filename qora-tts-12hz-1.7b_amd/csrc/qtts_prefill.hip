@@ -1,15 +1,19 @@
 // qtts_prefill.hip — batched talker prefill for long prompts on the matrix
 // cores (prefill_talker_raw_from, talker.rs:379-482).
 //
-// A prompt of M rows runs layer by layer: per layer
-//   k_row_inv            1/rms of every residual row         gemv.rs:445-454
-//   k_gemm_q4 (store)    [M x 2048] x [2048 x 4096] q|k|v    talker.rs:392-400
-//   k_prefill_qkv_post   QK-norm, RoPE, K/V append           talker.rs:402-425
+// A prompt of M rows runs layer by layer (k_row_inv first: 1/rms of every
+// input row, gemv.rs:445-454): per layer
+//   k_gemm_q4 (parts)    [M x 2048] x [2048 x 4096] q|k|v,   talker.rs:392-400
+//                        input norm fused, 3 k-slices
+//   k_prefill_qkv_post   slices summed, QK-norm, RoPE,       talker.rs:402-425
+//                        K/V append
 //   k_prefill_attn_mx    causal attention over the cache     talker.rs:427-458
-//   k_gemm_q4 (add)      x += attn x o_proj                  talker.rs:460-461
-//   k_row_inv            post-attention norm
-//   k_gemm_q4 (swiglu)   silu(gate) * up, gate|up fused      talker.rs:464-472
-//   k_gemm_q4 (add)      x += h x down_proj                  talker.rs:473-474
+//   k_gemm_q4 (parts)    attn x o_proj, 6 k-slices           talker.rs:460
+//   k_resid_add_inv      x += slices; post-attention 1/rms   talker.rs:461-468
+//   k_gemm_q4 (swiglu)   silu(gate) * up, gate|up fused,     talker.rs:470-474
+//                        post-attention norm fused
+//   k_gemm_q4 (parts)    h x down_proj, 6 k-slices           talker.rs:475
+//   k_resid_add_inv      x += slices; next layer's 1/rms     talker.rs:476
 // then k_final_rms on the last row (talker.rs:477-481).
 //
 // k_gemm_q4 contracts f32 operands with f32 accumulation, the arithmetic
