@@ -2268,16 +2268,29 @@ k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, DevState *st, const float *
     }
     if (j >= H) return;
     // n_groups is 1..15 (checked at upload).  Every code and row value is
-    // loaded first (group indices clamped, so each load is unconditional),
-    // then summed in group order.
+    // loaded first, then summed in group order: the 16 codes as eight 8-byte
+    // loads, group g's code u[g + 1] for g < n_groups - 1 and the last
+    // group's from the candidates (or u[n_groups]); groups past n_groups
+    // repeat the last group's row (loaded, never summed).  No load sits
+    // behind a branch, so none waits for another.
     constexpr int MAXG = 15;
+    static_assert(offsetof(DevState, used) % 8 == 0, "codes as 8-byte loads");
+    uint32_t u[16];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint2 w = ((const uint2 *)st->used)[i];
+        u[2 * i] = w.x;
+        u[2 * i + 1] = w.y;
+    }
+    uint32_t lastc = u[1];
+#pragma unroll
+    for (int i = 2; i < 16; i++) lastc = i == n_groups ? u[i] : lastc;
+    if (cand_last) lastc = last;
     uint32_t code[MAXG];
 #pragma unroll
-    for (int g = 0; g < MAXG; g++) {
-        const int gg = min(g, n_groups - 1);
-        code[g] = (cand_last && gg == n_groups - 1) ? last : st->used[gg + 1];
-    }
-    const float sem = q4_row_value(tcodec, st->used[0], j);
+    for (int g = 0; g < MAXG; g++) code[g] = g < n_groups - 1 ? u[g + 1] : lastc;
+    const int f = st->frame_idx, n_text = st->n_text;
+    const float sem = q4_row_value(tcodec, u[0], j);
     float val[MAXG];
 #pragma unroll
     for (int g = 0; g < MAXG; g++) {
@@ -2292,8 +2305,7 @@ k_combine(Q4Rows tcodec, Q4Rows cpemb, int n_groups, DevState *st, const float *
     for (int g = 0; g < MAXG; g++)
         if (g < n_groups) sum += val[g];
     float v = sem + sum;
-    const int f = st->frame_idx;
-    const float *tr = (f < st->n_text) ? text + (size_t)f * H : pad;
+    const float *tr = (f < n_text) ? text + (size_t)f * H : pad;
     v += tr[j];
     x[j] = v;
 }
@@ -2736,13 +2748,33 @@ k_step_end(const float *part, int S, int npad, int V, const float *hid_work, int
 {
     const int t = threadIdx.x;
     if (frame_mode && st->stop) return;
-    for (int j = t; j < V; j += blockDim.x) {
-        float v = 0.0f;
-#pragma unroll 4
-        for (int s = 0; s < S; s++) v += part[(size_t)s * npad + j];
-        logits[j] = v;
+    // V and npad are whole 32-column groups (checked at upload), V <= 4096.
+    // The common case (up to four columns per thread, up to four slices,
+    // up to two hidden values) issues every load before its first wait;
+    // the loops below take the rest.
+    constexpr int JV = 4, SV = 4, HV = 2;
+    float pv[JV][SV], hv[HV];
+#pragma unroll
+    for (int q = 0; q < JV; q++)
+#pragma unroll
+        for (int s = 0; s < SV; s++)
+            pv[q][s] = part[(size_t)min(s, S - 1) * npad + min(t + q * 1024, V - 1)];
+#pragma unroll
+    for (int q = 0; q < HV; q++) hv[q] = hid_work[min(t + q * 1024, H - 1)];
+#pragma unroll
+    for (int q = 0; q < JV; q++) {
+        const int j = t + q * 1024;
+        float v = pv[q][0];
+#pragma unroll
+        for (int s = 1; s < SV; s++)
+            if (s < S) v += pv[q][s];
+        for (int s = SV; s < S; s++) v += part[(size_t)s * npad + j];
+        if (j < V) logits[j] = v;
     }
-    for (int j = t; j < H; j += blockDim.x) hidden[j] = hid_work[j];
+#pragma unroll
+    for (int q = 0; q < HV; q++)
+        if (t + q * 1024 < H) hidden[t + q * 1024] = hv[q];
+    for (int j = t + HV * 1024; j < H; j += 1024) hidden[j] = hid_work[j];
     const int f = st->frame_idx;
     if (frame_mode && t < 16) {
         ring_pred[(size_t)(f - st->ring_base) * 16 + t] = st->pred[t];

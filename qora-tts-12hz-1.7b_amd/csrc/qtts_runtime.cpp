@@ -847,6 +847,11 @@ static int upload_model(qtts_ctx *c, const qtts_talker_host *t, const qtts_predi
     if (p->n_groups < 1 || p->n_groups > 15 || !p->lm_heads || !p->codec_embeddings)
         return fail(c, QTTS_ERR_INVALID, "predictor needs 1..15 heads and embeddings");
     if (t->vocab > 4096 || t->vocab <= 0) return fail(c, QTTS_ERR_UNSUPPORTED, "talker vocab must be <= 4096");
+    // the step end, the sampler and the predictor's argmax read whole 32-column
+    // groups of the heads' partial sums (the 12 Hz model's 3072 and 2048 are)
+    if (t->vocab % 32 || p->vocab <= 0 || p->vocab % 32)
+        return fail(c, QTTS_ERR_UNSUPPORTED, "codec vocab sizes must be multiples of 32 (talker %d, predictor %d)",
+                    t->vocab, p->vocab);
     if (t->hidden > 2048 || p->hidden > 2048 || t->hidden % 32 || p->hidden % 32)
         return fail(c, QTTS_ERR_UNSUPPORTED, "hidden sizes must be multiples of 32 and <= 2048");
     if (t->rope_max_pos < 1 || !t->rope_cos || !t->rope_sin || p->rope_max_pos < PRED_KV_CAP)

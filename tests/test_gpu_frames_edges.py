@@ -192,3 +192,26 @@ def test_wait_give_up_reported_then_recovers(ctx_factory, model):
     assert c.kv_len() == 16
     got, _ = c.gen_frames(6)
     assert np.array_equal(got, ref_frames)
+
+
+def test_codec_vocab_not_whole_groups_refused(ctx_factory):
+    """A codec vocabulary that does not fill whole 32-column groups is refused
+    at upload with QTTS_ERR_UNSUPPORTED: the step end, the sampler and the
+    predictor's argmax read whole groups of the heads' partial sums, and the
+    12 Hz model's vocabularies (3072, 2048) are whole groups.  The context
+    takes a supported model afterwards."""
+    c = ctx_factory(64)
+    p = synth.make_predictor(seed=704, n_layers=1, rope_max_pos=64)
+    t = synth.make_talker(seed=703, n_layers=1, vocab=3000, text_vocab=256, rope_max_pos=128)
+    with pytest.raises(qtts.QttsError) as e:
+        c.upload_model(t, p)
+    assert e.value.code == qtts.ERR_UNSUPPORTED
+    t = synth.make_talker(seed=703, n_layers=1, text_vocab=256, rope_max_pos=128)
+    p2 = synth.make_predictor(seed=704, n_layers=1, vocab=2000, rope_max_pos=64)
+    with pytest.raises(qtts.QttsError) as e:
+        c.upload_model(t, p2)
+    assert e.value.code == qtts.ERR_UNSUPPORTED
+    c.upload_model(t, p)
+    X = np.random.Generator(np.random.PCG64(705)).standard_normal((4, t.hidden)).astype(np.float32)
+    lg = c.apply_codec_head(c.prefill_talker_raw_from(X, 0))
+    assert lg.shape == (3072,) and np.isfinite(lg).all()
