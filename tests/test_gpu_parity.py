@@ -408,15 +408,18 @@ def test_predictor_row_tables_bit_identical(ctx_factory, small_model, monkeypatc
                                    {"TQKV": "3", "TDOWN": "12", "PQKV": "2", "PDOWN": "3"},
                                    {"TQKV": "9", "HEAD": "7", "PQKV": "7"},
                                    {"PGU": "14", "PDOWN": "15"}, {"PGU": "15", "PDOWN": "15"},
-                                   {"TGU": "15", "TDOWN": "15"}])
+                                   {"TGU": "15", "TDOWN": "15"}, {"PHEAD": "12", "HEAD": "0"}])
 def test_alternative_tiles_step_and_chain(ctx_factory, small_model, tiles, monkeypatch):
     """Other tile shapes per role (QTTS_TILE_<ROLE>): split-K gate|up with the
     SwiGLU prologue in the down projection, the unfused predictor attention,
     multi-slice q|k|v, the RMSNorm prologue's register rows on two- and
     four-group tiles, the predictor's gate|up + down launch on paired
     gate|up tiles (SwiGLU in their epilogue) and on 512-thread one-group
-    tiles, and the talker's on one-group tiles; a talker step at KV 100 and
-    the predictor codes match the oracle."""
+    tiles, and the talker's on one-group tiles; two-slice predictor heads
+    (argmax over the summed partials instead of per-tile candidates) and an
+    eight-slice codec head (the step end's loop past its four unrolled
+    slices); a talker step at KV 100 and the predictor codes match the
+    oracle."""
     for role, cfg in tiles.items():
         monkeypatch.setenv(f"QTTS_TILE_{role}", cfg)
     t, p = small_model
