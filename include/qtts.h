@@ -252,7 +252,10 @@ int qtts_embed_lookup_q4(qtts_ctx *ctx, const qtts_w *w, int64_t row,
 /* ---- model level ------------------------------------------------------ */
 
 /* Upload talker + predictor.  Replaces holding `TalkerWeights` /
- * `CodePredictorWeights` (talker.rs:33-56, code_predictor.rs:28-46). */
+ * `CodePredictorWeights` (talker.rs:33-56, code_predictor.rs:28-46).
+ * QTTS_ERR_UNSUPPORTED for shapes other than the 12 Hz model's layout:
+ * 16 query / 8 KV heads of 128, hidden sizes multiples of 32 up to 2048,
+ * codec vocabularies multiples of 32 (talker at most 4096). */
 int qtts_model_upload(qtts_ctx *ctx, const qtts_talker_host *talker,
                       const qtts_predictor_host *predictor);
 
