@@ -391,31 +391,34 @@ __global__ void k_vq_gather(const float *first, const float *const *rest, int n_
 }
 
 // Column RMSNorm (rms_norm_f32, decoder.rs:589-598) of x [H][T]:
-// workgroup of 16 positions x 16 channel groups; the sum of squares is
-// the 16 group partials added in group order.
-__global__ void __launch_bounds__(256)
+// workgroup of 16 positions x COLRMS_CG channel groups; the sum of squares
+// is the group partials added in group order.  At the 12 Hz shapes (512
+// channels, 160 positions per decode) the grid is 10 workgroups, so each
+// takes 16 waves.
+constexpr int COLRMS_CG = 64;
+__global__ void __launch_bounds__(16 * COLRMS_CG)
 k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *out)
 {
-    __shared__ float red[16][17];
+    __shared__ float red[COLRMS_CG][17];
     const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
     const int t = blockIdx.x * 16 + tl;
     const bool ok = t < T;
     const float *xc = x + min(t, T - 1);
     float ss = 0.0f;
 #pragma unroll 8
-    for (int h = cg; h < H; h += 16) {
+    for (int h = cg; h < H; h += COLRMS_CG) {
         const float v = xc[(size_t)h * T];
         ss = fmaf(v, v, ss);
     }
     red[cg][tl] = ss;
     __syncthreads();
     float tot = 0.0f;
-#pragma unroll
-    for (int g = 0; g < 16; g++) tot += red[g][tl];
+#pragma unroll 8
+    for (int g = 0; g < COLRMS_CG; g++) tot += red[g][tl];
     const float inv = 1.0f / sqrtf(tot / (float)H + eps);
     if (!ok) return;
 #pragma unroll 8
-    for (int h = cg; h < H; h += 16) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
+    for (int h = cg; h < H; h += COLRMS_CG) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
 }
 
 // Rotate-half RoPE (apply_rope_split_half, decoder.rs:631-655) of the q and
@@ -578,20 +581,25 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
 
 // ConvNeXt front (decoder.rs:346-352): causal depthwise conv then LayerNorm
 // over channels per position (layer_norm_channel_first, decoder.rs:668-690).
-// Workgroup of 16 positions x 16 channel groups: the conv values go to the
-// output buffer, then the column statistics (group partials in group order).
-__global__ void __launch_bounds__(256)
+// Workgroup of 16 positions x DWLN_CG channel groups: thread (cg, tl) takes
+// position 16*blockIdx.x + tl and channels cg, cg + DWLN_CG, ...; the conv
+// values go to the output buffer, then the column statistics (group
+// partials summed in group order).  At the 12 Hz shapes (1024 channels,
+// 320 and 640 positions) the grid is 20-40 workgroups, so each takes 16
+// waves: a thread walks 16 channels, not 64.
+constexpr int DWLN_CG = 64;
+__global__ void __launch_bounds__(16 * DWLN_CG)
 k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int K, const float *g, const float *b,
         float eps, float *out)
 {
-    __shared__ float red[2][16][17];
+    __shared__ float red[2][DWLN_CG][17];
     const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
     const int t = blockIdx.x * 16 + tl;
     const bool ok = t < L;
     const int tc = min(t, L - 1);
     float s1 = 0.0f;
 #pragma unroll 4
-    for (int c = cg; c < C; c += 16) {
+    for (int c = cg; c < C; c += DWLN_CG) {
         const float *xr = x + (size_t)c * L;
         const float *wr = dw_w + (size_t)c * K;
         float v = dw_b[c];
@@ -606,25 +614,25 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     red[0][cg][tl] = s1;
     __syncthreads();
     float mean = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; q++) mean += red[0][q][tl];
+#pragma unroll 8
+    for (int q = 0; q < DWLN_CG; q++) mean += red[0][q][tl];
     mean /= (float)C;
     float s2 = 0.0f;
 #pragma unroll 8
-    for (int c = cg; c < C; c += 16) {
+    for (int c = cg; c < C; c += DWLN_CG) {
         const float d = ok ? out[(size_t)c * L + t] - mean : 0.0f;
         s2 += d * d;
     }
     red[1][cg][tl] = s2;
     __syncthreads();
     float var = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; q++) var += red[1][q][tl];
+#pragma unroll 8
+    for (int q = 0; q < DWLN_CG; q++) var += red[1][q][tl];
     var /= (float)C;
     const float inv = 1.0f / sqrtf(var + eps);
     if (!ok) return;
 #pragma unroll 8
-    for (int c = cg; c < C; c += 16) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
+    for (int c = cg; c < C; c += DWLN_CG) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
 }
 
 // Output conv (one channel, causal, conv.rs:191-228) on the snake input,
@@ -821,7 +829,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
     const bool att_tile = d.window + ATT_QB - 1 <= 16 * ATT_SLOTS && att_lds <= 65536;
     for (int l = 0; l < d.n_tf; l++) {
         const DecLayer &L = d.tf[l];
-        hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
+        hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         if (!att_tile) {   // the tiled kernel applies RoPE while staging
@@ -846,14 +854,14 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         ConvOut ro = plain_out(ws.b, T, nullptr);
         ro.scale = L.attn_scale;
         DCHK(conv_gemm<CE_SCALE_RES>(L.o, H, causal_in(ws.e, A, T, 1, 1), ro, T, ws, s));
-        hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, L.post_norm, H, T, 1e-5f, ws.c);
+        hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, L.post_norm, H, T, 1e-5f, ws.c);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_SWIGLU>(L.gate_up, 2 * I, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         ConvOut mo = plain_out(ws.b, T, nullptr);
         mo.scale = L.mlp_scale;
         DCHK(conv_gemm<CE_SCALE_RES>(L.down, H, causal_in(ws.d, I, T, 1, 1), mo, T, ws, s));
     }
-    hipLaunchKernelGGL(k_col_rms, cols, dim3(256), 0, s, ws.b, d.tf_norm, H, T, 1e-5f, ws.c);
+    hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, d.tf_norm, H, T, 1e-5f, ws.c);
     DCHK(hipGetLastError());
     DCHK(conv_gemm<CE_STORE>(d.tf_out_w, LAT, causal_in(ws.c, H, T, 1, 1), plain_out(ws.a, T, d.tf_out_b), T, ws, s));
     // 4. upsample stages: ConvT (phases) then ConvNeXt; the signal moves
@@ -865,7 +873,7 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         const int Lo = L * U.conv_t.stride;
         DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), ws, s));
         L = Lo;
-        hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(256), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
+        hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
                            U.norm_w, U.norm_b, 1e-5f, ws.c);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_GELU>(U.pw1, U.inner, causal_in(ws.c, U.ch, L, 1, 1), plain_out(ws.d, L, U.pw1_b), L, ws, s));
