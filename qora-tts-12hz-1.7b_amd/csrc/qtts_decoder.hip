@@ -639,27 +639,44 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
 // clamp to [-1, 1] (decoder.rs:567-570), written from sample `cut` on.
 // Workgroup per 256 samples; 16-channel slabs of the input with the
 // (K-1)*dil left halo (at most OUT_HALO, zero before position 0) staged in
-// LDS; each thread sums channel by channel, taps in order.
+// LDS through registers, the next slab's loads in flight while the current
+// one is summed; each thread sums channel by channel, taps in order.
 constexpr int OUT_HALO = 64;
 
 __global__ void __launch_bounds__(256)
 k_out_conv(const float *x, int C, int L, const float *w, float bias, int K, int dil, int64_t cut, float *out)
 {
     constexpr int W = 256 + OUT_HALO;
+    constexpr int PER = 16 * W / 256;             // slab values per thread
+    static_assert(16 * W % 256 == 0, "whole slabs per thread");
     __shared__ float xs[16][W];
     const int tl = threadIdx.x, t0 = blockIdx.x * 256, t = t0 + tl;
     const int pad = (K - 1) * dil;
+    // a slab's values in registers: all PER loads issued together, the next
+    // slab's while the current one is summed (the last slab loads itself
+    // again, in bounds, rather than branch around the loads)
+    float v[PER];
+    const auto fetch = [&](int c0) {
+        const int nc = min(16, C - c0);
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int idx = tl + i * 256, cc = idx / W, j = idx - cc * W, p = t0 - pad + j;
+            const bool ok = cc < nc && p >= 0 && p < L;
+            v[i] = *(ok ? x + (size_t)(c0 + cc) * L + p : k_zero);
+        }
+    };
+    fetch(0);
     float s = bias;
     for (int c0 = 0; c0 < C; c0 += 16) {
         const int nc = min(16, C - c0);
         __syncthreads();
-#pragma unroll 4
-        for (int i = tl; i < 16 * W; i += 256) {
-            const int cc = i / W, j = i - cc * W, p = t0 - pad + j;
-            const bool ok = cc < nc && p >= 0 && p < L;
-            xs[cc][j] = *(ok ? x + (size_t)(c0 + cc) * L + p : k_zero);
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int idx = tl + i * 256, cc = idx / W, j = idx - cc * W;
+            xs[cc][j] = v[i];
         }
         __syncthreads();
+        fetch(c0 + 16 < C ? c0 + 16 : c0);
         for (int cc = 0; cc < nc; cc++) {
             const float *wr = w + (size_t)(c0 + cc) * K;
             for (int k = 0; k < K; k++) s += xs[cc][tl + k * dil] * wr[k];
