@@ -475,8 +475,8 @@ k_dec_attn(const float *qkv, int heads, int T, int W, float *out)
 
 // Sliding-window attention, workgroup per (head, 16 queries): the key and
 // value columns those queries see (positions t0-W+1 .. t0+15, zero before
-// position 0) and the 16 query columns staged in LDS, q and k rotated
-// (RoPE) as they are staged.  Scores: lane (query
+// position 0) and the 16 query columns staged in LDS (every load issued
+// first), q and k then rotated (RoPE) in place.  Scores: lane (query
 // qi, key slot kl) holds keys kl + 16i; softmax max and sum over the 16
 // lanes of the query's row (DPP); then lane (qi, dim group dg) sums
 // p.v over the query's W keys in position order (keys before position 0
@@ -487,21 +487,6 @@ static inline size_t attn_tile_lds(int hd, int W)
 {
     const int nkp = ATT_QB + W;   // NK + 1
     return (size_t)(2 * hd * nkp + hd * ATT_QB + ATT_QB * nkp) * sizeof(float);
-}
-
-template <int HD>
-__device__ __forceinline__ float rope_at(const float *row0, int d, int T, int p, const float *cs, const float *sn,
-                                         int64_t rope_rows)
-{
-    // row0: dimension 0 of this head's q or k rows ([HD][T]); rotate-half
-    // RoPE of element (d, p) as k_rope_cf computes it
-    const float x = row0[(size_t)d * T + p];
-    if (p >= rope_rows) return x;
-    constexpr int half = HD / 2;
-    const int i = d < half ? d : d - half;
-    const float xp = row0[(size_t)(d < half ? d + half : d - half) * T + p];
-    const float c = cs[(size_t)p * half + i], s = sn[(size_t)p * half + i];
-    return d < half ? x * c - xp * s : x * c + xp * s;
 }
 
 template <int HD>
@@ -517,19 +502,87 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
     const float *q = qkv + (size_t)h * HD * T, *k = qkv + (A + (size_t)h * HD) * T,
                 *v = qkv + (2 * A + (size_t)h * HD) * T;
     float *Ks = sm, *Vs = Ks + HD * NKP, *Qs = Vs + HD * NKP, *Ps = Qs + HD * ATT_QB;
-#pragma unroll 4
-    for (int i = tid; i < HD * NK; i += 256) {
-        const int d = i / NK, j = i - d * NK, p = kb + j;
-        const bool ok = p >= 0 && p < T;
-        const int pc = min(max(p, 0), T - 1);
-        const float kr = rope_at<HD>(k, d, T, pc, cs, sn, rope_rows);
-        Ks[d * NKP + j] = ok ? kr : 0.0f;
-        Vs[d * NKP + j] = *(ok ? v + (size_t)d * T + pc : k_zero);
+    // Every global load of the tile first (K and V of the window, Q of the
+    // block, the RoPE values of the pairs this thread rotates; clamped, so
+    // none is conditional), then the raw rows into LDS, then rotate-half
+    // RoPE in place: the partner of row d is row d +- HD/2 of the same tile.
+    constexpr int half = HD / 2;
+    constexpr int KE = (HD * 16 * ATT_SLOTS + 255) / 256;        // K / V elements per thread, at most
+    constexpr int QE = (HD * ATT_QB + 255) / 256;                // Q elements per thread
+    constexpr int KR = (half * 16 * ATT_SLOTS + 255) / 256;      // K pairs per thread, at most
+    constexpr int QR = (half * ATT_QB + 255) / 256;              // Q pairs per thread
+    float kraw[KE], vraw[KE], qraw[QE], kc[KR], ks[KR], qc[QR], qs[QR];
+#pragma unroll
+    for (int u = 0; u < KE; u++) {
+        const int i = min(tid + u * 256, HD * NK - 1);
+        const int d = i / NK, j = i - d * NK, pc = min(max(kb + j, 0), T - 1);
+        kraw[u] = k[(size_t)d * T + pc];
+        vraw[u] = v[(size_t)d * T + pc];
     }
-    for (int i = tid; i < HD * ATT_QB; i += 256) {
-        const int d = i / ATT_QB, j = i - d * ATT_QB, p = t0 + j;
-        const float qr = rope_at<HD>(q, d, T, min(p, T - 1), cs, sn, rope_rows);
-        Qs[i] = p < T ? qr : 0.0f;
+#pragma unroll
+    for (int u = 0; u < QE; u++) {
+        const int i = min(tid + u * 256, HD * ATT_QB - 1);
+        const int d = i / ATT_QB, j = i - d * ATT_QB;
+        qraw[u] = q[(size_t)d * T + min(t0 + j, T - 1)];
+    }
+    const int64_t rmax = rope_rows - 1;
+#pragma unroll
+    for (int u = 0; u < KR; u++) {
+        const int i = min(tid + u * 256, half * NK - 1);
+        const int d = i / NK, j = i - d * NK;
+        const int64_t pr = min((int64_t)min(max(kb + j, 0), T - 1), rmax);
+        kc[u] = cs[pr * half + d];
+        ks[u] = sn[pr * half + d];
+    }
+#pragma unroll
+    for (int u = 0; u < QR; u++) {
+        const int i = min(tid + u * 256, half * ATT_QB - 1);
+        const int d = i / ATT_QB, j = i - d * ATT_QB;
+        const int64_t pr = min((int64_t)min(t0 + j, T - 1), rmax);
+        qc[u] = cs[pr * half + d];
+        qs[u] = sn[pr * half + d];
+    }
+#pragma unroll
+    for (int u = 0; u < KE; u++) {
+        const int i = tid + u * 256;
+        if (i < HD * NK) {
+            const int d = i / NK, j = i - d * NK, p = kb + j;
+            const bool ok = p >= 0 && p < T;
+            Ks[d * NKP + j] = ok ? kraw[u] : 0.0f;
+            Vs[d * NKP + j] = ok ? vraw[u] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < QE; u++) {
+        const int i = tid + u * 256;
+        if (i < HD * ATT_QB) Qs[i] = t0 + (i % ATT_QB) < T ? qraw[u] : 0.0f;
+    }
+    __syncthreads();
+    // positions past the table stay unrotated, as k_rope_cf leaves them;
+    // positions outside the sequence hold zeros
+#pragma unroll
+    for (int u = 0; u < KR; u++) {
+        const int i = tid + u * 256;
+        if (i < half * NK) {
+            const int d = i / NK, j = i - d * NK, p = kb + j;
+            if (p >= 0 && p < T && p < rope_rows) {
+                const float x = Ks[d * NKP + j], xp = Ks[(d + half) * NKP + j];
+                Ks[d * NKP + j] = x * kc[u] - xp * ks[u];
+                Ks[(d + half) * NKP + j] = xp * kc[u] + x * ks[u];
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < QR; u++) {
+        const int i = tid + u * 256;
+        if (i < half * ATT_QB) {
+            const int d = i / ATT_QB, j = i - d * ATT_QB, p = t0 + j;
+            if (p < T && p < rope_rows) {
+                const float x = Qs[d * ATT_QB + j], xp = Qs[(d + half) * ATT_QB + j];
+                Qs[d * ATT_QB + j] = x * qc[u] - xp * qs[u];
+                Qs[(d + half) * ATT_QB + j] = xp * qc[u] + x * qs[u];
+            }
+        }
     }
     __syncthreads();
     const int qi = tid >> 4, kl = tid & 15;
