@@ -80,8 +80,20 @@ __device__ __forceinline__ RowPar row_par(const ConvOut &o, int m)
     return r;
 }
 
+// The element the epilogue reads at idx before storing there: y of
+// CE_SCALE_RES, the residual of CE_STORE_SNAKE (none when o.res is null).
 template <int EPI>
-__device__ __forceinline__ void epi_store(const ConvOut &o, const RowPar &r, size_t idx, float acc)
+constexpr bool epi_reads() { return EPI == CE_SCALE_RES || EPI == CE_STORE_SNAKE; }
+
+template <int EPI>
+__device__ __forceinline__ const float *epi_src(const ConvOut &o)
+{
+    return EPI == CE_SCALE_RES ? o.y : EPI == CE_STORE_SNAKE ? o.res : nullptr;
+}
+
+// ext: the element epi_src() holds at idx (read by the caller).
+template <int EPI>
+__device__ __forceinline__ void epi_store(const ConvOut &o, const RowPar &r, size_t idx, float acc, float ext)
 {
     const float v = acc + r.bias;
     if (EPI == CE_STORE) {
@@ -89,20 +101,21 @@ __device__ __forceinline__ void epi_store(const ConvOut &o, const RowPar &r, siz
     } else if (EPI == CE_GELU) {
         o.y[idx] = v * 0.5f * (1.0f + tanhf(v * 0.7071067811865476f));
     } else if (EPI == CE_SCALE_RES) {
-        o.y[idx] = o.y[idx] + r.scale * v;
+        o.y[idx] = ext + r.scale * v;
     } else {
-        const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + o.res[idx] : v;
+        const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + ext : v;
         const float s = sinf(r.a * xv);
         if (EPI == CE_STORE_SNAKE) o.x[idx] = xv;
         o.y[idx] = xv + r.ib * s * s;
     }
 }
 
-// SwiGLU rows (2j, 2j + 1) = (gate, up) -> y[j]
-__device__ __forceinline__ void epi_swiglu(const ConvOut &o, int m, size_t col, float g, float u)
+// SwiGLU rows (2j, 2j + 1) = (gate, up) -> y[j]; bg, bu: their biases (0
+// without)
+__device__ __forceinline__ void epi_swiglu(const ConvOut &o, int m, size_t col, float g, float u, float bg, float bu)
 {
-    g += o.bias ? o.bias[m] : 0.0f;
-    u += o.bias ? o.bias[m + 1] : 0.0f;
+    g += bg;
+    u += bu;
     o.y[(size_t)(m >> 1) * o.ldy + col] = silu_f(g) * u;
 }
 
@@ -142,8 +155,8 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
     constexpr int TILE_BYTES = X3 ? X3_BYTES : F32_BYTES;
     // the staging tiles first (their bank layout assumes the block's base),
-    // then the range check's per-wave maxima
-    __shared__ __attribute__((aligned(16))) unsigned char lds[TILE_BYTES + 16];
+    // then the range check's per-wave maxima and the epilogue's row constants
+    __shared__ __attribute__((aligned(16))) unsigned char lds[TILE_BYTES + 16 + 16 * BM];
     // f32: As[2][BM*CLD], Bs[2][CGN*CLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [CGN*HLD]
     float(*As)[BM * CLD] = (float(*)[BM * CLD])lds;
     float(*Bs)[CGN * CLD] = (float(*)[CGN * CLD])(lds + 2 * BM * CLD * 4);
@@ -279,6 +292,37 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
                 mfma_chunk<MB>(acc, As[buf], Bs[buf], cb, lane);
         });
 
+    // What the epilogue reads (the residual, or y of y += ...) at this
+    // thread's outputs, loaded together once the contraction is done (its
+    // registers are free then).  Read by the epilogue one element at a
+    // time, between its stores to the same buffers, each load would wait
+    // out a memory round trip of its own.
+    float ext[epi_reads<EPI>() ? MB : 1][4][2];
+    const float *esrc = epi_src<EPI>(o);
+    if (epi_reads<EPI>() && g.ks == 1 && esrc) {
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + 16 * i + 4 * q + e;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = n0 + 16 * (2 * wv + j) + r16;
+                    ext[i][e][j] = *((m < M && n < N) ? esrc + (size_t)m * o.ldy + (size_t)n * o.os + o.oo : k_zero);
+                }
+            }
+    }
+    // The tile's per-row epilogue constants (bias, snake or scale), one row
+    // per thread into LDS, for the same reason; the barrier below (the
+    // range check's on X3) publishes them.
+    float *rp = (float *)(lds + TILE_BYTES + 16);   // [4][BM]: bias, a, ib, scale
+    if (g.ks == 1 && t < BM) {
+        const RowPar r = row_par<EPI>(o, min(m0 + t, M - 1));
+        rp[t] = r.bias;
+        rp[BM + t] = r.a;
+        rp[2 * BM + t] = r.ib;
+        rp[3 * BM + t] = r.scale;
+    }
     // The split holds an input as f16 hi + lo: f32-accurate below the f16
     // maximum and, through lo, to 2^-25 absolute.  A workgroup whose inputs
     // reach 65504, or are all below 2^-14 but not zero, flags the decode,
@@ -290,6 +334,8 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         __syncthreads();
         const float mx = fmaxf(fmaxf(wmx[0], wmx[1]), fmaxf(wmx[2], wmx[3]));
         if (t == 0 && g.range_flag && (!(mx < 65504.0f) || (mx > 0.0f && mx < 0x1p-14f))) *g.range_flag = 1;
+    } else {
+        if (g.ks == 1) __syncthreads();
     }
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
     if (g.ks > 1) {
@@ -318,7 +364,9 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     const int n = n0 + 16 * (2 * wv + j) + r16;
-                    if (n < N) epi_swiglu(o, m, (size_t)n * o.os + o.oo, acc[i][j][e], acc[i][j][e + 1]);
+                    if (n < N)
+                        epi_swiglu(o, m, (size_t)n * o.os + o.oo, acc[i][j][e], acc[i][j][e + 1], rp[m - m0],
+                                   rp[m - m0 + 1]);
                 }
             }
             continue;
@@ -327,11 +375,14 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         for (int e = 0; e < 4; e++) {
             const int m = m0 + 16 * i + 4 * q + e;
             if (m >= M) continue;
-            const RowPar r = row_par<EPI>(o, m);
+            const int lr = m - m0;
+            const RowPar r = {rp[lr], rp[BM + lr], rp[2 * BM + lr], rp[3 * BM + lr]};
 #pragma unroll
             for (int j = 0; j < 2; j++) {
                 const int n = n0 + 16 * (2 * wv + j) + r16;
-                if (n < N) epi_store<EPI>(o, r, (size_t)m * o.ldy + (size_t)n * o.os + o.oo, acc[i][j][e]);
+                if (n < N)
+                    epi_store<EPI>(o, r, (size_t)m * o.ldy + (size_t)n * o.os + o.oo, acc[i][j][e],
+                                   epi_reads<EPI>() && esrc ? ext[epi_reads<EPI>() ? i : 0][e][j] : 0.0f);
             }
         }
     }
@@ -359,12 +410,14 @@ k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
             gs += pp[(size_t)m * N + n];
             us += pp[(size_t)(m + 1) * N + n];
         }
-        epi_swiglu(o, m, col, gs, us);
+        epi_swiglu(o, m, col, gs, us, o.bias ? o.bias[m] : 0.0f, o.bias ? o.bias[m + 1] : 0.0f);
         return;
     }
     float sum = 0.0f;
     for (int sl = 0; sl < ks; sl++) sum += part[((size_t)sl * nph + ph) * plane + (size_t)mr * N + n];
-    epi_store<EPI>(o, row_par<EPI>(o, mr), (size_t)mr * o.ldy + col, sum);
+    const size_t idx = (size_t)mr * o.ldy + col;
+    const float *esrc = epi_src<EPI>(o);
+    epi_store<EPI>(o, row_par<EPI>(o, mr), idx, sum, esrc ? esrc[idx] : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
