@@ -163,8 +163,24 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     const auto ha = [&](int buf, int hl) { return (_Float16 *)lds + (size_t)(buf * 2 + hl) * XSTRIDE; };
     const auto hb = [&](int buf, int hl) { return ha(buf, hl) + (size_t)BM * MFMA_HLD; };
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int tiles = g.tm * g.tn, tile = blockIdx.x % tiles, rest = blockIdx.x / tiles;
-    const int ph = rest % g.nph, slice = rest / g.nph;
+    const int tiles = g.tm * g.tn;
+    int tile, ph, slice;
+    if (g.nph > 1 && g.ks == 1 && tiles % 8 == 0) {
+        // The stride phases of a tile 8 workgroup indices apart: workgroup i
+        // runs on XCD i mod 8, so they share an XCD and are dispatched
+        // together, and the output lines they interleave into (column
+        // n * nph + ph) are completed in that XCD's L2 instead of from
+        // several, one phase at a time.
+        const int k = blockIdx.x >> 3;
+        ph = k % g.nph;
+        tile = (k / g.nph) * 8 + (blockIdx.x & 7);
+        slice = 0;
+    } else {
+        tile = blockIdx.x % tiles;
+        const int rest = blockIdx.x / tiles;
+        ph = rest % g.nph;
+        slice = rest / g.nph;
+    }
     const int mt = tile % g.tm, nt = tile / g.tm;
     const int m0 = mt * BM, n0 = nt * CGN;
     A += (size_t)ph * M * Kd;
@@ -389,7 +405,9 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
 }
 
 // Split-K reduction: thread per (phase, row, column) (row pairs for
-// SwiGLU); slices added in slice order, then the epilogue.
+// SwiGLU); slices added in slice order, then the epilogue.  The phase is
+// the fastest index, so that consecutive threads store consecutive output
+// columns n * nph + ph.
 template <int EPI>
 __global__ void __launch_bounds__(256)
 k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
@@ -397,9 +415,9 @@ k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
     const int rows = EPI == CE_SWIGLU ? M / 2 : M;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (int64_t)nph * rows * N) return;
-    const int n = (int)(id % N);
-    const int64_t r2 = id / N;
-    const int mr = (int)(r2 % rows), ph = (int)(r2 / rows);
+    const int ph = (int)(id % nph);
+    const int64_t r2 = id / nph;
+    const int n = (int)(r2 % N), mr = (int)(r2 / N);
     const size_t plane = (size_t)M * N;
     const size_t col = (size_t)n * o.os + (nph > 1 ? ph : o.oo);
     if (EPI == CE_SWIGLU) {
