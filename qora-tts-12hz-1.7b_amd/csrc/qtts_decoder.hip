@@ -209,11 +209,43 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     const bool bcok = pos0 < N;
     const float *xb = in.x;
 
+    // Interior chunks (tap-major): every row, k, tap position and column of
+    // the tile in range, decided per chunk from wave-uniform values.  Each
+    // load is then a wave-uniform base (scalar registers) plus a per-lane
+    // byte offset fixed for the whole contraction: no per-lane address
+    // arithmetic, compare or select per load.
+    const int bqu = __builtin_amdgcn_readfirstlane(bq);   // t >> 7: one value per wave
+    const bool tile_in = m0 + BM <= M && n0 + CGN <= N && (size_t)M * Kd < (size_t{1} << 30);
+    const unsigned b_vo = 4u * (unsigned)pos0;
+    unsigned a_vo[NA];
+#pragma unroll
+    for (int j = 0; j < NA; j++) a_vo[j] = 4u * (unsigned)((arow[j] - A) + akk[j]);
+
     struct Fetch {
         f32x4 a[NA];
         f32x4 b[4];
     };
     auto fetch = [&](Fetch &f, int k0) {
+        if (TM) {
+            const int tap = k0 / in.IC, icb = k0 - tap * in.IC;
+            const int pofs = tap * in.dil - in.pad;
+            if (tile_in && k0 + CGK <= Kd && icb + CGK <= in.IC && n0 + pofs >= 0 && n0 + CGN + pofs <= in.L_in) {
+                const char *ab = (const char *)(A + k0);
+#pragma unroll
+                for (int j = 0; j < NA; j++) f.a[j] = ld4((const float *)(ab + a_vo[j]));
+                const size_t ldx4 = (size_t)in.ldx * 4;
+                const char *xr = (const char *)(xb + (size_t)icb * in.ldx + pofs);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const char *row = xr + (size_t)(4 * (X3 ? 4 * bqu + i : bqu + 2 * i)) * ldx4;
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = *(const float *)(row + e * ldx4 + b_vo);
+                    f.b[i] = f32x4{v[0], v[1], v[2], v[3]};
+                }
+                return;
+            }
+        }
         // Out-of-range rows, chunk tails and taps read k_zero: selecting the
         // address rather than the value keeps every load unconditional (a
         // select on the value lets the compiler sink each load into a
