@@ -22,6 +22,7 @@
 #include "qtts_kernels.h"
 #include "qtts_devutil.h"
 #include "qtts_mfma.h"
+#include "qtts_snake.h"
 
 #include <algorithm>
 
@@ -104,9 +105,8 @@ __device__ __forceinline__ void epi_store(const ConvOut &o, const RowPar &r, siz
         o.y[idx] = ext + r.scale * v;
     } else {
         const float xv = (EPI == CE_STORE_SNAKE && o.res) ? v + ext : v;
-        const float s = sinf(r.a * xv);
         if (EPI == CE_STORE_SNAKE) o.x[idx] = xv;
-        o.y[idx] = xv + r.ib * s * s;
+        o.y[idx] = xv + r.ib * snake_sin2(r.a * xv);
     }
 }
 
@@ -849,8 +849,7 @@ __global__ void k_snake(const float *x, int C, int L, const float *alpha, const 
     if (t >= L) return;
     const float a = expf(alpha[c]), ib = expf(-beta[c]);
     const float v = x[(size_t)c * L + t];
-    const float s = sinf(a * v);
-    out[(size_t)c * L + t] = v + ib * s * s;
+    out[(size_t)c * L + t] = v + ib * snake_sin2(a * v);
 }
 
 // ---------------------------------------------------------------------------
