@@ -294,9 +294,12 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     float bmax = 0.0f;
     auto stage = [&](const Fetch &f, int buf) {
         if constexpr (X3) {
+            // a chain, two values per step: one v_max3 with |.| modifiers each
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                bmax = fmaxf(bmax, fmaxf(fmaxf(fabsf(f.b[i].x), fabsf(f.b[i].y)), fmaxf(fabsf(f.b[i].z), fabsf(f.b[i].w))));
+            for (int i = 0; i < 4; i++) {
+                bmax = fmaxf(fmaxf(bmax, fabsf(f.b[i].x)), fabsf(f.b[i].y));
+                bmax = fmaxf(fmaxf(bmax, fabsf(f.b[i].z)), fabsf(f.b[i].w));
+            }
 #pragma unroll
             for (int j = 0; j < NA; j++) {
                 const int r = aoff[j] / CLD, kk = aoff[j] - r * CLD;
