@@ -130,6 +130,32 @@ def test_decode_without_decoder(ctx_factory):
     assert e.value.code == qtts.ERR_STATE
 
 
+@pytest.mark.parametrize("f32", [False, True])
+def test_snake_wide_arguments_vs_oracle(ctx_factory, monkeypatch, f32):
+    """SnakeBeta arguments e^alpha * x past 2^14 take the epilogues'
+    out-of-line sinf call (qtts_snake.h): with e^alpha = 1.2e6 every
+    |x| >= 0.014 does, in the same waves whose smaller values take the
+    series.  e^-beta = 1.1e-7 keeps sin^2's sensitivity to the rounding of
+    x below the bar, so the comparison sees what the call could break
+    around it: the epilogue's other values and registers (sin^2 itself is
+    pinned on the host, test_snake_sin2.py)."""
+    d = small_decoder(seed=23)
+    for b in d.vocos_blocks:
+        for r in b.residuals:
+            r.act2_alpha = np.full_like(r.act2_alpha, 14.0)
+            r.act2_beta = np.full_like(r.act2_beta, 16.0)
+    c = ctx_factory(64)
+    c.upload_decoder(d)
+    if f32:
+        monkeypatch.setenv("QTTS_DEC_F32", "1")
+    codes = codes_for(d, 40, 4900)
+    ref = O.decode_to_audio(d, codes, threads=16)
+    got = c.decode_to_audio(codes)
+    assert np.all(np.isfinite(got))
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+
+
 @pytest.fixture(scope="module")
 def full():
     return synth.make_decoder(seed=7)
