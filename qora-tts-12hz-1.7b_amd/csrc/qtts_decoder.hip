@@ -527,6 +527,44 @@ k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *ou
     for (int h = cg; h < H; h += COLRMS_CG) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
 }
 
+// The same for H <= COLRMS_CG * COLRMS_NV with each thread's values kept in
+// registers between the two passes: the reload of x and the store of out
+// no longer alternate channel by channel (each reload after a store that
+// may alias it waited out a round trip).  Same operations, same order.
+constexpr int COLRMS_NV = 16;
+__global__ void __launch_bounds__(16 * COLRMS_CG)
+k_col_rms_r(const float *x, const float *gamma, int H, int T, float eps, float *out)
+{
+    __shared__ float red[COLRMS_CG][17];
+    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
+    const int t = blockIdx.x * 16 + tl;
+    const bool ok = t < T;
+    const float *xc = x + min(t, T - 1);
+    float xv[COLRMS_NV], gv[COLRMS_NV];
+#pragma unroll
+    for (int u = 0; u < COLRMS_NV; u++) {
+        const int h = min(cg + u * COLRMS_CG, H - 1);
+        xv[u] = xc[(size_t)h * T];
+        gv[u] = gamma[h];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < COLRMS_NV; u++)
+        if (cg + u * COLRMS_CG < H) ss = fmaf(xv[u], xv[u], ss);
+    red[cg][tl] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll 8
+    for (int g = 0; g < COLRMS_CG; g++) tot += red[g][tl];
+    const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+    if (!ok) return;
+#pragma unroll
+    for (int u = 0; u < COLRMS_NV; u++) {
+        const int h = cg + u * COLRMS_CG;
+        if (h < H) out[(size_t)h * T + t] = xv[u] * inv * gv[u];
+    }
+}
+
 // Rotate-half RoPE (apply_rope_split_half, decoder.rs:631-655) of the q and
 // k rows of qkv [3A][T] in place; positions past the table stay unrotated.
 __global__ void k_rope_cf(float *qkv, int heads, int hd, int T, const float *cs, const float *sn, int64_t rope_rows)
@@ -794,6 +832,65 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     for (int c = cg; c < C; c += DWLN_CG) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
 }
 
+// The same for the ConvNeXt kernel of 7 taps and C <= DWLN_CMAX, the conv
+// values kept in LDS instead of the output buffer: a store to LDS cannot
+// alias the next channel's global loads (a store to the output could, and
+// made every channel wait out a round trip), and the statistics and the
+// normalisation read them back from LDS.  Same operations, same order.
+constexpr int DWLN_CMAX = 1024, DWLN_K = 7;
+__global__ void __launch_bounds__(16 * DWLN_CG)
+k_dw_ln_r(const float *x, int C, int L, const float *dw_w, const float *dw_b, const float *g, const float *b, float eps,
+          float *out)
+{
+    __shared__ float red[2][DWLN_CG][17];
+    __shared__ float vs[DWLN_CMAX][17];
+    __shared__ float gs[DWLN_CMAX], bs[DWLN_CMAX];   // the norm's gamma and beta, loaded with the conv's inputs
+    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
+    const int t = blockIdx.x * 16 + tl;
+    const bool ok = t < L;
+    const int tc = min(t, L - 1);
+    float s1 = 0.0f;
+#pragma unroll 4
+    for (int c = cg; c < C; c += DWLN_CG) {
+        const float *xr = x + (size_t)c * L;
+        const float *wr = dw_w + (size_t)c * DWLN_K;
+        float v = dw_b[c];
+#pragma unroll
+        for (int k = 0; k < DWLN_K; k++) {
+            const int p = tc + k - (DWLN_K - 1);
+            v += p >= 0 ? xr[max(p, 0)] * wr[k] : 0.0f;
+        }
+        vs[c][tl] = v;
+        s1 += v;
+        if (tl == 0) {
+            gs[c] = g[c];
+            bs[c] = b[c];
+        }
+    }
+    red[0][cg][tl] = s1;
+    __syncthreads();
+    float mean = 0.0f;
+#pragma unroll 8
+    for (int q = 0; q < DWLN_CG; q++) mean += red[0][q][tl];
+    mean /= (float)C;
+    float s2 = 0.0f;
+#pragma unroll 8
+    for (int c = cg; c < C; c += DWLN_CG) {
+        const float d = ok ? vs[c][tl] - mean : 0.0f;
+        s2 += d * d;
+    }
+    red[1][cg][tl] = s2;
+    __syncthreads();
+    float var = 0.0f;
+#pragma unroll 8
+    for (int q = 0; q < DWLN_CG; q++) var += red[1][q][tl];
+    var /= (float)C;
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (!ok) return;
+#pragma unroll 8
+    for (int c = cg; c < C; c += DWLN_CG) out[(size_t)c * L + t] = (vs[c][tl] - mean) * inv * gs[c] + bs[c];
+}
+
 // Output conv (one channel, causal, conv.rs:191-228) on the snake input,
 // clamp to [-1, 1] (decoder.rs:567-570), written from sample `cut` on.
 // Workgroup per 256 samples; 16-channel slabs of the input with the
@@ -982,6 +1079,16 @@ static hipError_t conv_t_phases(const DecConvT &w, const float *x, int L_in, Con
     return conv_gemm<EPI>(w.phases, w.oc, in, o, L_in, ws, s, w.stride);
 }
 
+// Column RMSNorm of x [H][T]: the register-resident kernel where H fits it
+static void col_rms(const float *x, const float *gamma, int H, int T, float *out, hipStream_t s)
+{
+    const dim3 grid((T + 15) / 16), block(16 * COLRMS_CG);
+    if (H <= COLRMS_CG * COLRMS_NV)
+        hipLaunchKernelGGL(k_col_rms_r, grid, block, 0, s, x, gamma, H, T, 1e-5f, out);
+    else
+        hipLaunchKernelGGL(k_col_rms, grid, block, 0, s, x, gamma, H, T, 1e-5f, out);
+}
+
 hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
                           float *audio, hipStream_t s)
 {
@@ -999,12 +1106,11 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
                              plain_out(ws.a, T, d.pre_conv.b), T, ws, s));
     // 3. transformer on [H][T]: x in ws.b, normed in ws.c, q|k|v in ws.d, attention in ws.e
     DCHK(conv_gemm<CE_STORE>(d.tf_in_w, H, causal_in(ws.a, LAT, T, 1, 1), plain_out(ws.b, T, d.tf_in_b), T, ws, s));
-    const dim3 cols((T + 15) / 16);
     const size_t att_lds = attn_tile_lds(d.head_dim, d.window);
     const bool att_tile = d.window + ATT_QB - 1 <= 16 * ATT_SLOTS && att_lds <= 65536;
     for (int l = 0; l < d.n_tf; l++) {
         const DecLayer &L = d.tf[l];
-        hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, L.in_norm, H, T, 1e-5f, ws.c);
+        col_rms(ws.b, L.in_norm, H, T, ws.c, s);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_STORE>(L.qkv, 3 * A, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         if (!att_tile) {   // the tiled kernel applies RoPE while staging
@@ -1029,14 +1135,14 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         ConvOut ro = plain_out(ws.b, T, nullptr);
         ro.scale = L.attn_scale;
         DCHK(conv_gemm<CE_SCALE_RES>(L.o, H, causal_in(ws.e, A, T, 1, 1), ro, T, ws, s));
-        hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, L.post_norm, H, T, 1e-5f, ws.c);
+        col_rms(ws.b, L.post_norm, H, T, ws.c, s);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_SWIGLU>(L.gate_up, 2 * I, causal_in(ws.c, H, T, 1, 1), plain_out(ws.d, T, nullptr), T, ws, s));
         ConvOut mo = plain_out(ws.b, T, nullptr);
         mo.scale = L.mlp_scale;
         DCHK(conv_gemm<CE_SCALE_RES>(L.down, H, causal_in(ws.d, I, T, 1, 1), mo, T, ws, s));
     }
-    hipLaunchKernelGGL(k_col_rms, cols, dim3(16 * COLRMS_CG), 0, s, ws.b, d.tf_norm, H, T, 1e-5f, ws.c);
+    col_rms(ws.b, d.tf_norm, H, T, ws.c, s);
     DCHK(hipGetLastError());
     DCHK(conv_gemm<CE_STORE>(d.tf_out_w, LAT, causal_in(ws.c, H, T, 1, 1), plain_out(ws.a, T, d.tf_out_b), T, ws, s));
     // 4. upsample stages: ConvT (phases) then ConvNeXt; the signal moves
@@ -1048,8 +1154,12 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         const int Lo = L * U.conv_t.stride;
         DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), ws, s));
         L = Lo;
-        hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b, U.dw_k,
-                           U.norm_w, U.norm_b, 1e-5f, ws.c);
+        if (U.dw_k == DWLN_K && U.ch <= DWLN_CMAX)
+            hipLaunchKernelGGL(k_dw_ln_r, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b,
+                               U.norm_w, U.norm_b, 1e-5f, ws.c);
+        else
+            hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b,
+                               U.dw_k, U.norm_w, U.norm_b, 1e-5f, ws.c);
         DCHK(hipGetLastError());
         DCHK(conv_gemm<CE_GELU>(U.pw1, U.inner, causal_in(ws.c, U.ch, L, 1, 1), plain_out(ws.d, L, U.pw1_b), L, ws, s));
         ConvOut po = plain_out(other, L, U.pw2_b);
