@@ -527,40 +527,52 @@ k_col_rms(const float *x, const float *gamma, int H, int T, float eps, float *ou
     for (int h = cg; h < H; h += COLRMS_CG) out[(size_t)h * T + t] = xc[(size_t)h * T] * inv * gamma[h];
 }
 
-// The same for H <= COLRMS_CG * COLRMS_NV with each thread's values kept in
-// registers between the two passes: the reload of x and the store of out
-// no longer alternate channel by channel (each reload after a store that
-// may alias it waited out a round trip).  Same operations, same order.
-constexpr int COLRMS_NV = 16;
-__global__ void __launch_bounds__(16 * COLRMS_CG)
+// A column sum over the 1024 threads of a workgroup of 4 positions x 256
+// channel groups (thread 4g + tl: group g, position tl): over the 16 groups
+// of a wave by lane exchanges, then over the 16 waves in order.
+__device__ __forceinline__ float col_sum_tp4(float v, float (*wred)[4], int tl)
+{
+#pragma unroll
+    for (int m = 4; m < 64; m *= 2) v += __shfl_xor(v, m);
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    if (lane < 4) wred[wv][lane] = v;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; q++) tot += wred[q][tl];
+    return tot;
+}
+
+// The same on a grid four times wider, for H <= 1024: workgroups of 4
+// positions x 256 channel groups (40 workgroups at 160 positions, where 16
+// positions gave 10), each thread's values kept in registers between the
+// two passes (the reload of x and the store of out no longer alternate:
+// each reload after a store that may alias it waited out a round trip).
+constexpr int COLRMS_NV = 4;
+__global__ void __launch_bounds__(1024)
 k_col_rms_r(const float *x, const float *gamma, int H, int T, float eps, float *out)
 {
-    __shared__ float red[COLRMS_CG][17];
-    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
-    const int t = blockIdx.x * 16 + tl;
+    __shared__ float wred[16][4];
+    const int tl = threadIdx.x & 3, cg = threadIdx.x >> 2;
+    const int t = blockIdx.x * 4 + tl;
     const bool ok = t < T;
     const float *xc = x + min(t, T - 1);
     float xv[COLRMS_NV], gv[COLRMS_NV];
 #pragma unroll
     for (int u = 0; u < COLRMS_NV; u++) {
-        const int h = min(cg + u * COLRMS_CG, H - 1);
+        const int h = min(cg + 256 * u, H - 1);
         xv[u] = xc[(size_t)h * T];
         gv[u] = gamma[h];
     }
     float ss = 0.0f;
 #pragma unroll
     for (int u = 0; u < COLRMS_NV; u++)
-        if (cg + u * COLRMS_CG < H) ss = fmaf(xv[u], xv[u], ss);
-    red[cg][tl] = ss;
-    __syncthreads();
-    float tot = 0.0f;
-#pragma unroll 8
-    for (int g = 0; g < COLRMS_CG; g++) tot += red[g][tl];
-    const float inv = 1.0f / sqrtf(tot / (float)H + eps);
+        if (cg + 256 * u < H) ss = fmaf(xv[u], xv[u], ss);
+    const float inv = 1.0f / sqrtf(col_sum_tp4(ss, wred, tl) / (float)H + eps);
     if (!ok) return;
 #pragma unroll
     for (int u = 0; u < COLRMS_NV; u++) {
-        const int h = cg + u * COLRMS_CG;
+        const int h = cg + 256 * u;
         if (h < H) out[(size_t)h * T + t] = xv[u] * inv * gv[u];
     }
 }
@@ -832,26 +844,29 @@ k_dw_ln(const float *x, int C, int L, const float *dw_w, const float *dw_b, int 
     for (int c = cg; c < C; c += DWLN_CG) out[(size_t)c * L + t] = (out[(size_t)c * L + t] - mean) * inv * g[c] + b[c];
 }
 
-// The same for the ConvNeXt kernel of 7 taps and C <= DWLN_CMAX, the conv
-// values kept in LDS instead of the output buffer: a store to LDS cannot
-// alias the next channel's global loads (a store to the output could, and
-// made every channel wait out a round trip), and the statistics and the
-// normalisation read them back from LDS.  Same operations, same order.
-constexpr int DWLN_CMAX = 1024, DWLN_K = 7;
-__global__ void __launch_bounds__(16 * DWLN_CG)
+// The same for the ConvNeXt kernel of 7 taps and C <= DWLN_CMAX, on a grid
+// four times wider: workgroups of DWLN_TP = 4 positions x 256 channel
+// groups (80-160 workgroups at the 12 Hz shapes, where 16 positions gave
+// 20-40).  The conv values and the affine parameters are kept in LDS (a
+// store there cannot alias the next channel's global loads); a column's
+// sums are taken over the 16 groups of a wave by lane exchanges, then over
+// the 16 waves in order.
+constexpr int DWLN_CMAX = 1024, DWLN_K = 7, DWLN_TP = 4, DWLN_G = 1024 / DWLN_TP;
+static_assert(DWLN_TP == 4, "col_sum_tp4 sums columns of 4 positions");
+__global__ void __launch_bounds__(1024)
 k_dw_ln_r(const float *x, int C, int L, const float *dw_w, const float *dw_b, const float *g, const float *b, float eps,
           float *out)
 {
-    __shared__ float red[2][DWLN_CG][17];
-    __shared__ float vs[DWLN_CMAX][17];
-    __shared__ float gs[DWLN_CMAX], bs[DWLN_CMAX];   // the norm's gamma and beta, loaded with the conv's inputs
-    const int tl = threadIdx.x & 15, cg = threadIdx.x >> 4;
-    const int t = blockIdx.x * 16 + tl;
+    __shared__ float wred[2][16][DWLN_TP];
+    __shared__ float vs[DWLN_CMAX][DWLN_TP + 1];
+    __shared__ float gs[DWLN_CMAX], bs[DWLN_CMAX];
+    const int tl = threadIdx.x & (DWLN_TP - 1), cg = threadIdx.x / DWLN_TP;
+    const int t = blockIdx.x * DWLN_TP + tl;
     const bool ok = t < L;
     const int tc = min(t, L - 1);
     float s1 = 0.0f;
 #pragma unroll 4
-    for (int c = cg; c < C; c += DWLN_CG) {
+    for (int c = cg; c < C; c += DWLN_G) {
         const float *xr = x + (size_t)c * L;
         const float *wr = dw_w + (size_t)c * DWLN_K;
         float v = dw_b[c];
@@ -867,28 +882,18 @@ k_dw_ln_r(const float *x, int C, int L, const float *dw_w, const float *dw_b, co
             bs[c] = b[c];
         }
     }
-    red[0][cg][tl] = s1;
-    __syncthreads();
-    float mean = 0.0f;
-#pragma unroll 8
-    for (int q = 0; q < DWLN_CG; q++) mean += red[0][q][tl];
-    mean /= (float)C;
+    const float mean = col_sum_tp4(s1, wred[0], tl) / (float)C;
     float s2 = 0.0f;
-#pragma unroll 8
-    for (int c = cg; c < C; c += DWLN_CG) {
+#pragma unroll 4
+    for (int c = cg; c < C; c += DWLN_G) {
         const float d = ok ? vs[c][tl] - mean : 0.0f;
         s2 += d * d;
     }
-    red[1][cg][tl] = s2;
-    __syncthreads();
-    float var = 0.0f;
-#pragma unroll 8
-    for (int q = 0; q < DWLN_CG; q++) var += red[1][q][tl];
-    var /= (float)C;
+    const float var = col_sum_tp4(s2, wred[1], tl) / (float)C;
     const float inv = 1.0f / sqrtf(var + eps);
     if (!ok) return;
-#pragma unroll 8
-    for (int c = cg; c < C; c += DWLN_CG) out[(size_t)c * L + t] = (vs[c][tl] - mean) * inv * gs[c] + bs[c];
+#pragma unroll 4
+    for (int c = cg; c < C; c += DWLN_G) out[(size_t)c * L + t] = (vs[c][tl] - mean) * inv * gs[c] + bs[c];
 }
 
 // Output conv (one channel, causal, conv.rs:191-228) on the snake input,
@@ -1082,11 +1087,10 @@ static hipError_t conv_t_phases(const DecConvT &w, const float *x, int L_in, Con
 // Column RMSNorm of x [H][T]: the register-resident kernel where H fits it
 static void col_rms(const float *x, const float *gamma, int H, int T, float *out, hipStream_t s)
 {
-    const dim3 grid((T + 15) / 16), block(16 * COLRMS_CG);
-    if (H <= COLRMS_CG * COLRMS_NV)
-        hipLaunchKernelGGL(k_col_rms_r, grid, block, 0, s, x, gamma, H, T, 1e-5f, out);
+    if (H <= 256 * COLRMS_NV)
+        hipLaunchKernelGGL(k_col_rms_r, dim3((T + 3) / 4), dim3(1024), 0, s, x, gamma, H, T, 1e-5f, out);
     else
-        hipLaunchKernelGGL(k_col_rms, grid, block, 0, s, x, gamma, H, T, 1e-5f, out);
+        hipLaunchKernelGGL(k_col_rms, dim3((T + 15) / 16), dim3(16 * COLRMS_CG), 0, s, x, gamma, H, T, 1e-5f, out);
 }
 
 hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32_t *codes, int T, int64_t cut,
@@ -1155,8 +1159,8 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         DCHK(conv_t_phases<CE_STORE>(U.conv_t, sig, L, plain_out(other, Lo, U.conv_t.b), ws, s));
         L = Lo;
         if (U.dw_k == DWLN_K && U.ch <= DWLN_CMAX)
-            hipLaunchKernelGGL(k_dw_ln_r, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b,
-                               U.norm_w, U.norm_b, 1e-5f, ws.c);
+            hipLaunchKernelGGL(k_dw_ln_r, dim3((L + DWLN_TP - 1) / DWLN_TP), dim3(1024), 0, s, other, U.ch, L, U.dw_w,
+                               U.dw_b, U.norm_w, U.norm_b, 1e-5f, ws.c);
         else
             hipLaunchKernelGGL(k_dw_ln, dim3((L + 15) / 16), dim3(16 * DWLN_CG), 0, s, other, U.ch, L, U.dw_w, U.dw_b,
                                U.dw_k, U.norm_w, U.norm_b, 1e-5f, ws.c);
