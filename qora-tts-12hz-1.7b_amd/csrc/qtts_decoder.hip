@@ -630,19 +630,22 @@ k_dec_attn(const float *qkv, int heads, int T, int W, float *out)
 }
 
 // Sliding-window attention, workgroup per (head, 16 queries): the key and
-// value columns those queries see (positions t0-W+1 .. t0+15, zero before
-// position 0) and the 16 query columns staged in LDS (every load issued
-// first), q and k then rotated (RoPE) in place.  Scores: lane (query
-// qi, key slot kl) holds keys kl + 16i; softmax max and sum over the 16
-// lanes of the query's row (DPP); then lane (qi, dim group dg) sums
-// p.v over the query's W keys in position order (keys before position 0
-// have p = 0 and v = 0).  Needs W + 15 <= 16 * ATT_SLOTS.
+// value rows those queries see (positions t0-W+1 .. t0+15, zero before
+// position 0) and the 16 query rows staged in LDS position-major, HD + 4
+// floats a row (every global load issued first), q and k then rotated
+// (RoPE) in place.  Scores: lane (query qi, key slot kl) holds keys
+// kl + 16i, its query row in registers and each key row read as 16-byte
+// vectors (rows 68 floats apart: 16 rows cover the 64 banks once), the dot
+// product in dimension order; softmax max and sum over the 16 lanes of the
+// query's row (DPP); then lane (qi, dim group kl) sums p.v for dims
+// 4kl..4kl+3 over the query's W keys in position order (keys before
+// position 0 have p = 0 and v = 0).  Needs W + 15 <= 16 * ATT_SLOTS.
 constexpr int ATT_QB = 16, ATT_SLOTS = 7;
 
 static inline size_t attn_tile_lds(int hd, int W)
 {
-    const int nkp = ATT_QB + W;   // NK + 1
-    return (size_t)(2 * hd * nkp + hd * ATT_QB + ATT_QB * nkp) * sizeof(float);
+    const int nk = ATT_QB + W - 1, kp = hd + 4;
+    return (size_t)(2 * nk * kp + ATT_QB * kp + ATT_QB * (nk + 1)) * sizeof(float);
 }
 
 template <int HD>
@@ -650,18 +653,20 @@ __global__ void __launch_bounds__(256)
 k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, const float *sn, int64_t rope_rows,
                 float *out)
 {
+    static_assert(HD % 4 == 0 && HD / 4 <= 16, "a lane's p.v takes 4 consecutive dims of 16 groups");
     extern __shared__ float sm[];
+    constexpr int KP = HD + 4;                 // floats per staged row
     const int NK = ATT_QB + W - 1, NKP = NK + 1;
     const int h = blockIdx.y, t0 = blockIdx.x * ATT_QB, kb = t0 - (W - 1);
     const int tid = threadIdx.x;
     const size_t A = (size_t)heads * HD;
     const float *q = qkv + (size_t)h * HD * T, *k = qkv + (A + (size_t)h * HD) * T,
                 *v = qkv + (2 * A + (size_t)h * HD) * T;
-    float *Ks = sm, *Vs = Ks + HD * NKP, *Qs = Vs + HD * NKP, *Ps = Qs + HD * ATT_QB;
+    float *Ks = sm, *Vs = Ks + NK * KP, *Qs = Vs + NK * KP, *Ps = Qs + ATT_QB * KP;
     // Every global load of the tile first (K and V of the window, Q of the
     // block, the RoPE values of the pairs this thread rotates; clamped, so
     // none is conditional), then the raw rows into LDS, then rotate-half
-    // RoPE in place: the partner of row d is row d +- HD/2 of the same tile.
+    // RoPE in place: the partner of dim d is dim d +- HD/2 of the same row.
     constexpr int half = HD / 2;
     constexpr int KE = (HD * 16 * ATT_SLOTS + 255) / 256;        // K / V elements per thread, at most
     constexpr int QE = (HD * ATT_QB + 255) / 256;                // Q elements per thread
@@ -704,14 +709,17 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
         if (i < HD * NK) {
             const int d = i / NK, j = i - d * NK, p = kb + j;
             const bool ok = p >= 0 && p < T;
-            Ks[d * NKP + j] = ok ? kraw[u] : 0.0f;
-            Vs[d * NKP + j] = ok ? vraw[u] : 0.0f;
+            Ks[j * KP + d] = ok ? kraw[u] : 0.0f;
+            Vs[j * KP + d] = ok ? vraw[u] : 0.0f;
         }
     }
 #pragma unroll
     for (int u = 0; u < QE; u++) {
         const int i = tid + u * 256;
-        if (i < HD * ATT_QB) Qs[i] = t0 + (i % ATT_QB) < T ? qraw[u] : 0.0f;
+        if (i < HD * ATT_QB) {
+            const int d = i / ATT_QB, j = i - d * ATT_QB;
+            Qs[j * KP + d] = t0 + j < T ? qraw[u] : 0.0f;
+        }
     }
     __syncthreads();
     // positions past the table stay unrotated, as k_rope_cf leaves them;
@@ -722,9 +730,10 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
         if (i < half * NK) {
             const int d = i / NK, j = i - d * NK, p = kb + j;
             if (p >= 0 && p < T && p < rope_rows) {
-                const float x = Ks[d * NKP + j], xp = Ks[(d + half) * NKP + j];
-                Ks[d * NKP + j] = x * kc[u] - xp * ks[u];
-                Ks[(d + half) * NKP + j] = xp * kc[u] + x * ks[u];
+                float *row = Ks + j * KP;
+                const float x = row[d], xp = row[d + half];
+                row[d] = x * kc[u] - xp * ks[u];
+                row[d + half] = xp * kc[u] + x * ks[u];
             }
         }
     }
@@ -734,15 +743,19 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
         if (i < half * ATT_QB) {
             const int d = i / ATT_QB, j = i - d * ATT_QB, p = t0 + j;
             if (p < T && p < rope_rows) {
-                const float x = Qs[d * ATT_QB + j], xp = Qs[(d + half) * ATT_QB + j];
-                Qs[d * ATT_QB + j] = x * qc[u] - xp * qs[u];
-                Qs[(d + half) * ATT_QB + j] = xp * qc[u] + x * qs[u];
+                float *row = Qs + j * KP;
+                const float x = row[d], xp = row[d + half];
+                row[d] = x * qc[u] - xp * qs[u];
+                row[d + half] = xp * qc[u] + x * qs[u];
             }
         }
     }
     __syncthreads();
     const int qi = tid >> 4, kl = tid & 15;
     const float scale = 1.0f / sqrtf((float)HD);
+    f32x4 qv[HD / 4];
+#pragma unroll
+    for (int e = 0; e < HD / 4; e++) qv[e] = *(const f32x4 *)(Qs + qi * KP + 4 * e);
     float sc[ATT_SLOTS];
     float m = -INFINITY;
 #pragma unroll
@@ -751,8 +764,15 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
         const bool ok = j < NK && j >= qi && j <= qi + W - 1 && kb + j >= 0;
         float dot = 0.0f;
         if (ok) {
-#pragma unroll 16
-            for (int d = 0; d < HD; d++) dot = fmaf(Qs[d * ATT_QB + qi], Ks[d * NKP + j], dot);
+            const float *kr = Ks + j * KP;
+#pragma unroll
+            for (int e = 0; e < HD / 4; e++) {
+                const f32x4 k4 = *(const f32x4 *)(kr + 4 * e);
+                dot = fmaf(qv[e].x, k4.x, dot);
+                dot = fmaf(qv[e].y, k4.y, dot);
+                dot = fmaf(qv[e].z, k4.z, dot);
+                dot = fmaf(qv[e].w, k4.w, dot);
+            }
         }
         sc[i] = ok ? dot * scale : -INFINITY;
         m = fmaxf(m, sc[i]);
@@ -772,20 +792,25 @@ k_dec_attn_tile(const float *qkv, int heads, int T, int W, const float *cs, cons
         if (j < NK) Ps[qi * NKP + j] = sc[i] * il;
     }
     __syncthreads();
-    constexpr int DE = HD / 16;
-    float o[DE];
-#pragma unroll
-    for (int e = 0; e < DE; e++) o[e] = 0.0f;
+    const int t = t0 + qi;
+    if (4 * kl >= HD) return;
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
     const float *pr = Ps + qi * NKP + qi;
+    const float *vr = Vs + qi * KP + 4 * kl;
     for (int r = 0; r < W; r++) {
         const float pv = pr[r];
-#pragma unroll
-        for (int e = 0; e < DE; e++) o[e] = fmaf(pv, Vs[(kl + 16 * e) * NKP + qi + r], o[e]);
+        const f32x4 v4 = *(const f32x4 *)(vr + r * KP);
+        o.x = fmaf(pv, v4.x, o.x);
+        o.y = fmaf(pv, v4.y, o.y);
+        o.z = fmaf(pv, v4.z, o.z);
+        o.w = fmaf(pv, v4.w, o.w);
     }
-    const int t = t0 + qi;
     if (t >= T) return;
-#pragma unroll
-    for (int e = 0; e < DE; e++) out[((size_t)h * HD + kl + 16 * e) * T + t] = o[e];
+    float *op = out + ((size_t)h * HD + 4 * kl) * T + t;
+    op[0] = o.x;
+    op[(size_t)T] = o.y;
+    op[2 * (size_t)T] = o.z;
+    op[3 * (size_t)T] = o.w;
 }
 
 // ConvNeXt front (decoder.rs:346-352): causal depthwise conv then LayerNorm
