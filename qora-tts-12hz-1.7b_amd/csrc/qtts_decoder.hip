@@ -136,6 +136,14 @@ struct GemmGeo {
     int32_t *range_flag;        // X3: set when a workgroup's staged inputs leave the split's range
 };
 
+// The second half of a Vocos residual unit, fused behind its k 7 conv
+// (FUSE): the 1x1 conv [BM][BM] weights, and its output (x += conv + bias,
+// y = the next snake of x, CE_STORE_SNAKE with the residual x).
+struct ConvFuse {
+    const float *A2;
+    ConvOut o2;
+};
+
 // X3: the split-f16 contraction (qtts_mfma.h): weights and gathered inputs
 // staged as f16 hi + lo, three f16 matrix products per pair, f32
 // accumulation; otherwise v_mfma_f32_16x16x4_f32 on f32 operands.  On X3
@@ -145,18 +153,25 @@ struct GemmGeo {
 // transposed order (the 4 rows of a half-wave write 80 dwords apart,
 // disjoint bank ranges).
 
-template <int MB, int EPI, bool TM, bool X3>
+template <int MB, int EPI, bool TM, bool X3, bool FUSE = false>
 __global__ void __launch_bounds__(256, 2)
-k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo g)
+k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo g, ConvFuse fz)
 {
     constexpr int BM = 16 * MB;
     constexpr int NA = (BM * CGK / 4 + 255) / 256;
     constexpr int XSTRIDE = (BM + CGN) * MFMA_HLD;   // halves per (buffer, half) on X3
     constexpr int F32_BYTES = 2 * (BM + CGN) * CLD * 4, X3_BYTES = 2 * 2 * XSTRIDE * 2;
     constexpr int TILE_BYTES = X3 ? X3_BYTES : F32_BYTES;
+    // FUSE: the 1x1 conv's B operand, BM channels in BM / 32 chunks of hi and
+    // lo [CGN][HLD] tiles, then one A tile pair [BM][HLD]
+    constexpr int B2_HALVES = CGN * MFMA_HLD;
+    constexpr int FUSE_BYTES = (2 * (BM / CGK) * B2_HALVES + 2 * BM * MFMA_HLD) * 2;
+    constexpr int REGION = FUSE && FUSE_BYTES > TILE_BYTES ? FUSE_BYTES : TILE_BYTES;
+    constexpr int WMX_BYTES = FUSE ? 32 : 16;
+    static_assert(!FUSE || (X3 && TM && EPI == CE_SNAKE && BM % CGK == 0), "the fused 1x1 conv takes a split-f16 k 7 conv");
     // the staging tiles first (their bank layout assumes the block's base),
     // then the range check's per-wave maxima and the epilogue's row constants
-    __shared__ __attribute__((aligned(16))) unsigned char lds[TILE_BYTES + 16 + 16 * BM];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[REGION + WMX_BYTES + 16 * BM];
     // f32: As[2][BM*CLD], Bs[2][CGN*CLD]; X3: per buffer Ah, Al [BM*HLD] and Bh, Bl [CGN*HLD]
     float(*As)[BM * CLD] = (float(*)[BM * CLD])lds;
     float(*Bs)[CGN * CLD] = (float(*)[CGN * CLD])(lds + 2 * BM * CLD * 4);
@@ -366,7 +381,7 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     // The tile's per-row epilogue constants (bias, snake or scale), one row
     // per thread into LDS, for the same reason; the barrier below (the
     // range check's on X3) publishes them.
-    float *rp = (float *)(lds + TILE_BYTES + 16);   // [4][BM]: bias, a, ib, scale
+    float *rp = (float *)(lds + REGION + WMX_BYTES);   // [4][BM]: bias, a, ib, scale
     if (g.ks == 1 && t < BM) {
         const RowPar r = row_par<EPI>(o, min(m0 + t, M - 1));
         rp[t] = r.bias;
@@ -379,7 +394,7 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     // reach 65504, or are all below 2^-14 but not zero, flags the decode,
     // which the host then repeats on the f32 matrix path.
     if constexpr (X3) {
-        float *wmx = (float *)(lds + TILE_BYTES);
+        float *wmx = (float *)(lds + REGION);
         const float m = wave_max_dpp(bmax);
         if (lane == 0) wmx[wv] = m;
         __syncthreads();
@@ -387,6 +402,106 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
         if (t == 0 && g.range_flag && (!(mx < 65504.0f) || (mx > 0.0f && mx < 0x1p-14f))) *g.range_flag = 1;
     } else {
         if (g.ks == 1) __syncthreads();
+    }
+    if constexpr (FUSE) {
+        // The rest of the Vocos residual unit in this workgroup (one row
+        // tile holds all BM channels; no split): the k 7 conv's output
+        // t1 = snake(acc + bias), formed as its epilogue would form it, goes
+        // into LDS as f16 hi + lo -- the values the 1x1 conv's staging would
+        // split after a round trip through memory (zero past column N, as it
+        // would read there) -- then the 1x1 contraction over BM / 32 chunks
+        // and its epilogue (x += conv + bias; y = the next snake of x).
+        // Same operations in the same order as the two launches.
+        _Float16 *b2 = (_Float16 *)lds;
+        _Float16 *a2h = b2 + 2 * (BM / CGK) * B2_HALVES, *a2l = a2h + BM * MFMA_HLD;
+        float *wmx = (float *)(lds + REGION);
+        f32x4 av[BM / CGK][NA];   // the 1x1 weights, every chunk loaded first
+#pragma unroll
+        for (int c = 0; c < BM / CGK; c++)
+#pragma unroll
+            for (int j = 0; j < NA; j++) av[c][j] = ld4(fz.A2 + (size_t)(aoff[j] / CLD) * BM + c * CGK + akk[j]);
+        float xr[MB][4][2];       // the residual x at this thread's outputs
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int m = 16 * i + 4 * q + e, n = n0 + 16 * (2 * wv + j) + r16;
+                    xr[i][e][j] = *(n < N ? fz.o2.res + (size_t)m * fz.o2.ldy + n : k_zero);
+                }
+        float tmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int cl = 16 * (2 * wv + j) + r16;
+                const bool nok = n0 + cl < N;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int lr = 16 * i + 4 * q + e;
+                    const float xv = acc[i][j][e] + rp[lr];
+                    v[e] = nok ? xv + rp[2 * BM + lr] * snake_sin2(rp[BM + lr] * xv) : 0.0f;
+                }
+                tmax = fmaxf(fmaxf(tmax, fabsf(v[0])), fabsf(v[1]));
+                tmax = fmaxf(fmaxf(tmax, fabsf(v[2])), fabsf(v[3]));
+                uint32_t h01, l01, h23, l23;
+                split_f16_pair(v[0], v[1], h01, l01);
+                split_f16_pair(v[2], v[3], h23, l23);
+                const int c = i >> 1, kk = 16 * (i & 1) + 4 * q;
+                *(uint2 *)&b2[(2 * c) * B2_HALVES + cl * MFMA_HLD + kk] = uint2{h01, h23};
+                *(uint2 *)&b2[(2 * c + 1) * B2_HALVES + cl * MFMA_HLD + kk] = uint2{l01, l23};
+            }
+        {
+            const float m = wave_max_dpp(tmax);
+            if (lane == 0) wmx[4 + wv] = m;
+        }
+        __syncthreads();   // t1 staged; every read of the k 7 conv's row constants done
+        {
+            const float mx = fmaxf(fmaxf(wmx[4], wmx[5]), fmaxf(wmx[6], wmx[7]));
+            if (t == 0 && g.range_flag && (!(mx < 65504.0f) || (mx > 0.0f && mx < 0x1p-14f))) *g.range_flag = 1;
+        }
+        if (t < BM) {
+            const RowPar r = row_par<CE_STORE_SNAKE>(fz.o2, t);
+            rp[t] = r.bias;
+            rp[BM + t] = r.a;
+            rp[2 * BM + t] = r.ib;
+        }
+        f32x4 acc2[MB][2];
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc2[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int c = 0; c < BM / CGK; c++) {
+#pragma unroll
+            for (int j = 0; j < NA; j++) {
+                const int r = aoff[j] / CLD, kk = aoff[j] - r * CLD;
+                uint32_t h01, l01, h23, l23;
+                split_f16_pair(av[c][j].x, av[c][j].y, h01, l01);
+                split_f16_pair(av[c][j].z, av[c][j].w, h23, l23);
+                *(uint2 *)&a2h[r * MFMA_HLD + kk] = uint2{h01, h23};
+                *(uint2 *)&a2l[r * MFMA_HLD + kk] = uint2{l01, l23};
+            }
+            __syncthreads();
+            mfma_chunk_x3<MB>(acc2, a2h, a2l, b2 + (2 * c) * B2_HALVES, b2 + (2 * c + 1) * B2_HALVES, cb, lane);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = 16 * i + 4 * q + e;
+                const RowPar r = {rp[m], rp[BM + m], rp[2 * BM + m], 0.0f};
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const int n = n0 + 16 * (2 * wv + j) + r16;
+                    if (n < N)
+                        epi_store<CE_STORE_SNAKE>(fz.o2, r, (size_t)m * fz.o2.ldy + n, acc2[i][j][e], xr[i][e][j]);
+                }
+            }
+        return;
     }
     // element e of acc[i][j]: row 16i + 4q + e, column 16(2wv + j) + r16
     if (g.ks > 1) {
@@ -998,6 +1113,14 @@ static int conv_mb(int M, bool tm)
     return M >= 64 ? 4 : (M >= 32 ? 2 : 1);
 }
 
+// Vocos residual units fused where they fit (vocos_res_fused) unless
+// QTTS_DEC_FUSE_VOC=0 (read at every launch, as dec_x3)
+static bool dec_fuse_voc()
+{
+    const char *v = getenv("QTTS_DEC_FUSE_VOC");
+    return !(v && *v == '0');
+}
+
 // the split-f16 contraction unless QTTS_DEC_F32=1
 static bool dec_x3()
 {
@@ -1014,11 +1137,11 @@ static void conv_launch_x(int mb, dim3 grid, const float *A, int M, int Kd, cons
     switch (mb) {
     case 6:
         if constexpr (TM)
-            hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g);
+            hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{});
         break;
-    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
-    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
-    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g); break;
+    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
+    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
+    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
     }
 }
 
@@ -1081,6 +1204,48 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
 static ConvIn causal_in(const float *x, int IC, int L, int K, int dil)
 {
     return ConvIn{x, L, L, IC, K, dil, (K - 1) * dil};
+}
+
+static ConvOut plain_out(float *y, int ld, const float *bias);
+
+// A Vocos residual unit -- conv1 (k, dilation) + snake, then the 1x1
+// conv2 + residual + the next snake (conv.rs, decoder.rs:515-540) -- as one
+// launch (k_conv_gemm's FUSE form) where its channels fill one 96-row tile
+// and conv1 needs no split of its contraction.  sn: conv1's input; the next
+// snake goes to out_sn (conv1's neighbouring tiles still read sn); x: the
+// residual, updated in place.  *done = false: nothing launched, the caller
+// runs the two convs.
+static hipError_t vocos_res_fused(const DecVocosRes &R, int ch, const float *sn, float *out_sn, float *x, int L,
+                                  const float *next_alpha, const float *next_beta, const DecoderWs &ws, hipStream_t s,
+                                  bool *done)
+{
+    *done = false;
+    if (ch != 96 || ws.f32 || !dec_fuse_voc() || R.c2.k != 1 || !conv_tap_major(ch, R.c1.k) || conv_mb(ch, true) != 6)
+        return hipSuccess;
+    const int Kd = ch * R.c1.k, nch = (Kd + CGK - 1) / CGK, tn = (L + CGN - 1) / CGN;
+    if (Kd & 3 || pick_ks(tn, nch, (size_t)ch * L, ws) != 1) return hipSuccess;
+    GemmGeo g{};
+    g.tm = 1;
+    g.tn = tn;
+    g.nph = 1;
+    g.ks = 1;
+    g.cps = nch;
+    g.part = ws.part;
+    g.range_flag = ws.range_flag;
+    ConvOut c1 = plain_out(nullptr, L, R.c1.b);
+    c1.alpha = R.a2_alpha;
+    c1.beta = R.a2_beta;
+    ConvFuse fz{};
+    fz.A2 = R.c2.w;
+    fz.o2 = plain_out(out_sn, L, R.c2.b);
+    fz.o2.x = x;
+    fz.o2.res = x;
+    fz.o2.alpha = next_alpha;
+    fz.o2.beta = next_beta;
+    hipLaunchKernelGGL((k_conv_gemm<6, CE_SNAKE, true, true, true>), dim3(tn), dim3(256), 0, s, R.c1.w, ch, Kd,
+                       causal_in(sn, ch, L, R.c1.k, R.c1.dil), c1, L, g, fz);
+    *done = true;
+    return hipGetLastError();
 }
 
 static ConvOut plain_out(float *y, int ld, const float *bias)
@@ -1225,16 +1390,22 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
         std::swap(sn, t1);   // sn = snake(x)
         for (int r = 0; r < B.n_res; r++) {
             const DecVocosRes &R = B.res[r];
+            const float *nal = r + 1 < B.n_res ? B.res[r + 1].a1_alpha
+                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
+            const float *nbe = r + 1 < B.n_res ? B.res[r + 1].a1_beta
+                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_beta : d.final_beta);
+            bool fused;
+            DCHK(vocos_res_fused(R, ch, sn, t1, x, L, nal, nbe, ws, s, &fused));
+            if (fused) {
+                std::swap(sn, t1);   // sn = the next snake of x
+                continue;
+            }
             // conv1 (k 7, dilation) with act2 fused: t1 = snake2(conv1(sn))
             ConvOut c1 = plain_out(t1, L, R.c1.b);
             c1.alpha = R.a2_alpha;
             c1.beta = R.a2_beta;
             DCHK(conv_gemm<CE_SNAKE>(R.c1.w, ch, causal_in(sn, ch, L, R.c1.k, R.c1.dil), c1, L, ws, s));
             // conv2 (k 1) + residual: x += conv2(t1); sn = next snake(x)
-            const float *nal = r + 1 < B.n_res ? B.res[r + 1].a1_alpha
-                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_alpha : d.final_alpha);
-            const float *nbe = r + 1 < B.n_res ? B.res[r + 1].a1_beta
-                                               : (b + 1 < d.n_voc ? d.voc[b + 1].pre_beta : d.final_beta);
             ConvOut c2 = plain_out(sn, L, R.c2.b);
             c2.x = x;
             c2.res = x;

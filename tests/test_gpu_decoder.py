@@ -194,6 +194,18 @@ def test_decode_full_dims_longer_vs_oracle(full_ctx, full):
     assert ok, f"rel err {e}"
 
 
+def test_fused_vocos_unit_bit_identical(full_ctx, full, monkeypatch):
+    """The last Vocos block's residual units (96 channels: one row tile)
+    run as one launch each at 80 frames -- the k 7 conv's snake output kept
+    in LDS as the 1x1 conv's operand -- with the same bits as the two
+    launches (QTTS_DEC_FUSE_VOC=0)."""
+    codes = codes_for(full, 80, 5100)
+    fused = full_ctx.decode_to_audio(codes)
+    monkeypatch.setenv("QTTS_DEC_FUSE_VOC", "0")
+    apart = full_ctx.decode_to_audio(codes)
+    assert np.array_equal(fused.view(np.uint32), apart.view(np.uint32))
+
+
 def test_decode_full_dims_properties(full_ctx, full):
     """Warmup trim (bit-identical: same length, same kernels) and causality
     (within 1e-5, see test_decode_is_causal) at the full shapes, at lengths
