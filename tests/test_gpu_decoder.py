@@ -206,6 +206,28 @@ def test_fused_vocos_unit_bit_identical(full_ctx, full, monkeypatch):
     assert np.array_equal(fused.view(np.uint32), apart.view(np.uint32))
 
 
+def test_fused_vocos_unit_column_tail(ctx_factory, monkeypatch):
+    """The fused Vocos residual unit where the last column tile is partial:
+    a small decoder whose one Vocos block keeps 96 channels at rate 8, 2049
+    frames -> 65,568 positions = 512 whole 128-column tiles + 32 columns
+    (the 12 Hz shapes always give whole tiles: 1920 samples a frame).
+    Against the oracle, and bit-identical to the two launches."""
+    d = synth.make_decoder(seed=29, latent=64, hidden=64, n_heads=4, head_dim=16, inter=128, n_tf_layers=2,
+                           codebook_size=64, codebook_dim=32, vq_dim=32, vocos=(96, 96), rates=(8,),
+                           rope_max_pos=4096)
+    c = ctx_factory(64)
+    c.upload_decoder(d)
+    codes = codes_for(d, 2049, 5200)
+    ref = O.decode_to_audio(d, codes, threads=16)
+    got = c.decode_to_audio(codes)
+    assert got.size == ref.size == 65568
+    ok, e = close(got, ref)
+    assert ok, f"rel err {e}"
+    monkeypatch.setenv("QTTS_DEC_FUSE_VOC", "0")
+    apart = c.decode_to_audio(codes)
+    assert np.array_equal(got.view(np.uint32), apart.view(np.uint32))
+
+
 def test_decode_full_dims_properties(full_ctx, full):
     """Warmup trim (bit-identical: same length, same kernels) and causality
     (within 1e-5, see test_decode_is_causal) at the full shapes, at lengths
