@@ -557,11 +557,14 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
 // Split-K reduction: thread per (phase, row, column) (row pairs for
 // SwiGLU); slices added in slice order, then the epilogue.  The phase is
 // the fastest index, so that consecutive threads store consecutive output
-// columns n * nph + ph.
-template <int EPI>
+// columns n * nph + ph.  KS: the slice count when fixed at compile time (0:
+// ks at run time), so that a thread's slice loads are all issued before the
+// first addition instead of one round trip each.
+template <int EPI, int KS>
 __global__ void __launch_bounds__(256)
-k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
+k_conv_reduce(const float *part, int ks_arg, int nph, int M, int N, ConvOut o)
 {
+    const int ks = KS ? KS : ks_arg;
     const int rows = EPI == CE_SWIGLU ? M / 2 : M;
     const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (int64_t)nph * rows * N) return;
@@ -573,16 +576,39 @@ k_conv_reduce(const float *part, int ks, int nph, int M, int N, ConvOut o)
     if (EPI == CE_SWIGLU) {
         const int m = 2 * mr;
         float gs = 0.0f, us = 0.0f;
-        for (int sl = 0; sl < ks; sl++) {
-            const float *pp = part + ((size_t)sl * nph + ph) * plane;
-            gs += pp[(size_t)m * N + n];
-            us += pp[(size_t)(m + 1) * N + n];
+        if constexpr (KS > 0) {
+            float gv[KS > 0 ? KS : 1], uv[KS > 0 ? KS : 1];
+#pragma unroll
+            for (int sl = 0; sl < KS; sl++) {
+                const float *pp = part + ((size_t)sl * nph + ph) * plane;
+                gv[sl] = pp[(size_t)m * N + n];
+                uv[sl] = pp[(size_t)(m + 1) * N + n];
+            }
+#pragma unroll
+            for (int sl = 0; sl < KS; sl++) {
+                gs += gv[sl];
+                us += uv[sl];
+            }
+        } else {
+            for (int sl = 0; sl < ks; sl++) {
+                const float *pp = part + ((size_t)sl * nph + ph) * plane;
+                gs += pp[(size_t)m * N + n];
+                us += pp[(size_t)(m + 1) * N + n];
+            }
         }
         epi_swiglu(o, m, col, gs, us, o.bias ? o.bias[m] : 0.0f, o.bias ? o.bias[m + 1] : 0.0f);
         return;
     }
     float sum = 0.0f;
-    for (int sl = 0; sl < ks; sl++) sum += part[((size_t)sl * nph + ph) * plane + (size_t)mr * N + n];
+    if constexpr (KS > 0) {
+        float pv[KS > 0 ? KS : 1];
+#pragma unroll
+        for (int sl = 0; sl < KS; sl++) pv[sl] = part[((size_t)sl * nph + ph) * plane + (size_t)mr * N + n];
+#pragma unroll
+        for (int sl = 0; sl < KS; sl++) sum += pv[sl];
+    } else {
+        for (int sl = 0; sl < ks; sl++) sum += part[((size_t)sl * nph + ph) * plane + (size_t)mr * N + n];
+    }
     const size_t idx = (size_t)mr * o.ldy + col;
     const float *esrc = epi_src<EPI>(o);
     epi_store<EPI>(o, row_par<EPI>(o, mr), idx, sum, esrc ? esrc[idx] : 0.0f);
@@ -1194,8 +1220,15 @@ static hipError_t conv_gemm(const float *A, int M, const ConvIn &in, const ConvO
     DCHK(hipGetLastError());
     if (g.ks > 1) {
         const int64_t n = (int64_t)nph * (EPI == CE_SWIGLU ? M / 2 : M) * N;
-        hipLaunchKernelGGL(k_conv_reduce<EPI>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ws.part, g.ks, nph,
-                           M, N, o);
+        const dim3 rg((unsigned)((n + 255) / 256));
+        if (g.ks == 2)
+            hipLaunchKernelGGL((k_conv_reduce<EPI, 2>), rg, dim3(256), 0, s, ws.part, g.ks, nph, M, N, o);
+        else if (g.ks == 4)
+            hipLaunchKernelGGL((k_conv_reduce<EPI, 4>), rg, dim3(256), 0, s, ws.part, g.ks, nph, M, N, o);
+        else if (g.ks == 8)
+            hipLaunchKernelGGL((k_conv_reduce<EPI, 8>), rg, dim3(256), 0, s, ws.part, g.ks, nph, M, N, o);
+        else
+            hipLaunchKernelGGL((k_conv_reduce<EPI, 0>), rg, dim3(256), 0, s, ws.part, g.ks, nph, M, N, o);
         DCHK(hipGetLastError());
     }
     return hipSuccess;
