@@ -168,7 +168,8 @@ k_conv_gemm(const float *A, int M, int Kd, ConvIn in, ConvOut o, int N, GemmGeo 
     constexpr int FUSE_BYTES = (2 * (BM / CGK) * B2_HALVES + 2 * BM * MFMA_HLD) * 2;
     constexpr int REGION = FUSE && FUSE_BYTES > TILE_BYTES ? FUSE_BYTES : TILE_BYTES;
     constexpr int WMX_BYTES = FUSE ? 32 : 16;
-    static_assert(!FUSE || (X3 && TM && EPI == CE_SNAKE && BM % CGK == 0), "the fused 1x1 conv takes a split-f16 k 7 conv");
+    static_assert(!FUSE || (X3 && TM && EPI == CE_SNAKE && BM % CGK == 0),
+                  "the fused 1x1 conv takes a split-f16 k 7 conv");
     // the staging tiles first (their bank layout assumes the block's base),
     // then the range check's per-wave maxima and the epilogue's row constants
     __shared__ __attribute__((aligned(16))) unsigned char lds[REGION + WMX_BYTES + 16 * BM];
@@ -621,19 +622,37 @@ k_conv_reduce(const float *part, int ks_arg, int nph, int M, int N, ConvOut o)
 // VQ inputs (codebook_lookup, decoder.rs:147-191) as one contraction of
 // 2*D rows: rows 0..D-1 = first codebook row of code 0, rows D..2D-1 = the
 // sum of the other codebooks' rows (added in codebook order).  codes
-// [n_cb][T]; out [2D][T].
+// [n_cb][T]; out [2D][T].  NR: the number of other codebooks when fixed at
+// compile time (0: n_rest at run time); with it every code, row pointer and
+// row value is loaded before the sum, not one dependent chain per codebook.
+template <int NR>
 __global__ void k_vq_gather(const float *first, const float *const *rest, int n_rest, int D, const uint32_t *codes,
                             int T, int rows_cb, float *out)
 {
     const int d = blockIdx.y, t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T) return;
     const uint32_t c0 = min(codes[t], (uint32_t)(rows_cb - 1));
-    out[(size_t)d * T + t] = first[(size_t)c0 * D + d];
+    const float f = first[(size_t)c0 * D + d];
     float s = 0.0f;
-    for (int g = 0; g < n_rest; g++) {
-        const uint32_t c = min(codes[(size_t)(g + 1) * T + t], (uint32_t)(rows_cb - 1));
-        s += rest[g][(size_t)c * D + d];
+    if constexpr (NR > 0) {
+        uint32_t c[NR];
+        const float *row[NR];
+        float v[NR];
+#pragma unroll
+        for (int g = 0; g < NR; g++) c[g] = min(codes[(size_t)(g + 1) * T + t], (uint32_t)(rows_cb - 1));
+#pragma unroll
+        for (int g = 0; g < NR; g++) row[g] = rest[g];
+#pragma unroll
+        for (int g = 0; g < NR; g++) v[g] = row[g][(size_t)c[g] * D + d];
+#pragma unroll
+        for (int g = 0; g < NR; g++) s += v[g];
+    } else {
+        for (int g = 0; g < n_rest; g++) {
+            const uint32_t c = min(codes[(size_t)(g + 1) * T + t], (uint32_t)(rows_cb - 1));
+            s += rest[g][(size_t)c * D + d];
+        }
     }
+    out[(size_t)d * T + t] = f;
     out[(size_t)(D + d) * T + t] = s;
 }
 
@@ -1165,9 +1184,15 @@ static void conv_launch_x(int mb, dim3 grid, const float *A, int M, int Kd, cons
         if constexpr (TM)
             hipLaunchKernelGGL((k_conv_gemm<6, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{});
         break;
-    case 4: hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
-    case 2: hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
-    default: hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{}); break;
+    case 4:
+        hipLaunchKernelGGL((k_conv_gemm<4, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{});
+        break;
+    case 2:
+        hipLaunchKernelGGL((k_conv_gemm<2, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{});
+        break;
+    default:
+        hipLaunchKernelGGL((k_conv_gemm<1, EPI, TM, X3>), grid, dim3(256), 0, s, A, M, Kd, in, o, N, g, ConvFuse{});
+        break;
     }
 }
 
@@ -1324,8 +1349,12 @@ hipError_t enqueue_decode(const DecoderDev &d, const DecoderWs &ws, const uint32
     const int D = d.codebook_dim, V = d.vq_dim, H = d.hidden, A = d.n_heads * d.head_dim, I = d.inter;
     const int LAT = d.latent;
     // 1. VQ -> [V][T]
-    hipLaunchKernelGGL(k_vq_gather, dim3((T + 63) / 64, D), dim3(64), 0, s, d.first_codebook, d.rest_codebooks,
-                       d.n_rest, D, codes, T, d.codebook_size, ws.a);
+    if (d.n_rest == 15)
+        hipLaunchKernelGGL(k_vq_gather<15>, dim3((T + 63) / 64, D), dim3(64), 0, s, d.first_codebook, d.rest_codebooks,
+                           d.n_rest, D, codes, T, d.codebook_size, ws.a);
+    else
+        hipLaunchKernelGGL(k_vq_gather<0>, dim3((T + 63) / 64, D), dim3(64), 0, s, d.first_codebook, d.rest_codebooks,
+                           d.n_rest, D, codes, T, d.codebook_size, ws.a);
     DCHK(hipGetLastError());
     DCHK(conv_gemm<CE_STORE>(d.vq_proj, V, causal_in(ws.a, 2 * D, T, 1, 1), plain_out(ws.b, T, nullptr), T, ws, s));
     // 2. pre-conv -> [LAT][T]
